@@ -1,0 +1,26 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line(
+        "markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library"
+    )
+
+
+@pytest.fixture(scope="session")
+def gpu_lib():
+    """The HIP library on cuda:0; GPU tests fail loudly if it is missing."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test collected on a host without a GPU")
+    from mamba4_amd import _lib
+
+    return _lib.load()
