@@ -1,0 +1,157 @@
+/*
+ * mamba4_memread.h -- C ABI of the MI355X (gfx950) Mamba 4 memory read.
+ *
+ * Plain pointers and sizes only: every array is a contiguous float32 device
+ * buffer in the layout named next to it, owned by the caller.  `stream` is
+ * a hipStream_t passed as void* (NULL = the null stream).  No function
+ * allocates or frees caller memory, synchronises the device, or keeps
+ * state between calls other than an optional profiling log.  Functions are
+ * reentrant; calls on one stream run in order.
+ *
+ * Shapes: B batch, T tokens, H heads, key width D = 64 (M4MR_KEY_DIM),
+ * value width P = 64 (M4MR_VALUE_DIM), chunk c in [1, 64],
+ * NC = ceil(T / c) chunks.  Callers with narrower keys or values pad them
+ * with zeros (and the floor with ones); the padded coordinates then solve
+ * to zero and read nothing, as in lm/kernels/mamba4_fused.py:292-297.
+ *
+ * Return value: 0 on success, M4MR_EINVAL for a bad argument (nothing is
+ * launched), M4MR_EHIP for a HIP launch error.  m4mr_last_error() returns
+ * the calling thread's last message.  A non-positive pivot (for example a
+ * non-positive floor) is not an error: like the reference
+ * (lm/kernels/mamba4_fused.py:111) it propagates NaN.
+ */
+#ifndef MAMBA4_MEMREAD_H
+#define MAMBA4_MEMREAD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define M4MR_KEY_DIM 64
+#define M4MR_VALUE_DIM 64
+#define M4MR_MAX_CHUNK 64
+/* Packed lower factor per token-head: 64*65/2 floats, column-major, the
+ * diagonal holding the reciprocal pivot 1/L_jj (the reference keeps the
+ * same reciprocal convention, lm/kernels/mamba4_fused.py:113). */
+#define M4MR_FACTOR_FLOATS 2080
+
+#define M4MR_OK 0
+#define M4MR_EINVAL 1
+#define M4MR_EHIP 2
+
+/* Library version string, e.g. "mamba4_memread 0.1 gfx950". */
+const char* m4mr_version(void);
+
+/* Last error message of the calling thread ("" if none). */
+const char* m4mr_last_error(void);
+
+/*
+ * Forward memory read with stored factors.
+ *
+ * Replaces selective_memory_fused (lm/kernels/mamba4_fused.py:372-454) and
+ * the forward of its custom VJP, _chunk_solve_forward
+ * (lm/kernels/mamba4_fused.py:329-337), behind selective_gaussian_memory
+ * (lm/kernels/mamba4.py:228-262).
+ *
+ * inputs   keys, queries [B,T,H,D]; values [B,T,H,P]; beta, log_decay
+ *          [B,T,H]; floor [H,D]; init_evidence [B,H,D,D] and init_cross
+ *          [B,H,P,D] (both NULL for a zero initial state).
+ * outputs  output [B,T,H,P]; variance [B,T,H]; final_evidence [B,H,D,D];
+ *          final_cross [B,H,P,D].
+ * residuals (what the backward consumes; the reference tags the
+ *          equivalent arrays "memory_solve"):
+ *          solved [B,T,H,D] (y_t = A_t^-1 q_t);
+ *          factors [B,T,H,M4MR_FACTOR_FLOATS];
+ *          start_evidence [B,H,NC,D,D]; start_cross [B,H,NC,P,D].
+ */
+int m4mr_forward(const float* keys, const float* values, const float* queries,
+                 const float* beta, const float* log_decay, const float* floor,
+                 const float* init_evidence, const float* init_cross,
+                 int B, int T, int H, int chunk,
+                 float* output, float* variance,
+                 float* final_evidence, float* final_cross,
+                 float* solved, float* factors,
+                 float* start_evidence, float* start_cross,
+                 void* stream);
+
+/* Bytes of device workspace m4mr_backward needs for these sizes. */
+size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk);
+
+/*
+ * Backward of m4mr_forward: the VJP for every input and the initial state.
+ *
+ * Replaces _chunk_solve_backward (lm/kernels/mamba4_fused.py:340-366,
+ * including _factored_kernel :155-174 for z = A^-1 g) together with the
+ * JAX autodiff of the chunk glue around it (chunk statistics :411-415,
+ * carry lm/kernels/prefix.py:27-44, prefix sums prefix.py:17-24 and reads
+ * lm/kernels/mamba4_fused.py:439-447).  Only triangular solves with the
+ * stored factors are used; nothing is refactored.
+ *
+ * cotangents d_output [B,T,H,P]; d_variance [B,T,H]; d_final_evidence
+ *          [B,H,D,D] and d_final_cross [B,H,P,D] (NULL = zero).
+ * gradients d_keys, d_queries [B,T,H,D]; d_values [B,T,H,P]; d_beta,
+ *          d_log_decay [B,T,H]; d_floor [H,D]; d_init_evidence [B,H,D,D];
+ *          d_init_cross [B,H,P,D].  The evidence cotangents are the
+ *          symmetric form -(z y^T + y z^T)/2 of spd_solve's VJP
+ *          (lm/kernels/mamba4.py:208-215).
+ * workspace at least m4mr_backward_workspace_bytes(B, T, H, chunk) bytes,
+ *          256-byte aligned.
+ */
+int m4mr_backward(const float* keys, const float* values, const float* queries,
+                  const float* beta, const float* log_decay, const float* floor,
+                  int B, int T, int H, int chunk,
+                  const float* solved, const float* factors,
+                  const float* start_evidence, const float* start_cross,
+                  const float* d_output, const float* d_variance,
+                  const float* d_final_evidence, const float* d_final_cross,
+                  float* d_keys, float* d_values, float* d_queries,
+                  float* d_beta, float* d_log_decay, float* d_floor,
+                  float* d_init_evidence, float* d_init_cross,
+                  void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/*
+ * Triangular re-solve with stored factors: z_i = A_i^-1 rhs_i for N
+ * token-heads, factors [N, M4MR_FACTOR_FLOATS], rhs and z [N, D] (z may
+ * alias rhs).  Replaces factored_solve / _factored_kernel
+ * (lm/kernels/mamba4_fused.py:316-320,155-174).
+ */
+int m4mr_factored_solve(const float* factors, const float* rhs, float* z,
+                        long N, void* stream);
+
+/*
+ * One cached decode step, updating the state in place.
+ *
+ * Replaces selective_decode (lm/kernels/mamba4.py:341-355) for N = B*H
+ * independent states: evidence [N,D,D] and cross [N,P,D] are read and
+ * overwritten with lam*S + beta k k^T and lam*C + beta v k^T; key, query
+ * [N,D]; value [N,P]; beta, log_decay [N]; floor [H,D] with head = n % H.
+ * Writes output [N,P] = C y and variance [N] = q.y with
+ * (S + diag(floor)) y = q.
+ */
+int m4mr_decode_step(float* evidence, float* cross,
+                     const float* key, const float* value, const float* query,
+                     const float* beta, const float* log_decay, const float* floor,
+                     long N, int H,
+                     float* output, float* variance, void* stream);
+
+/*
+ * Kernel timing with HIP events recorded on the launch stream.  While
+ * enabled, every kernel launch is bracketed by a pair of events.
+ * m4mr_profile_read() waits for the recorded events and returns the total
+ * milliseconds and launch count of the kernels whose name equals `kernel`
+ * (see m4mr_profile_kernel_name), then m4mr_profile_reset() clears them.
+ */
+void m4mr_profile_enable(int on);
+void m4mr_profile_reset(void);
+int m4mr_profile_read(const char* kernel, double* total_ms, long* launches);
+/* Name of the i-th kernel the library launches, NULL past the end. */
+const char* m4mr_profile_kernel_name(int i);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA4_MEMREAD_H */

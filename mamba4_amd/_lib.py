@@ -1,0 +1,113 @@
+"""ctypes binding of the C ABI in include/mamba4_memread.h.
+
+``load()`` opens the in-tree ``libmamba4_memread.so`` and raises if it is
+missing: there is no fallback implementation.
+"""
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libmamba4_memread.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "mamba4_memread.h")
+
+EINVAL = 1
+EHIP = 2
+FACTOR_FLOATS = 2080
+KEY_DIM = 64
+VALUE_DIM = 64
+MAX_CHUNK = 64
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_long
+_S = ctypes.c_size_t
+
+SIGNATURES = {
+    "m4mr_version": (ctypes.c_char_p, []),
+    "m4mr_last_error": (ctypes.c_char_p, []),
+    "m4mr_forward": (_I, [_P] * 8 + [_I] * 4 + [_P] * 8 + [_P]),
+    "m4mr_backward_workspace_bytes": (_S, [_I] * 4),
+    "m4mr_backward": (
+        _I,
+        [_P] * 6 + [_I] * 4 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
+    ),
+    "m4mr_factored_solve": (_I, [_P, _P, _P, _L, _P]),
+    "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _P, _P, _P]),
+    "m4mr_profile_enable": (None, [_I]),
+    "m4mr_profile_reset": (None, []),
+    "m4mr_profile_read": (
+        _I,
+        [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)],
+    ),
+    "m4mr_profile_kernel_name": (ctypes.c_char_p, [_I]),
+}
+
+_lib = None
+
+
+class MemreadError(RuntimeError):
+    """A HIP launch failure reported by the library."""
+
+
+def header_functions():
+    """Names of the functions declared in include/mamba4_memread.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(m4mr_\w+)\s*\(", text, re.M)))
+
+
+def load():
+    """Open the HIP library (once) and attach the C signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIBRARY):
+        raise RuntimeError(
+            f"{LIBRARY} is not built; run `python -m mamba4_amd.build` "
+            "(the memory read has no non-HIP implementation)"
+        )
+    lib = ctypes.CDLL(LIBRARY)
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def check(rc):
+    """Raise the library's last error for a non-zero return code."""
+    if rc == 0:
+        return
+    message = load().m4mr_last_error().decode()
+    if rc == EINVAL:
+        raise ValueError(message)
+    raise MemreadError(message)
+
+
+def profile_enable(on=True):
+    load().m4mr_profile_enable(1 if on else 0)
+
+
+def profile_reset():
+    load().m4mr_profile_reset()
+
+
+def profile_read(kernel):
+    """(total milliseconds, launches) of one kernel since the last reset."""
+    total = ctypes.c_double()
+    count = ctypes.c_long()
+    check(load().m4mr_profile_read(kernel.encode(), ctypes.byref(total), ctypes.byref(count)))
+    return total.value, count.value
+
+
+def kernel_names():
+    lib = load()
+    names, i = [], 0
+    while True:
+        name = lib.m4mr_profile_kernel_name(i)
+        if name is None:
+            return names
+        names.append(name.decode())
+        i += 1

@@ -1,0 +1,354 @@
+// C ABI of the gfx950 memory read (declared in include/mamba4_memread.h).
+//
+// Each entry point validates its arguments on the host, then launches a
+// fixed sequence of kernels on the caller's stream.  Nothing here allocates
+// device memory or synchronises; the only global state is the optional
+// profiling log (mutex-protected) and a per-thread error message.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/mamba4_memread.h"
+#include "common.hpp"
+
+namespace m4 {
+__global__ void fwd_states_kernel(Dims, const float*, const float*, const float*, const float*,
+                                  const float*, const float*, float*, float*, float*, float*);
+__global__ void bwd_states_kernel(Dims, const float*, const float*, const float*, const float*,
+                                  const float*, const float*, const float*, float*, float*,
+                                  float*, float*);
+__global__ void fwd_factor_kernel(Dims, const float*, const float*, const float*, const float*,
+                                  const float*, const float*, float*, float*);
+__global__ void factored_solve_kernel(const float*, const float*, float*, long);
+__global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
+                                   const float*, const float*, const float*, int, float*, float*);
+__global__ void fwd_read_kernel(Dims, const float*, const float*, const float*, const float*,
+                                const float*, const float*, const float*, float*, float*);
+__global__ void bwd_dy_kernel(Dims, const float*, const float*, const float*, const float*,
+                              const float*, const float*, const float*, const float*, float*);
+__global__ void bwd_grads_kernel(Dims, const float*, const float*, const float*, const float*,
+                                 const float*, const float*, const float*, const float*,
+                                 const float*, const float*, const float*, const float*, float*,
+                                 float*, float*, float*, float*, float*);
+__global__ void floor_reduce_kernel(Dims, const float*, float*);
+}  // namespace m4
+
+namespace {
+
+using m4::Dims;
+
+thread_local std::string g_error;
+
+const char* const kKernelNames[] = {"fwd_states", "fwd_factor",     "fwd_read",
+                                    "bwd_dy",     "factored_solve", "bwd_states",
+                                    "bwd_grads",  "floor_reduce",   "decode_step"};
+
+struct ProfRecord {
+  const char* name;
+  hipEvent_t start, stop;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRecord> g_prof;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+constexpr size_t kChunkLdsBytes = 4 * m4::TILE * sizeof(float);
+constexpr size_t kGradsLdsBytes = 7 * m4::TILE * sizeof(float);
+
+bool configured = false;
+std::mutex g_cfg_mu;
+
+int configure() {
+  std::lock_guard<std::mutex> lock(g_cfg_mu);
+  if (configured) return M4MR_OK;
+  struct {
+    const void* fn;
+    size_t bytes;
+  } big[] = {{(const void*)m4::fwd_read_kernel, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel, kChunkLdsBytes},
+             {(const void*)m4::bwd_grads_kernel, kGradsLdsBytes}};
+  for (auto& k : big) {
+    hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)k.bytes);
+    if (e != hipSuccess)
+      return fail(M4MR_EHIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+  }
+  configured = true;
+  return M4MR_OK;
+}
+
+// Launch `body` on `stream`, bracketed by profiling events when enabled.
+template <typename F>
+int launch(const char* name, hipStream_t stream, F&& body) {
+  hipEvent_t a = nullptr, b = nullptr;
+  bool prof;
+  {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    prof = g_prof_on;
+  }
+  if (prof) {
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess ||
+        hipEventRecord(a, stream) != hipSuccess)
+      return fail(M4MR_EHIP, std::string(name) + ": profiling event setup failed");
+  }
+  body();
+  hipError_t e = hipGetLastError();
+  if (prof) {
+    if (hipEventRecord(b, stream) != hipSuccess)
+      return fail(M4MR_EHIP, std::string(name) + ": profiling event record failed");
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    g_prof.push_back({name, a, b});
+  }
+  if (e != hipSuccess) return fail(M4MR_EHIP, std::string(name) + ": " + hipGetErrorString(e));
+  return M4MR_OK;
+}
+
+bool bad_dims(int B, int T, int H, int chunk, std::string* why) {
+  if (B <= 0 || T <= 0 || H <= 0) {
+    *why = "B, T and H must be positive";
+    return true;
+  }
+  if (chunk < 1 || chunk > M4MR_MAX_CHUNK) {
+    *why = "chunk must lie in [1, 64]";
+    return true;
+  }
+  const double tokens = (double)B * T * H;
+  if (tokens * M4MR_FACTOR_FLOATS > 9.0e18 || (double)B * H > 2.0e9) {
+    *why = "problem too large";
+    return true;
+  }
+  return false;
+}
+
+Dims make_dims(int B, int T, int H, int chunk) {
+  Dims d;
+  d.B = B;
+  d.T = T;
+  d.H = H;
+  d.chunk = chunk;
+  d.NC = (T + chunk - 1) / chunk;
+  return d;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct BackwardWorkspace {
+  float *z, *end_s, *end_c, *floor_part;
+  size_t bytes;
+};
+
+BackwardWorkspace carve(void* base, int B, int T, int H, int chunk) {
+  const Dims d = make_dims(B, T, H, chunk);
+  const size_t tok = (size_t)B * T * H;
+  const size_t seqs = (size_t)B * H * d.NC;
+  size_t off = 0;
+  BackwardWorkspace w;
+  char* p = static_cast<char*>(base);
+  w.z = reinterpret_cast<float*>(p + off);
+  off = align256(off + tok * 64 * sizeof(float));
+  w.end_s = reinterpret_cast<float*>(p + off);
+  off = align256(off + seqs * 4096 * sizeof(float));
+  w.end_c = reinterpret_cast<float*>(p + off);
+  off = align256(off + seqs * 4096 * sizeof(float));
+  w.floor_part = reinterpret_cast<float*>(p + off);
+  off = align256(off + seqs * 64 * sizeof(float));
+  w.bytes = off;
+  return w;
+}
+
+bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* m4mr_version(void) { return "mamba4_memread 0.1 gfx950"; }
+
+const char* m4mr_last_error(void) { return g_error.c_str(); }
+
+int m4mr_forward(const float* keys, const float* values, const float* queries,
+                 const float* beta, const float* log_decay, const float* floor,
+                 const float* init_evidence, const float* init_cross, int B, int T, int H,
+                 int chunk, float* output, float* variance, float* final_evidence,
+                 float* final_cross, float* solved, float* factors, float* start_evidence,
+                 float* start_cross, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_dims(B, T, H, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_forward: " + why);
+  const void* need[] = {keys,     values,        queries,     beta,   log_decay,
+                        floor,    output,        variance,    final_evidence,
+                        final_cross, solved,     factors,     start_evidence, start_cross};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_forward: a required pointer is NULL");
+  if ((init_evidence == nullptr) != (init_cross == nullptr))
+    return fail(M4MR_EINVAL, "m4mr_forward: init_evidence and init_cross must both be set or both NULL");
+  const void* vec[] = {keys, values, queries, solved, factors, output, start_evidence,
+                       start_cross, final_evidence, final_cross, init_evidence, init_cross};
+  for (const void* p : vec)
+    if (p && misaligned(p)) return fail(M4MR_EINVAL, "m4mr_forward: arrays must be 16-byte aligned");
+  if (int rc = configure()) return rc;
+  const Dims d = make_dims(B, T, H, chunk);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned seqs = (unsigned)B * H * d.NC;
+  int rc = launch("fwd_states", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_states_kernel, dim3(B * H, 8), dim3(256), 0, st, d, keys, values,
+                       beta, log_decay, init_evidence, init_cross, start_evidence, start_cross,
+                       final_evidence, final_cross);
+  });
+  if (rc) return rc;
+  rc = launch("fwd_factor", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3(seqs), dim3(64), 0, st, d, keys, queries,
+                       beta, log_decay, floor, start_evidence, solved, factors);
+  });
+  if (rc) return rc;
+  return launch("fwd_read", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_read_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, keys,
+                       values, queries, beta, log_decay, solved, start_cross, output, variance);
+  });
+}
+
+size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk) {
+  std::string why;
+  if (bad_dims(B, T, H, chunk, &why)) return 0;
+  return carve(nullptr, B, T, H, chunk).bytes;
+}
+
+int m4mr_backward(const float* keys, const float* values, const float* queries,
+                  const float* beta, const float* log_decay, const float* floor, int B, int T,
+                  int H, int chunk, const float* solved, const float* factors,
+                  const float* start_evidence, const float* start_cross, const float* d_output,
+                  const float* d_variance, const float* d_final_evidence,
+                  const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
+                  float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
+                  float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_dims(B, T, H, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_backward: " + why);
+  const void* need[] = {keys,    values,     queries,         beta,         log_decay,
+                        floor,   solved,     factors,         start_evidence, start_cross,
+                        d_output, d_variance, d_keys,         d_values,     d_queries,
+                        d_beta,  d_log_decay, d_floor,        d_init_evidence, d_init_cross,
+                        workspace};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_backward: a required pointer is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(M4MR_EINVAL, "m4mr_backward: workspace must be 256-byte aligned");
+  const BackwardWorkspace ws = carve(workspace, B, T, H, chunk);
+  if (workspace_bytes < ws.bytes)
+    return fail(M4MR_EINVAL, "m4mr_backward: workspace too small (need " +
+                                 std::to_string(ws.bytes) + " bytes)");
+  const void* vec[] = {keys, values, queries, solved, factors, start_evidence, start_cross,
+                       d_output, d_final_evidence, d_final_cross, d_init_evidence, d_init_cross};
+  for (const void* p : vec)
+    if (p && misaligned(p)) return fail(M4MR_EINVAL, "m4mr_backward: arrays must be 16-byte aligned");
+  if (int rc = configure()) return rc;
+  const Dims d = make_dims(B, T, H, chunk);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned seqs = (unsigned)B * H * d.NC;
+  const long tokens = (long)B * T * H;
+  int rc = launch("bwd_dy", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_dy_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, keys,
+                       values, queries, beta, log_decay, start_cross, d_output, d_variance, ws.z);
+  });
+  if (rc) return rc;
+  rc = launch("factored_solve", st, [&] {
+    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0,
+                       st, factors, ws.z, ws.z, tokens);
+  });
+  if (rc) return rc;
+  rc = launch("bwd_states", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_states_kernel, dim3(B * H, 8), dim3(256), 0, st, d, beta,
+                       log_decay, solved, ws.z, d_output, d_final_evidence, d_final_cross,
+                       ws.end_s, ws.end_c, d_init_evidence, d_init_cross);
+  });
+  if (rc) return rc;
+  rc = launch("bwd_grads", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_grads_kernel, dim3(seqs), dim3(256), kGradsLdsBytes, st, d, keys,
+                       values, beta, log_decay, solved, ws.z, d_output, d_variance,
+                       start_evidence, start_cross, ws.end_s, ws.end_c, d_keys, d_values,
+                       d_queries, d_beta, d_log_decay, ws.floor_part);
+  });
+  if (rc) return rc;
+  return launch("floor_reduce", st, [&] {
+    hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H), dim3(64), 0, st, d, ws.floor_part,
+                       d_floor);
+  });
+}
+
+int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N,
+                        void* stream) {
+  g_error.clear();
+  if (N <= 0) return fail(M4MR_EINVAL, "m4mr_factored_solve: N must be positive");
+  if (!factors || !rhs || !z) return fail(M4MR_EINVAL, "m4mr_factored_solve: NULL pointer");
+  if (misaligned(factors)) return fail(M4MR_EINVAL, "m4mr_factored_solve: factors must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return launch("factored_solve", st, [&] {
+    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st,
+                       factors, rhs, z, N);
+  });
+}
+
+int m4mr_decode_step(float* evidence, float* cross, const float* key, const float* value,
+                     const float* query, const float* beta, const float* log_decay,
+                     const float* floor, long N, int H, float* output, float* variance,
+                     void* stream) {
+  g_error.clear();
+  if (N <= 0 || H <= 0 || N % H != 0)
+    return fail(M4MR_EINVAL, "m4mr_decode_step: N must be a positive multiple of H");
+  const void* need[] = {evidence, cross, key, value, query, beta, log_decay, floor, output, variance};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_decode_step: a required pointer is NULL");
+  if (misaligned(evidence) || misaligned(cross))
+    return fail(M4MR_EINVAL, "m4mr_decode_step: states must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return launch("decode_step", st, [&] {
+    hipLaunchKernelGGL(m4::decode_step_kernel, dim3((unsigned)N), dim3(64), 0, st, evidence, cross,
+                       key, value, query, beta, log_decay, floor, H, output, variance);
+  });
+}
+
+void m4mr_profile_enable(int on) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof_on = on != 0;
+}
+
+void m4mr_profile_reset(void) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  for (auto& r : g_prof) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  g_prof.clear();
+}
+
+int m4mr_profile_read(const char* kernel, double* total_ms, long* launches) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  double sum = 0.0;
+  long count = 0;
+  for (auto& r : g_prof) {
+    if (std::strcmp(r.name, kernel) != 0) continue;
+    if (hipEventSynchronize(r.stop) != hipSuccess) return fail(M4MR_EHIP, "profile: event sync failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess)
+      return fail(M4MR_EHIP, "profile: elapsed time failed");
+    sum += ms;
+    ++count;
+  }
+  if (total_ms) *total_ms = sum;
+  if (launches) *launches = count;
+  return M4MR_OK;
+}
+
+const char* m4mr_profile_kernel_name(int i) {
+  const int n = (int)(sizeof(kKernelNames) / sizeof(kKernelNames[0]));
+  return (i >= 0 && i < n) ? kKernelNames[i] : nullptr;
+}
+
+}  // extern "C"

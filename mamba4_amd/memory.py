@@ -1,0 +1,299 @@
+"""Mamba 4 selective memory read on MI355X: the lm/kernels/mamba4.py API.
+
+Same names, arguments, NamedTuples and error behaviour as the reference's
+``selective_gaussian_memory`` (lm/kernels/mamba4.py:228-338),
+``selective_decode`` (:341-355), ``selective_initial_state`` (:221-225),
+``SelectiveState`` / ``SelectiveResult`` (:18-28), with torch tensors on a
+ROCm device in place of JAX arrays.  Every call runs the gfx950 HIP library
+through its C ABI on the current torch stream; there is no other
+implementation, and CPU tensors are rejected.
+
+The forward stores each token's Cholesky factor, and the backward consumes
+the residual set the reference tags ``"memory_solve"``
+(lm/kernels/mamba4_fused.py:333-336): it issues only triangular solves and
+chunk contractions, never a second factorization.
+"""
+
+from typing import NamedTuple
+
+import torch
+import torch.nn.functional as F
+
+from mamba4_amd import _lib
+
+# Solver strings the reference accepts (lm/config.py:50,
+# lm/kernels/mamba4.py:164-182,249) plus "mi355x".  All of them select the
+# HIP path: the factorization backend changes only the arithmetic schedule,
+# never the solved system (lm/kernels/mamba4.py:193-194).
+SOLVERS = (None, "loop", "blocked", "unrolled", "auto", "fused", "mi355x")
+MEMORY_SOLVE = "memory_solve"
+
+
+class SelectiveState(NamedTuple):
+    """Evidence-only sufficient statistics; precision adds the fixed floor."""
+
+    evidence: torch.Tensor
+    cross: torch.Tensor
+
+
+class SelectiveResult(NamedTuple):
+    output: torch.Tensor
+    variance: torch.Tensor
+    state: SelectiveState
+
+
+def _check_solver(solver):
+    if solver not in SOLVERS:
+        raise ValueError(f"Unknown SPD solve backend {solver}")
+
+
+def _stream():
+    return ctypes_stream(torch.cuda.current_stream())
+
+
+def ctypes_stream(stream):
+    return stream.cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError(
+                "the MI355X memory read needs ROCm device tensors; got a CPU tensor"
+            )
+
+
+def selective_initial_state(batch, heads, key_dim, value_dim, device="cuda"):
+    return SelectiveState(
+        torch.zeros((batch, heads, key_dim, key_dim), dtype=torch.float32, device=device),
+        torch.zeros((batch, heads, value_dim, key_dim), dtype=torch.float32, device=device),
+    )
+
+
+class _MemoryRead(torch.autograd.Function):
+    """Custom VJP around m4mr_forward / m4mr_backward (fixed D = P = 64)."""
+
+    @staticmethod
+    def forward(ctx, keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk):
+        lib = _lib.load()
+        batch, time, heads, _ = keys.shape
+        count = -(-time // chunk)
+        dev = keys.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        output = torch.empty((batch, time, heads, _lib.VALUE_DIM), **f32)
+        variance = torch.empty((batch, time, heads), **f32)
+        final_s = torch.empty((batch, heads, 64, 64), **f32)
+        final_c = torch.empty((batch, heads, _lib.VALUE_DIM, 64), **f32)
+        solved = torch.empty((batch, time, heads, 64), **f32)
+        factors = torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
+        start_s = torch.empty((batch, heads, count, 64, 64), **f32)
+        start_c = torch.empty((batch, heads, count, _lib.VALUE_DIM, 64), **f32)
+        _lib.check(
+            lib.m4mr_forward(
+                _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
+                _ptr(floor), _ptr(init_s), _ptr(init_c), batch, time, heads, chunk,
+                _ptr(output), _ptr(variance), _ptr(final_s), _ptr(final_c),
+                _ptr(solved), _ptr(factors), _ptr(start_s), _ptr(start_c), _stream(),
+            )
+        )
+        # The residual set the reference checkpoints as "memory_solve".
+        ctx.save_for_backward(
+            keys, values, queries, beta, log_decay, floor, solved, factors, start_s, start_c
+        )
+        ctx.chunk = chunk
+        ctx.has_initial = init_s is not None
+        return output, variance, final_s, final_c
+
+    @staticmethod
+    def backward(ctx, d_output, d_variance, d_final_s, d_final_c):
+        lib = _lib.load()
+        (keys, values, queries, beta, log_decay, floor, solved, factors, start_s,
+         start_c) = ctx.saved_tensors
+        batch, time, heads, _ = keys.shape
+        chunk = ctx.chunk
+
+        def dense(g, like):
+            if g is None:
+                return torch.zeros_like(like)
+            return g.to(torch.float32).contiguous()
+
+        d_output = dense(d_output, values)
+        d_variance = dense(d_variance, beta)
+        d_final_s = None if d_final_s is None else d_final_s.to(torch.float32).contiguous()
+        d_final_c = None if d_final_c is None else d_final_c.to(torch.float32).contiguous()
+        grads = [torch.empty_like(t) for t in (keys, values, queries, beta, log_decay, floor)]
+        f32 = dict(dtype=torch.float32, device=keys.device)
+        d_init_s = torch.empty((batch, heads, _lib.KEY_DIM, _lib.KEY_DIM), **f32)
+        d_init_c = torch.empty((batch, heads, _lib.VALUE_DIM, _lib.KEY_DIM), **f32)
+        nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, chunk)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
+        _lib.check(
+            lib.m4mr_backward(
+                _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
+                _ptr(floor), batch, time, heads, chunk, _ptr(solved), _ptr(factors),
+                _ptr(start_s), _ptr(start_c), _ptr(d_output), _ptr(d_variance),
+                _ptr(d_final_s), _ptr(d_final_c), *(_ptr(g) for g in grads),
+                _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace), nbytes, _stream(),
+            )
+        )
+        d_init = (d_init_s, d_init_c) if ctx.has_initial else (None, None)
+        return (*grads, *d_init, None)
+
+
+def _pad_last(x, width, value=0.0):
+    extra = width - x.shape[-1]
+    return x if extra == 0 else F.pad(x, (0, extra), value=value)
+
+
+def selective_gaussian_memory(
+    keys,
+    values,
+    queries,
+    beta,
+    log_decay,
+    floor,
+    *,
+    chunk_size=64,
+    initial=None,
+    solver=None,
+):
+    """Exact chunked reads of the fixed-floor selective Gaussian memory.
+
+    keys/queries [B,T,H,D], values [B,T,H,P], beta and log_decay [B,T,H]
+    (log_decay <= 0), floor [H,D] positive; D, P <= 64.  With
+    S_t = lam_t S_(t-1) + beta_t k k^T and C_t likewise, each token reads
+    C_t y_t and q_t^T y_t where (S_t + diag(floor)) y_t = q_t.  Returns
+    SelectiveResult(output [B,T,H,P], variance [B,T,H],
+    SelectiveState(evidence [B,H,D,D], cross [B,H,P,D])); gradients reach
+    every input and ``initial``.
+    """
+    _check_solver(solver)
+    keys, values, queries = (torch.as_tensor(a) for a in (keys, values, queries))
+    batch, time, heads, dim = keys.shape
+    value_dim = values.shape[-1]
+    if queries.shape != keys.shape or values.shape[:3] != keys.shape[:3]:
+        raise ValueError("Selective memory keys, values and queries disagree")
+    _require_device(keys, values, queries)
+    keys, values, queries = (a.to(torch.float32) for a in (keys, values, queries))
+    if dim > _lib.KEY_DIM or value_dim > _lib.VALUE_DIM:
+        raise ValueError(
+            f"key and value widths must be <= {_lib.KEY_DIM}; got {dim} and {value_dim}"
+        )
+    if chunk_size < 1:
+        raise ValueError("chunk_size must be positive")
+    device = keys.device
+    shape = (batch, time, heads)
+    beta = torch.as_tensor(beta, dtype=torch.float32, device=device).expand(shape)
+    log_decay = torch.as_tensor(log_decay, dtype=torch.float32, device=device).expand(shape)
+    floor = torch.as_tensor(floor, dtype=torch.float32, device=device).expand(heads, dim)
+    _require_device(beta, log_decay, floor)
+    # Padded key coordinates form an identity block (zero keys, unit floor):
+    # they solve to zero and leave the true coordinates unchanged
+    # (lm/kernels/mamba4_fused.py:292-297).  Padded values read nothing.
+    k = _pad_last(keys, _lib.KEY_DIM).contiguous()
+    q = _pad_last(queries, _lib.KEY_DIM).contiguous()
+    v = _pad_last(values, _lib.VALUE_DIM).contiguous()
+    f = _pad_last(floor, _lib.KEY_DIM, value=1.0).contiguous()
+    init_s = init_c = None
+    if initial is not None:
+        init_s = torch.as_tensor(initial.evidence).to(torch.float32)
+        init_c = torch.as_tensor(initial.cross).to(torch.float32)
+        _require_device(init_s, init_c)
+        init_s = F.pad(init_s, (0, _lib.KEY_DIM - dim, 0, _lib.KEY_DIM - dim)).contiguous()
+        init_c = F.pad(
+            init_c, (0, _lib.KEY_DIM - dim, 0, _lib.VALUE_DIM - value_dim)
+        ).contiguous()
+    chunk = min(int(chunk_size), _lib.MAX_CHUNK)
+    with torch.cuda.device(device):
+        output, variance, final_s, final_c = _MemoryRead.apply(
+            k, v, q, beta.contiguous(), log_decay.contiguous(), f, init_s, init_c, chunk
+        )
+    return SelectiveResult(
+        output[..., :value_dim],
+        variance,
+        SelectiveState(final_s[..., :dim, :dim], final_c[..., :value_dim, :dim]),
+    )
+
+
+def selective_decode(state, key, value, query, beta, log_decay, floor, solver=None):
+    """One exact write/read from a cached state: O(D^3 + P D) refactor.
+
+    state.evidence [B,H,D,D], state.cross [B,H,P,D]; key/query [B,H,D];
+    value [B,H,P]; beta/log_decay [B,H]; floor [H,D].  Returns
+    SelectiveResult(output [B,H,P], variance [B,H], new state); the input
+    state is not modified (see ``selective_decode_`` for the in-place form).
+    Widths below 64 are zero-padded like the prefill path.
+    """
+    _check_solver(solver)
+    evidence = torch.as_tensor(state.evidence)
+    cross = torch.as_tensor(state.cross)
+    _require_device(evidence, cross)
+    dim, value_dim = evidence.shape[-1], cross.shape[-2]
+    if dim > _lib.KEY_DIM or value_dim > _lib.VALUE_DIM:
+        raise ValueError(
+            f"key and value widths must be <= {_lib.KEY_DIM}; got {dim} and {value_dim}"
+        )
+    kd, vd = _lib.KEY_DIM - dim, _lib.VALUE_DIM - value_dim
+    padded = SelectiveState(
+        F.pad(evidence.to(torch.float32), (0, kd, 0, kd)).contiguous(),
+        F.pad(cross.to(torch.float32), (0, kd, 0, vd)).contiguous(),
+    )
+    device = evidence.device
+    floor = torch.as_tensor(floor, dtype=torch.float32, device=device).expand(
+        evidence.shape[1], dim
+    )
+    out = selective_decode_(
+        padded,
+        _pad_last(torch.as_tensor(key, device=device).to(torch.float32), _lib.KEY_DIM),
+        _pad_last(torch.as_tensor(value, device=device).to(torch.float32), _lib.VALUE_DIM),
+        _pad_last(torch.as_tensor(query, device=device).to(torch.float32), _lib.KEY_DIM),
+        beta,
+        log_decay,
+        _pad_last(floor, _lib.KEY_DIM, value=1.0),
+        solver,
+    )
+    return SelectiveResult(
+        out.output[..., :value_dim],
+        out.variance,
+        SelectiveState(
+            out.state.evidence[..., :dim, :dim], out.state.cross[..., :value_dim, :dim]
+        ),
+    )
+
+
+def selective_decode_(state, key, value, query, beta, log_decay, floor, solver=None):
+    """In-place ``selective_decode``: overwrites ``state`` with the new state.
+
+    Needs float32 contiguous state tensors with D = P = 64.
+    """
+    _check_solver(solver)
+    lib = _lib.load()
+    evidence, cross = state.evidence, state.cross
+    _require_device(evidence, cross)
+    batch, heads, dim, _ = evidence.shape
+    value_dim = cross.shape[-2]
+    if (dim, value_dim) != (_lib.KEY_DIM, _lib.VALUE_DIM):
+        raise ValueError("the in-place decode needs D = P = 64 states")
+    if evidence.dtype != torch.float32 or not evidence.is_contiguous() or not cross.is_contiguous():
+        raise ValueError("the in-place decode needs contiguous float32 states")
+    device = evidence.device
+    f32 = dict(dtype=torch.float32, device=device)
+    key, value, query = (torch.as_tensor(a).to(**f32).contiguous() for a in (key, value, query))
+    beta = torch.as_tensor(beta, **f32).expand(batch, heads).contiguous()
+    log_decay = torch.as_tensor(log_decay, **f32).expand(batch, heads).contiguous()
+    floor = torch.as_tensor(floor, **f32).expand(heads, dim).contiguous()
+    output = torch.empty((batch, heads, value_dim), **f32)
+    variance = torch.empty((batch, heads), **f32)
+    with torch.cuda.device(device):
+        _lib.check(
+            lib.m4mr_decode_step(
+                _ptr(evidence), _ptr(cross), _ptr(key), _ptr(value), _ptr(query),
+                _ptr(beta), _ptr(log_decay), _ptr(floor), batch * heads, heads,
+                _ptr(output), _ptr(variance), _stream(),
+            )
+        )
+    return SelectiveResult(output, variance, state)

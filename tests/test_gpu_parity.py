@@ -1,0 +1,216 @@
+"""GPU parity of the HIP memory read against the pinned CPU oracle.
+
+Tolerances (fp32 HIP vs float64 oracle):
+* reference test shapes (floor >= 0.25): the reference's own tolerances,
+  values rtol 3e-5 / atol 3e-6 (lm/tests/test_mamba4.py:43), gradients
+  rtol 2e-4 / atol 2e-5 (:103, :404);
+* benchmark configs (floor 1e-2): normwise max|d| / max|ref| <= 1e-4 on
+  outputs and state, <= 1e-3 on gradients.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import memread as oracle
+from tests.gpu_helpers import NAMES, announce, host, normwise, run_gpu, to_device
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "config0.npz")
+
+
+def arrays(time=13, heads=3, dim=4, value_dim=5, seed=0, batch=2):
+    """The reference test fixture's distributions (lm/tests/test_mamba4.py:19-29)."""
+    rng = np.random.default_rng(seed)
+    k = rng.normal(size=(batch, time, heads, dim)).astype(np.float32)
+    q = rng.normal(size=k.shape).astype(np.float32)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    v = rng.normal(size=(batch, time, heads, value_dim)).astype(np.float32)
+    beta = rng.uniform(0.05, 1.0, size=k.shape[:-1]).astype(np.float32)
+    decay = rng.uniform(0.3, 0.999, size=k.shape[:-1]).astype(np.float32)
+    floor = rng.uniform(0.25, 1.5, size=(heads, dim)).astype(np.float32)
+    return dict(keys=k, values=v, queries=q, beta=beta, log_decay=np.log(decay), floor=floor)
+
+
+@pytest.mark.parametrize("chunk", [1, 4, 5, 13, 16, 64])
+def test_chunked_reads_match_dense_oracle(gpu_lib, chunk):
+    # lm/tests/test_mamba4.py:32-43, every chunk size incl. padded chunks.
+    data = arrays()
+    announce(f"chunked reads chunk={chunk} B2 T13 H3 D4 P5")
+    got = run_gpu(data, chunk=chunk)
+    want = oracle.dense_reference(*(data[n] for n in NAMES))
+    for key, ref in zip(["output", "variance", "evidence", "cross"], want):
+        np.testing.assert_allclose(got[key], ref, rtol=3e-5, atol=3e-6, err_msg=key)
+
+
+@pytest.mark.parametrize("chunk", [4, 8, 64])
+def test_all_gradients_match_oracle(gpu_lib, chunk):
+    # lm/tests/test_mamba4.py:84-104 and :382-404, with an initial state and
+    # cotangents on every output including the final state.
+    data = arrays(time=21, dim=6)
+    rng = np.random.default_rng(12)
+    root = rng.normal(size=(2, 3, 6, 6)) / 6
+    s0 = (root @ np.swapaxes(root, -1, -2)).astype(np.float32)
+    c0 = (rng.normal(size=(2, 3, 5, 6)) * 0.3).astype(np.float32)
+    d_out = rng.normal(size=data["values"].shape).astype(np.float32)
+    d_var = rng.normal(size=data["beta"].shape).astype(np.float32)
+    d_s = rng.normal(size=s0.shape).astype(np.float32)
+    d_s = 0.5 * (d_s + np.swapaxes(d_s, -1, -2))
+    d_c = rng.normal(size=c0.shape).astype(np.float32)
+    announce(f"gradients chunk={chunk} B2 T21 H3 D6 P5")
+    got = run_gpu(data, chunk=chunk, initial=(s0, c0), cotangents=(d_out, d_var, d_s, d_c))
+    args = [data[n].astype(np.float64) for n in NAMES]
+    _, res = oracle.forward(*args, chunk=chunk, initial=(s0, c0))
+    want = oracle.backward(res, d_out, d_var, d_s, d_c)
+    for n in NAMES:
+        np.testing.assert_allclose(got["d_" + n], want[n], rtol=2e-4, atol=2e-5, err_msg=n)
+        assert np.linalg.norm(got["d_" + n]) > 1e-6, n
+    np.testing.assert_allclose(
+        got["d_initial_evidence"], want["initial_evidence"], rtol=2e-4, atol=2e-5
+    )
+    np.testing.assert_allclose(got["d_initial_cross"], want["initial_cross"], rtol=2e-4, atol=2e-5)
+
+
+def test_config0_matches_golden_fixture(gpu_lib):
+    g = np.load(GOLDEN)
+    data = {n: g["in_" + n] for n in NAMES}
+    cot = (g["d_output"], g["d_variance"], g["d_final_evidence"], g["d_final_cross"])
+    announce("config0 golden B2 L256 H1 D64 fwd+bwd")
+    got = run_gpu(data, chunk=64, cotangents=cot)
+    for key in ["output", "variance", "evidence", "cross"]:
+        err = normwise(got[key], g[key])
+        assert err <= 1e-4, (key, err)
+    for n in NAMES:
+        err = normwise(got["d_" + n], g["grad_" + n])
+        assert err <= 1e-3, (n, err)
+
+
+def test_config0_chunk_sizes_agree_with_golden(gpu_lib):
+    g = np.load(GOLDEN)
+    data = {n: g["in_" + n] for n in NAMES}
+    for chunk in (16, 32, 37):
+        announce(f"config0 chunk={chunk}")
+        got = run_gpu(data, chunk=chunk)
+        assert normwise(got["output"], g["output"]) <= 1e-4, chunk
+        assert normwise(got["variance"], g["variance"]) <= 1e-4, chunk
+
+
+def test_continuation_and_decode_match_prefill(gpu_lib):
+    # lm/tests/test_mamba4.py:107-134.
+    from mamba4_amd import SelectiveState, selective_decode, selective_gaussian_memory
+
+    data = arrays()
+    announce("continuation + decode B2 T13 H3 D4 P5")
+    full = run_gpu(data, chunk=4)
+    first = run_gpu({n: (data[n][:, :6] if n != "floor" else data[n]) for n in NAMES}, chunk=4)
+    second = run_gpu(
+        {n: (data[n][:, 6:] if n != "floor" else data[n]) for n in NAMES},
+        chunk=4,
+        initial=(first["evidence"], first["cross"]),
+    )
+    np.testing.assert_allclose(second["output"], full["output"][:, 6:], rtol=3e-5, atol=3e-6)
+    dev = torch.device("cuda:0")
+    state = SelectiveState(torch.zeros(2, 3, 4, 4, device=dev), torch.zeros(2, 3, 5, 4, device=dev))
+    t = lambda a: torch.tensor(a, device=dev)  # noqa: E731
+    for i in range(13):
+        step = selective_decode(
+            state, t(data["keys"][:, i]), t(data["values"][:, i]), t(data["queries"][:, i]),
+            t(data["beta"][:, i]), t(data["log_decay"][:, i]), t(data["floor"]),
+        )
+        state = step.state
+        np.testing.assert_allclose(host(step.output), full["output"][:, i], rtol=3e-5, atol=3e-6)
+        np.testing.assert_allclose(host(step.variance), full["variance"][:, i], rtol=3e-5, atol=3e-6)
+    np.testing.assert_allclose(host(state.evidence), full["evidence"], rtol=3e-5, atol=3e-6)
+
+
+def test_exact_recall_of_orthonormal_keys(gpu_lib):
+    # lm/tests/test_mamba4.py:137-152: read(k_i) = v_i / (1 + floor / beta).
+    dim, value_dim = 4, 3
+    keys = np.eye(dim, dtype=np.float32)[None, :, None, :]
+    values = np.random.default_rng(1).normal(size=(1, dim, 1, value_dim)).astype(np.float32)
+    data = dict(
+        keys=keys, values=values, queries=keys, beta=np.full((1, dim, 1), 2.0, np.float32),
+        log_decay=np.zeros((1, dim, 1), np.float32), floor=np.full((1, dim), 1e-3, np.float32),
+    )
+    announce("exact recall")
+    got = run_gpu(data, chunk=2)
+    np.testing.assert_allclose(got["output"], values / (1 + 5e-4), rtol=1e-5)
+
+
+def test_stored_factors_reproduce_each_precision(gpu_lib):
+    """Calls m4mr_forward through the C ABI and unpacks the packed factors."""
+    data = arrays(time=10, heads=2, dim=64, value_dim=64, seed=3)
+    data["floor"] = np.full_like(data["floor"], 0.05)
+    B, T, H, c = 2, 10, 2, 4
+    dev = torch.device("cuda:0")
+    ins = to_device([data[n] for n in NAMES])
+    f32 = dict(dtype=torch.float32, device=dev)
+    count = -(-T // c)
+    outs = dict(
+        output=torch.empty(B, T, H, 64, **f32), variance=torch.empty(B, T, H, **f32),
+        final_s=torch.empty(B, H, 64, 64, **f32), final_c=torch.empty(B, H, 64, 64, **f32),
+        solved=torch.empty(B, T, H, 64, **f32), factors=torch.empty(B, T, H, 2080, **f32),
+        start_s=torch.empty(B, H, count, 64, 64, **f32), start_c=torch.empty(B, H, count, 64, 64, **f32),
+    )
+    announce("C-ABI forward, factor unpack B2 T10 H2 D64")
+    rc = gpu_lib.m4mr_forward(
+        *(t.data_ptr() for t in ins), None, None, B, T, H, c,
+        *(t.data_ptr() for t in outs.values()), torch.cuda.current_stream().cuda_stream,
+    )
+    assert rc == 0, gpu_lib.m4mr_last_error()
+    torch.cuda.synchronize()
+    packed = host(outs["factors"])
+    lower = np.zeros((B, T, H, 64, 64))
+    for j in range(64):
+        start = j * 64 - j * (j - 1) // 2
+        lower[..., j:, j] = packed[..., start : start + 64 - j]
+    diag = np.einsum("...ii->...i", lower)
+    true_lower = np.tril(lower, -1) + np.einsum("...i,ij->...ij", 1 / diag, np.eye(64))
+    rebuilt = true_lower @ np.swapaxes(true_lower, -1, -2)
+    for t in range(T):
+        _, _, s_t, _ = oracle.dense_reference(
+            *(data[n][:, : t + 1] if n != "floor" else data[n] for n in NAMES)
+        )
+        a_t = s_t + data["floor"][None, :, :, None] * np.eye(64)
+        assert normwise(rebuilt[:, t], a_t) < 1e-5, t
+    y = np.linalg.solve(
+        rebuilt, data["queries"].astype(np.float64)[..., None]
+    )[..., 0]
+    assert normwise(host(outs["solved"]), y) < 1e-4
+
+
+def test_factored_solve_entry_point(gpu_lib):
+    rng = np.random.default_rng(8)
+    N = 37
+    a = rng.normal(size=(N, 64, 64))
+    a = a @ np.swapaxes(a, -1, -2) / 64 + 0.1 * np.eye(64)
+    lower = oracle.cholesky_reciprocal(a)
+    packed = np.concatenate([lower[:, j:, j] for j in range(64)], axis=1)
+    rhs = rng.normal(size=(N, 64))
+    fac, r = to_device([packed, rhs])
+    z = torch.empty_like(r)
+    announce("factored_solve N=37")
+    rc = gpu_lib.m4mr_factored_solve(
+        fac.data_ptr(), r.data_ptr(), z.data_ptr(), N, torch.cuda.current_stream().cuda_stream
+    )
+    assert rc == 0
+    torch.cuda.synchronize()
+    want = np.linalg.solve(a, rhs[..., None])[..., 0]
+    assert normwise(host(z), want) < 1e-4
+
+
+def test_nonpositive_floor_propagates_nan(gpu_lib):
+    # Failure mode of the reference (lm/kernels/mamba4_fused.py:111): a
+    # non-positive pivot gives NaN rather than an error.
+    data = arrays(time=5)
+    data["keys"][:, 0] = 0.0
+    data["floor"][0, 0] = -1.0
+    announce("negative floor NaN propagation")
+    got = run_gpu(data, chunk=4)
+    assert np.isnan(got["variance"][:, 0, 0]).all()
+    assert np.isfinite(got["variance"][:, :, 1:]).all()

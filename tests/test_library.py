@@ -1,0 +1,86 @@
+"""Host-only checks of the C ABI and the Python boundary (no GPU needed)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from mamba4_amd import _lib
+from mamba4_amd import memory
+
+
+def test_library_exports_every_header_function():
+    lib = _lib.load()
+    names = _lib.header_functions()
+    assert "m4mr_forward" in names and "m4mr_backward" in names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of date"
+
+
+def test_version_and_kernel_names():
+    lib = _lib.load()
+    assert lib.m4mr_version().decode().startswith("mamba4_memread")
+    names = _lib.kernel_names()
+    assert "fwd_factor" in names and "factored_solve" in names
+
+
+def test_invalid_sizes_are_rejected_before_any_launch():
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    rc = lib.m4mr_forward(*([null] * 8), 0, 16, 1, 64, *([null] * 8), null)
+    assert rc == _lib.EINVAL
+    assert "positive" in lib.m4mr_last_error().decode()
+    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 65, *([null] * 8), null)
+    assert rc == _lib.EINVAL
+    assert "chunk" in lib.m4mr_last_error().decode()
+    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 16, *([null] * 8), null)
+    assert rc == _lib.EINVAL
+    assert "NULL" in lib.m4mr_last_error().decode()
+    rc = lib.m4mr_decode_step(*([null] * 8), 6, 4, null, null, null)
+    assert rc == _lib.EINVAL
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EINVAL)
+
+
+def test_workspace_size_covers_every_intermediate():
+    B, T, H, c = 2, 100, 3, 16
+    count = -(-T // c)
+    need = _lib.load().m4mr_backward_workspace_bytes(B, T, H, c)
+    floats = B * T * H * 64 + 2 * B * H * count * 4096 + B * H * count * 64
+    assert need >= 4 * floats
+    assert need % 256 == 0
+    assert _lib.load().m4mr_backward_workspace_bytes(B, T, H, 0) == 0
+
+
+def test_python_api_rejects_cpu_tensors_and_unknown_solvers():
+    k = torch.zeros(1, 4, 1, 8)
+    v = torch.zeros(1, 4, 1, 8)
+    with pytest.raises(ValueError, match="ROCm device"):
+        memory.selective_gaussian_memory(k, v, k, 0.5, -0.1, torch.ones(1, 8))
+    with pytest.raises(ValueError, match="Unknown SPD solve backend"):
+        memory.selective_gaussian_memory(k, v, k, 0.5, -0.1, torch.ones(1, 8), solver="qr")
+
+
+def test_shape_mismatch_message_matches_reference():
+    k = torch.zeros(1, 4, 1, 8)
+    with pytest.raises(ValueError, match="keys, values and queries disagree"):
+        memory.selective_gaussian_memory(
+            k, torch.zeros(1, 5, 1, 8), k, 0.5, -0.1, torch.ones(1, 8)
+        )
+
+
+def test_synthetic_inputs_follow_the_documented_distributions():
+    from mamba4_amd.inputs import synthetic_inputs, round_to_bf16
+
+    d = synthetic_inputs(2, 64, 3, cotangents=True)
+    assert np.all(d["keys"][:, 0] == 0)  # shifted: the first write has a zero key
+    np.testing.assert_allclose(np.linalg.norm(d["keys"][:, 1:], axis=-1), 1, rtol=1e-6)
+    np.testing.assert_allclose(np.linalg.norm(d["queries"], axis=-1), 1, rtol=1e-6)
+    assert np.all(d["log_decay"] < 0) and np.all((d["beta"] > 0) & (d["beta"] < 1))
+    assert d["floor"].shape == (3, 64) and np.all(d["floor"] == np.float32(1e-2))
+    x = np.array([1.0, 1.00390625, 1.0078125, 3.14159], np.float32)
+    np.testing.assert_array_equal(
+        round_to_bf16(x), torch.tensor(x).to(torch.bfloat16).float().numpy()
+    )
