@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Memory-read fwd+bwd benchmark on one MI355X (BASELINE.json metric).
+
+A step is one forward (chunk states, per-token factor + solve + factor
+store, reads) and one backward (dy, factored re-solve, reverse carry,
+gradient contractions, floor reduction) of the memory read over one batch
+of synthetic config-2 input (B=16, L=1024, H=8, D=P=64, fp32), called
+through the C ABI with every buffer preallocated in HBM before the timed
+region.  Prints one JSON line with the throughput, the roofline of the
+dominant kernel (HIP events on the launch stream), the factorization's
+fp32 rate, factor-streaming bandwidth and a CPU baseline (the NumPy oracle
+on a one-row sample of the same workload, on this host's cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+CORES = len(os.sched_getaffinity(0))
+for _var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+    os.environ.setdefault(_var, str(CORES))
+
+import numpy as np  # noqa: E402
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "memory-read fwd+bwd tokens/sec at B16 L1024 H8 d64; % fp32 peak, % HBM BW"
+HBM_PEAK_GBPS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+FACTOR_BYTES = 8320  # packed lower factor per token-head
+CHOLESKY_FLOP = 89440  # D^3/3 + D^2/2 + D/6 at D = 64
+RESOLVE_BYTES = 8832  # factor + rhs + z per token-head in the backward re-solve
+
+NAMES = ["keys", "values", "queries", "beta", "log_decay", "floor"]
+
+# Algorithmic work per token-head of each kernel at D = P = 64, chunk 64:
+# (bound, amount, unit).  HBM kernels count the bytes their algorithm must
+# move; contraction kernels count 2 flop per multiply-add of their products.
+KERNEL_WORK = {
+    "fwd_factor": ("hbm", FACTOR_BYTES, "B"),
+    "factored_solve": ("hbm", RESOLVE_BYTES, "B"),
+    "fwd_read": ("mfma", 3 * 8192, "flop"),  # Y K^T, (G) V, Y C0^T
+    "bwd_dy": ("mfma", 3 * 8192, "flop"),  # dO V^T, (G) K, dO C0
+    "bwd_grads": ("mfma", 13 * 8192, "flop"),  # 13 chunk products
+    "fwd_states": ("mfma", 2 * 8192, "flop"),  # K^T diag K, V^T diag K
+    "bwd_states": ("mfma", 3 * 8192, "flop"),  # sym(Z^T Y), dO^T Y
+    "floor_reduce": ("hbm", 4, "B"),
+}
+
+
+def roofline(kernel, ms, token_heads):
+    bound, amount, unit = KERNEL_WORK[kernel]
+    seconds = ms / 1e3
+    if bound == "hbm":
+        achieved = amount * token_heads / seconds / 1e9
+        peak, unit_out = HBM_PEAK_GBPS, "GB/s"
+    else:
+        achieved = amount * token_heads / seconds / 1e12
+        peak, unit_out = FP32_PEAK_TFLOPS, "TFLOP/s"
+    return {
+        "kernel": kernel,
+        "bound": bound,
+        "achieved": achieved,
+        "peak": peak,
+        "unit": unit_out,
+        "frac": achieved / peak,
+        "traffic": None,
+    }
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--chunk", type=int, default=64)
+    p.add_argument("--workload", default="config2", choices=["config2"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+class Problem:
+    """Device buffers for one fwd+bwd step through the C ABI."""
+
+    def __init__(self, data, chunk):
+        import torch
+
+        from mamba4_amd import _lib
+
+        self.lib = _lib.load()
+        self.check = _lib.check
+        dev = torch.device("cuda:0")
+        self.B, self.T, self.H, _ = data["keys"].shape
+        self.chunk = chunk
+        count = -(-self.T // chunk)
+        B, T, H = self.B, self.T, self.H
+
+        def put(a):
+            return torch.tensor(np.asarray(a, np.float32), device=dev)
+
+        self.inputs = [put(data[n]) for n in NAMES]
+        self.d_output = put(data["d_output"])
+        self.d_variance = put(data["d_variance"])
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.fwd_out = [
+            torch.empty(B, T, H, 64, **f32),  # output
+            torch.empty(B, T, H, **f32),  # variance
+            torch.empty(B, H, 64, 64, **f32),  # final evidence
+            torch.empty(B, H, 64, 64, **f32),  # final cross
+            torch.empty(B, T, H, 64, **f32),  # solved
+            torch.empty(B, T, H, _lib.FACTOR_FLOATS, **f32),  # factors
+            torch.empty(B, H, count, 64, 64, **f32),  # start evidence
+            torch.empty(B, H, count, 64, 64, **f32),  # start cross
+        ]
+        self.grads = [torch.empty_like(t) for t in self.inputs]
+        self.d_init = [torch.empty(B, H, 64, 64, **f32), torch.empty(B, H, 64, 64, **f32)]
+        self.ws_bytes = self.lib.m4mr_backward_workspace_bytes(B, T, H, chunk)
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def forward(self):
+        p = [t.data_ptr() for t in self.inputs]
+        o = [t.data_ptr() for t in self.fwd_out]
+        self.check(
+            self.lib.m4mr_forward(*p, None, None, self.B, self.T, self.H, self.chunk, *o,
+                                  self.stream)
+        )
+
+    def backward(self):
+        p = [t.data_ptr() for t in self.inputs]
+        o = self.fwd_out
+        self.check(
+            self.lib.m4mr_backward(
+                *p, self.B, self.T, self.H, self.chunk, o[4].data_ptr(), o[5].data_ptr(),
+                o[6].data_ptr(), o[7].data_ptr(), self.d_output.data_ptr(),
+                self.d_variance.data_ptr(), None, None, *(g.data_ptr() for g in self.grads),
+                *(g.data_ptr() for g in self.d_init), self.workspace.data_ptr(), self.ws_bytes,
+                self.stream,
+            )
+        )
+
+
+def copy_bandwidth_gbps():
+    """Read+write bandwidth of a 2 GiB device-to-device copy (torch copy_)."""
+    import torch
+
+    n = 1 << 29
+    a = torch.empty(n, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    start.record()
+    for _ in range(reps):
+        b.copy_(a)
+    stop.record()
+    torch.cuda.synchronize()
+    seconds = start.elapsed_time(stop) / 1e3 / reps
+    del a, b
+    return 2 * n * 4 / seconds / 1e9
+
+
+def cpu_baseline(data):
+    """The NumPy oracle (float32) on batch row 0 of the workload, fwd+bwd."""
+    from oracle import memread as oracle
+
+    row = {n: data[n][:1] for n in NAMES if n != "floor"}
+    row["floor"] = data["floor"]
+    start = time.perf_counter()
+    _, res = oracle.forward(*(row[n] for n in NAMES), chunk=64, dtype=np.float32)
+    oracle.backward(res, data["d_output"][:1], data["d_variance"][:1])
+    seconds = time.perf_counter() - start
+    tokens = row["keys"].shape[1]
+    _, T, H, D = row["keys"].shape
+    return {
+        "value": tokens / seconds,
+        "unit": "tokens/s",
+        "cores": int(os.environ.get("OPENBLAS_NUM_THREADS", CORES)),
+        "kind": "port",
+        "sample": (
+            f"oracle.memread fwd+bwd in float32 NumPy on batch row 0 of the workload "
+            f"(B=1, L={T}, H={H}, D={D}; 1/16 of config 2), {seconds:.1f} s, "
+            f"BLAS threads = {os.environ.get('OPENBLAS_NUM_THREADS')}"
+        ),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py measures one MI355X: the memory read shards over (batch, head) with "
+            "no communication, and this build runs on one GPU only; use --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from mamba4_amd import _lib
+    from mamba4_amd.inputs import workload_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        sys.exit(2)
+    data = workload_inputs(args.workload, seed=0, cotangents=True)
+    problem = Problem(data, args.chunk)
+    B, T, H = problem.B, problem.T, problem.H
+    token_heads = B * T * H
+
+    for _ in range(args.warmup):
+        problem.forward()
+        problem.backward()
+    torch.cuda.synchronize()
+
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        problem.forward()
+        problem.backward()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.profile_enable(False)
+    seconds = (t1 - t0) / args.steps
+    kernels = {}
+    for name in _lib.kernel_names():
+        total, count = _lib.profile_read(name)
+        if count:
+            kernels[name] = total / count
+    _lib.profile_reset()
+
+    dominant = max(kernels, key=kernels.get)
+    factor_s = kernels["fwd_factor"] / 1e3
+    resolve_s = kernels["factored_solve"] / 1e3
+    store_gbps = FACTOR_BYTES * token_heads / factor_s / 1e9
+    load_gbps = RESOLVE_BYTES * token_heads / resolve_s / 1e9
+    copy_gbps = copy_bandwidth_gbps()
+
+    line = {
+        "metric": METRIC,
+        "value": B * T / seconds,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": seconds * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "config2: memory-read fwd+bwd, B=16 L=1024 H=8 D=P=64 fp32, floor 1e-2",
+            "batch": B,
+            "seq_len": T,
+            "heads": H,
+            "key_dim": 64,
+            "value_dim": 64,
+            "chunk": args.chunk,
+        },
+        "roofline": roofline(dominant, kernels[dominant], token_heads),
+        "factorization_fp32": {
+            "kernel": "fwd_factor",
+            "achieved_tflops": CHOLESKY_FLOP * token_heads / factor_s / 1e12,
+            "peak_tflops": FP32_PEAK_TFLOPS,
+            "frac": CHOLESKY_FLOP * token_heads / factor_s / 1e12 / FP32_PEAK_TFLOPS,
+        },
+        "factor_streaming_hbm": {
+            "store_GBps": store_gbps,
+            "store_frac": store_gbps / HBM_PEAK_GBPS,
+            "load_GBps": load_gbps,
+            "load_frac": load_gbps / HBM_PEAK_GBPS,
+            "copy_kernel_GBps": copy_gbps,
+        },
+        "kernel_ms": kernels,
+        "kernel_roofline": {k: roofline(k, v, token_heads)["frac"] for k, v in kernels.items()},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(data)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

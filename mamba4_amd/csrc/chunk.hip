@@ -381,14 +381,27 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   }
 }
 
-// d floor[h][c] = sum_{b, n} floor_part[(b*H + h)*NC + n][c], fixed order.
-__global__ __launch_bounds__(64) void floor_reduce_kernel(Dims d, const float* __restrict__ part,
-                                                         float* __restrict__ d_floor) {
-  const int h = blockIdx.x, c = threadIdx.x;
-  float v = 0.f;
-  for (int b = 0; b < d.B; ++b)
-    for (int n = 0; n < d.NC; ++n) v += part[(((long)b * d.H + h) * d.NC + n) * 64 + c];
-  d_floor[h * 64 + c] = v;
+// d floor[h][c] = sum_{b, n} floor_part[(b*H + h)*NC + n][c] in a fixed
+// order: thread (q, c4) sums entries e = q, q+16, ... of the flattened
+// (b, n) index as float4 columns 4c4..4c4+3, then the 16 partials are added
+// in q order.  Deterministic run to run.
+__global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* __restrict__ part,
+                                                          float* __restrict__ d_floor) {
+  const int h = blockIdx.x, q = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+  const int entries = d.B * d.NC;
+  __shared__ f4 partial[16][16];
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+  for (int e = q; e < entries; e += 16) {
+    const int b = e / d.NC, n = e % d.NC;
+    acc += *reinterpret_cast<const f4*>(part + (((long)b * d.H + h) * d.NC + n) * 64 + 4 * c4);
+  }
+  partial[q][c4] = acc;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    f4 total = partial[0][threadIdx.x];
+    for (int k = 1; k < 16; ++k) total += partial[k][threadIdx.x];
+    *reinterpret_cast<f4*>(d_floor + h * 64 + 4 * threadIdx.x) = total;
+  }
 }
 
 }  // namespace m4
