@@ -47,8 +47,10 @@ KERNEL_WORK = {
     "fwd_read": ("mfma", 3 * 8192, "flop"),  # Y K^T, (G) V, Y C0^T
     "bwd_dy": ("mfma", 3 * 8192, "flop"),  # dO V^T, (G) K, dO C0
     "bwd_grads": ("mfma", 13 * 8192, "flop"),  # 13 chunk products
-    "fwd_states": ("mfma", 2 * 8192, "flop"),  # K^T diag K, V^T diag K
-    "bwd_states": ("mfma", 3 * 8192, "flop"),  # sym(Z^T Y), dO^T Y
+    "fwd_stats": ("mfma", 2 * 8192, "flop"),  # K^T diag K, V^T diag K
+    "fwd_scan": ("hbm", 16384 * 3 * 2 // 64, "B"),  # r+w of 2 evidence + 1 cross state / chunk
+    "bwd_local": ("mfma", 2 * 8192, "flop"),  # Z^T diag Y, dO^T diag Y
+    "bwd_scan": ("hbm", 16384 * 2 * 2 // 64, "B"),  # r+w of 1 evidence + 1 cross state / chunk
     "floor_reduce": ("hbm", 4, "B"),
 }
 
@@ -97,7 +99,7 @@ class Problem:
         dev = torch.device("cuda:0")
         self.B, self.T, self.H, _ = data["keys"].shape
         self.chunk = chunk
-        count = -(-self.T // chunk)
+        count, starts = _lib.start_counts(self.T, chunk)
         B, T, H = self.B, self.T, self.H
 
         def put(a):
@@ -114,7 +116,7 @@ class Problem:
             torch.empty(B, H, 64, 64, **f32),  # final cross
             torch.empty(B, T, H, 64, **f32),  # solved
             torch.empty(B, T, H, _lib.FACTOR_FLOATS, **f32),  # factors
-            torch.empty(B, H, count, 64, 64, **f32),  # start evidence
+            torch.empty(B, H, starts, 64, 64, **f32),  # start evidence
             torch.empty(B, H, count, 64, 64, **f32),  # start cross
         ]
         self.grads = [torch.empty_like(t) for t in self.inputs]

@@ -32,10 +32,11 @@ extern "C" {
 #define M4MR_KEY_DIM 64
 #define M4MR_VALUE_DIM 64
 #define M4MR_MAX_CHUNK 64
-/* Packed lower factor per token-head: 64*65/2 floats, column-major, the
- * diagonal holding the reciprocal pivot 1/L_jj (the reference keeps the
- * same reciprocal convention, lm/kernels/mamba4_fused.py:113). */
-#define M4MR_FACTOR_FLOATS 2080
+/* Stored lower factor per token-head: the lower triangle row by row, row i
+ * padded to 4*ceil((i+1)/4) floats (16-byte aligned rows), 2176 floats in
+ * all; the diagonal holds the reciprocal pivot 1/L_ii (the reference keeps
+ * the same reciprocal convention, lm/kernels/mamba4_fused.py:113). */
+#define M4MR_FACTOR_FLOATS 2176
 
 #define M4MR_OK 0
 #define M4MR_EINVAL 1
@@ -64,7 +65,11 @@ const char* m4mr_last_error(void);
  *          equivalent arrays "memory_solve"):
  *          solved [B,T,H,D] (y_t = A_t^-1 q_t);
  *          factors [B,T,H,M4MR_FACTOR_FLOATS];
- *          start_evidence [B,H,NC,D,D]; start_cross [B,H,NC,P,D].
+ *          start_evidence [B,H,NS,D,D], the evidence at the start of each
+ *          sub-chunk (chunks above 32 tokens split in two halves of
+ *          ceil(chunk/2) tokens, so NS = 2*NC, else NS = NC);
+ *          start_cross [B,H,NC,P,D], the cross statistics at each chunk start.
+ *          m4mr_start_counts() returns NC and NS.
  */
 int m4mr_forward(const float* keys, const float* values, const float* queries,
                  const float* beta, const float* log_decay, const float* floor,
@@ -75,6 +80,9 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
                  float* solved, float* factors,
                  float* start_evidence, float* start_cross,
                  void* stream);
+
+/* Number of chunks NC and of evidence start states NS for T tokens. */
+int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts);
 
 /* Bytes of device workspace m4mr_backward needs for these sizes. */
 size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk);

@@ -14,7 +14,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "mamba4_memread.h")
 
 EINVAL = 1
 EHIP = 2
-FACTOR_FLOATS = 2080
+FACTOR_FLOATS = 2176
 KEY_DIM = 64
 VALUE_DIM = 64
 MAX_CHUNK = 64
@@ -29,6 +29,7 @@ SIGNATURES = {
     "m4mr_last_error": (ctypes.c_char_p, []),
     "m4mr_forward": (_I, [_P] * 8 + [_I] * 4 + [_P] * 8 + [_P]),
     "m4mr_backward_workspace_bytes": (_S, [_I] * 4),
+    "m4mr_start_counts": (_I, [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "m4mr_backward": (
         _I,
         [_P] * 6 + [_I] * 4 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
@@ -100,6 +101,13 @@ def profile_read(kernel):
     count = ctypes.c_long()
     check(load().m4mr_profile_read(kernel.encode(), ctypes.byref(total), ctypes.byref(count)))
     return total.value, count.value
+
+
+def start_counts(time, chunk):
+    """(NC, NS): chunk start states and evidence start states for T tokens."""
+    nc, ns = _I(), _I()
+    check(load().m4mr_start_counts(time, chunk, ctypes.byref(nc), ctypes.byref(ns)))
+    return nc.value, ns.value
 
 
 def kernel_names():

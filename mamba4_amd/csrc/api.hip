@@ -15,16 +15,20 @@
 #include "common.hpp"
 
 namespace m4 {
-__global__ void fwd_states_kernel(Dims, const float*, const float*, const float*, const float*,
-                                  const float*, const float*, float*, float*, float*, float*);
-__global__ void bwd_states_kernel(Dims, const float*, const float*, const float*, const float*,
-                                  const float*, const float*, const float*, float*, float*,
-                                  float*, float*);
+__global__ void fwd_stats_kernel(Dims, const float*, const float*, const float*, const float*,
+                                 float*, float*);
+__global__ void fwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
+                                float*, float*);
+__global__ void bwd_local_kernel(Dims, const float*, const float*, const float*, const float*,
+                                 const float*, float*, float*);
+__global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
+                                float*, float*);
 __global__ void fwd_factor_kernel(Dims, const float*, const float*, const float*, const float*,
                                   const float*, const float*, float*, float*);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
 __global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
-                                   const float*, const float*, const float*, int, float*, float*);
+                                   const float*, const float*, const float*, long, int, float*,
+                                   float*);
 __global__ void fwd_read_kernel(Dims, const float*, const float*, const float*, const float*,
                                 const float*, const float*, const float*, float*, float*);
 __global__ void bwd_dy_kernel(Dims, const float*, const float*, const float*, const float*,
@@ -42,9 +46,9 @@ using m4::Dims;
 
 thread_local std::string g_error;
 
-const char* const kKernelNames[] = {"fwd_states", "fwd_factor",     "fwd_read",
-                                    "bwd_dy",     "factored_solve", "bwd_states",
-                                    "bwd_grads",  "floor_reduce",   "decode_step"};
+const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_factor", "fwd_read",
+                                    "bwd_dy",         "factored_solve", "bwd_local", "bwd_scan",
+                                    "bwd_grads",      "floor_reduce", "decode_step"};
 
 struct ProfRecord {
   const char* name;
@@ -59,6 +63,7 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
+constexpr size_t kStatsLdsBytes = 3 * m4::TILE * sizeof(float);
 constexpr size_t kChunkLdsBytes = 4 * m4::TILE * sizeof(float);
 constexpr size_t kGradsLdsBytes = 7 * m4::TILE * sizeof(float);
 
@@ -71,7 +76,9 @@ int configure() {
   struct {
     const void* fn;
     size_t bytes;
-  } big[] = {{(const void*)m4::fwd_read_kernel, kChunkLdsBytes},
+  } big[] = {{(const void*)m4::fwd_stats_kernel, kStatsLdsBytes},
+             {(const void*)m4::bwd_local_kernel, kChunkLdsBytes},
+             {(const void*)m4::fwd_read_kernel, kChunkLdsBytes},
              {(const void*)m4::bwd_dy_kernel, kChunkLdsBytes},
              {(const void*)m4::bwd_grads_kernel, kGradsLdsBytes}};
   for (auto& k : big) {
@@ -134,6 +141,11 @@ Dims make_dims(int B, int T, int H, int chunk) {
   d.H = H;
   d.chunk = chunk;
   d.NC = (T + chunk - 1) / chunk;
+  // Chunks above 32 tokens split in two sub-chunks for the factor kernel, so
+  // it sees twice as many independent token sequences.
+  d.rsub = chunk > 32 ? 2 : 1;
+  d.sub = (chunk + d.rsub - 1) / d.rsub;
+  d.NS = d.NC * d.rsub;
   return d;
 }
 
@@ -197,21 +209,37 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
   const Dims d = make_dims(B, T, H, chunk);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned seqs = (unsigned)B * H * d.NC;
-  int rc = launch("fwd_states", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_states_kernel, dim3(B * H, 8), dim3(256), 0, st, d, keys, values,
-                       beta, log_decay, init_evidence, init_cross, start_evidence, start_cross,
-                       final_evidence, final_cross);
+  const unsigned subseqs = (unsigned)B * H * d.NS;
+  int rc = launch("fwd_stats", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_stats_kernel, dim3(seqs), dim3(256), kStatsLdsBytes, st, d, keys,
+                       values, beta, log_decay, start_evidence, start_cross);
+  });
+  if (rc) return rc;
+  rc = launch("fwd_scan", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 8), dim3(256), 0, st, d, log_decay,
+                       init_evidence, init_cross, start_evidence, start_cross, final_evidence,
+                       final_cross);
   });
   if (rc) return rc;
   rc = launch("fwd_factor", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3(seqs), dim3(64), 0, st, d, keys, queries,
-                       beta, log_decay, floor, start_evidence, solved, factors);
+    hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3((subseqs + 3) / 4), dim3(64), 0, st, d, keys,
+                       queries, beta, log_decay, floor, start_evidence, solved, factors);
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {
     hipLaunchKernelGGL(m4::fwd_read_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, keys,
                        values, queries, beta, log_decay, solved, start_cross, output, variance);
   });
+}
+
+int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {
+  g_error.clear();
+  std::string why;
+  if (bad_dims(1, T, 1, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_start_counts: " + why);
+  const Dims d = make_dims(1, T, 1, chunk);
+  if (chunks) *chunks = d.NC;
+  if (evidence_starts) *evidence_starts = d.NS;
+  return M4MR_OK;
 }
 
 size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk) {
@@ -259,14 +287,19 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   rc = launch("factored_solve", st, [&] {
-    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0,
+    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(64), 0,
                        st, factors, ws.z, ws.z, tokens);
   });
   if (rc) return rc;
-  rc = launch("bwd_states", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_states_kernel, dim3(B * H, 8), dim3(256), 0, st, d, beta,
-                       log_decay, solved, ws.z, d_output, d_final_evidence, d_final_cross,
-                       ws.end_s, ws.end_c, d_init_evidence, d_init_cross);
+  rc = launch("bwd_local", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_local_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, beta,
+                       log_decay, solved, ws.z, d_output, ws.end_s, ws.end_c);
+  });
+  if (rc) return rc;
+  rc = launch("bwd_scan", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 8), dim3(256), 0, st, d, log_decay,
+                       d_final_evidence, d_final_cross, ws.end_s, ws.end_c, d_init_evidence,
+                       d_init_cross);
   });
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
@@ -290,7 +323,7 @@ int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N
   if (misaligned(factors)) return fail(M4MR_EINVAL, "m4mr_factored_solve: factors must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   return launch("factored_solve", st, [&] {
-    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st,
+    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
                        factors, rhs, z, N);
   });
 }
@@ -309,8 +342,9 @@ int m4mr_decode_step(float* evidence, float* cross, const float* key, const floa
     return fail(M4MR_EINVAL, "m4mr_decode_step: states must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   return launch("decode_step", st, [&] {
-    hipLaunchKernelGGL(m4::decode_step_kernel, dim3((unsigned)N), dim3(64), 0, st, evidence, cross,
-                       key, value, query, beta, log_decay, floor, H, output, variance);
+    hipLaunchKernelGGL(m4::decode_step_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
+                       evidence, cross, key, value, query, beta, log_decay, floor, N, H, output,
+                       variance);
   });
 }
 

@@ -305,7 +305,9 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   __syncthreads();
 
   // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>.
-  load_matrix(Kt, start_s + si.seq * 4096);
+  // The chunk's start evidence is the start of its first sub-chunk.
+  const long bh = si.seq / d.NC;
+  load_matrix(Kt, start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
   load_matrix(Vt, start_c + si.seq * 4096);
   __syncthreads();
   {

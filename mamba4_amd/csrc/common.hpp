@@ -10,12 +10,16 @@ constexpr int VD = 64;      // value width P
 constexpr int MAXC = 64;    // largest chunk
 constexpr int LDT = 65;     // row stride of a 64x64 LDS tile (odd: conflict-free columns)
 constexpr int TILE = 64 * LDT;
-constexpr int FACTOR = 2080;  // packed lower factor floats per token-head
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Problem shape.  Chunks of `chunk` tokens carry the decayed statistics;
+// each chunk splits into `rsub` sub-chunks of up to `sub` tokens, and the
+// factor kernel starts one token sequence per sub-chunk from its stored
+// evidence (NS = NC * rsub start states).
 struct Dims {
   int B, T, H, chunk, NC;
+  int sub, rsub, NS;
 };
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
@@ -31,8 +35,12 @@ __device__ __forceinline__ int chunk_len(const Dims& d, int n) {
   return left < d.chunk ? left : d.chunk;
 }
 
-// Offset of column j in the packed column-major lower factor.
-__host__ __device__ constexpr int factor_col(int j) { return j * 64 - (j * (j - 1)) / 2; }
+// First token (within chunk n) and length of sub-chunk u of chunk n.
+__device__ __forceinline__ int sub_first(const Dims& d, int u) { return u * d.sub; }
+__device__ __forceinline__ int sub_len(const Dims& d, int n, int u) {
+  const int first = u * d.sub, end = min(chunk_len(d, n), first + d.sub);
+  return end > first ? end - first : 0;
+}
 
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ __forceinline__ float wave_inclusive_sum(float x) {

@@ -1,0 +1,187 @@
+// Four 64x64 SPD matrices per wave, one per 16-lane DPP row.
+//
+// Lane a of row-group mu (lane = 16*mu + a) owns rows a, a+16, a+32, a+48 of
+// matrix mu: slot m holds row a+16m, columns 0..15+16m, in A[m][k].  Slots
+// are sized for the longest row of the slot (a = 15), so columns past a row's
+// diagonal are scratch that is zeroed after the factorization.  Every
+// cross-lane value the factorization and the two substitutions need lives in
+// the same 16-lane row, so it moves by DPP row_newbcast (broadcast of one
+// lane of the row), folded into the consuming FMA where the compiler can.
+// No LDS is touched and 74% of the issued FMA lanes do useful work.
+//
+// Factor storage ("padded rows"): the lower triangle row by row, row i
+// padded to a multiple of 4 floats (4*ceil((i+1)/4)), 2176 floats per
+// matrix; the diagonal holds the reciprocal pivot 1/L_ii.  Lane a writes or
+// reads its four rows with 16-byte accesses.
+#pragma once
+
+#include <utility>
+
+#include "common.hpp"
+
+namespace m4 {
+
+constexpr int ROWS_FACTOR = 2176;  // floats per stored factor
+
+// Floats before row i in the padded-row layout: with i = 4p + s,
+// 4 (p+1) (2p + s).
+__host__ __device__ constexpr int row_offset(int i) {
+  return 4 * ((i >> 2) + 1) * (2 * (i >> 2) + (i & 3));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+
+// Value of x at lane `src` of this lane's 16-lane row (src known after unrolling).
+__device__ __forceinline__ float bcast16(float x, int src) {
+  switch (src) {
+    case 0: return dpp<0x150>(x);
+    case 1: return dpp<0x151>(x);
+    case 2: return dpp<0x152>(x);
+    case 3: return dpp<0x153>(x);
+    case 4: return dpp<0x154>(x);
+    case 5: return dpp<0x155>(x);
+    case 6: return dpp<0x156>(x);
+    case 7: return dpp<0x157>(x);
+    case 8: return dpp<0x158>(x);
+    case 9: return dpp<0x159>(x);
+    case 10: return dpp<0x15A>(x);
+    case 11: return dpp<0x15B>(x);
+    case 12: return dpp<0x15C>(x);
+    case 13: return dpp<0x15D>(x);
+    case 14: return dpp<0x15E>(x);
+    default: return dpp<0x15F>(x);
+  }
+}
+
+// Sum over the 16 lanes of the row; every lane receives the total.
+__device__ __forceinline__ float sum16(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+constexpr int slot_cols(int m) { return 16 * (m + 1); }
+
+// In-place Cholesky of A + diag(floor); fl[m] is the floor of row a+16m.
+// Right-looking: at step j the pivot is broadcast from lane j%16, column j
+// is scaled by its reciprocal square root, and every later column of every
+// later row takes one DPP-fed FMA.  On return A holds L below the diagonal,
+// 1/L_ii on it and zeros above.  The 64 steps are expanded at compile time
+// so every register index is static.
+template <int J>
+__device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)[4], int a) {
+  constexpr int mj = J >> 4, lj = J & 15;
+  const float piv = bcast16(A[mj][J] + fl[mj], lj);
+  // v_rsq_f32 (1 ulp), as the reference's lax.rsqrt pivot
+  // (lm/kernels/mamba4_fused.py:111); a non-positive pivot gives NaN.
+  const float rs = __builtin_amdgcn_rsqf(piv);
+#pragma unroll
+  for (int m = mj; m < 4; ++m) A[m][J] *= rs;
+  // A[m][k] += (-l_ij) * l_kj.  Column k's broadcast l_kj is consumed at
+  // once by every row slot that holds column k (slots m >= k/16), which
+  // keeps one broadcast live at a time.
+  float nl[4];
+#pragma unroll
+  for (int m = mj; m < 4; ++m) nl[m] = -A[m][J];
+#pragma unroll
+  for (int k = J + 1; k < 64; ++k) {
+    const float lkj = bcast16(A[k >> 4][J], k & 15);
+#pragma unroll
+    for (int m = (k >> 4) > mj ? (k >> 4) : mj; m < 4; ++m)
+      A[m][k] = __builtin_fmaf(lkj, nl[m], A[m][k]);
+  }
+  A[mj][J] = a == lj ? rs : A[mj][J];
+}
+
+template <int... J>
+__device__ __forceinline__ void factor_steps(float (&A)[4][64], const float (&fl)[4], int a,
+                                             std::integer_sequence<int, J...>) {
+  (factor_step<J>(A, fl, a), ...);
+}
+
+__device__ __forceinline__ void factor_rows16(float (&A)[4][64], const float (&fl)[4]) {
+  const int a = threadIdx.x & 15;
+  factor_steps(A, fl, a, std::make_integer_sequence<int, 64>{});
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int c = 1; c < 16; ++c) A[m][16 * m + c] = c > a ? 0.f : A[m][16 * m + c];
+}
+
+// y = (L L^T)^-1 r for a factor from factor_rows16; r is consumed.
+template <int J>
+__device__ __forceinline__ void forward_step(const float (&A)[4][64], float (&r)[4],
+                                             float (&w)[4], int a) {
+  constexpr int mj = J >> 4, lj = J & 15;
+  const float wj = bcast16(r[mj] * A[mj][J], lj);
+  w[mj] = a == lj ? wj : w[mj];
+#pragma unroll
+  for (int m = mj; m < 4; ++m) r[m] -= A[m][J] * wj;
+}
+
+template <int J>
+__device__ __forceinline__ void backward_step(const float (&A)[4][64], const float (&w)[4],
+                                              float (&y)[4], int a) {
+  constexpr int mj = J >> 4, lj = J & 15;
+  float p = 0.f;
+#pragma unroll
+  for (int m = mj; m < 4; ++m) p += A[m][J] * y[m];
+  const float yj = (w[mj] - sum16(p)) * A[mj][J];
+  y[mj] = a == lj ? yj : y[mj];
+}
+
+template <int... J>
+__device__ __forceinline__ void solve_steps(const float (&A)[4][64], float (&r)[4], float (&w)[4],
+                                            float (&y)[4], int a,
+                                            std::integer_sequence<int, J...>) {
+  (forward_step<J>(A, r, w, a), ...);
+  (backward_step<63 - J>(A, w, y, a), ...);
+}
+
+__device__ __forceinline__ void solve_rows16(const float (&A)[4][64], float (&r)[4], float (&y)[4]) {
+  const int a = threadIdx.x & 15;
+  float w[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) y[m] = 0.f;
+  solve_steps(A, r, w, y, a, std::make_integer_sequence<int, 64>{});
+}
+
+// Padded-row factor store / load for this lane's four rows.
+__device__ __forceinline__ void store_rows16(const float (&A)[4][64], float* __restrict__ fac) {
+  const int a = threadIdx.x & 15;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = a + 16 * m, p = i >> 2;
+    float* row = fac + row_offset(i);
+#pragma unroll
+    for (int q = 0; q < 4 * m + 4; ++q)
+      if (q <= p)
+        *reinterpret_cast<f4*>(row + 4 * q) =
+            f4{A[m][4 * q], A[m][4 * q + 1], A[m][4 * q + 2], A[m][4 * q + 3]};
+  }
+}
+
+__device__ __forceinline__ void load_rows16(float (&A)[4][64], const float* __restrict__ fac) {
+  const int a = threadIdx.x & 15;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = a + 16 * m, p = i >> 2;
+    const float* row = fac + row_offset(i);
+#pragma unroll
+    for (int q = 0; q < 4 * m + 4; ++q) {
+      f4 v = f4{0.f, 0.f, 0.f, 0.f};
+      if (q <= p) v = *reinterpret_cast<const f4*>(row + 4 * q);
+      A[m][4 * q] = v[0];
+      A[m][4 * q + 1] = v[1];
+      A[m][4 * q + 2] = v[2];
+      A[m][4 * q + 3] = v[3];
+    }
+  }
+}
+
+}  // namespace m4

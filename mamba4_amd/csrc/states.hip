@@ -1,121 +1,212 @@
-// Chunk-boundary states: the forward decayed carry of chunk statistics and
-// the backward reverse carry of start-state cotangents.
+// Chunk-boundary states: chunk statistics on MFMA plus an elementwise scan.
 //
 // Forward (lm/kernels/mamba4_fused.py:411-425 with chunk_carry,
-// lm/kernels/prefix.py:27-44): per (b, h) the chunks are walked in order,
-//   start[n] = running,  running = exp(P_last,n) running + X_n^T diag(tail_n) K_n
-// with X = K for the evidence and X = V for the cross statistics.
-// Backward: the transpose of that carry, walked in reverse,
-//   end[n] = running,  running = U_n + exp(P_last,n) running,
-// U_n = sum_t exp(P_t) (-(z_t y_t^T + y_t z_t^T)/2) for the evidence and
-// sum_t exp(P_t) dout_t y_t^T for the cross statistics.
+// lm/kernels/prefix.py:27-44).  fwd_stats_kernel computes, for every chunk
+// in parallel, the statistics K^T diag(tail) K of each sub-chunk and
+// V^T diag(tail) K of the chunk, tail_s = beta_s exp(P_last - P_s), and
+// writes them into the start-state buffers.  fwd_scan_kernel then turns them
+// into start states in place, walking chunks in order per matrix element:
+//   start[u] = running;  running = exp(sum of log decays in u) running + stat[u]
+// and writes the final state.
 //
-// Grid (B*H, 8): blockIdx.y 0..3 owns evidence rows [16y, 16y+16), 4..7 the
-// cross rows [16(y-4), ...).  Each of the 256 threads keeps 4 consecutive
-// columns of one row in registers for the whole walk, so the running state
-// never leaves the chip; every chunk costs one read of its token rows.
+// Backward: the transpose of that carry.  bwd_local_kernel computes each
+// chunk's start-state cotangents U = -(M + M^T)/2, M = Z^T diag(e^P) Y, and
+// V = dOut^T diag(e^P) Y; bwd_scan_kernel walks chunks in reverse,
+//   end[n] = running;  running = U_n + exp(sum of log decays in n) running,
+// leaving each chunk's end-state cotangent and the initial-state gradient.
 #include "common.hpp"
 
 namespace m4 {
 
-__global__ __launch_bounds__(256) void fwd_states_kernel(
+__device__ __forceinline__ float* mat(float* base, long index) { return base + index * 4096; }
+
+__global__ __launch_bounds__(256) void fwd_stats_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
-    const float* __restrict__ init_s, const float* __restrict__ init_c,
-    float* __restrict__ start_s, float* __restrict__ start_c,
+    float* __restrict__ start_s, float* __restrict__ start_c) {
+  extern __shared__ float smem[];
+  float* K = smem;
+  float* V = K + TILE;
+  float* W = V + TILE;
+  __shared__ ChunkScalars cs;
+  const long seq = blockIdx.x;
+  const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
+  const int len = chunk_len(d, n), w = threadIdx.x >> 6;
+  const int kpad = (len + 3) & ~3;
+  auto rows = [&](const float* base) {
+    return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * 64; };
+  };
+  load_rows(K, len, rows(keys));
+  load_rows(V, len, rows(values));
+  load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
+  __syncthreads();
+
+  for (int u = 0; u < d.rsub; ++u) {
+    const int first = sub_first(d, u), cnt = sub_len(d, n, u);
+    const float p_end = cnt > 0 ? cs.prefix[first + cnt - 1] : 0.f;
+    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+      const int s = e >> 6, c = e & 63;
+      const bool in = s >= first && s < first + cnt;
+      W[s * LDT + c] = in ? cs.beta[s] * expf(p_end - cs.prefix[s]) * K[s * LDT + c] : 0.f;
+    }
+    __syncthreads();
+    f4 acc[4];
+    zero4(acc);
+    tile_mma<true, false>(acc, W, LDT, K, LDT, kpad, w);  // sum_s tail_s k_s k_s^T
+    float* out = mat(start_s, (long)bh * d.NS + (long)n * d.rsub + u);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[acc_row(w, r) * 64 + acc_col(jb)] = acc[jb][r];
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int s = e >> 6, c = e & 63;
+    W[s * LDT + c] = s < len ? cs.tail[s] * V[s * LDT + c] : 0.f;
+  }
+  __syncthreads();
+  f4 acc[4];
+  zero4(acc);
+  tile_mma<true, false>(acc, W, LDT, K, LDT, kpad, w);  // sum_s tail_s v_s k_s^T
+  float* out = mat(start_c, (long)bh * d.NC + n);
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[acc_row(w, r) * 64 + acc_col(jb)] = acc[jb][r];
+}
+
+// exp(sum of log decays) over the tokens of step `i` of the scan: a
+// sub-chunk (evidence) or a chunk (cross statistics).
+__device__ __forceinline__ float step_decay(const Dims& d, const float* log_decay, int b, int h,
+                                            int i, bool sub) {
+  int first, cnt;
+  if (sub) {
+    const int n = i / d.rsub, u = i % d.rsub;
+    first = n * d.chunk + sub_first(d, u);
+    cnt = sub_len(d, n, u);
+  } else {
+    first = i * d.chunk;
+    cnt = chunk_len(d, i);
+  }
+  float g = 0.f;
+  for (int t = 0; t < cnt; ++t) g += log_decay[token_head(d, b, first + t, h)];
+  return expf(g);
+}
+
+// Grid (B*H, 8): y in 0..3 scans evidence elements [1024y, 1024y+1024) over
+// the NS sub-chunks, y in 4..7 the cross-statistic elements over NC chunks.
+__global__ __launch_bounds__(256) void fwd_scan_kernel(
+    Dims d, const float* __restrict__ log_decay, const float* __restrict__ init_s,
+    const float* __restrict__ init_c, float* __restrict__ start_s, float* __restrict__ start_c,
     float* __restrict__ final_s, float* __restrict__ final_c) {
   const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
   const bool cross = blockIdx.y >= 4;
-  const int r0 = 16 * (blockIdx.y & 3);
-  const int tid = threadIdx.x, row = tid >> 4, col = (tid & 15) * 4;
-
-  __shared__ float kbuf[MAXC * 64];
-  __shared__ float xbuf[MAXC * 16];
-  __shared__ ChunkScalars cs;
-
+  const int elem = 1024 * (blockIdx.y & 3) + 4 * threadIdx.x;
+  const int steps = cross ? d.NC : d.NS;
+  float* buf = cross ? start_c + (long)bh * d.NC * 4096 : start_s + (long)bh * d.NS * 4096;
   const float* init = cross ? init_c : init_s;
-  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-  if (init) acc = *reinterpret_cast<const f4*>(init + ((long)bh * 64 + r0 + row) * 64 + col);
-  const float* xsrc = cross ? values : keys;
-  float* starts = cross ? start_c : start_s;
-
-  for (int n = 0; n < d.NC; ++n) {
-    const int len = chunk_len(d, n);
-    for (int e = tid; e < len * 16; e += 256) {
-      const int s = e >> 4, q = (e & 15) * 4;
-      const long th = token_head(d, b, n * d.chunk + s, h);
-      *reinterpret_cast<f4*>(kbuf + s * 64 + q) = *reinterpret_cast<const f4*>(keys + th * 64 + q);
-    }
-    for (int e = tid; e < len * 4; e += 256) {
-      const int s = e >> 2, q = (e & 3) * 4;
-      const long th = token_head(d, b, n * d.chunk + s, h);
-      *reinterpret_cast<f4*>(xbuf + s * 16 + q) =
-          *reinterpret_cast<const f4*>(xsrc + th * 64 + r0 + q);
-    }
-    load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
+  __shared__ float decay[256];
+  f4 running = f4{0.f, 0.f, 0.f, 0.f};
+  if (init) running = *reinterpret_cast<const f4*>(init + (long)bh * 4096 + elem);
+  for (int base = 0; base < steps; base += 256) {
+    const int count = min(256, steps - base);
     __syncthreads();
-    *reinterpret_cast<f4*>(starts + (((long)bh * d.NC + n) * 64 + r0 + row) * 64 + col) = acc;
-    const float decay = expf(cs.prefix[MAXC - 1]);
-    acc *= decay;
-    for (int s = 0; s < len; ++s) {
-      const float x = xbuf[s * 16 + row] * cs.tail[s];
-      const f4 kv = *reinterpret_cast<const f4*>(kbuf + s * 64 + col);
-      acc += x * kv;
-    }
+    if (threadIdx.x < count)
+      decay[threadIdx.x] = step_decay(d, log_decay, b, h, base + threadIdx.x, !cross);
     __syncthreads();
+    for (int i = 0; i < count; ++i) {
+      f4* p = reinterpret_cast<f4*>(buf + (long)(base + i) * 4096 + elem);
+      const f4 stat = *p;
+      *p = running;
+      running = decay[i] * running + stat;
+    }
   }
   float* fin = cross ? final_c : final_s;
-  *reinterpret_cast<f4*>(fin + ((long)bh * 64 + r0 + row) * 64 + col) = acc;
+  *reinterpret_cast<f4*>(fin + (long)bh * 4096 + elem) = running;
 }
 
-__global__ __launch_bounds__(256) void bwd_states_kernel(
+__global__ __launch_bounds__(256) void bwd_local_kernel(
     Dims d, const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ solved, const float* __restrict__ z,
-    const float* __restrict__ d_output, const float* __restrict__ d_final_s,
+    const float* __restrict__ d_output, float* __restrict__ end_s, float* __restrict__ end_c) {
+  extern __shared__ float smem[];
+  float* Y = smem;
+  float* Zw = Y + TILE;
+  float* Dw = Zw + TILE;
+  float* M = Dw + TILE;
+  __shared__ ChunkScalars cs;
+  const long seq = blockIdx.x;
+  const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
+  const int len = chunk_len(d, n), w = threadIdx.x >> 6;
+  const int kpad = (len + 3) & ~3;
+  auto rows = [&](const float* base) {
+    return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * 64; };
+  };
+  load_rows(Y, len, rows(solved));
+  load_rows(Zw, len, rows(z));
+  load_rows(Dw, len, rows(d_output));
+  load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
+  __syncthreads();
+  for (int e = threadIdx.x; e < len * 64; e += 256) {
+    const int t = e >> 6, c = e & 63;
+    const float carried = expf(cs.prefix[t]);
+    Zw[t * LDT + c] *= carried;
+    Dw[t * LDT + c] *= carried;
+  }
+  __syncthreads();
+  f4 acc[4];
+  zero4(acc);
+  tile_mma<true, false>(acc, Zw, LDT, Y, LDT, kpad, w);  // M = sum_t e^P z_t y_t^T
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[acc_row(w, r) * LDT + acc_col(jb)] = acc[jb][r];
+  __syncthreads();
+  float* us = mat(end_s, (long)bh * d.NC + n);
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = acc_row(w, r), j = acc_col(jb);
+      us[i * 64 + j] = -0.5f * (acc[jb][r] + M[j * LDT + i]);
+    }
+  zero4(acc);
+  tile_mma<true, false>(acc, Dw, LDT, Y, LDT, kpad, w);  // V = sum_t e^P dout_t y_t^T
+  float* uc = mat(end_c, (long)bh * d.NC + n);
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) uc[acc_row(w, r) * 64 + acc_col(jb)] = acc[jb][r];
+}
+
+// Grid (B*H, 8) as fwd_scan_kernel, walking chunks in reverse.
+__global__ __launch_bounds__(256) void bwd_scan_kernel(
+    Dims d, const float* __restrict__ log_decay, const float* __restrict__ d_final_s,
     const float* __restrict__ d_final_c, float* __restrict__ end_s, float* __restrict__ end_c,
     float* __restrict__ d_init_s, float* __restrict__ d_init_c) {
   const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
   const bool cross = blockIdx.y >= 4;
-  const int r0 = 16 * (blockIdx.y & 3);
-  const int tid = threadIdx.x, row = tid >> 4, col = (tid & 15) * 4;
-
-  __shared__ float ybuf[MAXC * 64];
-  __shared__ float zbuf[MAXC * 64];  // z (evidence) or dout (cross)
-  __shared__ ChunkScalars cs;
-
+  const int elem = 1024 * (blockIdx.y & 3) + 4 * threadIdx.x;
+  float* buf = (cross ? end_c : end_s) + (long)bh * d.NC * 4096;
   const float* fin = cross ? d_final_c : d_final_s;
-  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-  if (fin) acc = *reinterpret_cast<const f4*>(fin + ((long)bh * 64 + r0 + row) * 64 + col);
-  const float* other = cross ? d_output : z;
-  float* ends = cross ? end_c : end_s;
-
-  for (int n = d.NC - 1; n >= 0; --n) {
-    const int len = chunk_len(d, n);
-    for (int e = tid; e < len * 16; e += 256) {
-      const int s = e >> 4, q = (e & 15) * 4;
-      const long th = token_head(d, b, n * d.chunk + s, h);
-      *reinterpret_cast<f4*>(ybuf + s * 64 + q) = *reinterpret_cast<const f4*>(solved + th * 64 + q);
-      *reinterpret_cast<f4*>(zbuf + s * 64 + q) = *reinterpret_cast<const f4*>(other + th * 64 + q);
-    }
-    load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
+  __shared__ float decay[256];
+  f4 running = f4{0.f, 0.f, 0.f, 0.f};
+  if (fin) running = *reinterpret_cast<const f4*>(fin + (long)bh * 4096 + elem);
+  for (int top = d.NC; top > 0; top -= 256) {
+    const int count = min(256, top);
     __syncthreads();
-    *reinterpret_cast<f4*>(ends + (((long)bh * d.NC + n) * 64 + r0 + row) * 64 + col) = acc;
-    acc *= expf(cs.prefix[MAXC - 1]);
-    const int i = r0 + row;
-    for (int t = 0; t < len; ++t) {
-      const float w = expf(cs.prefix[t]);
-      const f4 yv = *reinterpret_cast<const f4*>(ybuf + t * 64 + col);
-      if (cross) {
-        acc += (w * zbuf[t * 64 + i]) * yv;
-      } else {
-        const f4 zv = *reinterpret_cast<const f4*>(zbuf + t * 64 + col);
-        acc -= (0.5f * w) * (zbuf[t * 64 + i] * yv + ybuf[t * 64 + i] * zv);
-      }
-    }
+    if (threadIdx.x < count)
+      decay[threadIdx.x] = step_decay(d, log_decay, b, h, top - count + threadIdx.x, false);
     __syncthreads();
+    for (int i = count - 1; i >= 0; --i) {
+      f4* p = reinterpret_cast<f4*>(buf + (long)(top - count + i) * 4096 + elem);
+      const f4 local = *p;
+      *p = running;
+      running = local + decay[i] * running;
+    }
   }
   float* dinit = cross ? d_init_c : d_init_s;
-  *reinterpret_cast<f4*>(dinit + ((long)bh * 64 + r0 + row) * 64 + col) = acc;
+  *reinterpret_cast<f4*>(dinit + (long)bh * 4096 + elem) = running;
 }
 
 }  // namespace m4

@@ -81,7 +81,7 @@ class _MemoryRead(torch.autograd.Function):
     def forward(ctx, keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk):
         lib = _lib.load()
         batch, time, heads, _ = keys.shape
-        count = -(-time // chunk)
+        count, starts = _lib.start_counts(time, chunk)
         dev = keys.device
         f32 = dict(dtype=torch.float32, device=dev)
         output = torch.empty((batch, time, heads, _lib.VALUE_DIM), **f32)
@@ -90,7 +90,7 @@ class _MemoryRead(torch.autograd.Function):
         final_c = torch.empty((batch, heads, _lib.VALUE_DIM, 64), **f32)
         solved = torch.empty((batch, time, heads, 64), **f32)
         factors = torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
-        start_s = torch.empty((batch, heads, count, 64, 64), **f32)
+        start_s = torch.empty((batch, heads, starts, 64, 64), **f32)
         start_c = torch.empty((batch, heads, count, _lib.VALUE_DIM, 64), **f32)
         _lib.check(
             lib.m4mr_forward(

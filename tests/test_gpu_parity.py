@@ -23,6 +23,26 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "config0.npz")
 
 
+def row_offset(i):
+    """Floats before row i of a stored factor (rows padded to 4 floats)."""
+    p, s = i // 4, i % 4
+    return 4 * (p + 1) * (2 * p + s)
+
+
+def unpack_factors(packed):
+    lower = np.zeros(packed.shape[:-1] + (64, 64))
+    for i in range(64):
+        lower[..., i, : i + 1] = packed[..., row_offset(i) : row_offset(i) + i + 1]
+    return lower
+
+
+def pack_factors(lower):
+    packed = np.zeros(lower.shape[:-2] + (2176,))
+    for i in range(64):
+        packed[..., row_offset(i) : row_offset(i) + i + 1] = lower[..., i, : i + 1]
+    return packed
+
+
 def arrays(time=13, heads=3, dim=4, value_dim=5, seed=0, batch=2):
     """The reference test fixture's distributions (lm/tests/test_mamba4.py:19-29)."""
     rng = np.random.default_rng(seed)
@@ -150,12 +170,12 @@ def test_stored_factors_reproduce_each_precision(gpu_lib):
     dev = torch.device("cuda:0")
     ins = to_device([data[n] for n in NAMES])
     f32 = dict(dtype=torch.float32, device=dev)
-    count = -(-T // c)
+    count, starts = -(-T // c), -(-T // c)
     outs = dict(
         output=torch.empty(B, T, H, 64, **f32), variance=torch.empty(B, T, H, **f32),
         final_s=torch.empty(B, H, 64, 64, **f32), final_c=torch.empty(B, H, 64, 64, **f32),
-        solved=torch.empty(B, T, H, 64, **f32), factors=torch.empty(B, T, H, 2080, **f32),
-        start_s=torch.empty(B, H, count, 64, 64, **f32), start_c=torch.empty(B, H, count, 64, 64, **f32),
+        solved=torch.empty(B, T, H, 64, **f32), factors=torch.empty(B, T, H, 2176, **f32),
+        start_s=torch.empty(B, H, starts, 64, 64, **f32), start_c=torch.empty(B, H, count, 64, 64, **f32),
     )
     announce("C-ABI forward, factor unpack B2 T10 H2 D64")
     rc = gpu_lib.m4mr_forward(
@@ -164,11 +184,7 @@ def test_stored_factors_reproduce_each_precision(gpu_lib):
     )
     assert rc == 0, gpu_lib.m4mr_last_error()
     torch.cuda.synchronize()
-    packed = host(outs["factors"])
-    lower = np.zeros((B, T, H, 64, 64))
-    for j in range(64):
-        start = j * 64 - j * (j - 1) // 2
-        lower[..., j:, j] = packed[..., start : start + 64 - j]
+    lower = unpack_factors(host(outs["factors"]))
     diag = np.einsum("...ii->...i", lower)
     true_lower = np.tril(lower, -1) + np.einsum("...i,ij->...ij", 1 / diag, np.eye(64))
     rebuilt = true_lower @ np.swapaxes(true_lower, -1, -2)
@@ -189,8 +205,7 @@ def test_factored_solve_entry_point(gpu_lib):
     N = 37
     a = rng.normal(size=(N, 64, 64))
     a = a @ np.swapaxes(a, -1, -2) / 64 + 0.1 * np.eye(64)
-    lower = oracle.cholesky_reciprocal(a)
-    packed = np.concatenate([lower[:, j:, j] for j in range(64)], axis=1)
+    packed = pack_factors(oracle.cholesky_reciprocal(a))
     rhs = rng.normal(size=(N, 64))
     fac, r = to_device([packed, rhs])
     z = torch.empty_like(r)
