@@ -55,6 +55,24 @@ KERNEL_WORK = {
 }
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "config2_hbm_traffic.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by its copy-kernel calibration),
+    or None when the summary does not list it."""
+    try:
+        lines = open(TRAFFIC_SUMMARY).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 6 and cells[0] == kernel:
+            return float(cells[5].replace(",", "")) * 1e6
+    return None
+
+
 def roofline(kernel, ms, token_heads):
     bound, amount, unit = KERNEL_WORK[kernel]
     seconds = ms / 1e3
@@ -71,7 +89,9 @@ def roofline(kernel, ms, token_heads):
         "peak": peak,
         "unit": unit_out,
         "frac": achieved / peak,
-        "traffic": None,
+        "traffic": measured_traffic(kernel),
+        "traffic_unit": "B per launch (rocprofv3, profiles/config2_hbm_traffic.md)",
+        "algorithmic_bytes" if bound == "hbm" else "algorithmic_flop": amount * token_heads,
     }
 
 

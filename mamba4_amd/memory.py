@@ -232,6 +232,24 @@ def selective_decode(state, key, value, query, beta, log_decay, floor, solver=No
     evidence = torch.as_tensor(state.evidence)
     cross = torch.as_tensor(state.cross)
     _require_device(evidence, cross)
+    inputs = (evidence, cross, key, value, query, beta, log_decay, floor)
+    if torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in inputs
+    ):
+        # A differentiable step is the one-token prefill from `state`: the
+        # same HIP kernels with the custom VJP attached.
+        one = selective_gaussian_memory(
+            torch.as_tensor(key)[:, None],
+            torch.as_tensor(value)[:, None],
+            torch.as_tensor(query)[:, None],
+            torch.as_tensor(beta, device=evidence.device).expand(evidence.shape[:2])[:, None],
+            torch.as_tensor(log_decay, device=evidence.device).expand(evidence.shape[:2])[:, None],
+            floor,
+            chunk_size=1,
+            initial=SelectiveState(evidence, cross),
+            solver=solver,
+        )
+        return SelectiveResult(one.output[:, 0], one.variance[:, 0], one.state)
     dim, value_dim = evidence.shape[-1], cross.shape[-2]
     if dim > _lib.KEY_DIM or value_dim > _lib.VALUE_DIM:
         raise ValueError(

@@ -229,3 +229,60 @@ def test_nonpositive_floor_propagates_nan(gpu_lib):
     got = run_gpu(data, chunk=4)
     assert np.isnan(got["variance"][:, 0, 0]).all()
     assert np.isfinite(got["variance"][:, :, 1:]).all()
+
+
+def decode_problem(batch=4, heads=8, seed=21, steps=1):
+    """Resident states after a 96-token prefill (slow decay, floor 1e-2),
+    then `steps` new tokens, as BASELINE config 4 at a small batch."""
+    from mamba4_amd.inputs import synthetic_inputs
+
+    pre = synthetic_inputs(batch, 96 + steps, heads, decay_mean=3.0, seed=seed)
+    head = {n: (pre[n][:, :96] if n != "floor" else pre[n]) for n in NAMES}
+    _, _, s, c = oracle.dense_reference(*(head[n] for n in NAMES))
+    tail = {n: (pre[n][:, 96:] if n != "floor" else pre[n]) for n in NAMES}
+    return s.astype(np.float32), c.astype(np.float32), tail
+
+
+def test_decode_in_place_matches_oracle_over_steps(gpu_lib):
+    from mamba4_amd import SelectiveState, selective_decode_
+
+    s, c, tail = decode_problem(steps=5)
+    dev = torch.device("cuda:0")
+    state = SelectiveState(torch.tensor(s, device=dev), torch.tensor(c, device=dev))
+    want_s, want_c = s.astype(np.float64), c.astype(np.float64)
+    announce("in-place decode B4 H8 D64, 5 steps")
+    for i in range(5):
+        args = [tail[n][:, i] if n != "floor" else tail[n] for n in NAMES]
+        step = selective_decode_(state, *(torch.tensor(a, device=dev) for a in args))
+        out, var, want_s, want_c = oracle.decode_step(want_s, want_c, *args)
+        assert normwise(host(step.output), out) <= 1e-4, i
+        assert normwise(host(step.variance), var) <= 1e-4, i
+    assert normwise(host(state.evidence), want_s) <= 1e-5
+    assert normwise(host(state.cross), want_c) <= 1e-5
+
+
+def test_decode_gradients_match_one_token_oracle(gpu_lib):
+    from mamba4_amd import SelectiveState, selective_decode
+
+    s, c, tail = decode_problem(batch=2, heads=3, seed=5)
+    dev = torch.device("cuda:0")
+    args = [tail[n][:, 0] if n != "floor" else tail[n] for n in NAMES]
+    tensors = [torch.tensor(a, device=dev, requires_grad=True) for a in args]
+    st = [torch.tensor(x, device=dev, requires_grad=True) for x in (s, c)]
+    rng = np.random.default_rng(3)
+    d_out = rng.normal(size=(2, 3, 64))
+    d_var = rng.normal(size=(2, 3))
+    announce("differentiable decode B2 H3 D64")
+    step = selective_decode(SelectiveState(*st), *tensors)
+    loss = (step.output * torch.tensor(d_out, device=dev, dtype=torch.float32)).sum()
+    loss = loss + (step.variance * torch.tensor(d_var, device=dev, dtype=torch.float32)).sum()
+    loss.backward()
+    one = {n: (tail[n][:, :1] if n != "floor" else tail[n]) for n in NAMES}
+    _, res = oracle.forward(*(one[n].astype(np.float64) for n in NAMES), chunk=1, initial=(s, c))
+    want = oracle.backward(res, d_out[:, None], d_var[:, None])
+    for n, t in zip(NAMES, tensors):
+        got = host(t.grad)
+        ref = want[n][:, 0] if n != "floor" else want[n]
+        assert normwise(got, ref) <= 1e-3, n
+    assert normwise(host(st[0].grad), want["initial_evidence"]) <= 1e-3
+    assert normwise(host(st[1].grad), want["initial_cross"]) <= 1e-3
