@@ -2,12 +2,17 @@
 
 Usage: ``python -m mamba4_amd.build`` (or ``__graft_entry__.build()``).
 hipcc cross-compiles for gfx950 without a GPU.  Every HIP source is built
-with packed-FP32 instruction selection disabled.
+with packed-FP32 instruction selection disabled.  The sources compile in
+parallel; the ones with hand-written DPP multiply-adds are also compiled to
+assembly and checked by ``check_dpp_hazards`` before the library is
+replaced.
 """
 
 import os
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -20,8 +25,6 @@ FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
-    "-fPIC",
-    "-shared",
     "-Wall",
     "-Wno-unused-function",
     "-Xclang",
@@ -30,29 +33,80 @@ FLAGS = [
     "-packed-fp32-ops",
 ]
 
+# Sources whose inline-asm DPP multiply-adds are re-checked on the compiled code.
+HAZARD_CHECKED = ["factor.hip"]
+
+_NOISE = "is not a recognized feature for this target"
+
 
 def hipcc():
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     return os.path.join(rocm, "bin", "hipcc")
 
 
+def _run(cmd):
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    stderr = "\n".join(line for line in proc.stderr.splitlines() if _NOISE not in line)
+    return proc.returncode, stderr
+
+
 def build(verbose=False):
     """Compile every source into the shared library; raises on failure."""
-    sources = [os.path.join(CSRC, s) for s in SOURCES]
-    out_tmp = LIBRARY + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-I", os.path.join(ROOT, "include"), "-o", out_tmp, *sources]
+    include = ["-I", os.path.join(ROOT, "include")]
+    with tempfile.TemporaryDirectory(prefix="m4mr_build_") as tmp:
+        jobs = {}
+        for src in SOURCES:
+            obj = os.path.join(tmp, src.replace(".hip", ".o"))
+            jobs[src] = (obj, [hipcc(), *FLAGS, "-fPIC", "-c", *include, "-o", obj,
+                               os.path.join(CSRC, src)])
+        asms = {}
+        for src in HAZARD_CHECKED:
+            asm = os.path.join(tmp, src.replace(".hip", ".s"))
+            asms[src] = (asm, [hipcc(), *FLAGS, "--cuda-device-only", "-S", *include, "-o", asm,
+                               os.path.join(CSRC, src)])
+        workers = min(8, len(jobs) + len(asms))
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            results = {k: pool.submit(_run, cmd) for k, (_, cmd) in jobs.items()}
+            asm_results = {k: pool.submit(_run, cmd) for k, (_, cmd) in asms.items()}
+            for src, fut in list(results.items()) + list(asm_results.items()):
+                rc, stderr = fut.result()
+                if rc != 0:
+                    raise RuntimeError(f"hipcc failed on {src} ({rc}):\n{stderr}")
+                if verbose and stderr.strip():
+                    print(stderr, file=sys.stderr)
+        check_hazards({src: open(path).read() for src, (path, _) in asms.items()}, verbose)
+        out_tmp = os.path.join(tmp, "lib.so")
+        rc, stderr = _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", out_tmp,
+                           *(obj for obj, _ in jobs.values())])
+        if rc != 0:
+            raise RuntimeError(f"link failed ({rc}):\n{stderr}")
+        _install(out_tmp)
     if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{stderr}")
-    if stderr.strip() and verbose:
-        print(stderr, file=sys.stderr)
-    os.replace(out_tmp, LIBRARY)
+        print(LIBRARY, flush=True)
     return LIBRARY
 
 
+def _install(path):
+    """Copy the linked library next to the package, replacing it atomically."""
+    staging = LIBRARY + ".tmp"
+    with open(path, "rb") as src, open(staging, "wb") as dst:
+        dst.write(src.read())
+    os.chmod(staging, 0o755)
+    os.replace(staging, LIBRARY)
+
+
+def check_hazards(asm_texts, verbose=False):
+    """Raise if a hand-written DPP read in the compiled code is unsafe."""
+    from mamba4_amd import check_dpp_hazards
+
+    for src, text in asm_texts.items():
+        problems = check_dpp_hazards.check(text)
+        if problems:
+            raise RuntimeError(f"DPP hazard in {src}:\n" + "\n".join(problems[:20]))
+        if verbose:
+            print(f"{src}: {text.count('v_fmac_f32_dpp')} DPP multiply-adds, no hazards",
+                  flush=True)
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    build(verbose=True)

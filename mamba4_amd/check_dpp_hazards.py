@@ -1,0 +1,78 @@
+"""Static check of the hand-written DPP multiply-adds in compiled gfx950 code.
+
+rows16.hpp emits ``v_fmac_f32_dpp`` through inline asm, which the compiler's
+hazard recognizer does not inspect.  GFX9 requires two wait states between
+a VALU instruction that writes a VGPR and a DPP instruction that reads it.
+This script reads the AMD assembly of our own build and fails if any
+``v_fmac_f32_dpp`` reads, as its DPP source, a VGPR written by a VALU
+instruction fewer than two wait states earlier (every instruction counts
+one wait state, ``s_nop N`` counts N+1).  After a label or branch the
+history is unknown, so a DPP multiply-add within two wait states of one is
+also reported.
+"""
+
+import re
+import sys
+
+_REG = re.compile(r"v\[(\d+):(\d+)\]|v(\d+)")
+
+
+def _regs(text):
+    out = set()
+    for m in _REG.finditer(text):
+        if m.group(3) is not None:
+            out.add(int(m.group(3)))
+        else:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    return out
+
+
+def check(asm_text):
+    """Return a list of violation descriptions (empty when the code is safe)."""
+    problems = []
+    history = []  # (wait states since, set of VGPRs written) for recent VALU writes
+    unknown = 0  # wait states left during which the history is unknown
+    kernel = "?"
+    for line_no, raw in enumerate(asm_text.splitlines(), 1):
+        line = raw.split(";")[0].strip()
+        if not line or line.startswith("."):
+            if line.startswith(".type") or line.startswith(".globl"):
+                kernel = line.split()[-1].split(",")[0]
+            continue
+        if line.endswith(":"):
+            history, unknown = [], 2
+            continue
+        mnemonic, _, operands = line.partition(" ")
+        if mnemonic == "v_fmac_f32_dpp":
+            ops = [o.strip() for o in operands.split(",")]
+            src0 = _regs(ops[1])
+            if unknown > 0:
+                problems.append(f"{kernel}:{line_no}: DPP FMA right after a label/branch")
+            for age, written in history:
+                if age < 2 and written & src0:
+                    problems.append(f"{kernel}:{line_no}: {line} reads v{sorted(written & src0)} "
+                                    f"written {age} wait state(s) earlier")
+        waits = int(operands) + 1 if mnemonic == "s_nop" else 1
+        history = [(age + waits, w) for age, w in history if age + waits < 2]
+        unknown = max(0, unknown - waits)
+        if mnemonic.startswith("s_branch") or mnemonic.startswith("s_cbranch"):
+            history, unknown = [], 2
+        if mnemonic.startswith("v_") and not mnemonic.startswith("v_cmp"):
+            dst = operands.split(",")[0]
+            written = _regs(dst)
+            if written:
+                history.append((0, written))
+    return problems
+
+
+def main(paths):
+    bad = []
+    for path in paths:
+        bad += [f"{path}: {p}" for p in check(open(path).read())]
+    for p in bad:
+        print(p, file=sys.stderr)
+    return 1 if bad else 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))

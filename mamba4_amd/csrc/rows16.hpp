@@ -65,6 +65,31 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// acc += src[lane L of the row] * mul as one v_fmac_f32_dpp (row_newbcast:L).
+// The caller guarantees src was not written by the previous two VALU
+// instructions (see factor_step).
+template <int L>
+__device__ __forceinline__ void fmac_bcast(float& acc, float src, float mul) {
+  asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+               : "+v"(acc)
+               : "v"(src), "v"(mul), "n"(L));
+}
+
+// Column K of every row slot that holds it (slots m >= K/16 and >= J/16)
+// takes l_KJ, broadcast from lane K%16 of slot K/16.
+template <int J, int K>
+__device__ __forceinline__ void update_column(float (&A)[4][64], const float (&nl)[4]) {
+  constexpr int r = K >> 4, mj = J >> 4, m0 = r > mj ? r : mj;
+#pragma unroll
+  for (int m = m0; m < 4; ++m) fmac_bcast<(K & 15)>(A[m][K], A[r][J], nl[m]);
+}
+
+template <int J, int... I>
+__device__ __forceinline__ void update_columns(float (&A)[4][64], const float (&nl)[4],
+                                               std::integer_sequence<int, I...>) {
+  (update_column<J, J + 1 + I>(A, nl), ...);
+}
+
 constexpr int slot_cols(int m) { return 16 * (m + 1); }
 
 // In-place Cholesky of A + diag(floor); fl[m] is the floor of row a+16m.
@@ -82,19 +107,27 @@ __device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)
   const float rs = __builtin_amdgcn_rsqf(piv);
 #pragma unroll
   for (int m = mj; m < 4; ++m) A[m][J] *= rs;
-  // A[m][k] += (-l_ij) * l_kj.  Column k's broadcast l_kj is consumed at
-  // once by every row slot that holds column k (slots m >= k/16), which
-  // keeps one broadcast live at a time.
+  // GFX9 needs two wait states between a VALU write of a VGPR and a DPP read
+  // of it, and the compiler's hazard tracking does not see inside inline asm.
+  // Passing the freshly scaled column through this s_nop as in/out operands
+  // orders every write of it before the nop and every DPP read after it.
+  // (The build re-checks this hazard on the compiled code, see
+  // mamba4_amd/check_dpp_hazards.py.)
+  if constexpr (mj == 0)
+    asm volatile("s_nop 1" : "+v"(A[0][J]), "+v"(A[1][J]), "+v"(A[2][J]), "+v"(A[3][J]));
+  else if constexpr (mj == 1)
+    asm volatile("s_nop 1" : "+v"(A[1][J]), "+v"(A[2][J]), "+v"(A[3][J]));
+  else if constexpr (mj == 2)
+    asm volatile("s_nop 1" : "+v"(A[2][J]), "+v"(A[3][J]));
+  else
+    asm volatile("s_nop 1" : "+v"(A[3][J]));
   float nl[4];
 #pragma unroll
   for (int m = mj; m < 4; ++m) nl[m] = -A[m][J];
-#pragma unroll
-  for (int k = J + 1; k < 64; ++k) {
-    const float lkj = bcast16(A[k >> 4][J], k & 15);
-#pragma unroll
-    for (int m = (k >> 4) > mj ? (k >> 4) : mj; m < 4; ++m)
-      A[m][k] = __builtin_fmaf(lkj, nl[m], A[m][k]);
-  }
+  // A[m][k] += (-l_ij) * l_kj as one v_fmac_f32_dpp per element, the l_kj
+  // operand broadcast straight from lane k%16 (the compiler keeps the
+  // broadcast in a separate v_mov_b32_dpp otherwise).
+  update_columns<J>(A, nl, std::make_integer_sequence<int, 63 - J>{});
   A[mj][J] = a == lj ? rs : A[mj][J];
 }
 
