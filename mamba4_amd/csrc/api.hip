@@ -222,7 +222,7 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   rc = launch("fwd_factor", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3((subseqs + 3) / 4), dim3(64), 0, st, d, keys,
+    hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3((subseqs + 3) / 4), dim3(128), 0, st, d, keys,
                        queries, beta, log_decay, floor, start_evidence, solved, factors);
   });
   if (rc) return rc;

@@ -6,9 +6,10 @@
 // evidence it applies each token's gated rank-one update
 // E = lam E + beta k k^T (:90-92), factors E + diag(floor) by Cholesky with
 // reciprocal pivots (:93-113), solves L L^T y = q (:45-75) and stores the
-// factor.  Each wave runs four (batch, head, chunk) sequences that share the
-// chunk index; the running evidence of each lives in LDS between tokens
-// (40 KB per wave, quad-interleaved so every 16-byte access is
+// factor.  A block runs four (batch, head, sub-chunk) sequences that share
+// the sub-chunk index, one per 16-lane row, with two waves taking alternate
+// tokens; the running evidence of each sequence lives in LDS between tokens
+// (40 KB per block, quad-interleaved so every 16-byte access is
 // conflict-free), the working matrix in VGPRs.
 //
 // factored_solve_kernel restates _factored_kernel (:155-174): stream four
@@ -31,12 +32,39 @@ __device__ __forceinline__ int wave_max4(int x) {
   return max(max(a0, a1), max(a2, a3));
 }
 
-__global__ __launch_bounds__(64) void fwd_factor_kernel(
+// One token's inputs for this lane's four rows: key and query rows a+16m,
+// beta and the decay lam.
+struct TokenInputs {
+  float k[4], q[4], beta, lam;
+  long th;
+};
+
+__device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const float* keys,
+                                           const float* queries, const float* beta,
+                                           const float* log_decay, int b, int h, int t, int a) {
+  in.th = token_head(d, b, t, h);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    in.k[m] = keys[in.th * 64 + a + 16 * m];
+    in.q[m] = queries[in.th * 64 + a + 16 * m];
+  }
+  in.beta = beta[in.th];
+  in.lam = expf(log_decay[in.th]);
+}
+
+// Two waves share the four sequences of a block and take alternate tokens:
+// wave w factors tokens base+w for base = 0, 2, 4, ...  The running evidence
+// lives in LDS; in turn (wave 0, then wave 1) each wave reads it, applies
+// its token's rank-one update, writes it back and keeps the updated copy in
+// registers.  Only these short update turns are serialized; the two waves'
+// factorizations and solves overlap, and a block holds one 40 KB evidence
+// buffer for two waves.
+__global__ __launch_bounds__(128) void fwd_factor_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ queries,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ floor, const float* __restrict__ start_s,
     float* __restrict__ solved, float* __restrict__ factors) {
-  const int lane = threadIdx.x, a = lane & 15, mu = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, a = lane & 15, mu = lane >> 4;
   const int BH = d.B * d.H;
   const long nseq = (long)BH * d.NS;
   long seq = (long)blockIdx.x * 4 + mu;
@@ -50,55 +78,67 @@ __global__ __launch_bounds__(64) void fwd_factor_kernel(
   const int t0 = n * d.chunk + sub_first(d, u);
   const int steps = wave_max4(len);
 
-  __shared__ f4 evidence[40 * 64];  // [quad][lane]
-  const float* s0 = start_s + ((long)bh * d.NS + ns) * 4096;
+  __shared__ f4 evidence[40 * 64];  // [quad][lane], shared by both waves
+  if (wave == 0) {
+    const float* s0 = start_s + ((long)bh * d.NS + ns) * 4096;
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int q = 0; q < 4 * m + 4; ++q)
-      evidence[slot_quad(m, q) * 64 + lane] =
-          *reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
+      for (int q = 0; q < 4 * m + 4; ++q)
+        evidence[slot_quad(m, q) * 64 + lane] =
+            *reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
+  }
   float fl[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) fl[m] = floor[h * 64 + a + 16 * m];
+  // Rows past their sequence read token 0 (in bounds; never stored).
+  auto token = [&](int tt) { return tt < len ? t0 + tt : 0; };
+  TokenInputs cur;
+  load_token(cur, d, keys, queries, beta, log_decay, b, h, token(wave), a);
+  __syncthreads();
 
-  for (int tt = 0; tt < steps; ++tt) {
-    const bool valid = tt < len;
-    const long th = token_head(d, b, valid ? t0 + tt : 0, h);
-    float kr[4], qr[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      kr[m] = keys[th * 64 + a + 16 * m];
-      qr[m] = queries[th * 64 + a + 16 * m];
-    }
-    const float bt = beta[th];
-    const float lam = expf(log_decay[th]);
+  for (int base = 0; base < steps; base += 2) {
+    const int tt = base + wave;
+    const bool mine = tt < steps;  // uniform over the wave
+    const bool valid = tt < len;   // per 16-lane row
     float A[4][64];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const float bk = bt * kr[m];
+    for (int turn = 0; turn < 2; ++turn) {
+      if (turn == wave && mine) {
 #pragma unroll
-      for (int q = 0; q < 4 * m + 4; ++q) {
-        f4 sv = evidence[slot_quad(m, q) * 64 + lane];
+        for (int m = 0; m < 4; ++m) {
+          const float bk = cur.beta * cur.k[m];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int k = 4 * q + e;
-          sv[e] = lam * sv[e] + bk * bcast16(kr[k >> 4], k & 15);
-          A[m][k] = sv[e];
+          for (int q = 0; q < 4 * m + 4; ++q) {
+            f4 sv = evidence[slot_quad(m, q) * 64 + lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k = 4 * q + e;
+              sv[e] = cur.lam * sv[e] + bk * bcast16(cur.k[k >> 4], k & 15);
+              A[m][k] = sv[e];
+            }
+            evidence[slot_quad(m, q) * 64 + lane] = sv;
+            // Keeps the compiler from hoisting all 40 LDS reads ahead of the
+            // arithmetic (which would need 160 more registers).
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
-        evidence[slot_quad(m, q) * 64 + lane] = sv;
-        // Keep the scheduler from hoisting all 40 LDS reads ahead of the
-        // updates (that doubles the live registers and spills to AGPRs).
-        __builtin_amdgcn_sched_barrier(0);
       }
+      __syncthreads();
     }
-    factor_rows16(A, fl);
-    float y[4];
-    solve_rows16(A, qr, y);
-    if (valid) {
+    if (mine) {
+      // Prefetch this wave's next token; the factorization covers the latency.
+      TokenInputs next;
+      load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
+      factor_rows16(A, fl);
+      float y[4];
+      solve_rows16(A, cur.q, y);
+      if (valid) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) solved[th * 64 + a + 16 * m] = y[m];
-      store_rows16(A, factors + th * ROWS_FACTOR);
+        for (int m = 0; m < 4; ++m) solved[cur.th * 64 + a + 16 * m] = y[m];
+        store_rows16(A, factors + cur.th * ROWS_FACTOR);
+      }
+      cur = next;
     }
   }
 }

@@ -286,3 +286,16 @@ def test_decode_gradients_match_one_token_oracle(gpu_lib):
         assert normwise(got, ref) <= 1e-3, n
     assert normwise(host(st[0].grad), want["initial_evidence"]) <= 1e-3
     assert normwise(host(st[1].grad), want["initial_cross"]) <= 1e-3
+
+
+@pytest.mark.parametrize("time, chunk", [(90, 64), (1, 64), (33, 64), (65, 64), (7, 3)])
+def test_ragged_lengths_and_empty_sub_chunks(gpu_lib, time, chunk):
+    """Sequence ends inside a chunk, an empty second sub-chunk (T=90: the
+    last chunk holds 26 tokens), a single token, and chunk boundaries +-1."""
+    data = arrays(time=time, heads=3, dim=64, value_dim=64, seed=time)
+    data["floor"] = np.full_like(data["floor"], 0.05)
+    announce(f"ragged T={time} chunk={chunk}")
+    got = run_gpu(data, chunk=chunk)
+    want = oracle.dense_reference(*(data[n] for n in NAMES))
+    for key, ref in zip(["output", "variance", "evidence", "cross"], want):
+        assert normwise(got[key], ref) <= 1e-5, (key, time, chunk)
