@@ -146,6 +146,30 @@ int m4mr_decode_step(float* evidence, float* cross,
                      float* output, float* variance, void* stream);
 
 /*
+ * Batched SPD solve: precision_n y_n = rhs_n for N systems of width dim
+ * (1 <= dim <= 64).  precision [N,dim,dim] row-major, of which only the
+ * lower triangle (column <= row) is read; rhs and solution [N,dim].  When
+ * `factors` is non-NULL it receives each system's factor
+ * [N, M4MR_FACTOR_FLOATS] (the system padded to 64 with an identity block),
+ * the residual m4mr_spd_solve_backward consumes.
+ * Replaces spd_solve and its forward rule (lm/kernels/mamba4.py:190-201,
+ * _factor_and_solve :164-187); every reference backend ("loop",
+ * "blocked", "unrolled", "auto", "fused") solves the same system.
+ */
+int m4mr_spd_solve(const float* precision, const float* rhs, long N, int dim,
+                   float* solution, float* factors, void* stream);
+
+/*
+ * VJP of m4mr_spd_solve (lm/kernels/mamba4.py:204-215): with
+ * z = precision^-1 d_solution from the stored factors, writes
+ * d_rhs = z [N,dim] and the full symmetric d_precision = -(z y^T + y z^T)/2
+ * [N,dim,dim], y = solution.  No refactorization.
+ */
+int m4mr_spd_solve_backward(const float* factors, const float* solution,
+                            const float* d_solution, long N, int dim,
+                            float* d_precision, float* d_rhs, void* stream);
+
+/*
  * Kernel timing with HIP events recorded on the launch stream.  While
  * enabled, every kernel launch is bracketed by a pair of events.
  * m4mr_profile_read() waits for the recorded events and returns the total

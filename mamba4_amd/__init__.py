@@ -2,7 +2,8 @@
 
 A drop-in for the reference's lm/kernels memory-read API
 (``selective_gaussian_memory``, ``selective_decode``,
-``selective_initial_state``, ``SelectiveState``, ``SelectiveResult``),
+``selective_initial_state``, ``spd_solve``, ``SelectiveState``,
+``SelectiveResult``),
 implemented by hand-written HIP kernels behind the C ABI in
 ``include/mamba4_memread.h``.
 """
@@ -16,6 +17,7 @@ from mamba4_amd.memory import (  # noqa: F401
     selective_decode_,
     selective_gaussian_memory,
     selective_initial_state,
+    spd_solve,
 )
 
 __all__ = [
@@ -27,4 +29,5 @@ __all__ = [
     "selective_decode_",
     "selective_gaussian_memory",
     "selective_initial_state",
+    "spd_solve",
 ]

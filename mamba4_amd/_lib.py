@@ -36,6 +36,8 @@ SIGNATURES = {
     ),
     "m4mr_factored_solve": (_I, [_P, _P, _P, _L, _P]),
     "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _P, _P, _P]),
+    "m4mr_spd_solve": (_I, [_P, _P, _L, _I, _P, _P, _P]),
+    "m4mr_spd_solve_backward": (_I, [_P, _P, _P, _L, _I, _P, _P, _P]),
     "m4mr_profile_enable": (None, [_I]),
     "m4mr_profile_reset": (None, []),
     "m4mr_profile_read": (

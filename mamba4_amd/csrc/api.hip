@@ -38,6 +38,9 @@ __global__ void bwd_grads_kernel(Dims, const float*, const float*, const float*,
                                  const float*, const float*, const float*, const float*, float*,
                                  float*, float*, float*, float*, float*);
 __global__ void floor_reduce_kernel(Dims, const float*, float*);
+__global__ void spd_solve_kernel(const float*, const float*, long, int, float*, float*);
+__global__ void spd_backward_kernel(const float*, const float*, const float*, long, int, float*,
+                                    float*);
 }  // namespace m4
 
 namespace {
@@ -48,7 +51,8 @@ thread_local std::string g_error;
 
 const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_factor", "fwd_read",
                                     "bwd_dy",         "factored_solve", "bwd_local", "bwd_scan",
-                                    "bwd_grads",      "floor_reduce", "decode_step"};
+                                    "bwd_grads",      "floor_reduce", "decode_step",
+                                    "spd_solve",      "spd_backward"};
 
 struct ProfRecord {
   const char* name;
@@ -174,6 +178,10 @@ BackwardWorkspace carve(void* base, int B, int T, int H, int chunk) {
   w.bytes = off;
   return w;
 }
+
+// Four systems per 64-thread block on a one-dimensional grid of at most
+// 2^31 - 1 blocks.
+constexpr long kMaxSystems = ((1L << 31) - 1) * 4;
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
@@ -318,7 +326,8 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
 int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N,
                         void* stream) {
   g_error.clear();
-  if (N <= 0) return fail(M4MR_EINVAL, "m4mr_factored_solve: N must be positive");
+  if (N <= 0 || N > kMaxSystems)
+    return fail(M4MR_EINVAL, "m4mr_factored_solve: need 0 < N < 2^33");
   if (!factors || !rhs || !z) return fail(M4MR_EINVAL, "m4mr_factored_solve: NULL pointer");
   if (misaligned(factors)) return fail(M4MR_EINVAL, "m4mr_factored_solve: factors must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -333,7 +342,7 @@ int m4mr_decode_step(float* evidence, float* cross, const float* key, const floa
                      const float* floor, long N, int H, float* output, float* variance,
                      void* stream) {
   g_error.clear();
-  if (N <= 0 || H <= 0 || N % H != 0)
+  if (N <= 0 || N > kMaxSystems || H <= 0 || N % H != 0)
     return fail(M4MR_EINVAL, "m4mr_decode_step: N must be a positive multiple of H");
   const void* need[] = {evidence, cross, key, value, query, beta, log_decay, floor, output, variance};
   for (const void* p : need)
@@ -345,6 +354,40 @@ int m4mr_decode_step(float* evidence, float* cross, const float* key, const floa
     hipLaunchKernelGGL(m4::decode_step_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
                        evidence, cross, key, value, query, beta, log_decay, floor, N, H, output,
                        variance);
+  });
+}
+
+int m4mr_spd_solve(const float* precision, const float* rhs, long N, int dim, float* solution,
+                   float* factors, void* stream) {
+  g_error.clear();
+  if (N <= 0 || N > kMaxSystems || dim < 1 || dim > M4MR_KEY_DIM)
+    return fail(M4MR_EINVAL, "m4mr_spd_solve: need 0 < N < 2^33 and 1 <= dim <= 64");
+  if (!precision || !rhs || !solution)
+    return fail(M4MR_EINVAL, "m4mr_spd_solve: a required pointer is NULL");
+  if ((factors && misaligned(factors)) || (dim == M4MR_KEY_DIM && misaligned(precision)))
+    return fail(M4MR_EINVAL, "m4mr_spd_solve: factors (and a 64-wide precision) must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return launch("spd_solve", st, [&] {
+    hipLaunchKernelGGL(m4::spd_solve_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
+                       precision, rhs, N, dim, solution, factors);
+  });
+}
+
+int m4mr_spd_solve_backward(const float* factors, const float* solution,
+                            const float* d_solution, long N, int dim, float* d_precision,
+                            float* d_rhs, void* stream) {
+  g_error.clear();
+  if (N <= 0 || N > kMaxSystems || dim < 1 || dim > M4MR_KEY_DIM)
+    return fail(M4MR_EINVAL, "m4mr_spd_solve_backward: need 0 < N < 2^33 and 1 <= dim <= 64");
+  if (!factors || !solution || !d_solution || !d_precision || !d_rhs)
+    return fail(M4MR_EINVAL, "m4mr_spd_solve_backward: a required pointer is NULL");
+  if (misaligned(factors) || (dim == M4MR_KEY_DIM && misaligned(d_precision)))
+    return fail(M4MR_EINVAL,
+                "m4mr_spd_solve_backward: factors (and a 64-wide d_precision) must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return launch("spd_backward", st, [&] {
+    hipLaunchKernelGGL(m4::spd_backward_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
+                       factors, solution, d_solution, N, dim, d_precision, d_rhs);
   });
 }
 

@@ -161,6 +161,121 @@ __global__ __launch_bounds__(64) void factored_solve_kernel(const float* __restr
     for (int m = 0; m < 4; ++m) z[th * 64 + a + 16 * m] = y[m];
 }
 
+// Batched SPD solve, four systems per wave: precision [N,dim,dim] (only
+// k <= i is read), rhs [N,dim] -> solution [N,dim] and, when `factors` is
+// non-null, each system's factor in the padded-row layout.  Systems are
+// padded to 64 with an identity block, so the padded coordinates solve to
+// zero, as the reference pads its lanes with identity systems
+// (lm/kernels/mamba4_fused.py:292-299).  Restates _factor_and_solve
+// (lm/kernels/mamba4.py:164-187).
+__global__ __launch_bounds__(64) void spd_solve_kernel(const float* __restrict__ precision,
+                                                       const float* __restrict__ rhs, long N,
+                                                       int dim, float* __restrict__ solution,
+                                                       float* __restrict__ factors) {
+  const int lane = threadIdx.x, a = lane & 15, mu = lane >> 4;
+  long n = (long)blockIdx.x * 4 + mu;
+  const bool active = n < N;
+  if (!active) n = N - 1;
+  const float* P = precision + n * dim * dim;
+  float A[4][64];
+  if (dim == 64) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int i = a + 16 * m, p = i >> 2;
+#pragma unroll
+      for (int q = 0; q < 4 * m + 4; ++q) {
+        f4 v = f4{0.f, 0.f, 0.f, 0.f};
+        if (q <= p) v = *reinterpret_cast<const f4*>(P + i * 64 + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) A[m][4 * q + e] = 4 * q + e <= i ? v[e] : 0.f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int i = a + 16 * m;
+#pragma unroll
+      for (int k = 0; k < slot_cols(m); ++k) {
+        float v = k == i ? 1.f : 0.f;
+        if (i < dim && k <= i) v = P[i * dim + k];
+        A[m][k] = v;
+      }
+    }
+  }
+  const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+  factor_rows16(A, zero);
+  float r[4], y[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = a + 16 * m;
+    r[m] = i < dim ? rhs[n * dim + i] : 0.f;
+  }
+  solve_rows16(A, r, y);
+  if (active) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      if (a + 16 * m < dim) solution[n * dim + a + 16 * m] = y[m];
+    if (factors) store_rows16(A, factors + n * ROWS_FACTOR);
+  }
+}
+
+// VJP of the batched SPD solve (lm/kernels/mamba4.py:204-215): z = A^-1 g
+// from the stored factor, d_rhs = z and d_precision = -(z y^T + y z^T) / 2.
+__global__ __launch_bounds__(64) void spd_backward_kernel(
+    const float* __restrict__ factors, const float* __restrict__ solution,
+    const float* __restrict__ d_solution, long N, int dim, float* __restrict__ d_precision,
+    float* __restrict__ d_rhs) {
+  const int lane = threadIdx.x, a = lane & 15, mu = lane >> 4;
+  long n = (long)blockIdx.x * 4 + mu;
+  const bool active = n < N;
+  if (!active) n = N - 1;
+  float A[4][64];
+  load_rows16(A, factors + n * ROWS_FACTOR);
+  float g[4], y[4], z[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int i = a + 16 * m;
+    g[m] = i < dim ? d_solution[n * dim + i] : 0.f;
+    y[m] = i < dim ? solution[n * dim + i] : 0.f;
+  }
+  solve_rows16(A, g, z);
+  if (!active) return;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (a + 16 * m < dim) d_rhs[n * dim + a + 16 * m] = z[m];
+  float* dP = d_precision + n * dim * dim;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    float yk[4], zk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 4 * q + e;
+      yk[e] = bcast16(y[k >> 4], k & 15);
+      zk[e] = bcast16(z[k >> 4], k & 15);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int i = a + 16 * m;
+      if (i >= dim) continue;
+      f4 v;
+      {
+        // Both products rounded on their own (no contraction into an FMA),
+        // so the sum, and d_precision, is exactly symmetric.
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = -0.5f * (z[m] * yk[e] + y[m] * zk[e]);
+      }
+      if (dim == 64) {
+        *reinterpret_cast<f4*>(dP + i * 64 + 4 * q) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (4 * q + e < dim) dP[i * dim + 4 * q + e] = v[e];
+      }
+    }
+  }
+}
+
 // One decode step for four (batch*head) states per wave, in place.
 __global__ __launch_bounds__(64) void decode_step_kernel(
     float* __restrict__ evidence, float* __restrict__ cross, const float* __restrict__ key,

@@ -3,7 +3,8 @@
 Same names, arguments, NamedTuples and error behaviour as the reference's
 ``selective_gaussian_memory`` (lm/kernels/mamba4.py:228-338),
 ``selective_decode`` (:341-355), ``selective_initial_state`` (:221-225),
-``SelectiveState`` / ``SelectiveResult`` (:18-28), with torch tensors on a
+``spd_solve`` (:190-217), ``SelectiveState`` / ``SelectiveResult``
+(:18-28), with torch tensors on a
 ROCm device in place of JAX arrays.  Every call runs the gfx950 HIP library
 through its C ABI on the current torch stream; there is no other
 implementation, and CPU tensors are rejected.
@@ -142,6 +143,73 @@ class _MemoryRead(torch.autograd.Function):
         )
         d_init = (d_init_s, d_init_c) if ctx.has_initial else (None, None)
         return (*grads, *d_init, None)
+
+
+class _SpdSolve(torch.autograd.Function):
+    """Custom VJP around m4mr_spd_solve / m4mr_spd_solve_backward."""
+
+    @staticmethod
+    def forward(ctx, precision, rhs):
+        lib = _lib.load()
+        count, dim = rhs.shape
+        f32 = dict(dtype=torch.float32, device=rhs.device)
+        solution = torch.empty((count, dim), **f32)
+        factors = torch.empty((count, _lib.FACTOR_FLOATS), **f32)
+        _lib.check(
+            lib.m4mr_spd_solve(
+                _ptr(precision), _ptr(rhs), count, dim, _ptr(solution), _ptr(factors), _stream()
+            )
+        )
+        ctx.save_for_backward(factors, solution)
+        return solution
+
+    @staticmethod
+    def backward(ctx, gradient):
+        lib = _lib.load()
+        factors, solution = ctx.saved_tensors
+        count, dim = solution.shape
+        gradient = gradient.to(torch.float32).contiguous()
+        d_precision = torch.empty((count, dim, dim), dtype=torch.float32, device=solution.device)
+        d_rhs = torch.empty_like(solution)
+        _lib.check(
+            lib.m4mr_spd_solve_backward(
+                _ptr(factors), _ptr(solution), _ptr(gradient), count, dim,
+                _ptr(d_precision), _ptr(d_rhs), _stream(),
+            )
+        )
+        return d_precision, d_rhs
+
+
+def spd_solve(precision, rhs, backend=None):
+    """Solve precision @ y = rhs for SPD [...,d,d] precision and [...,d] rhs.
+
+    Only the lower triangle is read.  The backward pass reuses the stored
+    Cholesky factor: z = A^-1 g, d rhs = z and d A = -sym(z y^T); no
+    inverse is formed and nothing is refactored.  Every reference backend
+    string selects the same HIP solve (the backend changes only the
+    arithmetic schedule, never the solved system, lm/kernels/mamba4.py:193-194).
+    Widths up to 64.
+    """
+    _check_solver(backend)
+    precision = torch.as_tensor(precision)
+    rhs = torch.as_tensor(rhs)
+    dim = rhs.shape[-1]
+    if precision.shape != rhs.shape + (dim,):
+        raise ValueError(
+            f"spd_solve needs precision [...,d,d] and rhs [...,d]; got "
+            f"{tuple(precision.shape)} and {tuple(rhs.shape)}"
+        )
+    _require_device(precision, rhs)
+    if dim > _lib.KEY_DIM:
+        raise ValueError(f"spd_solve supports widths <= {_lib.KEY_DIM}; got {dim}")
+    batch = rhs.shape[:-1]
+    if rhs.numel() == 0:
+        return torch.zeros(rhs.shape, dtype=torch.float32, device=rhs.device)
+    flat_a = precision.to(torch.float32).reshape(-1, dim, dim).contiguous()
+    flat_b = rhs.to(torch.float32).reshape(-1, dim).contiguous()
+    with torch.cuda.device(rhs.device):
+        solution = _SpdSolve.apply(flat_a, flat_b)
+    return solution.reshape(batch + (dim,))
 
 
 def _pad_last(x, width, value=0.0):

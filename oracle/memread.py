@@ -28,6 +28,8 @@ Functions:
 * ``decode_step`` -- one cached write/read (lm/kernels/mamba4.py:341-355).
 * ``cholesky_reciprocal`` / ``factored_solve`` -- the factor and the two
   substitutions with reciprocal pivots (lm/kernels/mamba4_fused.py:45-113).
+* ``spd_solve`` / ``spd_solve_backward`` -- the batched SPD solve and its
+  VJP (lm/kernels/mamba4.py:164-215).
 
 ``PINNED`` names, for every function, the tests that pin it against the
 reference's known answers, invariants, an independent float64 autodiff and
@@ -42,7 +44,7 @@ PINNED = {
         "tests/test_oracle.py::test_dense_zero_key_reads_the_floor",
         "tests/test_oracle.py::test_dense_single_write_retention",
         "tests/test_oracle.py::test_dense_floor_bounds_every_precision",
-        "tests/test_oracle.py::test_dense_matches_analysis_evidence_state_closed_form",
+        "tests/test_oracle.py::test_dense_matches_weighted_batch_closed_form",
     ],
     "forward": [
         "tests/test_oracle.py::test_chunked_forward_matches_dense_for_every_chunk",
@@ -62,6 +64,13 @@ PINNED = {
     ],
     "factored_solve": [
         "tests/test_oracle.py::test_factored_solve_matches_dense_solve",
+    ],
+    "spd_solve": [
+        "tests/test_oracle.py::test_spd_solve_matches_dense_solve_and_reads_lower_triangle",
+    ],
+    "spd_solve_backward": [
+        "tests/test_oracle.py::test_spd_solve_backward_matches_float64_autograd",
+        "tests/test_oracle.py::test_planted_spd_backward_mistakes_are_caught",
     ],
 }
 
@@ -160,6 +169,30 @@ def factored_solve(lower, rhs):
             - np.einsum("...k,...k->...", lower[..., j + 1 :, j], value[..., j + 1 :])
         ) * lower[..., j, j]
     return value
+
+
+def spd_solve(precision, rhs):
+    """Solve precision y = rhs for SPD [..., d, d] precision, [..., d] rhs.
+
+    Restates spd_solve / _factor_and_solve (lm/kernels/mamba4.py:164-201):
+    only the lower triangle is read (``cholesky_reciprocal`` touches column
+    entries on and below the diagonal only), then the two substitutions.
+    Returns (solution, lower factor).
+    """
+    precision = np.asarray(precision, np.float64)
+    lower = cholesky_reciprocal(precision)
+    return factored_solve(lower, np.asarray(rhs, np.float64)), lower
+
+
+def spd_solve_backward(lower, solution, gradient):
+    """VJP of ``spd_solve`` (lm/kernels/mamba4.py:204-215).
+
+    z = A^-1 g from the stored factor; d rhs = z and
+    d precision = -(z y^T + y z^T) / 2, the symmetric form.
+    """
+    z = factored_solve(lower, gradient)
+    outer = z[..., :, None] * np.asarray(solution)[..., None, :]
+    return -0.5 * (outer + np.swapaxes(outer, -1, -2)), z
 
 
 def _chunked(x, batch, count, chunk, padding):

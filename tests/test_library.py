@@ -84,3 +84,29 @@ def test_synthetic_inputs_follow_the_documented_distributions():
     np.testing.assert_array_equal(
         round_to_bf16(x), torch.tensor(x).to(torch.bfloat16).float().numpy()
     )
+
+
+def test_spd_solve_arguments_are_checked_before_any_launch():
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.c_void_p(ctypes.addressof(buf))
+    assert lib.m4mr_spd_solve(p, p, 0, 6, p, null, null) == _lib.EINVAL
+    assert lib.m4mr_spd_solve(p, p, 4, 65, p, null, null) == _lib.EINVAL
+    assert "dim" in lib.m4mr_last_error().decode()
+    assert lib.m4mr_spd_solve(null, p, 4, 6, p, null, null) == _lib.EINVAL
+    assert "NULL" in lib.m4mr_last_error().decode()
+    assert lib.m4mr_spd_solve(p, p, 1 << 34, 6, p, null, null) == _lib.EINVAL
+    assert lib.m4mr_spd_solve_backward(p, p, p, 4, 0, p, p, null) == _lib.EINVAL
+    assert lib.m4mr_spd_solve_backward(p, p, null, 4, 6, p, p, null) == _lib.EINVAL
+    assert lib.m4mr_factored_solve(p, p, p, 1 << 34, null) == _lib.EINVAL
+
+
+def test_spd_solve_python_checks():
+    a = torch.eye(6).expand(7, 6, 6)
+    with pytest.raises(ValueError, match="ROCm device"):
+        memory.spd_solve(a, torch.zeros(7, 6))
+    with pytest.raises(ValueError, match=r"precision \[...,d,d\]"):
+        memory.spd_solve(a, torch.zeros(7, 5))
+    with pytest.raises(ValueError, match="Unknown SPD solve backend"):
+        memory.spd_solve(a, torch.zeros(7, 6), backend="qr")

@@ -335,3 +335,78 @@ def test_planted_backward_mistakes_are_caught(plant, tmp_path):
     spec.loader.exec_module(module)
     with pytest.raises(AssertionError):
         compare_to_autograd(module, chunk=4)
+
+
+def spd_problem(seed=4, count=7, dim=6):
+    """The reference's spd_solve test problem (lm/tests/test_mamba4.py:60-64)."""
+    rng = np.random.default_rng(seed)
+    a = rng.normal(size=(count, dim, dim))
+    a = a @ np.swapaxes(a, -1, -2) + 0.5 * np.eye(dim)
+    rhs = rng.normal(size=(count, dim))
+    return a, rhs
+
+
+def test_spd_solve_matches_dense_solve_and_reads_lower_triangle():
+    a, rhs = spd_problem()
+    got, _ = oracle.spd_solve(a, rhs)
+    np.testing.assert_allclose(got, np.linalg.solve(a, rhs[..., None])[..., 0], rtol=1e-10)
+    garbage = a + np.triu(np.random.default_rng(1).normal(size=a.shape) * 50, 1)
+    again, _ = oracle.spd_solve(garbage, rhs)
+    np.testing.assert_array_equal(again, got)
+
+
+def compare_spd_to_autograd(module):
+    a, rhs = spd_problem()
+    # The reference's check: d/d(matrix) of sum(sin(solve(sym(matrix), rhs)))
+    # against a dense float64 solve (lm/tests/test_mamba4.py:60-81).
+    matrix = torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    vector = torch.tensor(rhs, dtype=torch.float64, requires_grad=True)
+    symmetric = (matrix + matrix.transpose(-1, -2)) / 2
+    torch.sin(torch.linalg.solve(symmetric, vector[..., None])[..., 0]).sum().backward()
+    solution, lower = module.spd_solve(a, rhs)
+    d_a, d_rhs = module.spd_solve_backward(lower, solution, np.cos(solution))
+    np.testing.assert_allclose(sym(d_a), matrix.grad.numpy(), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(d_rhs, vector.grad.numpy(), rtol=1e-9, atol=1e-12)
+    # The VJP itself is the symmetric form of -z y^T (autograd of a plain solve).
+    plain = torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    torch.sin(torch.linalg.solve(plain, vector.detach()[..., None])[..., 0]).sum().backward()
+    np.testing.assert_allclose(d_a, sym(plain.grad.numpy()), rtol=1e-9, atol=1e-12)
+
+
+def test_spd_solve_backward_matches_float64_autograd():
+    compare_spd_to_autograd(oracle)
+
+
+SPD_PLANTS = [
+    ("-0.5 * (outer + np.swapaxes", "-1.0 * (outer + np.swapaxes"),
+    ("z[..., :, None] * np.asarray(solution)[..., None, :]", "z[..., :, None] * z[..., None, :]"),
+    ("z = factored_solve(lower, gradient)", "z = np.asarray(gradient, np.float64)"),
+    ("(outer + np.swapaxes(outer, -1, -2))", "(outer - np.swapaxes(outer, -1, -2))"),
+]
+
+
+def _planted_module(plant, tmp_path):
+    source = open(oracle.__file__).read()
+    assert plant[0] in source, plant[0]
+    path = tmp_path / "planted.py"
+    path.write_text(source.replace(plant[0], plant[1]))
+    spec = importlib.util.spec_from_file_location("planted_oracle", path)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+@pytest.mark.parametrize("plant", SPD_PLANTS, ids=[p[1][:30] for p in SPD_PLANTS])
+def test_planted_spd_backward_mistakes_are_caught(plant, tmp_path):
+    with pytest.raises(AssertionError):
+        compare_spd_to_autograd(_planted_module(plant, tmp_path))
+
+
+def test_every_pinning_test_named_by_the_oracle_exists():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for function, tests in oracle.PINNED.items():
+        assert hasattr(oracle, function), function
+        for name in tests:
+            path, test = name.split("::")
+            text = open(os.path.join(root, path)).read()
+            assert f"def {test}(" in text, name
