@@ -57,56 +57,66 @@ __global__ __launch_bounds__(256) void fwd_read_kernel(
   float* Y = smem;
   float* K = Y + TILE;  // keys, then values
   float* G = K + TILE;
-  float* C0 = G + TILE;
+  float* C0 = G + TILE;  // C0 transposed: C0[e][p]
   __shared__ ChunkScalars cs;
   const SeqIndex si = seq_index(d);
-  const int w = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
 
-  load_rows(Y, si.len, rows_of(solved, d, si));
-  load_rows(K, si.len, rows_of(keys, d, si));
+  // Every global tile is fetched up front; values and C0 wait in registers
+  // while the scores are computed.
+  TileRegs ry, rk, rv, rq;
+  TileRegsT rc;
+  ry.fetch_rows(si.len, rows_of(solved, d, si));
+  rk.fetch_rows(si.len, rows_of(keys, d, si));
+  rv.fetch_rows(si.len, rows_of(values, d, si));
+  rq.fetch_rows(si.len, rows_of(queries, d, si));
+  rc.fetch_matrix(start_c + si.seq * 4096);
+  ry.store(Y);
+  rk.store(K);
+  rc.store(C0);
   load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
   __syncthreads();
 
+  // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
+  // the 16 lanes that hold the rest of each row.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = (threadIdx.x >> 4) + 16 * j;
+    const f4 prod = rq.v[j] * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
+    const float v = row16_sum(prod[0] + prod[1] + prod[2] + prod[3]);
+    if ((threadIdx.x & 15) == 0 && t < si.len)
+      variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] = v;
+  }
+
   f4 acc[4];
   zero4(acc);
-  tile_mma<false, true>(acc, Y, LDT, K, LDT, 64, w);  // scores y_t . k_s
+  tile_mma<false, true>(acc, Y, K, 64, w);  // scores y_t . k_s
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = acc_row(w, r), s = acc_col(jb);
+    for (int q = 0; q < 4; ++q) {
+      const int t = acc_row(w, q), s = acc_col<false>(jb);
       float v = 0.f;
-      if (s <= t && t < si.len) v = acc[jb][r] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
+      if (s <= t && t < si.len) v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
       G[t * LDT + s] = v;
     }
   __syncthreads();
-  load_rows(K, si.len, rows_of(values, d, si));
-  load_matrix(C0, start_c + si.seq * 4096);
+  rv.store(K);
   __syncthreads();
 
   f4 out[4], inh[4];
   zero4(out);
   zero4(inh);
-  const int kpad = (si.len + 3) & ~3;
-  tile_mma<false, false>(out, G, LDT, K, LDT, kpad, w);  // within-chunk reads
-  tile_mma<false, true>(inh, Y, LDT, C0, LDT, 64, w);    // inherited reads y_t . C0[p]
+  tile_mma<false, false>(out, G, K, k_terms(si.len), w);  // within-chunk reads
+  tile_mma<false, false>(inh, Y, C0, 64, w);              // inherited reads y_t . C0[p]
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = acc_row(w, r);
+  for (int q = 0; q < 4; ++q) {
+    const int t = acc_row(w, q);
     if (t < si.len) {
       const float carried = expf(cs.prefix[t]);
       float* dst = output + token_head(d, si.b, si.n * d.chunk + t, si.h) * 64;
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) dst[acc_col(jb)] = out[jb][r] + carried * inh[jb][r];
+      *reinterpret_cast<f4*>(dst + c4) = quad_row(out, q) + carried * quad_row(inh, q);
     }
-  }
-  if (threadIdx.x < si.len) {
-    const int t = threadIdx.x;
-    const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
-    const float* q = queries + th * 64;
-    float v = 0.f;
-    for (int e = 0; e < 64; ++e) v += q[e] * Y[t * LDT + e];
-    variance[th] = v;
   }
 }
 
@@ -123,48 +133,62 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
   float* C0 = G + TILE;
   __shared__ ChunkScalars cs;
   const SeqIndex si = seq_index(d);
-  const int w = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
 
-  load_rows(DO, si.len, rows_of(d_output, d, si));
-  load_rows(V, si.len, rows_of(values, d, si));
+  TileRegs rd, rv, rk, rc;
+  rd.fetch_rows(si.len, rows_of(d_output, d, si));
+  rv.fetch_rows(si.len, rows_of(values, d, si));
+  rk.fetch_rows(si.len, rows_of(keys, d, si));
+  rc.fetch_matrix(start_c + si.seq * 4096);
+  // Queries and d_variance of this lane's accumulator rows (read in the epilogue).
+  f4 qv[4];
+  float dvar[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int t = acc_row(w, q);
+    qv[q] = f4{0.f, 0.f, 0.f, 0.f};
+    dvar[q] = 0.f;
+    if (t < si.len) {
+      const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+      qv[q] = *reinterpret_cast<const f4*>(queries + th * 64 + c4);
+      dvar[q] = d_variance[th];
+    }
+  }
+  rd.store(DO);
+  rv.store(V);
+  rc.store(C0);
   load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
   __syncthreads();
 
   f4 acc[4];
   zero4(acc);
-  tile_mma<false, true>(acc, DO, LDT, V, LDT, 64, w);  // dout_t . v_s
+  tile_mma<false, true>(acc, DO, V, 64, w);  // dout_t . v_s
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = acc_row(w, r), s = acc_col(jb);
+    for (int q = 0; q < 4; ++q) {
+      const int t = acc_row(w, q), s = acc_col<false>(jb);
       float v = 0.f;
-      if (s <= t && t < si.len) v = acc[jb][r] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
+      if (s <= t && t < si.len) v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
       G[t * LDT + s] = v;
     }
   __syncthreads();
-  load_rows(V, si.len, rows_of(keys, d, si));
-  load_matrix(C0, start_c + si.seq * 4096);
+  rk.store(V);
   __syncthreads();
 
   f4 within[4], inh[4];
   zero4(within);
   zero4(inh);
-  const int kpad = (si.len + 3) & ~3;
-  tile_mma<false, false>(within, G, LDT, V, LDT, kpad, w);  // sum_s G[t][s] k_s
-  tile_mma<false, false>(inh, DO, LDT, C0, LDT, 64, w);     // C0^T dout_t
+  tile_mma<false, false>(within, G, V, k_terms(si.len), w);  // sum_s G[t][s] k_s
+  tile_mma<false, false>(inh, DO, C0, 64, w);                // C0^T dout_t
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = acc_row(w, r);
+  for (int q = 0; q < 4; ++q) {
+    const int t = acc_row(w, q);
     if (t < si.len) {
       const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
       const float carried = expf(cs.prefix[t]);
-      const float dv = d_variance[th];
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        const int e = acc_col(jb);
-        ybar[th * 64 + e] = within[jb][r] + carried * inh[jb][r] + dv * queries[th * 64 + e];
-      }
+      *reinterpret_cast<f4*>(ybar + th * 64 + c4) =
+          quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qv[q];
     }
   }
 }
@@ -191,16 +215,36 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   __shared__ float colpart[4][64];
   __shared__ float rowE[64], colD2[64], quad[64], startdot[64];
   __shared__ float red[256];
+  __shared__ f4 fpart[4][16];
   const SeqIndex si = seq_index(d);
-  const int w = threadIdx.x >> 6, l = lane_id();
-  const int kpad = (si.len + 3) & ~3;
+  const int w = threadIdx.x >> 6, l = lane_id(), c4 = 4 * (l & 15);
+  const int kt = k_terms(si.len);
+  // d_variance of this thread's tile-fetch rows (threadIdx/16 + 16j).
+  float dvar[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = (threadIdx.x >> 4) + 16 * j;
+    dvar[j] = t < si.len ? d_variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] : 0.f;
+  }
 
-  load_rows(Kt, si.len, rows_of(keys, d, si));
-  load_rows(Vt, si.len, rows_of(values, d, si));
-  load_rows(Yt, si.len, rows_of(solved, d, si));
-  load_rows(Zt, si.len, rows_of(z, d, si));
-  load_rows(Dt, si.len, rows_of(d_output, d, si));
+  {
+    TileRegs r[5];
+    r[0].fetch_rows(si.len, rows_of(keys, d, si));
+    r[1].fetch_rows(si.len, rows_of(values, d, si));
+    r[2].fetch_rows(si.len, rows_of(solved, d, si));
+    r[3].fetch_rows(si.len, rows_of(z, d, si));
+    r[4].fetch_rows(si.len, rows_of(d_output, d, si));
+    r[0].store(Kt);
+    r[1].store(Vt);
+    r[2].store(Yt);
+    r[3].store(Zt);
+    r[4].store(Dt);
+  }
   load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
+  // The end-state cotangents of phase 3 load while phases 1 and 2 run.
+  TileRegs rg, rh;
+  rg.fetch_matrix(end_s + si.seq * 4096);
+  rh.fetch_matrix(end_c + si.seq * 4096);
   __syncthreads();
 
   // Phase 1: gy = Y K^T, gz = Z K^T, gv = dOut V^T and their weighted mixes.
@@ -209,38 +253,38 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
     zero4(gy);
     zero4(gz);
     zero4(gv);
-    tile_mma<false, true>(gy, Yt, LDT, Kt, LDT, 64, w);
-    tile_mma<false, true>(gz, Zt, LDT, Kt, LDT, 64, w);
-    tile_mma<false, true>(gv, Dt, LDT, Vt, LDT, 64, w);
+    tile_mma<false, true>(gy, Yt, Kt, 64, w);
+    tile_mma<false, true>(gz, Zt, Kt, 64, w);
+    tile_mma<false, true>(gv, Dt, Vt, 64, w);
     float rsum[4] = {0.f, 0.f, 0.f, 0.f};
     float csum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = acc_row(w, r), s = acc_col(jb);
+      for (int q = 0; q < 4; ++q) {
+        const int t = acc_row(w, q), s = acc_col<false>(jb);
         float my = 0.f, mz = 0.f, d2 = 0.f;
         if (s <= t && t < si.len) {
           const float dec = expf(cs.prefix[t] - cs.prefix[s]);
-          const float mix = gv[jb][r] - gz[jb][r];
-          d2 = dec * gy[jb][r] * mix;
-          my = dec * cs.beta[s] * gy[jb][r];
+          const float mix = gv[jb][q] - gz[jb][q];
+          d2 = dec * gy[jb][q] * mix;
+          my = dec * cs.beta[s] * gy[jb][q];
           mz = dec * cs.beta[s] * mix;
         }
         M1[t * LDT + s] = my;
         M2[t * LDT + s] = mz;
-        rsum[r] += cs.beta[s] * d2;
+        rsum[q] += cs.beta[s] * d2;
         csum[jb] += d2;
       }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = row16_sum(rsum[r]);
-      if ((l & 15) == 0) rowE[acc_row(w, r)] = v;
+    for (int q = 0; q < 4; ++q) {
+      const float v = row16_sum(rsum[q]);
+      if ((l & 15) == 0) rowE[acc_row(w, q)] = v;
     }
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const float v = group4_sum(csum[jb]);
-      if (l < 16) colpart[w][acc_col(jb)] = v;
+      if (l < 16) colpart[w][acc_col<false>(jb)] = v;
     }
   }
   __syncthreads();
@@ -249,91 +293,108 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
     colD2[s] = colpart[0][s] + colpart[1][s] + colpart[2][s] + colpart[3][s];
   }
 
-  // Phase 2: within-chunk key and value gradients.
+  // Phase 2: within-chunk key and value gradients (rows s, columns 4r..4r+3).
   f4 dk[4], dv[4];
   zero4(dk);
   zero4(dv);
   {
     f4 tmp[4];
     zero4(tmp);
-    tile_mma<true, false>(dk, M2, LDT, Yt, LDT, kpad, w);   // sum_t W(gv-gz)[t][s] y_t
-    tile_mma<true, false>(tmp, M1, LDT, Zt, LDT, kpad, w);  // sum_t W gy[t][s] z_t
-    tile_mma<true, false>(dv, M1, LDT, Dt, LDT, kpad, w);   // sum_t W gy[t][s] dout_t
+    tile_mma<true, false>(dk, M2, Yt, kt, w);   // sum_t W(gv-gz)[t][s] y_t
+    tile_mma<true, false>(tmp, M1, Zt, kt, w);  // sum_t W gy[t][s] z_t
+    tile_mma<true, false>(dv, M1, Dt, kt, w);   // sum_t W gy[t][s] dout_t
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) dk[jb] -= tmp[jb];
   }
   __syncthreads();
 
-  // Phase 3: chunk-end terms through the end-state cotangents G, H.
-  load_matrix(M1, end_s + si.seq * 4096);
-  load_matrix(M2, end_c + si.seq * 4096);
+  // Phase 3: chunk-end terms through the end-state cotangents G, H.  G is
+  // replaced by G + G^T in LDS (each off-diagonal pair by one thread), so
+  // (G + G^T) k_s is a single product.
+  rg.store(M1);
+  rh.store(M2);
+  // The start states of phase 4 load while phase 3 runs.
+  const long bh = si.seq / d.NC;
+  TileRegs rs, rc;
+  rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
+  rc.fetch_matrix(start_c + si.seq * 4096);
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int i = e >> 6, j = e & 63;
+    if (i < j) {
+      const float v = M1[i * LDT + j] + M1[j * LDT + i];
+      M1[i * LDT + j] = v;
+      M1[j * LDT + i] = v;
+    } else if (i == j) {
+      M1[i * LDT + i] *= 2.f;
+    }
+  }
   __syncthreads();
   {
     f4 gk[4], hk[4], hv[4];
     zero4(gk);
     zero4(hk);
     zero4(hv);
-    tile_mma<false, true>(gk, Kt, LDT, M1, LDT, 64, w);   // G k_s
-    tile_mma<false, false>(gk, Kt, LDT, M1, LDT, 64, w);  // + G^T k_s
-    tile_mma<false, true>(hk, Kt, LDT, M2, LDT, 64, w);   // H k_s
-    tile_mma<false, false>(hv, Vt, LDT, M2, LDT, 64, w);  // H^T v_s
+    tile_mma<false, false>(gk, Kt, M1, 64, w);       // (G + G^T) k_s
+    tile_mma<false, true, true>(hk, Kt, M2, 64, w);  // H k_s
+    tile_mma<false, false>(hv, Vt, M2, 64, w);       // H^T v_s
     float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
+    for (int q = 0; q < 4; ++q) {
+      const int s = acc_row(w, q);
+      const f4 kr = *reinterpret_cast<const f4*>(Kt + s * LDT + c4);
+      const f4 vr = *reinterpret_cast<const f4*>(Vt + s * LDT + c4);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int s = acc_row(w, r), e = acc_col(jb);
-        qpart[r] += 0.5f * Kt[s * LDT + e] * gk[jb][r] + Vt[s * LDT + e] * hk[jb][r];
-      }
+      for (int jb = 0; jb < 4; ++jb) qpart[q] += 0.5f * kr[jb] * gk[jb][q] + vr[jb] * hk[jb][q];
+    }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int s = acc_row(w, r);
-      const float qv = row16_sum(qpart[r]);
+    for (int q = 0; q < 4; ++q) {
+      const int s = acc_row(w, q);
+      const float qv = row16_sum(qpart[q]);
       if ((l & 15) == 0) quad[s] = qv;
       if (s < si.len) {
         const float tl = cs.tail[s];
         const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          const int e = acc_col(jb);
-          d_keys[th * 64 + e] = dk[jb][r] + tl * (gk[jb][r] + hv[jb][r]);
-          d_values[th * 64 + e] = dv[jb][r] + tl * hk[jb][r];
-        }
+        *reinterpret_cast<f4*>(d_keys + th * 64 + c4) =
+            quad_row(dk, q) + tl * (quad_row(gk, q) + quad_row(hv, q));
+        *reinterpret_cast<f4*>(d_values + th * 64 + c4) = quad_row(dv, q) + tl * quad_row(hk, q);
       }
     }
   }
   __syncthreads();
 
-  // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>.
-  // The chunk's start evidence is the start of its first sub-chunk.
-  const long bh = si.seq / d.NC;
-  load_matrix(Kt, start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
-  load_matrix(Vt, start_c + si.seq * 4096);
+  // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>
+  // (<G, S0> = <G + G^T, S0> / 2 since S0 is symmetric).  The chunk's start
+  // evidence is the start of its first sub-chunk.
+  rs.store(Kt);
+  rc.store(Vt);
   __syncthreads();
   {
     float part = 0.f;
     for (int e = threadIdx.x; e < 4096; e += 256) {
       const int row = e >> 6, col = e & 63;
-      part += M1[row * LDT + col] * Kt[row * LDT + col] + M2[row * LDT + col] * Vt[row * LDT + col];
+      part += 0.5f * M1[row * LDT + col] * Kt[row * LDT + col] +
+              M2[row * LDT + col] * Vt[row * LDT + col];
     }
     red[threadIdx.x] = part;
     f4 ys[4], dc[4];
     zero4(ys);
     zero4(dc);
-    tile_mma<false, false>(ys, Yt, LDT, Kt, LDT, 64, w);  // y_t^T S0
-    tile_mma<false, false>(dc, Dt, LDT, Vt, LDT, 64, w);  // dout_t^T C0
+    tile_mma<false, false>(ys, Yt, Kt, 64, w);  // y_t^T S0
+    tile_mma<false, false>(dc, Dt, Vt, 64, w);  // dout_t^T C0
     float sp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
+    for (int q = 0; q < 4; ++q) {
+      const int t = acc_row(w, q);
+      const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
+      const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = acc_row(w, r), e = acc_col(jb);
-        sp[r] += dc[jb][r] * Yt[t * LDT + e] - ys[jb][r] * Zt[t * LDT + e];
-      }
+      for (int jb = 0; jb < 4; ++jb) sp[q] += dc[jb][q] * yr[jb] - ys[jb][q] * zr[jb];
+    }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = acc_row(w, r);
-      const float v = row16_sum(sp[r]);
+    for (int q = 0; q < 4; ++q) {
+      const int t = acc_row(w, q);
+      const float v = row16_sum(sp[q]);
       if ((l & 15) == 0) startdot[t] = expf(cs.prefix[t]) * v;
     }
   }
@@ -370,16 +431,32 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
       d_log_decay[th] = suffix;
     }
   }
-  for (int e = threadIdx.x; e < si.len * 64; e += 256) {
-    const int t = e >> 6, c = e & 63;
-    const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
-    d_queries[th * 64 + c] = Zt[t * LDT + c] + d_variance[th] * Yt[t * LDT + c];
-  }
-  if (threadIdx.x < 64) {
-    const int c = threadIdx.x;
-    float v = 0.f;
-    for (int t = 0; t < si.len; ++t) v -= Zt[t * LDT + c] * Yt[t * LDT + c];
-    floor_part[si.seq * 64 + c] = v;
+  // Queries, d q_t = z_t + dvar_t y_t, in the tile-fetch layout (rows
+  // r0 + 16j, columns q4..q4+3), and the floor partial -sum_t z_t * y_t:
+  // per thread over its four rows, then over the lanes and waves holding the
+  // same columns, in a fixed order.
+  {
+    f4 fsum = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = (threadIdx.x >> 4) + 16 * j;
+      const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
+      const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
+      if (t < si.len) {
+        const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+        *reinterpret_cast<f4*>(d_queries + th * 64 + c4) = zr + dvar[j] * yr;
+      }
+      fsum -= zr * yr;  // zero past the chunk's tokens
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fsum[i] = group4_sum(fsum[i]);
+    if (l < 16) fpart[w][l] = fsum;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      const f4 total = fpart[0][threadIdx.x] + fpart[1][threadIdx.x] + fpart[2][threadIdx.x] +
+                       fpart[3][threadIdx.x];
+      *reinterpret_cast<f4*>(floor_part + si.seq * 64 + 4 * threadIdx.x) = total;
+    }
   }
 }
 

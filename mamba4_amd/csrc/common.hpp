@@ -8,7 +8,8 @@ namespace m4 {
 constexpr int KD = 64;      // key width D
 constexpr int VD = 64;      // value width P
 constexpr int MAXC = 64;    // largest chunk
-constexpr int LDT = 65;     // row stride of a 64x64 LDS tile (odd: conflict-free columns)
+constexpr int LDT = 68;     // row stride of a 64x64 LDS tile: 16-byte rows, and rows
+                            // r = 0..7 start in distinct 4-bank groups
 constexpr int TILE = 64 * LDT;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -97,65 +98,144 @@ __device__ inline void load_chunk_scalars(ChunkScalars& cs, const Dims& d, const
   }
 }
 
-// 64x64 tile GEMM on MFMA 16x16x4 f32, one 16-row strip per wave:
-//   acc[jb] += sum_k A(i, k) B(k, j),  i in [16w, 16w+16), j in [16jb, 16jb+16)
-// A(i,k) = TA ? A[k*lda + i] : A[i*lda + k];  B(k,j) = TB ? B[j*ldb + k] : B[k*ldb + j].
-// Operand lane layout (verified on gfx950): A lane = i + 16k, B lane = j + 16k;
-// result acc[jb][r] = C[16w + 4*(lane>>4) + r][16jb + (lane&15)].
-// K must be a multiple of 4 with zero padding past the real extent.
-template <bool TA, bool TB>
-__device__ __forceinline__ void tile_mma(f4 acc[4], const float* A, int lda, const float* B,
-                                         int ldb, int K, int w) {
-  const int l = lane_id();
-  const int r = l & 15, kq = l >> 4;
-  for (int k0 = 0; k0 < K; k0 += 4) {
-    const int k = k0 + kq;
-    const float a = TA ? A[k * lda + 16 * w + r] : A[(16 * w + r) * lda + k];
+// 64x64 tile product on MFMA 16x16x4 f32, one 16-row strip per wave:
+//   acc += A B,  rows i in [16w, 16w+16),  K (a multiple of 16) terms,
+//   A(i,k) = TA ? A[k*LDT + i] : A[i*LDT + k],
+//   B(k,j) = TB ? B[j*LDT + k] : B[k*LDT + j].
+// MFMA operand layout (16x16x4): lane (g = lane>>4, r = lane&15) supplies
+// A(row r, k-slot g) and B(k-slot g, column r); accumulator element q of the
+// lane is C(row 4g+q, column r).  Within each 16-wide block of k, MFMA step
+// e feeds lane group g the term k = k0 + 4g + e, so every lane's four k are
+// adjacent and a k-contiguous operand arrives in one 16-byte LDS read.
+// Column order of the result (see acc_col):
+//   QUAD = false: accumulator jb holds columns 16jb + r;
+//   QUAD = true:  accumulator jb holds columns 4r + jb, so a lane's four
+//                 accumulators are four adjacent columns of one row and a
+//                 k-major B (TB = false) arrives in one 16-byte read per e.
+// TB = false with QUAD = false falls back to scalar B reads.
+template <bool TA, bool TB, bool QUAD>
+__device__ __forceinline__ void mma_block(f4 acc[4], const float* A, const float* B, int k0,
+                                          int w) {
+  const int l = lane_id(), r = l & 15, kk = k0 + 4 * (l >> 4);
+  f4 a;
+  if (TA) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = A[(kk + e) * LDT + 16 * w + r];
+  } else {
+    a = *reinterpret_cast<const f4*>(A + (16 * w + r) * LDT + kk);
+  }
+  if (TB) {
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
-      const float bv = TB ? B[(16 * jb + r) * ldb + k] : B[k * ldb + 16 * jb + r];
-      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[jb], 0, 0, 0);
+      const int col = QUAD ? 4 * r + jb : 16 * jb + r;
+      const f4 b = *reinterpret_cast<const f4*>(B + col * LDT + kk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc[jb], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f4 b;
+      if (QUAD) {
+        b = *reinterpret_cast<const f4*>(B + (kk + e) * LDT + 4 * r);
+      } else {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) b[jb] = B[(kk + e) * LDT + 16 * jb + r];
+      }
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[jb], acc[jb], 0, 0, 0);
     }
   }
 }
+
+template <bool TA, bool TB, bool QUAD = !TB>
+__device__ __forceinline__ void tile_mma(f4 acc[4], const float* A, const float* B, int K, int w) {
+  if (K == 64) {
+#pragma unroll
+    for (int k0 = 0; k0 < 64; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
+  } else {
+    for (int k0 = 0; k0 < K; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
+  }
+}
+
+// Terms a product over `len` tokens needs: len rounded up to 16 (the tiles
+// are zero past len).
+__device__ __forceinline__ int k_terms(int len) { return (len + 15) & ~15; }
 
 __device__ __forceinline__ void zero4(f4 acc[4]) {
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) acc[jb] = f4{0.f, 0.f, 0.f, 0.f};
 }
 
-// Row / column of accumulator element (jb, r) for wave w and this lane.
-__device__ __forceinline__ int acc_row(int w, int r) { return 16 * w + 4 * (lane_id() >> 4) + r; }
-__device__ __forceinline__ int acc_col(int jb) { return 16 * jb + (lane_id() & 15); }
-
-// Copy rows [0, rows) of a [*, width=64] token-major global slab into a
-// 64xLDT LDS tile, zero-filling rows [rows, 64).  src(row) gives the row's
-// global pointer.  Uses all threads of the block.
-template <typename RowPtr>
-__device__ inline void load_rows(float* tile, int rows, RowPtr src) {
-  for (int e = threadIdx.x; e < 64 * 16; e += blockDim.x) {
-    const int row = e >> 4, q = (e & 15) * 4;
-    f4 v = f4{0.f, 0.f, 0.f, 0.f};
-    if (row < rows) v = *reinterpret_cast<const f4*>(src(row) + q);
-    float* dst = tile + row * LDT + q;
-    dst[0] = v[0];
-    dst[1] = v[1];
-    dst[2] = v[2];
-    dst[3] = v[3];
-  }
+// Row / column of accumulator element (jb, q) for wave w and this lane.
+__device__ __forceinline__ int acc_row(int w, int q) { return 16 * w + 4 * (lane_id() >> 4) + q; }
+template <bool QUAD>
+__device__ __forceinline__ int acc_col(int jb) {
+  return QUAD ? 4 * (lane_id() & 15) + jb : 16 * jb + (lane_id() & 15);
 }
 
-// Copy a dense row-major 64x64 global matrix into a 64xLDT LDS tile.
-__device__ inline void load_matrix(float* tile, const float* src) {
-  for (int e = threadIdx.x; e < 64 * 16; e += blockDim.x) {
-    const int row = e >> 4, q = (e & 15) * 4;
-    f4 v = *reinterpret_cast<const f4*>(src + row * 64 + q);
-    float* dst = tile + row * LDT + q;
-    dst[0] = v[0];
-    dst[1] = v[1];
-    dst[2] = v[2];
-    dst[3] = v[3];
-  }
+// Row q of a QUAD accumulator set: columns 4r..4r+3 of row acc_row(w, q).
+__device__ __forceinline__ f4 quad_row(const f4 acc[4], int q) {
+  return f4{acc[0][q], acc[1][q], acc[2][q], acc[3][q]};
 }
+
+// Kernels built on these tiles run 256 threads (4 waves).
+constexpr int BLOCK = 256;
+
+// One 64x64 tile staged through registers: thread i fetches the float4 at
+// column quad i%16 of rows i/16 + 16j (j = 0..3), and stores it later.  A
+// kernel fetches every tile of a phase before storing any, so all of the
+// phase's global loads are in flight together.
+struct TileRegs {
+  f4 v[4];
+
+  // Rows [0, rows) of a token-major slab, row(s) = global pointer of row s;
+  // rows past `rows` are zero.
+  template <typename RowPtr>
+  __device__ __forceinline__ void fetch_rows(int rows, RowPtr row) {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + 16 * j;
+      v[j] = r < rows ? *reinterpret_cast<const f4*>(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  // A dense row-major 64x64 matrix.
+  __device__ __forceinline__ void fetch_matrix(const float* src) {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const f4*>(src + (r0 + 16 * j) * 64 + q);
+  }
+
+  __device__ __forceinline__ void store(float* tile) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(tile + (r0 + 16 * j) * LDT + q) = v[j];
+  }
+};
+
+// The transpose of a dense row-major 64x64 matrix: tile[c][r] = src[r][c].
+// Thread i fetches row i%64, column quads i/64 + 4j; the scalar LDS stores
+// of a wave then fall in consecutive banks.
+struct TileRegsT {
+  f4 v[4];
+
+  __device__ __forceinline__ void fetch_matrix(const float* src) {
+    const int r = threadIdx.x & 63, q0 = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const f4*>(src + r * 64 + 4 * (q0 + 4 * j));
+  }
+
+  __device__ __forceinline__ void store(float* tile) const {
+    const int r = threadIdx.x & 63, q0 = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tile[(4 * (q0 + 4 * j) + i) * LDT + r] = v[j][i];
+  }
+};
 
 }  // namespace m4

@@ -31,13 +31,16 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(
   __shared__ ChunkScalars cs;
   const long seq = blockIdx.x;
   const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
-  const int len = chunk_len(d, n), w = threadIdx.x >> 6;
-  const int kpad = (len + 3) & ~3;
+  const int len = chunk_len(d, n), w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
+  const int kt = k_terms(len);
   auto rows = [&](const float* base) {
     return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * 64; };
   };
-  load_rows(K, len, rows(keys));
-  load_rows(V, len, rows(values));
+  TileRegs rk, rv;
+  rk.fetch_rows(len, rows(keys));
+  rv.fetch_rows(len, rows(values));
+  rk.store(K);
+  rv.store(V);
   load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
   __syncthreads();
 
@@ -52,12 +55,11 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(
     __syncthreads();
     f4 acc[4];
     zero4(acc);
-    tile_mma<true, false>(acc, W, LDT, K, LDT, kpad, w);  // sum_s tail_s k_s k_s^T
+    tile_mma<true, false>(acc, W, K, kt, w);  // sum_s tail_s k_s k_s^T
     float* out = mat(start_s, (long)bh * d.NS + (long)n * d.rsub + u);
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) out[acc_row(w, r) * 64 + acc_col(jb)] = acc[jb][r];
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f4*>(out + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
     __syncthreads();
   }
   for (int e = threadIdx.x; e < 64 * 64; e += 256) {
@@ -67,12 +69,11 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(
   __syncthreads();
   f4 acc[4];
   zero4(acc);
-  tile_mma<true, false>(acc, W, LDT, K, LDT, kpad, w);  // sum_s tail_s v_s k_s^T
+  tile_mma<true, false>(acc, W, K, kt, w);  // sum_s tail_s v_s k_s^T
   float* out = mat(start_c, (long)bh * d.NC + n);
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) out[acc_row(w, r) * 64 + acc_col(jb)] = acc[jb][r];
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<f4*>(out + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
 }
 
 // exp(sum of log decays) over the tokens of step `i` of the scan: a
@@ -89,9 +90,13 @@ __device__ __forceinline__ float step_decay(const Dims& d, const float* log_deca
     cnt = chunk_len(d, i);
   }
   float g = 0.f;
+#pragma unroll 8
   for (int t = 0; t < cnt; ++t) g += log_decay[token_head(d, b, first + t, h)];
   return expf(g);
 }
+
+// Steps of a scan whose loads are issued together.
+constexpr int SCAN_BATCH = 8;
 
 // Grid (B*H, 8): y in 0..3 scans evidence elements [1024y, 1024y+1024) over
 // the NS sub-chunks, y in 4..7 the cross-statistic elements over NC chunks.
@@ -114,11 +119,18 @@ __global__ __launch_bounds__(256) void fwd_scan_kernel(
     if (threadIdx.x < count)
       decay[threadIdx.x] = step_decay(d, log_decay, b, h, base + threadIdx.x, !cross);
     __syncthreads();
-    for (int i = 0; i < count; ++i) {
-      f4* p = reinterpret_cast<f4*>(buf + (long)(base + i) * 4096 + elem);
-      const f4 stat = *p;
-      *p = running;
-      running = decay[i] * running + stat;
+    for (int i0 = 0; i0 < count; i0 += SCAN_BATCH) {
+      const int m = min(SCAN_BATCH, count - i0);
+      f4 stat[SCAN_BATCH];
+#pragma unroll
+      for (int j = 0; j < SCAN_BATCH; ++j)
+        if (j < m) stat[j] = *reinterpret_cast<const f4*>(buf + (long)(base + i0 + j) * 4096 + elem);
+#pragma unroll
+      for (int j = 0; j < SCAN_BATCH; ++j)
+        if (j < m) {
+          *reinterpret_cast<f4*>(buf + (long)(base + i0 + j) * 4096 + elem) = running;
+          running = decay[i0 + j] * running + stat[j];
+        }
     }
   }
   float* fin = cross ? final_c : final_s;
@@ -137,14 +149,18 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   __shared__ ChunkScalars cs;
   const long seq = blockIdx.x;
   const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
-  const int len = chunk_len(d, n), w = threadIdx.x >> 6;
-  const int kpad = (len + 3) & ~3;
+  const int len = chunk_len(d, n), w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
+  const int kt = k_terms(len);
   auto rows = [&](const float* base) {
     return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * 64; };
   };
-  load_rows(Y, len, rows(solved));
-  load_rows(Zw, len, rows(z));
-  load_rows(Dw, len, rows(d_output));
+  TileRegs ry, rz, rd;
+  ry.fetch_rows(len, rows(solved));
+  rz.fetch_rows(len, rows(z));
+  rd.fetch_rows(len, rows(d_output));
+  ry.store(Y);
+  rz.store(Zw);
+  rd.store(Dw);
   load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
   __syncthreads();
   for (int e = threadIdx.x; e < len * 64; e += 256) {
@@ -156,27 +172,26 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   __syncthreads();
   f4 acc[4];
   zero4(acc);
-  tile_mma<true, false>(acc, Zw, LDT, Y, LDT, kpad, w);  // M = sum_t e^P z_t y_t^T
+  tile_mma<true, false>(acc, Zw, Y, kt, w);  // M = sum_t e^P z_t y_t^T
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) M[acc_row(w, r) * LDT + acc_col(jb)] = acc[jb][r];
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<f4*>(M + acc_row(w, q) * LDT + c4) = quad_row(acc, q);
   __syncthreads();
   float* us = mat(end_s, (long)bh * d.NC + n);
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
+  for (int q = 0; q < 4; ++q) {
+    const int i = acc_row(w, q);
+    f4 v;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = acc_row(w, r), j = acc_col(jb);
-      us[i * 64 + j] = -0.5f * (acc[jb][r] + M[j * LDT + i]);
-    }
+    for (int jb = 0; jb < 4; ++jb) v[jb] = -0.5f * (acc[jb][q] + M[(c4 + jb) * LDT + i]);
+    *reinterpret_cast<f4*>(us + i * 64 + c4) = v;
+  }
   zero4(acc);
-  tile_mma<true, false>(acc, Dw, LDT, Y, LDT, kpad, w);  // V = sum_t e^P dout_t y_t^T
+  tile_mma<true, false>(acc, Dw, Y, kt, w);  // V = sum_t e^P dout_t y_t^T
   float* uc = mat(end_c, (long)bh * d.NC + n);
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) uc[acc_row(w, r) * 64 + acc_col(jb)] = acc[jb][r];
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<f4*>(uc + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
 }
 
 // Grid (B*H, 8) as fwd_scan_kernel, walking chunks in reverse.
@@ -198,11 +213,18 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
     if (threadIdx.x < count)
       decay[threadIdx.x] = step_decay(d, log_decay, b, h, top - count + threadIdx.x, false);
     __syncthreads();
-    for (int i = count - 1; i >= 0; --i) {
-      f4* p = reinterpret_cast<f4*>(buf + (long)(top - count + i) * 4096 + elem);
-      const f4 local = *p;
-      *p = running;
-      running = local + decay[i] * running;
+    for (int i0 = count - 1; i0 >= 0; i0 -= SCAN_BATCH) {
+      const int m = min(SCAN_BATCH, i0 + 1);
+      f4 local[SCAN_BATCH];
+#pragma unroll
+      for (int j = 0; j < SCAN_BATCH; ++j)
+        if (j < m) local[j] = *reinterpret_cast<const f4*>(buf + (long)(top - count + i0 - j) * 4096 + elem);
+#pragma unroll
+      for (int j = 0; j < SCAN_BATCH; ++j)
+        if (j < m) {
+          *reinterpret_cast<f4*>(buf + (long)(top - count + i0 - j) * 4096 + elem) = running;
+          running = local[j] + decay[i0 - j] * running;
+        }
     }
   }
   float* dinit = cross ? d_init_c : d_init_s;
