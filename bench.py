@@ -11,7 +11,13 @@ dominant kernel (HIP events on the launch stream), the factorization's
 fp32 rate, factor-streaming bandwidth and a CPU baseline (the NumPy oracle
 on a one-row sample of the same workload, on this host's cores).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+With --workload config4 a step is instead one in-place decode step of
+2048 sequences x 8 heads of resident (S, C) states: the
+states are the end states of a 1024-token gated recurrence with
+lambda = sigmoid(N(3,1)), built by this library's own forward, and each step
+writes one new token into every state, refactors and reads.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config2|config4]
 """
 
 import argparse
@@ -57,6 +63,15 @@ KERNEL_WORK = {
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "config2_hbm_traffic.md")
 
+# Config 4 (decode): 2048 sequences x 8 heads of resident 64x64 states.
+DECODE_METRIC = "decode-step tokens/sec, 2048 sequences x 8 heads d64 resident states; % HBM BW"
+DECODE_BATCH, DECODE_HEADS, DECODE_CONTEXT = 2048, 8, 1024
+# HBM bytes one decode step must move per (sequence, head) state with the
+# API's full-matrix state layout: read + write of S and of C (4 x 16 KiB),
+# the token's key, value and query (3 x 256 B), beta and log_decay, and the
+# output row and variance.
+DECODE_STATE_BYTES = 4 * 16384 + 3 * 256 + 8 + 256 + 4
+
 
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3
@@ -101,7 +116,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--chunk", type=int, default=64)
-    p.add_argument("--workload", default="config2", choices=["config2"])
+    p.add_argument("--workload", default="config2", choices=["config2", "config4"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -165,6 +180,186 @@ class Problem:
                 self.stream,
             )
         )
+
+
+class Decode:
+    """Config-4 resident states and token sets for in-place decode steps."""
+
+    TOKEN_SETS = 8
+
+    def __init__(self, seed=0, slice_rows=128):
+        import torch
+
+        from mamba4_amd import _lib
+
+        self.lib = _lib.load()
+        self.check = _lib.check
+        dev = torch.device("cuda:0")
+        B, H, T = DECODE_BATCH, DECODE_HEADS, DECODE_CONTEXT
+        f32 = dict(dtype=torch.float32, device=dev)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        self.evidence = torch.empty(B, H, 64, 64, **f32)
+        self.cross = torch.empty(B, H, 64, 64, **f32)
+        self.floor = torch.full((H, 64), 1e-2, **f32)
+        stream = torch.cuda.current_stream().cuda_stream
+        # End states of a T-token recurrence, built slice by slice with this
+        # library's forward (config-0 distributions, lambda = sigmoid(N(3,1))).
+        R = slice_rows
+        count, starts = _lib.start_counts(T, 64)
+        scratch = [
+            torch.empty(R, T, H, 64, **f32),  # output
+            torch.empty(R, T, H, **f32),  # variance
+        ]
+        residual = [
+            torch.empty(R, T, H, 64, **f32),  # solved
+            torch.empty(R, T, H, _lib.FACTOR_FLOATS, **f32),  # factors
+            torch.empty(R, H, starts, 64, 64, **f32),
+            torch.empty(R, H, count, 64, 64, **f32),
+        ]
+        for first in range(0, B, R):
+            k, v, q, beta, log_decay = self._tokens(gen, (R, T, H), shift=True)
+            self.check(
+                self.lib.m4mr_forward(
+                    k.data_ptr(), v.data_ptr(), q.data_ptr(), beta.data_ptr(),
+                    log_decay.data_ptr(), self.floor.data_ptr(), None, None, R, T, H, 64,
+                    scratch[0].data_ptr(), scratch[1].data_ptr(),
+                    self.evidence[first:first + R].data_ptr(),
+                    self.cross[first:first + R].data_ptr(),
+                    *(t.data_ptr() for t in residual), stream,
+                )
+            )
+        del scratch, residual
+        self.tokens = [self._tokens(gen, (B, H), shift=False) for _ in range(self.TOKEN_SETS)]
+        self.output = torch.empty(B, H, 64, **f32)
+        self.variance = torch.empty(B, H, **f32)
+        self.stream = stream
+        self.calls = 0
+        torch.cuda.synchronize()
+
+    @staticmethod
+    def _tokens(gen, shape, shift):
+        """q, k unit-norm N(0,1); v N(0,1); beta = sigmoid(N(0,1));
+        log_decay = log sigmoid(N(3,1)); keys shifted one token when `shift`."""
+        import torch
+        import torch.nn.functional as F
+
+        kw = dict(device=gen.device, generator=gen, dtype=torch.float32)
+        q = torch.randn(*shape, 64, **kw)
+        k = torch.randn(*shape, 64, **kw)
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = k / k.norm(dim=-1, keepdim=True)
+        if shift:
+            k = torch.cat([torch.zeros_like(k[:, :1]), k[:, :-1]], dim=1)
+        v = torch.randn(*shape, 64, **kw)
+        log_decay = -F.softplus(-(torch.randn(*shape, **kw) + 3.0))
+        beta = torch.sigmoid(torch.randn(*shape, **kw))
+        return [t.contiguous() for t in (k, v, q, beta, log_decay)]
+
+    def step(self):
+        k, v, q, beta, log_decay = self.tokens[self.calls % self.TOKEN_SETS]
+        self.calls += 1
+        self.check(
+            self.lib.m4mr_decode_step(
+                self.evidence.data_ptr(), self.cross.data_ptr(), k.data_ptr(), v.data_ptr(),
+                q.data_ptr(), beta.data_ptr(), log_decay.data_ptr(), self.floor.data_ptr(),
+                DECODE_BATCH * DECODE_HEADS, DECODE_HEADS, self.output.data_ptr(),
+                self.variance.data_ptr(), self.stream,
+            )
+        )
+
+
+def decode_cpu_baseline(decode, sample=2048):
+    """The NumPy oracle's decode_step (float32) on `sample` of the states."""
+    from oracle import memread as oracle
+
+    states = sample // DECODE_HEADS
+    s = decode.evidence[:states].cpu().numpy()
+    c = decode.cross[:states].cpu().numpy()
+    k, v, q, beta, log_decay = (t[:states].cpu().numpy() for t in decode.tokens[0])
+    floor = decode.floor.cpu().numpy()
+    start = time.perf_counter()
+    oracle.decode_step(s, c, k, v, q, beta, log_decay, floor, dtype=np.float32)
+    seconds = time.perf_counter() - start
+    step_seconds = seconds * (DECODE_BATCH * DECODE_HEADS) / (states * DECODE_HEADS)
+    return {
+        "value": DECODE_BATCH / step_seconds,
+        "unit": "tokens/s",
+        "cores": int(os.environ.get("OPENBLAS_NUM_THREADS", CORES)),
+        "kind": "port",
+        "sample": (
+            f"oracle.memread.decode_step in float32 NumPy on {states} of the 2048 sequences "
+            f"({states * DECODE_HEADS} states), {seconds:.2f} s, scaled to a full step; "
+            f"BLAS threads = {os.environ.get('OPENBLAS_NUM_THREADS')}"
+        ),
+    }
+
+
+def main_decode(args):
+    import torch
+
+    from mamba4_amd import _lib
+
+    decode = Decode(seed=0)
+    steps = args.steps
+    for _ in range(args.warmup):
+        decode.step()
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        decode.step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.profile_enable(False)
+    total, count = _lib.profile_read("decode_step")
+    _lib.profile_reset()
+    seconds = (t1 - t0) / steps
+    kernel_s = total / count / 1e3
+    states = DECODE_BATCH * DECODE_HEADS
+    achieved = DECODE_STATE_BYTES * states / kernel_s / 1e9
+    assert torch.isfinite(decode.variance).all(), "decode produced non-finite reads"
+    line = {
+        "metric": DECODE_METRIC,
+        "value": DECODE_BATCH / seconds,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": seconds * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (
+                "config4: in-place decode step, 2048 sequences x 8 heads, D=P=64 fp32, "
+                "states = end states of a 1024-token recurrence (lambda = sigmoid(N(3,1)))"
+            ),
+            "sequences": DECODE_BATCH,
+            "heads": DECODE_HEADS,
+            "key_dim": 64,
+            "value_dim": 64,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_step",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": None,
+            "algorithmic_bytes": DECODE_STATE_BYTES * states,
+        },
+        "kernel_ms": {"decode_step": kernel_s * 1e3},
+        "copy_kernel_GBps": copy_bandwidth_gbps(),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = decode_cpu_baseline(decode)
+    print(json.dumps(line), flush=True)
 
 
 def copy_bandwidth_gbps():
@@ -233,6 +428,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "config4":
+        return main_decode(args)
     data = workload_inputs(args.workload, seed=0, cotangents=True)
     problem = Problem(data, args.chunk)
     B, T, H = problem.B, problem.T, problem.H

@@ -277,6 +277,15 @@ __global__ __launch_bounds__(64) void spd_backward_kernel(
 }
 
 // One decode step for four (batch*head) states per wave, in place.
+//
+// The states stream through coalesced passes: in each, the 16 lanes of DPP
+// row mu sweep whole 256-byte rows of state mu (lane c holds column quad c),
+// so one 16-byte access instruction covers four full rows.  The update
+// lam S + beta k k^T (and lam C + beta v k^T) is applied in that layout, the
+// row's key (or value) arriving by DPP broadcast from the lane that holds it.
+// The factorization needs rows a+16m in lane a: each 16-row slot of the
+// updated S passes through a 17 KB LDS buffer (rows padded to 17 quads, so
+// both the quad-wise writes and the row-wise reads are conflict-free).
 __global__ __launch_bounds__(64) void decode_step_kernel(
     float* __restrict__ evidence, float* __restrict__ cross, const float* __restrict__ key,
     const float* __restrict__ value, const float* __restrict__ query,
@@ -297,46 +306,63 @@ __global__ __launch_bounds__(64) void decode_step_kernel(
     qr[m] = query[nidx * 64 + a + 16 * m];
     fl[m] = floor[(nidx % H) * 64 + a + 16 * m];
   }
+  // Column quad a of the key: k[4a .. 4a+3].
+  const f4 kq = *reinterpret_cast<const f4*>(key + nidx * 64 + 4 * a);
   const float bt = beta[nidx], lam = expf(log_decay[nidx]);
+  __shared__ f4 stage[4 * 16 * 17];  // [state][row][quad], 17 quads per row
+  f4* mine = stage + mu * 16 * 17;
+
   float A[4][64];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    float* row = S + (a + 16 * m) * 64;
-    const float bk = bt * kr[m];
+    // Coalesced update of rows 16m .. 16m+15; the row's key comes from the
+    // lane that holds it in this row's slot (bcast16 of kr[m]).
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      f4 sv = *reinterpret_cast<const f4*>(row + 4 * q);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int k = 4 * q + e;
-        sv[e] = lam * sv[e] + bk * bcast16(kr[k >> 4], k & 15);
-        if (k < slot_cols(m)) A[m][k] = sv[e];
-      }
-      if (active) *reinterpret_cast<f4*>(row + 4 * q) = sv;
+    for (int r = 0; r < 16; ++r) {
+      f4* p = reinterpret_cast<f4*>(S + (16 * m + r) * 64) + a;
+      const float bk = bt * bcast16(kr[m], r);
+      const f4 sv = lam * *p + bk * kq;
+      if (active) *p = sv;
+      mine[r * 17 + a] = sv;
     }
+    __syncthreads();
+    // Row a of this slot, columns 0 .. 16m+15, into the factorization layout.
+#pragma unroll
+    for (int q = 0; q < 4 * m + 4; ++q) {
+      const f4 v = mine[a * 17 + q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) A[m][4 * q + e] = v[e];
+    }
+    __syncthreads();
   }
   float qcopy[4] = {qr[0], qr[1], qr[2], qr[3]};
   factor_rows16(A, fl);
   float y[4];
   solve_rows16(A, qcopy, y);
+  // y[4a .. 4a+3] for the coalesced read: y_j lives in lane j%16, slot j/16.
+  __shared__ float ys[4][64];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) ys[mu][a + 16 * m] = y[m];
+  __syncthreads();
+  const f4 yq = *reinterpret_cast<const f4*>(&ys[mu][4 * a]);
+  float out[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      f4* p = reinterpret_cast<f4*>(C + (16 * m + r) * 64) + a;
+      const float bv = bt * bcast16(vr[m], r);
+      const f4 cv = lam * *p + bv * kq;
+      if (active) *p = cv;
+      // Row 16m + r of the read, summed over the 16 column quads.
+      const float part = sum16(cv[0] * yq[0] + cv[1] * yq[1] + cv[2] * yq[2] + cv[3] * yq[3]);
+      out[m] = a == r ? part : out[m];
+    }
+  }
   float var = 0.f;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    float* row = C + (a + 16 * m) * 64;
-    const float bv = bt * vr[m];
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      f4 cv = *reinterpret_cast<const f4*>(row + 4 * q);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int k = 4 * q + e;
-        cv[e] = lam * cv[e] + bv * bcast16(kr[k >> 4], k & 15);
-        acc += cv[e] * bcast16(y[k >> 4], k & 15);
-      }
-      if (active) *reinterpret_cast<f4*>(row + 4 * q) = cv;
-    }
-    if (active) output[nidx * 64 + a + 16 * m] = acc;
+    if (active) output[nidx * 64 + a + 16 * m] = out[m];
     var += qr[m] * y[m];
   }
   var = sum16(var);

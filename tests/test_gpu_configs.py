@@ -77,3 +77,44 @@ def test_config2_full_size(gpu_lib):
 
 def test_config3_full_size_bf16_inputs_slow_decay(gpu_lib):
     run_config("config3", oracle_row=31)
+
+
+def test_config4_decode_full_size(gpu_lib):
+    """Decode at the config-4 shape: 2048 sequences x 8 heads of resident
+    states (here the end states of a 16-token prefill), two in-place steps.
+    A sample of states is checked against the float64 oracle's decode_step;
+    every read must be finite and satisfy the floor bound."""
+    import torch
+
+    from mamba4_amd import SelectiveState, selective_decode_, selective_gaussian_memory
+    from mamba4_amd.inputs import synthetic_inputs
+    from tests.gpu_helpers import host, to_device
+
+    batch, heads = 2048, 8
+    data = synthetic_inputs(batch, 17, heads, decay_mean=3.0, seed=4)
+    announce("config4 decode: 16-token prefill for the resident states")
+    prefix = to_device([data[n][:, :16] if n != "floor" else data[n] for n in NAMES])
+    with torch.no_grad():
+        state = selective_gaussian_memory(*prefix, chunk_size=16).state
+    evidence, cross = state.evidence.contiguous(), state.cross.contiguous()
+    sample = np.arange(0, batch, 97)
+    s_ref = host(evidence)[sample]
+    c_ref = host(cross)[sample]
+    for step in range(2):
+        announce(f"config4 decode: in-place step {step}")
+        t = 16 if step == 0 else 15
+        tok = to_device([data[n][:, t] for n in NAMES if n != "floor"])
+        floor = to_device([data["floor"]])[0]
+        out = selective_decode_(SelectiveState(evidence, cross), *tok, floor)
+        got_out, got_var = host(out.output), host(out.variance)
+        assert np.isfinite(got_out).all() and np.isfinite(got_var).all()
+        q = data["queries"][:, t].astype(np.float64)
+        assert (got_var >= -1e-6).all()
+        assert (got_var <= np.sum(q * q, -1) / data["floor"].min() * (1 + 1e-5)).all()
+        args = [data[n][sample, t] for n in ["keys", "values", "queries", "beta", "log_decay"]]
+        ref_out, ref_var, s_ref, c_ref = oracle.decode_step(s_ref, c_ref, *args, data["floor"])
+        assert normwise(got_out[sample], ref_out) <= 1e-4
+        assert normwise(got_var[sample], ref_var) <= 1e-4
+        assert normwise(host(evidence)[sample], s_ref) <= 1e-5
+        assert normwise(host(cross)[sample], c_ref) <= 1e-5
+
