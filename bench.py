@@ -62,6 +62,7 @@ KERNEL_WORK = {
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "config2_hbm_traffic.md")
+DECODE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "config4_decode_hbm_traffic.md")
 
 # Config 4 (decode): 2048 sequences x 8 heads of resident 64x64 states.
 DECODE_METRIC = "decode-step tokens/sec, 2048 sequences x 8 heads d64 resident states; % HBM BW"
@@ -73,12 +74,12 @@ DECODE_BATCH, DECODE_HEADS, DECODE_CONTEXT = 2048, 8, 1024
 DECODE_STATE_BYTES = 4 * 16384 + 3 * 256 + 8 + 256 + 4
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3
+def measured_traffic(kernel, summary=TRAFFIC_SUMMARY):
+    """HBM bytes per launch of `kernel` from a committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (scaled by its copy-kernel calibration),
     or None when the summary does not list it."""
     try:
-        lines = open(TRAFFIC_SUMMARY).read().splitlines()
+        lines = open(summary).read().splitlines()
     except OSError:
         return None
     for line in lines:
@@ -351,7 +352,8 @@ def main_decode(args):
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic("decode_step", DECODE_TRAFFIC_SUMMARY),
+            "traffic_unit": "B per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "algorithmic_bytes": DECODE_STATE_BYTES * states,
         },
         "kernel_ms": {"decode_step": kernel_s * 1e3},
