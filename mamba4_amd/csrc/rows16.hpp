@@ -92,15 +92,19 @@ __device__ __forceinline__ void update_columns(float (&A)[4][64], const float (&
 
 constexpr int slot_cols(int m) { return 16 * (m + 1); }
 
-// In-place Cholesky of A + diag(floor); fl[m] is the floor of row a+16m.
-// Right-looking: at step j the pivot is broadcast from lane j%16, column j
-// is scaled by its reciprocal square root, and every later column of every
-// later row takes one DPP-fed FMA.  On return A holds L below the diagonal,
-// 1/L_ii on it and zeros above.  The 64 steps are expanded at compile time
-// so every register index is static.
+template <int Off, int... I>
+constexpr std::integer_sequence<int, (Off + I)...> offset_sequence(std::integer_sequence<int, I...>) {
+  return {};
+}
+
+// One elimination step of column J inside its 16-column panel P = J/16:
+// the pivot is broadcast from lane J%16, column J is scaled by its
+// reciprocal square root, and every later column of the panel takes one
+// DPP-fed FMA in every row slot that holds it.  Columns right of the panel
+// are updated afterwards, for all 16 columns at once, by panel_update.
 template <int J>
 __device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)[4], int a) {
-  constexpr int mj = J >> 4, lj = J & 15;
+  constexpr int mj = J >> 4, lj = J & 15, panel_end = 16 * mj + 15;
   const float piv = bcast16(A[mj][J] + fl[mj], lj);
   // v_rsq_f32 (1 ulp), as the reference's lax.rsqrt pivot
   // (lm/kernels/mamba4_fused.py:111); a non-positive pivot gives NaN.
@@ -127,7 +131,7 @@ __device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)
   // A[m][k] += (-l_ij) * l_kj as one v_fmac_f32_dpp per element, the l_kj
   // operand broadcast straight from lane k%16 (the compiler keeps the
   // broadcast in a separate v_mov_b32_dpp otherwise).
-  update_columns<J>(A, nl, std::make_integer_sequence<int, 63 - J>{});
+  update_columns<J>(A, nl, std::make_integer_sequence<int, panel_end - J>{});
   A[mj][J] = a == lj ? rs : A[mj][J];
 }
 
@@ -137,9 +141,113 @@ __device__ __forceinline__ void factor_steps(float (&A)[4][64], const float (&fl
   (factor_step<J>(A, fl, a), ...);
 }
 
+// Exchange of lane groups and register quads: q[g][e] is element e of
+// register quad g.  Afterwards lane (g, a) holds in quad mu what lane
+// (mu, a) held in quad g (a 4x4 transpose of 16-lane rows against quads;
+// its own inverse).  Two v_permlane32_swap then two v_permlane16_swap per
+// element: permlane32_swap(x, y) yields rows (x0, x1, y0, y1) and
+// (x2, x3, y2, y3), permlane16_swap(x, y) yields (x0, y0, x2, y2) and
+// (x1, y1, x3, y3) (checked on gfx950 with an in-bounds probe).
+__device__ __forceinline__ void exchange_quads(float& q0, float& q1, float& q2, float& q3) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(q0), __float_as_uint(q2),
+                                                  false, false);
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(q1), __float_as_uint(q3),
+                                                  false, false);
+  const auto t = __builtin_amdgcn_permlane16_swap(r[0], s[0], false, false);
+  const auto u = __builtin_amdgcn_permlane16_swap(r[1], s[1], false, false);
+  q0 = __uint_as_float(t[0]);
+  q1 = __uint_as_float(t[1]);
+  q2 = __uint_as_float(u[0]);
+  q3 = __uint_as_float(u[1]);
+}
+
+// The 16x16 block of columns C0..C0+15 of one row slot, exchanged in place.
+template <int C0>
+__device__ __forceinline__ void exchange_block(float (&row)[64]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    exchange_quads(row[C0 + e], row[C0 + 4 + e], row[C0 + 8 + e], row[C0 + 12 + e]);
+}
+
+// Trailing update of block (I, K) after panel P: A_IK -= L_I L_K^T for all
+// four matrices, with L_I, L_K the panel's 16x16 blocks in slots I and K,
+// already exchanged so that lane (g, r) holds in quad mu columns 4g..4g+3
+// of row r of matrix mu's block.  MFMA step e of lane group g then takes
+// the term k = 4g + e, and v_mfma_f32_16x16x4_f32 with A = L_K, B = L_I
+// gives D = L_K L_I^T = (L_I L_K^T)^T, i.e. lane (g, c) holds row c of
+// L_I L_K^T, columns 4g..4g+3, per matrix: exchanging the four accumulators
+// brings matrix mu's row c to lane (mu, c), the rows16 layout.
+template <int P, int I, int K>
+__device__ __forceinline__ void panel_block(float (&A)[4][64]) {
+  f4 acc[4];
+#pragma unroll
+  for (int mu = 0; mu < 4; ++mu) {
+    acc[mu] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      acc[mu] = __builtin_amdgcn_mfma_f32_16x16x4f32(A[K][16 * P + 4 * mu + e],
+                                                    A[I][16 * P + 4 * mu + e], acc[mu], 0, 0, 0);
+  }
+  float d[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d[g][e] = acc[g][e];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) exchange_quads(d[0][e], d[1][e], d[2][e], d[3][e]);
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * g + e] -= d[g][e];
+}
+
+// Rank-16 update of the trailing matrix after panel P (slots > P).
+template <int P>
+__device__ __forceinline__ void panel_update(float (&A)[4][64]) {
+  if constexpr (P < 3) {
+#pragma unroll
+    for (int i = P + 1; i < 4; ++i) {
+      if (i == 1) exchange_block<16 * P>(A[1]);
+      if (i == 2) exchange_block<16 * P>(A[2]);
+      if (i == 3) exchange_block<16 * P>(A[3]);
+    }
+    if constexpr (P < 1) {
+      panel_block<P, 1, 1>(A);
+      panel_block<P, 2, 1>(A);
+      panel_block<P, 3, 1>(A);
+    }
+    if constexpr (P < 2) {
+      panel_block<P, 2, 2>(A);
+      panel_block<P, 3, 2>(A);
+    }
+    panel_block<P, 3, 3>(A);
+#pragma unroll
+    for (int i = P + 1; i < 4; ++i) {
+      if (i == 1) exchange_block<16 * P>(A[1]);
+      if (i == 2) exchange_block<16 * P>(A[2]);
+      if (i == 3) exchange_block<16 * P>(A[3]);
+    }
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl)[4], int a) {
+  factor_steps(A, fl, a, offset_sequence<16 * P>(std::make_integer_sequence<int, 16>{}));
+  panel_update<P>(A);
+}
+
+// In-place Cholesky of A + diag(floor); fl[m] is the floor of row a+16m.
+// Blocked right-looking, four 16-column panels: each panel is eliminated
+// column by column with DPP-fed FMAs (factor_step), then the trailing
+// matrix takes the panel's rank-16 update on MFMA (panel_update).  On
+// return A holds L below the diagonal, 1/L_ii on it and zeros above.  All
+// steps are expanded at compile time so every register index is static.
 __device__ __forceinline__ void factor_rows16(float (&A)[4][64], const float (&fl)[4]) {
   const int a = threadIdx.x & 15;
-  factor_steps(A, fl, a, std::make_integer_sequence<int, 64>{});
+  factor_panel<0>(A, fl, a);
+  factor_panel<1>(A, fl, a);
+  factor_panel<2>(A, fl, a);
+  factor_panel<3>(A, fl, a);
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
