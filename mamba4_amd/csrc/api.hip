@@ -72,7 +72,15 @@ constexpr size_t kChunkLdsBytes = 4 * m4::TILE * sizeof(float);
 constexpr size_t kGradsLdsBytes = 7 * m4::TILE * sizeof(float);
 
 bool configured = false;
+int g_cus = 256;  // compute units of the device (set by configure())
 std::mutex g_cfg_mu;
+
+// Grid of a persistent chunk kernel: `per_cu` resident blocks per compute
+// unit, never more blocks than chunks.
+unsigned persistent_grid(unsigned chunks, int per_cu) {
+  const unsigned cap = (unsigned)(g_cus * per_cu);
+  return chunks < cap ? chunks : cap;
+}
 
 int configure() {
   std::lock_guard<std::mutex> lock(g_cfg_mu);
@@ -91,6 +99,11 @@ int configure() {
     if (e != hipSuccess)
       return fail(M4MR_EHIP, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
   }
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+      cus > 0)
+    g_cus = cus;
   configured = true;
   return M4MR_OK;
 }
@@ -235,7 +248,8 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_read_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, keys,
+    hipLaunchKernelGGL(m4::fwd_read_kernel, dim3(persistent_grid(seqs, 2)), dim3(256),
+                       kChunkLdsBytes, st, d, keys,
                        values, queries, beta, log_decay, solved, start_cross, output, variance);
   });
 }

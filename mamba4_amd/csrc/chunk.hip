@@ -23,9 +23,9 @@ struct SeqIndex {
   long seq;
 };
 
-__device__ __forceinline__ SeqIndex seq_index(const Dims& d) {
+__device__ __forceinline__ SeqIndex seq_at(const Dims& d, long seq) {
   SeqIndex s;
-  s.seq = blockIdx.x;
+  s.seq = seq;
   s.n = (int)(s.seq % d.NC);
   const int bh = (int)(s.seq / d.NC);
   s.b = bh / d.H;
@@ -33,6 +33,8 @@ __device__ __forceinline__ SeqIndex seq_index(const Dims& d) {
   s.len = chunk_len(d, s.n);
   return s;
 }
+
+__device__ __forceinline__ SeqIndex seq_index(const Dims& d) { return seq_at(d, blockIdx.x); }
 
 struct TokenRows {
   const float* base;
@@ -47,6 +49,11 @@ __device__ __forceinline__ TokenRows rows_of(const float* base, const Dims& d, c
   return TokenRows{base, d, si.b, si.h, si.n * d.chunk};
 }
 
+// Persistent: block i handles chunks i, i + gridDim.x, ...  The next chunk's
+// tiles load into registers while this chunk is computed: Y, K and C0 right
+// after this chunk's are in LDS, its queries once this chunk's variance is
+// done, its values once this chunk's values are in LDS (at most five tiles
+// in flight per thread, keeping two blocks per CU).
 __global__ __launch_bounds__(256) void fwd_read_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ values,
     const float* __restrict__ queries, const float* __restrict__ beta,
@@ -59,64 +66,81 @@ __global__ __launch_bounds__(256) void fwd_read_kernel(
   float* G = K + TILE;
   float* C0 = G + TILE;  // C0 transposed: C0[e][p]
   __shared__ ChunkScalars cs;
-  const SeqIndex si = seq_index(d);
+  const long nseq = (long)d.B * d.H * d.NC;
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
-
-  // Every global tile is fetched up front; values and C0 wait in registers
-  // while the scores are computed.
+  long seq = blockIdx.x;
+  SeqIndex si = seq_at(d, seq);
   TileRegs ry, rk, rv, rq;
   TileRegsT rc;
   ry.fetch_rows(si.len, rows_of(solved, d, si));
   rk.fetch_rows(si.len, rows_of(keys, d, si));
-  rv.fetch_rows(si.len, rows_of(values, d, si));
-  rq.fetch_rows(si.len, rows_of(queries, d, si));
   rc.fetch_matrix(start_c + si.seq * 4096);
-  ry.store(Y);
-  rk.store(K);
-  rc.store(C0);
-  load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
-  __syncthreads();
+  rq.fetch_rows(si.len, rows_of(queries, d, si));
+  rv.fetch_rows(si.len, rows_of(values, d, si));
 
-  // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
-  // the 16 lanes that hold the rest of each row.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = (threadIdx.x >> 4) + 16 * j;
-    const f4 prod = rq.v[j] * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
-    const float v = row16_sum(prod[0] + prod[1] + prod[2] + prod[3]);
-    if ((threadIdx.x & 15) == 0 && t < si.len)
-      variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] = v;
-  }
+  for (;;) {
+    ry.store(Y);
+    rk.store(K);
+    rc.store(C0);
+    load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
+    __syncthreads();
+    const long next = seq + gridDim.x;
+    const bool more = next < nseq;  // uniform over the block
+    const SeqIndex sn = seq_at(d, more ? next : seq);
+    if (more) {
+      ry.fetch_rows(sn.len, rows_of(solved, d, sn));
+      rk.fetch_rows(sn.len, rows_of(keys, d, sn));
+      rc.fetch_matrix(start_c + sn.seq * 4096);
+    }
 
-  f4 acc[4];
-  zero4(acc);
-  tile_mma<false, true>(acc, Y, K, 64, w);  // scores y_t . k_s
+    // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
+    // the 16 lanes that hold the rest of each row.
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
+    for (int j = 0; j < 4; ++j) {
+      const int t = (threadIdx.x >> 4) + 16 * j;
+      const f4 prod = rq.v[j] * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
+      const float v = row16_sum(prod[0] + prod[1] + prod[2] + prod[3]);
+      if ((threadIdx.x & 15) == 0 && t < si.len)
+        variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] = v;
+    }
+    if (more) rq.fetch_rows(sn.len, rows_of(queries, d, sn));
+
+    f4 acc[4];
+    zero4(acc);
+    tile_mma<false, true>(acc, Y, K, 64, w);  // scores y_t . k_s
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = acc_row(w, q), s = acc_col<false>(jb);
+        float v = 0.f;
+        if (s <= t && t < si.len)
+          v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
+        G[t * LDT + s] = v;
+      }
+    __syncthreads();
+    rv.store(K);
+    __syncthreads();
+    if (more) rv.fetch_rows(sn.len, rows_of(values, d, sn));
+
+    f4 out[4], inh[4];
+    zero4(out);
+    zero4(inh);
+    tile_mma<false, false>(out, G, K, k_terms(si.len), w);  // within-chunk reads
+    tile_mma<false, false>(inh, Y, C0, 64, w);              // inherited reads y_t . C0[p]
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(w, q), s = acc_col<false>(jb);
-      float v = 0.f;
-      if (s <= t && t < si.len) v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
-      G[t * LDT + s] = v;
+      const int t = acc_row(w, q);
+      if (t < si.len) {
+        const float carried = expf(cs.prefix[t]);
+        float* dst = output + token_head(d, si.b, si.n * d.chunk + t, si.h) * 64;
+        *reinterpret_cast<f4*>(dst + c4) = quad_row(out, q) + carried * quad_row(inh, q);
+      }
     }
-  __syncthreads();
-  rv.store(K);
-  __syncthreads();
-
-  f4 out[4], inh[4];
-  zero4(out);
-  zero4(inh);
-  tile_mma<false, false>(out, G, K, k_terms(si.len), w);  // within-chunk reads
-  tile_mma<false, false>(inh, Y, C0, 64, w);              // inherited reads y_t . C0[p]
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int t = acc_row(w, q);
-    if (t < si.len) {
-      const float carried = expf(cs.prefix[t]);
-      float* dst = output + token_head(d, si.b, si.n * d.chunk + t, si.h) * 64;
-      *reinterpret_cast<f4*>(dst + c4) = quad_row(out, q) + carried * quad_row(inh, q);
-    }
+    if (!more) break;
+    __syncthreads();  // the tiles and scalars are read; the next chunk may overwrite them
+    si = sn;
+    seq = next;
   }
 }
 

@@ -125,14 +125,18 @@ __device__ __forceinline__ void mma_block(f4 acc[4], const float* A, const float
     a = *reinterpret_cast<const f4*>(A + (16 * w + r) * LDT + kk);
   }
   if (TB) {
+    f4 b[4];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int col = QUAD ? 4 * r + jb : 16 * jb + r;
-      const f4 b = *reinterpret_cast<const f4*>(B + col * LDT + kk);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc[jb], 0, 0, 0);
+      b[jb] = *reinterpret_cast<const f4*>(B + col * LDT + kk);
     }
+    // Consecutive MFMAs go to different accumulators (no dependent chain).
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[jb][e], acc[jb], 0, 0, 0);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {

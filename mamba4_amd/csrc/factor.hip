@@ -118,9 +118,10 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
               A[m][k] = sv[e];
             }
             evidence[slot_quad(m, q) * 64 + lane] = sv;
-            // Keeps the compiler from hoisting all 40 LDS reads ahead of the
-            // arithmetic (which would need 160 more registers).
-            __builtin_amdgcn_sched_barrier(0);
+            // Every fourth quad: keeps the compiler from hoisting all 40 LDS
+            // reads ahead of the arithmetic (which would need 160 more
+            // registers) while four reads stay in flight together.
+            if ((q & 3) == 3) __builtin_amdgcn_sched_barrier(0);
           }
         }
       }
