@@ -32,10 +32,16 @@ extern "C" {
 #define M4MR_KEY_DIM 64
 #define M4MR_VALUE_DIM 64
 #define M4MR_MAX_CHUNK 64
-/* Stored lower factor per token-head: the lower triangle row by row, row i
- * padded to 4*ceil((i+1)/4) floats (16-byte aligned rows), 2176 floats in
- * all; the diagonal holds the reciprocal pivot 1/L_ii (the reference keeps
- * the same reciprocal convention, lm/kernels/mamba4_fused.py:113). */
+/* Stored lower factor per token-head, 2176 floats: the lower triangle in
+ * 16-byte column quads.  Row i = a + 16m (a < 16) holds quads 0..i/4; for
+ * each row slot m and quad q the quads of rows a + 16m that hold it are
+ * stored contiguously in increasing a, runs in increasing q, slots in
+ * increasing m: row i's quad q is quad R(m,q) + a of the factor with
+ * R(m,q) = 32m^2 + 8m + (q <= 4m ? 16q : 16(4m+1) + {-4, 4, 8}[q-4m-1]).
+ * Entries above the diagonal inside a stored quad are zero.  The diagonal
+ * holds the reciprocal pivot 1/L_ii (the reference keeps the same reciprocal
+ * convention, lm/kernels/mamba4_fused.py:113).  The layout is private to the
+ * residuals, as the reference's packing is (lm/kernels/mamba4_fused.py:36-42). */
 #define M4MR_FACTOR_FLOATS 2176
 
 #define M4MR_OK 0

@@ -9,10 +9,13 @@
 // lane of the row), folded into the consuming FMA where the compiler can.
 // No LDS is touched and 74% of the issued FMA lanes do useful work.
 //
-// Factor storage ("padded rows"): the lower triangle row by row, row i
-// padded to a multiple of 4 floats (4*ceil((i+1)/4)), 2176 floats per
-// matrix; the diagonal holds the reciprocal pivot 1/L_ii.  Lane a writes or
-// reads its four rows with 16-byte accesses.
+// Factor storage ("quad runs"): row i = a + 16m holds the column quads
+// 0..i/4.  For each row slot m and column quad q, the quads of the lanes that
+// hold it (a >= 4 max(0, q - 4m)) are stored contiguously in lane order, so
+// one 16-byte store or load instruction of a 16-lane row covers a 64..256-byte
+// run and whole 128-byte lines over a slot.  Slots follow each other and runs
+// go in increasing q: 544 quads, 2176 floats per matrix; the diagonal holds
+// the reciprocal pivot 1/L_ii.
 #pragma once
 
 #include <utility>
@@ -23,10 +26,17 @@ namespace m4 {
 
 constexpr int ROWS_FACTOR = 2176;  // floats per stored factor
 
-// Floats before row i in the padded-row layout: with i = 4p + s,
-// 4 (p+1) (2p + s).
-__host__ __device__ constexpr int row_offset(int i) {
-  return 4 * ((i >> 2) + 1) * (2 * (i >> 2) + (i & 3));
+// Quads before row slot m: slot m holds 16 (4m + 1) + 12 + 8 + 4 quads.
+__host__ __device__ constexpr int slot_base(int m) { return 32 * m * m + 8 * m; }
+
+// Lane a's quad q of row slot m is quad run_quad(m, q) + a of the factor.
+// Runs q <= 4m hold all 16 lanes; runs q = 4m + r (r = 1, 2, 3) start at
+// lane 4r.
+__host__ __device__ constexpr int run_quad(int m, int q) {
+  return slot_base(m) + (q <= 4 * m ? 16 * q
+                                    : 16 * (4 * m + 1) + (q == 4 * m + 1   ? -4
+                                                          : q == 4 * m + 2 ? 4
+                                                                           : 8));
 }
 
 template <int CTRL>
@@ -292,31 +302,30 @@ __device__ __forceinline__ void solve_rows16(const float (&A)[4][64], float (&r)
   solve_steps(A, r, w, y, a, std::make_integer_sequence<int, 64>{});
 }
 
-// Padded-row factor store / load for this lane's four rows.
+// Quad-run factor store / load for this lane's four rows.
 __device__ __forceinline__ void store_rows16(const float (&A)[4][64], float* __restrict__ fac) {
   const int a = threadIdx.x & 15;
+  f4* lane = reinterpret_cast<f4*>(fac) + a;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const int i = a + 16 * m, p = i >> 2;
-    float* row = fac + row_offset(i);
+    const int p = (a + 16 * m) >> 2;
 #pragma unroll
     for (int q = 0; q < 4 * m + 4; ++q)
       if (q <= p)
-        *reinterpret_cast<f4*>(row + 4 * q) =
-            f4{A[m][4 * q], A[m][4 * q + 1], A[m][4 * q + 2], A[m][4 * q + 3]};
+        lane[run_quad(m, q)] = f4{A[m][4 * q], A[m][4 * q + 1], A[m][4 * q + 2], A[m][4 * q + 3]};
   }
 }
 
 __device__ __forceinline__ void load_rows16(float (&A)[4][64], const float* __restrict__ fac) {
   const int a = threadIdx.x & 15;
+  const f4* lane = reinterpret_cast<const f4*>(fac) + a;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const int i = a + 16 * m, p = i >> 2;
-    const float* row = fac + row_offset(i);
+    const int p = (a + 16 * m) >> 2;
 #pragma unroll
     for (int q = 0; q < 4 * m + 4; ++q) {
       f4 v = f4{0.f, 0.f, 0.f, 0.f};
-      if (q <= p) v = *reinterpret_cast<const f4*>(row + 4 * q);
+      if (q <= p) v = lane[run_quad(m, q)];
       A[m][4 * q] = v[0];
       A[m][4 * q + 1] = v[1];
       A[m][4 * q + 2] = v[2];
