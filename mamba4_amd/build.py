@@ -36,6 +36,11 @@ FLAGS = [
 # Sources whose inline-asm DPP multiply-adds are re-checked on the compiled code.
 HAZARD_CHECKED = ["factor.hip"]
 
+# Per-source extra flags.  The factorization accumulates its trailing blocks
+# in place with MFMA; keeping MFMA operands and results in VGPRs avoids a
+# second copy of those blocks in AGPRs (which would halve the occupancy).
+SOURCE_FLAGS = {"factor.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 _NOISE = "is not a recognized feature for this target"
 
 
@@ -57,13 +62,13 @@ def build(verbose=False):
         jobs = {}
         for src in SOURCES:
             obj = os.path.join(tmp, src.replace(".hip", ".o"))
-            jobs[src] = (obj, [hipcc(), *FLAGS, "-fPIC", "-c", *include, "-o", obj,
-                               os.path.join(CSRC, src)])
+            jobs[src] = (obj, [hipcc(), *FLAGS, *SOURCE_FLAGS.get(src, []), "-fPIC", "-c",
+                               *include, "-o", obj, os.path.join(CSRC, src)])
         asms = {}
         for src in HAZARD_CHECKED:
             asm = os.path.join(tmp, src.replace(".hip", ".s"))
-            asms[src] = (asm, [hipcc(), *FLAGS, "--cuda-device-only", "-S", *include, "-o", asm,
-                               os.path.join(CSRC, src)])
+            asms[src] = (asm, [hipcc(), *FLAGS, *SOURCE_FLAGS.get(src, []), "--cuda-device-only",
+                               "-S", *include, "-o", asm, os.path.join(CSRC, src)])
         workers = min(8, len(jobs) + len(asms))
         with ThreadPoolExecutor(max_workers=workers) as pool:
             results = {k: pool.submit(_run, cmd) for k, (_, cmd) in jobs.items()}

@@ -58,8 +58,9 @@ def check(asm_text):
         if mnemonic.startswith("s_branch") or mnemonic.startswith("s_cbranch"):
             history, unknown = [], 2
         if mnemonic.startswith("v_") and not mnemonic.startswith("v_cmp"):
-            dst = operands.split(",")[0]
-            written = _regs(dst)
+            ops = operands.split(",")
+            # v_permlane16_swap / v_permlane32_swap write both of their operands.
+            written = _regs(ops[0]) | (_regs(ops[1]) if "_swap" in mnemonic else set())
             if written:
                 history.append((0, written))
     return problems

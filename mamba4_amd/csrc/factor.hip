@@ -33,9 +33,12 @@ __device__ __forceinline__ int wave_max4(int x) {
 }
 
 // One token's inputs for this lane's four rows: key and query rows a+16m,
-// beta and the decay lam.
+// beta and the log decay.  The decay's exponential is taken where it is used,
+// so nothing waits on these loads until the next token's turn; the factor
+// stores issued in between then stay in flight (vmcnt counts loads and stores
+// in issue order).
 struct TokenInputs {
-  float k[4], q[4], beta, lam;
+  float k[4], q[4], beta, log_lam;
   long th;
 };
 
@@ -49,7 +52,7 @@ __device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const
     in.q[m] = queries[in.th * 64 + a + 16 * m];
   }
   in.beta = beta[in.th];
-  in.lam = expf(log_decay[in.th]);
+  in.log_lam = log_decay[in.th];
 }
 
 // Two waves share the four sequences of a block and take alternate tokens:
@@ -78,6 +81,7 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
   const int t0 = n * d.chunk + sub_first(d, u);
   const int steps = wave_max4(len);
 
+  // The running evidence, negated (the factorization's working convention).
   __shared__ f4 evidence[40 * 64];  // [quad][lane], shared by both waves
   if (wave == 0) {
     const float* s0 = start_s + ((long)bh * d.NS + ns) * 4096;
@@ -86,7 +90,7 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
 #pragma unroll
       for (int q = 0; q < 4 * m + 4; ++q)
         evidence[slot_quad(m, q) * 64 + lane] =
-            *reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
+            -*reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
   }
   float fl[4];
 #pragma unroll
@@ -105,16 +109,17 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
 #pragma unroll
     for (int turn = 0; turn < 2; ++turn) {
       if (turn == wave && mine) {
+        const float lam = expf(cur.log_lam);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const float bk = cur.beta * cur.k[m];
+          const float nbk = -cur.beta * cur.k[m];
 #pragma unroll
           for (int q = 0; q < 4 * m + 4; ++q) {
             f4 sv = evidence[slot_quad(m, q) * 64 + lane];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int k = 4 * q + e;
-              sv[e] = cur.lam * sv[e] + bk * bcast16(cur.k[k >> 4], k & 15);
+              sv[e] = lam * sv[e] + nbk * bcast16(cur.k[k >> 4], k & 15);
               A[m][k] = sv[e];
             }
             evidence[slot_quad(m, q) * 64 + lane] = sv;
@@ -131,9 +136,9 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
       // Prefetch this wave's next token; the factorization covers the latency.
       TokenInputs next;
       load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
-      factor_rows16(A, fl);
-      float y[4];
-      solve_rows16(A, cur.q, y);
+      float nw[4], y[4];
+      factor_rows16(A, fl, cur.q, nw);
+      backward_rows16(A, nw, y);
       if (valid) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) solved[cur.th * 64 + a + 16 * m] = y[m];
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(64) void factored_solve_kernel(const float* __restr
 
 // Batched SPD solve, four systems per wave: precision [N,dim,dim] (only
 // k <= i is read), rhs [N,dim] -> solution [N,dim] and, when `factors` is
-// non-null, each system's factor in the padded-row layout.  Systems are
+// non-null, each system's factor in the quad-run layout.  Systems are
 // padded to 64 with an identity block, so the padded coordinates solve to
 // zero, as the reference pads its lanes with identity systems
 // (lm/kernels/mamba4_fused.py:292-299).  Restates _factor_and_solve
@@ -188,7 +193,7 @@ __global__ __launch_bounds__(64) void spd_solve_kernel(const float* __restrict__
         f4 v = f4{0.f, 0.f, 0.f, 0.f};
         if (q <= p) v = *reinterpret_cast<const f4*>(P + i * 64 + 4 * q);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) A[m][4 * q + e] = 4 * q + e <= i ? v[e] : 0.f;
+        for (int e = 0; e < 4; ++e) A[m][4 * q + e] = 4 * q + e <= i ? -v[e] : 0.f;
       }
     }
   } else {
@@ -199,19 +204,19 @@ __global__ __launch_bounds__(64) void spd_solve_kernel(const float* __restrict__
       for (int k = 0; k < slot_cols(m); ++k) {
         float v = k == i ? 1.f : 0.f;
         if (i < dim && k <= i) v = P[i * dim + k];
-        A[m][k] = v;
+        A[m][k] = -v;
       }
     }
   }
   const float zero[4] = {0.f, 0.f, 0.f, 0.f};
-  factor_rows16(A, zero);
-  float r[4], y[4];
+  float r[4], nw[4], y[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int i = a + 16 * m;
     r[m] = i < dim ? rhs[n * dim + i] : 0.f;
   }
-  solve_rows16(A, r, y);
+  factor_rows16(A, zero, r, nw);
+  backward_rows16(A, nw, y);
   if (active) {
 #pragma unroll
     for (int m = 0; m < 4; ++m)
@@ -287,28 +292,29 @@ __global__ __launch_bounds__(64) void spd_backward_kernel(
 // The factorization needs rows a+16m in lane a: each 16-row slot of the
 // updated S passes through a 17 KB LDS buffer (rows padded to 17 quads, so
 // both the quad-wise writes and the row-wise reads are conflict-free).
-__global__ __launch_bounds__(64) void decode_step_kernel(
-    float* __restrict__ evidence, float* __restrict__ cross, const float* __restrict__ key,
-    const float* __restrict__ value, const float* __restrict__ query,
-    const float* __restrict__ beta, const float* __restrict__ log_decay,
-    const float* __restrict__ floor, long N, int H, float* __restrict__ output,
-    float* __restrict__ variance) {
+// Two waves per SIMD: the value, query and key quad are read again after the
+// factorization rather than held in registers across it.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
+                   const float* __restrict__ key, const float* __restrict__ value,
+                   const float* __restrict__ query, const float* __restrict__ beta,
+                   const float* __restrict__ log_decay, const float* __restrict__ floor, long N,
+                   int H, float* __restrict__ output, float* __restrict__ variance) {
   const int lane = threadIdx.x, a = lane & 15, mu = lane >> 4;
   long nidx = (long)blockIdx.x * 4 + mu;
   const bool active = nidx < N;
   if (!active) nidx = N - 1;
   float* S = evidence + nidx * 4096;
   float* C = cross + nidx * 4096;
-  float kr[4], vr[4], qr[4], fl[4];
+  float kr[4], qr[4], fl[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     kr[m] = key[nidx * 64 + a + 16 * m];
-    vr[m] = value[nidx * 64 + a + 16 * m];
     qr[m] = query[nidx * 64 + a + 16 * m];
     fl[m] = floor[(nidx % H) * 64 + a + 16 * m];
   }
   // Column quad a of the key: k[4a .. 4a+3].
-  const f4 kq = *reinterpret_cast<const f4*>(key + nidx * 64 + 4 * a);
+  f4 kq = *reinterpret_cast<const f4*>(key + nidx * 64 + 4 * a);
   const float bt = beta[nidx], lam = expf(log_decay[nidx]);
   __shared__ f4 stage[4 * 16 * 17];  // [state][row][quad], 17 quads per row
   f4* mine = stage + mu * 16 * 17;
@@ -327,19 +333,35 @@ __global__ __launch_bounds__(64) void decode_step_kernel(
       mine[r * 17 + a] = sv;
     }
     __syncthreads();
-    // Row a of this slot, columns 0 .. 16m+15, into the factorization layout.
+    // Into the factorization layout, negated: block column 0 as row a of this
+    // slot, blocks (m, K >= 1) exchanged (lane (g, j) takes quad 4K + g of
+    // row j of every state).
 #pragma unroll
-    for (int q = 0; q < 4 * m + 4; ++q) {
+    for (int q = 0; q < 4; ++q) {
       const f4 v = mine[a * 17 + q];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) A[m][4 * q + e] = v[e];
+      for (int e = 0; e < 4; ++e) A[m][4 * q + e] = -v[e];
     }
+#pragma unroll
+    for (int K = 1; K <= m; ++K)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const f4 v = stage[s * 16 * 17 + a * 17 + 4 * K + mu];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) A[m][16 * K + 4 * s + e] = -v[e];
+      }
     __syncthreads();
   }
-  float qcopy[4] = {qr[0], qr[1], qr[2], qr[3]};
-  factor_rows16(A, fl);
-  float y[4];
-  solve_rows16(A, qcopy, y);
+  float nw[4], y[4];
+  factor_exchanged(A, fl, qr, nw);
+  backward_rows16(A, nw, y);
+  float vr[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    vr[m] = value[nidx * 64 + a + 16 * m];
+    qr[m] = query[nidx * 64 + a + 16 * m];
+  }
+  kq = *reinterpret_cast<const f4*>(key + nidx * 64 + 4 * a);
   // y[4a .. 4a+3] for the coalesced read: y_j lives in lane j%16, slot j/16.
   __shared__ float ys[4][64];
 #pragma unroll

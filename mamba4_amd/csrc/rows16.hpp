@@ -86,18 +86,19 @@ __device__ __forceinline__ void fmac_bcast(float& acc, float src, float mul) {
 }
 
 // Column K of every row slot that holds it (slots m >= K/16 and >= J/16)
-// takes l_KJ, broadcast from lane K%16 of slot K/16.
+// takes l_iJ l_KJ, l_KJ broadcast from lane K%16 of slot K/16 and l_iJ
+// = L[m][J] of this lane.
 template <int J, int K>
-__device__ __forceinline__ void update_column(float (&A)[4][64], const float (&nl)[4]) {
+__device__ __forceinline__ void update_column(float (&A)[4][64], const float (&L)[4][64]) {
   constexpr int r = K >> 4, mj = J >> 4, m0 = r > mj ? r : mj;
 #pragma unroll
-  for (int m = m0; m < 4; ++m) fmac_bcast<(K & 15)>(A[m][K], A[r][J], nl[m]);
+  for (int m = m0; m < 4; ++m) fmac_bcast<(K & 15)>(A[m][K], A[r][J], L[m][J]);
 }
 
 template <int J, int... I>
-__device__ __forceinline__ void update_columns(float (&A)[4][64], const float (&nl)[4],
+__device__ __forceinline__ void update_columns(float (&A)[4][64], const float (&L)[4][64],
                                                std::integer_sequence<int, I...>) {
-  (update_column<J, J + 1 + I>(A, nl), ...);
+  (update_column<J, J + 1 + I>(A, L), ...);
 }
 
 constexpr int slot_cols(int m) { return 16 * (m + 1); }
@@ -107,48 +108,62 @@ constexpr std::integer_sequence<int, (Off + I)...> offset_sequence(std::integer_
   return {};
 }
 
-// One elimination step of column J inside its 16-column panel P = J/16:
-// the pivot is broadcast from lane J%16, column J is scaled by its
-// reciprocal square root, and every later column of the panel takes one
-// DPP-fed FMA in every row slot that holds it.  Columns right of the panel
-// are updated afterwards, for all 16 columns at once, by panel_update.
+// Factorization convention.  The working matrix is held negated: before
+// column J is eliminated, A[m][k] holds -(E + diag(floor) - sum_{j<J} l_ij
+// l_kj) without the floor, i.e. -E minus the updates so far.  Every update
+// then adds l_ij l_kj (an FMA with no negation), the pivot is floor - A_JJ,
+// and the trailing blocks accumulate their MFMA updates in place (D = C + A B).
+//
+// Block layouts.  "Rows": lane (mu, a) holds row 16I + a of matrix mu in
+// A[I][16K + c], c = 0..15 (the slot layout above).  "Exchanged": lane
+// (g, j) holds in A[I][16K + 4mu + e] element (16I + j, 16K + 4g + e) of
+// matrix mu.  exchange_block converts one 16x16 block of all four matrices
+// between the two (it is its own inverse).  Exchanged is the operand layout
+// of v_mfma_f32_16x16x4_f32 for a 16x16 block (A(i, k) in lane i + 16k: row
+// i of the block, column 4k + e in MFMA step e) and also its accumulator
+// layout for a product whose rows are block columns (D(i, j) in lane
+// j + 16(i/4), element i%4).
+
+// One elimination step of column J inside its 16-column panel P = J/16,
+// with the forward substitution of the right-hand side r folded in: the
+// pivot floor - A_JJ is broadcast from lane J%16, column J becomes l_iJ =
+// -A_iJ / sqrt(pivot), every later column of the panel takes l_iJ l_KJ by one
+// DPP-fed FMA per slot, and r_i takes -l_iJ w_J with w_J = r_J / l_JJ.  The
+// step records -w_J in nw (lane J%16 of slot J/16) and 1/l_JJ on the
+// diagonal.  Columns right of the panel are updated by panel_update.
 template <int J>
-__device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)[4], int a) {
+__device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)[4],
+                                            float (&r)[4], float (&nw)[4], int a) {
   constexpr int mj = J >> 4, lj = J & 15, panel_end = 16 * mj + 15;
-  const float piv = bcast16(A[mj][J] + fl[mj], lj);
+  const float piv = bcast16(fl[mj] - A[mj][J], lj);
   // v_rsq_f32 (1 ulp), as the reference's lax.rsqrt pivot
   // (lm/kernels/mamba4_fused.py:111); a non-positive pivot gives NaN.
   const float rs = __builtin_amdgcn_rsqf(piv);
 #pragma unroll
-  for (int m = mj; m < 4; ++m) A[m][J] *= rs;
+  for (int m = mj; m < 4; ++m) A[m][J] = -A[m][J] * rs;
+  float nwj = -r[mj] * rs;  // -w_J in lane J%16: r_J is final once column J is reached
   // GFX9 needs two wait states between a VALU write of a VGPR and a DPP read
   // of it, and the compiler's hazard tracking does not see inside inline asm.
-  // Passing the freshly scaled column through this s_nop as in/out operands
-  // orders every write of it before the nop and every DPP read after it.
-  // (The build re-checks this hazard on the compiled code, see
-  // mamba4_amd/check_dpp_hazards.py.)
-  if constexpr (mj == 0)
-    asm volatile("s_nop 1" : "+v"(A[0][J]), "+v"(A[1][J]), "+v"(A[2][J]), "+v"(A[3][J]));
-  else if constexpr (mj == 1)
-    asm volatile("s_nop 1" : "+v"(A[1][J]), "+v"(A[2][J]), "+v"(A[3][J]));
-  else if constexpr (mj == 2)
-    asm volatile("s_nop 1" : "+v"(A[2][J]), "+v"(A[3][J]));
-  else
-    asm volatile("s_nop 1" : "+v"(A[3][J]));
-  float nl[4];
-#pragma unroll
-  for (int m = mj; m < 4; ++m) nl[m] = -A[m][J];
-  // A[m][k] += (-l_ij) * l_kj as one v_fmac_f32_dpp per element, the l_kj
+  // The DPP sources of this step are column J of slot mj and -w_J; passing
+  // them through this s_nop as in/out operands orders their writes before
+  // the nop and every DPP read after it.  (The build re-checks this hazard on
+  // the compiled code, see mamba4_amd/check_dpp_hazards.py.)
+  asm volatile("s_nop 1" : "+v"(A[mj][J]), "+v"(nwj));
+  // A[m][k] += l_ij * l_kj as one v_fmac_f32_dpp per element, the l_kj
   // operand broadcast straight from lane k%16 (the compiler keeps the
   // broadcast in a separate v_mov_b32_dpp otherwise).
-  update_columns<J>(A, nl, std::make_integer_sequence<int, panel_end - J>{});
+  update_columns<J>(A, A, std::make_integer_sequence<int, panel_end - J>{});
+#pragma unroll
+  for (int m = mj; m < 4; ++m) fmac_bcast<lj>(r[m], nwj, A[m][J]);
+  nw[mj] = a == lj ? nwj : nw[mj];
   A[mj][J] = a == lj ? rs : A[mj][J];
 }
 
 template <int... J>
-__device__ __forceinline__ void factor_steps(float (&A)[4][64], const float (&fl)[4], int a,
+__device__ __forceinline__ void factor_steps(float (&A)[4][64], const float (&fl)[4],
+                                             float (&r)[4], float (&nw)[4], int a,
                                              std::integer_sequence<int, J...>) {
-  (factor_step<J>(A, fl, a), ...);
+  (factor_step<J>(A, fl, r, nw, a), ...);
 }
 
 // Exchange of lane groups and register quads: q[g][e] is element e of
@@ -179,89 +194,129 @@ __device__ __forceinline__ void exchange_block(float (&row)[64]) {
     exchange_quads(row[C0 + e], row[C0 + 4 + e], row[C0 + 8 + e], row[C0 + 12 + e]);
 }
 
-// Trailing update of block (I, K) after panel P: A_IK -= L_I L_K^T for all
-// four matrices, with L_I, L_K the panel's 16x16 blocks in slots I and K,
-// already exchanged so that lane (g, r) holds in quad mu columns 4g..4g+3
-// of row r of matrix mu's block.  MFMA step e of lane group g then takes
-// the term k = 4g + e, and v_mfma_f32_16x16x4_f32 with A = L_K, B = L_I
-// gives D = L_K L_I^T = (L_I L_K^T)^T, i.e. lane (g, c) holds row c of
-// L_I L_K^T, columns 4g..4g+3, per matrix: exchanging the four accumulators
-// brings matrix mu's row c to lane (mu, c), the rows16 layout.
+// Trailing block (I, K) after panel P, both in the exchanged layout:
+// A_IK += L_IP L_KP^T for all four matrices (the working matrix is negated).
+// MFMA step e of matrix mu takes A = block (K, P) and B = block (I, P) in
+// register 16P + 4mu + e, so D(i, j) = sum_c l_{16K+i, c} l_{16I+j, c} lands
+// on element (16I + j, 16K + i): accumulator mu is A[I][16K + 4mu .. +3].
 template <int P, int I, int K>
 __device__ __forceinline__ void panel_block(float (&A)[4][64]) {
-  f4 acc[4];
 #pragma unroll
   for (int mu = 0; mu < 4; ++mu) {
-    acc[mu] = f4{0.f, 0.f, 0.f, 0.f};
+    f4 acc = f4{A[I][16 * K + 4 * mu], A[I][16 * K + 4 * mu + 1], A[I][16 * K + 4 * mu + 2],
+                A[I][16 * K + 4 * mu + 3]};
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      acc[mu] = __builtin_amdgcn_mfma_f32_16x16x4f32(A[K][16 * P + 4 * mu + e],
-                                                    A[I][16 * P + 4 * mu + e], acc[mu], 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[K][16 * P + 4 * mu + e],
+                                                 A[I][16 * P + 4 * mu + e], acc, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * mu + e] = acc[e];
   }
-  float d[4][4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) d[g][e] = acc[g][e];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) exchange_quads(d[0][e], d[1][e], d[2][e], d[3][e]);
-#pragma unroll
-  for (int g = 0; g < 4; ++g)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * g + e] -= d[g][e];
 }
 
-// Rank-16 update of the trailing matrix after panel P (slots > P).
+// Slots I > P of block column C, exchanged in place.
+template <int P, int C>
+__device__ __forceinline__ void exchange_below(float (&A)[4][64]) {
+  if constexpr (P < 1) exchange_block<16 * C>(A[1]);
+  if constexpr (P < 2) exchange_block<16 * C>(A[2]);
+  if constexpr (P < 3) exchange_block<16 * C>(A[3]);
+}
+
+// Rank-16 update of the trailing blocks after panel P, then the next panel's
+// block column back to the rows layout.  The panel's L blocks go to the
+// exchanged layout for the MFMA and back to rows for the solves and the
+// store; the blocks of the next panel are updated first.
 template <int P>
 __device__ __forceinline__ void panel_update(float (&A)[4][64]) {
   if constexpr (P < 3) {
-#pragma unroll
-    for (int i = P + 1; i < 4; ++i) {
-      if (i == 1) exchange_block<16 * P>(A[1]);
-      if (i == 2) exchange_block<16 * P>(A[2]);
-      if (i == 3) exchange_block<16 * P>(A[3]);
+    exchange_below<P, P>(A);
+    if constexpr (P == 0) {
+      panel_block<0, 1, 1>(A);
+      panel_block<0, 2, 1>(A);
+      panel_block<0, 3, 1>(A);
+      panel_block<0, 2, 2>(A);
+      panel_block<0, 3, 2>(A);
+      panel_block<0, 3, 3>(A);
+    } else if constexpr (P == 1) {
+      panel_block<1, 2, 2>(A);
+      panel_block<1, 3, 2>(A);
+      panel_block<1, 3, 3>(A);
+    } else {
+      panel_block<2, 3, 3>(A);
     }
-    if constexpr (P < 1) {
-      panel_block<P, 1, 1>(A);
-      panel_block<P, 2, 1>(A);
-      panel_block<P, 3, 1>(A);
-    }
-    if constexpr (P < 2) {
-      panel_block<P, 2, 2>(A);
-      panel_block<P, 3, 2>(A);
-    }
-    panel_block<P, 3, 3>(A);
-#pragma unroll
-    for (int i = P + 1; i < 4; ++i) {
-      if (i == 1) exchange_block<16 * P>(A[1]);
-      if (i == 2) exchange_block<16 * P>(A[2]);
-      if (i == 3) exchange_block<16 * P>(A[3]);
-    }
+    exchange_below<P, P>(A);
+    exchange_below<P, P + 1>(A);
   }
 }
 
 template <int P>
-__device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl)[4], int a) {
-  factor_steps(A, fl, a, offset_sequence<16 * P>(std::make_integer_sequence<int, 16>{}));
+__device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl)[4],
+                                             float (&r)[4], float (&nw)[4], int a) {
+  factor_steps(A, fl, r, nw, a, offset_sequence<16 * P>(std::make_integer_sequence<int, 16>{}));
   panel_update<P>(A);
 }
 
-// In-place Cholesky of A + diag(floor); fl[m] is the floor of row a+16m.
-// Blocked right-looking, four 16-column panels: each panel is eliminated
-// column by column with DPP-fed FMAs (factor_step), then the trailing
-// matrix takes the panel's rank-16 update on MFMA (panel_update).  On
-// return A holds L below the diagonal, 1/L_ii on it and zeros above.  All
-// steps are expanded at compile time so every register index is static.
-__device__ __forceinline__ void factor_rows16(float (&A)[4][64], const float (&fl)[4]) {
+// Blocked right-looking Cholesky of E + diag(floor) with the forward
+// substitution of r folded in.  On entry A holds -E: block column 0 in the
+// rows layout, blocks (I, K >= 1) exchanged (factor_rows16 converts a full
+// rows-layout input).  Four 16-column panels: each is eliminated column by
+// column with DPP-fed FMAs (factor_step), then the trailing blocks take the
+// panel's rank-16 update on MFMA (panel_update).  On return A holds L below
+// the diagonal, 1/L_ii on it and zeros above (rows layout), r is consumed
+// and nw = -L^-1 r.  All steps are expanded at compile time so every
+// register index is static.
+__device__ __forceinline__ void factor_exchanged(float (&A)[4][64], const float (&fl)[4],
+                                                 float (&r)[4], float (&nw)[4]) {
   const int a = threadIdx.x & 15;
-  factor_panel<0>(A, fl, a);
-  factor_panel<1>(A, fl, a);
-  factor_panel<2>(A, fl, a);
-  factor_panel<3>(A, fl, a);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) nw[m] = 0.f;
+  factor_panel<0>(A, fl, r, nw, a);
+  factor_panel<1>(A, fl, r, nw, a);
+  factor_panel<2>(A, fl, r, nw, a);
+  factor_panel<3>(A, fl, r, nw, a);
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int c = 1; c < 16; ++c) A[m][16 * m + c] = c > a ? 0.f : A[m][16 * m + c];
+}
+
+// The same from a rows-layout -E: the six trailing blocks are exchanged first.
+__device__ __forceinline__ void factor_rows16(float (&A)[4][64], const float (&fl)[4],
+                                              float (&r)[4], float (&nw)[4]) {
+  exchange_block<16>(A[1]);
+  exchange_block<16>(A[2]);
+  exchange_block<32>(A[2]);
+  exchange_block<16>(A[3]);
+  exchange_block<32>(A[3]);
+  exchange_block<48>(A[3]);
+  factor_exchanged(A, fl, r, nw);
+}
+
+// y = L^-T w from nw = -w (factor_rows16 / factor_exchanged).
+template <int J>
+__device__ __forceinline__ void backward_step_nw(const float (&A)[4][64], const float (&nw)[4],
+                                                 float (&y)[4], int a) {
+  constexpr int mj = J >> 4, lj = J & 15;
+  float p = 0.f;
+#pragma unroll
+  for (int m = mj; m < 4; ++m) p += A[m][J] * y[m];
+  const float yj = -(nw[mj] + sum16(p)) * A[mj][J];
+  y[mj] = a == lj ? yj : y[mj];
+}
+
+template <int... J>
+__device__ __forceinline__ void backward_steps_nw(const float (&A)[4][64], const float (&nw)[4],
+                                                  float (&y)[4], int a,
+                                                  std::integer_sequence<int, J...>) {
+  (backward_step_nw<63 - J>(A, nw, y, a), ...);
+}
+
+__device__ __forceinline__ void backward_rows16(const float (&A)[4][64], const float (&nw)[4],
+                                                float (&y)[4]) {
+  const int a = threadIdx.x & 15;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) y[m] = 0.f;
+  backward_steps_nw(A, nw, y, a, std::make_integer_sequence<int, 64>{});
 }
 
 // y = (L L^T)^-1 r for a factor from factor_rows16; r is consumed.
@@ -312,7 +367,10 @@ __device__ __forceinline__ void store_rows16(const float (&A)[4][64], float* __r
 #pragma unroll
     for (int q = 0; q < 4 * m + 4; ++q)
       if (q <= p)
-        lane[run_quad(m, q)] = f4{A[m][4 * q], A[m][4 * q + 1], A[m][4 * q + 2], A[m][4 * q + 3]};
+        // Non-temporal: the factors are read back only by the backward pass.
+        __builtin_nontemporal_store(
+            f4{A[m][4 * q], A[m][4 * q + 1], A[m][4 * q + 2], A[m][4 * q + 3]},
+            &lane[run_quad(m, q)]);
   }
 }
 
