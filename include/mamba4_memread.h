@@ -176,6 +176,75 @@ int m4mr_spd_solve_backward(const float* factors, const float* solution,
                             float* d_precision, float* d_rhs, void* stream);
 
 /*
+ * Mixer prologue: the memory read's inputs from the caller's projections.
+ * Replaces the preprocessing inside SelectiveMemoryMixer.__call__
+ * (lm/models/mamba4.py:183-237): with key_shift, position t of `keys` is
+ * the raw key of t - 1 (position 0: `previous` [B,H,D], or zero when
+ * previous is NULL), :183-195; keys and queries are unit-normalised,
+ * x * rsqrt(sum x^2 + 1e-6) (_unit, :37-39); beta = beta_max *
+ * sigmoid(beta_raw + beta_bias[h]) (:196-210); log_decay = -exp(a_log[h]) *
+ * softplus(dt_raw + dt_bias[h]) (:211-221); floor = floor_min +
+ * softplus(floor_raw) (:231-237).  key, query, keys, queries [B,T,H,D]
+ * (D a multiple of 4); beta_raw, dt_raw, beta, log_decay [B,T,H];
+ * beta_bias, dt_bias, a_log [H]; floor_raw, floor [H,D].  With key_shift and
+ * a non-NULL `shifted` [B,H,D], the raw key of position T-1 (the cache entry
+ * of the next call, :191-195) is written there.  beta_max and floor_min
+ * must be positive (the reference raises ValueError otherwise).
+ */
+int m4mr_prologue_forward(const float* key, const float* query, const float* beta_raw,
+                          const float* dt_raw, const float* beta_bias, const float* dt_bias,
+                          const float* a_log, const float* floor_raw, const float* previous,
+                          int B, int T, int H, int D, float beta_max, float floor_min,
+                          int key_shift, float* keys, float* queries, float* beta,
+                          float* log_decay, float* floor, float* shifted, void* stream);
+
+/* Bytes of the workspace m4mr_prologue_backward and m4mr_epilogue_backward
+ * need for their per-head partial sums. */
+size_t m4mr_mixer_workspace_bytes(int B, int T, int H);
+
+/*
+ * VJP of m4mr_prologue_forward (the gradients JAX autodiff takes through
+ * lm/models/mamba4.py:183-237).  Cotangents d_keys, d_queries, d_beta,
+ * d_log_decay, d_floor and (with key_shift, may be NULL) d_shifted; writes
+ * d_key, d_query [B,T,H,D], d_beta_raw, d_dt_raw [B,T,H], d_beta_bias,
+ * d_dt_bias, d_a_log [H], d_floor_raw [H,D] and, if non-NULL, d_previous
+ * [B,H,D] (zero when previous is NULL or without key_shift).  The per-head
+ * sums run in a fixed order: results are identical run to run.
+ */
+int m4mr_prologue_backward(const float* key, const float* query, const float* beta_raw,
+                           const float* dt_raw, const float* beta_bias, const float* dt_bias,
+                           const float* a_log, const float* floor_raw, const float* previous,
+                           int B, int T, int H, int D, float beta_max, int key_shift,
+                           const float* d_keys, const float* d_queries, const float* d_beta,
+                           const float* d_log_decay, const float* d_floor,
+                           const float* d_shifted, float* d_key, float* d_query,
+                           float* d_beta_raw, float* d_dt_raw, float* d_beta_bias,
+                           float* d_dt_bias, float* d_a_log, float* d_floor_raw,
+                           float* d_previous, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/*
+ * Mixer epilogue: out = read * sigmoid(1 - confidence_scale[h] *
+ * log1p(variance)) + skip[h] * value, the confidence gate and D-skip of
+ * SelectiveMemoryMixer.__call__ (lm/models/mamba4.py:266-273).  read, value,
+ * out [B,T,H,P] (P a multiple of 4); variance [B,T,H]; confidence_scale,
+ * skip [H].
+ */
+int m4mr_epilogue_forward(const float* read, const float* variance, const float* value,
+                          const float* confidence_scale, const float* skip, int B, int T, int H,
+                          int P, float* out, void* stream);
+
+/*
+ * VJP of m4mr_epilogue_forward: d_read, d_value [B,T,H,P], d_variance
+ * [B,T,H], d_confidence_scale, d_skip [H] (fixed-order per-head sums).
+ */
+int m4mr_epilogue_backward(const float* read, const float* variance, const float* value,
+                           const float* confidence_scale, const float* skip, int B, int T, int H,
+                           int P, const float* d_out, float* d_read, float* d_variance,
+                           float* d_value, float* d_confidence_scale, float* d_skip,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Kernel timing with HIP events recorded on the launch stream.  While
  * enabled, every kernel launch is bracketed by a pair of events.
  * m4mr_profile_read() waits for the recorded events and returns the total

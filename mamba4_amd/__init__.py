@@ -5,7 +5,8 @@ A drop-in for the reference's lm/kernels memory-read API
 ``selective_initial_state``, ``spd_solve``, ``SelectiveState``,
 ``SelectiveResult``),
 implemented by hand-written HIP kernels behind the C ABI in
-``include/mamba4_memread.h``.
+``include/mamba4_memread.h``, plus the caller's preprocessing and read gating
+(``memory_inputs``, ``gated_read``; lm/models/mamba4.py:183-237, 266-273).
 """
 
 from mamba4_amd.memory import (  # noqa: F401
@@ -19,12 +20,16 @@ from mamba4_amd.memory import (  # noqa: F401
     selective_initial_state,
     spd_solve,
 )
+from mamba4_amd.mixer import MemoryInputs, gated_read, memory_inputs  # noqa: F401
 
 __all__ = [
     "MEMORY_SOLVE",
+    "MemoryInputs",
     "SOLVERS",
     "SelectiveResult",
     "SelectiveState",
+    "gated_read",
+    "memory_inputs",
     "selective_decode",
     "selective_decode_",
     "selective_gaussian_memory",

@@ -38,6 +38,14 @@ SIGNATURES = {
     "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _P, _P, _P]),
     "m4mr_spd_solve": (_I, [_P, _P, _L, _I, _P, _P, _P]),
     "m4mr_spd_solve_backward": (_I, [_P, _P, _P, _L, _I, _P, _P, _P]),
+    "m4mr_prologue_forward": (_I, [_P] * 9 + [_I] * 4 + [ctypes.c_float] * 2 + [_I] + [_P] * 7),
+    "m4mr_mixer_workspace_bytes": (_S, [_I] * 3),
+    "m4mr_prologue_backward": (
+        _I,
+        [_P] * 9 + [_I] * 4 + [ctypes.c_float, _I] + [_P] * 6 + [_P] * 9 + [_P, _S, _P],
+    ),
+    "m4mr_epilogue_forward": (_I, [_P] * 5 + [_I] * 4 + [_P, _P]),
+    "m4mr_epilogue_backward": (_I, [_P] * 5 + [_I] * 4 + [_P] * 6 + [_P, _S, _P]),
     "m4mr_profile_enable": (None, [_I]),
     "m4mr_profile_reset": (None, []),
     "m4mr_profile_read": (

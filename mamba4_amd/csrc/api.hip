@@ -38,6 +38,23 @@ __global__ void bwd_grads_kernel(Dims, const float*, const float*, const float*,
                                  const float*, const float*, const float*, const float*, float*,
                                  float*, float*, float*, float*, float*);
 __global__ void floor_reduce_kernel(Dims, const float*, float*);
+__global__ void prologue_forward_kernel(const float*, const float*, const float*, const float*,
+                                        const float*, const float*, const float*, const float*,
+                                        const float*, int, int, int, int, float, float, int,
+                                        float*, float*, float*, float*, float*, float*);
+__global__ void prologue_backward_kernel(const float*, const float*, const float*, const float*,
+                                         const float*, const float*, const float*, const float*,
+                                         const float*, int, int, int, int, float, int,
+                                         const float*, const float*, const float*, const float*,
+                                         const float*, const float*, float*, float*, float*,
+                                         float*, float*, float*, float*);
+__global__ void epilogue_forward_kernel(const float*, const float*, const float*, const float*,
+                                        const float*, int, int, int, int, float*);
+__global__ void epilogue_backward_kernel(const float*, const float*, const float*, const float*,
+                                         const float*, int, int, int, int, const float*, float*,
+                                         float*, float*, float*);
+__global__ void head_sums_kernel(const float*, long, int, int, float*, float*, float*);
+__global__ void zero_kernel(float*, long);
 __global__ void spd_solve_kernel(const float*, const float*, long, int, float*, float*);
 __global__ void spd_backward_kernel(const float*, const float*, const float*, long, int, float*,
                                     float*);
@@ -52,7 +69,9 @@ thread_local std::string g_error;
 const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_factor", "fwd_read",
                                     "bwd_dy",         "factored_solve", "bwd_local", "bwd_scan",
                                     "bwd_grads",      "floor_reduce", "decode_step",
-                                    "spd_solve",      "spd_backward"};
+                                    "spd_solve",      "spd_backward", "prologue_forward",
+                                    "prologue_backward", "epilogue_forward",
+                                    "epilogue_backward", "head_sums"};
 
 struct ProfRecord {
   const char* name;
@@ -402,6 +421,180 @@ int m4mr_spd_solve_backward(const float* factors, const float* solution,
   return launch("spd_backward", st, [&] {
     hipLaunchKernelGGL(m4::spd_backward_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
                        factors, solution, d_solution, N, dim, d_precision, d_rhs);
+  });
+}
+
+// ---------------------------------------------------------------- mixer --
+
+namespace {
+
+constexpr int kMixRows = 16;  // token-heads per prologue/epilogue block
+
+bool bad_mixer_dims(int B, int T, int H, int width, std::string* why) {
+  if (B <= 0 || T <= 0 || H <= 0) {
+    *why = "B, T and H must be positive";
+    return true;
+  }
+  if (width <= 0 || width % 4 != 0 || width > 4096) {
+    *why = "row width must be a positive multiple of 4 (at most 4096)";
+    return true;
+  }
+  if ((double)B * T * H * width > 9.0e18 || (double)B * T * H > 2.0e12) {
+    *why = "problem too large";
+    return true;
+  }
+  return false;
+}
+
+long mixer_blocks(int B, int T, int H) {
+  return ((long)B * T * H + kMixRows - 1) / kMixRows;
+}
+
+}  // namespace
+
+size_t m4mr_mixer_workspace_bytes(int B, int T, int H) {
+  if (B <= 0 || T <= 0 || H <= 0) return 0;
+  return (size_t)mixer_blocks(B, T, H) * H * 3 * sizeof(float);
+}
+
+int m4mr_prologue_forward(const float* key, const float* query, const float* beta_raw,
+                          const float* dt_raw, const float* beta_bias, const float* dt_bias,
+                          const float* a_log, const float* floor_raw, const float* previous,
+                          int B, int T, int H, int D, float beta_max, float floor_min,
+                          int key_shift, float* keys, float* queries, float* beta,
+                          float* log_decay, float* floor, float* shifted, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_mixer_dims(B, T, H, D, &why)) return fail(M4MR_EINVAL, "m4mr_prologue_forward: " + why);
+  if (!(beta_max > 0.f)) return fail(M4MR_EINVAL, "memory_beta_max must be positive");
+  if (!(floor_min > 0.f))
+    return fail(M4MR_EINVAL, "Selective floor must be positive and above its minimum");
+  const void* need[] = {key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
+                        keys, queries, beta, log_decay, floor};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_prologue_forward: a required pointer is NULL");
+  const void* vec[] = {key, query, previous, keys, queries, shifted};
+  for (const void* p : vec)
+    if (p && misaligned(p))
+      return fail(M4MR_EINVAL, "m4mr_prologue_forward: rows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return launch("prologue_forward", st, [&] {
+    hipLaunchKernelGGL(m4::prologue_forward_kernel, dim3((unsigned)mixer_blocks(B, T, H)),
+                       dim3(256), 0, st, key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log,
+                       floor_raw, key_shift ? previous : nullptr, B, T, H, D, beta_max,
+                       floor_min, key_shift ? 1 : 0, keys, queries, beta, log_decay, floor,
+                       key_shift ? shifted : nullptr);
+  });
+}
+
+int m4mr_prologue_backward(const float* key, const float* query, const float* beta_raw,
+                           const float* dt_raw, const float* beta_bias, const float* dt_bias,
+                           const float* a_log, const float* floor_raw, const float* previous,
+                           int B, int T, int H, int D, float beta_max, int key_shift,
+                           const float* d_keys, const float* d_queries, const float* d_beta,
+                           const float* d_log_decay, const float* d_floor,
+                           const float* d_shifted, float* d_key, float* d_query,
+                           float* d_beta_raw, float* d_dt_raw, float* d_beta_bias,
+                           float* d_dt_bias, float* d_a_log, float* d_floor_raw,
+                           float* d_previous, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_mixer_dims(B, T, H, D, &why))
+    return fail(M4MR_EINVAL, "m4mr_prologue_backward: " + why);
+  const void* need[] = {key,         query,     beta_raw,   dt_raw,     beta_bias, dt_bias,
+                        a_log,       floor_raw, d_keys,     d_queries,  d_beta,    d_log_decay,
+                        d_floor,     d_key,     d_query,    d_beta_raw, d_dt_raw,  d_beta_bias,
+                        d_dt_bias,   d_a_log,   d_floor_raw, workspace};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_prologue_backward: a required pointer is NULL");
+  if (workspace_bytes < m4mr_mixer_workspace_bytes(B, T, H))
+    return fail(M4MR_EINVAL, "m4mr_prologue_backward: workspace too small (need " +
+                                 std::to_string(m4mr_mixer_workspace_bytes(B, T, H)) + " bytes)");
+  const void* vec[] = {key, query, previous, d_keys, d_queries, d_shifted, d_key, d_query,
+                       d_previous};
+  for (const void* p : vec)
+    if (p && misaligned(p))
+      return fail(M4MR_EINVAL, "m4mr_prologue_backward: rows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const long blocks = mixer_blocks(B, T, H);
+  const bool shift = key_shift != 0;
+  int rc = launch("prologue_backward", st, [&] {
+    hipLaunchKernelGGL(m4::prologue_backward_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
+                       shift ? previous : nullptr, B, T, H, D, beta_max, shift ? 1 : 0, d_keys,
+                       d_queries, d_beta, d_log_decay, d_floor, shift ? d_shifted : nullptr,
+                       d_key, d_query, d_beta_raw, d_dt_raw, d_floor_raw,
+                       shift ? d_previous : nullptr, part);
+  });
+  if (rc) return rc;
+  if (d_previous && !shift) {
+    // Without the shift nothing reads `previous`: its cotangent is zero (a
+    // fill kernel rather than a memset, so the call can be graph-captured).
+    rc = launch("prologue_backward", st, [&] {
+      hipLaunchKernelGGL(m4::zero_kernel, dim3((unsigned)(((long)B * H * D + 255) / 256)),
+                         dim3(256), 0, st, d_previous, (long)B * H * D);
+    });
+    if (rc) return rc;
+  }
+  return launch("head_sums", st, [&] {
+    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 3), dim3(256), 0, st, part, blocks, H, 3,
+                       d_beta_bias, d_dt_bias, d_a_log);
+  });
+}
+
+int m4mr_epilogue_forward(const float* read, const float* variance, const float* value,
+                          const float* confidence_scale, const float* skip, int B, int T, int H,
+                          int P, float* out, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_mixer_dims(B, T, H, P, &why)) return fail(M4MR_EINVAL, "m4mr_epilogue_forward: " + why);
+  const void* need[] = {read, variance, value, confidence_scale, skip, out};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_epilogue_forward: a required pointer is NULL");
+  if (misaligned(read) || misaligned(value) || misaligned(out))
+    return fail(M4MR_EINVAL, "m4mr_epilogue_forward: rows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return launch("epilogue_forward", st, [&] {
+    hipLaunchKernelGGL(m4::epilogue_forward_kernel, dim3((unsigned)mixer_blocks(B, T, H)),
+                       dim3(256), 0, st, read, variance, value, confidence_scale, skip, B, T, H,
+                       P, out);
+  });
+}
+
+int m4mr_epilogue_backward(const float* read, const float* variance, const float* value,
+                           const float* confidence_scale, const float* skip, int B, int T, int H,
+                           int P, const float* d_out, float* d_read, float* d_variance,
+                           float* d_value, float* d_confidence_scale, float* d_skip,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_mixer_dims(B, T, H, P, &why))
+    return fail(M4MR_EINVAL, "m4mr_epilogue_backward: " + why);
+  const void* need[] = {read,     variance, value,   confidence_scale,   skip,   d_out, d_read,
+                        d_variance, d_value, d_confidence_scale, d_skip, workspace};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_epilogue_backward: a required pointer is NULL");
+  if (workspace_bytes < m4mr_mixer_workspace_bytes(B, T, H))
+    return fail(M4MR_EINVAL, "m4mr_epilogue_backward: workspace too small (need " +
+                                 std::to_string(m4mr_mixer_workspace_bytes(B, T, H)) + " bytes)");
+  const void* vec[] = {read, value, d_out, d_read, d_value};
+  for (const void* p : vec)
+    if (misaligned(p))
+      return fail(M4MR_EINVAL, "m4mr_epilogue_backward: rows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const long blocks = mixer_blocks(B, T, H);
+  int rc = launch("epilogue_backward", st, [&] {
+    hipLaunchKernelGGL(m4::epilogue_backward_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       read, variance, value, confidence_scale, skip, B, T, H, P, d_out, d_read,
+                       d_variance, d_value, part);
+  });
+  if (rc) return rc;
+  return launch("head_sums", st, [&] {
+    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 2), dim3(256), 0, st, part, blocks, H, 2,
+                       d_confidence_scale, d_skip, nullptr);
   });
 }
 
