@@ -344,7 +344,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_grads_kernel, dim3(seqs), dim3(256), kGradsLdsBytes, st, d, keys,
+    hipLaunchKernelGGL(m4::bwd_grads_kernel, dim3(seqs), dim3(512), kGradsLdsBytes, st, d, keys,
                        values, beta, log_decay, solved, ws.z, d_output, d_variance,
                        start_evidence, start_cross, ws.end_s, ws.end_c, d_keys, d_values,
                        d_queries, d_beta, d_log_decay, ws.floor_part);

@@ -54,7 +54,7 @@ __device__ __forceinline__ TokenRows rows_of(const float* base, const Dims& d, c
 // after this chunk's are in LDS, its queries once this chunk's variance is
 // done, its values once this chunk's values are in LDS (at most five tiles
 // in flight per thread, keeping two blocks per CU).
-__global__ __launch_bounds__(256) void fwd_read_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_read_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ values,
     const float* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ solved,
@@ -217,7 +217,14 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void bwd_grads_kernel(
+// Eight waves per chunk: wave w8 computes the 16-row strip ws = w8 % 4 of
+// every product, columns of half hf = w8 / 4 (two of the four 16-column
+// blocks; tile_mma_half), so each SIMD runs two waves of one chunk and one
+// wave's epilogue, LDS staging and barriers overlap the other's MFMAs.  Row
+// sums that span both halves meet in LDS and are added in half order.
+constexpr int GRADS_THREADS = 512;
+
+__global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ solved, const float* __restrict__ z,
@@ -237,98 +244,102 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   float* M2 = M1 + TILE;  // W * (gv - gz), then H_end
   __shared__ ChunkScalars cs;
   __shared__ float colpart[4][64];
+  __shared__ float rowpart[2][64], quadpart[2][64], startpart[2][64];
   __shared__ float rowE[64], colD2[64], quad[64], startdot[64];
-  __shared__ float red[256];
-  __shared__ f4 fpart[4][16];
+  __shared__ float red[GRADS_THREADS];
+  __shared__ f4 fpart[8][16];
   const SeqIndex si = seq_index(d);
-  const int w = threadIdx.x >> 6, l = lane_id(), c4 = 4 * (l & 15);
+  const int w8 = threadIdx.x >> 6, ws = w8 & 3, hf = w8 >> 2, l = lane_id();
+  const int r = l & 15, c4 = 4 * r;
   const int kt = k_terms(si.len);
-  // d_variance of this thread's tile-fetch rows (threadIdx/16 + 16j).
-  float dvar[4];
+  // d_variance of this thread's tile-fetch rows (threadIdx/16 + 32j).
+  float dvar[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = (threadIdx.x >> 4) + 16 * j;
+  for (int j = 0; j < 2; ++j) {
+    const int t = (threadIdx.x >> 4) + 32 * j;
     dvar[j] = t < si.len ? d_variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] : 0.f;
   }
 
   {
-    TileRegs r[5];
-    r[0].fetch_rows(si.len, rows_of(keys, d, si));
-    r[1].fetch_rows(si.len, rows_of(values, d, si));
-    r[2].fetch_rows(si.len, rows_of(solved, d, si));
-    r[3].fetch_rows(si.len, rows_of(z, d, si));
-    r[4].fetch_rows(si.len, rows_of(d_output, d, si));
-    r[0].store(Kt);
-    r[1].store(Vt);
-    r[2].store(Yt);
-    r[3].store(Zt);
-    r[4].store(Dt);
+    TileRegs2 rt[5];
+    rt[0].fetch_rows(si.len, rows_of(keys, d, si));
+    rt[1].fetch_rows(si.len, rows_of(values, d, si));
+    rt[2].fetch_rows(si.len, rows_of(solved, d, si));
+    rt[3].fetch_rows(si.len, rows_of(z, d, si));
+    rt[4].fetch_rows(si.len, rows_of(d_output, d, si));
+    rt[0].store(Kt);
+    rt[1].store(Vt);
+    rt[2].store(Yt);
+    rt[3].store(Zt);
+    rt[4].store(Dt);
   }
   load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
   // The end-state cotangents of phase 3 load while phases 1 and 2 run.
-  TileRegs rg, rh;
+  TileRegs2 rg, rh;
   rg.fetch_matrix(end_s + si.seq * 4096);
   rh.fetch_matrix(end_c + si.seq * 4096);
   __syncthreads();
 
   // Phase 1: gy = Y K^T, gz = Z K^T, gv = dOut V^T and their weighted mixes.
   {
-    f4 gy[4], gz[4], gv[4];
-    zero4(gy);
-    zero4(gz);
-    zero4(gv);
-    tile_mma<false, true>(gy, Yt, Kt, 64, w);
-    tile_mma<false, true>(gz, Zt, Kt, 64, w);
-    tile_mma<false, true>(gv, Dt, Vt, 64, w);
+    f4 gy[2], gz[2], gv[2];
+    zero2(gy);
+    zero2(gz);
+    zero2(gv);
+    tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf);
+    tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf);
+    tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf);
     float rsum[4] = {0.f, 0.f, 0.f, 0.f};
-    float csum[4] = {0.f, 0.f, 0.f, 0.f};
+    float csum[2] = {0.f, 0.f};
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int t = acc_row(w, q), s = acc_col<false>(jb);
+        const int t = acc_row(ws, q), s = 16 * (2 * hf + j) + r;
         float my = 0.f, mz = 0.f, d2 = 0.f;
         if (s <= t && t < si.len) {
           const float dec = expf(cs.prefix[t] - cs.prefix[s]);
-          const float mix = gv[jb][q] - gz[jb][q];
-          d2 = dec * gy[jb][q] * mix;
-          my = dec * cs.beta[s] * gy[jb][q];
+          const float mix = gv[j][q] - gz[j][q];
+          d2 = dec * gy[j][q] * mix;
+          my = dec * cs.beta[s] * gy[j][q];
           mz = dec * cs.beta[s] * mix;
         }
         M1[t * LDT + s] = my;
         M2[t * LDT + s] = mz;
         rsum[q] += cs.beta[s] * d2;
-        csum[jb] += d2;
+        csum[j] += d2;
       }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float v = row16_sum(rsum[q]);
-      if ((l & 15) == 0) rowE[acc_row(w, q)] = v;
+      if (r == 0) rowpart[hf][acc_row(ws, q)] = v;
     }
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const float v = group4_sum(csum[jb]);
-      if (l < 16) colpart[w][acc_col<false>(jb)] = v;
+    for (int j = 0; j < 2; ++j) {
+      const float v = group4_sum(csum[j]);
+      if (l < 16) colpart[ws][16 * (2 * hf + j) + r] = v;
     }
   }
   __syncthreads();
   if (threadIdx.x < 64) {
     const int s = threadIdx.x;
     colD2[s] = colpart[0][s] + colpart[1][s] + colpart[2][s] + colpart[3][s];
+    rowE[s] = rowpart[0][s] + rowpart[1][s];
   }
 
-  // Phase 2: within-chunk key and value gradients (rows s, columns 4r..4r+3).
-  f4 dk[4], dv[4];
-  zero4(dk);
-  zero4(dv);
+  // Phase 2: within-chunk key and value gradients (rows s, QUAD columns
+  // 4r + 2hf + j).
+  f4 dk[2], dv[2];
+  zero2(dk);
+  zero2(dv);
   {
-    f4 tmp[4];
-    zero4(tmp);
-    tile_mma<true, false>(dk, M2, Yt, kt, w);   // sum_t W(gv-gz)[t][s] y_t
-    tile_mma<true, false>(tmp, M1, Zt, kt, w);  // sum_t W gy[t][s] z_t
-    tile_mma<true, false>(dv, M1, Dt, kt, w);   // sum_t W gy[t][s] dout_t
+    f4 tmp[2];
+    zero2(tmp);
+    tile_mma_half<true, false>(dk, M2, Yt, kt, ws, hf);   // sum_t W(gv-gz)[t][s] y_t
+    tile_mma_half<true, false>(tmp, M1, Zt, kt, ws, hf);  // sum_t W gy[t][s] z_t
+    tile_mma_half<true, false>(dv, M1, Dt, kt, ws, hf);   // sum_t W gy[t][s] dout_t
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) dk[jb] -= tmp[jb];
+    for (int j = 0; j < 2; ++j) dk[j] -= tmp[j];
   }
   __syncthreads();
 
@@ -339,11 +350,11 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   rh.store(M2);
   // The start states of phase 4 load while phase 3 runs.
   const long bh = si.seq / d.NC;
-  TileRegs rs, rc;
+  TileRegs2 rs, rc;
   rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
   rc.fetch_matrix(start_c + si.seq * 4096);
   __syncthreads();
-  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+  for (int e = threadIdx.x; e < 64 * 64; e += GRADS_THREADS) {
     const int i = e >> 6, j = e & 63;
     if (i < j) {
       const float v = M1[i * LDT + j] + M1[j * LDT + i];
@@ -355,37 +366,39 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   }
   __syncthreads();
   {
-    f4 gk[4], hk[4], hv[4];
-    zero4(gk);
-    zero4(hk);
-    zero4(hv);
-    tile_mma<false, false>(gk, Kt, M1, 64, w);       // (G + G^T) k_s
-    tile_mma<false, true, true>(hk, Kt, M2, 64, w);  // H k_s
-    tile_mma<false, false>(hv, Vt, M2, 64, w);       // H^T v_s
+    f4 gk[2], hk[2], hv[2];
+    zero2(gk);
+    zero2(hk);
+    zero2(hv);
+    tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // (G + G^T) k_s
+    tile_mma_half<false, true, true>(hk, Kt, M2, 64, ws, hf);  // H k_s
+    tile_mma_half<false, false>(hv, Vt, M2, 64, ws, hf);       // H^T v_s
     float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int s = acc_row(w, q);
-      const f4 kr = *reinterpret_cast<const f4*>(Kt + s * LDT + c4);
-      const f4 vr = *reinterpret_cast<const f4*>(Vt + s * LDT + c4);
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) qpart[q] += 0.5f * kr[jb] * gk[jb][q] + vr[jb] * hk[jb][q];
+      const int s = acc_row(ws, q);
+      const float2 kr = *reinterpret_cast<const float2*>(Kt + s * LDT + c4 + 2 * hf);
+      const float2 vr = *reinterpret_cast<const float2*>(Vt + s * LDT + c4 + 2 * hf);
+      qpart[q] += 0.5f * kr.x * gk[0][q] + vr.x * hk[0][q];
+      qpart[q] += 0.5f * kr.y * gk[1][q] + vr.y * hk[1][q];
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int s = acc_row(w, q);
+      const int s = acc_row(ws, q);
       const float qv = row16_sum(qpart[q]);
-      if ((l & 15) == 0) quad[s] = qv;
+      if (r == 0) quadpart[hf][s] = qv;
       if (s < si.len) {
         const float tl = cs.tail[s];
         const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
-        *reinterpret_cast<f4*>(d_keys + th * 64 + c4) =
-            quad_row(dk, q) + tl * (quad_row(gk, q) + quad_row(hv, q));
-        *reinterpret_cast<f4*>(d_values + th * 64 + c4) = quad_row(dv, q) + tl * quad_row(hk, q);
+        *reinterpret_cast<float2*>(d_keys + th * 64 + c4 + 2 * hf) =
+            float2{dk[0][q] + tl * (gk[0][q] + hv[0][q]), dk[1][q] + tl * (gk[1][q] + hv[1][q])};
+        *reinterpret_cast<float2*>(d_values + th * 64 + c4 + 2 * hf) =
+            float2{dv[0][q] + tl * hk[0][q], dv[1][q] + tl * hk[1][q]};
       }
     }
   }
   __syncthreads();
+  if (threadIdx.x < 64) quad[threadIdx.x] = quadpart[0][threadIdx.x] + quadpart[1][threadIdx.x];
 
   // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>
   // (<G, S0> = <G + G^T, S0> / 2 since S0 is symmetric).  The chunk's start
@@ -395,38 +408,41 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
   __syncthreads();
   {
     float part = 0.f;
-    for (int e = threadIdx.x; e < 4096; e += 256) {
+    for (int e = threadIdx.x; e < 4096; e += GRADS_THREADS) {
       const int row = e >> 6, col = e & 63;
       part += 0.5f * M1[row * LDT + col] * Kt[row * LDT + col] +
               M2[row * LDT + col] * Vt[row * LDT + col];
     }
     red[threadIdx.x] = part;
-    f4 ys[4], dc[4];
-    zero4(ys);
-    zero4(dc);
-    tile_mma<false, false>(ys, Yt, Kt, 64, w);  // y_t^T S0
-    tile_mma<false, false>(dc, Dt, Vt, 64, w);  // dout_t^T C0
+    f4 ys[2], dc[2];
+    zero2(ys);
+    zero2(dc);
+    tile_mma_half<false, false>(ys, Yt, Kt, 64, ws, hf);  // y_t^T S0
+    tile_mma_half<false, false>(dc, Dt, Vt, 64, ws, hf);  // dout_t^T C0
     float sp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(w, q);
-      const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
-      const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) sp[q] += dc[jb][q] * yr[jb] - ys[jb][q] * zr[jb];
+      const int t = acc_row(ws, q);
+      const float2 yr = *reinterpret_cast<const float2*>(Yt + t * LDT + c4 + 2 * hf);
+      const float2 zr = *reinterpret_cast<const float2*>(Zt + t * LDT + c4 + 2 * hf);
+      sp[q] += dc[0][q] * yr.x - ys[0][q] * zr.x;
+      sp[q] += dc[1][q] * yr.y - ys[1][q] * zr.y;
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(w, q);
       const float v = row16_sum(sp[q]);
-      if ((l & 15) == 0) startdot[t] = expf(cs.prefix[t]) * v;
+      if (r == 0) startpart[hf][acc_row(ws, q)] = v;
     }
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    float v = red[threadIdx.x] + red[threadIdx.x + 64] + red[threadIdx.x + 128] + red[threadIdx.x + 192];
+    const int t = threadIdx.x;
+    startdot[t] = expf(cs.prefix[t]) * (startpart[0][t] + startpart[1][t]);
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < GRADS_THREADS / 64; ++k) v += red[t + 64 * k];
     v = group4_sum(row16_sum(v));
-    red[threadIdx.x] = v;  // every lane of wave 0 holds the total
+    red[t] = v;  // every lane of wave 0 holds the total
   }
   __syncthreads();
 
@@ -456,14 +472,14 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
     }
   }
   // Queries, d q_t = z_t + dvar_t y_t, in the tile-fetch layout (rows
-  // r0 + 16j, columns q4..q4+3), and the floor partial -sum_t z_t * y_t:
-  // per thread over its four rows, then over the lanes and waves holding the
+  // r0 + 32j, columns c4..c4+3), and the floor partial -sum_t z_t * y_t:
+  // per thread over its two rows, then over the lanes and waves holding the
   // same columns, in a fixed order.
   {
     f4 fsum = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = (threadIdx.x >> 4) + 16 * j;
+    for (int j = 0; j < 2; ++j) {
+      const int t = (threadIdx.x >> 4) + 32 * j;
       const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
       const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
       if (t < si.len) {
@@ -474,11 +490,12 @@ __global__ __launch_bounds__(256) void bwd_grads_kernel(
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) fsum[i] = group4_sum(fsum[i]);
-    if (l < 16) fpart[w][l] = fsum;
+    if (l < 16) fpart[w8][l] = fsum;
     __syncthreads();
     if (threadIdx.x < 16) {
-      const f4 total = fpart[0][threadIdx.x] + fpart[1][threadIdx.x] + fpart[2][threadIdx.x] +
-                       fpart[3][threadIdx.x];
+      f4 total = fpart[0][threadIdx.x];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) total += fpart[k][threadIdx.x];
       *reinterpret_cast<f4*>(floor_part + si.seq * 64 + 4 * threadIdx.x) = total;
     }
   }

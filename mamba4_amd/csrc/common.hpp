@@ -185,6 +185,68 @@ __device__ __forceinline__ f4 quad_row(const f4 acc[4], int q) {
   return f4{acc[0][q], acc[1][q], acc[2][q], acc[3][q]};
 }
 
+// Half of a 64x64 tile product for one of two waves sharing a 16-row strip:
+// acc[j] is the 16-column block jb = 2 hf + j of tile_mma's result (same
+// operand conventions, same accumulator layout per block).  A QUAD block jb
+// holds columns 4r + jb, so a wave's two blocks are columns 4r + 2hf, +1.
+template <bool TA, bool TB, bool QUAD>
+__device__ __forceinline__ void mma_block_half(f4 acc[2], const float* A, const float* B, int k0,
+                                               int w, int hf) {
+  const int l = lane_id(), r = l & 15, kk = k0 + 4 * (l >> 4);
+  f4 a;
+  if (TA) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = A[(kk + e) * LDT + 16 * w + r];
+  } else {
+    a = *reinterpret_cast<const f4*>(A + (16 * w + r) * LDT + kk);
+  }
+  if (TB) {
+    f4 b[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int jb = 2 * hf + j, col = QUAD ? 4 * r + jb : 16 * jb + r;
+      b[j] = *reinterpret_cast<const f4*>(B + col * LDT + kk);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float b[2];
+      if (QUAD) {
+        const float2 v = *reinterpret_cast<const float2*>(B + (kk + e) * LDT + 4 * r + 2 * hf);
+        b[0] = v.x;
+        b[1] = v.y;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) b[j] = B[(kk + e) * LDT + 16 * (2 * hf + j) + r];
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j], acc[j], 0, 0, 0);
+    }
+  }
+}
+
+template <bool TA, bool TB, bool QUAD = !TB>
+__device__ __forceinline__ void tile_mma_half(f4 acc[2], const float* A, const float* B, int K,
+                                              int w, int hf) {
+  if (K == 64) {
+#pragma unroll
+    for (int k0 = 0; k0 < 64; k0 += 16) mma_block_half<TA, TB, QUAD>(acc, A, B, k0, w, hf);
+  } else {
+    for (int k0 = 0; k0 < K; k0 += 16) mma_block_half<TA, TB, QUAD>(acc, A, B, k0, w, hf);
+  }
+}
+
+__device__ __forceinline__ void zero2(f4 acc[2]) {
+  acc[0] = f4{0.f, 0.f, 0.f, 0.f};
+  acc[1] = f4{0.f, 0.f, 0.f, 0.f};
+}
+
 // Kernels built on these tiles run 256 threads (4 waves).
 constexpr int BLOCK = 256;
 
@@ -218,6 +280,34 @@ struct TileRegs {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(tile + (r0 + 16 * j) * LDT + q) = v[j];
+  }
+};
+
+// TileRegs for a 512-thread block: thread i holds column quad i%16 of rows
+// i/16 + 32j (j = 0, 1).
+struct TileRegs2 {
+  f4 v[2];
+
+  template <typename RowPtr>
+  __device__ __forceinline__ void fetch_rows(int rows, RowPtr row) {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = r0 + 32 * j;
+      v[j] = r < rows ? *reinterpret_cast<const f4*>(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  __device__ __forceinline__ void fetch_matrix(const float* src) {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) v[j] = *reinterpret_cast<const f4*>(src + (r0 + 32 * j) * 64 + q);
+  }
+
+  __device__ __forceinline__ void store(float* tile) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) *reinterpret_cast<f4*>(tile + (r0 + 32 * j) * LDT + q) = v[j];
   }
 };
 
