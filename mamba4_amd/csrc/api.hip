@@ -351,7 +351,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   return launch("floor_reduce", st, [&] {
-    hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H), dim3(256), 0, st, d, ws.floor_part,
+    hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H * 16), dim3(256), 0, st, d, ws.floor_part,
                        d_floor);
   });
 }

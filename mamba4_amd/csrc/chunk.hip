@@ -501,27 +501,27 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   }
 }
 
-// d floor[h][c] = sum_{b, n} floor_part[(b*H + h)*NC + n][c] in a fixed
-// order: thread (q, c4) sums entries e = q, q+16, ... of the flattened
-// (b, n) index as float4 columns 4c4..4c4+3, then the 16 partials are added
-// in q order.  Deterministic run to run.
+// d floor[h][4c4 .. 4c4+3] = sum over (b, n) of floor_part[(b*H + h)*NC + n]
+// in a fixed order: block (h, c4) of 256 threads, thread i sums entries
+// e = i, i + 256, ... of the flattened (b, n) index, then a fixed tree adds
+// the 256 partials.  Deterministic run to run.
 __global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* __restrict__ part,
                                                           float* __restrict__ d_floor) {
-  const int h = blockIdx.x, q = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+  const int h = blockIdx.x >> 4, c4 = blockIdx.x & 15;
   const int entries = d.B * d.NC;
-  __shared__ f4 partial[16][16];
+  __shared__ f4 partial[256];
   f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-  for (int e = q; e < entries; e += 16) {
+  for (int e = threadIdx.x; e < entries; e += 256) {
     const int b = e / d.NC, n = e % d.NC;
     acc += *reinterpret_cast<const f4*>(part + (((long)b * d.H + h) * d.NC + n) * 64 + 4 * c4);
   }
-  partial[q][c4] = acc;
+  partial[threadIdx.x] = acc;
   __syncthreads();
-  if (threadIdx.x < 16) {
-    f4 total = partial[0][threadIdx.x];
-    for (int k = 1; k < 16; ++k) total += partial[k][threadIdx.x];
-    *reinterpret_cast<f4*>(d_floor + h * 64 + 4 * threadIdx.x) = total;
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) partial[threadIdx.x] += partial[threadIdx.x + w];
+    __syncthreads();
   }
+  if (threadIdx.x == 0) *reinterpret_cast<f4*>(d_floor + h * 64 + 4 * c4) = partial[0];
 }
 
 }  // namespace m4
