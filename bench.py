@@ -157,7 +157,7 @@ class Problem:
         ]
         self.grads = [torch.empty_like(t) for t in self.inputs]
         self.d_init = [torch.empty(B, H, 64, 64, **f32), torch.empty(B, H, 64, 64, **f32)]
-        self.ws_bytes = self.lib.m4mr_backward_workspace_bytes(B, T, H, chunk)
+        self.ws_bytes = self.lib.m4mr_backward_workspace_bytes(B, T, H, 64, chunk)
         self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
         self.stream = torch.cuda.current_stream().cuda_stream
 
@@ -165,7 +165,7 @@ class Problem:
         p = [t.data_ptr() for t in self.inputs]
         o = [t.data_ptr() for t in self.fwd_out]
         self.check(
-            self.lib.m4mr_forward(*p, None, None, self.B, self.T, self.H, self.chunk, *o,
+            self.lib.m4mr_forward(*p, None, None, self.B, self.T, self.H, 64, self.chunk, *o,
                                   self.stream)
         )
 
@@ -174,7 +174,7 @@ class Problem:
         o = self.fwd_out
         self.check(
             self.lib.m4mr_backward(
-                *p, self.B, self.T, self.H, self.chunk, o[4].data_ptr(), o[5].data_ptr(),
+                *p, self.B, self.T, self.H, 64, self.chunk, o[4].data_ptr(), o[5].data_ptr(),
                 o[6].data_ptr(), o[7].data_ptr(), self.d_output.data_ptr(),
                 self.d_variance.data_ptr(), None, None, *(g.data_ptr() for g in self.grads),
                 *(g.data_ptr() for g in self.d_init), self.workspace.data_ptr(), self.ws_bytes,
@@ -223,7 +223,7 @@ class Decode:
             self.check(
                 self.lib.m4mr_forward(
                     k.data_ptr(), v.data_ptr(), q.data_ptr(), beta.data_ptr(),
-                    log_decay.data_ptr(), self.floor.data_ptr(), None, None, R, T, H, 64,
+                    log_decay.data_ptr(), self.floor.data_ptr(), None, None, R, T, H, 64, 64,
                     scratch[0].data_ptr(), scratch[1].data_ptr(),
                     self.evidence[first:first + R].data_ptr(),
                     self.cross[first:first + R].data_ptr(),
@@ -264,7 +264,7 @@ class Decode:
             self.lib.m4mr_decode_step(
                 self.evidence.data_ptr(), self.cross.data_ptr(), k.data_ptr(), v.data_ptr(),
                 q.data_ptr(), beta.data_ptr(), log_decay.data_ptr(), self.floor.data_ptr(),
-                DECODE_BATCH * DECODE_HEADS, DECODE_HEADS, self.output.data_ptr(),
+                DECODE_BATCH * DECODE_HEADS, DECODE_HEADS, 64, self.output.data_ptr(),
                 self.variance.data_ptr(), self.stream,
             )
         )

@@ -9,10 +9,12 @@
  * reentrant; calls on one stream run in order.
  *
  * Shapes: B batch, T tokens, H heads, key width D = 64 (M4MR_KEY_DIM),
- * value width P = 64 (M4MR_VALUE_DIM), chunk c in [1, 64],
- * NC = ceil(T / c) chunks.  Callers with narrower keys or values pad them
- * with zeros (and the floor with ones); the padded coordinates then solve
- * to zero and read nothing, as in lm/kernels/mamba4_fused.py:292-297.
+ * value width P = value_dim, 64 (M4MR_VALUE_DIM) or 128 (M4MR_MAX_VALUE_DIM,
+ * the reference's trained memory_head_dim, lm/configs/mamba4-60m.json), chunk
+ * c in [1, 64], NC = ceil(T / c) chunks.  Callers with narrower keys or
+ * values pad them with zeros (and the floor with ones); the padded
+ * coordinates then solve to zero and read nothing, as in
+ * lm/kernels/mamba4_fused.py:292-297.
  *
  * Return value: 0 on success, M4MR_EINVAL for a bad argument (nothing is
  * launched), M4MR_EHIP for a HIP launch error.  m4mr_last_error() returns
@@ -31,6 +33,7 @@ extern "C" {
 
 #define M4MR_KEY_DIM 64
 #define M4MR_VALUE_DIM 64
+#define M4MR_MAX_VALUE_DIM 128
 #define M4MR_MAX_CHUNK 64
 /* Stored lower factor per token-head, 2176 floats: the lower triangle in
  * 16-byte column quads.  Row i = a + 16m (a < 16) holds quads 0..i/4; for
@@ -80,7 +83,7 @@ const char* m4mr_last_error(void);
 int m4mr_forward(const float* keys, const float* values, const float* queries,
                  const float* beta, const float* log_decay, const float* floor,
                  const float* init_evidence, const float* init_cross,
-                 int B, int T, int H, int chunk,
+                 int B, int T, int H, int value_dim, int chunk,
                  float* output, float* variance,
                  float* final_evidence, float* final_cross,
                  float* solved, float* factors,
@@ -91,7 +94,7 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts);
 
 /* Bytes of device workspace m4mr_backward needs for these sizes. */
-size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk);
+size_t m4mr_backward_workspace_bytes(int B, int T, int H, int value_dim, int chunk);
 
 /*
  * Backward of m4mr_forward: the VJP for every input and the initial state.
@@ -110,12 +113,12 @@ size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk);
  *          d_init_cross [B,H,P,D].  The evidence cotangents are the
  *          symmetric form -(z y^T + y z^T)/2 of spd_solve's VJP
  *          (lm/kernels/mamba4.py:208-215).
- * workspace at least m4mr_backward_workspace_bytes(B, T, H, chunk) bytes,
+ * workspace at least m4mr_backward_workspace_bytes(B, T, H, value_dim, chunk) bytes,
  *          256-byte aligned.
  */
 int m4mr_backward(const float* keys, const float* values, const float* queries,
                   const float* beta, const float* log_decay, const float* floor,
-                  int B, int T, int H, int chunk,
+                  int B, int T, int H, int value_dim, int chunk,
                   const float* solved, const float* factors,
                   const float* start_evidence, const float* start_cross,
                   const float* d_output, const float* d_variance,
@@ -148,7 +151,7 @@ int m4mr_factored_solve(const float* factors, const float* rhs, float* z,
 int m4mr_decode_step(float* evidence, float* cross,
                      const float* key, const float* value, const float* query,
                      const float* beta, const float* log_decay, const float* floor,
-                     long N, int H,
+                     long N, int H, int value_dim,
                      float* output, float* variance, void* stream);
 
 /*

@@ -17,6 +17,7 @@ EHIP = 2
 FACTOR_FLOATS = 2176
 KEY_DIM = 64
 VALUE_DIM = 64
+MAX_VALUE_DIM = 128
 MAX_CHUNK = 64
 
 _P = ctypes.c_void_p
@@ -27,15 +28,15 @@ _S = ctypes.c_size_t
 SIGNATURES = {
     "m4mr_version": (ctypes.c_char_p, []),
     "m4mr_last_error": (ctypes.c_char_p, []),
-    "m4mr_forward": (_I, [_P] * 8 + [_I] * 4 + [_P] * 8 + [_P]),
-    "m4mr_backward_workspace_bytes": (_S, [_I] * 4),
+    "m4mr_forward": (_I, [_P] * 8 + [_I] * 5 + [_P] * 8 + [_P]),
+    "m4mr_backward_workspace_bytes": (_S, [_I] * 5),
     "m4mr_start_counts": (_I, [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "m4mr_backward": (
         _I,
-        [_P] * 6 + [_I] * 4 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
+        [_P] * 6 + [_I] * 5 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
     ),
     "m4mr_factored_solve": (_I, [_P, _P, _P, _L, _P]),
-    "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _P, _P, _P]),
+    "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _I, _P, _P, _P]),
     "m4mr_spd_solve": (_I, [_P, _P, _L, _I, _P, _P, _P]),
     "m4mr_spd_solve_backward": (_I, [_P, _P, _P, _L, _I, _P, _P, _P]),
     "m4mr_prologue_forward": (_I, [_P] * 9 + [_I] * 4 + [ctypes.c_float] * 2 + [_I] + [_P] * 7),

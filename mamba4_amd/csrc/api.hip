@@ -27,7 +27,7 @@ __global__ void fwd_factor_kernel(Dims, const float*, const float*, const float*
                                   const float*, const float*, float*, float*);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
 __global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
-                                   const float*, const float*, const float*, long, int, float*,
+                                   const float*, const float*, const float*, long, int, int, float*,
                                    float*);
 __global__ void fwd_read_kernel(Dims, const float*, const float*, const float*, const float*,
                                 const float*, const float*, const float*, float*, float*);
@@ -153,9 +153,13 @@ int launch(const char* name, hipStream_t stream, F&& body) {
   return M4MR_OK;
 }
 
-bool bad_dims(int B, int T, int H, int chunk, std::string* why) {
+bool bad_dims(int B, int T, int H, int P, int chunk, std::string* why) {
   if (B <= 0 || T <= 0 || H <= 0) {
     *why = "B, T and H must be positive";
+    return true;
+  }
+  if (P != M4MR_VALUE_DIM && P != M4MR_MAX_VALUE_DIM) {
+    *why = "value_dim must be 64 or 128 (pad narrower values with zeros)";
     return true;
   }
   if (chunk < 1 || chunk > M4MR_MAX_CHUNK) {
@@ -163,18 +167,20 @@ bool bad_dims(int B, int T, int H, int chunk, std::string* why) {
     return true;
   }
   const double tokens = (double)B * T * H;
-  if (tokens * M4MR_FACTOR_FLOATS > 9.0e18 || (double)B * H > 2.0e9) {
+  if (tokens * M4MR_FACTOR_FLOATS > 9.0e18 || (double)B * H * (4 + 4 * (P / 64)) > 2.0e9) {
     *why = "problem too large";
     return true;
   }
   return false;
 }
 
-Dims make_dims(int B, int T, int H, int chunk) {
+Dims make_dims(int B, int T, int H, int P, int chunk) {
   Dims d;
   d.B = B;
   d.T = T;
   d.H = H;
+  d.P = P;
+  d.NV = P / 64;
   d.chunk = chunk;
   d.NC = (T + chunk - 1) / chunk;
   // Chunks above 32 tokens split in two sub-chunks for the factor kernel, so
@@ -192,8 +198,8 @@ struct BackwardWorkspace {
   size_t bytes;
 };
 
-BackwardWorkspace carve(void* base, int B, int T, int H, int chunk) {
-  const Dims d = make_dims(B, T, H, chunk);
+BackwardWorkspace carve(void* base, int B, int T, int H, int P, int chunk) {
+  const Dims d = make_dims(B, T, H, P, chunk);
   const size_t tok = (size_t)B * T * H;
   const size_t seqs = (size_t)B * H * d.NC;
   size_t off = 0;
@@ -204,7 +210,7 @@ BackwardWorkspace carve(void* base, int B, int T, int H, int chunk) {
   w.end_s = reinterpret_cast<float*>(p + off);
   off = align256(off + seqs * 4096 * sizeof(float));
   w.end_c = reinterpret_cast<float*>(p + off);
-  off = align256(off + seqs * 4096 * sizeof(float));
+  off = align256(off + seqs * d.NV * 4096 * sizeof(float));
   w.floor_part = reinterpret_cast<float*>(p + off);
   off = align256(off + seqs * 64 * sizeof(float));
   w.bytes = off;
@@ -228,12 +234,12 @@ const char* m4mr_last_error(void) { return g_error.c_str(); }
 int m4mr_forward(const float* keys, const float* values, const float* queries,
                  const float* beta, const float* log_decay, const float* floor,
                  const float* init_evidence, const float* init_cross, int B, int T, int H,
-                 int chunk, float* output, float* variance, float* final_evidence,
+                 int value_dim, int chunk, float* output, float* variance, float* final_evidence,
                  float* final_cross, float* solved, float* factors, float* start_evidence,
                  float* start_cross, void* stream) {
   g_error.clear();
   std::string why;
-  if (bad_dims(B, T, H, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_forward: " + why);
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_forward: " + why);
   const void* need[] = {keys,     values,        queries,     beta,   log_decay,
                         floor,    output,        variance,    final_evidence,
                         final_cross, solved,     factors,     start_evidence, start_cross};
@@ -246,7 +252,7 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
   for (const void* p : vec)
     if (p && misaligned(p)) return fail(M4MR_EINVAL, "m4mr_forward: arrays must be 16-byte aligned");
   if (int rc = configure()) return rc;
-  const Dims d = make_dims(B, T, H, chunk);
+  const Dims d = make_dims(B, T, H, value_dim, chunk);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned seqs = (unsigned)B * H * d.NC;
   const unsigned subseqs = (unsigned)B * H * d.NS;
@@ -256,7 +262,7 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   rc = launch("fwd_scan", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 8), dim3(256), 0, st, d, log_decay,
+    hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d, log_decay,
                        init_evidence, init_cross, start_evidence, start_cross, final_evidence,
                        final_cross);
   });
@@ -276,22 +282,23 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {
   g_error.clear();
   std::string why;
-  if (bad_dims(1, T, 1, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_start_counts: " + why);
-  const Dims d = make_dims(1, T, 1, chunk);
+  if (bad_dims(1, T, 1, M4MR_VALUE_DIM, chunk, &why))
+    return fail(M4MR_EINVAL, "m4mr_start_counts: " + why);
+  const Dims d = make_dims(1, T, 1, M4MR_VALUE_DIM, chunk);
   if (chunks) *chunks = d.NC;
   if (evidence_starts) *evidence_starts = d.NS;
   return M4MR_OK;
 }
 
-size_t m4mr_backward_workspace_bytes(int B, int T, int H, int chunk) {
+size_t m4mr_backward_workspace_bytes(int B, int T, int H, int value_dim, int chunk) {
   std::string why;
-  if (bad_dims(B, T, H, chunk, &why)) return 0;
-  return carve(nullptr, B, T, H, chunk).bytes;
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return 0;
+  return carve(nullptr, B, T, H, value_dim, chunk).bytes;
 }
 
 int m4mr_backward(const float* keys, const float* values, const float* queries,
                   const float* beta, const float* log_decay, const float* floor, int B, int T,
-                  int H, int chunk, const float* solved, const float* factors,
+                  int H, int value_dim, int chunk, const float* solved, const float* factors,
                   const float* start_evidence, const float* start_cross, const float* d_output,
                   const float* d_variance, const float* d_final_evidence,
                   const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
@@ -299,7 +306,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
                   float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream) {
   g_error.clear();
   std::string why;
-  if (bad_dims(B, T, H, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_backward: " + why);
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_backward: " + why);
   const void* need[] = {keys,    values,     queries,         beta,         log_decay,
                         floor,   solved,     factors,         start_evidence, start_cross,
                         d_output, d_variance, d_keys,         d_values,     d_queries,
@@ -309,7 +316,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
     if (!p) return fail(M4MR_EINVAL, "m4mr_backward: a required pointer is NULL");
   if (reinterpret_cast<uintptr_t>(workspace) & 255)
     return fail(M4MR_EINVAL, "m4mr_backward: workspace must be 256-byte aligned");
-  const BackwardWorkspace ws = carve(workspace, B, T, H, chunk);
+  const BackwardWorkspace ws = carve(workspace, B, T, H, value_dim, chunk);
   if (workspace_bytes < ws.bytes)
     return fail(M4MR_EINVAL, "m4mr_backward: workspace too small (need " +
                                  std::to_string(ws.bytes) + " bytes)");
@@ -318,7 +325,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
   for (const void* p : vec)
     if (p && misaligned(p)) return fail(M4MR_EINVAL, "m4mr_backward: arrays must be 16-byte aligned");
   if (int rc = configure()) return rc;
-  const Dims d = make_dims(B, T, H, chunk);
+  const Dims d = make_dims(B, T, H, value_dim, chunk);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned seqs = (unsigned)B * H * d.NC;
   const long tokens = (long)B * T * H;
@@ -338,7 +345,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
   });
   if (rc) return rc;
   rc = launch("bwd_scan", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 8), dim3(256), 0, st, d, log_decay,
+    hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d, log_decay,
                        d_final_evidence, d_final_cross, ws.end_s, ws.end_c, d_init_evidence,
                        d_init_cross);
   });
@@ -372,11 +379,13 @@ int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N
 
 int m4mr_decode_step(float* evidence, float* cross, const float* key, const float* value,
                      const float* query, const float* beta, const float* log_decay,
-                     const float* floor, long N, int H, float* output, float* variance,
-                     void* stream) {
+                     const float* floor, long N, int H, int value_dim, float* output,
+                     float* variance, void* stream) {
   g_error.clear();
   if (N <= 0 || N > kMaxSystems || H <= 0 || N % H != 0)
     return fail(M4MR_EINVAL, "m4mr_decode_step: N must be a positive multiple of H");
+  if (value_dim != M4MR_VALUE_DIM && value_dim != M4MR_MAX_VALUE_DIM)
+    return fail(M4MR_EINVAL, "m4mr_decode_step: value_dim must be 64 or 128");
   const void* need[] = {evidence, cross, key, value, query, beta, log_decay, floor, output, variance};
   for (const void* p : need)
     if (!p) return fail(M4MR_EINVAL, "m4mr_decode_step: a required pointer is NULL");
@@ -385,8 +394,8 @@ int m4mr_decode_step(float* evidence, float* cross, const float* key, const floa
   hipStream_t st = static_cast<hipStream_t>(stream);
   return launch("decode_step", st, [&] {
     hipLaunchKernelGGL(m4::decode_step_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
-                       evidence, cross, key, value, query, beta, log_decay, floor, N, H, output,
-                       variance);
+                       evidence, cross, key, value, query, beta, log_decay, floor, N, H,
+                       value_dim / 64, output, variance);
   });
 }
 

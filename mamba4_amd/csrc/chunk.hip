@@ -36,17 +36,31 @@ __device__ __forceinline__ SeqIndex seq_at(const Dims& d, long seq) {
 
 __device__ __forceinline__ SeqIndex seq_index(const Dims& d) { return seq_at(d, blockIdx.x); }
 
+// Row s of a chunk's token-major slab: `width` floats per token-head, the
+// 64 columns from `offset` (a value tile of a P-wide row).
 struct TokenRows {
   const float* base;
   Dims d;
-  int b, h, t0;
+  int b, h, t0, width, offset;
   __device__ const float* operator()(int s) const {
-    return base + token_head(d, b, t0 + s, h) * 64;
+    return base + token_head(d, b, t0 + s, h) * width + offset;
   }
 };
 
 __device__ __forceinline__ TokenRows rows_of(const float* base, const Dims& d, const SeqIndex& si) {
-  return TokenRows{base, d, si.b, si.h, si.n * d.chunk};
+  return TokenRows{base, d, si.b, si.h, si.n * d.chunk, 64, 0};
+}
+
+// Value tile v of a P-wide row slab (values, reads and their cotangents).
+__device__ __forceinline__ TokenRows value_rows(const float* base, const Dims& d,
+                                                const SeqIndex& si, int v) {
+  return TokenRows{base, d, si.b, si.h, si.n * d.chunk, d.P, 64 * v};
+}
+
+// Tile v of chunk `seq`'s cross state [P, 64] (NV stacked 64x64 tiles).
+__device__ __forceinline__ const float* cross_tile(const float* base, const Dims& d, long seq,
+                                                   int v) {
+  return base + (seq * d.NV + v) * 4096;
 }
 
 // Persistent: block i handles chunks i, i + gridDim.x, ...  The next chunk's
@@ -74,9 +88,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   TileRegsT rc;
   ry.fetch_rows(si.len, rows_of(solved, d, si));
   rk.fetch_rows(si.len, rows_of(keys, d, si));
-  rc.fetch_matrix(start_c + si.seq * 4096);
+  rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   rq.fetch_rows(si.len, rows_of(queries, d, si));
-  rv.fetch_rows(si.len, rows_of(values, d, si));
+  rv.fetch_rows(si.len, value_rows(values, d, si, 0));
 
   for (;;) {
     ry.store(Y);
@@ -90,7 +104,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (more) {
       ry.fetch_rows(sn.len, rows_of(solved, d, sn));
       rk.fetch_rows(sn.len, rows_of(keys, d, sn));
-      rc.fetch_matrix(start_c + sn.seq * 4096);
+      // With more than one value tile, rc carries this chunk's later tiles
+      // and prefetches after the last of them.
+      if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
     }
 
     // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
@@ -118,23 +134,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
         G[t * LDT + s] = v;
       }
-    __syncthreads();
-    rv.store(K);
-    __syncthreads();
-    if (more) rv.fetch_rows(sn.len, rows_of(values, d, sn));
+    for (int v = 0; v < d.NV; ++v) {
+      if (v > 0) {
+        // Value tile v and cross tile v replace tile v - 1 once every wave
+        // has read it.
+        rv.fetch_rows(si.len, value_rows(values, d, si, v));
+        rc.fetch_matrix(cross_tile(start_c, d, si.seq, v));
+        __syncthreads();
+        rc.store(C0);
+      } else {
+        __syncthreads();
+      }
+      rv.store(K);
+      __syncthreads();
+      if (more && v == d.NV - 1) {
+        rv.fetch_rows(sn.len, value_rows(values, d, sn, 0));
+        if (d.NV > 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
+      }
 
-    f4 out[4], inh[4];
-    zero4(out);
-    zero4(inh);
-    tile_mma<false, false>(out, G, K, k_terms(si.len), w);  // within-chunk reads
-    tile_mma<false, false>(inh, Y, C0, 64, w);              // inherited reads y_t . C0[p]
+      f4 out[4], inh[4];
+      zero4(out);
+      zero4(inh);
+      tile_mma<false, false>(out, G, K, k_terms(si.len), w);  // within-chunk reads
+      tile_mma<false, false>(inh, Y, C0, 64, w);              // inherited reads y_t . C0[p]
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(w, q);
-      if (t < si.len) {
-        const float carried = expf(cs.prefix[t]);
-        float* dst = output + token_head(d, si.b, si.n * d.chunk + t, si.h) * 64;
-        *reinterpret_cast<f4*>(dst + c4) = quad_row(out, q) + carried * quad_row(inh, q);
+      for (int q = 0; q < 4; ++q) {
+        const int t = acc_row(w, q);
+        if (t < si.len) {
+          const float carried = expf(cs.prefix[t]);
+          float* dst = output + token_head(d, si.b, si.n * d.chunk + t, si.h) * d.P + 64 * v;
+          *reinterpret_cast<f4*>(dst + c4) = quad_row(out, q) + carried * quad_row(inh, q);
+        }
       }
     }
     if (!more) break;
@@ -160,10 +190,10 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
 
   TileRegs rd, rv, rk, rc;
-  rd.fetch_rows(si.len, rows_of(d_output, d, si));
-  rv.fetch_rows(si.len, rows_of(values, d, si));
+  rd.fetch_rows(si.len, value_rows(d_output, d, si, 0));
+  rv.fetch_rows(si.len, value_rows(values, d, si, 0));
   rk.fetch_rows(si.len, rows_of(keys, d, si));
-  rc.fetch_matrix(start_c + si.seq * 4096);
+  rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   // Queries and d_variance of this lane's accumulator rows (read in the epilogue).
   f4 qv[4];
   float dvar[4];
@@ -184,9 +214,24 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
   load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
   __syncthreads();
 
-  f4 acc[4];
+  // Both products sum over the value tiles: dout_t . v_s and C0^T dout_t.
+  f4 acc[4], inh[4];
   zero4(acc);
-  tile_mma<false, true>(acc, DO, V, 64, w);  // dout_t . v_s
+  zero4(inh);
+  for (int v = 0; v < d.NV; ++v) {
+    if (v > 0) {
+      rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+      rv.fetch_rows(si.len, value_rows(values, d, si, v));
+      rc.fetch_matrix(cross_tile(start_c, d, si.seq, v));
+      __syncthreads();
+      rd.store(DO);
+      rv.store(V);
+      rc.store(C0);
+      __syncthreads();
+    }
+    tile_mma<false, true>(acc, DO, V, 64, w);  // dout_t . v_s
+    tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
+  }
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
@@ -200,11 +245,9 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
   rk.store(V);
   __syncthreads();
 
-  f4 within[4], inh[4];
+  f4 within[4];
   zero4(within);
-  zero4(inh);
   tile_mma<false, false>(within, G, V, k_terms(si.len), w);  // sum_s G[t][s] k_s
-  tile_mma<false, false>(inh, DO, C0, 64, w);                // C0^T dout_t
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int t = acc_row(w, q);
@@ -222,7 +265,12 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
 // blocks; tile_mma_half), so each SIMD runs two waves of one chunk and one
 // wave's epilogue, LDS staging and barriers overlap the other's MFMAs.  Row
 // sums that span both halves meet in LDS and are added in half order.
+//
+// Value-dependent terms run once per 64-column value tile (NV <= 2): gv and
+// H^T v sum over the tiles, d values and H k are per tile; the tiles are
+// restaged in an order that starts from the tile already in LDS.
 constexpr int GRADS_THREADS = 512;
+constexpr int MAX_NV = 2;
 
 __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ values,
@@ -236,12 +284,12 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     float* __restrict__ floor_part) {
   extern __shared__ float smem[];
   float* Kt = smem;       // keys, then S0
-  float* Vt = Kt + TILE;  // values, then C0
+  float* Vt = Kt + TILE;  // a value tile, then a C0 tile
   float* Yt = Vt + TILE;
   float* Zt = Yt + TILE;
-  float* Dt = Zt + TILE;  // dout
-  float* M1 = Dt + TILE;  // W * gy, then G_end
-  float* M2 = M1 + TILE;  // W * (gv - gz), then H_end
+  float* Dt = Zt + TILE;  // a dout tile
+  float* M1 = Dt + TILE;  // W * gy, then G_end (then G + G^T)
+  float* M2 = M1 + TILE;  // W * (gv - gz), then an H_end tile
   __shared__ ChunkScalars cs;
   __shared__ float colpart[4][64];
   __shared__ float rowpart[2][64], quadpart[2][64], startpart[2][64];
@@ -251,7 +299,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   const SeqIndex si = seq_index(d);
   const int w8 = threadIdx.x >> 6, ws = w8 & 3, hf = w8 >> 2, l = lane_id();
   const int r = l & 15, c4 = 4 * r;
-  const int kt = k_terms(si.len);
+  const int kt = k_terms(si.len), last = d.NV - 1;
   // d_variance of this thread's tile-fetch rows (threadIdx/16 + 32j).
   float dvar[2];
 #pragma unroll
@@ -263,10 +311,10 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   {
     TileRegs2 rt[5];
     rt[0].fetch_rows(si.len, rows_of(keys, d, si));
-    rt[1].fetch_rows(si.len, rows_of(values, d, si));
+    rt[1].fetch_rows(si.len, value_rows(values, d, si, 0));
     rt[2].fetch_rows(si.len, rows_of(solved, d, si));
     rt[3].fetch_rows(si.len, rows_of(z, d, si));
-    rt[4].fetch_rows(si.len, rows_of(d_output, d, si));
+    rt[4].fetch_rows(si.len, value_rows(d_output, d, si, 0));
     rt[0].store(Kt);
     rt[1].store(Vt);
     rt[2].store(Yt);
@@ -274,13 +322,15 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     rt[4].store(Dt);
   }
   load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
-  // The end-state cotangents of phase 3 load while phases 1 and 2 run.
+  // The end-state cotangents of phase 3 load while phases 1 and 2 run (of H,
+  // the last value tile, the one phase 3 starts from).
   TileRegs2 rg, rh;
   rg.fetch_matrix(end_s + si.seq * 4096);
-  rh.fetch_matrix(end_c + si.seq * 4096);
+  rh.fetch_matrix(cross_tile(end_c, d, si.seq, last));
   __syncthreads();
 
-  // Phase 1: gy = Y K^T, gz = Z K^T, gv = dOut V^T and their weighted mixes.
+  // Phase 1: gy = Y K^T, gz = Z K^T, gv = sum over value tiles of dOut V^T,
+  // and their weighted mixes.  Leaves the last value and dout tiles in LDS.
   {
     f4 gy[2], gz[2], gv[2];
     zero2(gy);
@@ -289,6 +339,16 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf);
     tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf);
     tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf);
+    for (int v = 1; v < d.NV; ++v) {
+      TileRegs2 rv, rd;
+      rv.fetch_rows(si.len, value_rows(values, d, si, v));
+      rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+      __syncthreads();
+      rv.store(Vt);
+      rd.store(Dt);
+      __syncthreads();
+      tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf);
+    }
     float rsum[4] = {0.f, 0.f, 0.f, 0.f};
     float csum[2] = {0.f, 0.f};
 #pragma unroll
@@ -327,32 +387,46 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     rowE[s] = rowpart[0][s] + rowpart[1][s];
   }
 
-  // Phase 2: within-chunk key and value gradients (rows s, QUAD columns
-  // 4r + 2hf + j).
-  f4 dk[2], dv[2];
+  // Phase 2: within-chunk key gradient and the value gradient of each tile
+  // (rows s, QUAD columns 4r + 2hf + j).  Tiles from the last down, so the
+  // first dout tile is in LDS afterwards.
+  f4 dk[2], dv[MAX_NV][2];
   zero2(dk);
-  zero2(dv);
   {
     f4 tmp[2];
     zero2(tmp);
     tile_mma_half<true, false>(dk, M2, Yt, kt, ws, hf);   // sum_t W(gv-gz)[t][s] y_t
     tile_mma_half<true, false>(tmp, M1, Zt, kt, ws, hf);  // sum_t W gy[t][s] z_t
-    tile_mma_half<true, false>(dv, M1, Dt, kt, ws, hf);   // sum_t W gy[t][s] dout_t
 #pragma unroll
     for (int j = 0; j < 2; ++j) dk[j] -= tmp[j];
+  }
+#pragma unroll
+  for (int v = MAX_NV - 1; v >= 0; --v) {
+    zero2(dv[v]);
+    if (v < d.NV) {
+      if (v < last) {
+        TileRegs2 rd;
+        rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+        __syncthreads();
+        rd.store(Dt);
+        __syncthreads();
+      }
+      tile_mma_half<true, false>(dv[v], M1, Dt, kt, ws, hf);  // sum_t W gy[t][s] dout_t
+    }
   }
   __syncthreads();
 
   // Phase 3: chunk-end terms through the end-state cotangents G, H.  G is
   // replaced by G + G^T in LDS (each off-diagonal pair by one thread), so
-  // (G + G^T) k_s is a single product.
+  // (G + G^T) k_s is a single product.  H and the values go tile by tile from
+  // the last, leaving the first tile of each in LDS.
   rg.store(M1);
   rh.store(M2);
   // The start states of phase 4 load while phase 3 runs.
   const long bh = si.seq / d.NC;
   TileRegs2 rs, rc;
   rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
-  rc.fetch_matrix(start_c + si.seq * 4096);
+  rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   __syncthreads();
   for (int e = threadIdx.x; e < 64 * 64; e += GRADS_THREADS) {
     const int i = e >> 6, j = e & 63;
@@ -366,21 +440,45 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   }
   __syncthreads();
   {
-    f4 gk[2], hk[2], hv[2];
+    f4 gk[2], hv[2];
     zero2(gk);
-    zero2(hk);
     zero2(hv);
-    tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // (G + G^T) k_s
-    tile_mma_half<false, true, true>(hk, Kt, M2, 64, ws, hf);  // H k_s
-    tile_mma_half<false, false>(hv, Vt, M2, 64, ws, hf);       // H^T v_s
+    tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);  // (G + G^T) k_s
     float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int s = acc_row(ws, q);
-      const float2 kr = *reinterpret_cast<const float2*>(Kt + s * LDT + c4 + 2 * hf);
-      const float2 vr = *reinterpret_cast<const float2*>(Vt + s * LDT + c4 + 2 * hf);
-      qpart[q] += 0.5f * kr.x * gk[0][q] + vr.x * hk[0][q];
-      qpart[q] += 0.5f * kr.y * gk[1][q] + vr.y * hk[1][q];
+      const float2 kr = *reinterpret_cast<const float2*>(Kt + acc_row(ws, q) * LDT + c4 + 2 * hf);
+      qpart[q] += 0.5f * kr.x * gk[0][q] + 0.5f * kr.y * gk[1][q];
+    }
+#pragma unroll
+    for (int v = MAX_NV - 1; v >= 0; --v) {
+      if (v < d.NV) {
+        if (v < last) {
+          TileRegs2 rv, rhv;
+          rv.fetch_rows(si.len, value_rows(values, d, si, v));
+          rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
+          __syncthreads();
+          rv.store(Vt);
+          rhv.store(M2);
+          __syncthreads();
+        }
+        f4 hk[2];
+        zero2(hk);
+        tile_mma_half<false, true, true>(hk, Kt, M2, 64, ws, hf);  // H k_s
+        tile_mma_half<false, false>(hv, Vt, M2, 64, ws, hf);       // H^T v_s, summed
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int s = acc_row(ws, q);
+          const float2 vr = *reinterpret_cast<const float2*>(Vt + s * LDT + c4 + 2 * hf);
+          qpart[q] += vr.x * hk[0][q] + vr.y * hk[1][q];
+          if (s < si.len) {
+            const float tl = cs.tail[s];
+            const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
+            *reinterpret_cast<float2*>(d_values + th * d.P + 64 * v + c4 + 2 * hf) =
+                float2{dv[v][0][q] + tl * hk[0][q], dv[v][1][q] + tl * hk[1][q]};
+          }
+        }
+      }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -392,8 +490,6 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
         *reinterpret_cast<float2*>(d_keys + th * 64 + c4 + 2 * hf) =
             float2{dk[0][q] + tl * (gk[0][q] + hv[0][q]), dk[1][q] + tl * (gk[1][q] + hv[1][q])};
-        *reinterpret_cast<float2*>(d_values + th * 64 + c4 + 2 * hf) =
-            float2{dv[0][q] + tl * hk[0][q], dv[1][q] + tl * hk[1][q]};
       }
     }
   }
@@ -401,8 +497,9 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   if (threadIdx.x < 64) quad[threadIdx.x] = quadpart[0][threadIdx.x] + quadpart[1][threadIdx.x];
 
   // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>
-  // (<G, S0> = <G + G^T, S0> / 2 since S0 is symmetric).  The chunk's start
-  // evidence is the start of its first sub-chunk.
+  // (<G, S0> = <G + G^T, S0> / 2 since S0 is symmetric), the C0 terms summed
+  // over the value tiles from the first (whose H and dout tiles are in LDS).
+  // The chunk's start evidence is the start of its first sub-chunk.
   rs.store(Kt);
   rc.store(Vt);
   __syncthreads();
@@ -410,15 +507,31 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     float part = 0.f;
     for (int e = threadIdx.x; e < 4096; e += GRADS_THREADS) {
       const int row = e >> 6, col = e & 63;
-      part += 0.5f * M1[row * LDT + col] * Kt[row * LDT + col] +
-              M2[row * LDT + col] * Vt[row * LDT + col];
+      part += 0.5f * M1[row * LDT + col] * Kt[row * LDT + col];
     }
-    red[threadIdx.x] = part;
     f4 ys[2], dc[2];
     zero2(ys);
     zero2(dc);
     tile_mma_half<false, false>(ys, Yt, Kt, 64, ws, hf);  // y_t^T S0
-    tile_mma_half<false, false>(dc, Dt, Vt, 64, ws, hf);  // dout_t^T C0
+    for (int v = 0; v < d.NV; ++v) {
+      if (v > 0) {
+        TileRegs2 rhv, rcv, rd;
+        rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
+        rcv.fetch_matrix(cross_tile(start_c, d, si.seq, v));
+        rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+        __syncthreads();
+        rhv.store(M2);
+        rcv.store(Vt);
+        rd.store(Dt);
+        __syncthreads();
+      }
+      for (int e = threadIdx.x; e < 4096; e += GRADS_THREADS) {
+        const int row = e >> 6, col = e & 63;
+        part += M2[row * LDT + col] * Vt[row * LDT + col];
+      }
+      tile_mma_half<false, false>(dc, Dt, Vt, 64, ws, hf);  // dout_t^T C0, summed
+    }
+    red[threadIdx.x] = part;
     float sp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {

@@ -17,10 +17,13 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // Problem shape.  Chunks of `chunk` tokens carry the decayed statistics;
 // each chunk splits into `rsub` sub-chunks of up to `sub` tokens, and the
 // factor kernel starts one token sequence per sub-chunk from its stored
-// evidence (NS = NC * rsub start states).
+// evidence (NS = NC * rsub start states).  Value rows (values, reads and
+// their cotangents) are P = 64 NV floats wide; a cross state [P, 64] is NV
+// stacked 64x64 tiles, and every value-dependent product runs per tile.
 struct Dims {
   int B, T, H, chunk, NC;
   int sub, rsub, NS;
+  int P, NV;
 };
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }

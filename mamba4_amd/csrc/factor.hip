@@ -299,13 +299,13 @@ decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
                    const float* __restrict__ key, const float* __restrict__ value,
                    const float* __restrict__ query, const float* __restrict__ beta,
                    const float* __restrict__ log_decay, const float* __restrict__ floor, long N,
-                   int H, float* __restrict__ output, float* __restrict__ variance) {
+                   int H, int NV, float* __restrict__ output, float* __restrict__ variance) {
   const int lane = threadIdx.x, a = lane & 15, mu = lane >> 4;
   long nidx = (long)blockIdx.x * 4 + mu;
   const bool active = nidx < N;
   if (!active) nidx = N - 1;
   float* S = evidence + nidx * 4096;
-  float* C = cross + nidx * 4096;
+  const int P = 64 * NV;  // value width; the cross state is NV stacked 64x64 tiles
   float kr[4], qr[4], fl[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
@@ -355,12 +355,8 @@ decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
   float nw[4], y[4];
   factor_exchanged(A, fl, qr, nw);
   backward_rows16(A, nw, y);
-  float vr[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    vr[m] = value[nidx * 64 + a + 16 * m];
-    qr[m] = query[nidx * 64 + a + 16 * m];
-  }
+  for (int m = 0; m < 4; ++m) qr[m] = query[nidx * 64 + a + 16 * m];
   kq = *reinterpret_cast<const f4*>(key + nidx * 64 + 4 * a);
   // y[4a .. 4a+3] for the coalesced read: y_j lives in lane j%16, slot j/16.
   __shared__ float ys[4][64];
@@ -368,26 +364,31 @@ decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
   for (int m = 0; m < 4; ++m) ys[mu][a + 16 * m] = y[m];
   __syncthreads();
   const f4 yq = *reinterpret_cast<const f4*>(&ys[mu][4 * a]);
-  float out[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int v = 0; v < NV; ++v) {
+    float* C = cross + (nidx * NV + v) * 4096;
+    float vr[4], out[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < 4; ++m) vr[m] = value[nidx * P + 64 * v + a + 16 * m];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      f4* p = reinterpret_cast<f4*>(C + (16 * m + r) * 64) + a;
-      const float bv = bt * bcast16(vr[m], r);
-      const f4 cv = lam * *p + bv * kq;
-      if (active) *p = cv;
-      // Row 16m + r of the read, summed over the 16 column quads.
-      const float part = sum16(cv[0] * yq[0] + cv[1] * yq[1] + cv[2] * yq[2] + cv[3] * yq[3]);
-      out[m] = a == r ? part : out[m];
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        f4* p = reinterpret_cast<f4*>(C + (16 * m + r) * 64) + a;
+        const float bv = bt * bcast16(vr[m], r);
+        const f4 cv = lam * *p + bv * kq;
+        if (active) *p = cv;
+        // Row 16m + r of the read, summed over the 16 column quads.
+        const float part = sum16(cv[0] * yq[0] + cv[1] * yq[1] + cv[2] * yq[2] + cv[3] * yq[3]);
+        out[m] = a == r ? part : out[m];
+      }
     }
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      if (active) output[nidx * P + 64 * v + a + 16 * m] = out[m];
   }
   float var = 0.f;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (active) output[nidx * 64 + a + 16 * m] = out[m];
-    var += qr[m] * y[m];
-  }
+  for (int m = 0; m < 4; ++m) var += qr[m] * y[m];
   var = sum16(var);
   if (active && a == 0) variance[nidx] = var;
 }

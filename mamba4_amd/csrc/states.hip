@@ -9,6 +9,10 @@
 //   start[u] = running;  running = exp(sum of log decays in u) running + stat[u]
 // and writes the final state.
 //
+// Value-dependent states (cross statistics and their cotangents) are NV
+// stacked 64x64 tiles per state; each tile is one more product, and the scans
+// treat the NV * 4096 elements of a cross state alike.
+//
 // Backward: the transpose of that carry.  bwd_local_kernel computes each
 // chunk's start-state cotangents U = -(M + M^T)/2, M = Z^T diag(e^P) Y, and
 // V = dOut^T diag(e^P) Y; bwd_scan_kernel walks chunks in reverse,
@@ -33,12 +37,12 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(
   const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
   const int len = chunk_len(d, n), w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   const int kt = k_terms(len);
-  auto rows = [&](const float* base) {
-    return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * 64; };
+  auto rows = [&](const float* base, int width, int offset) {
+    return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * width + offset; };
   };
   TileRegs rk, rv;
-  rk.fetch_rows(len, rows(keys));
-  rv.fetch_rows(len, rows(values));
+  rk.fetch_rows(len, rows(keys, 64, 0));
+  rv.fetch_rows(len, rows(values, d.P, 0));
   rk.store(K);
   rv.store(V);
   load_chunk_scalars(cs, d, beta, log_decay, b, h, n);
@@ -62,18 +66,27 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(
       *reinterpret_cast<f4*>(out + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
     __syncthreads();
   }
-  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-    const int s = e >> 6, c = e & 63;
-    W[s * LDT + c] = s < len ? cs.tail[s] * V[s * LDT + c] : 0.f;
-  }
-  __syncthreads();
-  f4 acc[4];
-  zero4(acc);
-  tile_mma<true, false>(acc, W, K, kt, w);  // sum_s tail_s v_s k_s^T
-  float* out = mat(start_c, (long)bh * d.NC + n);
+  for (int v = 0; v < d.NV; ++v) {
+    if (v > 0) {
+      // Value tile v replaces tile v - 1 once every wave has read it.
+      rv.fetch_rows(len, rows(values, d.P, 64 * v));
+      __syncthreads();
+      rv.store(V);
+      __syncthreads();
+    }
+    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+      const int s = e >> 6, c = e & 63;
+      W[s * LDT + c] = s < len ? cs.tail[s] * V[s * LDT + c] : 0.f;
+    }
+    __syncthreads();
+    f4 acc[4];
+    zero4(acc);
+    tile_mma<true, false>(acc, W, K, kt, w);  // sum_s tail_s v_s k_s^T
+    float* out = mat(start_c, ((long)bh * d.NC + n) * d.NV + v);
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<f4*>(out + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f4*>(out + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
+  }
 }
 
 // exp(sum of log decays) over the tokens of step `i` of the scan: a
@@ -98,21 +111,23 @@ __device__ __forceinline__ float step_decay(const Dims& d, const float* log_deca
 // Steps of a scan whose loads are issued together.
 constexpr int SCAN_BATCH = 8;
 
-// Grid (B*H, 8): y in 0..3 scans evidence elements [1024y, 1024y+1024) over
-// the NS sub-chunks, y in 4..7 the cross-statistic elements over NC chunks.
+// Grid (B*H, 4 + 4 NV): y in 0..3 scans evidence elements [1024y, 1024y+1024)
+// over the NS sub-chunks, y >= 4 the cross-statistic elements
+// [1024(y-4), 1024(y-3)) of the NV * 4096 per state over NC chunks.
 __global__ __launch_bounds__(256) void fwd_scan_kernel(
     Dims d, const float* __restrict__ log_decay, const float* __restrict__ init_s,
     const float* __restrict__ init_c, float* __restrict__ start_s, float* __restrict__ start_c,
     float* __restrict__ final_s, float* __restrict__ final_c) {
   const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
   const bool cross = blockIdx.y >= 4;
-  const int elem = 1024 * (blockIdx.y & 3) + 4 * threadIdx.x;
+  const int elem = 1024 * (cross ? blockIdx.y - 4 : blockIdx.y) + 4 * threadIdx.x;
   const int steps = cross ? d.NC : d.NS;
-  float* buf = cross ? start_c + (long)bh * d.NC * 4096 : start_s + (long)bh * d.NS * 4096;
+  const long size = cross ? 4096L * d.NV : 4096L;  // floats per state
+  float* buf = (cross ? start_c : start_s) + (long)bh * steps * size;
   const float* init = cross ? init_c : init_s;
   __shared__ float decay[256];
   f4 running = f4{0.f, 0.f, 0.f, 0.f};
-  if (init) running = *reinterpret_cast<const f4*>(init + (long)bh * 4096 + elem);
+  if (init) running = *reinterpret_cast<const f4*>(init + (long)bh * size + elem);
   for (int base = 0; base < steps; base += 256) {
     const int count = min(256, steps - base);
     __syncthreads();
@@ -124,17 +139,17 @@ __global__ __launch_bounds__(256) void fwd_scan_kernel(
       f4 stat[SCAN_BATCH];
 #pragma unroll
       for (int j = 0; j < SCAN_BATCH; ++j)
-        if (j < m) stat[j] = *reinterpret_cast<const f4*>(buf + (long)(base + i0 + j) * 4096 + elem);
+        if (j < m) stat[j] = *reinterpret_cast<const f4*>(buf + (long)(base + i0 + j) * size + elem);
 #pragma unroll
       for (int j = 0; j < SCAN_BATCH; ++j)
         if (j < m) {
-          *reinterpret_cast<f4*>(buf + (long)(base + i0 + j) * 4096 + elem) = running;
+          *reinterpret_cast<f4*>(buf + (long)(base + i0 + j) * size + elem) = running;
           running = decay[i0 + j] * running + stat[j];
         }
     }
   }
   float* fin = cross ? final_c : final_s;
-  *reinterpret_cast<f4*>(fin + (long)bh * 4096 + elem) = running;
+  *reinterpret_cast<f4*>(fin + (long)bh * size + elem) = running;
 }
 
 __global__ __launch_bounds__(256) void bwd_local_kernel(
@@ -151,13 +166,13 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
   const int len = chunk_len(d, n), w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   const int kt = k_terms(len);
-  auto rows = [&](const float* base) {
-    return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * 64; };
+  auto rows = [&](const float* base, int width, int offset) {
+    return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * width + offset; };
   };
   TileRegs ry, rz, rd;
-  ry.fetch_rows(len, rows(solved));
-  rz.fetch_rows(len, rows(z));
-  rd.fetch_rows(len, rows(d_output));
+  ry.fetch_rows(len, rows(solved, 64, 0));
+  rz.fetch_rows(len, rows(z, 64, 0));
+  rd.fetch_rows(len, rows(d_output, d.P, 0));
   ry.store(Y);
   rz.store(Zw);
   rd.store(Dw);
@@ -186,27 +201,42 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
     for (int jb = 0; jb < 4; ++jb) v[jb] = -0.5f * (acc[jb][q] + M[(c4 + jb) * LDT + i]);
     *reinterpret_cast<f4*>(us + i * 64 + c4) = v;
   }
-  zero4(acc);
-  tile_mma<true, false>(acc, Dw, Y, kt, w);  // V = sum_t e^P dout_t y_t^T
-  float* uc = mat(end_c, (long)bh * d.NC + n);
+  for (int v = 0; v < d.NV; ++v) {
+    if (v > 0) {
+      // Value tile v of the read cotangent replaces tile v - 1.
+      rd.fetch_rows(len, rows(d_output, d.P, 64 * v));
+      __syncthreads();
+      rd.store(Dw);
+      __syncthreads();
+      for (int e = threadIdx.x; e < len * 64; e += 256) {
+        const int t = e >> 6, c = e & 63;
+        Dw[t * LDT + c] *= expf(cs.prefix[t]);
+      }
+      __syncthreads();
+    }
+    zero4(acc);
+    tile_mma<true, false>(acc, Dw, Y, kt, w);  // V = sum_t e^P dout_t y_t^T
+    float* uc = mat(end_c, ((long)bh * d.NC + n) * d.NV + v);
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<f4*>(uc + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f4*>(uc + acc_row(w, q) * 64 + c4) = quad_row(acc, q);
+  }
 }
 
-// Grid (B*H, 8) as fwd_scan_kernel, walking chunks in reverse.
+// Grid (B*H, 4 + 4 NV) as fwd_scan_kernel, walking chunks in reverse.
 __global__ __launch_bounds__(256) void bwd_scan_kernel(
     Dims d, const float* __restrict__ log_decay, const float* __restrict__ d_final_s,
     const float* __restrict__ d_final_c, float* __restrict__ end_s, float* __restrict__ end_c,
     float* __restrict__ d_init_s, float* __restrict__ d_init_c) {
   const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
   const bool cross = blockIdx.y >= 4;
-  const int elem = 1024 * (blockIdx.y & 3) + 4 * threadIdx.x;
-  float* buf = (cross ? end_c : end_s) + (long)bh * d.NC * 4096;
+  const int elem = 1024 * (cross ? blockIdx.y - 4 : blockIdx.y) + 4 * threadIdx.x;
+  const long size = cross ? 4096L * d.NV : 4096L;  // floats per state
+  float* buf = (cross ? end_c : end_s) + (long)bh * d.NC * size;
   const float* fin = cross ? d_final_c : d_final_s;
   __shared__ float decay[256];
   f4 running = f4{0.f, 0.f, 0.f, 0.f};
-  if (fin) running = *reinterpret_cast<const f4*>(fin + (long)bh * 4096 + elem);
+  if (fin) running = *reinterpret_cast<const f4*>(fin + (long)bh * size + elem);
   for (int top = d.NC; top > 0; top -= 256) {
     const int count = min(256, top);
     __syncthreads();
@@ -218,17 +248,17 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
       f4 local[SCAN_BATCH];
 #pragma unroll
       for (int j = 0; j < SCAN_BATCH; ++j)
-        if (j < m) local[j] = *reinterpret_cast<const f4*>(buf + (long)(top - count + i0 - j) * 4096 + elem);
+        if (j < m) local[j] = *reinterpret_cast<const f4*>(buf + (long)(top - count + i0 - j) * size + elem);
 #pragma unroll
       for (int j = 0; j < SCAN_BATCH; ++j)
         if (j < m) {
-          *reinterpret_cast<f4*>(buf + (long)(top - count + i0 - j) * 4096 + elem) = running;
+          *reinterpret_cast<f4*>(buf + (long)(top - count + i0 - j) * size + elem) = running;
           running = local[j] + decay[i0 - j] * running;
         }
     }
   }
   float* dinit = cross ? d_init_c : d_init_s;
-  *reinterpret_cast<f4*>(dinit + (long)bh * 4096 + elem) = running;
+  *reinterpret_cast<f4*>(dinit + (long)bh * size + elem) = running;
 }
 
 }  // namespace m4

@@ -75,28 +75,38 @@ def selective_initial_state(batch, heads, key_dim, value_dim, device="cuda"):
     )
 
 
+def _value_width(value_dim):
+    """The library's value width for `value_dim` columns: 64 or 128."""
+    if value_dim > _lib.MAX_VALUE_DIM:
+        raise ValueError(
+            f"value widths must be <= {_lib.MAX_VALUE_DIM}; got {value_dim}"
+        )
+    return _lib.VALUE_DIM if value_dim <= _lib.VALUE_DIM else _lib.MAX_VALUE_DIM
+
+
 class _MemoryRead(torch.autograd.Function):
-    """Custom VJP around m4mr_forward / m4mr_backward (fixed D = P = 64)."""
+    """Custom VJP around m4mr_forward / m4mr_backward (D = 64, P = 64 or 128)."""
 
     @staticmethod
     def forward(ctx, keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk):
         lib = _lib.load()
         batch, time, heads, _ = keys.shape
+        width = values.shape[-1]
         count, starts = _lib.start_counts(time, chunk)
         dev = keys.device
         f32 = dict(dtype=torch.float32, device=dev)
-        output = torch.empty((batch, time, heads, _lib.VALUE_DIM), **f32)
+        output = torch.empty((batch, time, heads, width), **f32)
         variance = torch.empty((batch, time, heads), **f32)
         final_s = torch.empty((batch, heads, 64, 64), **f32)
-        final_c = torch.empty((batch, heads, _lib.VALUE_DIM, 64), **f32)
+        final_c = torch.empty((batch, heads, width, 64), **f32)
         solved = torch.empty((batch, time, heads, 64), **f32)
         factors = torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
         start_s = torch.empty((batch, heads, starts, 64, 64), **f32)
-        start_c = torch.empty((batch, heads, count, _lib.VALUE_DIM, 64), **f32)
+        start_c = torch.empty((batch, heads, count, width, 64), **f32)
         _lib.check(
             lib.m4mr_forward(
                 _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
-                _ptr(floor), _ptr(init_s), _ptr(init_c), batch, time, heads, chunk,
+                _ptr(floor), _ptr(init_s), _ptr(init_c), batch, time, heads, width, chunk,
                 _ptr(output), _ptr(variance), _ptr(final_s), _ptr(final_c),
                 _ptr(solved), _ptr(factors), _ptr(start_s), _ptr(start_c), _stream(),
             )
@@ -115,6 +125,7 @@ class _MemoryRead(torch.autograd.Function):
         (keys, values, queries, beta, log_decay, floor, solved, factors, start_s,
          start_c) = ctx.saved_tensors
         batch, time, heads, _ = keys.shape
+        width = values.shape[-1]
         chunk = ctx.chunk
 
         def dense(g, like):
@@ -129,13 +140,13 @@ class _MemoryRead(torch.autograd.Function):
         grads = [torch.empty_like(t) for t in (keys, values, queries, beta, log_decay, floor)]
         f32 = dict(dtype=torch.float32, device=keys.device)
         d_init_s = torch.empty((batch, heads, _lib.KEY_DIM, _lib.KEY_DIM), **f32)
-        d_init_c = torch.empty((batch, heads, _lib.VALUE_DIM, _lib.KEY_DIM), **f32)
-        nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, chunk)
+        d_init_c = torch.empty((batch, heads, width, _lib.KEY_DIM), **f32)
+        nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, width, chunk)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
         _lib.check(
             lib.m4mr_backward(
                 _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
-                _ptr(floor), batch, time, heads, chunk, _ptr(solved), _ptr(factors),
+                _ptr(floor), batch, time, heads, width, chunk, _ptr(solved), _ptr(factors),
                 _ptr(start_s), _ptr(start_c), _ptr(d_output), _ptr(d_variance),
                 _ptr(d_final_s), _ptr(d_final_c), *(_ptr(g) for g in grads),
                 _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace), nbytes, _stream(),
@@ -232,7 +243,7 @@ def selective_gaussian_memory(
     """Exact chunked reads of the fixed-floor selective Gaussian memory.
 
     keys/queries [B,T,H,D], values [B,T,H,P], beta and log_decay [B,T,H]
-    (log_decay <= 0), floor [H,D] positive; D, P <= 64.  With
+    (log_decay <= 0), floor [H,D] positive; D <= 64, P <= 128.  With
     S_t = lam_t S_(t-1) + beta_t k k^T and C_t likewise, each token reads
     C_t y_t and q_t^T y_t where (S_t + diag(floor)) y_t = q_t.  Returns
     SelectiveResult(output [B,T,H,P], variance [B,T,H],
@@ -247,10 +258,9 @@ def selective_gaussian_memory(
         raise ValueError("Selective memory keys, values and queries disagree")
     _require_device(keys, values, queries)
     keys, values, queries = (a.to(torch.float32) for a in (keys, values, queries))
-    if dim > _lib.KEY_DIM or value_dim > _lib.VALUE_DIM:
-        raise ValueError(
-            f"key and value widths must be <= {_lib.KEY_DIM}; got {dim} and {value_dim}"
-        )
+    if dim > _lib.KEY_DIM:
+        raise ValueError(f"key widths must be <= {_lib.KEY_DIM}; got {dim}")
+    width = _value_width(value_dim)
     if chunk_size < 1:
         raise ValueError("chunk_size must be positive")
     device = keys.device
@@ -264,7 +274,7 @@ def selective_gaussian_memory(
     # (lm/kernels/mamba4_fused.py:292-297).  Padded values read nothing.
     k = _pad_last(keys, _lib.KEY_DIM).contiguous()
     q = _pad_last(queries, _lib.KEY_DIM).contiguous()
-    v = _pad_last(values, _lib.VALUE_DIM).contiguous()
+    v = _pad_last(values, width).contiguous()
     f = _pad_last(floor, _lib.KEY_DIM, value=1.0).contiguous()
     init_s = init_c = None
     if initial is not None:
@@ -273,7 +283,7 @@ def selective_gaussian_memory(
         _require_device(init_s, init_c)
         init_s = F.pad(init_s, (0, _lib.KEY_DIM - dim, 0, _lib.KEY_DIM - dim)).contiguous()
         init_c = F.pad(
-            init_c, (0, _lib.KEY_DIM - dim, 0, _lib.VALUE_DIM - value_dim)
+            init_c, (0, _lib.KEY_DIM - dim, 0, width - value_dim)
         ).contiguous()
     chunk = min(int(chunk_size), _lib.MAX_CHUNK)
     with torch.cuda.device(device):
@@ -319,11 +329,10 @@ def selective_decode(state, key, value, query, beta, log_decay, floor, solver=No
         )
         return SelectiveResult(one.output[:, 0], one.variance[:, 0], one.state)
     dim, value_dim = evidence.shape[-1], cross.shape[-2]
-    if dim > _lib.KEY_DIM or value_dim > _lib.VALUE_DIM:
-        raise ValueError(
-            f"key and value widths must be <= {_lib.KEY_DIM}; got {dim} and {value_dim}"
-        )
-    kd, vd = _lib.KEY_DIM - dim, _lib.VALUE_DIM - value_dim
+    if dim > _lib.KEY_DIM:
+        raise ValueError(f"key widths must be <= {_lib.KEY_DIM}; got {dim}")
+    width = _value_width(value_dim)
+    kd, vd = _lib.KEY_DIM - dim, width - value_dim
     padded = SelectiveState(
         F.pad(evidence.to(torch.float32), (0, kd, 0, kd)).contiguous(),
         F.pad(cross.to(torch.float32), (0, kd, 0, vd)).contiguous(),
@@ -335,7 +344,7 @@ def selective_decode(state, key, value, query, beta, log_decay, floor, solver=No
     out = selective_decode_(
         padded,
         _pad_last(torch.as_tensor(key, device=device).to(torch.float32), _lib.KEY_DIM),
-        _pad_last(torch.as_tensor(value, device=device).to(torch.float32), _lib.VALUE_DIM),
+        _pad_last(torch.as_tensor(value, device=device).to(torch.float32), width),
         _pad_last(torch.as_tensor(query, device=device).to(torch.float32), _lib.KEY_DIM),
         beta,
         log_decay,
@@ -354,7 +363,7 @@ def selective_decode(state, key, value, query, beta, log_decay, floor, solver=No
 def selective_decode_(state, key, value, query, beta, log_decay, floor, solver=None):
     """In-place ``selective_decode``: overwrites ``state`` with the new state.
 
-    Needs float32 contiguous state tensors with D = P = 64.
+    Needs float32 contiguous state tensors with D = 64 and P = 64 or 128.
     """
     _check_solver(solver)
     lib = _lib.load()
@@ -362,8 +371,8 @@ def selective_decode_(state, key, value, query, beta, log_decay, floor, solver=N
     _require_device(evidence, cross)
     batch, heads, dim, _ = evidence.shape
     value_dim = cross.shape[-2]
-    if (dim, value_dim) != (_lib.KEY_DIM, _lib.VALUE_DIM):
-        raise ValueError("the in-place decode needs D = P = 64 states")
+    if dim != _lib.KEY_DIM or value_dim not in (_lib.VALUE_DIM, _lib.MAX_VALUE_DIM):
+        raise ValueError("the in-place decode needs D = 64 and P = 64 or 128 states")
     if evidence.dtype != torch.float32 or not evidence.is_contiguous() or not cross.is_contiguous():
         raise ValueError("the in-place decode needs contiguous float32 states")
     device = evidence.device
@@ -378,7 +387,7 @@ def selective_decode_(state, key, value, query, beta, log_decay, floor, solver=N
         _lib.check(
             lib.m4mr_decode_step(
                 _ptr(evidence), _ptr(cross), _ptr(key), _ptr(value), _ptr(query),
-                _ptr(beta), _ptr(log_decay), _ptr(floor), batch * heads, heads,
+                _ptr(beta), _ptr(log_decay), _ptr(floor), batch * heads, heads, value_dim,
                 _ptr(output), _ptr(variance), _stream(),
             )
         )

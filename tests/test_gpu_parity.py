@@ -193,7 +193,7 @@ def test_stored_factors_reproduce_each_precision(gpu_lib):
     )
     announce("C-ABI forward, factor unpack B2 T10 H2 D64")
     rc = gpu_lib.m4mr_forward(
-        *(t.data_ptr() for t in ins), None, None, B, T, H, c,
+        *(t.data_ptr() for t in ins), None, None, B, T, H, 64, c,
         *(t.data_ptr() for t in outs.values()), torch.cuda.current_stream().cuda_stream,
     )
     assert rc == 0, gpu_lib.m4mr_last_error()
@@ -313,3 +313,62 @@ def test_ragged_lengths_and_empty_sub_chunks(gpu_lib, time, chunk):
     want = oracle.dense_reference(*(data[n] for n in NAMES))
     for key, ref in zip(["output", "variance", "evidence", "cross"], want):
         assert normwise(got[key], ref) <= 1e-5, (key, time, chunk)
+
+
+@pytest.mark.parametrize("value_dim,chunk", [(128, 64), (100, 16), (128, 5)])
+def test_wide_value_heads_forward_and_gradients(gpu_lib, value_dim, chunk):
+    """P = 128 value heads, the reference's trained memory_head_dim
+    (lm/configs/mamba4-60m.json, mamba4-125m.json): every value-dependent
+    product runs per 64-column value tile.  P = 100 is zero-padded to 128."""
+    data = arrays(time=150, heads=2, dim=64, value_dim=value_dim, seed=21)
+    rng = np.random.default_rng(22)
+    root = rng.normal(size=(2, 2, 64, 64)) / 64
+    s0 = (root @ np.swapaxes(root, -1, -2)).astype(np.float32)
+    c0 = (rng.normal(size=(2, 2, value_dim, 64)) * 0.3).astype(np.float32)
+    d_out = rng.normal(size=data["values"].shape).astype(np.float32)
+    d_var = rng.normal(size=data["beta"].shape).astype(np.float32)
+    d_s = rng.normal(size=s0.shape).astype(np.float32)
+    d_s = 0.5 * (d_s + np.swapaxes(d_s, -1, -2))
+    d_c = rng.normal(size=c0.shape).astype(np.float32)
+    announce(f"wide values P={value_dim} chunk={chunk} B2 T150 H2 D64")
+    got = run_gpu(data, chunk=chunk, initial=(s0, c0), cotangents=(d_out, d_var, d_s, d_c))
+    args = [data[n].astype(np.float64) for n in NAMES]
+    (out, var, s_end, c_end), res = oracle.forward(*args, chunk=chunk, initial=(s0, c0))
+    for key, ref in zip(["output", "variance", "evidence", "cross"], (out, var, s_end, c_end)):
+        assert normwise(got[key], ref) <= 1e-4, key
+    want = oracle.backward(res, d_out, d_var, d_s, d_c)
+    for n in NAMES:
+        assert normwise(got["d_" + n], want[n]) <= 1e-3, n
+    assert normwise(got["d_initial_evidence"], want["initial_evidence"]) <= 1e-3
+    assert normwise(got["d_initial_cross"], want["initial_cross"]) <= 1e-3
+
+
+def test_wide_value_heads_decode_in_place(gpu_lib):
+    from mamba4_amd import SelectiveState, selective_decode, selective_decode_
+
+    pre = arrays(time=40, heads=4, dim=64, value_dim=128, seed=32, batch=3)
+    _, _, s, c = oracle.dense_reference(*(pre[n] for n in NAMES))
+    s, c = s.astype(np.float32), c.astype(np.float32)
+    dev = torch.device("cuda:0")
+    state = SelectiveState(torch.tensor(s, device=dev), torch.tensor(c, device=dev))
+    want_s, want_c = s.astype(np.float64), c.astype(np.float64)
+    tok = arrays(time=3, heads=4, dim=64, value_dim=128, seed=33, batch=3)
+    tok["floor"] = pre["floor"]
+    announce("in-place decode P=128 B3 H4 D64, 3 steps")
+    for i in range(3):
+        args = [tok[n][:, i] if n != "floor" else tok[n] for n in NAMES]
+        step = selective_decode_(state, *(torch.tensor(a, device=dev) for a in args))
+        out, var, want_s, want_c = oracle.decode_step(want_s, want_c, *args)
+        assert normwise(host(step.output), out) <= 1e-4, i
+        assert normwise(host(step.variance), var) <= 1e-4, i
+    assert normwise(host(state.evidence), want_s) <= 1e-5
+    assert normwise(host(state.cross), want_c) <= 1e-5
+    # A narrower value width (96) pads to 128 on the copying path.
+    narrow = SelectiveState(torch.tensor(s, device=dev), torch.tensor(c[:, :, :96], device=dev))
+    args = [tok[n][:, 0] if n != "floor" else tok[n] for n in NAMES]
+    args[1] = args[1][..., :96]
+    step = selective_decode(narrow, *(torch.tensor(a, device=dev) for a in args))
+    out, var, _, _ = oracle.decode_step(s.astype(np.float64), c[:, :, :96].astype(np.float64),
+                                        *args)
+    assert normwise(host(step.output), out) <= 1e-4
+    assert normwise(host(step.variance), var) <= 1e-4

@@ -29,17 +29,23 @@ def test_version_and_kernel_names():
 def test_invalid_sizes_are_rejected_before_any_launch():
     lib = _lib.load()
     null = ctypes.c_void_p(0)
-    rc = lib.m4mr_forward(*([null] * 8), 0, 16, 1, 64, *([null] * 8), null)
+    rc = lib.m4mr_forward(*([null] * 8), 0, 16, 1, 64, 64, *([null] * 8), null)
     assert rc == _lib.EINVAL
     assert "positive" in lib.m4mr_last_error().decode()
-    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 65, *([null] * 8), null)
+    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 64, 65, *([null] * 8), null)
     assert rc == _lib.EINVAL
     assert "chunk" in lib.m4mr_last_error().decode()
-    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 16, *([null] * 8), null)
+    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 96, 16, *([null] * 8), null)
+    assert rc == _lib.EINVAL
+    assert "value_dim" in lib.m4mr_last_error().decode()
+    rc = lib.m4mr_forward(*([null] * 8), 1, 16, 1, 128, 16, *([null] * 8), null)
     assert rc == _lib.EINVAL
     assert "NULL" in lib.m4mr_last_error().decode()
-    rc = lib.m4mr_decode_step(*([null] * 8), 6, 4, null, null, null)
+    rc = lib.m4mr_decode_step(*([null] * 8), 6, 4, 64, null, null, null)
     assert rc == _lib.EINVAL
+    rc = lib.m4mr_decode_step(*([null] * 8), 8, 4, 32, null, null, null)
+    assert rc == _lib.EINVAL
+    assert "value_dim" in lib.m4mr_last_error().decode()
     with pytest.raises(ValueError):
         _lib.check(_lib.EINVAL)
 
@@ -47,11 +53,14 @@ def test_invalid_sizes_are_rejected_before_any_launch():
 def test_workspace_size_covers_every_intermediate():
     B, T, H, c = 2, 100, 3, 16
     count = -(-T // c)
-    need = _lib.load().m4mr_backward_workspace_bytes(B, T, H, c)
-    floats = B * T * H * 64 + 2 * B * H * count * 4096 + B * H * count * 64
-    assert need >= 4 * floats
-    assert need % 256 == 0
-    assert _lib.load().m4mr_backward_workspace_bytes(B, T, H, 0) == 0
+    for width in (64, 128):
+        need = _lib.load().m4mr_backward_workspace_bytes(B, T, H, width, c)
+        tiles = width // 64
+        floats = B * T * H * 64 + (1 + tiles) * B * H * count * 4096 + B * H * count * 64
+        assert need >= 4 * floats
+        assert need % 256 == 0
+    assert _lib.load().m4mr_backward_workspace_bytes(B, T, H, 64, 0) == 0
+    assert _lib.load().m4mr_backward_workspace_bytes(B, T, H, 80, c) == 0
 
 
 def test_python_api_rejects_cpu_tensors_and_unknown_solvers():

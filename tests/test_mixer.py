@@ -321,7 +321,8 @@ def test_gpu_epilogue_matches_oracle(gpu_lib, value_dim):
 
 
 @pytest.mark.gpu
-def test_gpu_mixer_memory_path_end_to_end(gpu_lib):
+@pytest.mark.parametrize("value_dim", [64, 128])
+def test_gpu_mixer_memory_path_end_to_end(gpu_lib, value_dim):
     """memory_inputs -> selective_gaussian_memory -> gated_read, the memory
     path of SelectiveMemoryMixer.__call__ (lm/models/mamba4.py:183-273), with
     gradients for every raw input and parameter against the composed float64
@@ -330,9 +331,8 @@ def test_gpu_mixer_memory_path_end_to_end(gpu_lib):
     from mamba4_amd import gated_read, memory_inputs, selective_gaussian_memory
     from oracle import memread
 
-    announce("mixer memory path end to end")
-    x = raw_inputs(batch=2, time=80, heads=2, dim=64, value_dim=64, seed=13)
-    x["value"] = x["value"][:, :80]
+    announce(f"mixer memory path end to end value_dim={value_dim}")
+    x = raw_inputs(batch=2, time=80, heads=2, dim=64, value_dim=value_dim, seed=13)
     names = PROLOGUE_ARGS + ["value", "confidence_scale", "skip"]
     t = _gpu(x, names, grad=True)
     inputs = memory_inputs(*(t[n] for n in PROLOGUE_ARGS), beta_max=BETA_MAX,
