@@ -255,6 +255,8 @@ int m4mr_epilogue_backward(const float* read, const float* variance, const float
  * (see m4mr_profile_kernel_name), then m4mr_profile_reset() clears them.
  */
 void m4mr_profile_enable(int on);
+/* Time only launches of `kernel` (NULL or "": every kernel). */
+void m4mr_profile_select(const char* kernel);
 void m4mr_profile_reset(void);
 int m4mr_profile_read(const char* kernel, double* total_ms, long* launches);
 /* Name of the i-th kernel the library launches, NULL past the end. */

@@ -48,6 +48,7 @@ SIGNATURES = {
     "m4mr_epilogue_forward": (_I, [_P] * 5 + [_I] * 4 + [_P, _P]),
     "m4mr_epilogue_backward": (_I, [_P] * 5 + [_I] * 4 + [_P] * 6 + [_P, _S, _P]),
     "m4mr_profile_enable": (None, [_I]),
+    "m4mr_profile_select": (None, [ctypes.c_char_p]),
     "m4mr_profile_reset": (None, []),
     "m4mr_profile_read": (
         _I,
@@ -100,6 +101,11 @@ def check(rc):
 
 def profile_enable(on=True):
     load().m4mr_profile_enable(1 if on else 0)
+
+
+def profile_select(kernel=None):
+    """Time only launches of `kernel` while profiling is on (None: every kernel)."""
+    load().m4mr_profile_select(kernel.encode() if kernel else None)
 
 
 def profile_reset():

@@ -79,7 +79,19 @@ struct ProfRecord {
 };
 std::mutex g_prof_mu;
 bool g_prof_on = false;
+std::string g_prof_only;         // empty: every kernel is timed
 std::vector<ProfRecord> g_prof;
+std::vector<hipEvent_t> g_event_pool;  // events of cleared records, reused
+
+// An event from the pool, or a new one (called with g_prof_mu held).
+hipError_t take_event(hipEvent_t* e) {
+  if (!g_event_pool.empty()) {
+    *e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return hipSuccess;
+  }
+  return hipEventCreate(e);
+}
 
 int fail(int code, const std::string& msg) {
   g_error = msg;
@@ -134,13 +146,12 @@ int launch(const char* name, hipStream_t stream, F&& body) {
   bool prof;
   {
     std::lock_guard<std::mutex> lock(g_prof_mu);
-    prof = g_prof_on;
-  }
-  if (prof) {
-    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess ||
-        hipEventRecord(a, stream) != hipSuccess)
+    prof = g_prof_on && (g_prof_only.empty() || g_prof_only == name);
+    if (prof && (take_event(&a) != hipSuccess || take_event(&b) != hipSuccess))
       return fail(M4MR_EHIP, std::string(name) + ": profiling event setup failed");
   }
+  if (prof && hipEventRecord(a, stream) != hipSuccess)
+    return fail(M4MR_EHIP, std::string(name) + ": profiling event record failed");
   body();
   hipError_t e = hipGetLastError();
   if (prof) {
@@ -612,11 +623,17 @@ void m4mr_profile_enable(int on) {
   g_prof_on = on != 0;
 }
 
+void m4mr_profile_select(const char* kernel) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof_only = kernel ? kernel : "";
+}
+
 void m4mr_profile_reset(void) {
   std::lock_guard<std::mutex> lock(g_prof_mu);
   for (auto& r : g_prof) {
-    (void)hipEventDestroy(r.start);
-    (void)hipEventDestroy(r.stop);
+    (void)hipEventSynchronize(r.stop);
+    g_event_pool.push_back(r.start);
+    g_event_pool.push_back(r.stop);
   }
   g_prof.clear();
 }
