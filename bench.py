@@ -58,6 +58,11 @@ KERNEL_WORK = {
     "bwd_local": ("mfma", 2 * 8192, "flop"),  # Z^T diag Y, dO^T diag Y
     "bwd_scan": ("hbm", 16384 * 2 * 2 // 64, "B"),  # r+w of 1 evidence + 1 cross state / chunk
     "floor_reduce": ("hbm", 4, "B"),
+    # Fused state walks: read k and v (or z, y and dO) once, beta and log
+    # decay, write one evidence state per 32-token sub-chunk (forward) or
+    # chunk and one cross state per chunk: 16 KiB / 32 + 16 KiB / 64.
+    "fwd_states": ("hbm", 256 + 256 + 8 + 512 + 256, "B"),
+    "bwd_states": ("hbm", 3 * 256 + 4 + 256 + 256, "B"),
 }
 
 

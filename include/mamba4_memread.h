@@ -79,6 +79,10 @@ const char* m4mr_last_error(void);
  *          ceil(chunk/2) tokens, so NS = 2*NC, else NS = NC);
  *          start_cross [B,H,NC,P,D], the cross statistics at each chunk start.
  *          m4mr_start_counts() returns NC and NS.
+ * The chunk-boundary states (here and in m4mr_backward) come from one fused
+ * walk per (b, h) state sequence when B*H*(1 + P/64) reaches the device's
+ * compute-unit count, else from chunk-parallel statistics plus a carry; the
+ * environment variable M4MR_STATE_WALK=fused|split overrides the choice.
  */
 int m4mr_forward(const float* keys, const float* values, const float* queries,
                  const float* beta, const float* log_decay, const float* floor,

@@ -6,6 +6,7 @@
 // profiling log (mutex-protected) and a per-thread error message.
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -23,6 +24,8 @@ __global__ void bwd_local_kernel(Dims, const float*, const float*, const float*,
                                  const float*, float*, float*);
 __global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
                                 float*, float*);
+template <bool BWD>
+__global__ void states_kernel(Dims, StateArgs);
 __global__ void fwd_factor_kernel(Dims, const float*, const float*, const float*, const float*,
                                   const float*, const float*, float*, float*);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
@@ -66,8 +69,9 @@ using m4::Dims;
 
 thread_local std::string g_error;
 
-const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_factor", "fwd_read",
-                                    "bwd_dy",         "factored_solve", "bwd_local", "bwd_scan",
+const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states", "fwd_factor",
+                                    "fwd_read",       "bwd_dy",    "factored_solve",
+                                    "bwd_local",      "bwd_scan",  "bwd_states",
                                     "bwd_grads",      "floor_reduce", "decode_step",
                                     "spd_solve",      "spd_backward", "prologue_forward",
                                     "prologue_backward", "epilogue_forward",
@@ -101,6 +105,7 @@ int fail(int code, const std::string& msg) {
 constexpr size_t kStatsLdsBytes = 3 * m4::TILE * sizeof(float);
 constexpr size_t kChunkLdsBytes = 4 * m4::TILE * sizeof(float);
 constexpr size_t kGradsLdsBytes = 7 * m4::TILE * sizeof(float);
+constexpr size_t kStatesLdsBytes = 4 * m4::TILE * sizeof(float);
 
 bool configured = false;
 int g_cus = 256;  // compute units of the device (set by configure())
@@ -123,7 +128,9 @@ int configure() {
              {(const void*)m4::bwd_local_kernel, kChunkLdsBytes},
              {(const void*)m4::fwd_read_kernel, kChunkLdsBytes},
              {(const void*)m4::bwd_dy_kernel, kChunkLdsBytes},
-             {(const void*)m4::bwd_grads_kernel, kGradsLdsBytes}};
+             {(const void*)m4::bwd_grads_kernel, kGradsLdsBytes},
+             {(const void*)m4::states_kernel<false>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<true>, kStatesLdsBytes}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)k.bytes);
@@ -162,6 +169,19 @@ int launch(const char* name, hipStream_t stream, F&& body) {
   }
   if (e != hipSuccess) return fail(M4MR_EHIP, std::string(name) + ": " + hipGetErrorString(e));
   return M4MR_OK;
+}
+
+// The chunk-boundary states run as one fused walk per (b, h) state sequence
+// when there are enough sequences to give every compute unit one; fewer
+// sequences take the chunk-parallel statistics plus a separate carry.  The
+// environment variable M4MR_STATE_WALK = "fused" or "split" overrides the
+// choice (both give the same states up to summation order).
+bool fused_states(int B, int H, const Dims& d) {
+  if (const char* mode = std::getenv("M4MR_STATE_WALK")) {
+    if (std::strcmp(mode, "fused") == 0) return true;
+    if (std::strcmp(mode, "split") == 0) return false;
+  }
+  return (long)B * H * (1 + d.NV) >= g_cus;
 }
 
 bool bad_dims(int B, int T, int H, int P, int chunk, std::string* why) {
@@ -267,16 +287,27 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned seqs = (unsigned)B * H * d.NC;
   const unsigned subseqs = (unsigned)B * H * d.NS;
-  int rc = launch("fwd_stats", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_stats_kernel, dim3(seqs), dim3(256), kStatsLdsBytes, st, d, keys,
-                       values, beta, log_decay, start_evidence, start_cross);
-  });
-  if (rc) return rc;
-  rc = launch("fwd_scan", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d, log_decay,
-                       init_evidence, init_cross, start_evidence, start_cross, final_evidence,
-                       final_cross);
-  });
+  int rc;
+  if (fused_states(B, H, d)) {
+    const m4::StateArgs args{keys,            values,      keys,           beta,   log_decay,
+                             init_evidence,   init_cross,  start_evidence, start_cross,
+                             final_evidence,  final_cross};
+    rc = launch("fwd_states", st, [&] {
+      hipLaunchKernelGGL(m4::states_kernel<false>, dim3(B * H, 1 + d.NV), dim3(512),
+                         kStatesLdsBytes, st, d, args);
+    });
+  } else {
+    rc = launch("fwd_stats", st, [&] {
+      hipLaunchKernelGGL(m4::fwd_stats_kernel, dim3(seqs), dim3(256), kStatsLdsBytes, st, d,
+                         keys, values, beta, log_decay, start_evidence, start_cross);
+    });
+    if (rc) return rc;
+    rc = launch("fwd_scan", st, [&] {
+      hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d,
+                         log_decay, init_evidence, init_cross, start_evidence, start_cross,
+                         final_evidence, final_cross);
+    });
+  }
   if (rc) return rc;
   rc = launch("fwd_factor", st, [&] {
     hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3((subseqs + 3) / 4), dim3(128), 0, st, d, keys,
@@ -350,16 +381,26 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
                        st, factors, ws.z, ws.z, tokens);
   });
   if (rc) return rc;
-  rc = launch("bwd_local", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_local_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, beta,
-                       log_decay, solved, ws.z, d_output, ws.end_s, ws.end_c);
-  });
-  if (rc) return rc;
-  rc = launch("bwd_scan", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d, log_decay,
-                       d_final_evidence, d_final_cross, ws.end_s, ws.end_c, d_init_evidence,
-                       d_init_cross);
-  });
+  if (fused_states(B, H, d)) {
+    const m4::StateArgs args{ws.z,             d_output,       solved,   beta,   log_decay,
+                             d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
+                             d_init_evidence,  d_init_cross};
+    rc = launch("bwd_states", st, [&] {
+      hipLaunchKernelGGL(m4::states_kernel<true>, dim3(B * H, 1 + d.NV), dim3(512),
+                         kStatesLdsBytes, st, d, args);
+    });
+  } else {
+    rc = launch("bwd_local", st, [&] {
+      hipLaunchKernelGGL(m4::bwd_local_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d,
+                         beta, log_decay, solved, ws.z, d_output, ws.end_s, ws.end_c);
+    });
+    if (rc) return rc;
+    rc = launch("bwd_scan", st, [&] {
+      hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d,
+                         log_decay, d_final_evidence, d_final_cross, ws.end_s, ws.end_c,
+                         d_init_evidence, d_init_cross);
+    });
+  }
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
     hipLaunchKernelGGL(m4::bwd_grads_kernel, dim3(seqs), dim3(512), kGradsLdsBytes, st, d, keys,

@@ -335,4 +335,19 @@ struct TileRegsT {
   }
 };
 
+// Arguments of the fused chunk-boundary state walk (states_kernel).
+struct StateArgs {
+  const float* rows_a;   // evidence a rows: forward keys (unused), backward z
+  const float* rows_ac;  // cross a rows: forward values, backward d_output
+  const float* rows_b;   // b rows: forward keys, backward solved
+  const float* beta;
+  const float* log_decay;
+  const float* first_s;  // state before the first step (NULL: zero)
+  const float* first_c;
+  float* steps_s;        // the state each step starts from
+  float* steps_c;
+  float* last_s;         // the state after the last step
+  float* last_c;
+};
+
 }  // namespace m4

@@ -261,4 +261,164 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
   *reinterpret_cast<f4*>(dinit + (long)bh * size + elem) = running;
 }
 
+// ---------------------------------------------------------------------------
+// Fused statistics and carry, for batches with enough (b, h) sequences to
+// fill the chip.  One 512-thread block walks one state sequence of one (b, h)
+// in order, keeping the carried state in its MFMA accumulators: blockIdx.y 0
+// is the evidence (sub-chunk steps forward, chunk steps backward), y = 1 + v
+// cross tile v (chunk steps).  Each step stores the state it starts from,
+// then takes state = decay * state + sum_t wt_t a_t b_t^T over the step's
+// tokens; the statistics never go through HBM.
+//   forward:  a = key (evidence) or value tile, b = key,
+//             wt = beta_t exp(P_last - P_t);  states ascend from init.
+//   backward: evidence a, b = (z, y) and (y, z) with wt = -exp(P_t) / 2,
+//             cross a = d_output tile, b = y with wt = exp(P_t);  states
+//             descend from the final-state cotangent (the transpose of the
+//             forward carry, as bwd_local_kernel + bwd_scan_kernel).
+// The next step's rows load into registers while the current step multiplies;
+// LDS holds two step buffers, so each step takes one barrier.
+// Wave w computes rows 16 (w % 4) .. +15 and column quads' halves w / 4 of
+// the 64x64 state tile.
+
+constexpr int STATES_THREADS = 512;
+
+struct alignas(16) StepBuffer {  // wt is read as float4
+  float wt[MAXC];
+  float decay;
+  int count;
+};
+
+// Tokens of step i: a sub-chunk of the forward evidence, else a chunk.
+__device__ __forceinline__ void step_span(const Dims& d, int i, bool sub, int& first, int& cnt) {
+  if (sub) {
+    const int n = i / d.rsub, u = i % d.rsub;
+    first = n * d.chunk + sub_first(d, u);
+    cnt = sub_len(d, n, u);
+  } else {
+    first = i * d.chunk;
+    cnt = chunk_len(d, i);
+  }
+}
+
+// acc += (A diag(wt))^T-by-B over k in [k0, k0 + 16) for rows 16 s.. of the
+// result and its columns 4r + 2hf + j (j = 0, 1): A(i, k) = A[k][16s + i]
+// wt[k], B(k, c) = B[k][c] (the tile_mma_half QUAD convention).
+__device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const float* B,
+                                               const float* wt, int k0, int s, int hf) {
+  const int l = lane_id(), r = l & 15, kk = k0 + 4 * (l >> 4);
+  const f4 t = *reinterpret_cast<const f4*>(wt + kk);
+  f4 a;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) a[e] = A[(kk + e) * LDT + 16 * s + r] * t[e];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float2 b = *reinterpret_cast<const float2*>(B + (kk + e) * LDT + 4 * r + 2 * hf);
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b.x, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b.y, acc[1], 0, 0, 0);
+  }
+}
+
+template <bool BWD>
+__global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArgs g) {
+  extern __shared__ float smem[];  // buffer u: b tile at 2u TILE, a tile at (2u + 1) TILE
+  __shared__ StepBuffer sb[2];
+  const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
+  const bool cross = blockIdx.y > 0;
+  const int v = cross ? (int)blockIdx.y - 1 : 0;
+  const bool sub = !BWD && !cross;
+  const int steps = sub ? d.NS : d.NC;
+  // Evidence a rows: the keys themselves (forward) or z (backward).
+  const bool own_a = cross || BWD;
+  const int w = threadIdx.x >> 6, s = w & 3, hf = w >> 2, l = lane_id();
+  const int elem = (16 * s + 4 * (l >> 4)) * 64 + 4 * (l & 15) + 2 * hf;  // + 64 q + j
+
+  auto step_index = [&](int i) {
+    return cross ? ((long)bh * d.NC + i) * d.NV + v : (long)bh * steps + i;
+  };
+  const long edge = cross ? (long)bh * d.NV + v : bh;
+
+  f4 acc[2];
+  zero2(acc);
+  if (const float* first = cross ? g.first_c : g.first_s) {
+    const float* src = first + edge * 4096 + elem;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float2 x = *reinterpret_cast<const float2*>(src + 64 * q);
+      acc[0][q] = x.x;
+      acc[1][q] = x.y;
+    }
+  }
+
+  TileRegs2 ra, rb;
+  float pg = 0.f, pb = 0.f;
+  auto fetch = [&](int i) {
+    int first, cnt;
+    step_span(d, i, sub, first, cnt);
+    rb.fetch_rows(cnt, [&](int r) { return g.rows_b + token_head(d, b, first + r, h) * 64; });
+    if (own_a) {
+      const int width = cross ? d.P : 64, offset = cross ? 64 * v : 0;
+      ra.fetch_rows(cnt, [&](int r) {
+        return (cross ? g.rows_ac : g.rows_a) + token_head(d, b, first + r, h) * width + offset;
+      });
+    }
+    if (w == 0) {
+      pg = 0.f;
+      pb = 0.f;
+      if (l < cnt) {
+        const long th = token_head(d, b, first + l, h);
+        pg = g.log_decay[th];
+        if (!BWD) pb = g.beta[th];
+      }
+    }
+  };
+  auto stage = [&](int u, int i) {
+    rb.store(smem + 2 * u * TILE);
+    if (own_a) ra.store(smem + (2 * u + 1) * TILE);
+    if (w == 0) {
+      const float p = wave_inclusive_sum(pg), last = __shfl(p, 63, 64);
+      sb[u].wt[l] = BWD ? (cross ? 1.f : -0.5f) * expf(p) : pb * expf(last - p);
+      if (l == 0) {
+        int first, cnt;
+        step_span(d, i, sub, first, cnt);
+        sb[u].decay = expf(last);
+        sb[u].count = cnt;
+      }
+    }
+  };
+
+  int i = BWD ? steps - 1 : 0;
+  const int stride = BWD ? -1 : 1;
+  fetch(i);
+  stage(0, i);
+  __syncthreads();
+  for (int k = 0; k < steps; ++k, i += stride) {
+    const int u = k & 1;
+    const bool more = k + 1 < steps;
+    if (more) fetch(i + stride);
+    float* dst = (cross ? g.steps_c : g.steps_s) + step_index(i) * 4096 + elem;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+    const float dk = sb[u].decay;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[j] *= dk;
+    const float* tb = smem + 2 * u * TILE;
+    const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
+    const int kt = k_terms(sb[u].count);
+    for (int k0 = 0; k0 < kt; k0 += 16) {
+      weighted_block(acc, ta, tb, sb[u].wt, k0, s, hf);
+      if (BWD && !cross) weighted_block(acc, tb, ta, sb[u].wt, k0, s, hf);
+    }
+    if (more) stage(u ^ 1, i + stride);
+    __syncthreads();
+  }
+  float* dst = (cross ? g.last_c : g.last_s) + edge * 4096 + elem;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+}
+
+template __global__ void states_kernel<false>(Dims, StateArgs);
+template __global__ void states_kernel<true>(Dims, StateArgs);
+
 }  // namespace m4

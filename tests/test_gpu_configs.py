@@ -10,10 +10,13 @@ properties are checked on every row:
 * the shifted first token has a zero key, so its variance is
   sum(q^2 / floor) and its read is zero (lm/tests/test_mamba4.py:364-375);
 * a one-row slice run on its own reproduces that row of the full batch
-  bit for bit (rows share no state).
+  bit for bit (rows share no state), on the same chunk-boundary state walk
+  as the full batch took.
 Tolerance: normwise max|d| / max|ref| <= 1e-4 on outputs, <= 1e-3 on
 gradients.
 """
+
+import os
 
 import numpy as np
 import pytest
@@ -44,12 +47,29 @@ def check_properties(data, got):
 def run_config(name, oracle_row, grad_tol=1e-3):
     data = workload_inputs(name, seed=0, cotangents=True)
     cot = (data["d_output"], data["d_variance"], None, None)
+    from mamba4_amd import _lib
+
     announce(f"{name} full size fwd+bwd")
-    full = run_gpu(data, chunk=64, cotangents=_cotangents(data))
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    try:
+        full = run_gpu(data, chunk=64, cotangents=_cotangents(data))
+    finally:
+        _lib.profile_enable(False)
+    walk = "fused" if _lib.profile_read("fwd_states")[1] else "split"
+    _lib.profile_reset()
     check_properties(data, full)
-    announce(f"{name} one-row slice")
+    announce(f"{name} one-row slice, {walk} state walk")
     sliced = rows_of(data, slice(oracle_row, oracle_row + 1))
-    one = run_gpu(sliced, chunk=64, cotangents=_cotangents(sliced))
+    saved = os.environ.get("M4MR_STATE_WALK")
+    os.environ["M4MR_STATE_WALK"] = walk
+    try:
+        one = run_gpu(sliced, chunk=64, cotangents=_cotangents(sliced))
+    finally:
+        if saved is None:
+            del os.environ["M4MR_STATE_WALK"]
+        else:
+            os.environ["M4MR_STATE_WALK"] = saved
     for key in ["output", "variance", "evidence", "cross", "d_keys", "d_values",
                 "d_queries", "d_beta", "d_log_decay"]:
         np.testing.assert_array_equal(one[key][0], full[key][oracle_row], err_msg=key)

@@ -372,3 +372,99 @@ def test_wide_value_heads_decode_in_place(gpu_lib):
                                         *args)
     assert normwise(host(step.output), out) <= 1e-4
     assert normwise(host(step.variance), var) <= 1e-4
+
+
+
+@pytest.fixture(params=["split", "fused"])
+def state_walk(request, monkeypatch):
+    """Both chunk-boundary state paths (M4MR_STATE_WALK), forced at any size."""
+    monkeypatch.setenv("M4MR_STATE_WALK", request.param)
+    return request.param
+
+
+@pytest.mark.parametrize("value_dim,chunk,time", [(5, 4, 21), (64, 64, 90), (128, 48, 100)])
+def test_state_walks_match_oracle(gpu_lib, state_walk, value_dim, chunk, time):
+    """Forward and every gradient through either state path, with an initial
+    state and final-state cotangents: ragged last chunks with an empty second
+    sub-chunk (T = 90, 100), P = 128, and chunks without sub-chunks (4)."""
+    from mamba4_amd import _lib
+
+    dim = 6 if value_dim == 5 else 64
+    data = arrays(time=time, heads=3, dim=dim, value_dim=value_dim, seed=time)
+    rng = np.random.default_rng(time + 1)
+    root = rng.normal(size=(2, 3, dim, dim)) / dim
+    s0 = (root @ np.swapaxes(root, -1, -2)).astype(np.float32)
+    c0 = (rng.normal(size=(2, 3, value_dim, dim)) * 0.3).astype(np.float32)
+    d_out = rng.normal(size=data["values"].shape).astype(np.float32)
+    d_var = rng.normal(size=data["beta"].shape).astype(np.float32)
+    d_s = rng.normal(size=s0.shape).astype(np.float32)
+    d_s = 0.5 * (d_s + np.swapaxes(d_s, -1, -2))
+    d_c = rng.normal(size=c0.shape).astype(np.float32)
+    announce(f"state walk {state_walk} P={value_dim} chunk={chunk} T={time} B2 H3 D{dim}")
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    try:
+        got = run_gpu(data, chunk=chunk, initial=(s0, c0), cotangents=(d_out, d_var, d_s, d_c))
+    finally:
+        _lib.profile_enable(False)
+    ran = {k: _lib.profile_read(k)[1] for k in ("fwd_states", "bwd_states", "fwd_scan", "bwd_scan")}
+    _lib.profile_reset()
+    fused = state_walk == "fused"
+    assert ran == {"fwd_states": int(fused), "bwd_states": int(fused),
+                   "fwd_scan": int(not fused), "bwd_scan": int(not fused)}, ran
+    args = [data[n].astype(np.float64) for n in NAMES]
+    (out, var, s_end, c_end), res = oracle.forward(*args, chunk=chunk, initial=(s0, c0))
+    for key, ref in zip(["output", "variance", "evidence", "cross"], (out, var, s_end, c_end)):
+        assert normwise(got[key], ref) <= 1e-5, key
+    want = oracle.backward(res, d_out, d_var, d_s, d_c)
+    for n in NAMES:
+        assert normwise(got["d_" + n], want[n]) <= 1e-4, n
+    assert normwise(got["d_initial_evidence"], want["initial_evidence"]) <= 1e-4
+    assert normwise(got["d_initial_cross"], want["initial_cross"]) <= 1e-4
+
+
+def test_state_walk_choice_at_full_batch(gpu_lib, monkeypatch):
+    """At B*H*(1 + P/64) >= compute units the fused walk is the default, and
+    both walks agree on every output and gradient (summation order only)."""
+    from mamba4_amd import _lib
+
+    batch, heads, time = 32, 8, 70
+    data = arrays(time=time, heads=heads, dim=64, value_dim=64, seed=5, batch=batch)
+    data["floor"] = np.full_like(data["floor"], 0.05)
+    rng = np.random.default_rng(6)
+    cot = (rng.normal(size=data["values"].shape).astype(np.float32),
+           rng.normal(size=data["beta"].shape).astype(np.float32),
+           np.zeros((batch, heads, 64, 64), np.float32),
+           np.zeros((batch, heads, 64, 64), np.float32))
+    results = {}
+    for mode in ["auto", "split"]:
+        if mode == "auto":
+            monkeypatch.delenv("M4MR_STATE_WALK", raising=False)
+        else:
+            monkeypatch.setenv("M4MR_STATE_WALK", mode)
+        announce(f"state walk {mode} B{batch} H{heads} T{time}")
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        try:
+            results[mode] = run_gpu(data, chunk=64, cotangents=cot)
+        finally:
+            _lib.profile_enable(False)
+        results[mode + "_fused"] = _lib.profile_read("fwd_states")[1]
+        _lib.profile_reset()
+    assert results["auto_fused"] == 1 and results["split_fused"] == 0
+    # Rounding differences of the two summation orders, amplified by the
+    # solves in the gradients (floor 0.05).
+    for key, ref in results["split"].items():
+        assert normwise(results["auto"][key], ref) <= (1e-4 if key.startswith("d_") else 1e-5), key
+    # The final state against a float64 recurrence of the same inputs.
+    k, v = data["keys"].astype(np.float64), data["values"].astype(np.float64)
+    lam = np.exp(data["log_decay"].astype(np.float64))
+    b = data["beta"].astype(np.float64)
+    s = np.zeros((batch, heads, 64, 64))
+    c = np.zeros((batch, heads, 64, 64))
+    for t in range(time):
+        kt = k[:, t]
+        s = lam[:, t, :, None, None] * s + b[:, t, :, None, None] * kt[..., :, None] * kt[..., None, :]
+        c = lam[:, t, :, None, None] * c + b[:, t, :, None, None] * v[:, t][..., :, None] * kt[..., None, :]
+    assert normwise(results["auto"]["evidence"], s) <= 1e-5
+    assert normwise(results["auto"]["cross"], c) <= 1e-5
