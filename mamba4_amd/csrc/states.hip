@@ -264,41 +264,32 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
 // ---------------------------------------------------------------------------
 // Fused statistics and carry, for batches with enough (b, h) sequences to
 // fill the chip.  One 512-thread block walks one state sequence of one (b, h)
-// in order, keeping the carried state in its MFMA accumulators: blockIdx.y 0
-// is the evidence (sub-chunk steps forward, chunk steps backward), y = 1 + v
-// cross tile v (chunk steps).  Each step stores the state it starts from,
-// then takes state = decay * state + sum_t wt_t a_t b_t^T over the step's
-// tokens; the statistics never go through HBM.
+// chunk by chunk, keeping the carried state in its MFMA accumulators:
+// blockIdx.y 0 is the evidence, y = 1 + v cross tile v.  Each chunk (each
+// sub-chunk, for the forward evidence) stores the state it starts from, then
+// takes state = decay * state + sum_t wt_t a_t b_t^T over its tokens; the
+// statistics never go through HBM.
 //   forward:  a = key (evidence) or value tile, b = key,
 //             wt = beta_t exp(P_last - P_t);  states ascend from init.
 //   backward: evidence a, b = (z, y) and (y, z) with wt = -exp(P_t) / 2,
 //             cross a = d_output tile, b = y with wt = exp(P_t);  states
 //             descend from the final-state cotangent (the transpose of the
 //             forward carry, as bwd_local_kernel + bwd_scan_kernel).
-// The next step's rows load into registers while the current step multiplies;
-// LDS holds two step buffers, so each step takes one barrier.
+// A step's rows load into registers two steps before it multiplies; LDS
+// holds two step buffers, so each step takes one barrier.
 // Wave w computes rows 16 (w % 4) .. +15 and column quads' halves w / 4 of
 // the 64x64 state tile.
 
 constexpr int STATES_THREADS = 512;
 
+// One chunk step in LDS: per part (the forward evidence's sub-chunks, else
+// the whole chunk) the token weights, zero outside the part, the decay over
+// the part and its token range [lo, hi).
 struct alignas(16) StepBuffer {  // wt is read as float4
-  float wt[MAXC];
-  float decay;
-  int count;
+  float wt[2][MAXC];
+  float decay[2];
+  int lo[2], hi[2];
 };
-
-// Tokens of step i: a sub-chunk of the forward evidence, else a chunk.
-__device__ __forceinline__ void step_span(const Dims& d, int i, bool sub, int& first, int& cnt) {
-  if (sub) {
-    const int n = i / d.rsub, u = i % d.rsub;
-    first = n * d.chunk + sub_first(d, u);
-    cnt = sub_len(d, n, u);
-  } else {
-    first = i * d.chunk;
-    cnt = chunk_len(d, i);
-  }
-}
 
 // acc += (A diag(wt))^T-by-B over k in [k0, k0 + 16) for rows 16 s.. of the
 // result and its columns 4r + 2hf + j (j = 0, 1): A(i, k) = A[k][16s + i]
@@ -325,15 +316,18 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
   const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
   const bool cross = blockIdx.y > 0;
   const int v = cross ? (int)blockIdx.y - 1 : 0;
-  const bool sub = !BWD && !cross;
-  const int steps = sub ? d.NS : d.NC;
+  // The forward evidence stores a state per sub-chunk: its chunk steps have
+  // rsub parts.
+  const int parts = !BWD && !cross ? d.rsub : 1;
+  const int steps = d.NC;
   // Evidence a rows: the keys themselves (forward) or z (backward).
   const bool own_a = cross || BWD;
   const int w = threadIdx.x >> 6, s = w & 3, hf = w >> 2, l = lane_id();
   const int elem = (16 * s + 4 * (l >> 4)) * 64 + 4 * (l & 15) + 2 * hf;  // + 64 q + j
 
-  auto step_index = [&](int i) {
-    return cross ? ((long)bh * d.NC + i) * d.NV + v : (long)bh * steps + i;
+  // The state stored before part `part` of chunk n.
+  auto state_index = [&](int n, int part) {
+    return cross ? ((long)bh * d.NC + n) * d.NV + v : ((long)bh * d.NC + n) * parts + part;
   };
   const long edge = cross ? (long)bh * d.NV + v : bh;
 
@@ -349,68 +343,91 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     }
   }
 
-  TileRegs2 ra, rb;
-  float pg = 0.f, pb = 0.f;
-  auto fetch = [&](int i) {
-    int first, cnt;
-    step_span(d, i, sub, first, cnt);
-    rb.fetch_rows(cnt, [&](int r) { return g.rows_b + token_head(d, b, first + r, h) * 64; });
+  // Rows and scalars of one step on their way from HBM to LDS.  Two sets
+  // rotate, so a step's loads are issued two steps before it multiplies.
+  struct StepRegs {
+    TileRegs2 ra, rb;
+    float pg, pb;
+  };
+  auto fetch = [&](StepRegs& R, int i) {
+    const int first = i * d.chunk, cnt = chunk_len(d, i);
+    R.rb.fetch_rows(cnt, [&](int r) { return g.rows_b + token_head(d, b, first + r, h) * 64; });
     if (own_a) {
       const int width = cross ? d.P : 64, offset = cross ? 64 * v : 0;
-      ra.fetch_rows(cnt, [&](int r) {
+      R.ra.fetch_rows(cnt, [&](int r) {
         return (cross ? g.rows_ac : g.rows_a) + token_head(d, b, first + r, h) * width + offset;
       });
     }
-    if (w == 0) {
-      pg = 0.f;
-      pb = 0.f;
-      if (l < cnt) {
-        const long th = token_head(d, b, first + l, h);
-        pg = g.log_decay[th];
-        if (!BWD) pb = g.beta[th];
-      }
+    R.pg = 0.f;
+    R.pb = 0.f;
+    if (w == 0 && l < cnt) {
+      const long th = token_head(d, b, first + l, h);
+      R.pg = g.log_decay[th];
+      if (!BWD) R.pb = g.beta[th];
     }
   };
-  auto stage = [&](int u, int i) {
-    rb.store(smem + 2 * u * TILE);
-    if (own_a) ra.store(smem + (2 * u + 1) * TILE);
+  auto stage = [&](const StepRegs& R, int u, int i) {
+    R.rb.store(smem + 2 * u * TILE);
+    if (own_a) R.ra.store(smem + (2 * u + 1) * TILE);
     if (w == 0) {
-      const float p = wave_inclusive_sum(pg), last = __shfl(p, 63, 64);
-      sb[u].wt[l] = BWD ? (cross ? 1.f : -0.5f) * expf(p) : pb * expf(last - p);
+      // Inclusive log-decay prefix over the chunk; part 0 ends at token
+      // `cut` - 1 (the sub-chunk boundary, or the chunk end).
+      const int cnt = chunk_len(d, i), cut = parts == 2 ? min(d.sub, cnt) : cnt;
+      const float p = wave_inclusive_sum(R.pg), last = __shfl(p, 63, 64);
+      const float mid = cut > 0 ? __shfl(p, cut - 1, 64) : 0.f;
+      if (BWD) {
+        sb[u].wt[0][l] = (cross ? 1.f : -0.5f) * expf(p);
+      } else {
+        sb[u].wt[0][l] = l < cut ? R.pb * expf(mid - p) : 0.f;
+        sb[u].wt[1][l] = l >= cut ? R.pb * expf(last - p) : 0.f;
+      }
       if (l == 0) {
-        int first, cnt;
-        step_span(d, i, sub, first, cnt);
-        sb[u].decay = expf(last);
-        sb[u].count = cnt;
+        sb[u].decay[0] = expf(parts == 2 ? mid : last);
+        sb[u].decay[1] = expf(last - mid);
+        sb[u].lo[0] = 0;
+        sb[u].hi[0] = cut;
+        sb[u].lo[1] = cut;
+        sb[u].hi[1] = cnt;
       }
     }
   };
 
-  int i = BWD ? steps - 1 : 0;
-  const int stride = BWD ? -1 : 1;
-  fetch(i);
-  stage(0, i);
+  const int i0 = BWD ? steps - 1 : 0, stride = BWD ? -1 : 1;
+  StepRegs R0, R1;
+  fetch(R0, i0);
+  if (steps > 1) fetch(R1, i0 + stride);
+  stage(R0, 0, i0);
   __syncthreads();
-  for (int k = 0; k < steps; ++k, i += stride) {
-    const int u = k & 1;
-    const bool more = k + 1 < steps;
-    if (more) fetch(i + stride);
-    float* dst = (cross ? g.steps_c : g.steps_s) + step_index(i) * 4096 + elem;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
-    const float dk = sb[u].decay;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[j] *= dk;
+  // Step k multiplies LDS buffer k & 1; `next` holds step k + 1 (staged into
+  // the other buffer at the end), `spare` (step k, already staged) receives
+  // step k + 2.
+  auto step = [&](int k, const StepRegs& next, StepRegs& spare) {
+    const int i = i0 + k * stride, u = k & 1;
+    if (k + 2 < steps) fetch(spare, i + 2 * stride);
     const float* tb = smem + 2 * u * TILE;
     const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
-    const int kt = k_terms(sb[u].count);
-    for (int k0 = 0; k0 < kt; k0 += 16) {
-      weighted_block(acc, ta, tb, sb[u].wt, k0, s, hf);
-      if (BWD && !cross) weighted_block(acc, tb, ta, sb[u].wt, k0, s, hf);
+    for (int part = 0; part < parts; ++part) {
+      float* dst = (cross ? g.steps_c : g.steps_s) + state_index(i, part) * 4096 + elem;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+      const float dk = sb[u].decay[part];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[j] *= dk;
+      // 16-token blocks that hold the part's tokens; the weights are zero
+      // outside the part.
+      const int lo = sb[u].lo[part], hi = lo < sb[u].hi[part] ? sb[u].hi[part] : 0;
+      for (int k0 = lo & ~15; k0 < hi; k0 += 16) {
+        weighted_block(acc, ta, tb, sb[u].wt[part], k0, s, hf);
+        if (BWD && !cross) weighted_block(acc, tb, ta, sb[u].wt[part], k0, s, hf);
+      }
     }
-    if (more) stage(u ^ 1, i + stride);
+    if (k + 1 < steps) stage(next, u ^ 1, i + stride);
     __syncthreads();
+  };
+  for (int k = 0; k < steps; k += 2) {
+    step(k, R1, R0);
+    if (k + 1 < steps) step(k + 1, R0, R1);
   }
   float* dst = (cross ? g.last_c : g.last_s) + edge * 4096 + elem;
 #pragma unroll
