@@ -17,7 +17,12 @@ states are the end states of a 1024-token gated recurrence with
 lambda = sigmoid(N(3,1)), built by this library's own forward, and each step
 writes one new token into every state, refactors and reads.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config2|config4]
+With --workload mixer a step is the memory read's neighbours on the same
+config-2 shape: the mixer prologue (key shift, unit q/k, gates, floor) and
+epilogue (confidence gate, D-skip), and the order head's gated scan, each
+forward and backward; every kernel is HBM-bound and reported against 8 TB/s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config2|config4|mixer]
 """
 
 import argparse
@@ -122,7 +127,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--chunk", type=int, default=64)
-    p.add_argument("--workload", default="config2", choices=["config2", "config4"])
+    p.add_argument("--workload", default="config2", choices=["config2", "config4", "mixer"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -369,6 +374,139 @@ def main_decode(args):
     print(json.dumps(line), flush=True)
 
 
+# Algorithmic HBM bytes per token-head of the mixer-path kernels at D = P = 64
+# (each input read once, each output written once).
+MIXER_METRIC = "mixer-path fwd+bwd tokens/sec at B16 L1024 H8 d64 (prologue, epilogue, order scan)"
+MIXER_WORK = {
+    "prologue_forward": 2 * 256 + 8 + 2 * 256 + 8,
+    "prologue_backward": 2 * 256 + 8 + 2 * 256 + 8 + 2 * 256 + 8,
+    "epilogue_forward": 2 * 256 + 4 + 256,
+    "epilogue_backward": 3 * 256 + 4 + 2 * 256 + 4,
+    "order_forward": 256 + 4 + 256,
+    "order_backward": 3 * 256 + 4 + 256 + 4,
+}
+# Kernels of each step of the mixer workload.
+MIXER_KERNELS = {
+    "prologue_forward": ["prologue_forward"],
+    "prologue_backward": ["prologue_backward", "head_sums"],
+    "epilogue_forward": ["epilogue_forward"],
+    "epilogue_backward": ["epilogue_backward", "head_sums"],
+    "order_forward": ["order_local", "order_carry", "order_apply"],
+    "order_backward": ["order_bwd_local", "order_bwd_carry", "order_bwd_apply"],
+}
+
+
+def main_mixer(args):
+    import torch
+
+    from mamba4_amd import _lib
+
+    lib = _lib.load()
+    check = _lib.check
+    B, T, H, D = 16, 1024, 8, 64
+    gen = torch.Generator(device="cuda:0").manual_seed(0)
+    f32 = dict(dtype=torch.float32, device="cuda:0")
+
+    def rand(*shape):
+        return torch.randn(*shape, generator=gen, **f32)
+
+    key, query, value, read = rand(B, T, H, D), rand(B, T, H, D), rand(B, T, H, D), rand(B, T, H, D)
+    beta_raw, dt_raw, order_raw = rand(B, T, H), rand(B, T, H), rand(B, T, H) + 2
+    variance = rand(B, T, H).abs()
+    beta_bias, dt_bias, a_log, conf, skip = rand(H), rand(H), rand(H) * 0.1, rand(H), rand(H)
+    floor_raw, previous = rand(H, D), rand(B, H, D)
+    log_order = torch.nn.functional.logsigmoid(order_raw)
+    e = torch.empty_like
+    keys, queries, beta, log_decay, floor, shifted = (e(key), e(query), e(beta_raw), e(dt_raw),
+                                                      e(floor_raw), e(previous))
+    g = [e(key), e(query), e(beta_raw), e(dt_raw), e(beta_bias), e(dt_bias), e(a_log),
+         e(floor_raw), e(previous)]
+    out, d_read, d_var, d_value, d_conf, d_skip = e(read), e(read), e(variance), e(value), e(conf), e(skip)
+    ordered, d_vals, d_logs = e(value), e(value), e(log_order)
+    mix_ws = torch.empty(lib.m4mr_mixer_workspace_bytes(B, T, H), dtype=torch.uint8, device="cuda:0")
+    ord_bytes = lib.m4mr_order_workspace_bytes(B, T, H, D, 64)
+    ord_ws = torch.empty(ord_bytes, dtype=torch.uint8, device="cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+
+    def step():
+        check(lib.m4mr_prologue_forward(
+            p(key), p(query), p(beta_raw), p(dt_raw), p(beta_bias), p(dt_bias), p(a_log),
+            p(floor_raw), p(previous), B, T, H, D, 1.0, 0.25, 1, p(keys), p(queries), p(beta),
+            p(log_decay), p(floor), p(shifted), st))
+        check(lib.m4mr_prologue_backward(
+            p(key), p(query), p(beta_raw), p(dt_raw), p(beta_bias), p(dt_bias), p(a_log),
+            p(floor_raw), p(previous), B, T, H, D, 1.0, 1, p(keys), p(queries), p(beta),
+            p(log_decay), p(floor), p(shifted), *(p(t) for t in g), p(mix_ws), mix_ws.numel(), st))
+        check(lib.m4mr_epilogue_forward(p(read), p(variance), p(value), p(conf), p(skip), B, T, H,
+                                        D, p(out), st))
+        check(lib.m4mr_epilogue_backward(p(read), p(variance), p(value), p(conf), p(skip), B, T,
+                                         H, D, p(out), p(d_read), p(d_var), p(d_value), p(d_conf),
+                                         p(d_skip), p(mix_ws), mix_ws.numel(), st))
+        check(lib.m4mr_order_forward(p(value), p(log_order), None, B, T, H, D, 64, p(ordered),
+                                     p(ord_ws), ord_bytes, st))
+        check(lib.m4mr_order_backward(p(value), p(log_order), None, p(ordered), p(out), B, T, H,
+                                      D, 64, p(d_vals), p(d_logs), None, p(ord_ws), ord_bytes, st))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(min(args.steps, 10)):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    kernel_ms = {}
+    for name in _lib.kernel_names():
+        total, count = _lib.profile_read(name)
+        if count:
+            kernel_ms[name] = total / count
+    _lib.profile_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    seconds = (time.perf_counter() - t0) / args.steps
+    token_heads = B * T * H
+    parts = {}
+    for part, names in MIXER_KERNELS.items():
+        ms = sum(kernel_ms.get(n, 0.0) for n in names)
+        gbps = MIXER_WORK[part] * token_heads / (ms / 1e3) / 1e9
+        parts[part] = {"ms": ms, "achieved_GBps": gbps, "frac": gbps / HBM_PEAK_GBPS}
+    dominant = max(parts, key=lambda k: parts[k]["ms"])
+    line = {
+        "metric": MIXER_METRIC,
+        "value": B * T / seconds,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": seconds * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "mixer path, B=16 L=1024 H=8 D=P=64 fp32", "batch": B,
+                   "seq_len": T, "heads": H, "key_dim": D, "value_dim": D},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": parts[dominant]["achieved_GBps"],
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": parts[dominant]["frac"],
+            "traffic": None,
+            "algorithmic_bytes": MIXER_WORK[dominant] * token_heads,
+        },
+        "parts": parts,
+        "kernel_ms": kernel_ms,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def copy_bandwidth_gbps():
     """Read+write bandwidth of a 2 GiB device-to-device copy (torch copy_)."""
     import torch
@@ -437,6 +575,8 @@ def main():
         sys.exit(2)
     if args.workload == "config4":
         return main_decode(args)
+    if args.workload == "mixer":
+        return main_mixer(args)
     data = workload_inputs(args.workload, seed=0, cotangents=True)
     problem = Problem(data, args.chunk)
     B, T, H = problem.B, problem.T, problem.H

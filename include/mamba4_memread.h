@@ -252,6 +252,34 @@ int m4mr_epilogue_backward(const float* read, const float* variance, const float
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Order head scan: output[b,t,h,c] = h_t with h_t = lam_t h_(t-1) +
+ * (1 - lam_t) values[b,t,h,c], lam_t = exp(log_decay[b,t,h]), the inflow
+ * taken as -expm1(log_decay), from h_(-1) = initial[b,h,c] (zero when
+ * initial is NULL).  Replaces order_memory_chunked
+ * (lm/models/mamba4.py:59-95; order_memory :46-56 is the same scan from the
+ * decays) and, over one token from the cached state, the order head's cached
+ * step (:283-287).  values, output [B,T,H,W] with 1 <= W <= 256; log_decay
+ * [B,T,H]; chunk 1..64 (the result does not depend on it beyond rounding).
+ * workspace: m4mr_order_workspace_bytes(B, T, H, W, chunk) bytes, 256-byte
+ * aligned (per-chunk carries).
+ */
+size_t m4mr_order_workspace_bytes(int B, int T, int H, int W, int chunk);
+int m4mr_order_forward(const float* values, const float* log_decay, const float* initial,
+                       int B, int T, int H, int W, int chunk, float* output, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
+ * VJP of m4mr_order_forward (the gradients JAX autodiff takes through
+ * order_memory_chunked): from `output` (the forward's) and d_output, writes
+ * d_values [B,T,H,W], d_log_decay [B,T,H] (summed over channels in a fixed
+ * order) and, if non-NULL, d_initial [B,H,W].
+ */
+int m4mr_order_backward(const float* values, const float* log_decay, const float* initial,
+                        const float* output, const float* d_output, int B, int T, int H, int W,
+                        int chunk, float* d_values, float* d_log_decay, float* d_initial,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Kernel timing with HIP events recorded on the launch stream.  While
  * enabled, every kernel launch is bracketed by a pair of events.
  * m4mr_profile_read() waits for the recorded events and returns the total

@@ -6,7 +6,9 @@ A drop-in for the reference's lm/kernels memory-read API
 ``SelectiveResult``),
 implemented by hand-written HIP kernels behind the C ABI in
 ``include/mamba4_memread.h``, plus the caller's preprocessing and read gating
-(``memory_inputs``, ``gated_read``; lm/models/mamba4.py:183-237, 266-273).
+(``memory_inputs``, ``gated_read``; lm/models/mamba4.py:183-237, 266-273)
+and the order head's gated scan (``order_memory_chunked``, ``order_memory``;
+lm/models/mamba4.py:46-95).
 """
 
 from mamba4_amd.memory import (  # noqa: F401
@@ -21,6 +23,7 @@ from mamba4_amd.memory import (  # noqa: F401
     spd_solve,
 )
 from mamba4_amd.mixer import MemoryInputs, gated_read, memory_inputs  # noqa: F401
+from mamba4_amd.order import order_memory, order_memory_chunked  # noqa: F401
 
 __all__ = [
     "MEMORY_SOLVE",
@@ -30,6 +33,8 @@ __all__ = [
     "SelectiveState",
     "gated_read",
     "memory_inputs",
+    "order_memory",
+    "order_memory_chunked",
     "selective_decode",
     "selective_decode_",
     "selective_gaussian_memory",

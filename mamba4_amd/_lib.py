@@ -47,6 +47,9 @@ SIGNATURES = {
     ),
     "m4mr_epilogue_forward": (_I, [_P] * 5 + [_I] * 4 + [_P, _P]),
     "m4mr_epilogue_backward": (_I, [_P] * 5 + [_I] * 4 + [_P] * 6 + [_P, _S, _P]),
+    "m4mr_order_workspace_bytes": (_S, [_I] * 5),
+    "m4mr_order_forward": (_I, [_P] * 3 + [_I] * 5 + [_P, _P, _S, _P]),
+    "m4mr_order_backward": (_I, [_P] * 5 + [_I] * 5 + [_P] * 4 + [_S, _P]),
     "m4mr_profile_enable": (None, [_I]),
     "m4mr_profile_select": (None, [ctypes.c_char_p]),
     "m4mr_profile_reset": (None, []),

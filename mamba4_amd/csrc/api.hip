@@ -58,6 +58,13 @@ __global__ void epilogue_backward_kernel(const float*, const float*, const float
                                          float*, float*, float*);
 __global__ void head_sums_kernel(const float*, long, int, int, float*, float*, float*);
 __global__ void zero_kernel(float*, long);
+__global__ void order_local_kernel(OrderDims, const float*, const float*, float*, float*);
+__global__ void order_carry_kernel(OrderDims, const float*, float*, const float*);
+__global__ void order_apply_kernel(OrderDims, const float*, const float*, const float*, float*);
+__global__ void order_bwd_local_kernel(OrderDims, const float*, const float*, float*, float*);
+__global__ void order_bwd_carry_kernel(OrderDims, float*, const float*, float*);
+__global__ void order_bwd_apply_kernel(OrderDims, const float*, const float*, const float*,
+                                       const float*, const float*, const float*, float*, float*);
 __global__ void spd_solve_kernel(const float*, const float*, long, int, float*, float*);
 __global__ void spd_backward_kernel(const float*, const float*, const float*, long, int, float*,
                                     float*);
@@ -75,7 +82,9 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "bwd_grads",      "floor_reduce", "decode_step",
                                     "spd_solve",      "spd_backward", "prologue_forward",
                                     "prologue_backward", "epilogue_forward",
-                                    "epilogue_backward", "head_sums"};
+                                    "epilogue_backward", "head_sums", "order_local",
+                                    "order_carry",    "order_apply", "order_bwd_local",
+                                    "order_bwd_carry", "order_bwd_apply"};
 
 struct ProfRecord {
   const char* name;
@@ -656,6 +665,124 @@ int m4mr_epilogue_backward(const float* read, const float* variance, const float
   return launch("head_sums", st, [&] {
     hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 2), dim3(256), 0, st, part, blocks, H, 2,
                        d_confidence_scale, d_skip, nullptr);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Order head scan.
+
+namespace {
+
+constexpr int kOrderMaxWidth = 256;
+
+bool bad_order_dims(int B, int T, int H, int W, int chunk, std::string* why) {
+  if (B <= 0 || T <= 0 || H <= 0) {
+    *why = "B, T and H must be positive";
+    return true;
+  }
+  if (W <= 0 || W > kOrderMaxWidth) {
+    *why = "the value width must be in 1.." + std::to_string(kOrderMaxWidth);
+    return true;
+  }
+  if (chunk <= 0 || chunk > m4::MAXC) {
+    *why = "chunk must be in 1.." + std::to_string(m4::MAXC);
+    return true;
+  }
+  if ((long)B * H * ((T + chunk - 1) / chunk) > INT32_MAX || (long)B * T * H * W > (1L << 40)) {
+    *why = "problem too large";
+    return true;
+  }
+  return false;
+}
+
+m4::OrderDims order_dims(int B, int T, int H, int W, int chunk) {
+  return m4::OrderDims{B, T, H, W, chunk, (T + chunk - 1) / chunk};
+}
+
+// Chunk states [B,H,NC,W] then chunk totals [B,H,NC].
+size_t order_workspace(const m4::OrderDims& d, float** states, float** totals, void* base) {
+  const size_t slots = (size_t)d.B * d.H * d.NC;
+  const size_t first = align256(slots * d.W * sizeof(float));
+  if (base) {
+    *states = static_cast<float*>(base);
+    *totals = reinterpret_cast<float*>(static_cast<char*>(base) + first);
+  }
+  return first + align256(slots * sizeof(float));
+}
+
+unsigned order_threads(int W) { return (unsigned)(64 * ((W + 63) / 64)); }
+
+}  // namespace
+
+size_t m4mr_order_workspace_bytes(int B, int T, int H, int W, int chunk) {
+  std::string why;
+  if (bad_order_dims(B, T, H, W, chunk, &why)) return 0;
+  return order_workspace(order_dims(B, T, H, W, chunk), nullptr, nullptr, nullptr);
+}
+
+int m4mr_order_forward(const float* values, const float* log_decay, const float* initial, int B,
+                       int T, int H, int W, int chunk, float* output, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_order_dims(B, T, H, W, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_order_forward: " + why);
+  if (!values || !log_decay || !output || !workspace)
+    return fail(M4MR_EINVAL, "m4mr_order_forward: a required pointer is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(M4MR_EINVAL, "m4mr_order_forward: workspace must be 256-byte aligned");
+  const m4::OrderDims d = order_dims(B, T, H, W, chunk);
+  float *states = nullptr, *totals = nullptr;
+  if (workspace_bytes < order_workspace(d, &states, &totals, workspace))
+    return fail(M4MR_EINVAL, "m4mr_order_forward: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned chunks = (unsigned)((long)B * H * d.NC), threads = order_threads(W);
+  int rc = launch("order_local", st, [&] {
+    hipLaunchKernelGGL(m4::order_local_kernel, dim3(chunks), dim3(threads), 0, st, d, values,
+                       log_decay, states, totals);
+  });
+  if (rc) return rc;
+  rc = launch("order_carry", st, [&] {
+    hipLaunchKernelGGL(m4::order_carry_kernel, dim3(B * H), dim3(threads), 0, st, d, initial,
+                       states, totals);
+  });
+  if (rc) return rc;
+  return launch("order_apply", st, [&] {
+    hipLaunchKernelGGL(m4::order_apply_kernel, dim3(chunks), dim3(threads), 0, st, d, values,
+                       log_decay, states, output);
+  });
+}
+
+int m4mr_order_backward(const float* values, const float* log_decay, const float* initial,
+                        const float* output, const float* d_output, int B, int T, int H, int W,
+                        int chunk, float* d_values, float* d_log_decay, float* d_initial,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_order_dims(B, T, H, W, chunk, &why))
+    return fail(M4MR_EINVAL, "m4mr_order_backward: " + why);
+  if (!values || !log_decay || !output || !d_output || !d_values || !d_log_decay || !workspace)
+    return fail(M4MR_EINVAL, "m4mr_order_backward: a required pointer is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(M4MR_EINVAL, "m4mr_order_backward: workspace must be 256-byte aligned");
+  const m4::OrderDims d = order_dims(B, T, H, W, chunk);
+  float *heads = nullptr, *totals = nullptr;
+  if (workspace_bytes < order_workspace(d, &heads, &totals, workspace))
+    return fail(M4MR_EINVAL, "m4mr_order_backward: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned chunks = (unsigned)((long)B * H * d.NC), threads = order_threads(W);
+  int rc = launch("order_bwd_local", st, [&] {
+    hipLaunchKernelGGL(m4::order_bwd_local_kernel, dim3(chunks), dim3(threads), 0, st, d,
+                       d_output, log_decay, heads, totals);
+  });
+  if (rc) return rc;
+  rc = launch("order_bwd_carry", st, [&] {
+    hipLaunchKernelGGL(m4::order_bwd_carry_kernel, dim3(B * H), dim3(threads), 0, st, d, heads,
+                       totals, d_initial);
+  });
+  if (rc) return rc;
+  return launch("order_bwd_apply", st, [&] {
+    hipLaunchKernelGGL(m4::order_bwd_apply_kernel, dim3(chunks), dim3(threads), 0, st, d, values,
+                       log_decay, initial, output, d_output, heads, d_values, d_log_decay);
   });
 }
 

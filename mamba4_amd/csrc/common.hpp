@@ -350,4 +350,10 @@ struct StateArgs {
   float* last_c;
 };
 
+// Shape of the order head's scan: values [B,T,H,W] in chunks of `chunk`
+// tokens, NC of them.
+struct OrderDims {
+  int B, T, H, W, chunk, NC;
+};
+
 }  // namespace m4
