@@ -609,7 +609,7 @@ int m4mr_prologue_backward(const float* key, const float* query, const float* be
     if (rc) return rc;
   }
   return launch("head_sums", st, [&] {
-    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 3), dim3(256), 0, st, part, blocks, H, 3,
+    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 3), dim3(1024), 0, st, part, blocks, H, 3,
                        d_beta_bias, d_dt_bias, d_a_log);
   });
 }
@@ -663,7 +663,7 @@ int m4mr_epilogue_backward(const float* read, const float* variance, const float
   });
   if (rc) return rc;
   return launch("head_sums", st, [&] {
-    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 2), dim3(256), 0, st, part, blocks, H, 2,
+    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 2), dim3(1024), 0, st, part, blocks, H, 2,
                        d_confidence_scale, d_skip, nullptr);
   });
 }

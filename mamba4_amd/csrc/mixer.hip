@@ -142,7 +142,7 @@ __device__ void block_head_partials(float (*vals)[J], const long* ths, int H, fl
     float s = 0.f;
     for (int row = 0; row < MIX_ROWS; ++row)
       if (ths[row] >= 0 && ths[row] % H == h) s += vals[row][j];
-    part[((long)blockIdx.x * H + h) * J + j] = s;
+    part[(long)(h * J + j) * gridDim.x + blockIdx.x] = s;
   }
 }
 
@@ -261,22 +261,32 @@ __global__ __launch_bounds__(256) void epilogue_backward_kernel(
   block_head_partials<2>(vals, ths, H, part);
 }
 
-// out[h * stride + j] (for the J outputs of each head) = sum over blocks, in
-// block order, of part[(block * H + h) * J + j].  One 256-thread block per
-// (h, j): each thread sums blocks i, i + 256, ... in order, then the 256
-// partials are added in a fixed tree.
-__global__ __launch_bounds__(256) void head_sums_kernel(const float* __restrict__ part,
-                                                        long blocks, int H, int J,
-                                                        float* __restrict__ o0,
-                                                        float* __restrict__ o1,
-                                                        float* __restrict__ o2) {
+// o_j[h] = sum over blocks of part[(h * J + j) * blocks + block], in a fixed
+// order: one 1024-thread block per (h, j); thread i sums blocks i, i + 1024,
+// ... in order (eight loads in flight), then the 1024 partials are added in
+// a fixed tree.  Results are identical run to run.
+constexpr int HEAD_SUM_THREADS = 1024;
+
+__global__ __launch_bounds__(HEAD_SUM_THREADS) void head_sums_kernel(
+    const float* __restrict__ part, long blocks, int H, int J, float* __restrict__ o0,
+    float* __restrict__ o1, float* __restrict__ o2) {
   const int h = blockIdx.x / J, j = blockIdx.x % J;
-  __shared__ float red[256];
+  __shared__ float red[HEAD_SUM_THREADS];
+  const float* src = part + (long)(h * J + j) * blocks;
   float s = 0.f;
-  for (long i = threadIdx.x; i < blocks; i += 256) s += part[(i * H + h) * J + j];
+  for (long i0 = threadIdx.x; i0 < blocks; i0 += 8L * HEAD_SUM_THREADS) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const long i = i0 + (long)k * HEAD_SUM_THREADS;
+      v[k] = i < blocks ? src[i] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += v[k];
+  }
   red[threadIdx.x] = s;
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
+  for (int w = HEAD_SUM_THREADS / 2; w > 0; w >>= 1) {
     if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
     __syncthreads();
   }
