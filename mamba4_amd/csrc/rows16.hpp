@@ -374,6 +374,11 @@ __device__ __forceinline__ void store_rows16(const float (&A)[4][64], float* __r
   }
 }
 
+// Every load is unconditional: quad run_quad(m, q) + a lies inside the
+// factor for every lane a and q <= 4m + 3 (the runs of a slot are laid out
+// for 16 lanes), so lanes past their row's last quad read a neighbour's
+// entry and zero it.  A load under a per-lane branch would make the compiler
+// wait for it inside the branch, serialising the stream.
 __device__ __forceinline__ void load_rows16(float (&A)[4][64], const float* __restrict__ fac) {
   const int a = threadIdx.x & 15;
   const f4* lane = reinterpret_cast<const f4*>(fac) + a;
@@ -382,12 +387,12 @@ __device__ __forceinline__ void load_rows16(float (&A)[4][64], const float* __re
     const int p = (a + 16 * m) >> 2;
 #pragma unroll
     for (int q = 0; q < 4 * m + 4; ++q) {
-      f4 v = f4{0.f, 0.f, 0.f, 0.f};
-      if (q <= p) v = lane[run_quad(m, q)];
-      A[m][4 * q] = v[0];
-      A[m][4 * q + 1] = v[1];
-      A[m][4 * q + 2] = v[2];
-      A[m][4 * q + 3] = v[3];
+      const f4 v = lane[run_quad(m, q)];
+      const bool in = q <= p;
+      A[m][4 * q] = in ? v[0] : 0.f;
+      A[m][4 * q + 1] = in ? v[1] : 0.f;
+      A[m][4 * q + 2] = in ? v[2] : 0.f;
+      A[m][4 * q + 3] = in ? v[3] : 0.f;
     }
   }
 }
