@@ -381,7 +381,8 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
   const unsigned seqs = (unsigned)B * H * d.NC;
   const long tokens = (long)B * T * H;
   int rc = launch("bwd_dy", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_dy_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d, keys,
+    hipLaunchKernelGGL(m4::bwd_dy_kernel, dim3(persistent_grid(seqs, 2)), dim3(256),
+                       kChunkLdsBytes, st, d, keys,
                        values, queries, beta, log_decay, start_cross, d_output, d_variance, ws.z);
   });
   if (rc) return rc;

@@ -174,7 +174,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-__global__ __launch_bounds__(256) void bwd_dy_kernel(
+// Persistent like fwd_read_kernel: block i handles chunks i, i + gridDim.x,
+// ...; the next chunk's dout, value and C0 tiles load into registers once
+// this chunk's last value tile is in LDS, its keys once this chunk's keys are
+// staged, and its queries and d_variance after this chunk's epilogue.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dy_kernel(
     Dims d, const float* __restrict__ keys, const float* __restrict__ values,
     const float* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ start_c,
@@ -186,77 +190,100 @@ __global__ __launch_bounds__(256) void bwd_dy_kernel(
   float* G = V + TILE;
   float* C0 = G + TILE;
   __shared__ ChunkScalars cs;
-  const SeqIndex si = seq_index(d);
+  const long nseq = (long)d.B * d.H * d.NC;
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
+  long seq = blockIdx.x;
+  SeqIndex si = seq_at(d, seq);
 
   TileRegs rd, rv, rk, rc;
+  // Queries and d_variance of this lane's accumulator rows (read in the epilogue).
+  f4 qv[4];
+  float dvar[4];
+  auto fetch_rows_q = [&](const SeqIndex& s) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = acc_row(w, q);
+      qv[q] = f4{0.f, 0.f, 0.f, 0.f};
+      dvar[q] = 0.f;
+      if (t < s.len) {
+        const long th = token_head(d, s.b, s.n * d.chunk + t, s.h);
+        qv[q] = *reinterpret_cast<const f4*>(queries + th * 64 + c4);
+        dvar[q] = d_variance[th];
+      }
+    }
+  };
   rd.fetch_rows(si.len, value_rows(d_output, d, si, 0));
   rv.fetch_rows(si.len, value_rows(values, d, si, 0));
   rk.fetch_rows(si.len, rows_of(keys, d, si));
   rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
-  // Queries and d_variance of this lane's accumulator rows (read in the epilogue).
-  f4 qv[4];
-  float dvar[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int t = acc_row(w, q);
-    qv[q] = f4{0.f, 0.f, 0.f, 0.f};
-    dvar[q] = 0.f;
-    if (t < si.len) {
-      const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
-      qv[q] = *reinterpret_cast<const f4*>(queries + th * 64 + c4);
-      dvar[q] = d_variance[th];
-    }
-  }
-  rd.store(DO);
-  rv.store(V);
-  rc.store(C0);
-  load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
-  __syncthreads();
+  fetch_rows_q(si);
 
-  // Both products sum over the value tiles: dout_t . v_s and C0^T dout_t.
-  f4 acc[4], inh[4];
-  zero4(acc);
-  zero4(inh);
-  for (int v = 0; v < d.NV; ++v) {
-    if (v > 0) {
-      rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
-      rv.fetch_rows(si.len, value_rows(values, d, si, v));
-      rc.fetch_matrix(cross_tile(start_c, d, si.seq, v));
-      __syncthreads();
-      rd.store(DO);
-      rv.store(V);
-      rc.store(C0);
-      __syncthreads();
+  for (;;) {
+    rd.store(DO);
+    rv.store(V);
+    rc.store(C0);
+    load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
+    __syncthreads();
+    const long next = seq + gridDim.x;
+    const bool more = next < nseq;  // uniform over the block
+    const SeqIndex sn = seq_at(d, more ? next : seq);
+
+    // Both products sum over the value tiles: dout_t . v_s and C0^T dout_t.
+    f4 acc[4], inh[4];
+    zero4(acc);
+    zero4(inh);
+    for (int v = 0; v < d.NV; ++v) {
+      if (v > 0) {
+        // Tile v replaces tile v - 1 once every wave has read it.
+        rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+        rv.fetch_rows(si.len, value_rows(values, d, si, v));
+        rc.fetch_matrix(cross_tile(start_c, d, si.seq, v));
+        __syncthreads();
+        rd.store(DO);
+        rv.store(V);
+        rc.store(C0);
+        __syncthreads();
+      }
+      if (more && v == d.NV - 1) {
+        rd.fetch_rows(sn.len, value_rows(d_output, d, sn, 0));
+        rv.fetch_rows(sn.len, value_rows(values, d, sn, 0));
+        rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
+      }
+      tile_mma<false, true>(acc, DO, V, 64, w);    // dout_t . v_s
+      tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
     }
-    tile_mma<false, true>(acc, DO, V, 64, w);  // dout_t . v_s
-    tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
-  }
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = acc_row(w, q), s = acc_col<false>(jb);
+        float v = 0.f;
+        if (s <= t && t < si.len) v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
+        G[t * LDT + s] = v;
+      }
+    __syncthreads();
+    rk.store(V);
+    __syncthreads();
+    if (more) rk.fetch_rows(sn.len, rows_of(keys, d, sn));
+
+    f4 within[4];
+    zero4(within);
+    tile_mma<false, false>(within, G, V, k_terms(si.len), w);  // sum_s G[t][s] k_s
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(w, q), s = acc_col<false>(jb);
-      float v = 0.f;
-      if (s <= t && t < si.len) v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
-      G[t * LDT + s] = v;
+      const int t = acc_row(w, q);
+      if (t < si.len) {
+        const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+        const float carried = expf(cs.prefix[t]);
+        *reinterpret_cast<f4*>(ybar + th * 64 + c4) =
+            quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qv[q];
+      }
     }
-  __syncthreads();
-  rk.store(V);
-  __syncthreads();
-
-  f4 within[4];
-  zero4(within);
-  tile_mma<false, false>(within, G, V, k_terms(si.len), w);  // sum_s G[t][s] k_s
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int t = acc_row(w, q);
-    if (t < si.len) {
-      const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
-      const float carried = expf(cs.prefix[t]);
-      *reinterpret_cast<f4*>(ybar + th * 64 + c4) =
-          quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qv[q];
-    }
+    if (!more) break;
+    fetch_rows_q(sn);
+    __syncthreads();  // the tiles and scalars are read; the next chunk may overwrite them
+    si = sn;
+    seq = next;
   }
 }
 
