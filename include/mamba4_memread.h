@@ -26,6 +26,7 @@
 #define MAMBA4_MEMREAD_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -94,6 +95,24 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
                  float* start_evidence, float* start_cross,
                  void* stream);
 
+/*
+ * m4mr_forward with bfloat16 keys, values and queries (raw 16-bit storage,
+ * the caller's bf16 arrays), read and widened to float32 inside the
+ * kernels; every other argument, the arithmetic and the outputs as in
+ * m4mr_forward.  The reference upcasts bf16 inputs to float32 before the
+ * memory read (lm/kernels/mamba4.py:263-265): results are identical to
+ * m4mr_forward on the upcast arrays.
+ */
+int m4mr_forward_bf16(const uint16_t* keys, const uint16_t* values, const uint16_t* queries,
+                      const float* beta, const float* log_decay, const float* floor,
+                      const float* init_evidence, const float* init_cross,
+                      int B, int T, int H, int value_dim, int chunk,
+                      float* output, float* variance,
+                      float* final_evidence, float* final_cross,
+                      float* solved, float* factors,
+                      float* start_evidence, float* start_cross,
+                      void* stream);
+
 /* Number of chunks NC and of evidence start states NS for T tokens. */
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts);
 
@@ -132,6 +151,23 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
                   float* d_init_evidence, float* d_init_cross,
                   void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/*
+ * m4mr_backward with bfloat16 keys, values and queries (as
+ * m4mr_forward_bf16); the gradients are float32.
+ */
+int m4mr_backward_bf16(const uint16_t* keys, const uint16_t* values, const uint16_t* queries,
+                       const float* beta, const float* log_decay, const float* floor,
+                       int B, int T, int H, int value_dim, int chunk,
+                       const float* solved, const float* factors,
+                       const float* start_evidence, const float* start_cross,
+                       const float* d_output, const float* d_variance,
+                       const float* d_final_evidence, const float* d_final_cross,
+                       float* d_keys, float* d_values, float* d_queries,
+                       float* d_beta, float* d_log_decay, float* d_floor,
+                       float* d_init_evidence, float* d_init_cross,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /*
  * Triangular re-solve with stored factors: z_i = A_i^-1 rhs_i for N

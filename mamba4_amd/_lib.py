@@ -29,9 +29,14 @@ SIGNATURES = {
     "m4mr_version": (ctypes.c_char_p, []),
     "m4mr_last_error": (ctypes.c_char_p, []),
     "m4mr_forward": (_I, [_P] * 8 + [_I] * 5 + [_P] * 8 + [_P]),
+    "m4mr_forward_bf16": (_I, [_P] * 8 + [_I] * 5 + [_P] * 8 + [_P]),
     "m4mr_backward_workspace_bytes": (_S, [_I] * 5),
     "m4mr_start_counts": (_I, [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "m4mr_backward": (
+        _I,
+        [_P] * 6 + [_I] * 5 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
+    ),
+    "m4mr_backward_bf16": (
         _I,
         [_P] * 6 + [_I] * 5 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
     ),

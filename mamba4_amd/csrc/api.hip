@@ -16,27 +16,32 @@
 #include "common.hpp"
 
 namespace m4 {
-__global__ void fwd_stats_kernel(Dims, const float*, const float*, const float*, const float*,
-                                 float*, float*);
+template <typename In>
+__global__ void fwd_stats_kernel(Dims, const In*, const In*, const float*, const float*, float*,
+                                 float*);
 __global__ void fwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
                                 float*, float*);
 __global__ void bwd_local_kernel(Dims, const float*, const float*, const float*, const float*,
                                  const float*, float*, float*);
 __global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
                                 float*, float*);
-template <bool BWD>
+template <bool BWD, typename In>
 __global__ void states_kernel(Dims, StateArgs);
-__global__ void fwd_factor_kernel(Dims, const float*, const float*, const float*, const float*,
+template <typename In>
+__global__ void fwd_factor_kernel(Dims, const In*, const In*, const float*, const float*,
                                   const float*, const float*, float*, float*);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
 __global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
                                    const float*, const float*, const float*, long, int, int, float*,
                                    float*);
-__global__ void fwd_read_kernel(Dims, const float*, const float*, const float*, const float*,
+template <typename In>
+__global__ void fwd_read_kernel(Dims, const In*, const In*, const In*, const float*,
                                 const float*, const float*, const float*, float*, float*);
-__global__ void bwd_dy_kernel(Dims, const float*, const float*, const float*, const float*,
+template <typename In>
+__global__ void bwd_dy_kernel(Dims, const In*, const In*, const In*, const float*,
                               const float*, const float*, const float*, const float*, float*);
-__global__ void bwd_grads_kernel(Dims, const float*, const float*, const float*, const float*,
+template <typename In>
+__global__ void bwd_grads_kernel(Dims, const In*, const In*, const float*, const float*,
                                  const float*, const float*, const float*, const float*,
                                  const float*, const float*, const float*, const float*, float*,
                                  float*, float*, float*, float*, float*);
@@ -133,13 +138,18 @@ int configure() {
   struct {
     const void* fn;
     size_t bytes;
-  } big[] = {{(const void*)m4::fwd_stats_kernel, kStatsLdsBytes},
+  } big[] = {{(const void*)m4::fwd_stats_kernel<float>, kStatsLdsBytes},
+             {(const void*)m4::fwd_stats_kernel<m4::bf16_t>, kStatsLdsBytes},
              {(const void*)m4::bwd_local_kernel, kChunkLdsBytes},
-             {(const void*)m4::fwd_read_kernel, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel, kChunkLdsBytes},
-             {(const void*)m4::bwd_grads_kernel, kGradsLdsBytes},
-             {(const void*)m4::states_kernel<false>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<true>, kStatesLdsBytes}};
+             {(const void*)m4::fwd_read_kernel<float>, kChunkLdsBytes},
+             {(const void*)m4::fwd_read_kernel<m4::bf16_t>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<float>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<m4::bf16_t>, kChunkLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<m4::bf16_t>, kGradsLdsBytes},
+             {(const void*)m4::states_kernel<false, float>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<false, m4::bf16_t>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<true, float>, kStatesLdsBytes}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)k.bytes);
@@ -263,6 +273,147 @@ constexpr long kMaxSystems = ((1L << 31) - 1) * 4;
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 
+// The memory read forward and backward for float32 or bfloat16 keys,
+// values and queries (the C entry points below).
+template <typename In>
+int forward_impl(const char* entry, const In* keys, const In* values, const In* queries,
+                 const float* beta, const float* log_decay, const float* floor,
+                 const float* init_evidence, const float* init_cross, int B, int T, int H,
+                 int value_dim, int chunk, float* output, float* variance, float* final_evidence,
+                 float* final_cross, float* solved, float* factors, float* start_evidence,
+                 float* start_cross, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
+  const void* need[] = {keys,     values,        queries,     beta,   log_decay,
+                        floor,    output,        variance,    final_evidence,
+                        final_cross, solved,     factors,     start_evidence, start_cross};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
+  if ((init_evidence == nullptr) != (init_cross == nullptr))
+    return fail(M4MR_EINVAL, std::string(entry) + ": init_evidence and init_cross must both be set or both NULL");
+  const void* vec[] = {keys, values, queries, solved, factors, output, start_evidence,
+                       start_cross, final_evidence, final_cross, init_evidence, init_cross};
+  for (const void* p : vec)
+    if (p && misaligned(p)) return fail(M4MR_EINVAL, std::string(entry) + ": arrays must be 16-byte aligned");
+  if (int rc = configure()) return rc;
+  const Dims d = make_dims(B, T, H, value_dim, chunk);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned seqs = (unsigned)B * H * d.NC;
+  const unsigned subseqs = (unsigned)B * H * d.NS;
+  int rc;
+  if (fused_states(B, H, d)) {
+    const m4::StateArgs args{keys,            values,      keys,           beta,   log_decay,
+                             init_evidence,   init_cross,  start_evidence, start_cross,
+                             final_evidence,  final_cross};
+    rc = launch("fwd_states", st, [&] {
+      hipLaunchKernelGGL((m4::states_kernel<false, In>), dim3(B * H, 1 + d.NV), dim3(512),
+                         kStatesLdsBytes, st, d, args);
+    });
+  } else {
+    rc = launch("fwd_stats", st, [&] {
+      hipLaunchKernelGGL(m4::fwd_stats_kernel<In>, dim3(seqs), dim3(256), kStatsLdsBytes, st, d,
+                         keys, values, beta, log_decay, start_evidence, start_cross);
+    });
+    if (rc) return rc;
+    rc = launch("fwd_scan", st, [&] {
+      hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d,
+                         log_decay, init_evidence, init_cross, start_evidence, start_cross,
+                         final_evidence, final_cross);
+    });
+  }
+  if (rc) return rc;
+  rc = launch("fwd_factor", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_factor_kernel<In>, dim3((subseqs + 3) / 4), dim3(128), 0, st, d, keys,
+                       queries, beta, log_decay, floor, start_evidence, solved, factors);
+  });
+  if (rc) return rc;
+  return launch("fwd_read", st, [&] {
+    hipLaunchKernelGGL(m4::fwd_read_kernel<In>, dim3(persistent_grid(seqs, 2)), dim3(256),
+                       kChunkLdsBytes, st, d, keys,
+                       values, queries, beta, log_decay, solved, start_cross, output, variance);
+  });
+}
+
+template <typename In>
+int backward_impl(const char* entry, const In* keys, const In* values, const In* queries,
+                  const float* beta, const float* log_decay, const float* floor, int B, int T,
+                  int H, int value_dim, int chunk, const float* solved, const float* factors,
+                  const float* start_evidence, const float* start_cross, const float* d_output,
+                  const float* d_variance, const float* d_final_evidence,
+                  const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
+                  float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
+                  float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
+  const void* need[] = {keys,    values,     queries,         beta,         log_decay,
+                        floor,   solved,     factors,         start_evidence, start_cross,
+                        d_output, d_variance, d_keys,         d_values,     d_queries,
+                        d_beta,  d_log_decay, d_floor,        d_init_evidence, d_init_cross,
+                        workspace};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(M4MR_EINVAL, std::string(entry) + ": workspace must be 256-byte aligned");
+  const BackwardWorkspace ws = carve(workspace, B, T, H, value_dim, chunk);
+  if (workspace_bytes < ws.bytes)
+    return fail(M4MR_EINVAL, std::string(entry) + ": workspace too small (need " +
+                                 std::to_string(ws.bytes) + " bytes)");
+  const void* vec[] = {keys, values, queries, solved, factors, start_evidence, start_cross,
+                       d_output, d_final_evidence, d_final_cross, d_init_evidence, d_init_cross};
+  for (const void* p : vec)
+    if (p && misaligned(p)) return fail(M4MR_EINVAL, std::string(entry) + ": arrays must be 16-byte aligned");
+  if (int rc = configure()) return rc;
+  const Dims d = make_dims(B, T, H, value_dim, chunk);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned seqs = (unsigned)B * H * d.NC;
+  const long tokens = (long)B * T * H;
+  int rc = launch("bwd_dy", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_dy_kernel<In>, dim3(persistent_grid(seqs, 2)), dim3(256),
+                       kChunkLdsBytes, st, d, keys,
+                       values, queries, beta, log_decay, start_cross, d_output, d_variance, ws.z);
+  });
+  if (rc) return rc;
+  rc = launch("factored_solve", st, [&] {
+    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(64), 0,
+                       st, factors, ws.z, ws.z, tokens);
+  });
+  if (rc) return rc;
+  if (fused_states(B, H, d)) {
+    const m4::StateArgs args{ws.z,             d_output,       solved,   beta,   log_decay,
+                             d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
+                             d_init_evidence,  d_init_cross};
+    rc = launch("bwd_states", st, [&] {
+      hipLaunchKernelGGL((m4::states_kernel<true, float>), dim3(B * H, 1 + d.NV), dim3(512),
+                         kStatesLdsBytes, st, d, args);
+    });
+  } else {
+    rc = launch("bwd_local", st, [&] {
+      hipLaunchKernelGGL(m4::bwd_local_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d,
+                         beta, log_decay, solved, ws.z, d_output, ws.end_s, ws.end_c);
+    });
+    if (rc) return rc;
+    rc = launch("bwd_scan", st, [&] {
+      hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d,
+                         log_decay, d_final_evidence, d_final_cross, ws.end_s, ws.end_c,
+                         d_init_evidence, d_init_cross);
+    });
+  }
+  if (rc) return rc;
+  rc = launch("bwd_grads", st, [&] {
+    hipLaunchKernelGGL(m4::bwd_grads_kernel<In>, dim3(seqs), dim3(512), kGradsLdsBytes, st, d, keys,
+                       values, beta, log_decay, solved, ws.z, d_output, d_variance,
+                       start_evidence, start_cross, ws.end_s, ws.end_c, d_keys, d_values,
+                       d_queries, d_beta, d_log_decay, ws.floor_part);
+  });
+  if (rc) return rc;
+  return launch("floor_reduce", st, [&] {
+    hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H * 16), dim3(256), 0, st, d, ws.floor_part,
+                       d_floor);
+  });
+}
+
 }  // namespace
 
 extern "C" {
@@ -277,57 +428,24 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
                  int value_dim, int chunk, float* output, float* variance, float* final_evidence,
                  float* final_cross, float* solved, float* factors, float* start_evidence,
                  float* start_cross, void* stream) {
-  g_error.clear();
-  std::string why;
-  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_forward: " + why);
-  const void* need[] = {keys,     values,        queries,     beta,   log_decay,
-                        floor,    output,        variance,    final_evidence,
-                        final_cross, solved,     factors,     start_evidence, start_cross};
-  for (const void* p : need)
-    if (!p) return fail(M4MR_EINVAL, "m4mr_forward: a required pointer is NULL");
-  if ((init_evidence == nullptr) != (init_cross == nullptr))
-    return fail(M4MR_EINVAL, "m4mr_forward: init_evidence and init_cross must both be set or both NULL");
-  const void* vec[] = {keys, values, queries, solved, factors, output, start_evidence,
-                       start_cross, final_evidence, final_cross, init_evidence, init_cross};
-  for (const void* p : vec)
-    if (p && misaligned(p)) return fail(M4MR_EINVAL, "m4mr_forward: arrays must be 16-byte aligned");
-  if (int rc = configure()) return rc;
-  const Dims d = make_dims(B, T, H, value_dim, chunk);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned seqs = (unsigned)B * H * d.NC;
-  const unsigned subseqs = (unsigned)B * H * d.NS;
-  int rc;
-  if (fused_states(B, H, d)) {
-    const m4::StateArgs args{keys,            values,      keys,           beta,   log_decay,
-                             init_evidence,   init_cross,  start_evidence, start_cross,
-                             final_evidence,  final_cross};
-    rc = launch("fwd_states", st, [&] {
-      hipLaunchKernelGGL(m4::states_kernel<false>, dim3(B * H, 1 + d.NV), dim3(512),
-                         kStatesLdsBytes, st, d, args);
-    });
-  } else {
-    rc = launch("fwd_stats", st, [&] {
-      hipLaunchKernelGGL(m4::fwd_stats_kernel, dim3(seqs), dim3(256), kStatsLdsBytes, st, d,
-                         keys, values, beta, log_decay, start_evidence, start_cross);
-    });
-    if (rc) return rc;
-    rc = launch("fwd_scan", st, [&] {
-      hipLaunchKernelGGL(m4::fwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d,
-                         log_decay, init_evidence, init_cross, start_evidence, start_cross,
-                         final_evidence, final_cross);
-    });
-  }
-  if (rc) return rc;
-  rc = launch("fwd_factor", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_factor_kernel, dim3((subseqs + 3) / 4), dim3(128), 0, st, d, keys,
-                       queries, beta, log_decay, floor, start_evidence, solved, factors);
-  });
-  if (rc) return rc;
-  return launch("fwd_read", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_read_kernel, dim3(persistent_grid(seqs, 2)), dim3(256),
-                       kChunkLdsBytes, st, d, keys,
-                       values, queries, beta, log_decay, solved, start_cross, output, variance);
-  });
+  return forward_impl("m4mr_forward", keys, values, queries, beta, log_decay, floor,
+                      init_evidence, init_cross, B, T, H, value_dim, chunk, output, variance,
+                      final_evidence, final_cross, solved, factors, start_evidence, start_cross,
+                      stream);
+}
+
+int m4mr_forward_bf16(const uint16_t* keys, const uint16_t* values, const uint16_t* queries,
+                      const float* beta, const float* log_decay, const float* floor,
+                      const float* init_evidence, const float* init_cross, int B, int T, int H,
+                      int value_dim, int chunk, float* output, float* variance,
+                      float* final_evidence, float* final_cross, float* solved, float* factors,
+                      float* start_evidence, float* start_cross, void* stream) {
+  return forward_impl("m4mr_forward_bf16", reinterpret_cast<const m4::bf16_t*>(keys),
+                      reinterpret_cast<const m4::bf16_t*>(values),
+                      reinterpret_cast<const m4::bf16_t*>(queries), beta, log_decay, floor,
+                      init_evidence, init_cross, B, T, H, value_dim, chunk, output, variance,
+                      final_evidence, final_cross, solved, factors, start_evidence, start_cross,
+                      stream);
 }
 
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {
@@ -355,74 +473,30 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
                   const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
                   float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
                   float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream) {
-  g_error.clear();
-  std::string why;
-  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, "m4mr_backward: " + why);
-  const void* need[] = {keys,    values,     queries,         beta,         log_decay,
-                        floor,   solved,     factors,         start_evidence, start_cross,
-                        d_output, d_variance, d_keys,         d_values,     d_queries,
-                        d_beta,  d_log_decay, d_floor,        d_init_evidence, d_init_cross,
-                        workspace};
-  for (const void* p : need)
-    if (!p) return fail(M4MR_EINVAL, "m4mr_backward: a required pointer is NULL");
-  if (reinterpret_cast<uintptr_t>(workspace) & 255)
-    return fail(M4MR_EINVAL, "m4mr_backward: workspace must be 256-byte aligned");
-  const BackwardWorkspace ws = carve(workspace, B, T, H, value_dim, chunk);
-  if (workspace_bytes < ws.bytes)
-    return fail(M4MR_EINVAL, "m4mr_backward: workspace too small (need " +
-                                 std::to_string(ws.bytes) + " bytes)");
-  const void* vec[] = {keys, values, queries, solved, factors, start_evidence, start_cross,
-                       d_output, d_final_evidence, d_final_cross, d_init_evidence, d_init_cross};
-  for (const void* p : vec)
-    if (p && misaligned(p)) return fail(M4MR_EINVAL, "m4mr_backward: arrays must be 16-byte aligned");
-  if (int rc = configure()) return rc;
-  const Dims d = make_dims(B, T, H, value_dim, chunk);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned seqs = (unsigned)B * H * d.NC;
-  const long tokens = (long)B * T * H;
-  int rc = launch("bwd_dy", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_dy_kernel, dim3(persistent_grid(seqs, 2)), dim3(256),
-                       kChunkLdsBytes, st, d, keys,
-                       values, queries, beta, log_decay, start_cross, d_output, d_variance, ws.z);
-  });
-  if (rc) return rc;
-  rc = launch("factored_solve", st, [&] {
-    hipLaunchKernelGGL(m4::factored_solve_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(64), 0,
-                       st, factors, ws.z, ws.z, tokens);
-  });
-  if (rc) return rc;
-  if (fused_states(B, H, d)) {
-    const m4::StateArgs args{ws.z,             d_output,       solved,   beta,   log_decay,
-                             d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
-                             d_init_evidence,  d_init_cross};
-    rc = launch("bwd_states", st, [&] {
-      hipLaunchKernelGGL(m4::states_kernel<true>, dim3(B * H, 1 + d.NV), dim3(512),
-                         kStatesLdsBytes, st, d, args);
-    });
-  } else {
-    rc = launch("bwd_local", st, [&] {
-      hipLaunchKernelGGL(m4::bwd_local_kernel, dim3(seqs), dim3(256), kChunkLdsBytes, st, d,
-                         beta, log_decay, solved, ws.z, d_output, ws.end_s, ws.end_c);
-    });
-    if (rc) return rc;
-    rc = launch("bwd_scan", st, [&] {
-      hipLaunchKernelGGL(m4::bwd_scan_kernel, dim3(B * H, 4 + 4 * d.NV), dim3(256), 0, st, d,
-                         log_decay, d_final_evidence, d_final_cross, ws.end_s, ws.end_c,
-                         d_init_evidence, d_init_cross);
-    });
-  }
-  if (rc) return rc;
-  rc = launch("bwd_grads", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_grads_kernel, dim3(seqs), dim3(512), kGradsLdsBytes, st, d, keys,
-                       values, beta, log_decay, solved, ws.z, d_output, d_variance,
-                       start_evidence, start_cross, ws.end_s, ws.end_c, d_keys, d_values,
-                       d_queries, d_beta, d_log_decay, ws.floor_part);
-  });
-  if (rc) return rc;
-  return launch("floor_reduce", st, [&] {
-    hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H * 16), dim3(256), 0, st, d, ws.floor_part,
-                       d_floor);
-  });
+  return backward_impl("m4mr_backward", keys, values, queries, beta, log_decay, floor, B, T, H,
+                       value_dim, chunk, solved, factors, start_evidence, start_cross, d_output,
+                       d_variance, d_final_evidence, d_final_cross, d_keys, d_values, d_queries,
+                       d_beta, d_log_decay, d_floor, d_init_evidence, d_init_cross, workspace,
+                       workspace_bytes, stream);
+}
+
+int m4mr_backward_bf16(const uint16_t* keys, const uint16_t* values, const uint16_t* queries,
+                       const float* beta, const float* log_decay, const float* floor, int B,
+                       int T, int H, int value_dim, int chunk, const float* solved,
+                       const float* factors, const float* start_evidence,
+                       const float* start_cross, const float* d_output,
+                       const float* d_variance, const float* d_final_evidence,
+                       const float* d_final_cross, float* d_keys, float* d_values,
+                       float* d_queries, float* d_beta, float* d_log_decay, float* d_floor,
+                       float* d_init_evidence, float* d_init_cross, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  return backward_impl("m4mr_backward_bf16", reinterpret_cast<const m4::bf16_t*>(keys),
+                       reinterpret_cast<const m4::bf16_t*>(values),
+                       reinterpret_cast<const m4::bf16_t*>(queries), beta, log_decay, floor, B,
+                       T, H, value_dim, chunk, solved, factors, start_evidence, start_cross,
+                       d_output, d_variance, d_final_evidence, d_final_cross, d_keys, d_values,
+                       d_queries, d_beta, d_log_decay, d_floor, d_init_evidence, d_init_cross,
+                       workspace, workspace_bytes, stream);
 }
 
 int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N,

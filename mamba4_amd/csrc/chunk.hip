@@ -36,25 +36,29 @@ __device__ __forceinline__ SeqIndex seq_at(const Dims& d, long seq) {
 
 __device__ __forceinline__ SeqIndex seq_index(const Dims& d) { return seq_at(d, blockIdx.x); }
 
-// Row s of a chunk's token-major slab: `width` floats per token-head, the
-// 64 columns from `offset` (a value tile of a P-wide row).
+// Row s of a chunk's token-major slab: `width` elements (float32 or
+// bfloat16) per token-head, the 64 columns from `offset` (a value tile of a
+// P-wide row).
+template <typename T>
 struct TokenRows {
-  const float* base;
+  const T* base;
   Dims d;
   int b, h, t0, width, offset;
-  __device__ const float* operator()(int s) const {
+  __device__ const T* operator()(int s) const {
     return base + token_head(d, b, t0 + s, h) * width + offset;
   }
 };
 
-__device__ __forceinline__ TokenRows rows_of(const float* base, const Dims& d, const SeqIndex& si) {
-  return TokenRows{base, d, si.b, si.h, si.n * d.chunk, 64, 0};
+template <typename T>
+__device__ __forceinline__ TokenRows<T> rows_of(const T* base, const Dims& d, const SeqIndex& si) {
+  return TokenRows<T>{base, d, si.b, si.h, si.n * d.chunk, 64, 0};
 }
 
 // Value tile v of a P-wide row slab (values, reads and their cotangents).
-__device__ __forceinline__ TokenRows value_rows(const float* base, const Dims& d,
-                                                const SeqIndex& si, int v) {
-  return TokenRows{base, d, si.b, si.h, si.n * d.chunk, d.P, 64 * v};
+template <typename T>
+__device__ __forceinline__ TokenRows<T> value_rows(const T* base, const Dims& d,
+                                                   const SeqIndex& si, int v) {
+  return TokenRows<T>{base, d, si.b, si.h, si.n * d.chunk, d.P, 64 * v};
 }
 
 // Tile v of chunk `seq`'s cross state [P, 64] (NV stacked 64x64 tiles).
@@ -68,9 +72,10 @@ __device__ __forceinline__ const float* cross_tile(const float* base, const Dims
 // after this chunk's are in LDS, its queries once this chunk's variance is
 // done, its values once this chunk's values are in LDS (at most five tiles
 // in flight per thread, keeping two blocks per CU).
+template <typename In>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_read_kernel(
-    Dims d, const float* __restrict__ keys, const float* __restrict__ values,
-    const float* __restrict__ queries, const float* __restrict__ beta,
+    Dims d, const In* __restrict__ keys, const In* __restrict__ values,
+    const In* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ solved,
     const float* __restrict__ start_c, float* __restrict__ output,
     float* __restrict__ variance) {
@@ -178,9 +183,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ...; the next chunk's dout, value and C0 tiles load into registers once
 // this chunk's last value tile is in LDS, its keys once this chunk's keys are
 // staged, and its queries and d_variance after this chunk's epilogue.
+template <typename In>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dy_kernel(
-    Dims d, const float* __restrict__ keys, const float* __restrict__ values,
-    const float* __restrict__ queries, const float* __restrict__ beta,
+    Dims d, const In* __restrict__ keys, const In* __restrict__ values,
+    const In* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ start_c,
     const float* __restrict__ d_output, const float* __restrict__ d_variance,
     float* __restrict__ ybar) {
@@ -207,7 +213,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       dvar[q] = 0.f;
       if (t < s.len) {
         const long th = token_head(d, s.b, s.n * d.chunk + t, s.h);
-        qv[q] = *reinterpret_cast<const f4*>(queries + th * 64 + c4);
+        qv[q] = load4(queries + th * 64 + c4);
         dvar[q] = d_variance[th];
       }
     }
@@ -299,8 +305,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 constexpr int GRADS_THREADS = 512;
 constexpr int MAX_NV = 2;
 
+template <typename In>
 __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
-    Dims d, const float* __restrict__ keys, const float* __restrict__ values,
+    Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ solved, const float* __restrict__ z,
     const float* __restrict__ d_output, const float* __restrict__ d_variance,
@@ -640,6 +647,21 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     }
   }
 }
+
+#define M4_CHUNK_KERNELS(In)                                                                  \
+  template __global__ void fwd_read_kernel<In>(Dims, const In*, const In*, const In*,          \
+                                               const float*, const float*, const float*,       \
+                                               const float*, float*, float*);                  \
+  template __global__ void bwd_dy_kernel<In>(Dims, const In*, const In*, const In*,            \
+                                             const float*, const float*, const float*,         \
+                                             const float*, const float*, float*);              \
+  template __global__ void bwd_grads_kernel<In>(                                               \
+      Dims, const In*, const In*, const float*, const float*, const float*, const float*,      \
+      const float*, const float*, const float*, const float*, const float*, const float*,      \
+      float*, float*, float*, float*, float*, float*);
+M4_CHUNK_KERNELS(float)
+M4_CHUNK_KERNELS(bf16_t)
+#undef M4_CHUNK_KERNELS
 
 // d floor[h][4c4 .. 4c4+3] = sum over (b, n) of floor_part[(b*H + h)*NC + n]
 // in a fixed order: block (h, c4) of 256 threads, thread i sums entries

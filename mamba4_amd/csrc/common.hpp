@@ -14,6 +14,21 @@ constexpr int TILE = 64 * LDT;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Inputs may be float32 or bfloat16 (raw 16-bit storage): loads widen to
+// float32, exactly (a bfloat16 is the high half of a float32).
+typedef unsigned short bf16_t;
+
+__device__ __forceinline__ f4 load4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ f4 load4(const bf16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return f4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+            __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+}
+__device__ __forceinline__ float load1(const float* p) { return *p; }
+__device__ __forceinline__ float load1(const bf16_t* p) {
+  return __uint_as_float((unsigned)*p << 16);
+}
+
 // Problem shape.  Chunks of `chunk` tokens carry the decayed statistics;
 // each chunk splits into `rsub` sub-chunks of up to `sub` tokens, and the
 // factor kernel starts one token sequence per sub-chunk from its stored
@@ -268,7 +283,7 @@ struct TileRegs {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = r0 + 16 * j;
-      v[j] = r < rows ? *reinterpret_cast<const f4*>(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
+      v[j] = r < rows ? load4(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
     }
   }
 
@@ -297,7 +312,7 @@ struct TileRegs2 {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = r0 + 32 * j;
-      v[j] = r < rows ? *reinterpret_cast<const f4*>(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
+      v[j] = r < rows ? load4(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
     }
   }
 
@@ -337,9 +352,10 @@ struct TileRegsT {
 
 // Arguments of the fused chunk-boundary state walk (states_kernel).
 struct StateArgs {
-  const float* rows_a;   // evidence a rows: forward keys (unused), backward z
-  const float* rows_ac;  // cross a rows: forward values, backward d_output
-  const float* rows_b;   // b rows: forward keys, backward solved
+  // Row slabs: float32, or in the forward the caller's input type.
+  const void* rows_a;    // evidence a rows: forward keys (unused), backward z
+  const void* rows_ac;   // cross a rows: forward values, backward d_output
+  const void* rows_b;    // b rows: forward keys, backward solved
   const float* beta;
   const float* log_decay;
   const float* first_s;  // state before the first step (NULL: zero)

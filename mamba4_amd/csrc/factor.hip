@@ -42,14 +42,15 @@ struct TokenInputs {
   long th;
 };
 
-__device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const float* keys,
-                                           const float* queries, const float* beta,
+template <typename In>
+__device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const In* keys,
+                                           const In* queries, const float* beta,
                                            const float* log_decay, int b, int h, int t, int a) {
   in.th = token_head(d, b, t, h);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    in.k[m] = keys[in.th * 64 + a + 16 * m];
-    in.q[m] = queries[in.th * 64 + a + 16 * m];
+    in.k[m] = load1(keys + in.th * 64 + a + 16 * m);
+    in.q[m] = load1(queries + in.th * 64 + a + 16 * m);
   }
   in.beta = beta[in.th];
   in.log_lam = log_decay[in.th];
@@ -62,8 +63,9 @@ __device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const
 // registers.  Only these short update turns are serialized; the two waves'
 // factorizations and solves overlap, and a block holds one 40 KB evidence
 // buffer for two waves.
+template <typename In>
 __global__ __launch_bounds__(128) void fwd_factor_kernel(
-    Dims d, const float* __restrict__ keys, const float* __restrict__ queries,
+    Dims d, const In* __restrict__ keys, const In* __restrict__ queries,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ floor, const float* __restrict__ start_s,
     float* __restrict__ solved, float* __restrict__ factors) {
@@ -148,6 +150,13 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
     }
   }
 }
+
+template __global__ void fwd_factor_kernel<float>(Dims, const float*, const float*, const float*,
+                                                  const float*, const float*, const float*,
+                                                  float*, float*);
+template __global__ void fwd_factor_kernel<bf16_t>(Dims, const bf16_t*, const bf16_t*,
+                                                   const float*, const float*, const float*,
+                                                   const float*, float*, float*);
 
 // z = A^-1 rhs from stored factors; four token-heads per wave.
 __global__ __launch_bounds__(64) void factored_solve_kernel(const float* __restrict__ factors,

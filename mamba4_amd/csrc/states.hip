@@ -24,8 +24,9 @@ namespace m4 {
 
 __device__ __forceinline__ float* mat(float* base, long index) { return base + index * 4096; }
 
+template <typename In>
 __global__ __launch_bounds__(256) void fwd_stats_kernel(
-    Dims d, const float* __restrict__ keys, const float* __restrict__ values,
+    Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     float* __restrict__ start_s, float* __restrict__ start_c) {
   extern __shared__ float smem[];
@@ -37,7 +38,7 @@ __global__ __launch_bounds__(256) void fwd_stats_kernel(
   const int n = (int)(seq % d.NC), bh = (int)(seq / d.NC), b = bh / d.H, h = bh % d.H;
   const int len = chunk_len(d, n), w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   const int kt = k_terms(len);
-  auto rows = [&](const float* base, int width, int offset) {
+  auto rows = [&](const In* base, int width, int offset) {
     return [=](int s) { return base + token_head(d, b, n * d.chunk + s, h) * width + offset; };
   };
   TileRegs rk, rv;
@@ -309,8 +310,13 @@ __device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const 
   }
 }
 
-template <bool BWD>
+// In: element type of the forward's key and value rows (the backward's rows
+// are float32).
+template <bool BWD, typename In>
 __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArgs g) {
+  const In* rows_a = static_cast<const In*>(g.rows_a);
+  const In* rows_ac = static_cast<const In*>(g.rows_ac);
+  const In* rows_b = static_cast<const In*>(g.rows_b);
   extern __shared__ float smem[];  // buffer u: b tile at 2u TILE, a tile at (2u + 1) TILE
   __shared__ StepBuffer sb[2];
   const int bh = blockIdx.x, b = bh / d.H, h = bh % d.H;
@@ -351,11 +357,11 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
   };
   auto fetch = [&](StepRegs& R, int i) {
     const int first = i * d.chunk, cnt = chunk_len(d, i);
-    R.rb.fetch_rows(cnt, [&](int r) { return g.rows_b + token_head(d, b, first + r, h) * 64; });
+    R.rb.fetch_rows(cnt, [&](int r) { return rows_b + token_head(d, b, first + r, h) * 64; });
     if (own_a) {
       const int width = cross ? d.P : 64, offset = cross ? 64 * v : 0;
       R.ra.fetch_rows(cnt, [&](int r) {
-        return (cross ? g.rows_ac : g.rows_a) + token_head(d, b, first + r, h) * width + offset;
+        return (cross ? rows_ac : rows_a) + token_head(d, b, first + r, h) * width + offset;
       });
     }
     R.pg = 0.f;
@@ -435,7 +441,12 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
 }
 
-template __global__ void states_kernel<false>(Dims, StateArgs);
-template __global__ void states_kernel<true>(Dims, StateArgs);
+template __global__ void states_kernel<false, float>(Dims, StateArgs);
+template __global__ void states_kernel<false, bf16_t>(Dims, StateArgs);
+template __global__ void states_kernel<true, float>(Dims, StateArgs);
+template __global__ void fwd_stats_kernel<float>(Dims, const float*, const float*, const float*,
+                                                 const float*, float*, float*);
+template __global__ void fwd_stats_kernel<bf16_t>(Dims, const bf16_t*, const bf16_t*,
+                                                  const float*, const float*, float*, float*);
 
 }  // namespace m4

@@ -85,7 +85,9 @@ def _value_width(value_dim):
 
 
 class _MemoryRead(torch.autograd.Function):
-    """Custom VJP around m4mr_forward / m4mr_backward (D = 64, P = 64 or 128)."""
+    """Custom VJP around m4mr_forward / m4mr_backward (D = 64, P = 64 or 128;
+    keys, values and queries float32, or all bfloat16 through the _bf16
+    entry points)."""
 
     @staticmethod
     def forward(ctx, keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk):
@@ -103,8 +105,10 @@ class _MemoryRead(torch.autograd.Function):
         factors = torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
         start_s = torch.empty((batch, heads, starts, 64, 64), **f32)
         start_c = torch.empty((batch, heads, count, width, 64), **f32)
+        # bfloat16 keys, values and queries are read and widened in the kernels.
+        entry = lib.m4mr_forward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_forward
         _lib.check(
-            lib.m4mr_forward(
+            entry(
                 _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
                 _ptr(floor), _ptr(init_s), _ptr(init_c), batch, time, heads, width, chunk,
                 _ptr(output), _ptr(variance), _ptr(final_s), _ptr(final_c),
@@ -130,21 +134,23 @@ class _MemoryRead(torch.autograd.Function):
 
         def dense(g, like):
             if g is None:
-                return torch.zeros_like(like)
+                return torch.zeros(like.shape, dtype=torch.float32, device=like.device)
             return g.to(torch.float32).contiguous()
 
         d_output = dense(d_output, values)
         d_variance = dense(d_variance, beta)
         d_final_s = None if d_final_s is None else d_final_s.to(torch.float32).contiguous()
         d_final_c = None if d_final_c is None else d_final_c.to(torch.float32).contiguous()
-        grads = [torch.empty_like(t) for t in (keys, values, queries, beta, log_decay, floor)]
         f32 = dict(dtype=torch.float32, device=keys.device)
+        grads = [torch.empty(t.shape, **f32) for t in (keys, values, queries, beta, log_decay,
+                                                        floor)]
         d_init_s = torch.empty((batch, heads, _lib.KEY_DIM, _lib.KEY_DIM), **f32)
         d_init_c = torch.empty((batch, heads, width, _lib.KEY_DIM), **f32)
         nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, width, chunk)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
+        entry = lib.m4mr_backward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_backward
         _lib.check(
-            lib.m4mr_backward(
+            entry(
                 _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
                 _ptr(floor), batch, time, heads, width, chunk, _ptr(solved), _ptr(factors),
                 _ptr(start_s), _ptr(start_c), _ptr(d_output), _ptr(d_variance),
@@ -257,7 +263,11 @@ def selective_gaussian_memory(
     if queries.shape != keys.shape or values.shape[:3] != keys.shape[:3]:
         raise ValueError("Selective memory keys, values and queries disagree")
     _require_device(keys, values, queries)
-    keys, values, queries = (a.to(torch.float32) for a in (keys, values, queries))
+    # bfloat16 keys, values and queries stay bfloat16: the kernels widen them
+    # on load, exactly as the reference's upcast (lm/kernels/mamba4.py:263-265).
+    # Any other mix is upcast here.
+    if not all(a.dtype == torch.bfloat16 for a in (keys, values, queries)):
+        keys, values, queries = (a.to(torch.float32) for a in (keys, values, queries))
     if dim > _lib.KEY_DIM:
         raise ValueError(f"key widths must be <= {_lib.KEY_DIM}; got {dim}")
     width = _value_width(value_dim)

@@ -468,3 +468,53 @@ def test_state_walk_choice_at_full_batch(gpu_lib, monkeypatch):
         c = lam[:, t, :, None, None] * c + b[:, t, :, None, None] * v[:, t][..., :, None] * kt[..., None, :]
     assert normwise(results["auto"]["evidence"], s) <= 1e-5
     assert normwise(results["auto"]["cross"], c) <= 1e-5
+
+
+@pytest.mark.parametrize("value_dim,chunk,batch,heads", [(64, 64, 2, 3), (128, 48, 2, 2),
+                                                         (64, 64, 32, 8)])
+def test_bf16_inputs_match_the_upcast_path_bit_for_bit(gpu_lib, value_dim, chunk, batch, heads):
+    """bfloat16 keys, values and queries go to m4mr_forward_bf16 /
+    m4mr_backward_bf16, which widen them in the kernels; the reference
+    upcasts them first (lm/kernels/mamba4.py:263-265).  Widening is exact,
+    so outputs, states and every gradient equal the float32 path on the
+    upcast arrays bit for bit (both state walks: B*H = 6, 4 and 256)."""
+    from mamba4_amd import SelectiveState, _lib, selective_gaussian_memory
+
+    data = arrays(time=90, heads=heads, dim=64, value_dim=value_dim, seed=value_dim + batch,
+                  batch=batch)
+    data["floor"] = np.full_like(data["floor"], 0.05)
+    rng = np.random.default_rng(7)
+    root = rng.normal(size=(batch, heads, 64, 64)) / 64
+    s0 = (root @ np.swapaxes(root, -1, -2)).astype(np.float32)
+    c0 = (rng.normal(size=(batch, heads, value_dim, 64)) * 0.3).astype(np.float32)
+    d_out = torch.tensor(rng.normal(size=data["values"].shape), dtype=torch.float32,
+                         device="cuda:0")
+    d_var = torch.tensor(rng.normal(size=data["beta"].shape), dtype=torch.float32,
+                         device="cuda:0")
+    announce(f"bf16 inputs P={value_dim} chunk={chunk} B{batch} H{heads} T90")
+    results = []
+    for dtype in (torch.bfloat16, torch.float32):
+        qkv = [torch.tensor(data[n], device="cuda:0").to(torch.bfloat16).to(dtype)
+               .requires_grad_(True) for n in ("keys", "values", "queries")]
+        rest = [torch.tensor(data[n], device="cuda:0").requires_grad_(True)
+                for n in ("beta", "log_decay", "floor")]
+        init = [torch.tensor(a, device="cuda:0").requires_grad_(True) for a in (s0, c0)]
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        try:
+            r = selective_gaussian_memory(qkv[0], qkv[1], qkv[2], *rest, chunk_size=chunk,
+                                          initial=SelectiveState(*init))
+            ((r.output * d_out).sum() + (r.variance * d_var).sum()
+             + r.state.evidence.sum() + r.state.cross.sum()).backward()
+        finally:
+            _lib.profile_enable(False)
+        _lib.profile_reset()
+        torch.cuda.synchronize()
+        grads = [t.grad.float() for t in qkv + rest + init]
+        results.append([r.output, r.variance, r.state.evidence, r.state.cross] + grads)
+    # The bfloat16 inputs' gradients reach them rounded to bfloat16 (autograd
+    # casts a gradient to its input's dtype); everything else is float32.
+    for i, (got, want) in enumerate(zip(*results)):
+        if 4 <= i < 7:
+            want = want.to(torch.bfloat16).float()
+        assert torch.equal(got, want), i
