@@ -17,12 +17,17 @@ states are the end states of a 1024-token gated recurrence with
 lambda = sigmoid(N(3,1)), built by this library's own forward, and each step
 writes one new token into every state, refactors and reads.
 
+With --workload config3 the step is the same fwd+bwd at BASELINE config 3
+(B=32, L=1024, H=12, slow decay) with bfloat16 keys, values and queries
+read natively by the kernels (m4mr_forward_bf16 / m4mr_backward_bf16).
+
 With --workload mixer a step is the memory read's neighbours on the same
 config-2 shape: the mixer prologue (key shift, unit q/k, gates, floor) and
 epilogue (confidence gate, D-skip), and the order head's gated scan, each
 forward and backward; every kernel is HBM-bound and reported against 8 TB/s.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload config2|config4|mixer]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--workload config2|config3|config4|mixer]
 """
 
 import argparse
@@ -41,6 +46,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "memory-read fwd+bwd tokens/sec at B16 L1024 H8 d64; % fp32 peak, % HBM BW"
+CONFIG3_METRIC = "memory-read fwd+bwd tokens/sec at B32 L1024 H12 d64, bf16 q/k/v"
 HBM_PEAK_GBPS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 FACTOR_BYTES = 8320  # packed lower factor per token-head
@@ -99,7 +105,7 @@ def measured_traffic(kernel, summary=TRAFFIC_SUMMARY):
     return None
 
 
-def roofline(kernel, ms, token_heads):
+def roofline(kernel, ms, token_heads, traffic=True):
     bound, amount, unit = KERNEL_WORK[kernel]
     seconds = ms / 1e3
     if bound == "hbm":
@@ -115,7 +121,7 @@ def roofline(kernel, ms, token_heads):
         "peak": peak,
         "unit": unit_out,
         "frac": achieved / peak,
-        "traffic": measured_traffic(kernel),
+        "traffic": measured_traffic(kernel) if traffic else None,
         "traffic_unit": "B per launch (rocprofv3, profiles/config2_hbm_traffic.md)",
         "algorithmic_bytes" if bound == "hbm" else "algorithmic_flop": amount * token_heads,
     }
@@ -127,7 +133,8 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--chunk", type=int, default=64)
-    p.add_argument("--workload", default="config2", choices=["config2", "config4", "mixer"])
+    p.add_argument("--workload", default="config2",
+                   choices=["config2", "config3", "config4", "mixer"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -135,12 +142,13 @@ def parse():
 class Problem:
     """Device buffers for one fwd+bwd step through the C ABI."""
 
-    def __init__(self, data, chunk):
+    def __init__(self, data, chunk, bf16_inputs=False):
         import torch
 
         from mamba4_amd import _lib
 
         self.lib = _lib.load()
+        self.bf16 = bf16_inputs
         self.check = _lib.check
         dev = torch.device("cuda:0")
         self.B, self.T, self.H, _ = data["keys"].shape
@@ -152,6 +160,9 @@ class Problem:
             return torch.tensor(np.asarray(a, np.float32), device=dev)
 
         self.inputs = [put(data[n]) for n in NAMES]
+        if bf16_inputs:
+            # Keys, values and queries in bfloat16, read by the _bf16 entry points.
+            self.inputs[:3] = [t.to(torch.bfloat16) for t in self.inputs[:3]]
         self.d_output = put(data["d_output"])
         self.d_variance = put(data["d_variance"])
         f32 = dict(dtype=torch.float32, device=dev)
@@ -165,7 +176,7 @@ class Problem:
             torch.empty(B, H, starts, 64, 64, **f32),  # start evidence
             torch.empty(B, H, count, 64, 64, **f32),  # start cross
         ]
-        self.grads = [torch.empty_like(t) for t in self.inputs]
+        self.grads = [torch.empty(t.shape, **f32) for t in self.inputs]
         self.d_init = [torch.empty(B, H, 64, 64, **f32), torch.empty(B, H, 64, 64, **f32)]
         self.ws_bytes = self.lib.m4mr_backward_workspace_bytes(B, T, H, 64, chunk)
         self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
@@ -174,16 +185,15 @@ class Problem:
     def forward(self):
         p = [t.data_ptr() for t in self.inputs]
         o = [t.data_ptr() for t in self.fwd_out]
-        self.check(
-            self.lib.m4mr_forward(*p, None, None, self.B, self.T, self.H, 64, self.chunk, *o,
-                                  self.stream)
-        )
+        entry = self.lib.m4mr_forward_bf16 if self.bf16 else self.lib.m4mr_forward
+        self.check(entry(*p, None, None, self.B, self.T, self.H, 64, self.chunk, *o, self.stream))
 
     def backward(self):
         p = [t.data_ptr() for t in self.inputs]
         o = self.fwd_out
+        entry = self.lib.m4mr_backward_bf16 if self.bf16 else self.lib.m4mr_backward
         self.check(
-            self.lib.m4mr_backward(
+            entry(
                 *p, self.B, self.T, self.H, 64, self.chunk, o[4].data_ptr(), o[5].data_ptr(),
                 o[6].data_ptr(), o[7].data_ptr(), self.d_output.data_ptr(),
                 self.d_variance.data_ptr(), None, None, *(g.data_ptr() for g in self.grads),
@@ -578,7 +588,7 @@ def main():
     if args.workload == "mixer":
         return main_mixer(args)
     data = workload_inputs(args.workload, seed=0, cotangents=True)
-    problem = Problem(data, args.chunk)
+    problem = Problem(data, args.chunk, bf16_inputs=args.workload == "config3")
     B, T, H = problem.B, problem.T, problem.H
     token_heads = B * T * H
 
@@ -628,8 +638,15 @@ def main():
     load_gbps = RESOLVE_BYTES * token_heads / resolve_s / 1e9
     copy_gbps = copy_bandwidth_gbps()
 
+    if args.workload == "config3":
+        metric = CONFIG3_METRIC
+        workload = ("config3: memory-read fwd+bwd, B=32 L=1024 H=12 D=P=64, bf16 q/k/v read "
+                    "natively (fp32 arithmetic), lambda = sigmoid(N(4,1)), floor 1e-2")
+    else:
+        metric = METRIC
+        workload = "config2: memory-read fwd+bwd, B=16 L=1024 H=8 D=P=64 fp32, floor 1e-2"
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": B * T / seconds,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -642,7 +659,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "config2: memory-read fwd+bwd, B=16 L=1024 H=8 D=P=64 fp32, floor 1e-2",
+            "workload": workload,
             "batch": B,
             "seq_len": T,
             "heads": H,
@@ -650,7 +667,9 @@ def main():
             "value_dim": 64,
             "chunk": args.chunk,
         },
-        "roofline": roofline(dominant, kernels[dominant], token_heads),
+        # The committed rocprof traffic summary is for config 2.
+        "roofline": roofline(dominant, kernels[dominant], token_heads,
+                             traffic=args.workload == "config2"),
         "factorization_fp32": {
             "kernel": "fwd_factor",
             "achieved_tflops": CHOLESKY_FLOP * token_heads / factor_s / 1e12,
@@ -665,7 +684,8 @@ def main():
             "copy_kernel_GBps": copy_gbps,
         },
         "kernel_ms": kernels,
-        "kernel_roofline": {k: roofline(k, v, token_heads)["frac"] for k, v in kernels.items()},
+        "kernel_roofline": {k: roofline(k, v, token_heads, traffic=False)["frac"]
+                            for k, v in kernels.items()},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(data)
