@@ -387,7 +387,8 @@ __device__ __forceinline__ void load_rows16(float (&A)[4][64], const float* __re
     const int p = (a + 16 * m) >> 2;
 #pragma unroll
     for (int q = 0; q < 4 * m + 4; ++q) {
-      const f4 v = lane[run_quad(m, q)];
+      // Non-temporal: each factor is read once, by this solve.
+      const f4 v = __builtin_nontemporal_load(&lane[run_quad(m, q)]);
       const bool in = q <= p;
       A[m][4 * q] = in ? v[0] : 0.f;
       A[m][4 * q + 1] = in ? v[1] : 0.f;
