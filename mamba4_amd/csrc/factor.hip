@@ -131,6 +131,22 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
             if ((q & 3) == 3) __builtin_amdgcn_sched_barrier(0);
           }
         }
+        // The trailing blocks (I, K >= 1) read back exchanged from the
+        // buffer this wave just wrote (LDS accesses of a wave complete in
+        // order): lane (g, j) takes quad 4K + g of row 16I + j of every
+        // sequence mu into A[I][16K + 4mu .. +3].  Replaces six register
+        // block exchanges (96 lane swaps) by 24 reads.
+        const int g = lane >> 4;
+#pragma unroll
+        for (int I = 1; I < 4; ++I)
+#pragma unroll
+          for (int K = 1; K <= I; ++K)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const f4 v = evidence[slot_quad(I, 4 * K + g) * 64 + 16 * s + a];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * s + e] = v[e];
+            }
       }
       __syncthreads();
     }
@@ -139,7 +155,7 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
       TokenInputs next;
       load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
       float nw[4], y[4];
-      factor_rows16(A, fl, cur.q, nw);
+      factor_exchanged(A, fl, cur.q, nw);
       backward_rows16(A, nw, y);
       if (valid) {
 #pragma unroll
