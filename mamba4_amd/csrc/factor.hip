@@ -56,20 +56,36 @@ __device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const
   in.log_lam = log_decay[in.th];
 }
 
+// Wait until the evidence buffer holds the updates of tokens 0..tt-1.  The
+// other wave of the block publishes each of its turns by writing the count;
+// a wait lasts at most one factorization of that wave plus its turn.  Bounded
+// all the same: after 2^16 polls (about 5 ms) the wave goes on.
+typedef __attribute__((address_space(3))) volatile int lds_int;
+
+__device__ __forceinline__ void wait_turn(lds_int* count, int tt) {
+  for (int i = 0; i < (1 << 16); ++i) {
+    if (__builtin_amdgcn_readfirstlane(*count) >= tt) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");  // no evidence read moves above the wait
+}
+
 // Two waves share the four sequences of a block and take alternate tokens:
 // wave w factors tokens base+w for base = 0, 2, 4, ...  The running evidence
-// lives in LDS; in turn (wave 0, then wave 1) each wave reads it, applies
-// its token's rank-one update, writes it back and keeps the updated copy in
-// registers.  Only these short update turns are serialized; the two waves'
-// factorizations and solves overlap, and a block holds one 40 KB evidence
-// buffer for two waves.
+// lives in LDS; each wave in its turn reads it, applies its token's rank-one
+// update, writes it back and keeps the updated copy in registers.  A turn
+// starts as soon as the other wave's previous turn is published (a token
+// count in LDS, no block barrier), so each wave runs turn, factorization,
+// turn, ... without waiting out the other wave's turn, the two waves offset
+// by one turn.  A block holds one 40 KB evidence buffer for two waves.
 template <typename In>
 __global__ __launch_bounds__(128) void fwd_factor_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ queries,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ floor, const float* __restrict__ start_s,
     float* __restrict__ solved, float* __restrict__ factors) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, a = lane & 15, mu = lane >> 4;
+  const int lane = threadIdx.x & 63, a = lane & 15, mu = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int BH = d.B * d.H;
   const long nseq = (long)BH * d.NS;
   long seq = (long)blockIdx.x * 4 + mu;
@@ -85,6 +101,11 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
 
   // The running evidence, negated (the factorization's working convention).
   __shared__ f4 evidence[40 * 64];  // [quad][lane], shared by both waves
+  // The turn count lives in the buffer (which fills the block's share of
+  // LDS at four blocks per CU): word 0 of lane 0's quad (0, 3), row 0,
+  // columns 12..15 of sequence 0, above the diagonal.  No turn writes that
+  // quad; the factorization reads it as scratch and zeroes it.
+  lds_int* const turn_count = (lds_int*)(&evidence[slot_quad(0, 3) * 64]);
   if (wave == 0) {
     const float* s0 = start_s + ((long)bh * d.NS + ns) * 4096;
 #pragma unroll
@@ -93,6 +114,7 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
       for (int q = 0; q < 4 * m + 4; ++q)
         evidence[slot_quad(m, q) * 64 + lane] =
             -*reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
+    if (lane == 0) *turn_count = 0;  // after this lane's quad (0, 3): LDS writes stay in order
   }
   float fl[4];
 #pragma unroll
@@ -105,65 +127,62 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
 
   for (int base = 0; base < steps; base += 2) {
     const int tt = base + wave;
-    const bool mine = tt < steps;  // uniform over the wave
-    const bool valid = tt < len;   // per 16-lane row
+    if (tt >= steps) break;       // uniform over the wave (wave 1, odd step counts)
+    const bool valid = tt < len;  // per 16-lane row
     float A[4][64];
+    wait_turn(turn_count, tt);
+    const float lam = expf(cur.log_lam);
 #pragma unroll
-    for (int turn = 0; turn < 2; ++turn) {
-      if (turn == wave && mine) {
-        const float lam = expf(cur.log_lam);
+    for (int m = 0; m < 4; ++m) {
+      const float nbk = -cur.beta * cur.k[m];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const float nbk = -cur.beta * cur.k[m];
+      for (int q = 0; q < 4 * m + 4; ++q) {
+        f4 sv = evidence[slot_quad(m, q) * 64 + lane];
 #pragma unroll
-          for (int q = 0; q < 4 * m + 4; ++q) {
-            f4 sv = evidence[slot_quad(m, q) * 64 + lane];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int k = 4 * q + e;
-              sv[e] = lam * sv[e] + nbk * bcast16(cur.k[k >> 4], k & 15);
-              A[m][k] = sv[e];
-            }
-            evidence[slot_quad(m, q) * 64 + lane] = sv;
-            // Every fourth quad: keeps the compiler from hoisting all 40 LDS
-            // reads ahead of the arithmetic (which would need 160 more
-            // registers) while four reads stay in flight together.
-            if ((q & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-          }
+        for (int e = 0; e < 4; ++e) {
+          const int k = 4 * q + e;
+          sv[e] = lam * sv[e] + nbk * bcast16(cur.k[k >> 4], k & 15);
+          A[m][k] = sv[e];
         }
-        // The trailing blocks (I, K >= 1) read back exchanged from the
-        // buffer this wave just wrote (LDS accesses of a wave complete in
-        // order): lane (g, j) takes quad 4K + g of row 16I + j of every
-        // sequence mu into A[I][16K + 4mu .. +3].  Replaces six register
-        // block exchanges (96 lane swaps) by 24 reads.
-        const int g = lane >> 4;
-#pragma unroll
-        for (int I = 1; I < 4; ++I)
-#pragma unroll
-          for (int K = 1; K <= I; ++K)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const f4 v = evidence[slot_quad(I, 4 * K + g) * 64 + 16 * s + a];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * s + e] = v[e];
-            }
+        if (m != 0 || q != 3 || lane != 0) evidence[slot_quad(m, q) * 64 + lane] = sv;
+        // Every fourth quad: keeps the compiler from hoisting all 40 LDS
+        // reads ahead of the arithmetic (which would need 160 more
+        // registers) while four reads stay in flight together.
+        if ((q & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
-      __syncthreads();
     }
-    if (mine) {
-      // Prefetch this wave's next token; the factorization covers the latency.
-      TokenInputs next;
-      load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
-      float nw[4], y[4];
-      factor_exchanged(A, fl, cur.q, nw);
-      backward_rows16(A, nw, y);
-      if (valid) {
+    // The trailing blocks (I, K >= 1) read back exchanged from the buffer
+    // this wave just wrote (LDS accesses of a wave complete in order): lane
+    // (g, j) takes quad 4K + g of row 16I + j of every sequence mu into
+    // A[I][16K + 4mu .. +3].  Replaces six register block exchanges (96
+    // lane swaps) by 24 reads.
+    const int g = lane >> 4;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) solved[cur.th * 64 + a + 16 * m] = y[m];
-        store_rows16(A, factors + cur.th * ROWS_FACTOR);
-      }
-      cur = next;
+    for (int I = 1; I < 4; ++I)
+#pragma unroll
+      for (int K = 1; K <= I; ++K)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const f4 v = evidence[slot_quad(I, 4 * K + g) * 64 + 16 * s + a];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * s + e] = v[e];
+        }
+    // Publish the turn once every LDS access of it has completed.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (lane == 0) *turn_count = tt + 1;
+
+    // Prefetch this wave's next token; the factorization covers the latency.
+    TokenInputs next;
+    load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
+    float nw[4], y[4];
+    factor_exchanged(A, fl, cur.q, nw);
+    backward_rows16(A, nw, y);
+    if (valid) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) solved[cur.th * 64 + a + 16 * m] = y[m];
+      store_rows16(A, factors + cur.th * ROWS_FACTOR);
     }
+    cur = next;
   }
 }
 
