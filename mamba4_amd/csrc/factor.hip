@@ -200,11 +200,13 @@ __global__ __launch_bounds__(64) void factored_solve_kernel(const float* __restr
   long th = (long)blockIdx.x * 4 + mu;
   const bool active = th < N;
   if (!active) th = N - 1;
-  float A[4][64];
-  load_rows16(A, factors + th * ROWS_FACTOR);
+  // The right-hand side first: the forward substitution needs it at its
+  // first step, and loads retire in issue order.
   float r[4], y[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) r[m] = rhs[th * 64 + a + 16 * m];
+  float A[4][64];
+  load_rows16(A, factors + th * ROWS_FACTOR);
   solve_rows16(A, r, y);
   if (active)
 #pragma unroll
@@ -279,8 +281,6 @@ __global__ __launch_bounds__(64) void spd_backward_kernel(
   long n = (long)blockIdx.x * 4 + mu;
   const bool active = n < N;
   if (!active) n = N - 1;
-  float A[4][64];
-  load_rows16(A, factors + n * ROWS_FACTOR);
   float g[4], y[4], z[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
@@ -288,6 +288,8 @@ __global__ __launch_bounds__(64) void spd_backward_kernel(
     g[m] = i < dim ? d_solution[n * dim + i] : 0.f;
     y[m] = i < dim ? solution[n * dim + i] : 0.f;
   }
+  float A[4][64];
+  load_rows16(A, factors + n * ROWS_FACTOR);
   solve_rows16(A, g, z);
   if (!active) return;
 #pragma unroll

@@ -374,22 +374,25 @@ __device__ __forceinline__ void store_rows16(const float (&A)[4][64], float* __r
   }
 }
 
-// Every load is unconditional: quad run_quad(m, q) + a lies inside the
-// factor for every lane a and q <= 4m + 3 (the runs of a slot are laid out
-// for 16 lanes), so lanes past their row's last quad read a neighbour's
-// entry and zero it.  A load under a per-lane branch would make the compiler
-// wait for it inside the branch, serialising the stream.
+// Every load is unconditional (a load under a per-lane branch would make
+// the compiler wait for it inside the branch, serialising the stream).  In a
+// run q = 4m + r (r = 1..3, lanes 4r..15) the lanes below 4r read the run's
+// first quad, so each instruction touches only its own run's lines, and zero
+// what they read.  The loads go column quad by column quad (q outer), in the
+// order the forward substitution consumes them: vmcnt retires loads in issue
+// order, so the first steps wait for the first few quads, not for all 40.
 __device__ __forceinline__ void load_rows16(float (&A)[4][64], const float* __restrict__ fac) {
   const int a = threadIdx.x & 15;
-  const f4* lane = reinterpret_cast<const f4*>(fac) + a;
+  const f4* base = reinterpret_cast<const f4*>(fac);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int p = (a + 16 * m) >> 2;
+  for (int q = 0; q < 16; ++q) {
 #pragma unroll
-    for (int q = 0; q < 4 * m + 4; ++q) {
+    for (int m = q / 4; m < 4; ++m) {  // slot m holds quads q <= 4m + 3
+      const int r = q - 4 * m;  // > 0: a partial run starting at lane 4r
+      const int lane = r > 0 ? max(a, 4 * r) : a;
       // Non-temporal: each factor is read once, by this solve.
-      const f4 v = __builtin_nontemporal_load(&lane[run_quad(m, q)]);
-      const bool in = q <= p;
+      const f4 v = __builtin_nontemporal_load(base + run_quad(m, q) + lane);
+      const bool in = r <= 0 || a >= 4 * r;
       A[m][4 * q] = in ? v[0] : 0.f;
       A[m][4 * q + 1] = in ? v[1] : 0.f;
       A[m][4 * q + 2] = in ? v[2] : 0.f;
