@@ -369,15 +369,22 @@ decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     // Coalesced update of rows 16m .. 16m+15; the row's key comes from the
-    // lane that holds it in this row's slot (bcast16 of kr[m]).
+    // lane that holds it in this row's slot (bcast16 of kr[m]).  All 16
+    // loads are issued before the first store (a store between them would
+    // leave one load in flight at a time).
+    f4* rows = reinterpret_cast<f4*>(S + 16 * m * 64) + a;
+    f4 sv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sv[r] = __builtin_nontemporal_load(rows + 16 * r);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      f4* p = reinterpret_cast<f4*>(S + (16 * m + r) * 64) + a;
       const float bk = bt * bcast16(kr[m], r);
-      const f4 sv = lam * *p + bk * kq;
-      if (active) *p = sv;
-      mine[r * 17 + a] = sv;
+      sv[r] = lam * sv[r] + bk * kq;
+      mine[r * 17 + a] = sv[r];
     }
+    if (active)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(sv[r], rows + 16 * r);
     __syncthreads();
     // Into the factorization layout, negated: block column 0 as row a of this
     // slot, blocks (m, K >= 1) exchanged (lane (g, j) takes quad 4K + g of
@@ -417,16 +424,23 @@ decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
     for (int m = 0; m < 4; ++m) vr[m] = value[nidx * P + 64 * v + a + 16 * m];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
+      // As for S: the slot's 16 row loads go out together.
+      f4* rows = reinterpret_cast<f4*>(C + 16 * m * 64) + a;
+      f4 cv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) cv[r] = __builtin_nontemporal_load(rows + 16 * r);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        f4* p = reinterpret_cast<f4*>(C + (16 * m + r) * 64) + a;
         const float bv = bt * bcast16(vr[m], r);
-        const f4 cv = lam * *p + bv * kq;
-        if (active) *p = cv;
+        cv[r] = lam * cv[r] + bv * kq;
         // Row 16m + r of the read, summed over the 16 column quads.
-        const float part = sum16(cv[0] * yq[0] + cv[1] * yq[1] + cv[2] * yq[2] + cv[3] * yq[3]);
+        const float part =
+            sum16(cv[r][0] * yq[0] + cv[r][1] * yq[1] + cv[r][2] * yq[2] + cv[r][3] * yq[3]);
         out[m] = a == r ? part : out[m];
       }
+      if (active)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(cv[r], rows + 16 * r);
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m)
