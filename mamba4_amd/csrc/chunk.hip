@@ -293,11 +293,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-// Eight waves per chunk: wave w8 computes the 16-row strip ws = w8 % 4 of
-// every product, columns of half hf = w8 / 4 (two of the four 16-column
-// blocks; tile_mma_half), so each SIMD runs two waves of one chunk and one
-// wave's epilogue, LDS staging and barriers overlap the other's MFMAs.  Row
-// sums that span both halves meet in LDS and are added in half order.
+// Eight waves per chunk: wave w8 computes the 16-row strip ws of every
+// product, columns of half hf = w8 / 4 (two of the four 16-column blocks;
+// tile_mma_half), so each SIMD runs two waves of one chunk and one wave's
+// epilogue, LDS staging and barriers overlap the other's MFMAs.  Row sums
+// that span both halves meet in LDS and are added in half order.
+//
+// The causal products skip what the mask zeroes: the within-chunk scores
+// (phase 1) only their blocks with s <= t, the masked contractions over t
+// (phase 2) only their terms t >= s.  Strip ws then costs ws + 1 blocks in
+// phase 1 and 4 - ws term blocks in phase 2, so the strips are paired
+// {k, 3 - k} on the waves k and k + 4 that share a SIMD (ws = w8 for
+// w8 < 4, 7 - w8 above).
 //
 // Value-dependent terms run once per 64-column value tile (NV <= 2): gv and
 // H^T v sum over the tiles, d values and H k are per tile; the tiles are
@@ -331,9 +338,12 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   __shared__ float red[GRADS_THREADS];
   __shared__ f4 fpart[8][16];
   const SeqIndex si = seq_index(d);
-  const int w8 = threadIdx.x >> 6, ws = w8 & 3, hf = w8 >> 2, l = lane_id();
+  const int w8 = threadIdx.x >> 6, ws = w8 < 4 ? w8 : 7 - w8, hf = w8 >> 2, l = lane_id();
   const int r = l & 15, c4 = 4 * r;
   const int kt = k_terms(si.len), last = d.NV - 1;
+  // Column blocks of this wave's half that hold some s <= t of its strip,
+  // and the first t of its strip (the masked products vanish outside).
+  const int causal_nj = min(2, max(0, ws - 2 * hf + 1)), t_begin = 16 * ws;
   // d_variance of this thread's tile-fetch rows (threadIdx/16 + 32j).
   float dvar[2];
 #pragma unroll
@@ -370,9 +380,9 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     zero2(gy);
     zero2(gz);
     zero2(gv);
-    tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf);
-    tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf);
-    tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf);
+    tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf, 0, causal_nj);
+    tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf, 0, causal_nj);
+    tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
     for (int v = 1; v < d.NV; ++v) {
       TileRegs2 rv, rd;
       rv.fetch_rows(si.len, value_rows(values, d, si, v));
@@ -381,7 +391,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       rv.store(Vt);
       rd.store(Dt);
       __syncthreads();
-      tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf);
+      tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
     }
     float rsum[4] = {0.f, 0.f, 0.f, 0.f};
     float csum[2] = {0.f, 0.f};
@@ -429,8 +439,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   {
     f4 tmp[2];
     zero2(tmp);
-    tile_mma_half<true, false>(dk, M2, Yt, kt, ws, hf);   // sum_t W(gv-gz)[t][s] y_t
-    tile_mma_half<true, false>(tmp, M1, Zt, kt, ws, hf);  // sum_t W gy[t][s] z_t
+    tile_mma_half<true, false>(dk, M2, Yt, kt, ws, hf, t_begin);   // sum_t W(gv-gz)[t][s] y_t
+    tile_mma_half<true, false>(tmp, M1, Zt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] z_t
 #pragma unroll
     for (int j = 0; j < 2; ++j) dk[j] -= tmp[j];
   }
@@ -445,7 +455,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         rd.store(Dt);
         __syncthreads();
       }
-      tile_mma_half<true, false>(dv[v], M1, Dt, kt, ws, hf);  // sum_t W gy[t][s] dout_t
+      tile_mma_half<true, false>(dv[v], M1, Dt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] dout_t
     }
   }
   __syncthreads();

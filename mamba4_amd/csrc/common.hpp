@@ -207,9 +207,10 @@ __device__ __forceinline__ f4 quad_row(const f4 acc[4], int q) {
 // acc[j] is the 16-column block jb = 2 hf + j of tile_mma's result (same
 // operand conventions, same accumulator layout per block).  A QUAD block jb
 // holds columns 4r + jb, so a wave's two blocks are columns 4r + 2hf, +1.
+// Only the first nj blocks (1 or 2, uniform over the wave) are computed.
 template <bool TA, bool TB, bool QUAD>
 __device__ __forceinline__ void mma_block_half(f4 acc[2], const float* A, const float* B, int k0,
-                                               int w, int hf) {
+                                               int w, int hf, int nj) {
   const int l = lane_id(), r = l & 15, kk = k0 + 4 * (l >> 4);
   f4 a;
   if (TA) {
@@ -223,13 +224,13 @@ __device__ __forceinline__ void mma_block_half(f4 acc[2], const float* A, const 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int jb = 2 * hf + j, col = QUAD ? 4 * r + jb : 16 * jb + r;
-      b[j] = *reinterpret_cast<const f4*>(B + col * LDT + kk);
+      if (j < nj) b[j] = *reinterpret_cast<const f4*>(B + col * LDT + kk);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
+        if (j < nj) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -240,23 +241,28 @@ __device__ __forceinline__ void mma_block_half(f4 acc[2], const float* A, const 
         b[1] = v.y;
       } else {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) b[j] = B[(kk + e) * LDT + 16 * (2 * hf + j) + r];
+        for (int j = 0; j < 2; ++j)
+          if (j < nj) b[j] = B[(kk + e) * LDT + 16 * (2 * hf + j) + r];
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j], acc[j], 0, 0, 0);
+        if (j < nj) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j], acc[j], 0, 0, 0);
     }
   }
 }
 
+// acc += the wave's half of A B over contraction terms [k_begin, K) (both
+// multiples of 16), computing its first nj column blocks.  Terms and blocks
+// left out must be known zero in the product (causal masks).
 template <bool TA, bool TB, bool QUAD = !TB>
 __device__ __forceinline__ void tile_mma_half(f4 acc[2], const float* A, const float* B, int K,
-                                              int w, int hf) {
-  if (K == 64) {
+                                              int w, int hf, int k_begin = 0, int nj = 2) {
+  if (nj <= 0) return;
+  if (K == 64 && k_begin == 0) {
 #pragma unroll
-    for (int k0 = 0; k0 < 64; k0 += 16) mma_block_half<TA, TB, QUAD>(acc, A, B, k0, w, hf);
+    for (int k0 = 0; k0 < 64; k0 += 16) mma_block_half<TA, TB, QUAD>(acc, A, B, k0, w, hf, nj);
   } else {
-    for (int k0 = 0; k0 < K; k0 += 16) mma_block_half<TA, TB, QUAD>(acc, A, B, k0, w, hf);
+    for (int k0 = k_begin; k0 < K; k0 += 16) mma_block_half<TA, TB, QUAD>(acc, A, B, k0, w, hf, nj);
   }
 }
 
