@@ -119,6 +119,32 @@ __global__ __launch_bounds__(256) void prologue_forward_kernel(
       floor[i] = floor_min + softplusf(floor_raw[i]);
   const MixRow r = mix_row(B, T, H);
   if (r.th < 0) return;
+  if (D == 64) {
+    // One quad per lane, and every load issued before any arithmetic or
+    // store (the general path below reads each row twice, one at a time).
+    const float* ks = key_source(key, previous, key_shift, r, T, H, D);
+    const int c = 4 * r.l;
+    const f4 kraw = *reinterpret_cast<const f4*>((ks ? ks : query + r.th * D) + c);
+    const f4 qv = *reinterpret_cast<const f4*>(query + r.th * D + c);
+    const f4 kown = *reinterpret_cast<const f4*>(key + r.th * D + c);
+    const float braw = beta_raw[r.th], draw = dt_raw[r.th];
+    const float bb = beta_bias[r.h], db = dt_bias[r.h], al = a_log[r.h];
+    const f4 kv = ks ? kraw : f4{0.f, 0.f, 0.f, 0.f};
+    float sk = 0.f, sq = 0.f;
+    sk += kv[0] * kv[0] + kv[1] * kv[1] + kv[2] * kv[2] + kv[3] * kv[3];
+    sq += qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] + qv[3] * qv[3];
+    const float rk = __builtin_amdgcn_rsqf(row_sum(sk) + 1e-6f);
+    const float rq = __builtin_amdgcn_rsqf(row_sum(sq) + 1e-6f);
+    *reinterpret_cast<f4*>(keys + r.th * D + c) = kv * rk;
+    *reinterpret_cast<f4*>(queries + r.th * D + c) = qv * rq;
+    if (key_shift && shifted && r.t == T - 1)
+      *reinterpret_cast<f4*>(shifted + ((long)r.b * H + r.h) * D + c) = kown;
+    if (r.l == 0) {
+      beta[r.th] = beta_max * sigmoidf(braw + bb);
+      log_decay[r.th] = -expf(al) * softplusf(draw + db);
+    }
+    return;
+  }
   unit_row(key_source(key, previous, key_shift, r, T, H, D), keys + r.th * D, D, r.l);
   unit_row(query + r.th * D, queries + r.th * D, D, r.l);
   if (key_shift && shifted && r.t == T - 1)
@@ -166,7 +192,54 @@ __global__ __launch_bounds__(256) void prologue_backward_kernel(
   const MixRow r = mix_row(B, T, H);
   const int row = threadIdx.x >> 4;
   if (r.l == 0) ths[row] = r.th;
-  if (r.th >= 0) {
+  if (r.th >= 0 && D == 64) {
+    // One quad per lane, every load issued before any arithmetic or store;
+    // the same arithmetic, in the same order, as the general path below.
+    const int c = 4 * r.l;
+    const float* ks = key_source(key, previous, key_shift, r, T, H, D);
+    const float* gs = d_shifted ? d_shifted + ((long)r.b * H + r.h) * D : d_queries + r.th * D;
+    const f4 kraw = *reinterpret_cast<const f4*>((ks ? ks : query + r.th * D) + c);
+    const f4 gk = *reinterpret_cast<const f4*>(d_keys + r.th * D + c);
+    const f4 qv = *reinterpret_cast<const f4*>(query + r.th * D + c);
+    const f4 gq = *reinterpret_cast<const f4*>(d_queries + r.th * D + c);
+    const f4 graw = *reinterpret_cast<const f4*>(gs + c);
+    const float braw = beta_raw[r.th], bb = beta_bias[r.h], dbeta = d_beta[r.th];
+    const float draw = dt_raw[r.th], dtb = dt_bias[r.h], al = a_log[r.h];
+    const float dl = d_log_decay[r.th];
+    const f4 kv = ks ? kraw : f4{0.f, 0.f, 0.f, 0.f};
+    auto vjp = [&](const f4& v, const f4& g) {
+      float sum = 0.f, yd = 0.f;
+      sum += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      const float rn = __builtin_amdgcn_rsqf(row_sum(sum) + 1e-6f);
+      yd += rn * (v[0] * g[0] + v[1] * g[1] + v[2] * g[2] + v[3] * g[3]);
+      yd = row_sum(yd);
+      return rn * (g - (rn * yd) * v);
+    };
+    const f4 dk = vjp(kv, gk), dq = vjp(qv, gq);
+    float* dst = nullptr;
+    if (!key_shift)
+      dst = d_key + r.th * D;
+    else if (r.t > 0)
+      dst = d_key + (r.th - H) * D;
+    else if (d_previous)
+      dst = d_previous + ((long)r.b * H + r.h) * D;
+    if (dst) *reinterpret_cast<f4*>(dst + c) = ks ? dk : f4{0.f, 0.f, 0.f, 0.f};
+    if (key_shift && r.t == T - 1)
+      *reinterpret_cast<f4*>(d_key + r.th * D + c) = d_shifted ? graw : f4{0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<f4*>(d_query + r.th * D + c) = dq;
+    if (r.l == 0) {
+      const float sg = sigmoidf(braw + bb);
+      const float db = dbeta * beta_max * sg * (1.f - sg);
+      const float u = draw + dtb;
+      const float rate = expf(al);
+      const float ddt = -dl * rate * sigmoidf(u);
+      d_beta_raw[r.th] = db;
+      d_dt_raw[r.th] = ddt;
+      vals[row][0] = db;
+      vals[row][1] = ddt;
+      vals[row][2] = -dl * rate * softplusf(u);
+    }
+  } else if (r.th >= 0) {
     // The key row that fed position t's key gets its cotangent: key t - 1
     // (or the cached previous key at t = 0) with the shift, else key t.
     float* dst = nullptr;
