@@ -106,15 +106,24 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
   // columns 12..15 of sequence 0, above the diagonal.  No turn writes that
   // quad; the factorization reads it as scratch and zeroes it.
   lds_int* const turn_count = (lds_int*)(&evidence[slot_quad(0, 3) * 64]);
-  if (wave == 0) {
+  {
+    // Both waves stage the start evidence: wave 0 slots 0..2 (24 quads),
+    // wave 1 slot 3 (16 quads).
     const float* s0 = start_s + ((long)bh * d.NS + ns) * 4096;
+    if (wave == 0) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+      for (int m = 0; m < 3; ++m)
 #pragma unroll
-      for (int q = 0; q < 4 * m + 4; ++q)
-        evidence[slot_quad(m, q) * 64 + lane] =
-            -*reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
-    if (lane == 0) *turn_count = 0;  // after this lane's quad (0, 3): LDS writes stay in order
+        for (int q = 0; q < 4 * m + 4; ++q)
+          evidence[slot_quad(m, q) * 64 + lane] =
+              -*reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
+      if (lane == 0) *turn_count = 0;  // after this lane's quad (0, 3): LDS writes stay in order
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        evidence[slot_quad(3, q) * 64 + lane] =
+            -*reinterpret_cast<const f4*>(s0 + (a + 48) * 64 + 4 * q);
+    }
   }
   float fl[4];
 #pragma unroll
