@@ -26,8 +26,13 @@ config-2 shape: the mixer prologue (key shift, unit q/k, gates, floor) and
 epilogue (confidence gate, D-skip), and the order head's gated scan, each
 forward and backward; every kernel is HBM-bound and reported against 8 TB/s.
 
+With --workload mixer_read a step is the mixer's memory path forward at the
+config-2 shape through the fused entry point (m4mr_mixer_forward: prologue,
+memory read and read gating in one pass over the raw projections); the same
+forward through the three separate entry points is timed beside it.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload config2|config3|config4|mixer]
+                       [--workload config2|config3|config4|mixer|mixer_read]
 """
 
 import argparse
@@ -134,7 +139,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--chunk", type=int, default=64)
     p.add_argument("--workload", default="config2",
-                   choices=["config2", "config3", "config4", "mixer"])
+                   choices=["config2", "config3", "config4", "mixer", "mixer_read"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -517,6 +522,102 @@ def main_mixer(args):
     print(json.dumps(line), flush=True)
 
 
+MIXER_READ_METRIC = ("mixer memory-path forward tokens/sec at B16 L1024 H8 d64 (prologue, "
+                     "memory read and read gating fused)")
+
+
+def main_mixer_read(args):
+    import ctypes
+
+    import torch
+
+    from mamba4_amd import _lib
+
+    lib = _lib.load()
+    check = _lib.check
+    B, T, H, D = 16, 1024, 8, 64
+    gen = torch.Generator(device="cuda:0").manual_seed(0)
+    f32 = dict(dtype=torch.float32, device="cuda:0")
+
+    def rand(*shape):
+        return torch.randn(*shape, generator=gen, **f32)
+
+    key, query, value = rand(B, T, H, D), rand(B, T, H, D), rand(B, T, H, D)
+    beta_raw, dt_raw = rand(B, T, H), rand(B, T, H)
+    beta_bias, dt_bias, a_log = rand(H), rand(H) - 2.0, rand(H).abs()
+    conf, skip, floor_raw = rand(H).abs() * 0.2, rand(H), rand(H, D)
+    count, starts = _lib.start_counts(T, 64)
+    e = torch.empty
+    output, read = e(B, T, H, D, **f32), e(B, T, H, D, **f32)
+    variance, shifted = e(B, T, H, **f32), e(B, H, D, **f32)
+    final_s, final_c = e(B, H, D, D, **f32), e(B, H, D, D, **f32)
+    solved, factors = e(B, T, H, D, **f32), e(B, T, H, _lib.FACTOR_FLOATS, **f32)
+    start_s, start_c = e(B, H, starts, D, D, **f32), e(B, H, count, D, D, **f32)
+    keys, queries, beta, log_decay = e(B, T, H, D, **f32), e(B, T, H, D, **f32), e(B, T, H, **f32), e(B, T, H, **f32)
+    floor = e(H, D, **f32)
+    params = _lib.MixerParams(beta_bias.data_ptr(), dt_bias.data_ptr(), a_log.data_ptr(),
+                              floor_raw.data_ptr(), None, conf.data_ptr(), skip.data_ptr(),
+                              1.0, 0.25, 1)
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+
+    def fused():
+        check(lib.m4mr_mixer_forward(
+            p(key), p(value), p(query), p(beta_raw), p(dt_raw), ctypes.byref(params), None, None,
+            B, T, H, D, 64, p(output), p(read), p(variance), p(beta), p(log_decay), p(floor),
+            p(final_s), p(final_c), p(solved),
+            p(factors), p(start_s), p(start_c), p(shifted), st))
+
+    def separate():
+        check(lib.m4mr_prologue_forward(
+            p(key), p(query), p(beta_raw), p(dt_raw), p(beta_bias), p(dt_bias), p(a_log),
+            p(floor_raw), None, B, T, H, D, 1.0, 0.25, 1, p(keys), p(queries), p(beta),
+            p(log_decay), p(floor), p(shifted), st))
+        check(lib.m4mr_forward(
+            p(keys), p(value), p(queries), p(beta), p(log_decay), p(floor), None, None, B, T, H,
+            D, 64, p(read), p(variance), p(final_s), p(final_c), p(solved), p(factors),
+            p(start_s), p(start_c), st))
+        check(lib.m4mr_epilogue_forward(p(read), p(variance), p(value), p(conf), p(skip), B, T,
+                                        H, D, p(output), st))
+
+    def timed(fn, steps):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    # The separate path's state walk is the fused walk too (the fused entry
+    # point always takes it).  The two are timed in alternation, best of
+    # three each, so that neither gets the colder clocks of the first run.
+    os.environ["M4MR_STATE_WALK"] = "fused"
+    runs = [(timed(fused, args.steps), timed(separate, args.steps)) for _ in range(3)]
+    seconds = min(r[0] for r in runs)
+    separate_seconds = min(r[1] for r in runs)
+    line = {
+        "metric": MIXER_READ_METRIC,
+        "value": B * T / seconds,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": seconds * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "mixer memory path forward, B=16 L=1024 H=8 D=P=64 fp32",
+                   "batch": B, "seq_len": T, "heads": H, "key_dim": D, "value_dim": D},
+        "separate_ms_per_step": separate_seconds * 1e3,
+        "fused_speedup": separate_seconds / seconds,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def copy_bandwidth_gbps():
     """Read+write bandwidth of a 2 GiB device-to-device copy (torch copy_)."""
     import torch
@@ -585,6 +686,8 @@ def main():
         sys.exit(2)
     if args.workload == "config4":
         return main_decode(args)
+    if args.workload == "mixer_read":
+        return main_mixer_read(args)
     if args.workload == "mixer":
         return main_mixer(args)
     data = workload_inputs(args.workload, seed=0, cotangents=True)

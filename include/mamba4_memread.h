@@ -113,6 +113,57 @@ int m4mr_forward_bf16(const uint16_t* keys, const uint16_t* values, const uint16
                       float* start_evidence, float* start_cross,
                       void* stream);
 
+/*
+ * The mixer's per-head parameters and gates for m4mr_mixer_forward
+ * (SelectiveMemoryMixer.__call__, lm/models/mamba4.py:183-237, 266-273).
+ */
+typedef struct {
+  const float* beta_bias;        /* [H] */
+  const float* dt_bias;          /* [H] */
+  const float* a_log;            /* [H] */
+  const float* floor_raw;        /* [H,D] */
+  const float* previous;         /* [B,H,D] cached raw key of position 0, or NULL (zero key) */
+  const float* confidence_scale; /* [H] */
+  const float* skip;             /* [H], the mixer's D */
+  float beta_max;                /* > 0 */
+  float floor_min;               /* > 0 */
+  int key_shift;                 /* nonzero: key t is the raw key of t - 1 */
+} m4mr_mixer_params;
+
+/*
+ * The memory read fused with the mixer's prologue and read gating.  Equal
+ * to m4mr_prologue_forward, then m4mr_forward, then m4mr_epilogue_forward
+ * (to float32 rounding: the row norms are summed in another order), without
+ * their separate passes over keys, queries and values: the memory-read
+ * kernels shift and unit-normalise each raw key and query row as they load
+ * it, a small kernel computes the gates (beta, log_decay [B,T,H] and floor
+ * [H,D], written out with the prologue's arithmetic) from the raw gate
+ * projections alone, and the read kernel writes
+ *   output = read * sigmoid(1 - confidence_scale[h] log1p(variance))
+ *            + skip[h] * value
+ * (lm/models/mamba4.py:266-273) as well as the ungated `read` (the
+ * backward's residual).  Replaces, in the mixer's forward, the prologue at
+ * lm/models/mamba4.py:183-237, the selective_gaussian_memory call at
+ * :239-249 and the gating at :266-273.
+ *
+ * key, query [B,T,H,D] (D = 64) raw projections; value [B,T,H,P];
+ * beta_raw, dt_raw [B,T,H]; outputs as m4mr_forward (output gated), plus
+ * read [B,T,H,P].  With params->key_shift and a non-NULL `shifted`
+ * [B,H,D], the raw key of position T-1 (the next call's `previous`) is
+ * written there.  Always takes the fused state walk.
+ */
+int m4mr_mixer_forward(const float* key, const float* value, const float* query,
+                       const float* beta_raw, const float* dt_raw,
+                       const m4mr_mixer_params* params,
+                       const float* init_evidence, const float* init_cross,
+                       int B, int T, int H, int value_dim, int chunk,
+                       float* output, float* read, float* variance,
+                       float* beta, float* log_decay, float* floor,
+                       float* final_evidence, float* final_cross,
+                       float* solved, float* factors,
+                       float* start_evidence, float* start_cross,
+                       float* shifted, void* stream);
+
 /* Number of chunks NC and of evidence start states NS for T tokens. */
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts);
 

@@ -22,17 +22,25 @@ from mamba4_amd.memory import (  # noqa: F401
     selective_initial_state,
     spd_solve,
 )
-from mamba4_amd.mixer import MemoryInputs, gated_read, memory_inputs  # noqa: F401
+from mamba4_amd.mixer import (  # noqa: F401
+    MemoryInputs,
+    MixerRead,
+    gated_read,
+    memory_inputs,
+    mixer_read,
+)
 from mamba4_amd.order import order_memory, order_memory_chunked  # noqa: F401
 
 __all__ = [
     "MEMORY_SOLVE",
     "MemoryInputs",
+    "MixerRead",
     "SOLVERS",
     "SelectiveResult",
     "SelectiveState",
     "gated_read",
     "memory_inputs",
+    "mixer_read",
     "order_memory",
     "order_memory_chunked",
     "selective_decode",

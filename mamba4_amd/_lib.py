@@ -25,11 +25,32 @@ _I = ctypes.c_int
 _L = ctypes.c_long
 _S = ctypes.c_size_t
 
+class MixerParams(ctypes.Structure):
+    """m4mr_mixer_params (include/mamba4_memread.h)."""
+
+    _fields_ = [
+        ("beta_bias", ctypes.c_void_p),
+        ("dt_bias", ctypes.c_void_p),
+        ("a_log", ctypes.c_void_p),
+        ("floor_raw", ctypes.c_void_p),
+        ("previous", ctypes.c_void_p),
+        ("confidence_scale", ctypes.c_void_p),
+        ("skip", ctypes.c_void_p),
+        ("beta_max", ctypes.c_float),
+        ("floor_min", ctypes.c_float),
+        ("key_shift", ctypes.c_int),
+    ]
+
+
 SIGNATURES = {
     "m4mr_version": (ctypes.c_char_p, []),
     "m4mr_last_error": (ctypes.c_char_p, []),
     "m4mr_forward": (_I, [_P] * 8 + [_I] * 5 + [_P] * 8 + [_P]),
     "m4mr_forward_bf16": (_I, [_P] * 8 + [_I] * 5 + [_P] * 8 + [_P]),
+    "m4mr_mixer_forward": (
+        _I,
+        [_P] * 5 + [ctypes.POINTER(MixerParams)] + [_P] * 2 + [_I] * 5 + [_P] * 13 + [_P],
+    ),
     "m4mr_backward_workspace_bytes": (_S, [_I] * 5),
     "m4mr_start_counts": (_I, [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "m4mr_backward": (

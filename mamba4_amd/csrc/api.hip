@@ -25,18 +25,19 @@ __global__ void bwd_local_kernel(Dims, const float*, const float*, const float*,
                                  const float*, float*, float*);
 __global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
                                 float*, float*);
-template <bool BWD, typename In>
+template <bool BWD, typename In, bool MIX>
 __global__ void states_kernel(Dims, StateArgs);
-template <typename In>
+template <typename In, bool MIX>
 __global__ void fwd_factor_kernel(Dims, const In*, const In*, const float*, const float*,
-                                  const float*, const float*, float*, float*);
+                                  const float*, const float*, float*, float*, MixerIn);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
 __global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
                                    const float*, const float*, const float*, long, int, int, float*,
                                    float*);
-template <typename In>
+template <typename In, bool MIX>
 __global__ void fwd_read_kernel(Dims, const In*, const In*, const In*, const float*,
-                                const float*, const float*, const float*, float*, float*);
+                                const float*, const float*, const float*, float*, float*, MixerIn,
+                                ReadGate);
 template <typename In>
 __global__ void bwd_dy_kernel(Dims, const In*, const In*, const In*, const float*,
                               const float*, const float*, const float*, const float*, float*);
@@ -62,6 +63,9 @@ __global__ void epilogue_backward_kernel(const float*, const float*, const float
                                          const float*, int, int, int, int, const float*, float*,
                                          float*, float*, float*);
 __global__ void head_sums_kernel(const float*, long, int, int, float*, float*, float*);
+__global__ void mixer_gates_kernel(const float*, const float*, const float*, const float*,
+                                   const float*, const float*, const float*, int, int, int, int,
+                                   float, float, float*, float*, float*, float*);
 __global__ void zero_kernel(float*, long);
 __global__ void order_local_kernel(OrderDims, const float*, const float*, float*, float*);
 __global__ void order_carry_kernel(OrderDims, const float*, float*, const float*);
@@ -89,7 +93,7 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "prologue_backward", "epilogue_forward",
                                     "epilogue_backward", "head_sums", "order_local",
                                     "order_carry",    "order_apply", "order_bwd_local",
-                                    "order_bwd_carry", "order_bwd_apply"};
+                                    "order_bwd_carry", "order_bwd_apply", "mixer_gates"};
 
 struct ProfRecord {
   const char* name;
@@ -141,15 +145,17 @@ int configure() {
   } big[] = {{(const void*)m4::fwd_stats_kernel<float>, kStatsLdsBytes},
              {(const void*)m4::fwd_stats_kernel<m4::bf16_t>, kStatsLdsBytes},
              {(const void*)m4::bwd_local_kernel, kChunkLdsBytes},
-             {(const void*)m4::fwd_read_kernel<float>, kChunkLdsBytes},
-             {(const void*)m4::fwd_read_kernel<m4::bf16_t>, kChunkLdsBytes},
+             {(const void*)m4::fwd_read_kernel<float, false>, kChunkLdsBytes},
+             {(const void*)m4::fwd_read_kernel<m4::bf16_t, false>, kChunkLdsBytes},
+             {(const void*)m4::fwd_read_kernel<float, true>, kChunkLdsBytes},
              {(const void*)m4::bwd_dy_kernel<float>, kChunkLdsBytes},
              {(const void*)m4::bwd_dy_kernel<m4::bf16_t>, kChunkLdsBytes},
              {(const void*)m4::bwd_grads_kernel<float>, kGradsLdsBytes},
              {(const void*)m4::bwd_grads_kernel<m4::bf16_t>, kGradsLdsBytes},
-             {(const void*)m4::states_kernel<false, float>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<false, m4::bf16_t>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<true, float>, kStatesLdsBytes}};
+             {(const void*)m4::states_kernel<false, float, false>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<false, m4::bf16_t, false>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<true, float, false>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<false, float, true>, kStatesLdsBytes}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)k.bytes);
@@ -275,25 +281,37 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) !=
 
 // The memory read forward and backward for float32 or bfloat16 keys,
 // values and queries (the C entry points below).
-template <typename In>
+// The forward launch sequence.  MIX: keys and queries come from the mixer's
+// raw projections (`mix`; the plain key and query pointers are unused), the
+// state walk is always the fused one, and the output is gated (`gate`).
+template <typename In, bool MIX>
 int forward_impl(const char* entry, const In* keys, const In* values, const In* queries,
                  const float* beta, const float* log_decay, const float* floor,
                  const float* init_evidence, const float* init_cross, int B, int T, int H,
                  int value_dim, int chunk, float* output, float* variance, float* final_evidence,
                  float* final_cross, float* solved, float* factors, float* start_evidence,
-                 float* start_cross, void* stream) {
+                 float* start_cross, void* stream, const m4::MixerIn& mix = {},
+                 const m4::ReadGate& gate = {}) {
   g_error.clear();
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
-  const void* need[] = {keys,     values,        queries,     beta,   log_decay,
-                        floor,    output,        variance,    final_evidence,
+  const void* need[] = {MIX ? (const void*)mix.key : keys,
+                        values,
+                        MIX ? (const void*)mix.query : queries,
+                        beta,          log_decay,   floor,
+                        output,        variance,    final_evidence,
                         final_cross, solved,     factors,     start_evidence, start_cross};
   for (const void* p : need)
     if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
+  if (MIX && (!gate.confidence_scale || !gate.skip || !gate.read))
+    return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
   if ((init_evidence == nullptr) != (init_cross == nullptr))
     return fail(M4MR_EINVAL, std::string(entry) + ": init_evidence and init_cross must both be set or both NULL");
-  const void* vec[] = {keys, values, queries, solved, factors, output, start_evidence,
-                       start_cross, final_evidence, final_cross, init_evidence, init_cross};
+  const void* vec[] = {MIX ? (const void*)mix.key : keys, values,
+                       MIX ? (const void*)mix.query : queries, solved, factors, output,
+                       start_evidence, start_cross, final_evidence, final_cross, init_evidence,
+                       init_cross, MIX ? (const void*)mix.previous : nullptr,
+                       MIX ? (const void*)gate.read : nullptr};
   for (const void* p : vec)
     if (p && misaligned(p)) return fail(M4MR_EINVAL, std::string(entry) + ": arrays must be 16-byte aligned");
   if (int rc = configure()) return rc;
@@ -302,12 +320,12 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   const unsigned seqs = (unsigned)B * H * d.NC;
   const unsigned subseqs = (unsigned)B * H * d.NS;
   int rc;
-  if (fused_states(B, H, d)) {
-    const m4::StateArgs args{keys,            values,      keys,           beta,   log_decay,
-                             init_evidence,   init_cross,  start_evidence, start_cross,
-                             final_evidence,  final_cross};
+  if (MIX || fused_states(B, H, d)) {
+    m4::StateArgs args{keys,            values,      keys,           beta,   log_decay,
+                       init_evidence,   init_cross,  start_evidence, start_cross,
+                       final_evidence,  final_cross, mix};
     rc = launch("fwd_states", st, [&] {
-      hipLaunchKernelGGL((m4::states_kernel<false, In>), dim3(B * H, 1 + d.NV), dim3(512),
+      hipLaunchKernelGGL((m4::states_kernel<false, In, MIX>), dim3(B * H, 1 + d.NV), dim3(512),
                          kStatesLdsBytes, st, d, args);
     });
   } else {
@@ -324,14 +342,15 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   }
   if (rc) return rc;
   rc = launch("fwd_factor", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_factor_kernel<In>, dim3((subseqs + 3) / 4), dim3(128), 0, st, d, keys,
-                       queries, beta, log_decay, floor, start_evidence, solved, factors);
+    hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX>), dim3((subseqs + 3) / 4), dim3(128), 0,
+                       st, d, keys, queries, beta, log_decay, floor, start_evidence, solved,
+                       factors, mix);
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {
-    hipLaunchKernelGGL(m4::fwd_read_kernel<In>, dim3(persistent_grid(seqs, 2)), dim3(256),
-                       kChunkLdsBytes, st, d, keys,
-                       values, queries, beta, log_decay, solved, start_cross, output, variance);
+    hipLaunchKernelGGL((m4::fwd_read_kernel<In, MIX>), dim3(persistent_grid(seqs, 2)), dim3(256),
+                       kChunkLdsBytes, st, d, keys, values, queries, beta, log_decay, solved,
+                       start_cross, output, variance, mix, gate);
   });
 }
 
@@ -385,7 +404,7 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                              d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
                              d_init_evidence,  d_init_cross};
     rc = launch("bwd_states", st, [&] {
-      hipLaunchKernelGGL((m4::states_kernel<true, float>), dim3(B * H, 1 + d.NV), dim3(512),
+      hipLaunchKernelGGL((m4::states_kernel<true, float, false>), dim3(B * H, 1 + d.NV), dim3(512),
                          kStatesLdsBytes, st, d, args);
     });
   } else {
@@ -428,7 +447,7 @@ int m4mr_forward(const float* keys, const float* values, const float* queries,
                  int value_dim, int chunk, float* output, float* variance, float* final_evidence,
                  float* final_cross, float* solved, float* factors, float* start_evidence,
                  float* start_cross, void* stream) {
-  return forward_impl("m4mr_forward", keys, values, queries, beta, log_decay, floor,
+  return forward_impl<float, false>("m4mr_forward", keys, values, queries, beta, log_decay, floor,
                       init_evidence, init_cross, B, T, H, value_dim, chunk, output, variance,
                       final_evidence, final_cross, solved, factors, start_evidence, start_cross,
                       stream);
@@ -440,12 +459,56 @@ int m4mr_forward_bf16(const uint16_t* keys, const uint16_t* values, const uint16
                       int value_dim, int chunk, float* output, float* variance,
                       float* final_evidence, float* final_cross, float* solved, float* factors,
                       float* start_evidence, float* start_cross, void* stream) {
-  return forward_impl("m4mr_forward_bf16", reinterpret_cast<const m4::bf16_t*>(keys),
+  return forward_impl<m4::bf16_t, false>("m4mr_forward_bf16", reinterpret_cast<const m4::bf16_t*>(keys),
                       reinterpret_cast<const m4::bf16_t*>(values),
                       reinterpret_cast<const m4::bf16_t*>(queries), beta, log_decay, floor,
                       init_evidence, init_cross, B, T, H, value_dim, chunk, output, variance,
                       final_evidence, final_cross, solved, factors, start_evidence, start_cross,
                       stream);
+}
+
+int m4mr_mixer_forward(const float* key, const float* value, const float* query,
+                       const float* beta_raw, const float* dt_raw,
+                       const m4mr_mixer_params* params, const float* init_evidence,
+                       const float* init_cross, int B, int T, int H, int value_dim, int chunk,
+                       float* output, float* read, float* variance, float* beta,
+                       float* log_decay, float* floor, float* final_evidence,
+                       float* final_cross, float* solved, float* factors,
+                       float* start_evidence, float* start_cross, float* shifted, void* stream) {
+  g_error.clear();
+  if (!params) return fail(M4MR_EINVAL, "m4mr_mixer_forward: params is NULL");
+  if (!(params->beta_max > 0.f))
+    return fail(M4MR_EINVAL, "m4mr_mixer_forward: beta_max must be positive");
+  if (!(params->floor_min > 0.f))
+    return fail(M4MR_EINVAL, "m4mr_mixer_forward: floor_min must be positive");
+  const void* need[] = {key,           query,          value,         beta_raw,
+                        dt_raw,        params->beta_bias, params->dt_bias, params->a_log,
+                        params->floor_raw, beta,        log_decay,     floor};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, "m4mr_mixer_forward: a required pointer is NULL");
+  std::string why;
+  if (bad_dims(B, T, H, value_dim, chunk, &why))
+    return fail(M4MR_EINVAL, "m4mr_mixer_forward: " + why);
+  if (int rc = configure()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const long tokens = (long)B * T * H;
+  if (key && misaligned(key)) return fail(M4MR_EINVAL, "m4mr_mixer_forward: arrays must be 16-byte aligned");
+  if (shifted && misaligned(shifted))
+    return fail(M4MR_EINVAL, "m4mr_mixer_forward: arrays must be 16-byte aligned");
+  int rc = launch("mixer_gates", st, [&] {
+    hipLaunchKernelGGL(m4::mixer_gates_kernel, dim3((unsigned)((tokens + 255) / 256)), dim3(256),
+                       0, st, beta_raw, dt_raw, params->beta_bias, params->dt_bias,
+                       params->a_log, params->floor_raw, key, B, T, H, 64, params->beta_max,
+                       params->floor_min, beta, log_decay, floor,
+                       params->key_shift ? shifted : nullptr);
+  });
+  if (rc) return rc;
+  const m4::MixerIn mix{key, query, params->previous, params->key_shift ? 1 : 0};
+  const m4::ReadGate gate{params->confidence_scale, params->skip, read};
+  return forward_impl<float, true>("m4mr_mixer_forward", nullptr, value, nullptr, beta, log_decay,
+                                   floor, init_evidence, init_cross, B, T, H, value_dim, chunk,
+                                   output, variance, final_evidence, final_cross, solved, factors,
+                                   start_evidence, start_cross, stream, mix, gate);
 }
 
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {

@@ -72,34 +72,62 @@ __device__ __forceinline__ const float* cross_tile(const float* base, const Dims
 // after this chunk's are in LDS, its queries once this chunk's variance is
 // done, its values once this chunk's values are in LDS (at most five tiles
 // in flight per thread, keeping two blocks per CU).
-template <typename In>
+//
+// MIX: keys and queries come from the mixer's raw projections (`mix`,
+// transformed on load: the key rows shifted and normalised at staging, the
+// queries normalised where used), and the output is gated (`gate`), the
+// ungated read kept in gate.read.
+template <typename In, bool MIX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_read_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const In* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ solved,
     const float* __restrict__ start_c, float* __restrict__ output,
-    float* __restrict__ variance) {
+    float* __restrict__ variance, MixerIn mix, ReadGate gate) {
   extern __shared__ float smem[];
   float* Y = smem;
   float* K = Y + TILE;  // keys, then values
   float* G = K + TILE;
   float* C0 = G + TILE;  // C0 transposed: C0[e][p]
   __shared__ ChunkScalars cs;
+  __shared__ float var_s[MIX ? MAXC : 1];  // MIX: the chunk's variances, for the gate
   const long nseq = (long)d.B * d.H * d.NC;
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
   TileRegs ry, rk, rv, rq;
   TileRegsT rc;
+  // MIX key rows: the raw source row of each position (the zero row of
+  // position 0 reads its query row and is zeroed at staging).
+  auto fetch_keys = [&](const SeqIndex& s) {
+    if constexpr (MIX) {
+      rk.fetch_rows(s.len, [&](int r) -> const float* {
+        const int t = s.n * d.chunk + r;
+        const float* p = mix_key_row(mix, d, s.b, t, s.h);
+        return p ? p : mix.query + token_head(d, s.b, t, s.h) * 64;
+      });
+    } else {
+      rk.fetch_rows(s.len, rows_of(keys, d, s));
+    }
+  };
+  auto fetch_queries = [&](const SeqIndex& s) {
+    if constexpr (MIX)
+      rq.fetch_rows(s.len, rows_of(mix.query, d, s));
+    else
+      rq.fetch_rows(s.len, rows_of(queries, d, s));
+  };
   ry.fetch_rows(si.len, rows_of(solved, d, si));
-  rk.fetch_rows(si.len, rows_of(keys, d, si));
+  fetch_keys(si);
   rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
-  rq.fetch_rows(si.len, rows_of(queries, d, si));
+  fetch_queries(si);
   rv.fetch_rows(si.len, value_rows(values, d, si, 0));
 
   for (;;) {
     ry.store(Y);
-    rk.store(K);
+    if constexpr (MIX)
+      rk.store_unit(K, mix.key_shift && !mix.previous && si.n == 0);
+    else
+      rk.store(K);
     rc.store(C0);
     load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
     __syncthreads();
@@ -108,7 +136,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const SeqIndex sn = seq_at(d, more ? next : seq);
     if (more) {
       ry.fetch_rows(sn.len, rows_of(solved, d, sn));
-      rk.fetch_rows(sn.len, rows_of(keys, d, sn));
+      fetch_keys(sn);
       // With more than one value tile, rc carries this chunk's later tiles
       // and prefetches after the last of them.
       if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
@@ -119,12 +147,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = (threadIdx.x >> 4) + 16 * j;
-      const f4 prod = rq.v[j] * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
+      const f4 qt = MIX ? mix_unit(rq.v[j]) : rq.v[j];
+      const f4 prod = qt * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
       const float v = row16_sum(prod[0] + prod[1] + prod[2] + prod[3]);
       if ((threadIdx.x & 15) == 0 && t < si.len)
         variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] = v;
+      if constexpr (MIX)
+        if ((threadIdx.x & 15) == 0) var_s[t] = v;
     }
-    if (more) rq.fetch_rows(sn.len, rows_of(queries, d, sn));
+    if (more) fetch_queries(sn);
 
     f4 acc[4];
     zero4(acc);
@@ -167,8 +198,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int t = acc_row(w, q);
         if (t < si.len) {
           const float carried = expf(cs.prefix[t]);
-          float* dst = output + token_head(d, si.b, si.n * d.chunk + t, si.h) * d.P + 64 * v;
-          *reinterpret_cast<f4*>(dst + c4) = quad_row(out, q) + carried * quad_row(inh, q);
+          const long row = token_head(d, si.b, si.n * d.chunk + t, si.h) * d.P + 64 * v;
+          const f4 x = quad_row(out, q) + carried * quad_row(inh, q);
+          if constexpr (MIX) {
+            // The epilogue's arithmetic: g x + D value (value tile v is in K).
+            const float g = mix_sigmoid(1.f - gate.confidence_scale[si.h] * log1pf(var_s[t]));
+            const float dv = gate.skip[si.h];
+            const f4 val = *reinterpret_cast<const f4*>(K + t * LDT + c4);
+            *reinterpret_cast<f4*>(gate.read + row + c4) = x;
+            *reinterpret_cast<f4*>(output + row + c4) = g * x + dv * val;
+          } else {
+            *reinterpret_cast<f4*>(output + row + c4) = x;
+          }
         }
       }
     }
@@ -659,9 +700,9 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
 }
 
 #define M4_CHUNK_KERNELS(In)                                                                  \
-  template __global__ void fwd_read_kernel<In>(Dims, const In*, const In*, const In*,          \
-                                               const float*, const float*, const float*,       \
-                                               const float*, float*, float*);                  \
+  template __global__ void fwd_read_kernel<In, false>(                                         \
+      Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
+      const float*, float*, float*, MixerIn, ReadGate);                                        \
   template __global__ void bwd_dy_kernel<In>(Dims, const In*, const In*, const In*,            \
                                              const float*, const float*, const float*,         \
                                              const float*, const float*, float*);              \
@@ -672,6 +713,10 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
 M4_CHUNK_KERNELS(float)
 M4_CHUNK_KERNELS(bf16_t)
 #undef M4_CHUNK_KERNELS
+template __global__ void fwd_read_kernel<float, true>(Dims, const float*, const float*,
+                                                      const float*, const float*, const float*,
+                                                      const float*, const float*, float*, float*,
+                                                      MixerIn, ReadGate);
 
 // d floor[h][4c4 .. 4c4+3] = sum over (b, n) of floor_part[(b*H + h)*NC + n]
 // in a fixed order: block (h, c4) of 256 threads, thread i sums entries

@@ -88,6 +88,57 @@ __device__ __forceinline__ float group4_sum(float x) {
   return x;
 }
 
+// The mixer's raw keys and queries as the memory read's inputs, transformed
+// on load (SelectiveMemoryMixer.__call__, lm/models/mamba4.py:183-195,
+// 37-39): key t is the unit-normalised raw key t - 1 with the shift
+// (position 0: the cached `previous` key, or a zero row), queries are
+// unit-normalised, x rsqrt(sum x^2 + 1e-6).  (beta, the log decay and the
+// floor, one value per token-head or per head, come precomputed.)
+struct MixerIn {
+  const float* key;       // raw keys [B,T,H,64]
+  const float* query;     // raw queries [B,T,H,64]
+  const float* previous;  // [B,H,64], or null: a zero key at position 0
+  int key_shift;
+};
+
+__device__ __forceinline__ float mix_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Raw source row of position t's key (null: the zero row).
+__device__ __forceinline__ const float* mix_key_row(const MixerIn& m, const Dims& d, int b, int t,
+                                                    int h) {
+  if (!m.key_shift) return m.key + token_head(d, b, t, h) * 64;
+  if (t > 0) return m.key + token_head(d, b, t - 1, h) * 64;
+  return m.previous ? m.previous + ((long)b * d.H + h) * 64 : nullptr;
+}
+
+// Sum over the 16 lanes of a DPP row by row-local swizzles (every lane
+// receives the total; no LDS round trip).
+__device__ __forceinline__ float row16_sum_dpp(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, true));
+  return x;
+}
+
+// Unit normalisation of a row held as one 4-float quad per lane of a
+// 16-lane DPP row.
+__device__ __forceinline__ f4 mix_unit(const f4& v) {
+  float s = 0.f;
+  s += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  return v * __builtin_amdgcn_rsqf(row16_sum_dpp(s) + 1e-6f);
+}
+
+// The mixer's read gating fused into the read (lm/models/mamba4.py:266-273):
+// out = read sigmoid(1 - confidence_scale log1p(variance)) + skip value,
+// per head; the ungated read is written to `read` as well (the backward's
+// residual).
+struct ReadGate {
+  const float* confidence_scale;  // [H]
+  const float* skip;              // [H] (the mixer's D)
+  float* read;                    // [B,T,H,P]
+};
+
 // Per-chunk log-decay prefix, tail weights and chunk length, staged in LDS
 // by wave 0: prefix[s] = sum_{r<=s} g_r, tail[s] = beta_s exp(P_last - P_s),
 // beta[s]; entries past the chunk's tokens are beta = 0, g = 0 padding.
@@ -305,6 +356,17 @@ struct TileRegs {
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(tile + (r0 + 16 * j) * LDT + q) = v[j];
   }
+
+  // The rows unit-normalised (mix_unit), row 0 as a zero row if zero_row0.
+  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + 16 * j;
+      const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : v[j];
+      *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
+    }
+  }
 };
 
 // TileRegs for a 512-thread block: thread i holds column quad i%16 of rows
@@ -332,6 +394,17 @@ struct TileRegs2 {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int j = 0; j < 2; ++j) *reinterpret_cast<f4*>(tile + (r0 + 32 * j) * LDT + q) = v[j];
+  }
+
+  // As TileRegs::store_unit.
+  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = r0 + 32 * j;
+      const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : v[j];
+      *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
+    }
   }
 };
 
@@ -370,6 +443,7 @@ struct StateArgs {
   float* steps_c;
   float* last_s;         // the state after the last step
   float* last_c;
+  MixerIn mix;           // forward with the mixer's projections (MIX): keys and gates
 };
 
 // Shape of the order head's scan: values [B,T,H,W] in chunks of `chunk`

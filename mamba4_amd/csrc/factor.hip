@@ -56,6 +56,46 @@ __device__ __forceinline__ void load_token(TokenInputs& in, const Dims& d, const
   in.log_lam = log_decay[in.th];
 }
 
+// MIX: the token's raw key and query (the shifted raw key row, whose zero
+// row at position 0 reads the query row and is zeroed by mix_token).
+__device__ __forceinline__ void load_token_mix(TokenInputs& in, bool& kzero, const Dims& d,
+                                               const MixerIn& mix, const float* beta,
+                                               const float* log_decay, int b, int h, int t,
+                                               int a) {
+  in.th = token_head(d, b, t, h);
+  const float* kp = mix_key_row(mix, d, b, t, h);
+  kzero = kp == nullptr;
+  if (kzero) kp = mix.query + in.th * 64;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    in.k[m] = kp[a + 16 * m];
+    in.q[m] = mix.query[in.th * 64 + a + 16 * m];
+  }
+  in.beta = beta[in.th];
+  in.log_lam = log_decay[in.th];
+}
+
+// MIX: unit-normalise the key and query rows (the 16 lanes of the row hold
+// its 64 elements, 4 each).
+__device__ __forceinline__ void mix_token(TokenInputs& in, bool kzero) {
+  float sk = 0.f, sq = 0.f;
+  sk += in.k[0] * in.k[0] + in.k[1] * in.k[1] + in.k[2] * in.k[2] + in.k[3] * in.k[3];
+  sq += in.q[0] * in.q[0] + in.q[1] * in.q[1] + in.q[2] * in.q[2] + in.q[3] * in.q[3];
+  const float rk = kzero ? 0.f : __builtin_amdgcn_rsqf(sum16(sk) + 1e-6f);
+  const float rq = __builtin_amdgcn_rsqf(sum16(sq) + 1e-6f);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    in.k[m] *= rk;
+    in.q[m] *= rq;
+  }
+}
+
+// Where rows past their sequence send their factor and solution: the
+// stores stay unconditional, so the wait for the next token's loads can
+// count them (a store skipped on some path would make the compiler wait for
+// every outstanding store).  Written concurrently with garbage; never read.
+__device__ __align__(256) float g_discard[ROWS_FACTOR + 64];
+
 // Wait until the evidence buffer holds the updates of tokens 0..tt-1.  The
 // other wave of the block publishes each of its turns by writing the count;
 // a wait lasts at most one factorization of that wave plus its turn.  Bounded
@@ -78,12 +118,15 @@ __device__ __forceinline__ void wait_turn(lds_int* count, int tt) {
 // count in LDS, no block barrier), so each wave runs turn, factorization,
 // turn, ... without waiting out the other wave's turn, the two waves offset
 // by one turn.  A block holds one 40 KB evidence buffer for two waves.
-template <typename In>
+//
+// MIX: keys and queries come from the mixer's raw projections (`mix`),
+// shifted and normalised as each token is loaded.
+template <typename In, bool MIX>
 __global__ __launch_bounds__(128) void fwd_factor_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ queries,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ floor, const float* __restrict__ start_s,
-    float* __restrict__ solved, float* __restrict__ factors) {
+    float* __restrict__ solved, float* __restrict__ factors, MixerIn mix) {
   const int lane = threadIdx.x & 63, a = lane & 15, mu = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int BH = d.B * d.H;
@@ -131,7 +174,20 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
   // Rows past their sequence read token 0 (in bounds; never stored).
   auto token = [&](int tt) { return tt < len ? t0 + tt : 0; };
   TokenInputs cur;
-  load_token(cur, d, keys, queries, beta, log_decay, b, h, token(wave), a);
+  bool kzero = false;
+  if constexpr (MIX) {
+    load_token_mix(cur, kzero, d, mix, beta, log_decay, b, h, token(wave), a);
+    mix_token(cur, kzero);
+  } else {
+    load_token(cur, d, keys, queries, beta, log_decay, b, h, token(wave), a);
+    // As at the end of each pass below: no load of `cur` is left pending at
+    // the loop's head.
+    asm volatile("" ::"v"(cur.k[0]), "v"(cur.k[1]), "v"(cur.k[2]), "v"(cur.k[3]), "v"(cur.q[0]),
+                 "v"(cur.q[1]), "v"(cur.q[2]), "v"(cur.q[3]), "v"(cur.beta), "v"(cur.log_lam));
+  }
+  // Nor of the floor (its loads would otherwise sink into the loop's
+  // preheader and every pass would wait for them behind the last stores).
+  asm volatile("" ::"v"(fl[0]), "v"(fl[1]), "v"(fl[2]), "v"(fl[3]));
   __syncthreads();
 
   for (int base = 0; base < steps; base += 2) {
@@ -182,25 +238,41 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
 
     // Prefetch this wave's next token; the factorization covers the latency.
     TokenInputs next;
-    load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
+    if constexpr (MIX)
+      load_token_mix(next, kzero, d, mix, beta, log_decay, b, h, token(tt + 2), a);
+    else
+      load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
     float nw[4], y[4];
     factor_exchanged(A, fl, cur.q, nw);
     backward_rows16(A, nw, y);
-    if (valid) {
+    float* const sol = valid ? solved + cur.th * 64 : g_discard + ROWS_FACTOR;
+    float* const fac = valid ? factors + cur.th * ROWS_FACTOR : g_discard;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) solved[cur.th * 64 + a + 16 * m] = y[m];
-      store_rows16(A, factors + cur.th * ROWS_FACTOR);
-    }
+    for (int m = 0; m < 4; ++m) sol[a + 16 * m] = y[m];
+    store_rows16(A, fac);
+    // Wait for the next token's loads here, where the wait can count the
+    // stores just issued (vmcnt retires in order; the loads came first): the
+    // polling loop in front of the next turn makes the compiler wait for
+    // every outstanding store instead.
+    if constexpr (MIX)
+      mix_token(next, kzero);
+    else
+      asm volatile("" ::"v"(next.k[0]), "v"(next.k[1]), "v"(next.k[2]), "v"(next.k[3]),
+                   "v"(next.q[0]), "v"(next.q[1]), "v"(next.q[2]), "v"(next.q[3]),
+                   "v"(next.beta), "v"(next.log_lam));
     cur = next;
   }
 }
 
-template __global__ void fwd_factor_kernel<float>(Dims, const float*, const float*, const float*,
-                                                  const float*, const float*, const float*,
-                                                  float*, float*);
-template __global__ void fwd_factor_kernel<bf16_t>(Dims, const bf16_t*, const bf16_t*,
-                                                   const float*, const float*, const float*,
-                                                   const float*, float*, float*);
+template __global__ void fwd_factor_kernel<float, false>(Dims, const float*, const float*,
+                                                         const float*, const float*, const float*,
+                                                         const float*, float*, float*, MixerIn);
+template __global__ void fwd_factor_kernel<bf16_t, false>(Dims, const bf16_t*, const bf16_t*,
+                                                          const float*, const float*, const float*,
+                                                          const float*, float*, float*, MixerIn);
+template __global__ void fwd_factor_kernel<float, true>(Dims, const float*, const float*,
+                                                        const float*, const float*, const float*,
+                                                        const float*, float*, float*, MixerIn);
 
 // z = A^-1 rhs from stored factors; four token-heads per wave.
 __global__ __launch_bounds__(64) void factored_solve_kernel(const float* __restrict__ factors,

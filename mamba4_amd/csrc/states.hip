@@ -312,7 +312,7 @@ __device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const 
 
 // In: element type of the forward's key and value rows (the backward's rows
 // are float32).
-template <bool BWD, typename In>
+template <bool BWD, typename In, bool MIX>
 __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArgs g) {
   const In* rows_a = static_cast<const In*>(g.rows_a);
   const In* rows_ac = static_cast<const In*>(g.rows_ac);
@@ -355,9 +355,20 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     TileRegs2 ra, rb;
     float pg, pb;
   };
+  // MIX (forward): the b rows are the keys from the mixer's raw projections
+  // (shifted; position 0's zero row reads its query row and is zeroed at
+  // staging), normalised at staging.
+  const MixerIn& mix = g.mix;
   auto fetch = [&](StepRegs& R, int i) {
     const int first = i * d.chunk, cnt = chunk_len(d, i);
-    R.rb.fetch_rows(cnt, [&](int r) { return rows_b + token_head(d, b, first + r, h) * 64; });
+    if constexpr (MIX) {
+      R.rb.fetch_rows(cnt, [&](int r) -> const float* {
+        const float* p = mix_key_row(mix, d, b, first + r, h);
+        return p ? p : mix.query + token_head(d, b, first + r, h) * 64;
+      });
+    } else {
+      R.rb.fetch_rows(cnt, [&](int r) { return rows_b + token_head(d, b, first + r, h) * 64; });
+    }
     if (own_a) {
       const int width = cross ? d.P : 64, offset = cross ? 64 * v : 0;
       R.ra.fetch_rows(cnt, [&](int r) {
@@ -373,7 +384,10 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     }
   };
   auto stage = [&](const StepRegs& R, int u, int i) {
-    R.rb.store(smem + 2 * u * TILE);
+    if constexpr (MIX)
+      R.rb.store_unit(smem + 2 * u * TILE, mix.key_shift && !mix.previous && i == 0);
+    else
+      R.rb.store(smem + 2 * u * TILE);
     if (own_a) R.ra.store(smem + (2 * u + 1) * TILE);
     if (w == 0) {
       // Inclusive log-decay prefix over the chunk; part 0 ends at token
@@ -441,9 +455,10 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
 }
 
-template __global__ void states_kernel<false, float>(Dims, StateArgs);
-template __global__ void states_kernel<false, bf16_t>(Dims, StateArgs);
-template __global__ void states_kernel<true, float>(Dims, StateArgs);
+template __global__ void states_kernel<false, float, false>(Dims, StateArgs);
+template __global__ void states_kernel<false, bf16_t, false>(Dims, StateArgs);
+template __global__ void states_kernel<true, float, false>(Dims, StateArgs);
+template __global__ void states_kernel<false, float, true>(Dims, StateArgs);
 template __global__ void fwd_stats_kernel<float>(Dims, const float*, const float*, const float*,
                                                  const float*, float*, float*);
 template __global__ void fwd_stats_kernel<bf16_t>(Dims, const bf16_t*, const bf16_t*,

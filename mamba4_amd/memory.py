@@ -125,41 +125,48 @@ class _MemoryRead(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_output, d_variance, d_final_s, d_final_c):
-        lib = _lib.load()
-        (keys, values, queries, beta, log_decay, floor, solved, factors, start_s,
-         start_c) = ctx.saved_tensors
-        batch, time, heads, _ = keys.shape
-        width = values.shape[-1]
-        chunk = ctx.chunk
+        grads = memread_backward(*ctx.saved_tensors, ctx.chunk, d_output, d_variance,
+                                 d_final_s, d_final_c)
+        d_init = grads[6:] if ctx.has_initial else (None, None)
+        return (*grads[:6], *d_init, None)
 
-        def dense(g, like):
-            if g is None:
-                return torch.zeros(like.shape, dtype=torch.float32, device=like.device)
-            return g.to(torch.float32).contiguous()
 
-        d_output = dense(d_output, values)
-        d_variance = dense(d_variance, beta)
-        d_final_s = None if d_final_s is None else d_final_s.to(torch.float32).contiguous()
-        d_final_c = None if d_final_c is None else d_final_c.to(torch.float32).contiguous()
-        f32 = dict(dtype=torch.float32, device=keys.device)
-        grads = [torch.empty(t.shape, **f32) for t in (keys, values, queries, beta, log_decay,
-                                                        floor)]
-        d_init_s = torch.empty((batch, heads, _lib.KEY_DIM, _lib.KEY_DIM), **f32)
-        d_init_c = torch.empty((batch, heads, width, _lib.KEY_DIM), **f32)
-        nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, width, chunk)
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
-        entry = lib.m4mr_backward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_backward
-        _lib.check(
-            entry(
-                _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
-                _ptr(floor), batch, time, heads, width, chunk, _ptr(solved), _ptr(factors),
-                _ptr(start_s), _ptr(start_c), _ptr(d_output), _ptr(d_variance),
-                _ptr(d_final_s), _ptr(d_final_c), *(_ptr(g) for g in grads),
-                _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace), nbytes, _stream(),
-            )
+def memread_backward(keys, values, queries, beta, log_decay, floor, solved, factors, start_s,
+                     start_c, chunk, d_output, d_variance, d_final_s, d_final_c):
+    """m4mr_backward on the forward's inputs and residual set: returns
+    (d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_evidence,
+    d_init_cross), all float32.  None cotangents are zero."""
+    lib = _lib.load()
+    batch, time, heads, _ = keys.shape
+    width = values.shape[-1]
+
+    def dense(g, like):
+        if g is None:
+            return torch.zeros(like.shape, dtype=torch.float32, device=like.device)
+        return g.to(torch.float32).contiguous()
+
+    d_output = dense(d_output, values)
+    d_variance = dense(d_variance, beta)
+    d_final_s = None if d_final_s is None else d_final_s.to(torch.float32).contiguous()
+    d_final_c = None if d_final_c is None else d_final_c.to(torch.float32).contiguous()
+    f32 = dict(dtype=torch.float32, device=keys.device)
+    grads = [torch.empty(t.shape, **f32) for t in (keys, values, queries, beta, log_decay,
+                                                    floor)]
+    d_init_s = torch.empty((batch, heads, _lib.KEY_DIM, _lib.KEY_DIM), **f32)
+    d_init_c = torch.empty((batch, heads, width, _lib.KEY_DIM), **f32)
+    nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, width, chunk)
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
+    entry = lib.m4mr_backward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_backward
+    _lib.check(
+        entry(
+            _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
+            _ptr(floor), batch, time, heads, width, chunk, _ptr(solved), _ptr(factors),
+            _ptr(start_s), _ptr(start_c), _ptr(d_output), _ptr(d_variance),
+            _ptr(d_final_s), _ptr(d_final_c), *(_ptr(g) for g in grads),
+            _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace), nbytes, _stream(),
         )
-        d_init = (d_init_s, d_init_c) if ctx.has_initial else (None, None)
-        return (*grads, *d_init, None)
+    )
+    return (*grads, d_init_s, d_init_c)
 
 
 class _SpdSolve(torch.autograd.Function):
