@@ -580,6 +580,45 @@ def main_mixer_read(args):
         check(lib.m4mr_epilogue_forward(p(read), p(variance), p(value), p(conf), p(skip), B, T,
                                         H, D, p(output), st))
 
+    # The backward legs: epilogue VJP, memory-read VJP, prologue VJP.
+    d_out = rand(B, T, H, D)
+    d_read, d_var, d_val_skip = e(B, T, H, D, **f32), e(B, T, H, **f32), e(B, T, H, D, **f32)
+    d_conf, d_skip = e(H, **f32), e(H, **f32)
+    g_mem = [e(B, T, H, D, **f32), e(B, T, H, D, **f32), e(B, T, H, D, **f32), e(B, T, H, **f32),
+             e(B, T, H, **f32), e(H, D, **f32), e(B, H, D, D, **f32), e(B, H, D, D, **f32)]
+    g_pro = [e(B, T, H, D, **f32), e(B, T, H, D, **f32), e(B, T, H, **f32), e(B, T, H, **f32),
+             e(H, **f32), e(H, **f32), e(H, **f32), e(H, D, **f32)]
+    bwd_bytes = lib.m4mr_backward_workspace_bytes(B, T, H, D, 64)
+    bwd_ws = torch.empty(bwd_bytes, dtype=torch.uint8, device="cuda:0")
+    mix_bytes = lib.m4mr_mixer_workspace_bytes(B, T, H)
+    mix_ws = torch.empty(mix_bytes, dtype=torch.uint8, device="cuda:0")
+
+    def backward(fused_memread):
+        check(lib.m4mr_epilogue_backward(p(read), p(variance), p(value), p(conf), p(skip), B, T,
+                                         H, D, p(d_out), p(d_read), p(d_var), p(d_val_skip),
+                                         p(d_conf), p(d_skip), p(mix_ws), mix_bytes, st))
+        tail = (B, T, H, D, 64, p(solved), p(factors), p(start_s), p(start_c), p(d_read),
+                p(d_var), None, None, *(p(g) for g in g_mem), p(bwd_ws), bwd_bytes, st)
+        if fused_memread:
+            check(lib.m4mr_mixer_backward(p(key), p(value), p(query), p(beta), p(log_decay),
+                                          p(floor), None, 1, *tail))
+        else:
+            check(lib.m4mr_backward(p(keys), p(value), p(queries), p(beta), p(log_decay),
+                                    p(floor), *tail))
+        check(lib.m4mr_prologue_backward(
+            p(key), p(query), p(beta_raw), p(dt_raw), p(beta_bias), p(dt_bias), p(a_log),
+            p(floor_raw), None, B, T, H, D, 1.0, 1, p(g_mem[0]), p(g_mem[2]), p(g_mem[3]),
+            p(g_mem[4]), p(g_mem[5]), None, *(p(g) for g in g_pro), None, p(mix_ws), mix_bytes,
+            st))
+
+    def fused_train():
+        fused()
+        backward(True)
+
+    def separate_train():
+        separate()
+        backward(False)
+
     def timed(fn, steps):
         for _ in range(args.warmup):
             fn()
@@ -597,6 +636,10 @@ def main_mixer_read(args):
     runs = [(timed(fused, args.steps), timed(separate, args.steps)) for _ in range(3)]
     seconds = min(r[0] for r in runs)
     separate_seconds = min(r[1] for r in runs)
+    train = [(timed(fused_train, args.steps), timed(separate_train, args.steps))
+             for _ in range(3)]
+    train_seconds = min(r[0] for r in train)
+    separate_train_seconds = min(r[1] for r in train)
     line = {
         "metric": MIXER_READ_METRIC,
         "value": B * T / seconds,
@@ -614,6 +657,9 @@ def main_mixer_read(args):
                    "batch": B, "seq_len": T, "heads": H, "key_dim": D, "value_dim": D},
         "separate_ms_per_step": separate_seconds * 1e3,
         "fused_speedup": separate_seconds / seconds,
+        "train_ms_per_step": train_seconds * 1e3,
+        "separate_train_ms_per_step": separate_train_seconds * 1e3,
+        "train_speedup": separate_train_seconds / train_seconds,
     }
     print(json.dumps(line), flush=True)
 

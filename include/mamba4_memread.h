@@ -164,6 +164,32 @@ int m4mr_mixer_forward(const float* key, const float* value, const float* query,
                        float* start_evidence, float* start_cross,
                        float* shifted, void* stream);
 
+/*
+ * Backward of the memory read inside m4mr_mixer_forward: m4mr_backward
+ * with the raw keys and queries (and the key shift's `previous`, key_shift)
+ * in place of the normalised ones, which bwd_dy and bwd_grads normalise as
+ * they load them, and the forward's beta, log_decay and floor.  The
+ * cotangents are those of the ungated read (d_read) and of the variance; the
+ * gradients are those of m4mr_backward (with respect to the normalised keys
+ * and queries and to the gates), for m4mr_prologue_backward to carry to the
+ * raw projections.  No counterpart in the reference, whose autodiff takes
+ * the same path through its prologue (lm/models/mamba4.py:183-237); it
+ * saves the prologue's recomputation in the fused mixer's backward.
+ * workspace as m4mr_backward.
+ */
+int m4mr_mixer_backward(const float* key, const float* value, const float* query,
+                        const float* beta, const float* log_decay, const float* floor,
+                        const float* previous, int key_shift,
+                        int B, int T, int H, int value_dim, int chunk,
+                        const float* solved, const float* factors,
+                        const float* start_evidence, const float* start_cross,
+                        const float* d_read, const float* d_variance,
+                        const float* d_final_evidence, const float* d_final_cross,
+                        float* d_keys, float* d_values, float* d_queries,
+                        float* d_beta, float* d_log_decay, float* d_floor,
+                        float* d_init_evidence, float* d_init_cross,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Number of chunks NC and of evidence start states NS for T tokens. */
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts);
 

@@ -38,14 +38,15 @@ template <typename In, bool MIX>
 __global__ void fwd_read_kernel(Dims, const In*, const In*, const In*, const float*,
                                 const float*, const float*, const float*, float*, float*, MixerIn,
                                 ReadGate);
-template <typename In>
+template <typename In, bool MIX>
 __global__ void bwd_dy_kernel(Dims, const In*, const In*, const In*, const float*,
-                              const float*, const float*, const float*, const float*, float*);
-template <typename In>
+                              const float*, const float*, const float*, const float*, float*,
+                              MixerIn);
+template <typename In, bool MIX>
 __global__ void bwd_grads_kernel(Dims, const In*, const In*, const float*, const float*,
                                  const float*, const float*, const float*, const float*,
                                  const float*, const float*, const float*, const float*, float*,
-                                 float*, float*, float*, float*, float*);
+                                 float*, float*, float*, float*, float*, MixerIn);
 __global__ void floor_reduce_kernel(Dims, const float*, float*);
 __global__ void prologue_forward_kernel(const float*, const float*, const float*, const float*,
                                         const float*, const float*, const float*, const float*,
@@ -148,10 +149,12 @@ int configure() {
              {(const void*)m4::fwd_read_kernel<float, false>, kChunkLdsBytes},
              {(const void*)m4::fwd_read_kernel<m4::bf16_t, false>, kChunkLdsBytes},
              {(const void*)m4::fwd_read_kernel<float, true>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<float>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<m4::bf16_t>, kChunkLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<m4::bf16_t>, kGradsLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<float, false>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<m4::bf16_t, false>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<float, true>, kChunkLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float, false>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float, true>, kGradsLdsBytes},
              {(const void*)m4::states_kernel<false, float, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, m4::bf16_t, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false>, kStatesLdsBytes},
@@ -354,7 +357,11 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   });
 }
 
-template <typename In>
+// The backward launch sequence.  MIX: keys and queries come from the
+// mixer's raw projections (`mix`; the plain key and query pointers are
+// unused), normalised on load by bwd_dy and bwd_grads; the gradients are
+// those of the normalised keys and queries, as in the plain case.
+template <typename In, bool MIX>
 int backward_impl(const char* entry, const In* keys, const In* values, const In* queries,
                   const float* beta, const float* log_decay, const float* floor, int B, int T,
                   int H, int value_dim, int chunk, const float* solved, const float* factors,
@@ -362,10 +369,17 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                   const float* d_variance, const float* d_final_evidence,
                   const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
                   float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
-                  float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream) {
+                  float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream,
+                  const m4::MixerIn& mix = {}) {
   g_error.clear();
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
+  if (MIX) {
+    keys = reinterpret_cast<const In*>(mix.key);
+    queries = reinterpret_cast<const In*>(mix.query);
+    if (mix.previous && misaligned(mix.previous))
+      return fail(M4MR_EINVAL, std::string(entry) + ": arrays must be 16-byte aligned");
+  }
   const void* need[] = {keys,    values,     queries,         beta,         log_decay,
                         floor,   solved,     factors,         start_evidence, start_cross,
                         d_output, d_variance, d_keys,         d_values,     d_queries,
@@ -389,9 +403,9 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   const unsigned seqs = (unsigned)B * H * d.NC;
   const long tokens = (long)B * T * H;
   int rc = launch("bwd_dy", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_dy_kernel<In>, dim3(persistent_grid(seqs, 2)), dim3(256),
-                       kChunkLdsBytes, st, d, keys,
-                       values, queries, beta, log_decay, start_cross, d_output, d_variance, ws.z);
+    hipLaunchKernelGGL((m4::bwd_dy_kernel<In, MIX>), dim3(persistent_grid(seqs, 2)), dim3(256),
+                       kChunkLdsBytes, st, d, keys, values, queries, beta, log_decay, start_cross,
+                       d_output, d_variance, ws.z, mix);
   });
   if (rc) return rc;
   rc = launch("factored_solve", st, [&] {
@@ -421,10 +435,10 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   }
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
-    hipLaunchKernelGGL(m4::bwd_grads_kernel<In>, dim3(seqs), dim3(512), kGradsLdsBytes, st, d, keys,
-                       values, beta, log_decay, solved, ws.z, d_output, d_variance,
+    hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX>), dim3(seqs), dim3(512), kGradsLdsBytes, st,
+                       d, keys, values, beta, log_decay, solved, ws.z, d_output, d_variance,
                        start_evidence, start_cross, ws.end_s, ws.end_c, d_keys, d_values,
-                       d_queries, d_beta, d_log_decay, ws.floor_part);
+                       d_queries, d_beta, d_log_decay, ws.floor_part, mix);
   });
   if (rc) return rc;
   return launch("floor_reduce", st, [&] {
@@ -511,6 +525,27 @@ int m4mr_mixer_forward(const float* key, const float* value, const float* query,
                                    start_evidence, start_cross, stream, mix, gate);
 }
 
+int m4mr_mixer_backward(const float* key, const float* value, const float* query,
+                        const float* beta, const float* log_decay, const float* floor,
+                        const float* previous, int key_shift, int B, int T, int H,
+                        int value_dim, int chunk, const float* solved, const float* factors,
+                        const float* start_evidence, const float* start_cross,
+                        const float* d_read, const float* d_variance,
+                        const float* d_final_evidence, const float* d_final_cross,
+                        float* d_keys, float* d_values, float* d_queries, float* d_beta,
+                        float* d_log_decay, float* d_floor, float* d_init_evidence,
+                        float* d_init_cross, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  g_error.clear();
+  if (!key || !query) return fail(M4MR_EINVAL, "m4mr_mixer_backward: a required pointer is NULL");
+  const m4::MixerIn mix{key, query, previous, key_shift ? 1 : 0};
+  return backward_impl<float, true>(
+      "m4mr_mixer_backward", nullptr, value, nullptr, beta, log_decay, floor, B, T, H, value_dim,
+      chunk, solved, factors, start_evidence, start_cross, d_read, d_variance, d_final_evidence,
+      d_final_cross, d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_evidence,
+      d_init_cross, workspace, workspace_bytes, stream, mix);
+}
+
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {
   g_error.clear();
   std::string why;
@@ -536,7 +571,7 @@ int m4mr_backward(const float* keys, const float* values, const float* queries,
                   const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
                   float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
                   float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream) {
-  return backward_impl("m4mr_backward", keys, values, queries, beta, log_decay, floor, B, T, H,
+  return backward_impl<float, false>("m4mr_backward", keys, values, queries, beta, log_decay, floor, B, T, H,
                        value_dim, chunk, solved, factors, start_evidence, start_cross, d_output,
                        d_variance, d_final_evidence, d_final_cross, d_keys, d_values, d_queries,
                        d_beta, d_log_decay, d_floor, d_init_evidence, d_init_cross, workspace,
@@ -553,7 +588,7 @@ int m4mr_backward_bf16(const uint16_t* keys, const uint16_t* values, const uint1
                        float* d_queries, float* d_beta, float* d_log_decay, float* d_floor,
                        float* d_init_evidence, float* d_init_cross, void* workspace,
                        size_t workspace_bytes, void* stream) {
-  return backward_impl("m4mr_backward_bf16", reinterpret_cast<const m4::bf16_t*>(keys),
+  return backward_impl<m4::bf16_t, false>("m4mr_backward_bf16", reinterpret_cast<const m4::bf16_t*>(keys),
                        reinterpret_cast<const m4::bf16_t*>(values),
                        reinterpret_cast<const m4::bf16_t*>(queries), beta, log_decay, floor, B,
                        T, H, value_dim, chunk, solved, factors, start_evidence, start_cross,

@@ -224,13 +224,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ...; the next chunk's dout, value and C0 tiles load into registers once
 // this chunk's last value tile is in LDS, its keys once this chunk's keys are
 // staged, and its queries and d_variance after this chunk's epilogue.
-template <typename In>
+//
+// MIX: keys and queries from the mixer's raw projections, as in
+// fwd_read_kernel (keys shifted and normalised at staging, queries
+// normalised where used).
+template <typename In, bool MIX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dy_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const In* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ start_c,
     const float* __restrict__ d_output, const float* __restrict__ d_variance,
-    float* __restrict__ ybar) {
+    float* __restrict__ ybar, MixerIn mix) {
   extern __shared__ float smem[];
   float* DO = smem;
   float* V = DO + TILE;  // values, then keys
@@ -254,14 +258,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       dvar[q] = 0.f;
       if (t < s.len) {
         const long th = token_head(d, s.b, s.n * d.chunk + t, s.h);
-        qv[q] = load4(queries + th * 64 + c4);
+        if constexpr (MIX)
+          qv[q] = load4(mix.query + th * 64 + c4);
+        else
+          qv[q] = load4(queries + th * 64 + c4);
         dvar[q] = d_variance[th];
       }
     }
   };
+  auto fetch_keys = [&](const SeqIndex& s) {
+    if constexpr (MIX) {
+      rk.fetch_rows(s.len, [&](int r) -> const float* {
+        const int t = s.n * d.chunk + r;
+        const float* p = mix_key_row(mix, d, s.b, t, s.h);
+        return p ? p : mix.query + token_head(d, s.b, t, s.h) * 64;
+      });
+    } else {
+      rk.fetch_rows(s.len, rows_of(keys, d, s));
+    }
+  };
   rd.fetch_rows(si.len, value_rows(d_output, d, si, 0));
   rv.fetch_rows(si.len, value_rows(values, d, si, 0));
-  rk.fetch_rows(si.len, rows_of(keys, d, si));
+  fetch_keys(si);
   rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   fetch_rows_q(si);
 
@@ -309,9 +327,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         G[t * LDT + s] = v;
       }
     __syncthreads();
-    rk.store(V);
+    if constexpr (MIX)
+      rk.store_unit(V, mix.key_shift && !mix.previous && si.n == 0);
+    else
+      rk.store(V);
     __syncthreads();
-    if (more) rk.fetch_rows(sn.len, rows_of(keys, d, sn));
+    if (more) fetch_keys(sn);
 
     f4 within[4];
     zero4(within);
@@ -322,8 +343,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (t < si.len) {
         const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
         const float carried = expf(cs.prefix[t]);
+        const f4 qn = MIX ? mix_unit(qv[q]) : qv[q];
         *reinterpret_cast<f4*>(ybar + th * 64 + c4) =
-            quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qv[q];
+            quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qn;
       }
     }
     if (!more) break;
@@ -353,7 +375,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 constexpr int GRADS_THREADS = 512;
 constexpr int MAX_NV = 2;
 
-template <typename In>
+//
+// MIX: keys from the mixer's raw projections, shifted and normalised at
+// staging (as in fwd_read_kernel).
+template <typename In, bool MIX>
 __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
@@ -363,7 +388,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     const float* __restrict__ end_s, const float* __restrict__ end_c,
     float* __restrict__ d_keys, float* __restrict__ d_values, float* __restrict__ d_queries,
     float* __restrict__ d_beta, float* __restrict__ d_log_decay,
-    float* __restrict__ floor_part) {
+    float* __restrict__ floor_part, MixerIn mix) {
   extern __shared__ float smem[];
   float* Kt = smem;       // keys, then S0
   float* Vt = Kt + TILE;  // a value tile, then a C0 tile
@@ -395,12 +420,23 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
 
   {
     TileRegs2 rt[5];
-    rt[0].fetch_rows(si.len, rows_of(keys, d, si));
+    if constexpr (MIX) {
+      rt[0].fetch_rows(si.len, [&](int r) -> const float* {
+        const int t = si.n * d.chunk + r;
+        const float* p = mix_key_row(mix, d, si.b, t, si.h);
+        return p ? p : mix.query + token_head(d, si.b, t, si.h) * 64;
+      });
+    } else {
+      rt[0].fetch_rows(si.len, rows_of(keys, d, si));
+    }
     rt[1].fetch_rows(si.len, value_rows(values, d, si, 0));
     rt[2].fetch_rows(si.len, rows_of(solved, d, si));
     rt[3].fetch_rows(si.len, rows_of(z, d, si));
     rt[4].fetch_rows(si.len, value_rows(d_output, d, si, 0));
-    rt[0].store(Kt);
+    if constexpr (MIX)
+      rt[0].store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0);
+    else
+      rt[0].store(Kt);
     rt[1].store(Vt);
     rt[2].store(Yt);
     rt[3].store(Zt);
@@ -703,13 +739,14 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   template __global__ void fwd_read_kernel<In, false>(                                         \
       Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
       const float*, float*, float*, MixerIn, ReadGate);                                        \
-  template __global__ void bwd_dy_kernel<In>(Dims, const In*, const In*, const In*,            \
-                                             const float*, const float*, const float*,         \
-                                             const float*, const float*, float*);              \
-  template __global__ void bwd_grads_kernel<In>(                                               \
+  template __global__ void bwd_dy_kernel<In, false>(Dims, const In*, const In*, const In*,     \
+                                                    const float*, const float*, const float*,  \
+                                                    const float*, const float*, float*,        \
+                                                    MixerIn);                                  \
+  template __global__ void bwd_grads_kernel<In, false>(                                        \
       Dims, const In*, const In*, const float*, const float*, const float*, const float*,      \
       const float*, const float*, const float*, const float*, const float*, const float*,      \
-      float*, float*, float*, float*, float*, float*);
+      float*, float*, float*, float*, float*, float*, MixerIn);
 M4_CHUNK_KERNELS(float)
 M4_CHUNK_KERNELS(bf16_t)
 #undef M4_CHUNK_KERNELS
@@ -717,6 +754,13 @@ template __global__ void fwd_read_kernel<float, true>(Dims, const float*, const 
                                                       const float*, const float*, const float*,
                                                       const float*, const float*, float*, float*,
                                                       MixerIn, ReadGate);
+template __global__ void bwd_dy_kernel<float, true>(Dims, const float*, const float*, const float*,
+                                                    const float*, const float*, const float*,
+                                                    const float*, const float*, float*, MixerIn);
+template __global__ void bwd_grads_kernel<float, true>(
+    Dims, const float*, const float*, const float*, const float*, const float*, const float*,
+    const float*, const float*, const float*, const float*, const float*, const float*, float*,
+    float*, float*, float*, float*, float*, MixerIn);
 
 // d floor[h][4c4 .. 4c4+3] = sum over (b, n) of floor_part[(b*H + h)*NC + n]
 // in a fixed order: block (h, c4) of 256 threads, thread i sums entries

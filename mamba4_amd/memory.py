@@ -132,10 +132,13 @@ class _MemoryRead(torch.autograd.Function):
 
 
 def memread_backward(keys, values, queries, beta, log_decay, floor, solved, factors, start_s,
-                     start_c, chunk, d_output, d_variance, d_final_s, d_final_c):
+                     start_c, chunk, d_output, d_variance, d_final_s, d_final_c, mixer=None):
     """m4mr_backward on the forward's inputs and residual set: returns
     (d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_evidence,
-    d_init_cross), all float32.  None cotangents are zero."""
+    d_init_cross), all float32.  None cotangents are zero.  With
+    ``mixer = (previous, key_shift)``, keys and queries are the mixer's raw
+    projections and m4mr_mixer_backward normalises them on load (the
+    gradients are still those of the normalised keys and queries)."""
     lib = _lib.load()
     batch, time, heads, _ = keys.shape
     width = values.shape[-1]
@@ -156,16 +159,17 @@ def memread_backward(keys, values, queries, beta, log_decay, floor, solved, fact
     d_init_c = torch.empty((batch, heads, width, _lib.KEY_DIM), **f32)
     nbytes = lib.m4mr_backward_workspace_bytes(batch, time, heads, width, chunk)
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
-    entry = lib.m4mr_backward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_backward
-    _lib.check(
-        entry(
-            _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
-            _ptr(floor), batch, time, heads, width, chunk, _ptr(solved), _ptr(factors),
-            _ptr(start_s), _ptr(start_c), _ptr(d_output), _ptr(d_variance),
-            _ptr(d_final_s), _ptr(d_final_c), *(_ptr(g) for g in grads),
-            _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace), nbytes, _stream(),
-        )
-    )
+    tail = (batch, time, heads, width, chunk, _ptr(solved), _ptr(factors), _ptr(start_s),
+            _ptr(start_c), _ptr(d_output), _ptr(d_variance), _ptr(d_final_s), _ptr(d_final_c),
+            *(_ptr(g) for g in grads), _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace), nbytes,
+            _stream())
+    head = (_ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay), _ptr(floor))
+    if mixer is not None:
+        previous, key_shift = mixer
+        _lib.check(lib.m4mr_mixer_backward(*head, _ptr(previous), int(key_shift), *tail))
+    else:
+        entry = lib.m4mr_backward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_backward
+        _lib.check(entry(*head, *tail))
     return (*grads, d_init_s, d_init_c)
 
 

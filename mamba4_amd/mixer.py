@@ -223,9 +223,9 @@ class MixerRead(NamedTuple):
 
 
 class _MixerRead(torch.autograd.Function):
-    """m4mr_mixer_forward, and its VJP through the separate kernels: the
-    prologue is re-run for the normalised inputs, then the epilogue VJP, the
-    memory-read VJP (from the forward's residuals) and the prologue VJP."""
+    """m4mr_mixer_forward, and its VJP: the epilogue VJP, the memory-read
+    VJP from the forward's residuals with the raw keys and queries
+    normalised on load (m4mr_mixer_backward), and the prologue VJP."""
 
     @staticmethod
     def forward(ctx, key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
@@ -264,7 +264,7 @@ class _MixerRead(torch.autograd.Function):
         )
         ctx.save_for_backward(key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log,
                               floor_raw, previous, confidence_scale, skip, read, variance,
-                              solved, factors, start_s, start_c)
+                              beta, log_decay, floor, solved, factors, start_s, start_c)
         ctx.beta_max, ctx.floor_min, ctx.key_shift, ctx.chunk = (beta_max, floor_min,
                                                                  key_shift, chunk)
         ctx.has_initial = init_s is not None
@@ -273,11 +273,8 @@ class _MixerRead(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_output, d_variance, d_final_s, d_final_c, d_shifted):
         (key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
-         confidence_scale, skip, read, variance, solved, factors, start_s,
-         start_c) = ctx.saved_tensors
-        keys, queries, beta, log_decay, floor, _ = _prologue_forward(
-            key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
-            ctx.beta_max, ctx.floor_min, ctx.key_shift)
+         confidence_scale, skip, read, variance, beta, log_decay, floor, solved, factors,
+         start_s, start_c) = ctx.saved_tensors
         if d_output is None:
             d_output = torch.zeros_like(read)
         d_read, d_var, d_skip_value, d_scale, d_skip = _epilogue_backward(
@@ -285,9 +282,9 @@ class _MixerRead(torch.autograd.Function):
         if d_variance is not None:
             d_var = d_var + _f32(d_variance)
         (d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_s,
-         d_init_c) = memread_backward(keys, value, queries, beta, log_decay, floor, solved,
+         d_init_c) = memread_backward(key, value, query, beta, log_decay, floor, solved,
                                       factors, start_s, start_c, ctx.chunk, d_read, d_var,
-                                      d_final_s, d_final_c)
+                                      d_final_s, d_final_c, mixer=(previous, ctx.key_shift))
         (d_key, d_query, d_beta_raw, d_dt_raw, d_beta_bias, d_dt_bias, d_a_log, d_floor_raw,
          d_previous) = _prologue_backward(
             key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
