@@ -29,6 +29,7 @@ from mamba4_amd.mixer import (  # noqa: F401
     memory_inputs,
     mixer_read,
 )
+from mamba4_amd.flashmamba import mamba3_fused  # noqa: F401
 from mamba4_amd.order import order_memory, order_memory_chunked  # noqa: F401
 
 __all__ = [
@@ -38,6 +39,7 @@ __all__ = [
     "SOLVERS",
     "SelectiveResult",
     "SelectiveState",
+    "mamba3_fused",
     "gated_read",
     "memory_inputs",
     "mixer_read",

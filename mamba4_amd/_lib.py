@@ -11,6 +11,7 @@ import re
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libmamba4_memread.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "mamba4_memread.h")
+HEADERS = [HEADER, os.path.join(os.path.dirname(HERE), "include", "mamba3_scan.h")]
 
 EINVAL = 1
 EHIP = 2
@@ -80,6 +81,9 @@ SIGNATURES = {
     "m4mr_order_workspace_bytes": (_S, [_I] * 5),
     "m4mr_order_forward": (_I, [_P] * 3 + [_I] * 5 + [_P, _P, _S, _P]),
     "m4mr_order_backward": (_I, [_P] * 5 + [_I] * 5 + [_P] * 4 + [_S, _P]),
+    "m3s_forward": (_I, [_P] * 9 + [_I] * 6 + [_P] * 4 + [_P]),
+    "m3s_backward_workspace_bytes": (_S, [_I] * 6),
+    "m3s_backward": (_I, [_P] * 9 + [_I] * 6 + [_P] * 4 + [_P] * 9 + [_P, _S, _P]),
     "m4mr_profile_enable": (None, [_I]),
     "m4mr_profile_select": (None, [ctypes.c_char_p]),
     "m4mr_profile_reset": (None, []),
@@ -98,9 +102,11 @@ class MemreadError(RuntimeError):
 
 
 def header_functions():
-    """Names of the functions declared in include/mamba4_memread.h."""
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(m4mr_\w+)\s*\(", text, re.M)))
+    """Names of the functions declared in include/mamba4_memread.h and
+    include/mamba3_scan.h."""
+    text = "".join(open(h).read() for h in HEADERS)
+    pattern = r"^\s*(?:const\s+)?\w+\**\s+\**((?:m4mr|m3s)_\w+)\s*\("
+    return sorted(set(re.findall(pattern, text, re.M)))
 
 
 def load():

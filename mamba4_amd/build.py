@@ -18,7 +18,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIBRARY = os.path.join(HERE, "libmamba4_memread.so")
-SOURCES = ["api.hip", "states.hip", "factor.hip", "chunk.hip", "mixer.hip", "order.hip"]
+SOURCES = ["api.hip", "states.hip", "factor.hip", "chunk.hip", "mixer.hip", "order.hip",
+           "scan3.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -12,8 +12,10 @@
 #include <string>
 #include <vector>
 
+#include "../../include/mamba3_scan.h"
 #include "../../include/mamba4_memread.h"
 #include "common.hpp"
+#include "scan3.hpp"
 
 namespace m4 {
 template <typename In>
@@ -94,7 +96,9 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "prologue_backward", "epilogue_forward",
                                     "epilogue_backward", "head_sums", "order_local",
                                     "order_carry",    "order_apply", "order_bwd_local",
-                                    "order_bwd_carry", "order_bwd_apply", "mixer_gates"};
+                                    "order_bwd_carry", "order_bwd_apply", "mixer_gates",
+                                    "m3_walk",        "m3_out",    "m3_walk_bwd", "m3_grad",
+                                    "m3_finish",      "m3_bias"};
 
 struct ProfRecord {
   const char* name;
@@ -158,7 +162,11 @@ int configure() {
              {(const void*)m4::states_kernel<false, float, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, m4::bf16_t, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<false, float, true>, kStatesLdsBytes}};
+             {(const void*)m4::states_kernel<false, float, true>, kStatesLdsBytes},
+             {(const void*)m3::walk_kernel<false>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true>, m3::kWalkLds},
+             {(const void*)m3::out_kernel, m3::kOutLds},
+             {(const void*)m3::grad_kernel, m3::kGradLds}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)k.bytes);
@@ -956,6 +964,152 @@ int m4mr_order_backward(const float* values, const float* log_decay, const float
   return launch("order_bwd_apply", st, [&] {
     hipLaunchKernelGGL(m4::order_bwd_apply_kernel, dim3(chunks), dim3(threads), 0, st, d, values,
                        log_decay, initial, output, d_output, heads, d_values, d_log_decay);
+  });
+}
+
+// ------------------------------------------------------------ mamba-3 --
+
+}  // extern "C"
+
+namespace {
+
+// Head groups of the gradient kernel: enough (b, chunk, group) blocks to give
+// every compute unit about two, each group's heads summed in registers.
+int m3_groups(int B, int T, int H) {
+  const long chunks = (long)B * ((T + m3::C - 1) / m3::C);
+  long g = (512 + chunks - 1) / chunks;
+  if (g < 1) g = 1;
+  if (g > H) g = H;
+  // Equal groups of hpg heads, none empty.
+  const long hpg = (H + g - 1) / g;
+  return (int)((H + hpg - 1) / hpg);
+}
+
+struct M3Workspace {
+  float *dh1, *dgam, *dscale, *ddt_loc, *D, *qb_part, *kb_part, *dc_part, *db_part, *dang_part;
+};
+
+// Carves the workspace (each array 256-byte aligned); returns the bytes used.
+size_t m3_workspace(int B, int T, int H, M3Workspace* ws, void* base) {
+  const long NC = (T + m3::C - 1) / m3::C, tp = NC * m3::C, G = m3_groups(B, T, H);
+  const long counts[10] = {(long)B * H * NC * m3::NT * m3::PT, (long)B * T * H, (long)B * T * H,
+                           (long)B * T * H, (long)B * H * NC * m3::AM, (long)B * NC * H * m3::NT,
+                           (long)B * NC * H * m3::NT, G * B * tp * m3::NT, G * B * tp * m3::NT,
+                           G * B * tp * m3::AM};
+  float** slots[10] = {&ws->dh1, &ws->dgam, &ws->dscale, &ws->ddt_loc, &ws->D,
+                       &ws->qb_part, &ws->kb_part, &ws->dc_part, &ws->db_part, &ws->dang_part};
+  size_t off = 0;
+  for (int i = 0; i < 10; ++i) {
+    if (base) *slots[i] = reinterpret_cast<float*>(static_cast<char*>(base) + off);
+    off += ((size_t)counts[i] * sizeof(float) + 255) & ~(size_t)255;
+  }
+  return off;
+}
+
+bool m3_bad_shape(const char* entry, int B, int T, int H, int N, int P, int A) {
+  std::string why;
+  if (B < 1 || T < 1 || H < 1) why = "need B, T, H >= 1";
+  else if (H > M3S_MAX_HEADS) why = "need H <= 128";
+  else if (N < 2 || N > M3S_MAX_STATE || N % 2) why = "need an even N in [2, 128]";
+  else if (P < 1 || P > M3S_MAX_VALUE) why = "need P in [1, 64]";
+  else if (A < 0 || 2 * A > N) why = "need 0 <= A <= N/2";
+  else if ((long)B * T * H * P >= (1L << 31) || (long)B * T * N >= (1L << 31))
+    why = "arrays above 2^31 elements";
+  if (why.empty()) return false;
+  fail(M4MR_EINVAL, std::string(entry) + ": " + why);
+  return true;
+}
+
+bool misaligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) != 0; }
+
+}  // namespace
+
+extern "C" {
+
+int m3s_forward(const float* c, const float* b, const float* x, const float* adt,
+                const float* dt, const float* trap_logits, const float* angles,
+                const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                int A, float* y, float* final_state, float* starts, float* phases, void* stream) {
+  g_error.clear();
+  if (m3_bad_shape("m3s_forward", B, T, H, N, P, A)) return M4MR_EINVAL;
+  if (!c || !b || !x || !adt || !dt || !trap_logits || (A > 0 && !angles) || !q_bias ||
+      !k_bias || !y || !starts || !phases)
+    return fail(M4MR_EINVAL, "m3s_forward: a required pointer is NULL");
+  if (misaligned8(c) || misaligned8(b) || misaligned8(q_bias) || misaligned8(k_bias) ||
+      misaligned(x) || misaligned(starts))
+    return fail(M4MR_EINVAL, "m3s_forward: c, b, biases need 8-byte and x, starts 16-byte alignment");
+  if (int rc = configure()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const m3::Shape s{B, T, H, N, P, A, (T + m3::C - 1) / m3::C};
+  int rc = launch("m3_walk", st, [&] {
+    hipLaunchKernelGGL(m3::walk_kernel<false>, dim3(B * H), dim3(256), m3::kWalkLds, st, s, b,
+                       k_bias, x, adt, dt, trap_logits, angles, phases, starts, nullptr,
+                       final_state);
+  });
+  if (rc) return rc;
+  return launch("m3_out", st, [&] {
+    hipLaunchKernelGGL(m3::out_kernel, dim3(B * s.NC * H), dim3(256), m3::kOutLds, st, s, c, b,
+                       x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, y);
+  });
+}
+
+size_t m3s_backward_workspace_bytes(int B, int T, int H, int N, int P, int A) {
+  (void)N;
+  (void)P;
+  (void)A;
+  if (B < 1 || T < 1 || H < 1) return 0;
+  return m3_workspace(B, T, H, nullptr, nullptr);
+}
+
+int m3s_backward(const float* c, const float* b, const float* x, const float* adt,
+                 const float* dt, const float* trap_logits, const float* angles,
+                 const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                 int A, const float* starts, const float* phases, const float* d_y,
+                 const float* d_final, float* d_c, float* d_b, float* d_x, float* d_adt,
+                 float* d_dt, float* d_trap, float* d_angles, float* d_q_bias, float* d_k_bias,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  g_error.clear();
+  if (m3_bad_shape("m3s_backward", B, T, H, N, P, A)) return M4MR_EINVAL;
+  if (!c || !b || !x || !adt || !dt || !trap_logits || (A > 0 && (!angles || !d_angles)) ||
+      !q_bias || !k_bias || !starts || !phases || !d_y || !d_c || !d_b || !d_x || !d_adt ||
+      !d_dt || !d_trap || !d_q_bias || !d_k_bias || !workspace)
+    return fail(M4MR_EINVAL, "m3s_backward: a required pointer is NULL");
+  if (misaligned8(c) || misaligned8(b) || misaligned8(q_bias) || misaligned8(k_bias) ||
+      misaligned(x) || misaligned(d_y) || misaligned(starts) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(M4MR_EINVAL,
+                "m3s_backward: c, b, biases need 8-byte, x, d_y, starts 16-byte and the "
+                "workspace 256-byte alignment");
+  M3Workspace ws{};
+  if (workspace_bytes < m3_workspace(B, T, H, &ws, workspace))
+    return fail(M4MR_EINVAL, "m3s_backward: workspace too small");
+  if (int rc = configure()) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const m3::Shape s{B, T, H, N, P, A, (T + m3::C - 1) / m3::C};
+  const int groups = m3_groups(B, T, H);
+  const m3::GradOut o{d_x,         d_adt,        ws.dgam,       ws.dscale,
+                      ws.ddt_loc,  ws.D,         ws.qb_part,    ws.kb_part,
+                      ws.dc_part,  ws.db_part,   ws.dang_part};
+  int rc = launch("m3_walk_bwd", st, [&] {
+    hipLaunchKernelGGL(m3::walk_kernel<true>, dim3(B * H), dim3(256), m3::kWalkLds, st, s, c,
+                       q_bias, d_y, adt, dt, trap_logits, angles, const_cast<float*>(phases),
+                       ws.dh1, d_final, nullptr);
+  });
+  if (rc) return rc;
+  rc = launch("m3_grad", st, [&] {
+    hipLaunchKernelGGL(m3::grad_kernel, dim3(B * s.NC * groups), dim3(256), m3::kGradLds, st, s,
+                       groups, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases,
+                       starts, ws.dh1, d_y, o);
+  });
+  if (rc) return rc;
+  rc = launch("m3_finish", st, [&] {
+    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC), dim3(256),
+                       (size_t)H * m3::AM * sizeof(float), st, s, groups, dt, trap_logits, angles,
+                       o, d_c, d_b, d_dt, d_trap, d_angles);
+  });
+  if (rc) return rc;
+  return launch("m3_bias", st, [&] {
+    hipLaunchKernelGGL(m3::bias_kernel, dim3(H), dim3(128), 0, st, s, o, d_q_bias, d_k_bias);
   });
 }
 

@@ -1,0 +1,798 @@
+// Mamba-3 SISO scan in FlashMamba's fused projection layout, for gfx950.
+//
+// Operator: mamba3_fused (lm/kernels/flashmamba.py:1125-1162) over fused_scan
+// (:901-1111).  One shared query row c_t and key row b_t per token [B,T,N],
+// values x [B,T,H*P], per-head log decays adt, steps dt, trapezoid logits
+// [B,T,H], shared angle rates [B,T,A], per-head biases [H,N].  Per head:
+//   theta_t = sum_{s<=t} angles_s dt_s;  q_t = rot(c_t + qb, theta_t),
+//   k_t = rot(b_t + kb, theta_t);  gamma = dt sigmoid(trap),
+//   scale_s = gamma_s + dt_{s+1} (1 - sigmoid(trap_{s+1})),
+//   within a chunk with p_t = sum of adt over the chunk up to t:
+//   y_t = sum_{s<t} e^{p_t - p_s} scale_s (q_t.k_s) v_s + gamma_t (q_t.k_t) v_t
+//         + e^{p_t} q_t^T S,    S <- e^{p_L} S + sum_s e^{p_L - p_s} scale_s k_s v_s^T.
+//
+// Kernels (chunks of C = 64 tokens, one token per lane of a wave; the state
+// S is a 128 x 64 float32 tile, N <= 128 and P <= 64 are zero-padded):
+//   walk_kernel<false>  one block per (b, h): walks the chunks in order,
+//                       stores each chunk's start state and start phase, and
+//                       the final state (the sequential part: one MFMA
+//                       product K^T (u v) per chunk).
+//   out_kernel          one block per (b, chunk, h): y from the stored start
+//                       state (scores, masked decay weights, two products).
+//   walk_kernel<true>   one block per (b, h), chunks in reverse: the state
+//                       cotangent at each chunk end.
+//   grad_kernel         one block per (b, chunk, head group): every gradient
+//                       of the chunk for the group's heads; the shared rows'
+//                       gradients accumulate over the group's heads in
+//                       registers.
+//   finish_kernel       one block per (b, chunk): sums the groups, adds the
+//                       phase gradient carried from later chunks, and turns
+//                       gamma / scale gradients into dt and trap gradients.
+//   bias_kernel         one block per head: the bias gradients.
+// All arithmetic is float32 (MFMA v_mfma_f32_16x16x4f32).
+#include <hip/hip_runtime.h>
+
+#include "scan3.hpp"
+
+namespace m3 {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ float wave_scan(float x) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o, 64);
+    if (l >= o) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// Sum over the 16 lanes sharing bits 4..5 of the lane index.
+__device__ __forceinline__ float row16_sum(float x) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// acc[j] += A[r0 .. r0+16, kb .. ke) * B[kb .. ke, c0 + 16 j .. +16) for j < jn,
+// with A(r, k) = A[r * AR + k * AK] and B(k, c) = B[k * BK + c * BC] in LDS.
+// Result element acc[j][i] is (row r0 + 4 (lane / 16) + i, column
+// c0 + 16 j + lane % 16).
+template <int J, int AR, int AK, int BK, int BC>
+__device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const float* B, int c0,
+                                    int kb, int ke, int jn = J) {
+  const int l = lane_id(), r = l & 15, q = l >> 4;
+  const float* pa = A + (r0 + r) * AR + q * AK;
+  const float* pb = B + q * BK + (c0 + r) * BC;
+#pragma unroll 2
+  for (int k = kb; k < ke; k += 4) {
+    const float a = pa[k * AK];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (j < jn)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb[k * BK + 16 * j * BC], acc[j], 0, 0,
+                                                      0);
+  }
+}
+
+template <int J>
+__device__ __forceinline__ void zero(f4 (&acc)[J]) {
+#pragma unroll
+  for (int j = 0; j < J; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+}
+
+__device__ __forceinline__ long tok_index(const Shape& s, int b, int t) {
+  return (long)b * s.T + t;
+}
+
+// Per-token scalars of chunk c for head h, one token per lane (lane < 64):
+// p (chunk-local running log decay), e^p, gamma, scale, u = scale e^{p_L - p}
+// and dt, written to LDS arrays of 64.  Padding tokens get zeros (and p
+// equal to the last real token's), so they contribute nothing.
+struct Scalars {
+  float *p, *ep, *gam, *scale, *u, *dt;
+};
+
+__device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
+                              const float* trap, int b, int h, int c, const Scalars& o) {
+  const int l = lane_id(), t = c * C + l;
+  const bool valid = t < s.T, next = t + 1 < s.T;
+  const long i = tok_index(s, b, t) * s.H + h;
+  const float a = valid ? adt[i] : 0.f, d = valid ? dt[i] : 0.f;
+  const float tr = valid ? trap[i] : 0.f;
+  const float dn = next ? dt[i + s.H] : 0.f, trn = next ? trap[i + s.H] : 0.f;
+  const float sig = 1.f / (1.f + expf(-tr)), sign = 1.f / (1.f + expf(-trn));
+  const float gam = d * sig, scale = gam + dn * (1.f - sign);
+  const float p = wave_scan(a), pl = __shfl(p, 63, 64);
+  o.p[l] = p;
+  o.ep[l] = expf(p);
+  o.gam[l] = gam;
+  o.scale[l] = scale;
+  o.u[l] = scale * expf(pl - p);
+  o.dt[l] = d;
+}
+
+// Phase table of chunk c: tab[t * LA + j] = th0[j] + sum_{s <= t} angles_s,j dt_s
+// (j < A), one token per lane, angles split over the four waves.  With
+// `advance`, th0[j] moves to the chunk's end phase (th0 lives in LDS and each
+// j belongs to one wave, whose lanes read it before lane 63 writes it).
+__device__ void phase_table(const Shape& s, const float* ang, const float* dt, int b, int h,
+                            int c, float* th0, float* tab, bool advance) {
+  const int l = lane_id(), w = threadIdx.x >> 6, t = c * C + l;
+  const bool valid = t < s.T;
+  const float d = valid ? dt[tok_index(s, b, t) * s.H + h] : 0.f;
+  for (int j = w; j < s.A; j += 4) {
+    const float x = valid ? ang[tok_index(s, b, t) * s.A + j] * d : 0.f;
+    const float incl = wave_scan(x);
+    const float base = th0[j];
+    tab[l * LA + j] = base + incl;
+    if (advance) {
+      __builtin_amdgcn_wave_barrier();
+      if (l == 63) th0[j] = base + incl;
+    }
+  }
+}
+
+// Rotated rows of chunk c into LDS [C][LQ]: dst[t][n] = rot(src_t + bias, theta_t)[n]
+// for t < C, n < NT, zero for padding tokens and coordinates.  One pair
+// (2j, 2j+1) per lane, tokens split over the waves.  With two sources both
+// are rotated by the same angles.
+template <int NSRC>
+__device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
+                            const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
+                            int b, int c) {
+  const int j = lane_id(), n = 2 * j;
+  const bool col = n < s.N;
+  float2 bs[NSRC];
+#pragma unroll
+  for (int k = 0; k < NSRC; ++k)
+    bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
+  for (int t = threadIdx.x >> 6; t < C; t += 4) {
+    const int tt = c * C + t;
+    const bool valid = col && tt < s.T;
+    float sn = 0.f, cs = 1.f;
+    if (valid && j < s.A) sincosf(tab[t * LA + j], &sn, &cs);
+#pragma unroll
+    for (int k = 0; k < NSRC; ++k) {
+      float2 u = float2{0.f, 0.f};
+      if (valid) {
+        u = *reinterpret_cast<const float2*>(src[k] + tok_index(s, b, tt) * s.N + n);
+        u.x += bs[k].x;
+        u.y += bs[k].y;
+      }
+      const float2 r = float2{u.x * cs - u.y * sn, u.x * sn + u.y * cs};
+      *reinterpret_cast<float2*>(dst[k] + t * LQ + n) = r;
+    }
+  }
+}
+
+// Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
+// row_scale[t] (nullptr: 1); zeros past T and P.
+__device__ void load_values(const Shape& s, const float* src, int b, int c, int h,
+                            const float* row_scale, float* dst) {
+  for (int e = threadIdx.x; e < C * (PT / 4); e += 256) {
+    const int t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
+    f4 v = f4{0.f, 0.f, 0.f, 0.f};
+    if (tt < s.T) {
+      const float* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
+      if (s.P % 4 == 0) {
+        if (p < s.P) v = *reinterpret_cast<const f4*>(row + p);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (p + k < s.P) v[k] = row[p + k];
+      }
+      if (row_scale) v *= row_scale[t];
+    }
+    *reinterpret_cast<f4*>(dst + t * LV + p) = v;
+  }
+}
+
+// A stored [NT][PT] state tile into LDS [NT][LV].
+__device__ void load_state(const float* src, float* dst) {
+  for (int e = threadIdx.x; e < NT * (PT / 4); e += 256) {
+    const int n = e / (PT / 4), p = 4 * (e % (PT / 4));
+    *reinterpret_cast<f4*>(dst + n * LV + p) = *reinterpret_cast<const f4*>(src + n * PT + p);
+  }
+}
+
+__device__ __forceinline__ long state_offset(const Shape& s, int b, int h, int c) {
+  return (((long)b * s.H + h) * s.NC + c) * (long)(NT * PT);
+}
+__device__ __forceinline__ long phase_offset(const Shape& s, int b, int h, int c) {
+  return (((long)b * s.H + h) * s.NC + c) * (long)AM;
+}
+
+// ---------------------------------------------------------------------------
+// State walks.  Forward (BWD = false): rows = keys b with k_bias, vals = x
+// scaled by u; S starts at zero; each chunk stores its start state to
+// `saved`, its start phase to theta0, then S <- e^{p_L} S + K^T (u v).
+// Backward (BWD = true): rows = queries c with q_bias, vals = d_y scaled by
+// e^p; S starts at d_final and the chunks run in reverse; each stores S (the
+// cotangent of the state at the chunk's end) to `saved`, then
+// S <- e^{p_L} S + Q^T (e^p dy).
+// LDS: rows [C][LQ], vals [C][LV], phase table [C][LA], th0 [AM], scalars.
+template <bool BWD>
+__global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, const float* bias,
+                                                   const float* vals, const float* adt,
+                                                   const float* dt, const float* trap,
+                                                   const float* ang, float* theta0, float* saved,
+                                                   const float* init, float* final_state) {
+  extern __shared__ float sm[];
+  float* rt = sm;
+  float* vt = rt + C * LQ;
+  float* tab = vt + C * LV;
+  float* th0 = tab + C * LA;
+  float* sc = th0 + AM;
+  const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
+  const int bh = blockIdx.x, b = bh / s.H, h = bh % s.H;
+  const int tid = threadIdx.x, w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
+
+  // Wave w holds state rows 32 w .. 32 w + 31 as two 16-row strips of four
+  // 16-column tiles.
+  f4 acc[2][4];
+#pragma unroll
+  for (int rt2 = 0; rt2 < 2; ++rt2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = 32 * w + 16 * rt2 + 4 * q + i, p = 16 * j + r;
+        float v = 0.f;
+        if (BWD && init && n < s.N && p < s.P) v = init[(((long)b * s.H + h) * s.N + n) * s.P + p];
+        acc[rt2][j][i] = v;
+      }
+    }
+  }
+  if (!BWD && tid < AM) th0[tid] = 0.f;
+  const float* const src[2] = {rows, rows};
+  const float* const bsrc[2] = {bias + (long)h * s.N, bias + (long)h * s.N};
+  float* const dst[2] = {rt, rt};
+
+  for (int step = 0; step < s.NC; ++step) {
+    const int c = BWD ? s.NC - 1 - step : step;
+    __syncthreads();  // the previous chunk's reads of the LDS tiles are done
+    if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
+    if (BWD) {
+      if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
+    } else {
+      if (tid < s.A) theta0[phase_offset(s, b, h, c) + tid] = th0[tid];
+    }
+    __syncthreads();
+    phase_table(s, ang, dt, b, h, c, th0, tab, !BWD);
+    __syncthreads();
+    rotate_rows<1>(s, src, bsrc, dst, tab, b, c);
+    load_values(s, vals, b, c, h, BWD ? S.ep : S.u, vt);
+    // Store this chunk's state (a lane's four rows of one column).
+    float* out = saved + state_offset(s, b, h, c);
+#pragma unroll
+    for (int rt2 = 0; rt2 < 2; ++rt2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          out[(32 * w + 16 * rt2 + 4 * q + i) * PT + 16 * j + r] = acc[rt2][j][i];
+    __syncthreads();
+    const float decay = expf(S.p[63]);
+#pragma unroll
+    for (int rt2 = 0; rt2 < 2; ++rt2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[rt2][j] *= decay;
+      // rows^T vals: A(n, t) = rt[t * LQ + n], B(t, p) = vt[t * LV + p].
+      mma<4, 1, LQ, LV, 1>(acc[rt2], rt, 32 * w + 16 * rt2, vt, 0, 0, C);
+    }
+  }
+  if (!BWD && final_state) {
+#pragma unroll
+    for (int rt2 = 0; rt2 < 2; ++rt2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = 32 * w + 16 * rt2 + 4 * q + i, p = 16 * j + r;
+          if (n < s.N && p < s.P)
+            final_state[(((long)b * s.H + h) * s.N + n) * s.P + p] = acc[rt2][j][i];
+        }
+  }
+}
+
+// Block index -> (b, chunk, h), heads fastest.  Consecutive blocks land on
+// different XCDs (round robin over 8); the remap gives each XCD a contiguous
+// run of (b, chunk) pairs, so the heads of one chunk share its rows in one L2.
+__device__ __forceinline__ int xcd_block(int total) {
+  const int id = blockIdx.x;
+  if (total % 8) return id;
+  return (id % 8) * (total / 8) + id / 8;
+}
+
+// ---------------------------------------------------------------------------
+// Output of one (b, chunk, h): y = (S o W) V + diag(e^p) Q S0 with scores
+// S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
+// LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 [NT][LV] (first the
+// phase table), V [C][LV], scalars.
+__global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, const float* bk,
+                                                  const float* x, const float* adt,
+                                                  const float* dt, const float* trap,
+                                                  const float* ang, const float* qb,
+                                                  const float* kb, const float* theta0,
+                                                  const float* starts, float* y) {
+  extern __shared__ float sm[];
+  float* qt = sm;
+  float* kt = qt + C * LQ;
+  float* h0 = kt + C * LQ;
+  float* tab = h0;
+  float* vt = h0 + NT * LV;
+  float* th0 = vt + C * LV;
+  float* sc = th0 + AM;
+  const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
+  const int total = s.B * s.NC * s.H, id = xcd_block(total);
+  const int h = id % s.H, c = (id / s.H) % s.NC, b = id / (s.H * s.NC);
+  const int tid = threadIdx.x, w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
+
+  if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
+  if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
+  __syncthreads();
+  phase_table(s, ang, dt, b, h, c, th0, tab, false);
+  __syncthreads();
+  {
+    const float* const src[2] = {cq, bk};
+    const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
+    float* const dst[2] = {qt, kt};
+    rotate_rows<2>(s, src, bsrc, dst, tab, b, c);
+  }
+  __syncthreads();
+  load_state(starts + state_offset(s, b, h, c), h0);
+  load_values(s, x, b, c, h, nullptr, vt);
+  __syncthreads();
+
+  f4 sco[4], qh[4];
+  zero(sco);
+  zero(qh);
+  mma<4, LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
+  mma<4, LQ, 1, LV, 1>(qh, qt, 16 * w, h0, 0, 0, NT);
+  __syncthreads();  // every wave is done with K
+  float* gs = kt;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j > w) break;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * q + i, u = 16 * j + r;
+      float wt = 0.f;
+      if (t > u) wt = expf(fminf(S.p[t] - S.p[u], 0.f)) * S.scale[u];
+      else if (t == u) wt = S.gam[t];
+      gs[t * LV + u] = sco[j][i] * wt;
+    }
+  }
+  // Each wave reads only its own rows of S o W.
+  f4 acc[4];
+  zero(acc);
+  mma<4, LV, 1, LV, 1>(acc, gs, 16 * w, vt, 0, 0, 16 * (w + 1));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * q + i, p = 16 * j + r, tt = c * C + t;
+      if (tt < s.T && p < s.P)
+        y[(tok_index(s, b, tt) * s.H + h) * s.P + p] = acc[j][i] + S.ep[t] * qh[j][i];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gradients of one (b, chunk) for the heads of group g.  Per head, with
+// G = dS o W (dS = dY V^T), the chunk's start state H0 and end cotangent dH1:
+//   dQ = G K + diag(e^p) dY H0^T          dK = G^T Q + diag(u) V dH1^T
+//   dV = (S o W)^T dY + diag(u) K dH1
+//   dgamma_t = S_tt dS_tt;  with F_ts = S_ts dS_ts e^{p_t - p_s} (s < t):
+//   dscale_s = sum_t F_ts + e^{p_L - p_s} g_s,  g_s = v_s . (K dH1)_s
+//   dp_t = sum_s F_ts scale_s - sum_t' F_t't scale_t + e^{p_t} dy_t . (Q H0)_t
+//          - u_t g_t + [t = last] (sum_s u_s g_s + e^{p_L} <dH1, H0>)
+//   d adt_s = sum_{t >= s} dp_t (within the chunk)
+// then the rotation's transpose (dq -> d(c + qb)) and the phase gradient
+// dtheta_t,j = dq_{2j+1} q_{2j} - dq_{2j} q_{2j+1} (+ the same for k), summed
+// from the end of the chunk: R_t = sum_{t' >= t} dtheta_t'.
+// LDS: R1 = 2 NT LV floats (Q, K; later H0, dH1; later dQ, dK), R2 = 2 NT LV
+// floats (H0, dH1; later V, dY, S o W, G), phase table [C][LA], scalars.
+__global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const float* cq,
+                                                   const float* bk, const float* x,
+                                                   const float* adt, const float* dt,
+                                                   const float* trap, const float* ang,
+                                                   const float* qb, const float* kb,
+                                                   const float* theta0, const float* starts,
+                                                   const float* dh1, const float* dy, GradOut o) {
+  extern __shared__ float sm[];
+  float* R1 = sm;
+  float* R2 = R1 + 2 * NT * LV;
+  float* tab = R2 + 2 * NT * LV;
+  float* th0 = tab + C * LA;
+  float* sc = th0 + AM;
+  const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
+  float* s_rowE = sc + 384;
+  float* s_colF = sc + 448;
+  float* s_colE = sc + 512;
+  float* s_qd = sc + 576;
+  float* s_g = sc + 640;
+  float* s_dgd = sc + 704;
+  float* s_ddt = sc + 768;
+  float* qbacc = sc + 832;
+  float* kbacc = qbacc + NT;
+  float* hsum = kbacc + NT;
+
+  const int total = s.B * s.NC * groups, id = xcd_block(total);
+  const int g = id % groups, c = (id / groups) % s.NC, b = id / (groups * s.NC);
+  const int hpg = (s.H + groups - 1) / groups, h_begin = g * hpg;
+  const int h_end = min(s.H, h_begin + hpg);
+  const int tid = threadIdx.x, w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
+  const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
+
+  // This group's sums over its heads accumulate in its own slices of
+  // dc_part, db_part and dang_part: every element belongs to one thread, which
+  // writes it for the group's first head and adds to it for the others.
+  const long tp = (long)s.NC * C;
+  float* dcp = o.dc_part + ((long)g * s.B + b) * tp * NT;
+  float* dbp = o.db_part + ((long)g * s.B + b) * tp * NT;
+  float* dap = o.dang_part + ((long)g * s.B + b) * tp * AM;
+
+  for (int h = h_begin; h < h_end; ++h) {
+    const bool first = h == h_begin;
+    __syncthreads();  // the previous head is done with every LDS array
+    if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
+    if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
+    if (tid < 64) {
+      s_colF[tid] = 0.f;
+      s_colE[tid] = 0.f;
+      s_ddt[tid] = 0.f;
+    }
+    if (tid < NT) {
+      qbacc[tid] = 0.f;
+      kbacc[tid] = 0.f;
+    }
+    if (tid == 0) hsum[0] = 0.f;
+    __syncthreads();
+    phase_table(s, ang, dt, b, h, c, th0, tab, false);
+    __syncthreads();
+    float* qt = R1;
+    float* kt = R1 + C * LQ;
+    {
+      const float* const src[2] = {cq, bk};
+      const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
+      float* const dst[2] = {qt, kt};
+      rotate_rows<2>(s, src, bsrc, dst, tab, b, c);
+    }
+    float* h0 = R2;
+    float* g1 = R2 + NT * LV;
+    load_state(starts + state_offset(s, b, h, c), h0);
+    load_state(dh1 + state_offset(s, b, h, c), g1);
+    __syncthreads();
+
+    // Q H0, K dH1 and the scores (wave w: rows 16 w .. 16 w + 15).
+    f4 sco[4], qh[4], kg[4];
+    zero(sco);
+    zero(qh);
+    zero(kg);
+    mma<4, LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
+    mma<4, LQ, 1, LV, 1>(qh, qt, 16 * w, h0, 0, 0, NT);
+    mma<4, LQ, 1, LV, 1>(kg, kt, 16 * w, g1, 0, 0, NT);
+    {
+      float part = 0.f;
+      for (int e = tid; e < NT * PT; e += 256) {
+        const int n = e / PT, p = e % PT;
+        part += h0[n * LV + p] * g1[n * LV + p];
+      }
+      part = wave_sum(part);
+      if (l == 0) atomicAdd(hsum, part);
+    }
+    __syncthreads();
+    float* vt = R2;
+    float* dyt = R2 + C * LV;
+    float* gs = R2 + 2 * C * LV;
+    float* gm = R2 + 3 * C * LV;
+    load_values(s, x, b, c, h, nullptr, vt);
+    load_values(s, dy, b, c, h, nullptr, dyt);
+    __syncthreads();
+
+    f4 dsc[4];
+    zero(dsc);
+    // dY V^T: A(t, p) = dY[t * LV + p], B(p, s) = V[s * LV + p].
+    mma<4, LV, 1, 1, LV>(dsc, dyt, 16 * w, vt, 0, 0, PT, w + 1);
+    {
+      float qd[4] = {0.f, 0.f, 0.f, 0.f}, gg[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * w + 4 * q + i, p = 16 * j + r;
+          qd[i] += qh[j][i] * dyt[t * LV + p];
+          gg[i] += kg[j][i] * vt[t * LV + p];
+        }
+      float rowE[4] = {0.f, 0.f, 0.f, 0.f};
+      float colF[4] = {0.f, 0.f, 0.f, 0.f}, colE[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j > w) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = 16 * w + 4 * q + i, u = 16 * j + r;
+            gs[t * LV + u] = 0.f;
+            gm[t * LV + u] = 0.f;
+          }
+          continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * w + 4 * q + i, u = 16 * j + r;
+          const float st = sco[j][i], ds = dsc[j][i];
+          float wt = 0.f;
+          if (t > u) {
+            const float dec = expf(fminf(S.p[t] - S.p[u], 0.f));
+            const float f = st * ds * dec;
+            wt = dec * S.scale[u];
+            rowE[i] += f * S.scale[u];
+            colF[j] += f;
+            colE[j] += f * S.scale[u];
+          } else if (t == u) {
+            wt = S.gam[t];
+            s_dgd[t] = st * ds;
+          }
+          gs[t * LV + u] = st * wt;
+          gm[t * LV + u] = ds * wt;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = row16_sum(qd[i]), bb = row16_sum(gg[i]), e = row16_sum(rowE[i]);
+        if (r == 0) {
+          const int t = 16 * w + 4 * q + i;
+          s_qd[t] = a;
+          s_g[t] = bb;
+          s_rowE[t] = e;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j > w) break;
+        float f = colF[j], e = colE[j];
+        f += __shfl_xor(f, 16, 64);
+        f += __shfl_xor(f, 32, 64);
+        e += __shfl_xor(e, 16, 64);
+        e += __shfl_xor(e, 32, 64);
+        if (q == 0) {
+          atomicAdd(&s_colF[16 * j + r], f);
+          atomicAdd(&s_colE[16 * j + r], e);
+        }
+      }
+    }
+    __syncthreads();
+
+    f4 dq[8], dk[8], dv[4];
+    zero(dq);
+    zero(dk);
+    zero(dv);
+    // G K: A(t, s) = G[t * LV + s], B(s, n) = K[s * LQ + n].
+    mma<8, LV, 1, LQ, 1>(dq, gm, 16 * w, kt, 0, 0, 16 * (w + 1));
+    // G^T Q: A(s, t) = G[t * LV + s], B(t, n) = Q[t * LQ + n].
+    mma<8, 1, LV, LQ, 1>(dk, gm, 16 * w, qt, 0, 16 * w, C);
+    // (S o W)^T dY.
+    mma<4, 1, LV, LV, 1>(dv, gs, 16 * w, dyt, 0, 16 * w, C);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * q + i, p = 16 * j + r, tt = c * C + t;
+        if (tt < s.T && p < s.P)
+          o.dx[(tok_index(s, b, tt) * s.H + h) * s.P + p] = dv[j][i] + S.u[t] * kg[j][i];
+      }
+    __syncthreads();  // Q, K, S o W and G are no longer read
+    for (int e = tid; e < C * PT; e += 256) {
+      const int t = e / PT, p = e % PT;
+      dyt[t * LV + p] *= S.ep[t];
+      vt[t * LV + p] *= S.u[t];
+    }
+    load_state(starts + state_offset(s, b, h, c), R1);
+    load_state(dh1 + state_offset(s, b, h, c), R1 + NT * LV);
+    __syncthreads();
+    // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0[n * LV + p].
+    mma<8, LV, 1, 1, LV>(dq, dyt, 16 * w, R1, 0, 0, PT);
+    mma<8, LV, 1, 1, LV>(dk, vt, 16 * w, R1 + NT * LV, 0, 0, PT);
+    __syncthreads();
+    float* dqt = R1;
+    float* dkt = R1 + C * LQ;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * q + i, n = 16 * j + r;
+        dqt[t * LQ + n] = dq[j][i];
+        dkt[t * LQ + n] = dk[j][i];
+      }
+    __syncthreads();
+
+    // Through the rotations: one pair per lane, tokens w, w + 4, ...
+    {
+      const bool col = n2 < s.N;
+      float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
+      if (col) {
+        bq = *reinterpret_cast<const float2*>(qb + (long)h * s.N + n2);
+        bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
+      }
+      float2 sq = float2{0.f, 0.f}, sk = float2{0.f, 0.f};
+#pragma unroll 1
+      for (int m = 0; m < 16; ++m) {
+        const int t = w + 4 * m, tt = c * C + t;
+        if (!col || tt >= s.T) {
+          if (first) {
+            *reinterpret_cast<float2*>(dcp + (c * C + t) * NT + n2) = float2{0.f, 0.f};
+            *reinterpret_cast<float2*>(dbp + (c * C + t) * NT + n2) = float2{0.f, 0.f};
+          }
+          continue;
+        }
+        const float2 gq = *reinterpret_cast<const float2*>(dqt + t * LQ + n2);
+        const float2 gk = *reinterpret_cast<const float2*>(dkt + t * LQ + n2);
+        float2 duq = gq, duk = gk;
+        if (l < s.A) {
+          float sn, cs;
+          sincosf(tab[t * LA + l], &sn, &cs);
+          float2 uq = *reinterpret_cast<const float2*>(cq + tok_index(s, b, tt) * s.N + n2);
+          float2 uk = *reinterpret_cast<const float2*>(bk + tok_index(s, b, tt) * s.N + n2);
+          uq.x += bq.x;
+          uq.y += bq.y;
+          uk.x += bkv.x;
+          uk.y += bkv.y;
+          const float q0 = uq.x * cs - uq.y * sn, q1 = uq.x * sn + uq.y * cs;
+          const float k0 = uk.x * cs - uk.y * sn, k1 = uk.x * sn + uk.y * cs;
+          tab[t * LA + l] = gq.y * q0 - gq.x * q1 + gk.y * k0 - gk.x * k1;
+          duq = float2{gq.x * cs + gq.y * sn, -gq.x * sn + gq.y * cs};
+          duk = float2{gk.x * cs + gk.y * sn, -gk.x * sn + gk.y * cs};
+        }
+        float2* pc = reinterpret_cast<float2*>(dcp + (c * C + t) * NT + n2);
+        float2* pb = reinterpret_cast<float2*>(dbp + (c * C + t) * NT + n2);
+        if (first) {
+          *pc = duq;
+          *pb = duk;
+        } else {
+          const float2 a = *pc, e = *pb;
+          *pc = float2{a.x + duq.x, a.y + duq.y};
+          *pb = float2{e.x + duk.x, e.y + duk.y};
+        }
+        sq.x += duq.x;
+        sq.y += duq.y;
+        sk.x += duk.x;
+        sk.y += duk.y;
+      }
+      if (col) {
+        atomicAdd(&qbacc[n2], sq.x);
+        atomicAdd(&qbacc[n2 + 1], sq.y);
+        atomicAdd(&kbacc[n2], sk.x);
+        atomicAdd(&kbacc[n2 + 1], sk.y);
+      }
+    }
+    __syncthreads();
+    // Phase gradients summed from the chunk's end (one token per lane).
+    {
+      const int tt = c * C + l;
+      const bool valid = tt < s.T;
+      float ddt = 0.f;
+#pragma unroll 1
+      for (int m = 0; m < 16; ++m) {
+        const int j = w + 4 * m;
+        if (j >= s.A) break;
+        const float xv = valid ? tab[l * LA + j] : 0.f;
+        const float incl = wave_scan(xv), tot = __shfl(incl, 63, 64);
+        const float R = tot - incl + xv;
+        float* pa = dap + (c * C + l) * AM + j;
+        *pa = (first ? 0.f : *pa) + R * S.dt[l];
+        if (valid) ddt += R * ang[tok_index(s, b, tt) * s.A + j];
+        if (l == 0) o.D[phase_offset(s, b, h, c) + j] = R;
+      }
+      atomicAdd(&s_ddt[l], ddt);
+    }
+    if (tid < NT) {
+      const long at = (((long)b * s.NC + c) * s.H + h) * NT + tid;
+      o.qb_part[at] = qbacc[tid];
+      o.kb_part[at] = kbacc[tid];
+    }
+    __syncthreads();
+    if (w == 0) {
+      const int tt = c * C + l;
+      const float pl = S.p[63];
+      const float ug = wave_sum(S.u[l] * s_g[l]);
+      float dp = s_rowE[l] - s_colE[l] + S.ep[l] * s_qd[l] - S.u[l] * s_g[l];
+      if (l == 63) dp += ug + expf(pl) * hsum[0];
+      const float dscale = s_colF[l] + expf(pl - S.p[l]) * s_g[l];
+      const float incl = wave_scan(dp), tot = __shfl(incl, 63, 64);
+      const float dadt = tot - incl + dp;
+      if (tt < s.T) {
+        const long i = tok_index(s, b, tt) * s.H + h;
+        o.d_adt[i] = dadt;
+        o.dgam[i] = s_dgd[l] + dscale;
+        o.dscale[i] = dscale;
+        o.ddt_loc[i] = s_ddt[l];
+      }
+    }
+  }
+
+}
+
+// ---------------------------------------------------------------------------
+// Per (b, chunk): phase gradients carried from later chunks, the group sums,
+// and the dt / trap gradients (gamma = dt sigma, prev = dt (1 - sigma);
+// scale_t = gamma_t + prev_{t+1}, so d prev_t = d scale_{t-1}).
+__global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const float* dt,
+                                                     const float* trap, const float* ang,
+                                                     GradOut o, float* d_c, float* d_b,
+                                                     float* d_dt, float* d_trap,
+                                                     float* d_angles) {
+  extern __shared__ float suf[];  // [H][AM]
+  const int b = blockIdx.x / s.NC, c = blockIdx.x % s.NC, tid = threadIdx.x;
+  for (int e = tid; e < s.H * s.A; e += 256) {
+    const int h = e / s.A, j = e % s.A;
+    float acc = 0.f;
+    for (int cc = c + 1; cc < s.NC; ++cc) acc += o.D[phase_offset(s, b, h, cc) + j];
+    suf[h * AM + j] = acc;
+  }
+  __syncthreads();
+  const long tp = (long)s.NC * C;
+  for (int e = tid; e < C * s.H; e += 256) {
+    const int t = e / s.H, h = e % s.H, tt = c * C + t;
+    if (tt >= s.T) continue;
+    const long i = tok_index(s, b, tt) * s.H + h;
+    const float d = dt[i], sig = 1.f / (1.f + expf(-trap[i]));
+    const float dg = o.dgam[i], dprev = tt > 0 ? o.dscale[i - s.H] : 0.f;
+    float carried = 0.f;
+    for (int j = 0; j < s.A; ++j) carried += suf[h * AM + j] * ang[tok_index(s, b, tt) * s.A + j];
+    d_dt[i] = dg * sig + dprev * (1.f - sig) + o.ddt_loc[i] + carried;
+    d_trap[i] = (dg - dprev) * d * sig * (1.f - sig);
+  }
+  for (int e = tid; e < C * s.A; e += 256) {
+    const int t = e / s.A, j = e % s.A, tt = c * C + t;
+    if (tt >= s.T) continue;
+    float acc = 0.f;
+    for (int g = 0; g < groups; ++g) acc += o.dang_part[(((long)g * s.B + b) * tp + tt) * AM + j];
+    for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dt[tok_index(s, b, tt) * s.H + h];
+    d_angles[tok_index(s, b, tt) * s.A + j] = acc;
+  }
+  for (int e = tid; e < C * s.N; e += 256) {
+    const int t = e / s.N, n = e % s.N, tt = c * C + t;
+    if (tt >= s.T) continue;
+    float ac = 0.f, ab = 0.f;
+    for (int g = 0; g < groups; ++g) {
+      const long at = (((long)g * s.B + b) * tp + tt) * NT + n;
+      ac += o.dc_part[at];
+      ab += o.db_part[at];
+    }
+    d_c[tok_index(s, b, tt) * s.N + n] = ac;
+    d_b[tok_index(s, b, tt) * s.N + n] = ab;
+  }
+}
+
+// Bias gradients: sums over (b, chunk) of the per-head partials.
+__global__ __launch_bounds__(128) void bias_kernel(Shape s, GradOut o, float* d_qb, float* d_kb) {
+  const int h = blockIdx.x, n = threadIdx.x;
+  if (n >= s.N) return;
+  float aq = 0.f, ak = 0.f;
+  for (int bc = 0; bc < s.B * s.NC; ++bc) {
+    const long at = ((long)bc * s.H + h) * NT + n;
+    aq += o.qb_part[at];
+    ak += o.kb_part[at];
+  }
+  d_qb[(long)h * s.N + n] = aq;
+  d_kb[(long)h * s.N + n] = ak;
+}
+
+template __global__ void walk_kernel<false>(Shape, const float*, const float*, const float*,
+                                            const float*, const float*, const float*,
+                                            const float*, float*, float*, const float*, float*);
+template __global__ void walk_kernel<true>(Shape, const float*, const float*, const float*,
+                                           const float*, const float*, const float*,
+                                           const float*, float*, float*, const float*, float*);
+
+}  // namespace m3

@@ -1,0 +1,56 @@
+// Shapes and kernel declarations of the gfx950 Mamba-3 scan (scan3.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace m3 {
+
+constexpr int C = 64;       // tokens per chunk (one per lane of a wave)
+constexpr int NT = 128;     // state rows held (N <= NT; padding is zero)
+constexpr int PT = 64;      // value columns held (P <= PT; padding is zero)
+constexpr int AM = 64;      // angle slots (A <= N / 2 <= AM)
+constexpr int LQ = NT + 4;  // LDS row stride of [C][NT] tiles
+constexpr int LV = PT + 4;  // LDS row stride of [C][PT], [C][C] and [NT][PT] tiles
+constexpr int LA = AM + 1;  // LDS row stride of [C][AM] phase tables
+
+// B batch, T tokens, H heads, N state width, P value width, A angle rates,
+// NC = ceil(T / C) chunks.
+struct Shape {
+  int B, T, H, N, P, A, NC;
+};
+
+// Outputs and per-chunk partials of grad_kernel (workspace except dx, d_adt).
+struct GradOut {
+  float* dx;        // [B,T,H*P]
+  float* d_adt;     // [B,T,H]
+  float* dgam;      // [B,T,H]  gradient of gamma (diagonal weight and scale)
+  float* dscale;    // [B,T,H]  gradient of scale alone
+  float* ddt_loc;   // [B,T,H]  phase gradient through dt within the chunk
+  float* D;         // [B,H,NC,AM] phase-gradient total of each chunk
+  float* qb_part;   // [B,NC,H,NT] query-bias gradient of each chunk
+  float* kb_part;   // [B,NC,H,NT]
+  float* dc_part;   // [G,B,NC*C,NT] query-row gradient of each head group
+  float* db_part;   // [G,B,NC*C,NT]
+  float* dang_part; // [G,B,NC*C,AM] angle gradient (chunk-local part)
+};
+
+// LDS bytes of each kernel.
+constexpr size_t kWalkLds = (size_t)(C * LQ + C * LV + C * LA + AM + 384) * sizeof(float);
+constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
+constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1096) * sizeof(float);
+
+template <bool BWD>
+__global__ void walk_kernel(Shape, const float*, const float*, const float*, const float*,
+                            const float*, const float*, const float*, float*, float*,
+                            const float*, float*);
+__global__ void out_kernel(Shape, const float*, const float*, const float*, const float*,
+                           const float*, const float*, const float*, const float*, const float*,
+                           const float*, const float*, float*);
+__global__ void grad_kernel(Shape, int, const float*, const float*, const float*, const float*,
+                            const float*, const float*, const float*, const float*, const float*,
+                            const float*, const float*, const float*, const float*, GradOut);
+__global__ void finish_kernel(Shape, int, const float*, const float*, const float*, GradOut,
+                              float*, float*, float*, float*, float*);
+__global__ void bias_kernel(Shape, GradOut, float*, float*);
+
+}  // namespace m3
