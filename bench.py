@@ -31,8 +31,15 @@ config-2 shape through the fused entry point (m4mr_mixer_forward: prologue,
 memory read and read gating in one pass over the raw projections); the same
 forward through the three separate entry points is timed beside it.
 
+With --workload mamba3 a step is the FlashMamba Mamba-3 scan (mamba3_fused,
+lm/kernels/flashmamba.py:1125-1162) forward and backward at the 125M model's
+Mamba-3 mixer shape (B=16, L=1024, H=24 heads of P=64, N=128, A=32 angle
+rates; lm/configs/mamba4-125m.json), fp32, through m3s_forward /
+m3s_backward; the roofline is the dominant kernel's MFMA rate against the
+fp32 peak.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload config2|config3|config4|mixer|mixer_read]
+                       [--workload config2|config3|config4|mixer|mixer_read|mamba3]
 """
 
 import argparse
@@ -139,7 +146,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--chunk", type=int, default=64)
     p.add_argument("--workload", default="config2",
-                   choices=["config2", "config3", "config4", "mixer", "mixer_read"])
+                   choices=["config2", "config3", "config4", "mixer", "mixer_read", "mamba3"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -664,6 +671,145 @@ def main_mixer_read(args):
     print(json.dumps(line), flush=True)
 
 
+MAMBA3_METRIC = ("Mamba-3 fused scan fwd+bwd tokens/sec at B16 L1024 H24 P64 N128 A32 "
+                 "(125M mixer shape); % fp32 MFMA peak")
+# Algorithmic flop per (chunk of 64 tokens, head) of each scan kernel at
+# N = 128, P = 64: 2 flop per multiply-add of the products the algorithm
+# needs, causal products counted over the 2080 (t, s <= t) pairs only.
+MAMBA3_FLOP = {
+    "m3_walk": 2 * 128 * 64 * 64,                                # K^T (u V)
+    "m3_out": 2 * (2080 * 128 + 64 * 128 * 64 + 2080 * 64),      # Q K^T, Q S0, (S o W) V
+    "m3_walk_bwd": 2 * 128 * 64 * 64,                            # Q^T (e^p dY)
+    "m3_grad": 2 * (3 * 2080 * 128 + 4 * 64 * 128 * 64 + 2 * 2080 * 64),
+}
+
+
+def mamba3_cpu_baseline(host):
+    """oracle.mamba3 (float64 NumPy) forward and backward on batch row 0."""
+    from oracle import mamba3 as oracle
+
+    row = {n: (v[:1] if n not in ("q_bias", "k_bias") else v) for n, v in host.items()
+           if n != "d_y"}
+    start = time.perf_counter()
+    oracle.forward(*(row[n] for n in oracle.ARGS))
+    oracle.backward(*(row[n] for n in oracle.ARGS), host["d_y"][:1], None)
+    seconds = time.perf_counter() - start
+    _, T, H = row["dt"].shape
+    return {
+        "value": T / seconds,
+        "unit": "tokens/s",
+        "cores": int(os.environ.get("OPENBLAS_NUM_THREADS", CORES)),
+        "kind": "port",
+        "sample": (f"oracle.mamba3 fwd+bwd in float64 NumPy on batch row 0 of the workload "
+                   f"(B=1, L={T}, H={H}; 1/16 of the step), {seconds:.1f} s"),
+    }
+
+
+def main_mamba3(args):
+    import torch
+
+    from mamba4_amd import _lib
+    from oracle import mamba3 as oracle
+
+    lib = _lib.load()
+    check = _lib.check
+    B, T, H, N, P, A = 16, 1024, 24, 128, 64, 32
+    NC = (T + 63) // 64
+    host = oracle.inputs(batch=B, length=T, heads=H, dim=N, width=P, angle_count=A, seed=0)
+    host["d_y"] = np.random.default_rng(1).normal(size=host["x"].shape)
+    dev = {n: torch.tensor(np.asarray(v, np.float32), device="cuda:0") for n, v in host.items()}
+    f32 = dict(dtype=torch.float32, device="cuda:0")
+    y = torch.empty(B, T, H * P, **f32)
+    final = torch.empty(B, H, N, P, **f32)
+    starts = torch.empty(B, H, NC, 8192, **f32)
+    phases = torch.empty(B, H, NC, 64, **f32)
+    grads = [torch.empty_like(dev[n]) for n in oracle.ARGS]
+    nbytes = lib.m3s_backward_workspace_bytes(B, T, H, N, P, A)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    ins = [dev[n].data_ptr() for n in oracle.ARGS]
+    dims = (B, T, H, N, P, A)
+
+    def step():
+        check(lib.m3s_forward(*ins, *dims, y.data_ptr(), final.data_ptr(), starts.data_ptr(),
+                              phases.data_ptr(), st))
+        check(lib.m3s_backward(*ins, *dims, starts.data_ptr(), phases.data_ptr(),
+                               dev["d_y"].data_ptr(), None, *(g.data_ptr() for g in grads),
+                               ws.data_ptr(), nbytes, st))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_select(None)
+    _lib.profile_enable(True)
+    for _ in range(min(args.steps, 10)):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    kernel_ms = {}
+    for name in _lib.kernel_names():
+        total, count = _lib.profile_read(name)
+        if count:
+            kernel_ms[name] = total / count
+    _lib.profile_reset()
+    dominant = max(MAMBA3_FLOP, key=lambda k: kernel_ms.get(k, 0.0))
+    # Timed region: events only on the dominant kernel's launches.
+    _lib.profile_select(dominant)
+    _lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    seconds = (time.perf_counter() - t0) / args.steps
+    _lib.profile_enable(False)
+    total, count = _lib.profile_read(dominant)
+    _lib.profile_reset()
+    _lib.profile_select(None)
+    dom_ms = total / count
+    units = B * NC * H
+    achieved = MAMBA3_FLOP[dominant] * units / (dom_ms / 1e3) / 1e12
+    kernels = {}
+    for name, flop in MAMBA3_FLOP.items():
+        ms = kernel_ms.get(name)
+        if ms:
+            rate = flop * units / (ms / 1e3) / 1e12
+            kernels[name] = {"ms": ms, "TFLOPs": rate, "frac": rate / FP32_PEAK_TFLOPS}
+    line = {
+        "metric": MAMBA3_METRIC,
+        "value": B * T / seconds,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": seconds * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "mamba3 scan fwd+bwd, B=16 L=1024 H=24 P=64 N=128 A=32 fp32",
+                   "batch": B, "seq_len": T, "heads": H, "state_dim": N, "head_dim": P,
+                   "angles": A},
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / FP32_PEAK_TFLOPS,
+            "traffic": None,
+            "algorithmic_flop": MAMBA3_FLOP[dominant] * units,
+        },
+        "kernels": kernels,
+        "kernel_ms": kernel_ms,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = mamba3_cpu_baseline(host)
+    print(json.dumps(line), flush=True)
+
+
 def copy_bandwidth_gbps():
     """Read+write bandwidth of a 2 GiB device-to-device copy (torch copy_)."""
     import torch
@@ -736,6 +882,8 @@ def main():
         return main_mixer_read(args)
     if args.workload == "mixer":
         return main_mixer(args)
+    if args.workload == "mamba3":
+        return main_mamba3(args)
     data = workload_inputs(args.workload, seed=0, cotangents=True)
     problem = Problem(data, args.chunk, bf16_inputs=args.workload == "config3")
     B, T, H = problem.B, problem.T, problem.H
