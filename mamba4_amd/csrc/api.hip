@@ -1109,7 +1109,7 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
   });
   if (rc) return rc;
   return launch("m3_bias", st, [&] {
-    hipLaunchKernelGGL(m3::bias_kernel, dim3(H), dim3(128), 0, st, s, o, d_q_bias, d_k_bias);
+    hipLaunchKernelGGL(m3::bias_kernel, dim3(H), dim3(1024), 0, st, s, o, d_q_bias, d_k_bias);
   });
 }
 

@@ -38,7 +38,15 @@ namespace m3 {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// The thread index through an empty asm: values derived from it cannot be
+// hoisted out of the kernels' chunk and head loops, so index arithmetic is
+// recomputed per iteration instead of occupying registers across the loop.
+__device__ __forceinline__ int tix() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int lane_id() { return tix() & 63; }
 
 __device__ __forceinline__ float wave_scan(float x) {
   const int l = lane_id();
@@ -63,24 +71,43 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Four consecutive-in-k operand values: one 16-byte LDS read when the
+// operand is contiguous along k (stride 1), four reads otherwise.
+template <int STRIDE>
+__device__ __forceinline__ f4 load_k4(const float* p) {
+  if constexpr (STRIDE == 1) {
+    return *reinterpret_cast<const f4*>(p);
+  } else {
+    return f4{p[0], p[STRIDE], p[2 * STRIDE], p[3 * STRIDE]};
+  }
+}
+
 // acc[j] += A[r0 .. r0+16, kb .. ke) * B[kb .. ke, c0 + 16 j .. +16) for j < jn,
-// with A(r, k) = A[r * AR + k * AK] and B(k, c) = B[k * BK + c * BC] in LDS.
-// Result element acc[j][i] is (row r0 + 4 (lane / 16) + i, column
-// c0 + 16 j + lane % 16).
+// with A(r, k) = A[r * AR + k * AK] and B(k, c) = B[k * BK + c * BC] in LDS;
+// kb and ke are multiples of 16.  Result element acc[j][i] is (row
+// r0 + 4 (lane / 16) + i, column c0 + 16 j + lane % 16).  Within each block
+// of 16 k the lanes of group q = lane / 16 take k = 4 q + e at MFMA step e
+// (the same assignment for A and B, so the sum is unchanged), which makes a
+// lane's four A (or B) values of the block contiguous when AK (BK) is 1.
+// All of a block's operands are read before its 4 J MFMAs issue.
 template <int J, int AR, int AK, int BK, int BC>
 __device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const float* B, int c0,
                                     int kb, int ke, int jn = J) {
   const int l = lane_id(), r = l & 15, q = l >> 4;
-  const float* pa = A + (r0 + r) * AR + q * AK;
-  const float* pb = B + q * BK + (c0 + r) * BC;
+  const float* pa = A + (r0 + r) * AR + 4 * q * AK;
+  const float* pb = B + 4 * q * BK + (c0 + r) * BC;
 #pragma unroll 2
-  for (int k = kb; k < ke; k += 4) {
-    const float a = pa[k * AK];
+  for (int k = kb; k < ke; k += 16) {
+    const f4 a = load_k4<AK>(pa + k * AK);
+    f4 b[J];
 #pragma unroll
     for (int j = 0; j < J; ++j)
-      if (j < jn)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pb[k * BK + 16 * j * BC], acc[j], 0, 0,
-                                                      0);
+      if (j < jn) b[j] = load_k4<BK>(pb + k * BK + 16 * j * BC);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (j < jn) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
   }
 }
 
@@ -127,12 +154,20 @@ __device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
 // j belongs to one wave, whose lanes read it before lane 63 writes it).
 __device__ void phase_table(const Shape& s, const float* ang, const float* dt, int b, int h,
                             int c, float* th0, float* tab, bool advance) {
-  const int l = lane_id(), w = threadIdx.x >> 6, t = c * C + l;
+  const int l = lane_id(), w = tix() >> 6, t = c * C + l;
   const bool valid = t < s.T;
   const float d = valid ? dt[tok_index(s, b, t) * s.H + h] : 0.f;
-  for (int j = w; j < s.A; j += 4) {
-    const float x = valid ? ang[tok_index(s, b, t) * s.A + j] * d : 0.f;
-    const float incl = wave_scan(x);
+  float xs[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int j = w + 4 * m;
+    xs[m] = valid && j < s.A ? ang[tok_index(s, b, t) * s.A + j] * d : 0.f;
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int j = w + 4 * m;
+    if (j >= s.A) break;
+    const float incl = wave_scan(xs[m]);
     const float base = th0[j];
     tab[l * LA + j] = base + incl;
     if (advance) {
@@ -144,64 +179,138 @@ __device__ void phase_table(const Shape& s, const float* ang, const float* dt, i
 
 // Rotated rows of chunk c into LDS [C][LQ]: dst[t][n] = rot(src_t + bias, theta_t)[n]
 // for t < C, n < NT, zero for padding tokens and coordinates.  One pair
-// (2j, 2j+1) per lane, tokens split over the waves.  With two sources both
-// are rotated by the same angles.
+// (2j, 2j+1) per lane, tokens w, w + 4, ... per wave; every global read is
+// issued before the first rotation.  With two sources both are rotated by
+// the same angles.
 template <int NSRC>
 __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
                             const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
                             int b, int c) {
-  const int j = lane_id(), n = 2 * j;
+  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
   const bool col = n < s.N;
+  float2 u[NSRC][16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int tt = c * C + w + 4 * m;
+    const bool valid = col && tt < s.T;
+#pragma unroll
+    for (int k = 0; k < NSRC; ++k)
+      u[k][m] = valid ? *reinterpret_cast<const float2*>(src[k] + tok_index(s, b, tt) * s.N + n)
+                      : float2{0.f, 0.f};
+  }
   float2 bs[NSRC];
 #pragma unroll
   for (int k = 0; k < NSRC; ++k)
     bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
-  for (int t = threadIdx.x >> 6; t < C; t += 4) {
-    const int tt = c * C + t;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int t = w + 4 * m, tt = c * C + t;
     const bool valid = col && tt < s.T;
     float sn = 0.f, cs = 1.f;
     if (valid && j < s.A) sincosf(tab[t * LA + j], &sn, &cs);
 #pragma unroll
     for (int k = 0; k < NSRC; ++k) {
-      float2 u = float2{0.f, 0.f};
-      if (valid) {
-        u = *reinterpret_cast<const float2*>(src[k] + tok_index(s, b, tt) * s.N + n);
-        u.x += bs[k].x;
-        u.y += bs[k].y;
-      }
-      const float2 r = float2{u.x * cs - u.y * sn, u.x * sn + u.y * cs};
-      *reinterpret_cast<float2*>(dst[k] + t * LQ + n) = r;
+      const float2 v = valid ? float2{u[k][m].x + bs[k].x, u[k][m].y + bs[k].y}
+                             : float2{0.f, 0.f};
+      *reinterpret_cast<float2*>(dst[k] + t * LQ + n) =
+          float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
+    }
+  }
+}
+
+// Raw rows of chunk c (no bias, no rotation) into LDS [C][LQ], zeros past T
+// and N; every global read is issued before the first store.
+template <int NSRC>
+__device__ void stage_rows(const Shape& s, const float* const (&src)[2], float* const (&dst)[2],
+                           int b, int c) {
+  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
+  const bool col = n < s.N;
+  float2 u[NSRC][16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int tt = c * C + w + 4 * m;
+    const bool valid = col && tt < s.T;
+#pragma unroll
+    for (int k = 0; k < NSRC; ++k)
+      u[k][m] = valid ? *reinterpret_cast<const float2*>(src[k] + tok_index(s, b, tt) * s.N + n)
+                      : float2{0.f, 0.f};
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m)
+#pragma unroll
+    for (int k = 0; k < NSRC; ++k)
+      *reinterpret_cast<float2*>(dst[k] + (w + 4 * m) * LQ + n) = u[k][m];
+}
+
+// rotate_rows on rows already staged in LDS, in place (each thread rewrites
+// the pairs it reads).
+template <int NSRC>
+__device__ void rotate_staged(const Shape& s, const float* const (&bias)[2],
+                              float* const (&rows)[2], const float* tab, int c) {
+  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
+  const bool col = n < s.N;
+  float2 bs[NSRC];
+#pragma unroll
+  for (int k = 0; k < NSRC; ++k)
+    bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
+#pragma unroll 2
+  for (int m = 0; m < 16; ++m) {
+    const int t = w + 4 * m, tt = c * C + t;
+    const bool valid = col && tt < s.T;
+    float sn = 0.f, cs = 1.f;
+    if (valid && j < s.A) sincosf(tab[t * LA + j], &sn, &cs);
+#pragma unroll
+    for (int k = 0; k < NSRC; ++k) {
+      float2* p = reinterpret_cast<float2*>(rows[k] + t * LQ + n);
+      const float2 u = *p;
+      const float2 v = valid ? float2{u.x + bs[k].x, u.y + bs[k].y} : float2{0.f, 0.f};
+      *p = float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
     }
   }
 }
 
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
-// row_scale[t] (nullptr: 1); zeros past T and P.
+// row_scale[t] (nullptr: 1); zeros past T and P.  Four 16-byte rows pieces
+// per thread, all read before any is stored.
 __device__ void load_values(const Shape& s, const float* src, int b, int c, int h,
                             const float* row_scale, float* dst) {
-  for (int e = threadIdx.x; e < C * (PT / 4); e += 256) {
-    const int t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
-    f4 v = f4{0.f, 0.f, 0.f, 0.f};
+  f4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tix() + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+    const int tt = c * C + t;
+    v[i] = f4{0.f, 0.f, 0.f, 0.f};
     if (tt < s.T) {
       const float* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
       if (s.P % 4 == 0) {
-        if (p < s.P) v = *reinterpret_cast<const f4*>(row + p);
+        if (p < s.P) v[i] = *reinterpret_cast<const f4*>(row + p);
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          if (p + k < s.P) v[k] = row[p + k];
+          if (p + k < s.P) v[i][k] = row[p + k];
       }
-      if (row_scale) v *= row_scale[t];
     }
-    *reinterpret_cast<f4*>(dst + t * LV + p) = v;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tix() + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+    *reinterpret_cast<f4*>(dst + t * LV + p) = row_scale ? v[i] * row_scale[t] : v[i];
   }
 }
 
-// A stored [NT][PT] state tile into LDS [NT][LV].
+// A stored [NT][PT] state tile into LDS [NT][LV]: eight 16-byte pieces per
+// thread, all read before any is stored.
 __device__ void load_state(const float* src, float* dst) {
-  for (int e = threadIdx.x; e < NT * (PT / 4); e += 256) {
-    const int n = e / (PT / 4), p = 4 * (e % (PT / 4));
-    *reinterpret_cast<f4*>(dst + n * LV + p) = *reinterpret_cast<const f4*>(src + n * PT + p);
+  f4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tix() + 256 * i;
+    v[i] = *reinterpret_cast<const f4*>(src + (e / (PT / 4)) * PT + 4 * (e % (PT / 4)));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tix() + 256 * i;
+    *reinterpret_cast<f4*>(dst + (e / (PT / 4)) * LV + 4 * (e % (PT / 4))) = v[i];
   }
 }
 
@@ -235,7 +344,7 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
   const int bh = blockIdx.x, b = bh / s.H, h = bh % s.H;
-  const int tid = threadIdx.x, w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
+  const int tid = tix(), w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
 
   // Wave w holds state rows 32 w .. 32 w + 31 as two 16-row strips of four
   // 16-column tiles.
@@ -336,7 +445,7 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
   const int total = s.B * s.NC * s.H, id = xcd_block(total);
   const int h = id % s.H, c = (id / s.H) % s.NC, b = id / (s.H * s.NC);
-  const int tid = threadIdx.x, w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
+  const int tid = tix(), w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
 
   if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
   if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
@@ -431,9 +540,6 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
   const int g = id % groups, c = (id / groups) % s.NC, b = id / (groups * s.NC);
   const int hpg = (s.H + groups - 1) / groups, h_begin = g * hpg;
   const int h_end = min(s.H, h_begin + hpg);
-  const int tid = threadIdx.x, w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
-  const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
-
   // This group's sums over its heads accumulate in its own slices of
   // dc_part, db_part and dang_part: every element belongs to one thread, which
   // writes it for the group's first head and adds to it for the others.
@@ -444,6 +550,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
 
   for (int h = h_begin; h < h_end; ++h) {
     const bool first = h == h_begin;
+    const int tid = tix(), w = tid >> 6, l = tid & 63, r = l & 15, q = l >> 4;
+    const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
     if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
     if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
@@ -462,16 +570,17 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     __syncthreads();
     float* qt = R1;
     float* kt = R1 + C * LQ;
-    {
-      const float* const src[2] = {cq, bk};
-      const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
-      float* const dst[2] = {qt, kt};
-      rotate_rows<2>(s, src, bsrc, dst, tab, b, c);
-    }
+    const float* const src2[2] = {cq, bk};
+    float* const qk[2] = {qt, kt};
+    stage_rows<2>(s, src2, qk, b, c);
     float* h0 = R2;
     float* g1 = R2 + NT * LV;
     load_state(starts + state_offset(s, b, h, c), h0);
     load_state(dh1 + state_offset(s, b, h, c), g1);
+    {
+      const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
+      rotate_staged<2>(s, bsrc, qk, tab, c);
+    }
     __syncthreads();
 
     // Q H0, K dH1 and the scores (wave w: rows 16 w .. 16 w + 15).
@@ -614,6 +723,10 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         dqt[t * LQ + n] = dq[j][i];
         dkt[t * LQ + n] = dk[j][i];
       }
+    {
+      float* const raw[2] = {R2, R2 + C * LQ};
+      stage_rows<2>(s, src2, raw, b, c);
+    }
     __syncthreads();
 
     // Through the rotations: one pair per lane, tokens w, w + 4, ...
@@ -625,14 +738,14 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
       }
       float2 sq = float2{0.f, 0.f}, sk = float2{0.f, 0.f};
-#pragma unroll 1
+#pragma unroll 2
       for (int m = 0; m < 16; ++m) {
         const int t = w + 4 * m, tt = c * C + t;
+        float2* pq = reinterpret_cast<float2*>(dqt + t * LQ + n2);
+        float2* pk = reinterpret_cast<float2*>(dkt + t * LQ + n2);
         if (!col || tt >= s.T) {
-          if (first) {
-            *reinterpret_cast<float2*>(dcp + (c * C + t) * NT + n2) = float2{0.f, 0.f};
-            *reinterpret_cast<float2*>(dbp + (c * C + t) * NT + n2) = float2{0.f, 0.f};
-          }
+          *pq = float2{0.f, 0.f};
+          *pk = float2{0.f, 0.f};
           continue;
         }
         const float2 gq = *reinterpret_cast<const float2*>(dqt + t * LQ + n2);
@@ -641,8 +754,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         if (l < s.A) {
           float sn, cs;
           sincosf(tab[t * LA + l], &sn, &cs);
-          float2 uq = *reinterpret_cast<const float2*>(cq + tok_index(s, b, tt) * s.N + n2);
-          float2 uk = *reinterpret_cast<const float2*>(bk + tok_index(s, b, tt) * s.N + n2);
+          float2 uq = *reinterpret_cast<const float2*>(R2 + t * LQ + n2);
+          float2 uk = *reinterpret_cast<const float2*>(R2 + C * LQ + t * LQ + n2);
           uq.x += bq.x;
           uq.y += bq.y;
           uk.x += bkv.x;
@@ -653,16 +766,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
           duq = float2{gq.x * cs + gq.y * sn, -gq.x * sn + gq.y * cs};
           duk = float2{gk.x * cs + gk.y * sn, -gk.x * sn + gk.y * cs};
         }
-        float2* pc = reinterpret_cast<float2*>(dcp + (c * C + t) * NT + n2);
-        float2* pb = reinterpret_cast<float2*>(dbp + (c * C + t) * NT + n2);
-        if (first) {
-          *pc = duq;
-          *pb = duk;
-        } else {
-          const float2 a = *pc, e = *pb;
-          *pc = float2{a.x + duq.x, a.y + duq.y};
-          *pb = float2{e.x + duk.x, e.y + duk.y};
-        }
+        *pq = duq;
+        *pk = duk;
         sq.x += duq.x;
         sq.y += duq.y;
         sk.x += duk.x;
@@ -680,17 +785,21 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     {
       const int tt = c * C + l;
       const bool valid = tt < s.T;
-      float ddt = 0.f;
-#pragma unroll 1
+      float ddt = 0.f, av[16];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const int j = w + 4 * m;
+        av[m] = valid && j < s.A ? ang[tok_index(s, b, tt) * s.A + j] : 0.f;
+      }
+#pragma unroll
       for (int m = 0; m < 16; ++m) {
         const int j = w + 4 * m;
         if (j >= s.A) break;
         const float xv = valid ? tab[l * LA + j] : 0.f;
         const float incl = wave_scan(xv), tot = __shfl(incl, 63, 64);
         const float R = tot - incl + xv;
-        float* pa = dap + (c * C + l) * AM + j;
-        *pa = (first ? 0.f : *pa) + R * S.dt[l];
-        if (valid) ddt += R * ang[tok_index(s, b, tt) * s.A + j];
+        tab[l * LA + j] = R * S.dt[l];
+        ddt += R * av[m];
         if (l == 0) o.D[phase_offset(s, b, h, c) + j] = R;
       }
       atomicAdd(&s_ddt[l], ddt);
@@ -701,6 +810,46 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
       o.kb_part[at] = kbacc[tid];
     }
     __syncthreads();
+    // This head's row and angle gradients into the group's sums: dc / db
+    // from the rotated-back tiles, the angle part from the phase table.
+    {
+      f4 prev[16];
+      if (!first) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int e = tid + 256 * i, t = e / (NT / 4), n = 4 * (e % (NT / 4));
+          prev[i] = *reinterpret_cast<const f4*>(dcp + (c * C + t) * NT + n);
+          prev[8 + i] = *reinterpret_cast<const f4*>(dbp + (c * C + t) * NT + n);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int e = tid + 256 * i, t = e / (NT / 4), n = 4 * (e % (NT / 4));
+        f4 vq = *reinterpret_cast<const f4*>(dqt + t * LQ + n);
+        f4 vk = *reinterpret_cast<const f4*>(dkt + t * LQ + n);
+        if (!first) {
+          vq += prev[i];
+          vk += prev[8 + i];
+        }
+        *reinterpret_cast<f4*>(dcp + (c * C + t) * NT + n) = vq;
+        *reinterpret_cast<f4*>(dbp + (c * C + t) * NT + n) = vk;
+      }
+      float pa[16];
+      if (!first) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int e = tid + 256 * i;
+          pa[i] = dap[(c * C + e / AM) * AM + e % AM];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int e = tid + 256 * i, t = e / AM, j = e % AM;
+        float v = j < s.A ? tab[t * LA + j] : 0.f;
+        if (!first) v += pa[i];
+        dap[(c * C + t) * AM + j] = v;
+      }
+    }
     if (w == 0) {
       const int tt = c * C + l;
       const float pl = S.p[63];
@@ -732,7 +881,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
                                                      float* d_dt, float* d_trap,
                                                      float* d_angles) {
   extern __shared__ float suf[];  // [H][AM]
-  const int b = blockIdx.x / s.NC, c = blockIdx.x % s.NC, tid = threadIdx.x;
+  const int b = blockIdx.x / s.NC, c = blockIdx.x % s.NC, tid = tix();
   for (int e = tid; e < s.H * s.A; e += 256) {
     const int h = e / s.A, j = e % s.A;
     float acc = 0.f;
@@ -774,18 +923,30 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   }
 }
 
-// Bias gradients: sums over (b, chunk) of the per-head partials.
-__global__ __launch_bounds__(128) void bias_kernel(Shape s, GradOut o, float* d_qb, float* d_kb) {
-  const int h = blockIdx.x, n = threadIdx.x;
-  if (n >= s.N) return;
+// Bias gradients: sums over (b, chunk) of the per-head partials; eight
+// threads per coordinate take every eighth (b, chunk) and combine in LDS.
+__global__ __launch_bounds__(1024) void bias_kernel(Shape s, GradOut o, float* d_qb, float* d_kb) {
+  __shared__ float part[2][8][NT];
+  const int h = blockIdx.x, n = tix() % NT, slice = tix() / NT;
   float aq = 0.f, ak = 0.f;
-  for (int bc = 0; bc < s.B * s.NC; ++bc) {
+  for (int bc = slice; bc < s.B * s.NC; bc += 8) {
     const long at = ((long)bc * s.H + h) * NT + n;
     aq += o.qb_part[at];
     ak += o.kb_part[at];
   }
-  d_qb[(long)h * s.N + n] = aq;
-  d_kb[(long)h * s.N + n] = ak;
+  part[0][slice][n] = aq;
+  part[1][slice][n] = ak;
+  __syncthreads();
+  if (slice == 0 && n < s.N) {
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sq += part[0][i][n];
+      sk += part[1][i][n];
+    }
+    d_qb[(long)h * s.N + n] = sq;
+    d_kb[(long)h * s.N + n] = sk;
+  }
 }
 
 template __global__ void walk_kernel<false>(Shape, const float*, const float*, const float*,
