@@ -71,6 +71,32 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// sin and cos of x (|x| < 2^16): x = k pi/2 + r with k = rint(2x/pi) and r by
+// Cody-Waite reduction (pi/2 as three float32 parts; k * part is exact for
+// |k| < 2^16 in the first, rounded once by the fused multiply-add in the
+// others), then Taylor polynomials of sin r and cos r on |r| <= pi/4 through
+// r^9 and r^10 (truncation below 2e-9), and the quadrant k mod 4.
+__device__ __forceinline__ void sin_cos(float x, float* sn, float* cs) {
+  const float k = rintf(x * 0.636619772f);
+  float r = fmaf(-k, 1.5703125f, x);
+  r = fmaf(-k, 4.838267923332751e-4f, r);
+  r = fmaf(-k, 2.5632829e-12f, r);
+  const float r2 = r * r;
+  float ps = fmaf(r2, 2.7557319e-6f, -1.9841270e-4f);
+  ps = fmaf(r2, ps, 8.3333333e-3f);
+  ps = fmaf(r2, ps, -1.6666667e-1f);
+  const float sr = fmaf(r * r2, ps, r);
+  float pc = fmaf(r2, -2.7557319e-7f, 2.4801587e-5f);
+  pc = fmaf(r2, pc, -1.3888889e-3f);
+  pc = fmaf(r2, pc, 4.1666668e-2f);
+  pc = fmaf(r2, pc, -0.5f);
+  const float cr = fmaf(r2, pc, 1.f);
+  const int quad = static_cast<int>(k) & 3;
+  const float s0 = (quad & 1) ? cr : sr, c0 = (quad & 1) ? sr : cr;
+  *sn = (quad & 2) ? -s0 : s0;
+  *cs = ((quad + 1) & 2) ? -c0 : c0;
+}
+
 // Four consecutive-in-k operand values: one 16-byte LDS read when the
 // operand is contiguous along k (stride 1), four reads otherwise.
 template <int STRIDE>
@@ -207,7 +233,7 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
     const int t = w + 4 * m, tt = c * C + t;
     const bool valid = col && tt < s.T;
     float sn = 0.f, cs = 1.f;
-    if (valid && j < s.A) sincosf(tab[t * LA + j], &sn, &cs);
+    if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
 #pragma unroll
     for (int k = 0; k < NSRC; ++k) {
       const float2 v = valid ? float2{u[k][m].x + bs[k].x, u[k][m].y + bs[k].y}
@@ -258,7 +284,7 @@ __device__ void rotate_staged(const Shape& s, const float* const (&bias)[2],
     const int t = w + 4 * m, tt = c * C + t;
     const bool valid = col && tt < s.T;
     float sn = 0.f, cs = 1.f;
-    if (valid && j < s.A) sincosf(tab[t * LA + j], &sn, &cs);
+    if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
 #pragma unroll
     for (int k = 0; k < NSRC; ++k) {
       float2* p = reinterpret_cast<float2*>(rows[k] + t * LQ + n);
@@ -540,16 +566,19 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
   const int g = id % groups, c = (id / groups) % s.NC, b = id / (groups * s.NC);
   const int hpg = (s.H + groups - 1) / groups, h_begin = g * hpg;
   const int h_end = min(s.H, h_begin + hpg);
-  // This group's sums over its heads accumulate in its own slices of
-  // dc_part, db_part and dang_part: every element belongs to one thread, which
-  // writes it for the group's first head and adds to it for the others.
-  const long tp = (long)s.NC * C;
-  float* dcp = o.dc_part + ((long)g * s.B + b) * tp * NT;
-  float* dbp = o.db_part + ((long)g * s.B + b) * tp * NT;
-  float* dap = o.dang_part + ((long)g * s.B + b) * tp * AM;
+  // This group's sums over its heads: the rotated-back row gradients of this
+  // thread's 16 (token, pair) slots and the angle gradients of its 16
+  // (token = lane, angle) slots stay in registers until the last head.
+  float2 dcacc[16], dbacc[16];
+  float dang[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    dcacc[m] = float2{0.f, 0.f};
+    dbacc[m] = float2{0.f, 0.f};
+    dang[m] = 0.f;
+  }
 
   for (int h = h_begin; h < h_end; ++h) {
-    const bool first = h == h_begin;
     const int tid = tix(), w = tid >> 6, l = tid & 63, r = l & 15, q = l >> 4;
     const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
@@ -738,22 +767,16 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
       }
       float2 sq = float2{0.f, 0.f}, sk = float2{0.f, 0.f};
-#pragma unroll 2
+#pragma unroll
       for (int m = 0; m < 16; ++m) {
         const int t = w + 4 * m, tt = c * C + t;
-        float2* pq = reinterpret_cast<float2*>(dqt + t * LQ + n2);
-        float2* pk = reinterpret_cast<float2*>(dkt + t * LQ + n2);
-        if (!col || tt >= s.T) {
-          *pq = float2{0.f, 0.f};
-          *pk = float2{0.f, 0.f};
-          continue;
-        }
+        if (!col || tt >= s.T) continue;
         const float2 gq = *reinterpret_cast<const float2*>(dqt + t * LQ + n2);
         const float2 gk = *reinterpret_cast<const float2*>(dkt + t * LQ + n2);
         float2 duq = gq, duk = gk;
         if (l < s.A) {
           float sn, cs;
-          sincosf(tab[t * LA + l], &sn, &cs);
+          sin_cos(tab[t * LA + l], &sn, &cs);
           float2 uq = *reinterpret_cast<const float2*>(R2 + t * LQ + n2);
           float2 uk = *reinterpret_cast<const float2*>(R2 + C * LQ + t * LQ + n2);
           uq.x += bq.x;
@@ -766,8 +789,10 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
           duq = float2{gq.x * cs + gq.y * sn, -gq.x * sn + gq.y * cs};
           duk = float2{gk.x * cs + gk.y * sn, -gk.x * sn + gk.y * cs};
         }
-        *pq = duq;
-        *pk = duk;
+        dcacc[m].x += duq.x;
+        dcacc[m].y += duq.y;
+        dbacc[m].x += duk.x;
+        dbacc[m].y += duk.y;
         sq.x += duq.x;
         sq.y += duq.y;
         sk.x += duk.x;
@@ -798,7 +823,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         const float xv = valid ? tab[l * LA + j] : 0.f;
         const float incl = wave_scan(xv), tot = __shfl(incl, 63, 64);
         const float R = tot - incl + xv;
-        tab[l * LA + j] = R * S.dt[l];
+        dang[m] += R * S.dt[l];
         ddt += R * av[m];
         if (l == 0) o.D[phase_offset(s, b, h, c) + j] = R;
       }
@@ -810,46 +835,6 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
       o.kb_part[at] = kbacc[tid];
     }
     __syncthreads();
-    // This head's row and angle gradients into the group's sums: dc / db
-    // from the rotated-back tiles, the angle part from the phase table.
-    {
-      f4 prev[16];
-      if (!first) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int e = tid + 256 * i, t = e / (NT / 4), n = 4 * (e % (NT / 4));
-          prev[i] = *reinterpret_cast<const f4*>(dcp + (c * C + t) * NT + n);
-          prev[8 + i] = *reinterpret_cast<const f4*>(dbp + (c * C + t) * NT + n);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int e = tid + 256 * i, t = e / (NT / 4), n = 4 * (e % (NT / 4));
-        f4 vq = *reinterpret_cast<const f4*>(dqt + t * LQ + n);
-        f4 vk = *reinterpret_cast<const f4*>(dkt + t * LQ + n);
-        if (!first) {
-          vq += prev[i];
-          vk += prev[8 + i];
-        }
-        *reinterpret_cast<f4*>(dcp + (c * C + t) * NT + n) = vq;
-        *reinterpret_cast<f4*>(dbp + (c * C + t) * NT + n) = vk;
-      }
-      float pa[16];
-      if (!first) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int e = tid + 256 * i;
-          pa[i] = dap[(c * C + e / AM) * AM + e % AM];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int e = tid + 256 * i, t = e / AM, j = e % AM;
-        float v = j < s.A ? tab[t * LA + j] : 0.f;
-        if (!first) v += pa[i];
-        dap[(c * C + t) * AM + j] = v;
-      }
-    }
     if (w == 0) {
       const int tt = c * C + l;
       const float pl = S.p[63];
@@ -869,6 +854,21 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     }
   }
 
+  // The group's sums, written once.
+  {
+    const int tid = tix(), w = tid >> 6, l = tid & 63;
+    const long tp = (long)s.NC * C;
+    float* dcp = o.dc_part + ((long)g * s.B + b) * tp * NT;
+    float* dbp = o.db_part + ((long)g * s.B + b) * tp * NT;
+    float* dap = o.dang_part + ((long)g * s.B + b) * tp * AM;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const long at = (long)(c * C + w + 4 * m) * NT + 2 * l;
+      *reinterpret_cast<float2*>(dcp + at) = dcacc[m];
+      *reinterpret_cast<float2*>(dbp + at) = dbacc[m];
+      dap[(long)(c * C + l) * AM + w + 4 * m] = dang[m];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
