@@ -108,7 +108,7 @@ __device__ __forceinline__ f4 load_k4(const float* p) {
   }
 }
 
-// acc[j] += A[r0 .. r0+16, kb .. ke) * B[kb .. ke, c0 + 16 j .. +16) for j < jn,
+// acc[j] += A[r0 .. r0+16, kb .. ke) * B[kb .. ke, c0 + 16 j .. +16) for j < J,
 // with A(r, k) = A[r * AR + k * AK] and B(k, c) = B[k * BK + c * BC] in LDS;
 // kb and ke are multiples of 16.  Result element acc[j][i] is (row
 // r0 + 4 (lane / 16) + i, column c0 + 16 j + lane % 16).  Within each block
@@ -118,7 +118,7 @@ __device__ __forceinline__ f4 load_k4(const float* p) {
 // All of a block's operands are read before its 4 J MFMAs issue.
 template <int J, int AR, int AK, int BK, int BC>
 __device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const float* B, int c0,
-                                    int kb, int ke, int jn = J) {
+                                    int kb, int ke) {
   const int l = lane_id(), r = l & 15, q = l >> 4;
   const float* pa = A + (r0 + r) * AR + 4 * q * AK;
   const float* pb = B + 4 * q * BK + (c0 + r) * BC;
@@ -127,13 +127,34 @@ __device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const 
     const f4 a = load_k4<AK>(pa + k * AK);
     f4 b[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-      if (j < jn) b[j] = load_k4<BK>(pb + k * BK + 16 * j * BC);
+    for (int j = 0; j < J; ++j) b[j] = load_k4<BK>(pb + k * BK + 16 * j * BC);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int j = 0; j < J; ++j)
-        if (j < jn) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
+  }
+}
+
+// mma over the first jn (1..4, the same for the whole wave) of four column
+// tiles: each count is its own straight-line instantiation, so no MFMA sits
+// under a per-tile branch.
+template <int AR, int AK, int BK, int BC>
+__device__ __forceinline__ void mma_first(f4 (&acc)[4], const float* A, int r0, const float* B,
+                                          int c0, int kb, int ke, int jn) {
+  switch (jn) {
+    case 1:
+      mma<1, AR, AK, BK, BC>(*reinterpret_cast<f4(*)[1]>(acc), A, r0, B, c0, kb, ke);
+      break;
+    case 2:
+      mma<2, AR, AK, BK, BC>(*reinterpret_cast<f4(*)[2]>(acc), A, r0, B, c0, kb, ke);
+      break;
+    case 3:
+      mma<3, AR, AK, BK, BC>(*reinterpret_cast<f4(*)[3]>(acc), A, r0, B, c0, kb, ke);
+      break;
+    default:
+      mma<4, AR, AK, BK, BC>(acc, A, r0, B, c0, kb, ke);
+      break;
   }
 }
 
@@ -471,7 +492,8 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
   const int total = s.B * s.NC * s.H, id = xcd_block(total);
   const int h = id % s.H, c = (id / s.H) % s.NC, b = id / (s.H * s.NC);
-  const int tid = tix(), w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
+  const int tid = tix(), l = lane_id(), r = l & 15, q = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
   if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
@@ -492,7 +514,7 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
   f4 sco[4], qh[4];
   zero(sco);
   zero(qh);
-  mma<4, LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
+  mma_first<LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
   mma<4, LQ, 1, LV, 1>(qh, qt, 16 * w, h0, 0, 0, NT);
   __syncthreads();  // every wave is done with K
   float* gs = kt;
@@ -579,7 +601,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
   }
 
   for (int h = h_begin; h < h_end; ++h) {
-    const int tid = tix(), w = tid >> 6, l = tid & 63, r = l & 15, q = l >> 4;
+    const int tid = tix(), l = tid & 63, r = l & 15, q = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
     if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
@@ -617,7 +640,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     zero(sco);
     zero(qh);
     zero(kg);
-    mma<4, LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
+    mma_first<LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
     mma<4, LQ, 1, LV, 1>(qh, qt, 16 * w, h0, 0, 0, NT);
     mma<4, LQ, 1, LV, 1>(kg, kt, 16 * w, g1, 0, 0, NT);
     {
@@ -641,7 +664,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     f4 dsc[4];
     zero(dsc);
     // dY V^T: A(t, p) = dY[t * LV + p], B(p, s) = V[s * LV + p].
-    mma<4, LV, 1, 1, LV>(dsc, dyt, 16 * w, vt, 0, 0, PT, w + 1);
+    mma_first<LV, 1, 1, LV>(dsc, dyt, 16 * w, vt, 0, 0, PT, w + 1);
     {
       float qd[4] = {0.f, 0.f, 0.f, 0.f}, gg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
