@@ -265,57 +265,6 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
   }
 }
 
-// Raw rows of chunk c (no bias, no rotation) into LDS [C][LQ], zeros past T
-// and N; every global read is issued before the first store.
-template <int NSRC>
-__device__ void stage_rows(const Shape& s, const float* const (&src)[2], float* const (&dst)[2],
-                           int b, int c) {
-  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
-  const bool col = n < s.N;
-  float2 u[NSRC][16];
-#pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int tt = c * C + w + 4 * m;
-    const bool valid = col && tt < s.T;
-#pragma unroll
-    for (int k = 0; k < NSRC; ++k)
-      u[k][m] = valid ? *reinterpret_cast<const float2*>(src[k] + tok_index(s, b, tt) * s.N + n)
-                      : float2{0.f, 0.f};
-  }
-#pragma unroll
-  for (int m = 0; m < 16; ++m)
-#pragma unroll
-    for (int k = 0; k < NSRC; ++k)
-      *reinterpret_cast<float2*>(dst[k] + (w + 4 * m) * LQ + n) = u[k][m];
-}
-
-// rotate_rows on rows already staged in LDS, in place (each thread rewrites
-// the pairs it reads).
-template <int NSRC>
-__device__ void rotate_staged(const Shape& s, const float* const (&bias)[2],
-                              float* const (&rows)[2], const float* tab, int c) {
-  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
-  const bool col = n < s.N;
-  float2 bs[NSRC];
-#pragma unroll
-  for (int k = 0; k < NSRC; ++k)
-    bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
-#pragma unroll 2
-  for (int m = 0; m < 16; ++m) {
-    const int t = w + 4 * m, tt = c * C + t;
-    const bool valid = col && tt < s.T;
-    float sn = 0.f, cs = 1.f;
-    if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
-#pragma unroll
-    for (int k = 0; k < NSRC; ++k) {
-      float2* p = reinterpret_cast<float2*>(rows[k] + t * LQ + n);
-      const float2 u = *p;
-      const float2 v = valid ? float2{u.x + bs[k].x, u.y + bs[k].y} : float2{0.f, 0.f};
-      *p = float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
-    }
-  }
-}
-
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
 // row_scale[t] (nullptr: 1); zeros past T and P.  Four 16-byte rows pieces
 // per thread, all read before any is stored.
@@ -599,6 +548,21 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     dbacc[m] = float2{0.f, 0.f};
     dang[m] = 0.f;
   }
+  // The chunk's raw query and key rows are the same for every head: this
+  // thread's 16 (token, pair) slots are read once and kept in registers.
+  float2 rc[16], rb[16];
+  {
+    const int tid = tix(), l = tid & 63, w = tid >> 6;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int tt = c * C + w + 4 * m;
+      const bool ok = 2 * l < s.N && tt < s.T;
+      rc[m] = ok ? *reinterpret_cast<const float2*>(cq + tok_index(s, b, tt) * s.N + 2 * l)
+                 : float2{0.f, 0.f};
+      rb[m] = ok ? *reinterpret_cast<const float2*>(bk + tok_index(s, b, tt) * s.N + 2 * l)
+                 : float2{0.f, 0.f};
+    }
+  }
 
   for (int h = h_begin; h < h_end; ++h) {
     const int tid = tix(), l = tid & 63, r = l & 15, q = l >> 4;
@@ -622,16 +586,30 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     __syncthreads();
     float* qt = R1;
     float* kt = R1 + C * LQ;
-    const float* const src2[2] = {cq, bk};
-    float* const qk[2] = {qt, kt};
-    stage_rows<2>(s, src2, qk, b, c);
     float* h0 = R2;
     float* g1 = R2 + NT * LV;
     load_state(starts + state_offset(s, b, h, c), h0);
     load_state(dh1 + state_offset(s, b, h, c), g1);
     {
-      const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
-      rotate_staged<2>(s, bsrc, qk, tab, c);
+      const bool col = n2 < s.N;
+      float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
+      if (col) {
+        bq = *reinterpret_cast<const float2*>(qb + (long)h * s.N + n2);
+        bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
+      }
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const int t = w + 4 * m, tt = c * C + t;
+        const bool valid = col && tt < s.T;
+        float sn = 0.f, cs = 1.f;
+        if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
+        const float2 u = valid ? float2{rc[m].x + bq.x, rc[m].y + bq.y} : float2{0.f, 0.f};
+        const float2 v = valid ? float2{rb[m].x + bkv.x, rb[m].y + bkv.y} : float2{0.f, 0.f};
+        *reinterpret_cast<float2*>(qt + t * LQ + n2) =
+            float2{u.x * cs - u.y * sn, u.x * sn + u.y * cs};
+        *reinterpret_cast<float2*>(kt + t * LQ + n2) =
+            float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
+      }
     }
     __syncthreads();
 
@@ -775,10 +753,6 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         dqt[t * LQ + n] = dq[j][i];
         dkt[t * LQ + n] = dk[j][i];
       }
-    {
-      float* const raw[2] = {R2, R2 + C * LQ};
-      stage_rows<2>(s, src2, raw, b, c);
-    }
     __syncthreads();
 
     // Through the rotations: one pair per lane, tokens w, w + 4, ...
@@ -800,8 +774,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         if (l < s.A) {
           float sn, cs;
           sin_cos(tab[t * LA + l], &sn, &cs);
-          float2 uq = *reinterpret_cast<const float2*>(R2 + t * LQ + n2);
-          float2 uk = *reinterpret_cast<const float2*>(R2 + C * LQ + t * LQ + n2);
+          float2 uq = rc[m], uk = rb[m];
           uq.x += bq.x;
           uq.y += bq.y;
           uk.x += bkv.x;
