@@ -48,26 +48,39 @@ __device__ __forceinline__ int tix() {
 }
 __device__ __forceinline__ int lane_id() { return tix() & 63; }
 
+// DPP move of x (as bits) with zeros where the source lane is out of range.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp0(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, true));
+}
+
+// Inclusive sum over the lanes of a wave: Hillis-Steele within each 16-lane
+// row (row_shr 1, 2, 4, 8), then row 0's total into rows 1 and 3
+// (row_bcast:15) and row 1's running total into rows 2 and 3 (row_bcast:31).
 __device__ __forceinline__ float wave_scan(float x) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float y = __shfl_up(x, o, 64);
-    if (l >= o) x += y;
-  }
+  x += dpp0<0x111, 0xf>(x);
+  x += dpp0<0x112, 0xf>(x);
+  x += dpp0<0x114, 0xf>(x);
+  x += dpp0<0x118, 0xf>(x);
+  x += dpp0<0x142, 0xa>(x);
+  x += dpp0<0x143, 0xc>(x);
   return x;
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
+__device__ __forceinline__ float lane63(float x) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
-// Sum over the 16 lanes sharing bits 4..5 of the lane index.
+__device__ __forceinline__ float wave_sum(float x) { return lane63(wave_scan(x)); }
+
+// Sum over the 16 lanes sharing bits 4..5 of the lane index (row_ror 8, 4,
+// 2, 1 within each row of 16: every lane ends with the row's total).
 __device__ __forceinline__ float row16_sum(float x) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  x += dpp0<0x128, 0xf>(x);
+  x += dpp0<0x124, 0xf>(x);
+  x += dpp0<0x122, 0xf>(x);
+  x += dpp0<0x121, 0xf>(x);
   return x;
 }
 
@@ -176,17 +189,26 @@ struct Scalars {
   float *p, *ep, *gam, *scale, *u, *dt;
 };
 
-__device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
-                              const float* trap, int b, int h, int c, const Scalars& o) {
-  const int l = lane_id(), t = c * C + l;
+// The raw per-token inputs of one lane's token (zeros past T).
+struct TokenIn {
+  float a, d, tr, dn, trn;
+};
+
+__device__ __forceinline__ TokenIn fetch_token(const Shape& s, const float* adt, const float* dt,
+                                               const float* trap, int b, int h, int c) {
+  const int t = c * C + lane_id();
   const bool valid = t < s.T, next = t + 1 < s.T;
   const long i = tok_index(s, b, t) * s.H + h;
-  const float a = valid ? adt[i] : 0.f, d = valid ? dt[i] : 0.f;
-  const float tr = valid ? trap[i] : 0.f;
-  const float dn = next ? dt[i + s.H] : 0.f, trn = next ? trap[i + s.H] : 0.f;
+  return TokenIn{valid ? adt[i] : 0.f, valid ? dt[i] : 0.f, valid ? trap[i] : 0.f,
+                 next ? dt[i + s.H] : 0.f, next ? trap[i + s.H] : 0.f};
+}
+
+__device__ void token_scalars(const TokenIn& in, const Scalars& o) {
+  const int l = lane_id();
+  const float a = in.a, d = in.d, tr = in.tr, dn = in.dn, trn = in.trn;
   const float sig = 1.f / (1.f + expf(-tr)), sign = 1.f / (1.f + expf(-trn));
   const float gam = d * sig, scale = gam + dn * (1.f - sign);
-  const float p = wave_scan(a), pl = __shfl(p, 63, 64);
+  const float p = wave_scan(a), pl = lane63(p);
   o.p[l] = p;
   o.ep[l] = expf(p);
   o.gam[l] = gam;
@@ -195,21 +217,34 @@ __device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
   o.dt[l] = d;
 }
 
+__device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
+                              const float* trap, int b, int h, int c, const Scalars& o) {
+  token_scalars(fetch_token(s, adt, dt, trap, b, h, c), o);
+}
+
 // Phase table of chunk c: tab[t * LA + j] = th0[j] + sum_{s <= t} angles_s,j dt_s
 // (j < A), one token per lane, angles split over the four waves.  With
 // `advance`, th0[j] moves to the chunk's end phase (th0 lives in LDS and each
 // j belongs to one wave, whose lanes read it before lane 63 writes it).
-__device__ void phase_table(const Shape& s, const float* ang, const float* dt, int b, int h,
-                            int c, float* th0, float* tab, bool advance) {
-  const int l = lane_id(), w = tix() >> 6, t = c * C + l;
+// This lane's token's angle rates j = w + 4 m (zeros past T and A).
+__device__ __forceinline__ void fetch_angles(const Shape& s, const float* ang, int b, int c,
+                                             float (&xs)[16]) {
+  const int w = tix() >> 6, t = c * C + lane_id();
   const bool valid = t < s.T;
-  const float d = valid ? dt[tok_index(s, b, t) * s.H + h] : 0.f;
-  float xs[16];
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
     const int j = w + 4 * m;
-    xs[m] = valid && j < s.A ? ang[tok_index(s, b, t) * s.A + j] * d : 0.f;
+    xs[m] = valid && j < s.A ? ang[tok_index(s, b, t) * s.A + j] : 0.f;
   }
+}
+
+// The phase table from fetched angle rates and this lane's dt.
+__device__ void phase_table(const Shape& s, const float (&rates)[16], float d, float* th0,
+                            float* tab, bool advance) {
+  const int l = lane_id(), w = tix() >> 6;
+  float xs[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) xs[m] = rates[m] * d;
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
     const int j = w + 4 * m;
@@ -222,6 +257,15 @@ __device__ void phase_table(const Shape& s, const float* ang, const float* dt, i
       if (l == 63) th0[j] = base + incl;
     }
   }
+}
+
+__device__ void phase_table(const Shape& s, const float* ang, const float* dt, int b, int h,
+                            int c, float* th0, float* tab, bool advance) {
+  const int t = c * C + lane_id();
+  const float d = t < s.T ? dt[tok_index(s, b, t) * s.H + h] : 0.f;
+  float rates[16];
+  fetch_angles(s, ang, b, c, rates);
+  phase_table(s, rates, d, th0, tab, advance);
 }
 
 // Rotated rows of chunk c into LDS [C][LQ]: dst[t][n] = rot(src_t + bias, theta_t)[n]
@@ -359,24 +403,74 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
     }
   }
   if (!BWD && tid < AM) th0[tid] = 0.f;
-  const float* const src[2] = {rows, rows};
-  const float* const bsrc[2] = {bias + (long)h * s.N, bias + (long)h * s.N};
-  float* const dst[2] = {rt, rt};
+  const bool col = 2 * l < s.N;
+  const float2 bs = col ? *reinterpret_cast<const float2*>(bias + (long)h * s.N + 2 * l)
+                        : float2{0.f, 0.f};
+
+  // Every global input of a chunk is fetched into registers one chunk ahead,
+  // while the previous chunk's product runs.
+  TokenIn tin;
+  float rates[16], th_in = 0.f;
+  float2 u[16];
+  f4 v[4];
+  auto fetch = [&](int c) {
+    tin = fetch_token(s, adt, dt, trap, b, h, c);
+    fetch_angles(s, ang, b, c, rates);
+    if (BWD && tid < s.A) th_in = theta0[phase_offset(s, b, h, c) + tid];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int tt = c * C + w + 4 * m;
+      u[m] = col && tt < s.T
+                 ? *reinterpret_cast<const float2*>(rows + tok_index(s, b, tt) * s.N + 2 * l)
+                 : float2{0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
+      v[i] = f4{0.f, 0.f, 0.f, 0.f};
+      if (tt < s.T) {
+        const float* row = vals + (tok_index(s, b, tt) * s.H + h) * s.P;
+        if (s.P % 4 == 0) {
+          if (p < s.P) v[i] = *reinterpret_cast<const f4*>(row + p);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (p + k < s.P) v[i][k] = row[p + k];
+        }
+      }
+    }
+  };
+  fetch(BWD ? s.NC - 1 : 0);
 
   for (int step = 0; step < s.NC; ++step) {
     const int c = BWD ? s.NC - 1 - step : step;
     __syncthreads();  // the previous chunk's reads of the LDS tiles are done
-    if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
+    if (w == 0) token_scalars(tin, S);
     if (BWD) {
-      if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
+      if (tid < s.A) th0[tid] = th_in;
     } else {
       if (tid < s.A) theta0[phase_offset(s, b, h, c) + tid] = th0[tid];
     }
     __syncthreads();
-    phase_table(s, ang, dt, b, h, c, th0, tab, !BWD);
+    phase_table(s, rates, tin.d, th0, tab, !BWD);
     __syncthreads();
-    rotate_rows<1>(s, src, bsrc, dst, tab, b, c);
-    load_values(s, vals, b, c, h, BWD ? S.ep : S.u, vt);
+    // Rotated rows (one pair per lane) and scaled values into LDS.
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int t = w + 4 * m, tt = c * C + t;
+      const bool valid = col && tt < s.T;
+      float sn = 0.f, cs = 1.f;
+      if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
+      const float2 x2 = valid ? float2{u[m].x + bs.x, u[m].y + bs.y} : float2{0.f, 0.f};
+      *reinterpret_cast<float2*>(rt + t * LQ + 2 * l) =
+          float2{x2.x * cs - x2.y * sn, x2.x * sn + x2.y * cs};
+    }
+    const float* row_scale = BWD ? S.ep : S.u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+      *reinterpret_cast<f4*>(vt + t * LV + p) = v[i] * row_scale[t];
+    }
     // Store this chunk's state (a lane's four rows of one column).
     float* out = saved + state_offset(s, b, h, c);
 #pragma unroll
@@ -386,6 +480,7 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           out[(32 * w + 16 * rt2 + 4 * q + i) * PT + 16 * j + r] = acc[rt2][j][i];
+    if (step + 1 < s.NC) fetch(BWD ? c - 1 : c + 1);
     __syncthreads();
     const float decay = expf(S.p[63]);
 #pragma unroll
@@ -817,7 +912,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         const int j = w + 4 * m;
         if (j >= s.A) break;
         const float xv = valid ? tab[l * LA + j] : 0.f;
-        const float incl = wave_scan(xv), tot = __shfl(incl, 63, 64);
+        const float incl = wave_scan(xv), tot = lane63(incl);
         const float R = tot - incl + xv;
         dang[m] += R * S.dt[l];
         ddt += R * av[m];
@@ -838,7 +933,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
       float dp = s_rowE[l] - s_colE[l] + S.ep[l] * s_qd[l] - S.u[l] * s_g[l];
       if (l == 63) dp += ug + expf(pl) * hsum[0];
       const float dscale = s_colF[l] + expf(pl - S.p[l]) * s_g[l];
-      const float incl = wave_scan(dp), tot = __shfl(incl, 63, 64);
+      const float incl = wave_scan(dp), tot = lane63(incl);
       const float dadt = tot - incl + dp;
       if (tt < s.T) {
         const long i = tok_index(s, b, tt) * s.H + h;
