@@ -354,6 +354,24 @@ __device__ void load_state(const float* src, float* dst) {
   }
 }
 
+// A stored [NT][PT] state tile into LDS transposed, [PT][LQ]: thread e takes
+// row n = e % NT (consecutive lanes, conflict-free LDS stores) and columns
+// 4 (e / NT) .. +3, all read before any is stored.
+__device__ void load_state_t(const float* src, float* dst) {
+  f4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tix() + 256 * i;
+    v[i] = *reinterpret_cast<const f4*>(src + (e % NT) * PT + 4 * (e / NT));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tix() + 256 * i, n = e % NT, p = 4 * (e / NT);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[(p + k) * LQ + n] = v[i][k];
+  }
+}
+
 __device__ __forceinline__ long state_offset(const Shape& s, int b, int h, int c) {
   return (((long)b * s.H + h) * s.NC + c) * (long)(NT * PT);
 }
@@ -681,10 +699,12 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     __syncthreads();
     float* qt = R1;
     float* kt = R1 + C * LQ;
+    // The start state and end cotangent transposed, [PT][LQ], for Q H0 and
+    // K dH1 with both operands contiguous along n.
     float* h0 = R2;
     float* g1 = R2 + NT * LV;
-    load_state(starts + state_offset(s, b, h, c), h0);
-    load_state(dh1 + state_offset(s, b, h, c), g1);
+    load_state_t(starts + state_offset(s, b, h, c), h0);
+    load_state_t(dh1 + state_offset(s, b, h, c), g1);
     {
       const bool col = n2 < s.N;
       float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
@@ -714,13 +734,15 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     zero(qh);
     zero(kg);
     mma_first<LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
-    mma<4, LQ, 1, LV, 1>(qh, qt, 16 * w, h0, 0, 0, NT);
-    mma<4, LQ, 1, LV, 1>(kg, kt, 16 * w, g1, 0, 0, NT);
+    // B(n, p) = H0t[p * LQ + n].
+    mma<4, LQ, 1, 1, LQ>(qh, qt, 16 * w, h0, 0, 0, NT);
+    mma<4, LQ, 1, 1, LQ>(kg, kt, 16 * w, g1, 0, 0, NT);
     {
       float part = 0.f;
+#pragma unroll 8
       for (int e = tid; e < NT * PT; e += 256) {
-        const int n = e / PT, p = e % PT;
-        part += h0[n * LV + p] * g1[n * LV + p];
+        const int n = e % NT, p = e / NT;
+        part += h0[p * LQ + n] * g1[p * LQ + n];
       }
       part = wave_sum(part);
       if (l == 0) atomicAdd(hsum, part);
@@ -971,38 +993,48 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
                                                      GradOut o, float* d_c, float* d_b,
                                                      float* d_dt, float* d_trap,
                                                      float* d_angles) {
-  extern __shared__ float suf[];  // [H][AM]
+  extern __shared__ float sm[];
+  float* suf = sm;                    // [H][AM] phase gradient from later chunks
+  float* angs = suf + s.H * AM;       // [C][A + 1] the chunk's angle rates
+  float* dts = angs + C * (s.A + 1);  // [C][H + 1] the chunk's dt
   const int b = blockIdx.x / s.NC, c = blockIdx.x % s.NC, tid = tix();
+  const int rows = min(C, s.T - c * C);
+  for (int e = tid; e < rows * s.A; e += 256) {
+    const int t = e / s.A, j = e % s.A;
+    angs[t * (s.A + 1) + j] = ang[tok_index(s, b, c * C + t) * s.A + j];
+  }
+  for (int e = tid; e < rows * s.H; e += 256) {
+    const int t = e / s.H, h = e % s.H;
+    dts[t * (s.H + 1) + h] = dt[tok_index(s, b, c * C + t) * s.H + h];
+  }
   for (int e = tid; e < s.H * s.A; e += 256) {
     const int h = e / s.A, j = e % s.A;
     float acc = 0.f;
+#pragma unroll 8
     for (int cc = c + 1; cc < s.NC; ++cc) acc += o.D[phase_offset(s, b, h, cc) + j];
     suf[h * AM + j] = acc;
   }
   __syncthreads();
   const long tp = (long)s.NC * C;
-  for (int e = tid; e < C * s.H; e += 256) {
+  for (int e = tid; e < rows * s.H; e += 256) {
     const int t = e / s.H, h = e % s.H, tt = c * C + t;
-    if (tt >= s.T) continue;
     const long i = tok_index(s, b, tt) * s.H + h;
-    const float d = dt[i], sig = 1.f / (1.f + expf(-trap[i]));
+    const float d = dts[t * (s.H + 1) + h], sig = 1.f / (1.f + expf(-trap[i]));
     const float dg = o.dgam[i], dprev = tt > 0 ? o.dscale[i - s.H] : 0.f;
     float carried = 0.f;
-    for (int j = 0; j < s.A; ++j) carried += suf[h * AM + j] * ang[tok_index(s, b, tt) * s.A + j];
+    for (int j = 0; j < s.A; ++j) carried += suf[h * AM + j] * angs[t * (s.A + 1) + j];
     d_dt[i] = dg * sig + dprev * (1.f - sig) + o.ddt_loc[i] + carried;
     d_trap[i] = (dg - dprev) * d * sig * (1.f - sig);
   }
-  for (int e = tid; e < C * s.A; e += 256) {
+  for (int e = tid; e < rows * s.A; e += 256) {
     const int t = e / s.A, j = e % s.A, tt = c * C + t;
-    if (tt >= s.T) continue;
     float acc = 0.f;
     for (int g = 0; g < groups; ++g) acc += o.dang_part[(((long)g * s.B + b) * tp + tt) * AM + j];
-    for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dt[tok_index(s, b, tt) * s.H + h];
+    for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dts[t * (s.H + 1) + h];
     d_angles[tok_index(s, b, tt) * s.A + j] = acc;
   }
-  for (int e = tid; e < C * s.N; e += 256) {
+  for (int e = tid; e < rows * s.N; e += 256) {
     const int t = e / s.N, n = e % s.N, tt = c * C + t;
-    if (tt >= s.T) continue;
     float ac = 0.f, ab = 0.f;
     for (int g = 0; g < groups; ++g) {
       const long at = (((long)g * s.B + b) * tp + tt) * NT + n;
