@@ -354,6 +354,35 @@ __device__ void load_state(const float* src, float* dst) {
   }
 }
 
+// Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
+// takes token t = e % C (consecutive lanes, conflict-free LDS stores) and
+// columns 4 (e / C) .. +3; zeros past T and P.
+__device__ void load_values_t(const Shape& s, const float* src, int b, int c, int h,
+                              float* dst) {
+  f4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tix() + 256 * i, t = e % C, p = 4 * (e / C), tt = c * C + t;
+    v[i] = f4{0.f, 0.f, 0.f, 0.f};
+    if (tt < s.T) {
+      const float* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
+      if (s.P % 4 == 0) {
+        if (p < s.P) v[i] = *reinterpret_cast<const f4*>(row + p);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (p + k < s.P) v[i][k] = row[p + k];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tix() + 256 * i, t = e % C, p = 4 * (e / C);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[(p + k) * LV + t] = v[i][k];
+  }
+}
+
 // A stored [NT][PT] state tile into LDS transposed, [PT][LQ]: thread e takes
 // row n = e % NT (consecutive lanes, conflict-free LDS stores) and columns
 // 4 (e / NT) .. +3, all read before any is stored.
@@ -535,8 +564,8 @@ __device__ __forceinline__ int xcd_block(int total) {
 // ---------------------------------------------------------------------------
 // Output of one (b, chunk, h): y = (S o W) V + diag(e^p) Q S0 with scores
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
-// LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 [NT][LV] (first the
-// phase table), V [C][LV], scalars.
+// LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 transposed
+// [PT][LQ] (first the phase table), V transposed [PT][LV], scalars.
 __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, const float* bk,
                                                   const float* x, const float* adt,
                                                   const float* dt, const float* trap,
@@ -569,15 +598,17 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
     rotate_rows<2>(s, src, bsrc, dst, tab, b, c);
   }
   __syncthreads();
-  load_state(starts + state_offset(s, b, h, c), h0);
-  load_values(s, x, b, c, h, nullptr, vt);
+  // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
+  // every product reads both operands contiguously along k.
+  load_state_t(starts + state_offset(s, b, h, c), h0);
+  load_values_t(s, x, b, c, h, vt);
   __syncthreads();
 
   f4 sco[4], qh[4];
   zero(sco);
   zero(qh);
   mma_first<LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
-  mma<4, LQ, 1, LV, 1>(qh, qt, 16 * w, h0, 0, 0, NT);
+  mma<4, LQ, 1, 1, LQ>(qh, qt, 16 * w, h0, 0, 0, NT);
   __syncthreads();  // every wave is done with K
   float* gs = kt;
 #pragma unroll
@@ -595,7 +626,8 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
   // Each wave reads only its own rows of S o W.
   f4 acc[4];
   zero(acc);
-  mma<4, LV, 1, LV, 1>(acc, gs, 16 * w, vt, 0, 0, 16 * (w + 1));
+  // B(s, p) = Vt[p * LV + s].
+  mma<4, LV, 1, 1, LV>(acc, gs, 16 * w, vt, 0, 0, 16 * (w + 1));
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
