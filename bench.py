@@ -91,6 +91,7 @@ KERNEL_WORK = {
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "config2_hbm_traffic.md")
 DECODE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "config4_decode_hbm_traffic.md")
+MAMBA3_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "mamba3_scan_hbm_traffic.md")
 
 # Config 4 (decode): 2048 sequences x 8 heads of resident 64x64 states.
 DECODE_METRIC = "decode-step tokens/sec, 2048 sequences x 8 heads d64 resident states; % HBM BW"
@@ -799,7 +800,8 @@ def main_mamba3(args):
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / FP32_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic(dominant, MAMBA3_TRAFFIC_SUMMARY),
+            "traffic_unit": "B per launch (rocprofv3, profiles/mamba3_scan_hbm_traffic.md)",
             "algorithmic_flop": MAMBA3_FLOP[dominant] * units,
         },
         "kernels": kernels,
