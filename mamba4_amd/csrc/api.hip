@@ -166,7 +166,8 @@ int configure() {
              {(const void*)m3::walk_kernel<false>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true>, m3::kWalkLds},
              {(const void*)m3::out_kernel, m3::kOutLds},
-             {(const void*)m3::grad_kernel, m3::kGradLds}};
+             {(const void*)m3::grad_kernel, m3::kGradLds},
+             {(const void*)m3::finish_kernel, m3::kFinishLdsMax}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)k.bytes);
@@ -1097,15 +1098,14 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
   });
   if (rc) return rc;
   rc = launch("m3_grad", st, [&] {
-    hipLaunchKernelGGL(m3::grad_kernel, dim3(B * s.NC * groups), dim3(256), m3::kGradLds, st, s,
+    hipLaunchKernelGGL(m3::grad_kernel, dim3(B * s.NC * groups), dim3(512), m3::kGradLds, st, s,
                        groups, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases,
                        starts, ws.dh1, d_y, o);
   });
   if (rc) return rc;
   rc = launch("m3_finish", st, [&] {
-    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC), dim3(256),
-                       (size_t)H * m3::AM * sizeof(float), st, s, groups, dt, trap_logits, angles,
-                       o, d_c, d_b, d_dt, d_trap, d_angles);
+    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC), dim3(256), m3::finish_lds(H, A), st,
+                       s, groups, dt, trap_logits, angles, o, d_c, d_b, d_dt, d_trap, d_angles);
   });
   if (rc) return rc;
   return launch("m3_bias", st, [&] {

@@ -149,6 +149,18 @@ __device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const 
   }
 }
 
+// mma over the first jn (0..2, the same for the whole wave) of two column
+// tiles, each count its own straight-line instantiation.
+template <int AR, int AK, int BK, int BC>
+__device__ __forceinline__ void mma_first2(f4 (&acc)[2], const float* A, int r0, const float* B,
+                                           int c0, int kb, int ke, int jn) {
+  if (jn >= 2) {
+    mma<2, AR, AK, BK, BC>(acc, A, r0, B, c0, kb, ke);
+  } else if (jn == 1) {
+    mma<1, AR, AK, BK, BC>(*reinterpret_cast<f4(*)[1]>(acc), A, r0, B, c0, kb, ke);
+  }
+}
+
 // mma over the first jn (1..4, the same for the whole wave) of four column
 // tiles: each count is its own straight-line instantiation, so no MFMA sits
 // under a per-tile branch.
@@ -226,28 +238,31 @@ __device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
 // (j < A), one token per lane, angles split over the four waves.  With
 // `advance`, th0[j] moves to the chunk's end phase (th0 lives in LDS and each
 // j belongs to one wave, whose lanes read it before lane 63 writes it).
-// This lane's token's angle rates j = w + 4 m (zeros past T and A).
+// This lane's token's angle rates j = w + NW m (zeros past T and A), for a
+// block of NW waves.
+template <int NW = 4>
 __device__ __forceinline__ void fetch_angles(const Shape& s, const float* ang, int b, int c,
-                                             float (&xs)[16]) {
+                                             float (&xs)[64 / NW]) {
   const int w = tix() >> 6, t = c * C + lane_id();
   const bool valid = t < s.T;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int j = w + 4 * m;
+  for (int m = 0; m < 64 / NW; ++m) {
+    const int j = w + NW * m;
     xs[m] = valid && j < s.A ? ang[tok_index(s, b, t) * s.A + j] : 0.f;
   }
 }
 
 // The phase table from fetched angle rates and this lane's dt.
-__device__ void phase_table(const Shape& s, const float (&rates)[16], float d, float* th0,
+template <int NW = 4>
+__device__ void phase_table(const Shape& s, const float (&rates)[64 / NW], float d, float* th0,
                             float* tab, bool advance) {
   const int l = lane_id(), w = tix() >> 6;
-  float xs[16];
+  float xs[64 / NW];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) xs[m] = rates[m] * d;
+  for (int m = 0; m < 64 / NW; ++m) xs[m] = rates[m] * d;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int j = w + 4 * m;
+  for (int m = 0; m < 64 / NW; ++m) {
+    const int j = w + NW * m;
     if (j >= s.A) break;
     const float incl = wave_scan(xs[m]);
     const float base = th0[j];
@@ -259,13 +274,14 @@ __device__ void phase_table(const Shape& s, const float (&rates)[16], float d, f
   }
 }
 
+template <int NW = 4>
 __device__ void phase_table(const Shape& s, const float* ang, const float* dt, int b, int h,
                             int c, float* th0, float* tab, bool advance) {
   const int t = c * C + lane_id();
   const float d = t < s.T ? dt[tok_index(s, b, t) * s.H + h] : 0.f;
-  float rates[16];
-  fetch_angles(s, ang, b, c, rates);
-  phase_table(s, rates, d, th0, tab, advance);
+  float rates[64 / NW];
+  fetch_angles<NW>(s, ang, b, c, rates);
+  phase_table<NW>(s, rates, d, th0, tab, advance);
 }
 
 // Rotated rows of chunk c into LDS [C][LQ]: dst[t][n] = rot(src_t + bias, theta_t)[n]
@@ -312,12 +328,13 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
 // row_scale[t] (nullptr: 1); zeros past T and P.  Four 16-byte rows pieces
 // per thread, all read before any is stored.
+template <int NTH = 256>
 __device__ void load_values(const Shape& s, const float* src, int b, int c, int h,
                             const float* row_scale, float* dst) {
-  f4 v[4];
+  f4 v[1024 / NTH];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tix() + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+  for (int i = 0; i < 1024 / NTH; ++i) {
+    const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
     const int tt = c * C + t;
     v[i] = f4{0.f, 0.f, 0.f, 0.f};
     if (tt < s.T) {
@@ -332,24 +349,25 @@ __device__ void load_values(const Shape& s, const float* src, int b, int c, int 
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tix() + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+  for (int i = 0; i < 1024 / NTH; ++i) {
+    const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
     *reinterpret_cast<f4*>(dst + t * LV + p) = row_scale ? v[i] * row_scale[t] : v[i];
   }
 }
 
 // A stored [NT][PT] state tile into LDS [NT][LV]: eight 16-byte pieces per
 // thread, all read before any is stored.
+template <int NTH = 256>
 __device__ void load_state(const float* src, float* dst) {
-  f4 v[8];
+  f4 v[2048 / NTH];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int e = tix() + 256 * i;
+  for (int i = 0; i < 2048 / NTH; ++i) {
+    const int e = tix() + NTH * i;
     v[i] = *reinterpret_cast<const f4*>(src + (e / (PT / 4)) * PT + 4 * (e % (PT / 4)));
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int e = tix() + 256 * i;
+  for (int i = 0; i < 2048 / NTH; ++i) {
+    const int e = tix() + NTH * i;
     *reinterpret_cast<f4*>(dst + (e / (PT / 4)) * LV + 4 * (e % (PT / 4))) = v[i];
   }
 }
@@ -386,16 +404,17 @@ __device__ void load_values_t(const Shape& s, const float* src, int b, int c, in
 // A stored [NT][PT] state tile into LDS transposed, [PT][LQ]: thread e takes
 // row n = e % NT (consecutive lanes, conflict-free LDS stores) and columns
 // 4 (e / NT) .. +3, all read before any is stored.
+template <int NTH = 256>
 __device__ void load_state_t(const float* src, float* dst) {
-  f4 v[8];
+  f4 v[2048 / NTH];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int e = tix() + 256 * i;
+  for (int i = 0; i < 2048 / NTH; ++i) {
+    const int e = tix() + NTH * i;
     v[i] = *reinterpret_cast<const f4*>(src + (e % NT) * PT + 4 * (e / NT));
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int e = tix() + 256 * i, n = e % NT, p = 4 * (e / NT);
+  for (int i = 0; i < 2048 / NTH; ++i) {
+    const int e = tix() + NTH * i, n = e % NT, p = 4 * (e / NT);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[(p + k) * LQ + n] = v[i][k];
   }
@@ -653,7 +672,7 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
 // from the end of the chunk: R_t = sum_{t' >= t} dtheta_t'.
 // LDS: R1 = 2 NT LV floats (Q, K; later H0, dH1; later dQ, dK), R2 = 2 NT LV
 // floats (H0, dH1; later V, dY, S o W, G), phase table [C][LA], scalars.
-__global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const float* cq,
+__global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const float* cq,
                                                    const float* bk, const float* x,
                                                    const float* adt, const float* dt,
                                                    const float* trap, const float* ang,
@@ -682,25 +701,27 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
   const int g = id % groups, c = (id / groups) % s.NC, b = id / (groups * s.NC);
   const int hpg = (s.H + groups - 1) / groups, h_begin = g * hpg;
   const int h_end = min(s.H, h_begin + hpg);
-  // This group's sums over its heads: the rotated-back row gradients of this
-  // thread's 16 (token, pair) slots and the angle gradients of its 16
-  // (token = lane, angle) slots stay in registers until the last head.
-  float2 dcacc[16], dbacc[16];
-  float dang[16];
+  // Eight waves: wave w owns row block wr = w & 3 of every 64-row tile and
+  // column half wc = w >> 2 of its columns.  This group's sums over its
+  // heads: the rotated-back row gradients of this thread's 8 (token
+  // w + 8 m, pair) slots and the angle gradients of its 8 (token = lane,
+  // angle w + 8 m) slots stay in registers until the last head.
+  float2 dcacc[8], dbacc[8];
+  float dang[8];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
+  for (int m = 0; m < 8; ++m) {
     dcacc[m] = float2{0.f, 0.f};
     dbacc[m] = float2{0.f, 0.f};
     dang[m] = 0.f;
   }
   // The chunk's raw query and key rows are the same for every head: this
-  // thread's 16 (token, pair) slots are read once and kept in registers.
-  float2 rc[16], rb[16];
+  // thread's 8 (token, pair) slots are read once and kept in registers.
+  float2 rc[8], rb[8];
   {
     const int tid = tix(), l = tid & 63, w = tid >> 6;
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const int tt = c * C + w + 4 * m;
+    for (int m = 0; m < 8; ++m) {
+      const int tt = c * C + w + 8 * m;
       const bool ok = 2 * l < s.N && tt < s.T;
       rc[m] = ok ? *reinterpret_cast<const float2*>(cq + tok_index(s, b, tt) * s.N + 2 * l)
                  : float2{0.f, 0.f};
@@ -711,7 +732,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
 
   for (int h = h_begin; h < h_end; ++h) {
     const int tid = tix(), l = tid & 63, r = l & 15, q = l >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
     const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
     if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
@@ -720,6 +741,9 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
       s_colF[tid] = 0.f;
       s_colE[tid] = 0.f;
       s_ddt[tid] = 0.f;
+      s_qd[tid] = 0.f;
+      s_g[tid] = 0.f;
+      s_rowE[tid] = 0.f;
     }
     if (tid < NT) {
       qbacc[tid] = 0.f;
@@ -727,7 +751,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     }
     if (tid == 0) hsum[0] = 0.f;
     __syncthreads();
-    phase_table(s, ang, dt, b, h, c, th0, tab, false);
+    phase_table<8>(s, ang, dt, b, h, c, th0, tab, false);
     __syncthreads();
     float* qt = R1;
     float* kt = R1 + C * LQ;
@@ -735,8 +759,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     // K dH1 with both operands contiguous along n.
     float* h0 = R2;
     float* g1 = R2 + NT * LV;
-    load_state_t(starts + state_offset(s, b, h, c), h0);
-    load_state_t(dh1 + state_offset(s, b, h, c), g1);
+    load_state_t<512>(starts + state_offset(s, b, h, c), h0);
+    load_state_t<512>(dh1 + state_offset(s, b, h, c), g1);
     {
       const bool col = n2 < s.N;
       float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
@@ -745,8 +769,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
       }
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int t = w + 4 * m, tt = c * C + t;
+      for (int m = 0; m < 8; ++m) {
+        const int t = w + 8 * m, tt = c * C + t;
         const bool valid = col && tt < s.T;
         float sn = 0.f, cs = 1.f;
         if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
@@ -760,19 +784,21 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     }
     __syncthreads();
 
-    // Q H0, K dH1 and the scores (wave w: rows 16 w .. 16 w + 15).
-    f4 sco[4], qh[4], kg[4];
+    // Q H0, K dH1 and the scores (rows 16 wr .. +15, columns 32 wc .. +31;
+    // the scores' causal tiles jt = 2 wc + j <= wr only).
+    const int ns = min(2, max(0, wr + 1 - 2 * wc));
+    f4 sco[2], qh[2], kg[2];
     zero(sco);
     zero(qh);
     zero(kg);
-    mma_first<LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
+    mma_first2<LQ, 1, 1, LQ>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
     // B(n, p) = H0t[p * LQ + n].
-    mma<4, LQ, 1, 1, LQ>(qh, qt, 16 * w, h0, 0, 0, NT);
-    mma<4, LQ, 1, 1, LQ>(kg, kt, 16 * w, g1, 0, 0, NT);
+    mma<2, LQ, 1, 1, LQ>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
+    mma<2, LQ, 1, 1, LQ>(kg, kt, 16 * wr, g1, 32 * wc, 0, NT);
     {
       float part = 0.f;
 #pragma unroll 8
-      for (int e = tid; e < NT * PT; e += 256) {
+      for (int e = tid; e < NT * PT; e += 512) {
         const int n = e % NT, p = e / NT;
         part += h0[p * LQ + n] * g1[p * LQ + n];
       }
@@ -784,32 +810,33 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     float* dyt = R2 + C * LV;
     float* gs = R2 + 2 * C * LV;
     float* gm = R2 + 3 * C * LV;
-    load_values(s, x, b, c, h, nullptr, vt);
-    load_values(s, dy, b, c, h, nullptr, dyt);
+    load_values<512>(s, x, b, c, h, nullptr, vt);
+    load_values<512>(s, dy, b, c, h, nullptr, dyt);
     __syncthreads();
 
-    f4 dsc[4];
+    f4 dsc[2];
     zero(dsc);
     // dY V^T: A(t, p) = dY[t * LV + p], B(p, s) = V[s * LV + p].
-    mma_first<LV, 1, 1, LV>(dsc, dyt, 16 * w, vt, 0, 0, PT, w + 1);
+    mma_first2<LV, 1, 1, LV>(dsc, dyt, 16 * wr, vt, 32 * wc, 0, PT, ns);
     {
       float qd[4] = {0.f, 0.f, 0.f, 0.f}, gg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int t = 16 * w + 4 * q + i, p = 16 * j + r;
+          const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r;
           qd[i] += qh[j][i] * dyt[t * LV + p];
           gg[i] += kg[j][i] * vt[t * LV + p];
         }
       float rowE[4] = {0.f, 0.f, 0.f, 0.f};
-      float colF[4] = {0.f, 0.f, 0.f, 0.f}, colE[4] = {0.f, 0.f, 0.f, 0.f};
+      float colF[2] = {0.f, 0.f}, colE[2] = {0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j > w) {
+      for (int j = 0; j < 2; ++j) {
+        const int jt = 2 * wc + j;
+        if (jt > wr) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int t = 16 * w + 4 * q + i, u = 16 * j + r;
+            const int t = 16 * wr + 4 * q + i, u = 16 * jt + r;
             gs[t * LV + u] = 0.f;
             gm[t * LV + u] = 0.f;
           }
@@ -817,7 +844,7 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int t = 16 * w + 4 * q + i, u = 16 * j + r;
+          const int t = 16 * wr + 4 * q + i, u = 16 * jt + r;
           const float st = sco[j][i], ds = dsc[j][i];
           float wt = 0.f;
           if (t > u) {
@@ -839,72 +866,75 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
       for (int i = 0; i < 4; ++i) {
         const float a = row16_sum(qd[i]), bb = row16_sum(gg[i]), e = row16_sum(rowE[i]);
         if (r == 0) {
-          const int t = 16 * w + 4 * q + i;
-          s_qd[t] = a;
-          s_g[t] = bb;
-          s_rowE[t] = e;
+          // The two column halves of a row block add into the same rows.
+          const int t = 16 * wr + 4 * q + i;
+          atomicAdd(&s_qd[t], a);
+          atomicAdd(&s_g[t], bb);
+          atomicAdd(&s_rowE[t], e);
         }
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j > w) break;
+      for (int j = 0; j < 2; ++j) {
+        const int jt = 2 * wc + j;
+        if (jt > wr) break;
         float f = colF[j], e = colE[j];
         f += __shfl_xor(f, 16, 64);
         f += __shfl_xor(f, 32, 64);
         e += __shfl_xor(e, 16, 64);
         e += __shfl_xor(e, 32, 64);
         if (q == 0) {
-          atomicAdd(&s_colF[16 * j + r], f);
-          atomicAdd(&s_colE[16 * j + r], e);
+          atomicAdd(&s_colF[16 * jt + r], f);
+          atomicAdd(&s_colE[16 * jt + r], e);
         }
       }
     }
     __syncthreads();
 
-    f4 dq[8], dk[8], dv[4];
+    // Rows 16 wr .. +15; dQ and dK columns 64 wc .. +63, dV columns 32 wc .. +31.
+    f4 dq[4], dk[4], dv[2];
     zero(dq);
     zero(dk);
     zero(dv);
     // G K: A(t, s) = G[t * LV + s], B(s, n) = K[s * LQ + n].
-    mma<8, LV, 1, LQ, 1>(dq, gm, 16 * w, kt, 0, 0, 16 * (w + 1));
+    mma<4, LV, 1, LQ, 1>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
     // G^T Q: A(s, t) = G[t * LV + s], B(t, n) = Q[t * LQ + n].
-    mma<8, 1, LV, LQ, 1>(dk, gm, 16 * w, qt, 0, 16 * w, C);
+    mma<4, 1, LV, LQ, 1>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
     // (S o W)^T dY.
-    mma<4, 1, LV, LV, 1>(dv, gs, 16 * w, dyt, 0, 16 * w, C);
+    mma<2, 1, LV, LV, 1>(dv, gs, 16 * wr, dyt, 32 * wc, 16 * wr, C);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * w + 4 * q + i, p = 16 * j + r, tt = c * C + t;
+        const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r, tt = c * C + t;
         if (tt < s.T && p < s.P)
           o.dx[(tok_index(s, b, tt) * s.H + h) * s.P + p] = dv[j][i] + S.u[t] * kg[j][i];
       }
     __syncthreads();  // Q, K, S o W and G are no longer read
-    for (int e = tid; e < C * PT; e += 256) {
+    for (int e = tid; e < C * PT; e += 512) {
       const int t = e / PT, p = e % PT;
       dyt[t * LV + p] *= S.ep[t];
       vt[t * LV + p] *= S.u[t];
     }
-    load_state(starts + state_offset(s, b, h, c), R1);
-    load_state(dh1 + state_offset(s, b, h, c), R1 + NT * LV);
+    load_state<512>(starts + state_offset(s, b, h, c), R1);
+    load_state<512>(dh1 + state_offset(s, b, h, c), R1 + NT * LV);
     __syncthreads();
     // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0[n * LV + p].
-    mma<8, LV, 1, 1, LV>(dq, dyt, 16 * w, R1, 0, 0, PT);
-    mma<8, LV, 1, 1, LV>(dk, vt, 16 * w, R1 + NT * LV, 0, 0, PT);
+    mma<4, LV, 1, 1, LV>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
+    mma<4, LV, 1, 1, LV>(dk, vt, 16 * wr, R1 + NT * LV, 64 * wc, 0, PT);
     __syncthreads();
     float* dqt = R1;
     float* dkt = R1 + C * LQ;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * w + 4 * q + i, n = 16 * j + r;
+        const int t = 16 * wr + 4 * q + i, n = 64 * wc + 16 * j + r;
         dqt[t * LQ + n] = dq[j][i];
         dkt[t * LQ + n] = dk[j][i];
       }
     __syncthreads();
 
-    // Through the rotations: one pair per lane, tokens w, w + 4, ...
+    // Through the rotations: one pair per lane, tokens w, w + 8, ...
     {
       const bool col = n2 < s.N;
       float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
@@ -914,8 +944,8 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
       }
       float2 sq = float2{0.f, 0.f}, sk = float2{0.f, 0.f};
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int t = w + 4 * m, tt = c * C + t;
+      for (int m = 0; m < 8; ++m) {
+        const int t = w + 8 * m, tt = c * C + t;
         if (!col || tt >= s.T) continue;
         const float2 gq = *reinterpret_cast<const float2*>(dqt + t * LQ + n2);
         const float2 gk = *reinterpret_cast<const float2*>(dkt + t * LQ + n2);
@@ -955,15 +985,15 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     {
       const int tt = c * C + l;
       const bool valid = tt < s.T;
-      float ddt = 0.f, av[16];
+      float ddt = 0.f, av[8];
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int j = w + 4 * m;
+      for (int m = 0; m < 8; ++m) {
+        const int j = w + 8 * m;
         av[m] = valid && j < s.A ? ang[tok_index(s, b, tt) * s.A + j] : 0.f;
       }
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int j = w + 4 * m;
+      for (int m = 0; m < 8; ++m) {
+        const int j = w + 8 * m;
         if (j >= s.A) break;
         const float xv = valid ? tab[l * LA + j] : 0.f;
         const float incl = wave_scan(xv), tot = lane63(incl);
@@ -1007,11 +1037,11 @@ __global__ __launch_bounds__(256) void grad_kernel(Shape s, int groups, const fl
     float* dbp = o.db_part + ((long)g * s.B + b) * tp * NT;
     float* dap = o.dang_part + ((long)g * s.B + b) * tp * AM;
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const long at = (long)(c * C + w + 4 * m) * NT + 2 * l;
+    for (int m = 0; m < 8; ++m) {
+      const long at = (long)(c * C + w + 8 * m) * NT + 2 * l;
       *reinterpret_cast<float2*>(dcp + at) = dcacc[m];
       *reinterpret_cast<float2*>(dbp + at) = dbacc[m];
-      dap[(long)(c * C + l) * AM + w + 4 * m] = dang[m];
+      dap[(long)(c * C + l) * AM + w + 8 * m] = dang[m];
     }
   }
 }
