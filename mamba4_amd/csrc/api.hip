@@ -1049,7 +1049,7 @@ int m3s_forward(const float* c, const float* b, const float* x, const float* adt
   });
   if (rc) return rc;
   return launch("m3_out", st, [&] {
-    hipLaunchKernelGGL(m3::out_kernel, dim3(B * s.NC * H), dim3(256), m3::kOutLds, st, s, c, b,
+    hipLaunchKernelGGL(m3::out_kernel, dim3(B * s.NC * H), dim3(512), m3::kOutLds, st, s, c, b,
                        x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, y);
   });
 }

@@ -289,16 +289,16 @@ __device__ void phase_table(const Shape& s, const float* ang, const float* dt, i
 // (2j, 2j+1) per lane, tokens w, w + 4, ... per wave; every global read is
 // issued before the first rotation.  With two sources both are rotated by
 // the same angles.
-template <int NSRC>
+template <int NSRC, int NW = 4>
 __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
                             const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
                             int b, int c) {
   const int j = lane_id(), n = 2 * j, w = tix() >> 6;
   const bool col = n < s.N;
-  float2 u[NSRC][16];
+  float2 u[NSRC][64 / NW];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int tt = c * C + w + 4 * m;
+  for (int m = 0; m < 64 / NW; ++m) {
+    const int tt = c * C + w + NW * m;
     const bool valid = col && tt < s.T;
 #pragma unroll
     for (int k = 0; k < NSRC; ++k)
@@ -310,8 +310,8 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
   for (int k = 0; k < NSRC; ++k)
     bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int t = w + 4 * m, tt = c * C + t;
+  for (int m = 0; m < 64 / NW; ++m) {
+    const int t = w + NW * m, tt = c * C + t;
     const bool valid = col && tt < s.T;
     float sn = 0.f, cs = 1.f;
     if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
@@ -375,12 +375,13 @@ __device__ void load_state(const float* src, float* dst) {
 // Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
 // takes token t = e % C (consecutive lanes, conflict-free LDS stores) and
 // columns 4 (e / C) .. +3; zeros past T and P.
+template <int NTH = 256>
 __device__ void load_values_t(const Shape& s, const float* src, int b, int c, int h,
                               float* dst) {
-  f4 v[4];
+  f4 v[1024 / NTH];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tix() + 256 * i, t = e % C, p = 4 * (e / C), tt = c * C + t;
+  for (int i = 0; i < 1024 / NTH; ++i) {
+    const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C), tt = c * C + t;
     v[i] = f4{0.f, 0.f, 0.f, 0.f};
     if (tt < s.T) {
       const float* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
@@ -394,8 +395,8 @@ __device__ void load_values_t(const Shape& s, const float* src, int b, int c, in
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tix() + 256 * i, t = e % C, p = 4 * (e / C);
+  for (int i = 0; i < 1024 / NTH; ++i) {
+    const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[(p + k) * LV + t] = v[i][k];
   }
@@ -585,7 +586,7 @@ __device__ __forceinline__ int xcd_block(int total) {
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
 // LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 transposed
 // [PT][LQ] (first the phase table), V transposed [PT][LV], scalars.
-__global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, const float* bk,
+__global__ __launch_bounds__(512) void out_kernel(Shape s, const float* cq, const float* bk,
                                                   const float* x, const float* adt,
                                                   const float* dt, const float* trap,
                                                   const float* ang, const float* qb,
@@ -602,56 +603,59 @@ __global__ __launch_bounds__(256) void out_kernel(Shape s, const float* cq, cons
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
   const int total = s.B * s.NC * s.H, id = xcd_block(total);
   const int h = id % s.H, c = (id / s.H) % s.NC, b = id / (s.H * s.NC);
+  // Eight waves: wave w owns row block wr = w & 3 and column half wc = w >> 2.
   const int tid = tix(), l = lane_id(), r = l & 15, q = l >> 4;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
 
   if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
   if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
   __syncthreads();
-  phase_table(s, ang, dt, b, h, c, th0, tab, false);
+  phase_table<8>(s, ang, dt, b, h, c, th0, tab, false);
   __syncthreads();
   {
     const float* const src[2] = {cq, bk};
     const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
     float* const dst[2] = {qt, kt};
-    rotate_rows<2>(s, src, bsrc, dst, tab, b, c);
+    rotate_rows<2, 8>(s, src, bsrc, dst, tab, b, c);
   }
   __syncthreads();
   // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
   // every product reads both operands contiguously along k.
-  load_state_t(starts + state_offset(s, b, h, c), h0);
-  load_values_t(s, x, b, c, h, vt);
+  load_state_t<512>(starts + state_offset(s, b, h, c), h0);
+  load_values_t<512>(s, x, b, c, h, vt);
   __syncthreads();
 
-  f4 sco[4], qh[4];
+  const int ns = min(2, max(0, wr + 1 - 2 * wc));
+  f4 sco[2], qh[2];
   zero(sco);
   zero(qh);
-  mma_first<LQ, 1, 1, LQ>(sco, qt, 16 * w, kt, 0, 0, NT, w + 1);
-  mma<4, LQ, 1, 1, LQ>(qh, qt, 16 * w, h0, 0, 0, NT);
+  mma_first2<LQ, 1, 1, LQ>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+  mma<2, LQ, 1, 1, LQ>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
   __syncthreads();  // every wave is done with K
   float* gs = kt;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (j > w) break;
+  for (int j = 0; j < 2; ++j) {
+    const int jt = 2 * wc + j;
+    if (jt > wr) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * q + i, u = 16 * j + r;
+      const int t = 16 * wr + 4 * q + i, u = 16 * jt + r;
       float wt = 0.f;
       if (t > u) wt = expf(fminf(S.p[t] - S.p[u], 0.f)) * S.scale[u];
       else if (t == u) wt = S.gam[t];
       gs[t * LV + u] = sco[j][i] * wt;
     }
   }
-  // Each wave reads only its own rows of S o W.
-  f4 acc[4];
+  __syncthreads();  // a row block's S o W comes from both of its waves
+  f4 acc[2];
   zero(acc);
   // B(s, p) = Vt[p * LV + s].
-  mma<4, LV, 1, 1, LV>(acc, gs, 16 * w, vt, 0, 0, 16 * (w + 1));
+  mma<2, LV, 1, 1, LV>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * q + i, p = 16 * j + r, tt = c * C + t;
+      const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r, tt = c * C + t;
       if (tt < s.T && p < s.P)
         y[(tok_index(s, b, tt) * s.H + h) * s.P + p] = acc[j][i] + S.ep[t] * qh[j][i];
     }
