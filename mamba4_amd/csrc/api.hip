@@ -1043,7 +1043,7 @@ int m3s_forward(const float* c, const float* b, const float* x, const float* adt
   hipStream_t st = static_cast<hipStream_t>(stream);
   const m3::Shape s{B, T, H, N, P, A, (T + m3::C - 1) / m3::C};
   int rc = launch("m3_walk", st, [&] {
-    hipLaunchKernelGGL(m3::walk_kernel<false>, dim3(B * H), dim3(256), m3::kWalkLds, st, s, b,
+    hipLaunchKernelGGL(m3::walk_kernel<false>, dim3(B * H), dim3(512), m3::kWalkLds, st, s, b,
                        k_bias, x, adt, dt, trap_logits, angles, phases, starts, nullptr,
                        final_state);
   });
@@ -1092,7 +1092,7 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
                       ws.ddt_loc,  ws.D,         ws.qb_part,    ws.kb_part,
                       ws.dc_part,  ws.db_part,   ws.dang_part};
   int rc = launch("m3_walk_bwd", st, [&] {
-    hipLaunchKernelGGL(m3::walk_kernel<true>, dim3(B * H), dim3(256), m3::kWalkLds, st, s, c,
+    hipLaunchKernelGGL(m3::walk_kernel<true>, dim3(B * H), dim3(512), m3::kWalkLds, st, s, c,
                        q_bias, d_y, adt, dt, trap_logits, angles, const_cast<float*>(phases),
                        ws.dh1, d_final, nullptr);
   });

@@ -438,7 +438,7 @@ __device__ __forceinline__ long phase_offset(const Shape& s, int b, int h, int c
 // S <- e^{p_L} S + Q^T (e^p dy).
 // LDS: rows [C][LQ], vals [C][LV], phase table [C][LA], th0 [AM], scalars.
 template <bool BWD>
-__global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, const float* bias,
+__global__ __launch_bounds__(512) void walk_kernel(Shape s, const float* rows, const float* bias,
                                                    const float* vals, const float* adt,
                                                    const float* dt, const float* trap,
                                                    const float* ang, float* theta0, float* saved,
@@ -453,16 +453,16 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
   const int bh = blockIdx.x, b = bh / s.H, h = bh % s.H;
   const int tid = tix(), w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
 
-  // Wave w holds state rows 32 w .. 32 w + 31 as two 16-row strips of four
-  // 16-column tiles.
-  f4 acc[2][4];
+  // Eight waves: wave w holds state rows 16 w .. 16 w + 15 as four 16-column
+  // tiles.
+  f4 acc[1][4];
 #pragma unroll
-  for (int rt2 = 0; rt2 < 2; ++rt2) {
+  for (int rt2 = 0; rt2 < 1; ++rt2) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int n = 32 * w + 16 * rt2 + 4 * q + i, p = 16 * j + r;
+        const int n = 16 * w + 4 * q + i, p = 16 * j + r;
         float v = 0.f;
         if (BWD && init && n < s.N && p < s.P) v = init[(((long)b * s.H + h) * s.N + n) * s.P + p];
         acc[rt2][j][i] = v;
@@ -477,23 +477,23 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
   // Every global input of a chunk is fetched into registers one chunk ahead,
   // while the previous chunk's product runs.
   TokenIn tin;
-  float rates[16], th_in = 0.f;
-  float2 u[16];
-  f4 v[4];
+  float rates[8], th_in = 0.f;
+  float2 u[8];
+  f4 v[2];
   auto fetch = [&](int c) {
     tin = fetch_token(s, adt, dt, trap, b, h, c);
-    fetch_angles(s, ang, b, c, rates);
+    fetch_angles<8>(s, ang, b, c, rates);
     if (BWD && tid < s.A) th_in = theta0[phase_offset(s, b, h, c) + tid];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const int tt = c * C + w + 4 * m;
+    for (int m = 0; m < 8; ++m) {
+      const int tt = c * C + w + 8 * m;
       u[m] = col && tt < s.T
                  ? *reinterpret_cast<const float2*>(rows + tok_index(s, b, tt) * s.N + 2 * l)
                  : float2{0.f, 0.f};
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
       v[i] = f4{0.f, 0.f, 0.f, 0.f};
       if (tt < s.T) {
         const float* row = vals + (tok_index(s, b, tt) * s.H + h) * s.P;
@@ -519,12 +519,12 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
       if (tid < s.A) theta0[phase_offset(s, b, h, c) + tid] = th0[tid];
     }
     __syncthreads();
-    phase_table(s, rates, tin.d, th0, tab, !BWD);
+    phase_table<8>(s, rates, tin.d, th0, tab, !BWD);
     __syncthreads();
     // Rotated rows (one pair per lane) and scaled values into LDS.
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const int t = w + 4 * m, tt = c * C + t;
+    for (int m = 0; m < 8; ++m) {
+      const int t = w + 8 * m, tt = c * C + t;
       const bool valid = col && tt < s.T;
       float sn = 0.f, cs = 1.f;
       if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
@@ -534,41 +534,33 @@ __global__ __launch_bounds__(256) void walk_kernel(Shape s, const float* rows, c
     }
     const float* row_scale = BWD ? S.ep : S.u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
       *reinterpret_cast<f4*>(vt + t * LV + p) = v[i] * row_scale[t];
     }
     // Store this chunk's state (a lane's four rows of one column).
     float* out = saved + state_offset(s, b, h, c);
 #pragma unroll
-    for (int rt2 = 0; rt2 < 2; ++rt2)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          out[(32 * w + 16 * rt2 + 4 * q + i) * PT + 16 * j + r] = acc[rt2][j][i];
+      for (int i = 0; i < 4; ++i) out[(16 * w + 4 * q + i) * PT + 16 * j + r] = acc[0][j][i];
     if (step + 1 < s.NC) fetch(BWD ? c - 1 : c + 1);
     __syncthreads();
     const float decay = expf(S.p[63]);
 #pragma unroll
-    for (int rt2 = 0; rt2 < 2; ++rt2) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[rt2][j] *= decay;
-      // rows^T vals: A(n, t) = rt[t * LQ + n], B(t, p) = vt[t * LV + p].
-      mma<4, 1, LQ, LV, 1>(acc[rt2], rt, 32 * w + 16 * rt2, vt, 0, 0, C);
-    }
+    for (int j = 0; j < 4; ++j) acc[0][j] *= decay;
+    // rows^T vals: A(n, t) = rt[t * LQ + n], B(t, p) = vt[t * LV + p].
+    mma<4, 1, LQ, LV, 1>(acc[0], rt, 16 * w, vt, 0, 0, C);
   }
   if (!BWD && final_state) {
 #pragma unroll
-    for (int rt2 = 0; rt2 < 2; ++rt2)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = 32 * w + 16 * rt2 + 4 * q + i, p = 16 * j + r;
-          if (n < s.N && p < s.P)
-            final_state[(((long)b * s.H + h) * s.N + n) * s.P + p] = acc[rt2][j][i];
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int n = 16 * w + 4 * q + i, p = 16 * j + r;
+        if (n < s.N && p < s.P)
+          final_state[(((long)b * s.H + h) * s.N + n) * s.P + p] = acc[0][j][i];
+      }
   }
 }
 
