@@ -1074,6 +1074,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   }
   __syncthreads();
   const long tp = (long)s.NC * C;
+#pragma unroll 4
   for (int e = tid; e < rows * s.H; e += 256) {
     const int t = e / s.H, h = e % s.H, tt = c * C + t;
     const long i = tok_index(s, b, tt) * s.H + h;
@@ -1084,6 +1085,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     d_dt[i] = dg * sig + dprev * (1.f - sig) + o.ddt_loc[i] + carried;
     d_trap[i] = (dg - dprev) * d * sig * (1.f - sig);
   }
+#pragma unroll 4
   for (int e = tid; e < rows * s.A; e += 256) {
     const int t = e / s.A, j = e % s.A, tt = c * C + t;
     float acc = 0.f;
@@ -1091,6 +1093,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dts[t * (s.H + 1) + h];
     d_angles[tok_index(s, b, tt) * s.A + j] = acc;
   }
+#pragma unroll 8
   for (int e = tid; e < rows * s.N; e += 256) {
     const int t = e / s.N, n = e % s.N, tt = c * C + t;
     float ac = 0.f, ab = 0.f;
