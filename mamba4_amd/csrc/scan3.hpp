@@ -38,6 +38,13 @@ struct GradOut {
 constexpr size_t kWalkLds = (size_t)(C * LQ + C * LV + C * LA + AM + 384) * sizeof(float);
 constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
 constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1096) * sizeof(float);
+// finish_kernel: [H][AM] + [C][A + 1] + [C][H + 1] floats, at most this.
+constexpr int kMaxHeads = 128;
+constexpr size_t kFinishLdsMax =
+    (size_t)(kMaxHeads * AM + C * (AM + 1) + C * (kMaxHeads + 1)) * sizeof(float);
+inline size_t finish_lds(int H, int A) {
+  return (size_t)(H * AM + C * (A + 1) + C * (H + 1)) * sizeof(float);
+}
 
 template <bool BWD>
 __global__ void walk_kernel(Shape, const float*, const float*, const float*, const float*,
