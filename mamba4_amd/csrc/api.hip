@@ -1104,7 +1104,7 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
   });
   if (rc) return rc;
   rc = launch("m3_finish", st, [&] {
-    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC), dim3(256), m3::finish_lds(H, A), st,
+    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC * 4), dim3(256), m3::finish_lds(H, A), st,
                        s, groups, dt, trap_logits, angles, o, d_c, d_b, d_dt, d_trap, d_angles);
   });
   if (rc) return rc;

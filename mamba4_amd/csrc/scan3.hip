@@ -25,7 +25,7 @@
 //                       of the chunk for the group's heads; the shared rows'
 //                       gradients accumulate over the group's heads in
 //                       registers.
-//   finish_kernel       one block per (b, chunk): sums the groups, adds the
+//   finish_kernel       four blocks per (b, chunk): sums the groups, adds the
 //                       phase gradient carried from later chunks, and turns
 //                       gamma / scale gradients into dt and trap gradients.
 //   bias_kernel         one block per head: the bias gradients.
@@ -1043,9 +1043,10 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
 }
 
 // ---------------------------------------------------------------------------
-// Per (b, chunk): phase gradients carried from later chunks, the group sums,
-// and the dt / trap gradients (gamma = dt sigma, prev = dt (1 - sigma);
-// scale_t = gamma_t + prev_{t+1}, so d prev_t = d scale_{t-1}).
+// Per (b, chunk, quarter of its tokens): phase gradients carried from later
+// chunks, the group sums, and the dt / trap gradients (gamma = dt sigma,
+// prev = dt (1 - sigma); scale_t = gamma_t + prev_{t+1}, so
+// d prev_t = d scale_{t-1}).
 __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const float* dt,
                                                      const float* trap, const float* ang,
                                                      GradOut o, float* d_c, float* d_b,
@@ -1055,14 +1056,16 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   float* suf = sm;                    // [H][AM] phase gradient from later chunks
   float* angs = suf + s.H * AM;       // [C][A + 1] the chunk's angle rates
   float* dts = angs + C * (s.A + 1);  // [C][H + 1] the chunk's dt
-  const int b = blockIdx.x / s.NC, c = blockIdx.x % s.NC, tid = tix();
-  const int rows = min(C, s.T - c * C);
+  // Four blocks per (b, chunk), each taking 16 of its tokens.
+  const int part = blockIdx.x % 4, bc = blockIdx.x / 4;
+  const int b = bc / s.NC, c = bc % s.NC, tid = tix();
+  const int t0 = 16 * part, rows = max(0, min(16, s.T - c * C - t0));
   for (int e = tid; e < rows * s.A; e += 256) {
-    const int t = e / s.A, j = e % s.A;
+    const int t = t0 + e / s.A, j = e % s.A;
     angs[t * (s.A + 1) + j] = ang[tok_index(s, b, c * C + t) * s.A + j];
   }
   for (int e = tid; e < rows * s.H; e += 256) {
-    const int t = e / s.H, h = e % s.H;
+    const int t = t0 + e / s.H, h = e % s.H;
     dts[t * (s.H + 1) + h] = dt[tok_index(s, b, c * C + t) * s.H + h];
   }
   for (int e = tid; e < s.H * s.A; e += 256) {
@@ -1076,7 +1079,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   const long tp = (long)s.NC * C;
 #pragma unroll 4
   for (int e = tid; e < rows * s.H; e += 256) {
-    const int t = e / s.H, h = e % s.H, tt = c * C + t;
+    const int t = t0 + e / s.H, h = e % s.H, tt = c * C + t;
     const long i = tok_index(s, b, tt) * s.H + h;
     const float d = dts[t * (s.H + 1) + h], sig = 1.f / (1.f + expf(-trap[i]));
     const float dg = o.dgam[i], dprev = tt > 0 ? o.dscale[i - s.H] : 0.f;
@@ -1087,7 +1090,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   }
 #pragma unroll 4
   for (int e = tid; e < rows * s.A; e += 256) {
-    const int t = e / s.A, j = e % s.A, tt = c * C + t;
+    const int t = t0 + e / s.A, j = e % s.A, tt = c * C + t;
     float acc = 0.f;
     for (int g = 0; g < groups; ++g) acc += o.dang_part[(((long)g * s.B + b) * tp + tt) * AM + j];
     for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dts[t * (s.H + 1) + h];
@@ -1095,7 +1098,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   }
 #pragma unroll 8
   for (int e = tid; e < rows * s.N; e += 256) {
-    const int t = e / s.N, n = e % s.N, tt = c * C + t;
+    const int t = t0 + e / s.N, n = e % s.N, tt = c * C + t;
     float ac = 0.f, ab = 0.f;
     for (int g = 0; g < groups; ++g) {
       const long at = (((long)g * s.B + b) * tp + tt) * NT + n;
