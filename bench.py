@@ -8,8 +8,15 @@ of synthetic config-2 input (B=16, L=1024, H=8, D=P=64, fp32), called
 through the C ABI with every buffer preallocated in HBM before the timed
 region.  Prints one JSON line with the throughput, the roofline of the
 dominant kernel (HIP events on the launch stream), the factorization's
-fp32 rate, factor-streaming bandwidth and a CPU baseline (the NumPy oracle
-on a one-row sample of the same workload, on this host's cores).
+fp32 rate (with and without the factor store), factor-streaming bandwidth
+and a CPU baseline (the NumPy oracle on config 0 and on a sample of the same
+workload, on this host's cores).
+
+With --workload ref125m the step is the same fwd+bwd at the one shape the
+reference publishes timings for (B=16, L=1024, H=12, D=64, P=128; inputs
+and projected-loss cotangents of scripts/kernel_benchmark.py:37-47,214-224),
+with vs_baseline against its TPU v4 figure (67.98 ms,
+lm/results/speed-125m/bench-kernels.json:291).
 
 With --workload config4 a step is instead one in-place decode step of
 2048 sequences x 8 heads of resident (S, C) states: the
@@ -39,7 +46,7 @@ m3s_backward; the roofline is the dominant kernel's MFMA rate against the
 fp32 peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload config2|config3|config4|mixer|mixer_read|mamba3]
+                       [--workload config2|config3|ref125m|config4|mixer|mixer_read|mamba3]
 """
 
 import argparse
@@ -59,6 +66,11 @@ sys.path.insert(0, ROOT)
 
 METRIC = "memory-read fwd+bwd tokens/sec at B16 L1024 H8 d64; % fp32 peak, % HBM BW"
 CONFIG3_METRIC = "memory-read fwd+bwd tokens/sec at B32 L1024 H12 d64, bf16 q/k/v"
+REF125M_METRIC = ("memory-read fwd+bwd tokens/sec at B16 L1024 H12 d64 P128 "
+                  "(the reference's kernel_benchmark shape)")
+# The reference's published fused fwd+bwd at that shape on one TPU v4:
+# 67.98 ms for 16 x 1024 tokens (lm/results/speed-125m/bench-kernels.json:291).
+REF125M_TPU_TOKENS_PER_S = 16 * 1024 / 0.06798
 HBM_PEAK_GBPS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 FACTOR_BYTES = 8320  # packed lower factor per token-head
@@ -147,7 +159,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--chunk", type=int, default=64)
     p.add_argument("--workload", default="config2",
-                   choices=["config2", "config3", "config4", "mixer", "mixer_read", "mamba3"])
+                   choices=["config2", "config3", "ref125m", "config4", "mixer", "mixer_read",
+                            "mamba3"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -178,28 +191,34 @@ class Problem:
             self.inputs[:3] = [t.to(torch.bfloat16) for t in self.inputs[:3]]
         self.d_output = put(data["d_output"])
         self.d_variance = put(data["d_variance"])
+        self.P = P = data["values"].shape[-1]
         f32 = dict(dtype=torch.float32, device=dev)
         self.fwd_out = [
-            torch.empty(B, T, H, 64, **f32),  # output
+            torch.empty(B, T, H, P, **f32),  # output
             torch.empty(B, T, H, **f32),  # variance
             torch.empty(B, H, 64, 64, **f32),  # final evidence
-            torch.empty(B, H, 64, 64, **f32),  # final cross
+            torch.empty(B, H, P, 64, **f32),  # final cross
             torch.empty(B, T, H, 64, **f32),  # solved
             torch.empty(B, T, H, _lib.FACTOR_FLOATS, **f32),  # factors
             torch.empty(B, H, starts, 64, 64, **f32),  # start evidence
-            torch.empty(B, H, count, 64, 64, **f32),  # start cross
+            torch.empty(B, H, count, P, 64, **f32),  # start cross
         ]
         self.grads = [torch.empty(t.shape, **f32) for t in self.inputs]
-        self.d_init = [torch.empty(B, H, 64, 64, **f32), torch.empty(B, H, 64, 64, **f32)]
-        self.ws_bytes = self.lib.m4mr_backward_workspace_bytes(B, T, H, 64, chunk)
+        self.d_init = [torch.empty(B, H, 64, 64, **f32), torch.empty(B, H, P, 64, **f32)]
+        self.ws_bytes = self.lib.m4mr_backward_workspace_bytes(B, T, H, P, chunk)
         self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
         self.stream = torch.cuda.current_stream().cuda_stream
 
-    def forward(self):
+    def forward(self, store=True):
+        """The forward; with store=False no factors are stored (factors = NULL,
+        the forward of a call that takes no gradient)."""
         p = [t.data_ptr() for t in self.inputs]
         o = [t.data_ptr() for t in self.fwd_out]
+        if not store:
+            o[5] = None
         entry = self.lib.m4mr_forward_bf16 if self.bf16 else self.lib.m4mr_forward
-        self.check(entry(*p, None, None, self.B, self.T, self.H, 64, self.chunk, *o, self.stream))
+        self.check(entry(*p, None, None, self.B, self.T, self.H, self.P, self.chunk, *o,
+                         self.stream))
 
     def backward(self):
         p = [t.data_ptr() for t in self.inputs]
@@ -207,7 +226,7 @@ class Problem:
         entry = self.lib.m4mr_backward_bf16 if self.bf16 else self.lib.m4mr_backward
         self.check(
             entry(
-                *p, self.B, self.T, self.H, 64, self.chunk, o[4].data_ptr(), o[5].data_ptr(),
+                *p, self.B, self.T, self.H, self.P, self.chunk, o[4].data_ptr(), o[5].data_ptr(),
                 o[6].data_ptr(), o[7].data_ptr(), self.d_output.data_ptr(),
                 self.d_variance.data_ptr(), None, None, *(g.data_ptr() for g in self.grads),
                 *(g.data_ptr() for g in self.d_init), self.workspace.data_ptr(), self.ws_bytes,
@@ -225,70 +244,24 @@ class Decode:
         import torch
 
         from mamba4_amd import _lib
+        from mamba4_amd.inputs import decode_states, device_tokens
 
         self.lib = _lib.load()
         self.check = _lib.check
-        dev = torch.device("cuda:0")
         B, H, T = DECODE_BATCH, DECODE_HEADS, DECODE_CONTEXT
-        f32 = dict(dtype=torch.float32, device=dev)
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(seed)
-        self.evidence = torch.empty(B, H, 64, 64, **f32)
-        self.cross = torch.empty(B, H, 64, 64, **f32)
-        self.floor = torch.full((H, 64), 1e-2, **f32)
-        stream = torch.cuda.current_stream().cuda_stream
-        # End states of a T-token recurrence, built slice by slice with this
-        # library's forward (config-0 distributions, lambda = sigmoid(N(3,1))).
-        R = slice_rows
-        count, starts = _lib.start_counts(T, 64)
-        scratch = [
-            torch.empty(R, T, H, 64, **f32),  # output
-            torch.empty(R, T, H, **f32),  # variance
-        ]
-        residual = [
-            torch.empty(R, T, H, 64, **f32),  # solved
-            torch.empty(R, T, H, _lib.FACTOR_FLOATS, **f32),  # factors
-            torch.empty(R, H, starts, 64, 64, **f32),
-            torch.empty(R, H, count, 64, 64, **f32),
-        ]
-        for first in range(0, B, R):
-            k, v, q, beta, log_decay = self._tokens(gen, (R, T, H), shift=True)
-            self.check(
-                self.lib.m4mr_forward(
-                    k.data_ptr(), v.data_ptr(), q.data_ptr(), beta.data_ptr(),
-                    log_decay.data_ptr(), self.floor.data_ptr(), None, None, R, T, H, 64, 64,
-                    scratch[0].data_ptr(), scratch[1].data_ptr(),
-                    self.evidence[first:first + R].data_ptr(),
-                    self.cross[first:first + R].data_ptr(),
-                    *(t.data_ptr() for t in residual), stream,
-                )
-            )
-        del scratch, residual
-        self.tokens = [self._tokens(gen, (B, H), shift=False) for _ in range(self.TOKEN_SETS)]
+        # End states of a T-token recurrence (config-0 distributions,
+        # lambda = sigmoid(N(3,1))), built by this library's forward.
+        self.evidence, self.cross, self.floor, _ = decode_states(B, H, T, seed=seed,
+                                                                  slice_rows=slice_rows)
+        gen = torch.Generator(device="cuda:0")
+        gen.manual_seed(seed + 1)
+        self.tokens = [device_tokens(gen, (B, H), shift=False) for _ in range(self.TOKEN_SETS)]
+        f32 = dict(dtype=torch.float32, device="cuda:0")
         self.output = torch.empty(B, H, 64, **f32)
         self.variance = torch.empty(B, H, **f32)
-        self.stream = stream
+        self.stream = torch.cuda.current_stream().cuda_stream
         self.calls = 0
         torch.cuda.synchronize()
-
-    @staticmethod
-    def _tokens(gen, shape, shift):
-        """q, k unit-norm N(0,1); v N(0,1); beta = sigmoid(N(0,1));
-        log_decay = log sigmoid(N(3,1)); keys shifted one token when `shift`."""
-        import torch
-        import torch.nn.functional as F
-
-        kw = dict(device=gen.device, generator=gen, dtype=torch.float32)
-        q = torch.randn(*shape, 64, **kw)
-        k = torch.randn(*shape, 64, **kw)
-        q = q / q.norm(dim=-1, keepdim=True)
-        k = k / k.norm(dim=-1, keepdim=True)
-        if shift:
-            k = torch.cat([torch.zeros_like(k[:, :1]), k[:, :-1]], dim=1)
-        v = torch.randn(*shape, 64, **kw)
-        log_decay = -F.softplus(-(torch.randn(*shape, **kw) + 3.0))
-        beta = torch.sigmoid(torch.randn(*shape, **kw))
-        return [t.contiguous() for t in (k, v, q, beta, log_decay)]
 
     def step(self):
         k, v, q, beta, log_decay = self.tokens[self.calls % self.TOKEN_SETS]
@@ -834,28 +807,87 @@ def copy_bandwidth_gbps():
     return 2 * n * 4 / seconds / 1e9
 
 
-def cpu_baseline(data):
-    """The NumPy oracle (float32) on batch row 0 of the workload, fwd+bwd."""
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def median_seconds(fn, runs=5):
+    """One warm-up call, then the median wall time of `runs` calls."""
+    fn()
+    times = []
+    for _ in range(runs):
+        start = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - start)
+    return float(np.median(times))
+
+
+def oracle_legs(data):
+    """Median seconds and token-head rates of the NumPy oracle (float32,
+    chunk 64) forward and forward+backward on `data`."""
     from oracle import memread as oracle
 
-    row = {n: data[n][:1] for n in NAMES if n != "floor"}
-    row["floor"] = data["floor"]
-    start = time.perf_counter()
-    _, res = oracle.forward(*(row[n] for n in NAMES), chunk=64, dtype=np.float32)
-    oracle.backward(res, data["d_output"][:1], data["d_variance"][:1])
-    seconds = time.perf_counter() - start
-    tokens = row["keys"].shape[1]
-    _, T, H, D = row["keys"].shape
+    args = [data[n] for n in NAMES]
+
+    def fwd():
+        return oracle.forward(*args, chunk=64, dtype=np.float32)
+
+    def fwd_bwd():
+        _, res = fwd()
+        oracle.backward(res, data["d_output"], data["d_variance"])
+
+    B, T, H, _ = data["keys"].shape
+    legs = {}
+    for label, fn in (("fwd", fwd), ("fwd_bwd", fwd_bwd)):
+        seconds = median_seconds(fn)
+        legs[label] = {"median_s": seconds, "token_heads_per_s": B * T * H / seconds}
+    return legs
+
+
+def cpu_baseline(data, workload, config0=True):
+    """The CPU baseline of the plan in BASELINE.md: this build's NumPy
+    restatement of the reference algorithm (oracle.memread, float32) on this
+    host, BLAS on every core, one warm-up then the median of five runs,
+    forward and forward+backward.  Config 0 runs in full; the benchmarked
+    workload on a sample of it (head 0 of batch row 0: the oracle's per-token
+    loop costs about the same for one head as the GPU's batch costs per
+    token-head, while a whole row takes minutes), scaled to the metric's
+    tokens/s by the workload's head count."""
+    heads = data["keys"].shape[2]
+    sample = {n: (a[:1, :, :1] if n != "floor" else a[:1]) for n, a in data.items()}
+    legs = {}
+    if config0:
+        from mamba4_amd.inputs import workload_inputs
+
+        for label, leg in oracle_legs(workload_inputs("config0", seed=0, cotangents=True)).items():
+            legs["config0_" + label + "_tokens_per_s"] = leg["token_heads_per_s"]
+    sampled = oracle_legs(sample)
+    for label, leg in sampled.items():
+        legs[workload + "_" + label + "_tokens_per_s"] = leg["token_heads_per_s"] / heads
+    T = data["keys"].shape[1]
+    threads = os.environ.get("OPENBLAS_NUM_THREADS")
     return {
-        "value": tokens / seconds,
+        "value": sampled["fwd_bwd"]["token_heads_per_s"] / heads,
         "unit": "tokens/s",
-        "cores": int(os.environ.get("OPENBLAS_NUM_THREADS", CORES)),
+        "cores": int(threads or CORES),
         "kind": "port",
         "sample": (
-            f"oracle.memread fwd+bwd in float32 NumPy on batch row 0 of the workload "
-            f"(B=1, L={T}, H={H}, D={D}; 1/16 of config 2), {seconds:.1f} s, "
-            f"BLAS threads = {os.environ.get('OPENBLAS_NUM_THREADS')}"
+            f"oracle.memread fwd+bwd in float32 NumPy on head 0 of batch row 0 of the "
+            f"{workload} workload (B=1, L={T}, H=1), median of 5 after 1 warm-up "
+            f"({sampled['fwd_bwd']['median_s']:.3f} s), scaled to tokens/s of the "
+            f"{heads}-head workload; config 0 in full; BLAS threads = {threads}, "
+            f"{CORES} cores in the affinity mask"
         ),
+        "cpu_model": cpu_model(),
+        "legs": legs,
     }
 
 
@@ -886,9 +918,14 @@ def main():
         return main_mixer(args)
     if args.workload == "mamba3":
         return main_mamba3(args)
-    data = workload_inputs(args.workload, seed=0, cotangents=True)
+    if args.workload == "ref125m":
+        from mamba4_amd.inputs import reference_benchmark_inputs
+
+        data = reference_benchmark_inputs(seed=0)
+    else:
+        data = workload_inputs(args.workload, seed=0, cotangents=True)
     problem = Problem(data, args.chunk, bf16_inputs=args.workload == "config3")
-    B, T, H = problem.B, problem.T, problem.H
+    B, T, H, P = problem.B, problem.T, problem.H, problem.P
     token_heads = B * T * H
 
     for _ in range(args.warmup):
@@ -931,19 +968,41 @@ def main():
     kernels[dominant] = total / count
     _lib.profile_reset()
     _lib.profile_select(None)
+    # The factor kernel without the factor store (a forward that takes no
+    # gradient), timed on its own after the timed region.
+    _lib.profile_select("fwd_factor")
+    _lib.profile_enable(True)
+    for _ in range(min(args.steps, 10)):
+        problem.forward(store=False)
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    total, count = _lib.profile_read("fwd_factor")
+    factor_only_ms = total / count
+    _lib.profile_reset()
+    _lib.profile_select(None)
     factor_s = kernels["fwd_factor"] / 1e3
     resolve_s = kernels["factored_solve"] / 1e3
     store_gbps = FACTOR_BYTES * token_heads / factor_s / 1e9
     load_gbps = RESOLVE_BYTES * token_heads / resolve_s / 1e9
     copy_gbps = copy_bandwidth_gbps()
 
+    vs_baseline = None
     if args.workload == "config3":
         metric = CONFIG3_METRIC
         workload = ("config3: memory-read fwd+bwd, B=32 L=1024 H=12 D=P=64, bf16 q/k/v read "
                     "natively (fp32 arithmetic), lambda = sigmoid(N(4,1)), floor 1e-2")
+    elif args.workload == "ref125m":
+        metric = REF125M_METRIC
+        workload = ("ref125m: memory-read fwd+bwd at the reference's published shape, B=16 "
+                    "L=1024 H=12 D=64 P=128 fp32, the inputs and projected-loss cotangents of "
+                    "scripts/kernel_benchmark.py:37-47,214-224")
+        vs_baseline = B * T / seconds / REF125M_TPU_TOKENS_PER_S
     else:
         metric = METRIC
         workload = "config2: memory-read fwd+bwd, B=16 L=1024 H=8 D=P=64 fp32, floor 1e-2"
+    # Contraction kernels' flop counts are per token-head at P = 64; the
+    # factor kernels' work does not depend on P.
+    p_free = P == 64 or dominant in ("fwd_factor", "factored_solve")
     line = {
         "metric": metric,
         "value": B * T / seconds,
@@ -954,7 +1013,7 @@ def main():
         "ms_per_step": seconds * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": vs_baseline,
         "dtype": "f32",
         "data": "synthetic",
         "config": {
@@ -963,17 +1022,25 @@ def main():
             "seq_len": T,
             "heads": H,
             "key_dim": 64,
-            "value_dim": 64,
+            "value_dim": P,
             "chunk": args.chunk,
         },
         # The committed rocprof traffic summary is for config 2.
-        "roofline": roofline(dominant, kernels[dominant], token_heads,
-                             traffic=args.workload == "config2"),
+        "roofline": (roofline(dominant, kernels[dominant], token_heads,
+                              traffic=args.workload == "config2") if p_free else None),
         "factorization_fp32": {
             "kernel": "fwd_factor",
             "achieved_tflops": CHOLESKY_FLOP * token_heads / factor_s / 1e12,
             "peak_tflops": FP32_PEAK_TFLOPS,
             "frac": CHOLESKY_FLOP * token_heads / factor_s / 1e12 / FP32_PEAK_TFLOPS,
+        },
+        # The same kernel without the factor store: the factorization alone.
+        "factor_only_ms": factor_only_ms,
+        "factorization_fp32_store_free": {
+            "kernel": "fwd_factor (factors = NULL)",
+            "achieved_tflops": CHOLESKY_FLOP * token_heads / factor_only_ms / 1e9,
+            "peak_tflops": FP32_PEAK_TFLOPS,
+            "frac": CHOLESKY_FLOP * token_heads / factor_only_ms / 1e9 / FP32_PEAK_TFLOPS,
         },
         "factor_streaming_hbm": {
             "store_GBps": store_gbps,
@@ -983,11 +1050,19 @@ def main():
             "copy_kernel_GBps": copy_gbps,
         },
         "kernel_ms": kernels,
-        "kernel_roofline": {k: roofline(k, v, token_heads, traffic=False)["frac"]
-                            for k, v in kernels.items()},
+        "kernel_roofline": ({k: roofline(k, v, token_heads, traffic=False)["frac"]
+                             for k, v in kernels.items()} if P == 64 else None),
     }
+    if args.workload == "ref125m":
+        line["baseline"] = {
+            "value": REF125M_TPU_TOKENS_PER_S,
+            "unit": "tokens/s",
+            "hardware": "1x TPU v4",
+            "source": "lm/results/speed-125m/bench-kernels.json:291 (67.98 ms fused fwd+bwd)",
+        }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(data)
+        line["cpu_baseline"] = cpu_baseline(data, args.workload,
+                                            config0=args.workload == "config2")
     print(json.dumps(line), flush=True)
 
 

@@ -59,7 +59,7 @@ const char* m4mr_version(void);
 const char* m4mr_last_error(void);
 
 /*
- * Forward memory read with stored factors.
+ * Forward memory read, storing each token's factor (or not, see `factors`).
  *
  * Replaces selective_memory_fused (lm/kernels/mamba4_fused.py:372-454) and
  * the forward of its custom VJP, _chunk_solve_forward
@@ -74,7 +74,11 @@ const char* m4mr_last_error(void);
  * residuals (what the backward consumes; the reference tags the
  *          equivalent arrays "memory_solve"):
  *          solved [B,T,H,D] (y_t = A_t^-1 q_t);
- *          factors [B,T,H,M4MR_FACTOR_FLOATS];
+ *          factors [B,T,H,M4MR_FACTOR_FLOATS], or NULL: the forward then
+ *          factors and solves without storing the factors, the reference's
+ *          store_factors=False mode (lm/kernels/mamba4_fused.py:183-232,
+ *          reached through the primal chunk_solve, :323-326) for forwards
+ *          that take no gradient; every other output is bit-identical;
  *          start_evidence [B,H,NS,D,D], the evidence at the start of each
  *          sub-chunk (chunks above 32 tokens split in two halves of
  *          ceil(chunk/2) tokens, so NS = 2*NC, else NS = NC);
@@ -84,6 +88,10 @@ const char* m4mr_last_error(void);
  * walk per (b, h) state sequence when B*H*(1 + P/64) reaches the device's
  * compute-unit count, else from chunk-parallel statistics plus a carry; the
  * environment variable M4MR_STATE_WALK=fused|split overrides the choice.
+ * The factor kernel's two waves per block hand the running evidence over
+ * through a bounded wait (M4MR_TURN_POLLS polls, default 65536, about 2 ms);
+ * a wait that gives up never yields a plausible wrong answer: every later
+ * solution and factor of that block's sequences is NaN.
  */
 int m4mr_forward(const float* keys, const float* values, const float* queries,
                  const float* beta, const float* log_decay, const float* floor,

@@ -29,9 +29,9 @@ __global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, 
                                 float*, float*);
 template <bool BWD, typename In, bool MIX>
 __global__ void states_kernel(Dims, StateArgs);
-template <typename In, bool MIX>
+template <typename In, bool MIX, bool STORE>
 __global__ void fwd_factor_kernel(Dims, const In*, const In*, const float*, const float*,
-                                  const float*, const float*, float*, float*, MixerIn);
+                                  const float*, const float*, float*, float*, MixerIn, int);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
 __global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
                                    const float*, const float*, const float*, long, int, int, float*,
@@ -98,7 +98,7 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "order_carry",    "order_apply", "order_bwd_local",
                                     "order_bwd_carry", "order_bwd_apply", "mixer_gates",
                                     "m3_walk",        "m3_out",    "m3_walk_bwd", "m3_grad",
-                                    "m3_finish",      "m3_bias"};
+                                    "m3_finish",      "m3_bias",   "m3_suffix"};
 
 struct ProfRecord {
   const char* name;
@@ -221,6 +221,14 @@ bool fused_states(int B, int H, const Dims& d) {
   return (long)B * H * (1 + d.NV) >= g_cus;
 }
 
+// Poll bound of the factor kernel's turn waits: 2^16, or M4MR_TURN_POLLS
+// (a negative value makes every wait give up, a test of the kernel's
+// give-up path: the results are then NaN).
+int turn_polls() {
+  if (const char* v = std::getenv("M4MR_TURN_POLLS")) return std::atoi(v);
+  return 1 << 16;
+}
+
 bool bad_dims(int B, int T, int H, int P, int chunk, std::string* why) {
   if (B <= 0 || T <= 0 || H <= 0) {
     *why = "B, T and H must be positive";
@@ -307,12 +315,13 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   g_error.clear();
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
+  // factors may be NULL: the forward then factors without storing.
   const void* need[] = {MIX ? (const void*)mix.key : keys,
                         values,
                         MIX ? (const void*)mix.query : queries,
                         beta,          log_decay,   floor,
                         output,        variance,    final_evidence,
-                        final_cross, solved,     factors,     start_evidence, start_cross};
+                        final_cross, solved,     start_evidence, start_cross};
   for (const void* p : need)
     if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
   if (MIX && (!gate.confidence_scale || !gate.skip || !gate.read))
@@ -353,10 +362,16 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
     });
   }
   if (rc) return rc;
+  const int polls = turn_polls();
   rc = launch("fwd_factor", st, [&] {
-    hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX>), dim3((subseqs + 3) / 4), dim3(128), 0,
-                       st, d, keys, queries, beta, log_decay, floor, start_evidence, solved,
-                       factors, mix);
+    if (factors)
+      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, true>), dim3((subseqs + 3) / 4),
+                         dim3(128), 0, st, d, keys, queries, beta, log_decay, floor,
+                         start_evidence, solved, factors, mix, polls);
+    else
+      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, false>), dim3((subseqs + 3) / 4),
+                         dim3(128), 0, st, d, keys, queries, beta, log_decay, floor,
+                         start_evidence, solved, factors, mix, polls);
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {
@@ -1103,6 +1118,14 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
                        starts, ws.dh1, d_y, o);
   });
   if (rc) return rc;
+  if (A > 0) {
+    rc = launch("m3_suffix", st, [&] {
+      const long n = (long)B * H * A;
+      hipLaunchKernelGGL(m3::suffix_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         s, o);
+    });
+    if (rc) return rc;
+  }
   rc = launch("m3_finish", st, [&] {
     hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC * 4), dim3(256), m3::finish_lds(H, A), st,
                        s, groups, dt, trap_logits, angles, o, d_c, d_b, d_dt, d_trap, d_angles);

@@ -97,17 +97,31 @@ __device__ __forceinline__ void mix_token(TokenInputs& in, bool kzero) {
 __device__ __align__(256) float g_discard[ROWS_FACTOR + 64];
 
 // Wait until the evidence buffer holds the updates of tokens 0..tt-1.  The
-// other wave of the block publishes each of its turns by writing the count;
-// a wait lasts at most one factorization of that wave plus its turn.  Bounded
-// all the same: after 2^16 polls (about 5 ms) the wave goes on.
+// other wave of the block publishes each of its turns by raising the count
+// (an LDS max); a wait lasts at most one factorization of that wave plus its
+// turn.  Bounded all the same, at `polls` polls (2^16 by default, about
+// 2 ms).  Returns the count last seen: below tt when the wait gave up.
 typedef __attribute__((address_space(3))) volatile int lds_int;
 
-__device__ __forceinline__ void wait_turn(lds_int* count, int tt) {
-  for (int i = 0; i < (1 << 16); ++i) {
-    if (__builtin_amdgcn_readfirstlane(*count) >= tt) break;
+// The count of a poisoned block: above every token count, so every later wait
+// passes at once and sees it.
+constexpr int kPoisoned = 1 << 24;
+
+__device__ __forceinline__ int wait_turn(lds_int* count, int tt, int polls) {
+  int seen = __builtin_amdgcn_readfirstlane(*count);
+  for (int i = 0; seen < tt && i < polls; ++i) {
     __builtin_amdgcn_s_sleep(1);
+    seen = __builtin_amdgcn_readfirstlane(*count);
   }
   asm volatile("" ::: "memory");  // no evidence read moves above the wait
+  return seen;
+}
+
+// count = max(count, v) in LDS (a published count never goes down, so a
+// poisoned block stays poisoned).
+__device__ __forceinline__ void raise_count(lds_int* count, int v) {
+  __hip_atomic_fetch_max((__attribute__((address_space(3))) int*)count, v, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Two waves share the four sequences of a block and take alternate tokens:
@@ -119,14 +133,24 @@ __device__ __forceinline__ void wait_turn(lds_int* count, int tt) {
 // turn, ... without waiting out the other wave's turn, the two waves offset
 // by one turn.  A block holds one 40 KB evidence buffer for two waves.
 //
+// A wave whose wait gives up (wait_turn) may read the evidence before the
+// other wave's update: it poisons the block's count at once, and every turn of
+// either wave from then on takes a NaN decay, so every later factor and
+// solution of the block's sequences is NaN rather than plausible and wrong.
+// A negative `polls` makes every wait but the first token's give up (a test
+// of this path; the host never sets it otherwise).
+//
 // MIX: keys and queries come from the mixer's raw projections (`mix`),
-// shifted and normalised as each token is loaded.
-template <typename In, bool MIX>
+// shifted and normalised as each token is loaded.  STORE = false: the factors
+// are not stored (`factors` is unused), the reference's store_factors=False
+// mode (lm/kernels/mamba4_fused.py:183-232), for forwards that take no
+// gradient.
+template <typename In, bool MIX, bool STORE>
 __global__ __launch_bounds__(128) void fwd_factor_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ queries,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ floor, const float* __restrict__ start_s,
-    float* __restrict__ solved, float* __restrict__ factors, MixerIn mix) {
+    float* __restrict__ solved, float* __restrict__ factors, MixerIn mix, int polls) {
   const int lane = threadIdx.x & 63, a = lane & 15, mu = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int BH = d.B * d.H;
@@ -195,8 +219,10 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
     if (tt >= steps) break;       // uniform over the wave (wave 1, odd step counts)
     const bool valid = tt < len;  // per 16-lane row
     float A[4][64];
-    wait_turn(turn_count, tt);
-    const float lam = expf(cur.log_lam);
+    const int seen = wait_turn(turn_count, tt, polls);
+    const bool gave_up = seen < tt || (polls < 0 && tt > 0);
+    if (gave_up && lane == 0) raise_count(turn_count, kPoisoned);
+    const float lam = gave_up || seen >= kPoisoned ? __builtin_nanf("") : expf(cur.log_lam);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const float nbk = -cur.beta * cur.k[m];
@@ -234,7 +260,7 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
         }
     // Publish the turn once every LDS access of it has completed.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (lane == 0) *turn_count = tt + 1;
+    if (lane == 0) raise_count(turn_count, tt + 1);
 
     // Prefetch this wave's next token; the factorization covers the latency.
     TokenInputs next;
@@ -246,10 +272,9 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
     factor_exchanged(A, fl, cur.q, nw);
     backward_rows16(A, nw, y);
     float* const sol = valid ? solved + cur.th * 64 : g_discard + ROWS_FACTOR;
-    float* const fac = valid ? factors + cur.th * ROWS_FACTOR : g_discard;
 #pragma unroll
     for (int m = 0; m < 4; ++m) sol[a + 16 * m] = y[m];
-    store_rows16(A, fac);
+    if constexpr (STORE) store_rows16(A, valid ? factors + cur.th * ROWS_FACTOR : g_discard);
     // Wait for the next token's loads here, where the wait can count the
     // stores just issued (vmcnt retires in order; the loads came first): the
     // polling loop in front of the next turn makes the compiler wait for
@@ -264,15 +289,17 @@ __global__ __launch_bounds__(128) void fwd_factor_kernel(
   }
 }
 
-template __global__ void fwd_factor_kernel<float, false>(Dims, const float*, const float*,
-                                                         const float*, const float*, const float*,
-                                                         const float*, float*, float*, MixerIn);
-template __global__ void fwd_factor_kernel<bf16_t, false>(Dims, const bf16_t*, const bf16_t*,
-                                                          const float*, const float*, const float*,
-                                                          const float*, float*, float*, MixerIn);
-template __global__ void fwd_factor_kernel<float, true>(Dims, const float*, const float*,
-                                                        const float*, const float*, const float*,
-                                                        const float*, float*, float*, MixerIn);
+#define M4_FWD_FACTOR(IN, MIX, STORE)                                                      \
+  template __global__ void fwd_factor_kernel<IN, MIX, STORE>(                              \
+      Dims, const IN*, const IN*, const float*, const float*, const float*, const float*, \
+      float*, float*, MixerIn, int);
+M4_FWD_FACTOR(float, false, true)
+M4_FWD_FACTOR(bf16_t, false, true)
+M4_FWD_FACTOR(float, true, true)
+M4_FWD_FACTOR(float, false, false)
+M4_FWD_FACTOR(bf16_t, false, false)
+M4_FWD_FACTOR(float, true, false)
+#undef M4_FWD_FACTOR
 
 // z = A^-1 rhs from stored factors; four token-heads per wave.
 __global__ __launch_bounds__(64) void factored_solve_kernel(const float* __restrict__ factors,

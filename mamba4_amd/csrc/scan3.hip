@@ -110,6 +110,16 @@ __device__ __forceinline__ void sin_cos(float x, float* sn, float* cs) {
   *cs = ((quad + 1) & 2) ? -c0 : c0;
 }
 
+// x - 2 pi k with k = rint(x / 2 pi), in [-pi, pi]: 2 pi as two float32 parts,
+// the first (6.28125) with 8 significant bits, so k times it is exact for
+// |k| < 2^16.  Keeps each chunk's stored start phase small, so the phases
+// inside a chunk stay far below sin_cos's 2^16 limit however long the
+// sequence.
+__device__ __forceinline__ float reduce_turns(float x) {
+  const float k = rintf(x * 0.159154943f);
+  return fmaf(-k, 1.9353071795864769e-3f, fmaf(-k, 6.28125f, x));
+}
+
 // Four consecutive-in-k operand values: one 16-byte LDS read when the
 // operand is contiguous along k (stride 1), four reads otherwise.
 template <int STRIDE>
@@ -236,8 +246,9 @@ __device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
 
 // Phase table of chunk c: tab[t * LA + j] = th0[j] + sum_{s <= t} angles_s,j dt_s
 // (j < A), one token per lane, angles split over the four waves.  With
-// `advance`, th0[j] moves to the chunk's end phase (th0 lives in LDS and each
-// j belongs to one wave, whose lanes read it before lane 63 writes it).
+// `advance`, th0[j] moves to the chunk's end phase reduced modulo 2 pi (th0
+// lives in LDS and each j belongs to one wave, whose lanes read it before
+// lane 63 writes it).
 // This lane's token's angle rates j = w + NW m (zeros past T and A), for a
 // block of NW waves.
 template <int NW = 4>
@@ -269,7 +280,7 @@ __device__ void phase_table(const Shape& s, const float (&rates)[64 / NW], float
     tab[l * LA + j] = base + incl;
     if (advance) {
       __builtin_amdgcn_wave_barrier();
-      if (l == 63) th0[j] = base + incl;
+      if (l == 63) th0[j] = reduce_turns(base + incl);
     }
   }
 }
@@ -682,16 +693,22 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
   float* th0 = tab + C * LA;
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
-  float* s_rowE = sc + 384;
-  float* s_colF = sc + 448;
-  float* s_colE = sc + 512;
-  float* s_qd = sc + 576;
-  float* s_g = sc + 640;
-  float* s_dgd = sc + 704;
-  float* s_ddt = sc + 768;
-  float* qbacc = sc + 832;
-  float* kbacc = qbacc + NT;
-  float* hsum = kbacc + NT;
+  // Every reduction over waves goes through one LDS slot per contributing
+  // wave, summed in a fixed order afterwards (no atomics), so the gradients
+  // are identical run to run.  Row sums: one slot per column half; column
+  // sums: one per row block; the H0 . dH1 product: one per wave.
+  float* s_rowE = sc + 384;   // [2][64]
+  float* s_qd = sc + 512;     // [2][64]
+  float* s_g = sc + 640;      // [2][64]
+  float* s_colF = sc + 768;   // [4][64]
+  float* s_colE = sc + 1024;  // [4][64]
+  float* s_dgd = sc + 1280;   // [64]
+  float* hsum = sc + 1344;    // [8]
+  // The bias and dt partials of the rotation and phase passes, one row per
+  // wave, in R2 (unused from the last dY / V product to the next head).
+  float* qbp = R2;            // [8][NT]
+  float* kbp = R2 + 8 * NT;   // [8][NT]
+  float* ddtp = R2 + 16 * NT; // [8][64]
 
   const int total = s.B * s.NC * groups, id = xcd_block(total);
   const int g = id % groups, c = (id / groups) % s.NC, b = id / (groups * s.NC);
@@ -733,19 +750,11 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
     __syncthreads();  // the previous head is done with every LDS array
     if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
     if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
-    if (tid < 64) {
+    // Column sums: the row blocks above a column block contribute nothing.
+    if (tid < 256) {
       s_colF[tid] = 0.f;
       s_colE[tid] = 0.f;
-      s_ddt[tid] = 0.f;
-      s_qd[tid] = 0.f;
-      s_g[tid] = 0.f;
-      s_rowE[tid] = 0.f;
     }
-    if (tid < NT) {
-      qbacc[tid] = 0.f;
-      kbacc[tid] = 0.f;
-    }
-    if (tid == 0) hsum[0] = 0.f;
     __syncthreads();
     phase_table<8>(s, ang, dt, b, h, c, th0, tab, false);
     __syncthreads();
@@ -799,7 +808,7 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         part += h0[p * LQ + n] * g1[p * LQ + n];
       }
       part = wave_sum(part);
-      if (l == 0) atomicAdd(hsum, part);
+      if (l == 0) hsum[w] = part;
     }
     __syncthreads();
     float* vt = R2;
@@ -862,11 +871,11 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
       for (int i = 0; i < 4; ++i) {
         const float a = row16_sum(qd[i]), bb = row16_sum(gg[i]), e = row16_sum(rowE[i]);
         if (r == 0) {
-          // The two column halves of a row block add into the same rows.
-          const int t = 16 * wr + 4 * q + i;
-          atomicAdd(&s_qd[t], a);
-          atomicAdd(&s_g[t], bb);
-          atomicAdd(&s_rowE[t], e);
+          // The two column halves of a row block sum into the same rows.
+          const int t = 64 * wc + 16 * wr + 4 * q + i;
+          s_qd[t] = a;
+          s_g[t] = bb;
+          s_rowE[t] = e;
         }
       }
 #pragma unroll
@@ -879,8 +888,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         e += __shfl_xor(e, 16, 64);
         e += __shfl_xor(e, 32, 64);
         if (q == 0) {
-          atomicAdd(&s_colF[16 * jt + r], f);
-          atomicAdd(&s_colE[16 * jt + r], e);
+          s_colF[64 * wr + 16 * jt + r] = f;
+          s_colE[64 * wr + 16 * jt + r] = e;
         }
       }
     }
@@ -969,12 +978,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         sk.x += duk.x;
         sk.y += duk.y;
       }
-      if (col) {
-        atomicAdd(&qbacc[n2], sq.x);
-        atomicAdd(&qbacc[n2 + 1], sq.y);
-        atomicAdd(&kbacc[n2], sk.x);
-        atomicAdd(&kbacc[n2 + 1], sk.y);
-      }
+      *reinterpret_cast<float2*>(qbp + w * NT + n2) = sq;
+      *reinterpret_cast<float2*>(kbp + w * NT + n2) = sk;
     }
     __syncthreads();
     // Phase gradients summed from the chunk's end (one token per lane).
@@ -998,21 +1003,40 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         ddt += R * av[m];
         if (l == 0) o.D[phase_offset(s, b, h, c) + j] = R;
       }
-      atomicAdd(&s_ddt[l], ddt);
+      ddtp[w * 64 + l] = ddt;
     }
     if (tid < NT) {
       const long at = (((long)b * s.NC + c) * s.H + h) * NT + tid;
-      o.qb_part[at] = qbacc[tid];
-      o.kb_part[at] = kbacc[tid];
+      float aq = 0.f, ak = 0.f;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        aq += qbp[v * NT + tid];
+        ak += kbp[v * NT + tid];
+      }
+      o.qb_part[at] = aq;
+      o.kb_part[at] = ak;
     }
     __syncthreads();
     if (w == 0) {
       const int tt = c * C + l;
       const float pl = S.p[63];
-      const float ug = wave_sum(S.u[l] * s_g[l]);
-      float dp = s_rowE[l] - s_colE[l] + S.ep[l] * s_qd[l] - S.u[l] * s_g[l];
-      if (l == 63) dp += ug + expf(pl) * hsum[0];
-      const float dscale = s_colF[l] + expf(pl - S.p[l]) * s_g[l];
+      const float qd = s_qd[l] + s_qd[64 + l], gl = s_g[l] + s_g[64 + l];
+      const float rowE = s_rowE[l] + s_rowE[64 + l];
+      float colF = 0.f, colE = 0.f, hs = 0.f, ddt = 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        colF += s_colF[64 * v + l];
+        colE += s_colE[64 * v + l];
+      }
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        hs += hsum[v];
+        ddt += ddtp[v * 64 + l];
+      }
+      const float ug = wave_sum(S.u[l] * gl);
+      float dp = rowE - colE + S.ep[l] * qd - S.u[l] * gl;
+      if (l == 63) dp += ug + expf(pl) * hs;
+      const float dscale = colF + expf(pl - S.p[l]) * gl;
       const float incl = wave_scan(dp), tot = lane63(incl);
       const float dadt = tot - incl + dp;
       if (tt < s.T) {
@@ -1020,7 +1044,7 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         o.d_adt[i] = dadt;
         o.dgam[i] = s_dgd[l] + dscale;
         o.dscale[i] = dscale;
-        o.ddt_loc[i] = s_ddt[l];
+        o.ddt_loc[i] = ddt;
       }
     }
   }
@@ -1070,10 +1094,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   }
   for (int e = tid; e < s.H * s.A; e += 256) {
     const int h = e / s.A, j = e % s.A;
-    float acc = 0.f;
-#pragma unroll 8
-    for (int cc = c + 1; cc < s.NC; ++cc) acc += o.D[phase_offset(s, b, h, cc) + j];
-    suf[h * AM + j] = acc;
+    suf[h * AM + j] = o.D[phase_offset(s, b, h, c) + j];
   }
   __syncthreads();
   const long tp = (long)s.NC * C;
@@ -1107,6 +1128,23 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     }
     d_c[tok_index(s, b, tt) * s.N + n] = ac;
     d_b[tok_index(s, b, tt) * s.N + n] = ab;
+  }
+}
+
+// Phase-gradient totals of the chunks after each chunk: o.D[b,h,c,j] becomes
+// sum_{c' > c} D[b,h,c',j], a reverse exclusive scan over the chunks with one
+// thread per (b, h, j), so finish_kernel reads one row per chunk.
+__global__ __launch_bounds__(256) void suffix_kernel(Shape s, GradOut o) {
+  const long id = (long)blockIdx.x * 256 + tix();
+  if (id >= (long)s.B * s.H * s.A) return;
+  const int j = (int)(id % s.A);
+  const long bh = id / s.A;
+  float* d = o.D + bh * s.NC * AM + j;
+  float acc = 0.f;
+  for (int c = s.NC - 1; c >= 0; --c) {
+    const float v = d[(long)c * AM];
+    d[(long)c * AM] = acc;
+    acc += v;
   }
 }
 

@@ -37,7 +37,7 @@ struct GradOut {
 // LDS bytes of each kernel.
 constexpr size_t kWalkLds = (size_t)(C * LQ + C * LV + C * LA + AM + 384) * sizeof(float);
 constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
-constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1096) * sizeof(float);
+constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1352) * sizeof(float);
 // finish_kernel: [H][AM] + [C][A + 1] + [C][H + 1] floats, at most this.
 constexpr int kMaxHeads = 128;
 constexpr size_t kFinishLdsMax =
@@ -58,6 +58,7 @@ __global__ void grad_kernel(Shape, int, const float*, const float*, const float*
                             const float*, const float*, const float*, const float*, GradOut);
 __global__ void finish_kernel(Shape, int, const float*, const float*, const float*, GradOut,
                               float*, float*, float*, float*, float*);
+__global__ void suffix_kernel(Shape, GradOut);
 __global__ void bias_kernel(Shape, GradOut, float*, float*);
 
 }  // namespace m3

@@ -90,3 +90,94 @@ def workload_inputs(name, seed=0, cotangents=False, **overrides):
     spec = dict(WORKLOADS[name])
     spec.update(overrides)
     return synthetic_inputs(seed=seed, cotangents=cotangents, **spec)
+
+
+def device_tokens(gen, shape, shift, decay_mean=3.0):
+    """Config-0 distributions drawn on the GPU with a torch generator: q, k
+    unit-norm N(0,1), v N(0,1), beta = sigmoid(N(0,1)), log_decay =
+    log sigmoid(N(decay_mean, 1)); with ``shift`` the keys move one position
+    along axis 1 (a zero key first).  Returns contiguous float32
+    (keys, values, queries, beta, log_decay) of shape ``shape + (64,)`` and
+    ``shape``."""
+    import torch
+    import torch.nn.functional as F
+
+    kw = dict(device=gen.device, generator=gen, dtype=torch.float32)
+    q = torch.randn(*shape, 64, **kw)
+    k = torch.randn(*shape, 64, **kw)
+    q = q / q.norm(dim=-1, keepdim=True)
+    k = k / k.norm(dim=-1, keepdim=True)
+    if shift:
+        k = torch.cat([torch.zeros_like(k[:, :1]), k[:, :-1]], dim=1)
+    v = torch.randn(*shape, 64, **kw)
+    log_decay = -F.softplus(-(torch.randn(*shape, **kw) + decay_mean))
+    beta = torch.sigmoid(torch.randn(*shape, **kw))
+    return [t.contiguous() for t in (k, v, q, beta, log_decay)]
+
+
+def decode_states(batch=2048, heads=8, context=1024, seed=0, slice_rows=128, keep_rows=()):
+    """BASELINE config 4's resident states on cuda:0: the end states (S, C)
+    [batch, heads, 64, 64] of a ``context``-token gated recurrence with
+    config-0 distributions and lambda = sigmoid(N(3,1)) (``device_tokens``),
+    built slice by slice with this library's forward, which stores no factors
+    (no gradient is taken).  Floor 1e-2.  Returns (evidence, cross, floor,
+    kept) where ``kept`` maps each row of ``keep_rows`` to its prefill inputs
+    as float64 host arrays (for checking its end state)."""
+    import torch
+
+    from mamba4_amd import memory
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    f32 = dict(dtype=torch.float32, device=dev)
+    evidence = torch.empty(batch, heads, 64, 64, **f32)
+    cross = torch.empty(batch, heads, 64, 64, **f32)
+    floor = torch.full((heads, 64), 1e-2, **f32)
+    kept = {}
+    for first in range(0, batch, slice_rows):
+        rows = min(slice_rows, batch - first)
+        k, v, q, beta, log_decay = device_tokens(gen, (rows, context, heads), shift=True)
+        with torch.no_grad():
+            out = memory.memread_forward(k, v, q, beta, log_decay, floor, None, None, 64,
+                                         store_factors=False)
+        evidence[first:first + rows] = out[2]
+        cross[first:first + rows] = out[3]
+        for r in keep_rows:
+            if first <= r < first + rows:
+                kept[r] = {n: t[r - first].double().cpu().numpy() for n, t in
+                           zip(("keys", "values", "queries", "beta", "log_decay"),
+                               (k, v, q, beta, log_decay))}
+        del k, v, q, beta, log_decay, out
+    torch.cuda.synchronize()
+    return evidence, cross, floor, kept
+
+
+def reference_benchmark_inputs(batch=16, length=1024, heads=12, dim=64, width=128, seed=0):
+    """The reference's own memory-read benchmark inputs
+    (scripts/kernel_benchmark.py:214-224, the shape its published TPU v4
+    timings use, lm/results/speed-125m/bench-kernels.json:284-291): unit
+    N(0,1) keys and queries (no key shift), N(0,1) values, beta ~ U(0.05, 1),
+    log_decay = log U(0.9, 0.999), floor ~ U(0.25, 1.5) per (head, column),
+    drawn in that order from default_rng(seed).  Its fwd+bwd differentiates
+    a fixed projection of the outputs (projected_loss, :37-47): the
+    cotangents are cos(i * 1.7) on the output and cos(i * 2.7) on the
+    variance, i the flat index (in float32, as there).  Returns float32 arrays, cotangents
+    included."""
+    rng = np.random.default_rng(seed)
+    k = rng.normal(size=(batch, length, heads, dim))
+    q = rng.normal(size=k.shape)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    v = rng.normal(size=(batch, length, heads, width))
+    beta = rng.uniform(0.05, 1.0, size=k.shape[:-1])
+    log_decay = np.log(rng.uniform(0.9, 0.999, size=k.shape[:-1]))
+    floor = rng.uniform(0.25, 1.5, size=(heads, dim))
+    out = {n: a.astype(np.float32) for n, a in
+           dict(keys=k, values=v, queries=q, beta=beta, log_decay=log_decay,
+                floor=floor).items()}
+    # As projected_loss forms them: a float32 index times float32 (index + 1.7).
+    for name, like, factor in (("d_output", v, 1.7), ("d_variance", beta, 2.7)):
+        phase = np.arange(like.size, dtype=np.float32) * np.float32(factor)
+        out[name] = np.cos(phase).astype(np.float32).reshape(like.shape)
+    return out

@@ -9,10 +9,12 @@ ROCm device in place of JAX arrays.  Every call runs the gfx950 HIP library
 through its C ABI on the current torch stream; there is no other
 implementation, and CPU tensors are rejected.
 
-The forward stores each token's Cholesky factor, and the backward consumes
-the residual set the reference tags ``"memory_solve"``
+A differentiable forward stores each token's Cholesky factor, and the
+backward consumes the residual set the reference tags ``"memory_solve"``
 (lm/kernels/mamba4_fused.py:333-336): it issues only triangular solves and
-chunk contractions, never a second factorization.
+chunk contractions, never a second factorization.  A forward that takes no
+gradient factors without storing (the reference's store_factors=False
+mode, lm/kernels/mamba4_fused.py:183-232).
 """
 
 from typing import NamedTuple
@@ -84,6 +86,43 @@ def _value_width(value_dim):
     return _lib.VALUE_DIM if value_dim <= _lib.VALUE_DIM else _lib.MAX_VALUE_DIM
 
 
+def memread_forward(keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk,
+                    store_factors=True):
+    """m4mr_forward (or m4mr_forward_bf16 for bfloat16 keys, values and
+    queries) on contiguous padded inputs: returns (output, variance,
+    final_evidence, final_cross, solved, factors, start_evidence, start_cross).
+    Without ``store_factors`` no factor buffer is allocated and ``factors``
+    is None: the kernels factor and solve without storing, the reference's
+    store_factors=False mode (lm/kernels/mamba4_fused.py:183-232); every
+    other array is bit-identical."""
+    lib = _lib.load()
+    batch, time, heads, _ = keys.shape
+    width = values.shape[-1]
+    count, starts = _lib.start_counts(time, chunk)
+    dev = keys.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    output = torch.empty((batch, time, heads, width), **f32)
+    variance = torch.empty((batch, time, heads), **f32)
+    final_s = torch.empty((batch, heads, 64, 64), **f32)
+    final_c = torch.empty((batch, heads, width, 64), **f32)
+    solved = torch.empty((batch, time, heads, 64), **f32)
+    factors = (torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
+               if store_factors else None)
+    start_s = torch.empty((batch, heads, starts, 64, 64), **f32)
+    start_c = torch.empty((batch, heads, count, width, 64), **f32)
+    # bfloat16 keys, values and queries are read and widened in the kernels.
+    entry = lib.m4mr_forward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_forward
+    _lib.check(
+        entry(
+            _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
+            _ptr(floor), _ptr(init_s), _ptr(init_c), batch, time, heads, width, chunk,
+            _ptr(output), _ptr(variance), _ptr(final_s), _ptr(final_c),
+            _ptr(solved), _ptr(factors), _ptr(start_s), _ptr(start_c), _stream(),
+        )
+    )
+    return output, variance, final_s, final_c, solved, factors, start_s, start_c
+
+
 class _MemoryRead(torch.autograd.Function):
     """Custom VJP around m4mr_forward / m4mr_backward (D = 64, P = 64 or 128;
     keys, values and queries float32, or all bfloat16 through the _bf16
@@ -91,29 +130,8 @@ class _MemoryRead(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk):
-        lib = _lib.load()
-        batch, time, heads, _ = keys.shape
-        width = values.shape[-1]
-        count, starts = _lib.start_counts(time, chunk)
-        dev = keys.device
-        f32 = dict(dtype=torch.float32, device=dev)
-        output = torch.empty((batch, time, heads, width), **f32)
-        variance = torch.empty((batch, time, heads), **f32)
-        final_s = torch.empty((batch, heads, 64, 64), **f32)
-        final_c = torch.empty((batch, heads, width, 64), **f32)
-        solved = torch.empty((batch, time, heads, 64), **f32)
-        factors = torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
-        start_s = torch.empty((batch, heads, starts, 64, 64), **f32)
-        start_c = torch.empty((batch, heads, count, width, 64), **f32)
-        # bfloat16 keys, values and queries are read and widened in the kernels.
-        entry = lib.m4mr_forward_bf16 if keys.dtype == torch.bfloat16 else lib.m4mr_forward
-        _lib.check(
-            entry(
-                _ptr(keys), _ptr(values), _ptr(queries), _ptr(beta), _ptr(log_decay),
-                _ptr(floor), _ptr(init_s), _ptr(init_c), batch, time, heads, width, chunk,
-                _ptr(output), _ptr(variance), _ptr(final_s), _ptr(final_c),
-                _ptr(solved), _ptr(factors), _ptr(start_s), _ptr(start_c), _stream(),
-            )
+        output, variance, final_s, final_c, solved, factors, start_s, start_c = memread_forward(
+            keys, values, queries, beta, log_decay, floor, init_s, init_c, chunk
         )
         # The residual set the reference checkpoints as "memory_solve".
         ctx.save_for_backward(
@@ -307,10 +325,18 @@ def selective_gaussian_memory(
             init_c, (0, _lib.KEY_DIM - dim, 0, width - value_dim)
         ).contiguous()
     chunk = min(int(chunk_size), _lib.MAX_CHUNK)
+    args = (k, v, q, beta.contiguous(), log_decay.contiguous(), f, init_s, init_c, chunk)
+    differentiable = (keys, values, queries, beta, log_decay, floor, init_s, init_c)
     with torch.cuda.device(device):
-        output, variance, final_s, final_c = _MemoryRead.apply(
-            k, v, q, beta.contiguous(), log_decay.contiguous(), f, init_s, init_c, chunk
-        )
+        if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in differentiable
+        ):
+            output, variance, final_s, final_c = _MemoryRead.apply(*args)
+        else:
+            # No gradient: factor and solve without storing the factors, as
+            # the reference's primal chunk_solve does
+            # (lm/kernels/mamba4_fused.py:323-326).
+            output, variance, final_s, final_c = memread_forward(*args, store_factors=False)[:4]
     return SelectiveResult(
         output[..., :value_dim],
         variance,

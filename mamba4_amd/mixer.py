@@ -230,7 +230,7 @@ class _MixerRead(torch.autograd.Function):
     @staticmethod
     def forward(ctx, key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
                 previous, confidence_scale, skip, init_s, init_c, beta_max, floor_min,
-                key_shift, chunk):
+                key_shift, chunk, store_factors):
         lib = _lib.load()
         batch, time, heads, dim = key.shape
         width = value.shape[-1]
@@ -244,7 +244,10 @@ class _MixerRead(torch.autograd.Function):
         final_s = torch.empty((batch, heads, dim, dim), **f32)
         final_c = torch.empty((batch, heads, width, dim), **f32)
         solved = torch.empty((batch, time, heads, dim), **f32)
-        factors = torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
+        # Without a gradient to take, the factors are not stored (the
+        # reference's store_factors=False mode, lm/kernels/mamba4_fused.py:183-232).
+        factors = (torch.empty((batch, time, heads, _lib.FACTOR_FLOATS), **f32)
+                   if store_factors else None)
         start_s = torch.empty((batch, heads, starts, dim, dim), **f32)
         start_c = torch.empty((batch, heads, count, width, dim), **f32)
         shifted = torch.empty((batch, heads, dim), **f32) if key_shift else None
@@ -293,7 +296,7 @@ class _MixerRead(torch.autograd.Function):
         d_init = (d_init_s, d_init_c) if ctx.has_initial else (None, None)
         return (d_key, d_values + d_skip_value, d_query, d_beta_raw, d_dt_raw, d_beta_bias,
                 d_dt_bias, d_a_log, d_floor_raw, d_previous, d_scale, d_skip, *d_init,
-                None, None, None, None)
+                None, None, None, None, None)
 
 
 def mixer_read(key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
@@ -346,9 +349,13 @@ def mixer_read(key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, f
         if init_s.shape != (batch, heads, dim, dim) or init_c.shape != (batch, heads, width, dim):
             raise ValueError("mixer_read needs an initial state [B,H,64,64], [B,H,P,64]")
     chunk = min(int(chunk_size), _lib.MAX_CHUNK)
+    differentiable = [key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
+                      previous, confidence_scale, skip, init_s, init_c]
+    store = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in differentiable)
     with torch.cuda.device(key.device):
         output, variance, final_s, final_c, shifted = _MixerRead.apply(
             key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
             previous, confidence_scale, skip, init_s, init_c, float(beta_max),
-            float(floor_min), bool(key_shift), chunk)
+            float(floor_min), bool(key_shift), chunk, store)
     return MixerRead(output, variance, SelectiveState(final_s, final_c), shifted)

@@ -61,3 +61,37 @@ def run_gpu(data, chunk=64, initial=None, cotangents=None, names=NAMES):
             out["d_initial_cross"] = host(init_tensors[1].grad)
     torch.cuda.synchronize()
     return out
+
+
+def run_quad(m, q):
+    """First quad of the run of column quad q of row slot m in a stored factor."""
+    base = 32 * m * m + 8 * m
+    if q <= 4 * m:
+        return base + 16 * q
+    return base + 16 * (4 * m + 1) + {1: -4, 2: 4, 3: 8}[q - 4 * m]
+
+
+def factor_index():
+    """[64, 64] float offsets of L_ij (j <= i) in a stored factor, -1 above."""
+    index = np.full((64, 64), -1)
+    for i in range(64):
+        a, m = i % 16, i // 16
+        for j in range(i + 1):
+            index[i, j] = 4 * (run_quad(m, j // 4) + a) + j % 4
+    return index
+
+
+FACTOR_INDEX = factor_index()
+LOWER = FACTOR_INDEX >= 0
+
+
+def unpack_factors(packed):
+    lower = np.zeros(packed.shape[:-1] + (64, 64))
+    lower[..., LOWER] = packed[..., FACTOR_INDEX[LOWER]]
+    return lower
+
+
+def pack_factors(lower):
+    packed = np.zeros(lower.shape[:-2] + (2176,))
+    packed[..., FACTOR_INDEX[LOWER]] = lower[..., LOWER]
+    return packed

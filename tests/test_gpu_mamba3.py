@@ -136,3 +136,66 @@ def test_full_size_row_against_oracle(gpu_lib):
             got = got[3:4]
         err = normwise(got.reshape(grads[n].shape), grads[n])
         assert err <= 1e-4, (n, err)
+
+
+@pytest.mark.gpu
+def test_backward_is_bit_reproducible(gpu_lib):
+    """Every reduction of the backward runs in a fixed order (per-wave LDS
+    slots, fixed-order sums; no atomics): two backward passes over the same
+    inputs give identical gradients for all nine inputs.  Twelve heads per
+    group, so every wave of the gradient kernel contributes to each sum."""
+    import torch
+
+    from gpu_helpers import announce
+
+    announce("mamba3 backward twice, B2 T300 H12 N128 P64 A32")
+    x = _rounded(m3.inputs(batch=2, length=300, heads=12, dim=128, width=64, angle_count=32,
+                           seed=21))
+    d_y = None
+    grads = []
+    for _ in range(2):
+        t = _gpu(x, grad=True)
+        y, final = _run(t)
+        if d_y is None:
+            rng = np.random.default_rng(22)
+            d_y = torch.tensor(rng.normal(size=y.shape), dtype=torch.float32, device="cuda:0")
+            d_f = torch.tensor(rng.normal(size=final.shape), dtype=torch.float32,
+                               device="cuda:0")
+        ((y * d_y).sum() + (final * d_f).sum()).backward()
+        torch.cuda.synchronize()
+        grads.append({n: t[n].grad.clone() for n in NAMES})
+    for n in NAMES:
+        assert torch.equal(grads[0][n], grads[1][n]), n
+
+
+@pytest.mark.gpu
+def test_long_sequence_large_phases(gpu_lib):
+    """Angle rates offset by 20 over 12288 tokens: the accumulated phases
+    reach 1e5, past the 2^16 range of the kernels' sin/cos.  Each chunk's
+    stored start phase is kept reduced modulo 2 pi, so every phase a chunk
+    rotates by stays below about 2 pi + 64 * max(rate * dt).  What remains is
+    float32 rounding of the phases within each chunk and of the carried start
+    phases over 192 chunks (about 1e-4 to 1e-3 rad against the float64
+    oracle's exact cumulative sums): outputs normwise <= 3e-3, gradients
+    <= 1e-2."""
+    import torch
+
+    from gpu_helpers import announce, normwise
+
+    announce("mamba3 B1 T12288 H2 N8 P4 A2, phases to 1e5")
+    x = m3.inputs(batch=1, length=12288, heads=2, dim=8, width=4, angle_count=2, seed=3)
+    x["angles"] = x["angles"] + 20.0
+    x = _rounded(x)
+    t = _gpu(x, grad=True)
+    y, final = _run(t)
+    rng = np.random.default_rng(4)
+    d_y = rng.normal(size=y.shape)
+    (y * torch.tensor(d_y, dtype=torch.float32, device="cuda:0")).sum().backward()
+    y_ref, final_ref = m3.forward(*(x[n] for n in NAMES))
+    assert normwise(_host(y), y_ref) <= 3e-3
+    assert normwise(_host(final), final_ref) <= 3e-3
+    grads = m3.backward(*(x[n] for n in NAMES), d_y, None)
+    for n in NAMES:
+        got = _host(t[n].grad).reshape(grads[n].shape)
+        err = normwise(got, grads[n])
+        assert err <= 1e-2, (n, err)
