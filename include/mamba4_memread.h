@@ -255,6 +255,36 @@ int m4mr_backward_bf16(const uint16_t* keys, const uint16_t* values, const uint1
                        void* stream);
 
 /*
+ * m4mr_backward that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving and training loops
+ * that allocate nothing per step, harnesses that forbid hipMalloc).  The
+ * backward's intermediates (z, the end-state cotangents, the per-chunk floor
+ * partials) live in a static device buffer of M4MR_STATIC_SCRATCH_BYTES
+ * (128 MiB) that each GPU the library runs on holds until the process ends;
+ * its address on a device is resolved at the first call on that device.
+ * Sizes whose m4mr_backward_workspace_bytes exceeds it return M4MR_EINVAL
+ * before any launch (128 MiB holds B*T*H = 131072 token-heads at P = 64,
+ * BASELINE config 2, with room to spare).  Every call on one GPU shares that
+ * GPU's buffer: calls that overlap on one GPU (on different streams, or from
+ * different threads without ordering) race and must not be issued.  Every
+ * other argument and every result as in m4mr_backward (float32 keys, values
+ * and queries).
+ */
+#define M4MR_STATIC_SCRATCH_BYTES (128u << 20)
+int m4mr_backward_noalloc(const float* keys, const float* values, const float* queries,
+                          const float* beta, const float* log_decay, const float* floor,
+                          int B, int T, int H, int value_dim, int chunk,
+                          const float* solved, const float* factors,
+                          const float* start_evidence, const float* start_cross,
+                          const float* d_output, const float* d_variance,
+                          const float* d_final_evidence, const float* d_final_cross,
+                          float* d_keys, float* d_values, float* d_queries,
+                          float* d_beta, float* d_log_decay, float* d_floor,
+                          float* d_init_evidence, float* d_init_cross,
+                          void* stream);
+
+/*
  * Triangular re-solve with stored factors: z_i = A_i^-1 rhs_i for N
  * token-heads, factors [N, M4MR_FACTOR_FLOATS], rhs and z [N, D] (z may
  * alias rhs).  Replaces factored_solve / _factored_kernel

@@ -20,6 +20,7 @@ KEY_DIM = 64
 VALUE_DIM = 64
 MAX_VALUE_DIM = 128
 MAX_CHUNK = 64
+STATIC_SCRATCH_BYTES = 128 << 20  # M4MR_STATIC_SCRATCH_BYTES
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -65,6 +66,10 @@ SIGNATURES = {
     "m4mr_backward_bf16": (
         _I,
         [_P] * 6 + [_I] * 5 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],
+    ),
+    "m4mr_backward_noalloc": (
+        _I,
+        [_P] * 6 + [_I] * 5 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P],
     ),
     "m4mr_factored_solve": (_I, [_P, _P, _P, _L, _P]),
     "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _I, _P, _P, _P]),

@@ -471,6 +471,38 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   });
 }
 
+// The allocation-free backward's workspace: one static device array per GPU
+// the library runs on, held until the process ends.  Its name in host code
+// is only a stand-in for the symbol: the device address of each GPU's copy
+// comes from hipGetSymbolAddress, resolved once per device (with that device
+// current) and kept in g_scratch_ptr; only that address is handed to kernels.
+static __device__ __align__(256) unsigned char scratch[M4MR_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` in *out (M4MR_OK), or an error.
+int scratch_on_current_device(const char* entry, void** out) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess)
+    return fail(M4MR_EHIP, std::string(entry) + ": hipGetDevice: " + hipGetErrorString(e));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(M4MR_EINVAL, std::string(entry) + ": device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(M4MR_EHIP, std::string(entry) + ": hipGetSymbolAddress(scratch): " +
+                                 hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return M4MR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -619,6 +651,35 @@ int m4mr_backward_bf16(const uint16_t* keys, const uint16_t* values, const uint1
                        d_output, d_variance, d_final_evidence, d_final_cross, d_keys, d_values,
                        d_queries, d_beta, d_log_decay, d_floor, d_init_evidence, d_init_cross,
                        workspace, workspace_bytes, stream);
+}
+
+int m4mr_backward_noalloc(const float* keys, const float* values, const float* queries,
+                          const float* beta, const float* log_decay, const float* floor, int B,
+                          int T, int H, int value_dim, int chunk, const float* solved,
+                          const float* factors, const float* start_evidence,
+                          const float* start_cross, const float* d_output,
+                          const float* d_variance, const float* d_final_evidence,
+                          const float* d_final_cross, float* d_keys, float* d_values,
+                          float* d_queries, float* d_beta, float* d_log_decay, float* d_floor,
+                          float* d_init_evidence, float* d_init_cross, void* stream) {
+  g_error.clear();
+  std::string why;
+  if (bad_dims(B, T, H, value_dim, chunk, &why))
+    return fail(M4MR_EINVAL, "m4mr_backward_noalloc: " + why);
+  // Sizes are checked before any HIP call.
+  const size_t need = carve(nullptr, B, T, H, value_dim, chunk).bytes;
+  if (need > (size_t)M4MR_STATIC_SCRATCH_BYTES)
+    return fail(M4MR_EINVAL, "m4mr_backward_noalloc: these sizes need " + std::to_string(need) +
+                                 " bytes of workspace, more than its static " +
+                                 std::to_string((size_t)M4MR_STATIC_SCRATCH_BYTES) +
+                                 "-byte buffer; use m4mr_backward with a workspace");
+  void* ws = nullptr;
+  if (int rc = scratch_on_current_device("m4mr_backward_noalloc", &ws)) return rc;
+  return backward_impl<float, false>(
+      "m4mr_backward_noalloc", keys, values, queries, beta, log_decay, floor, B, T, H, value_dim,
+      chunk, solved, factors, start_evidence, start_cross, d_output, d_variance,
+      d_final_evidence, d_final_cross, d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor,
+      d_init_evidence, d_init_cross, ws, (size_t)M4MR_STATIC_SCRATCH_BYTES, stream);
 }
 
 int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N,

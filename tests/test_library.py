@@ -119,3 +119,18 @@ def test_spd_solve_python_checks():
         memory.spd_solve(a, torch.zeros(7, 5))
     with pytest.raises(ValueError, match="Unknown SPD solve backend"):
         memory.spd_solve(a, torch.zeros(7, 6), backend="qr")
+
+
+def test_noalloc_backward_rejects_sizes_beyond_its_static_buffer():
+    """m4mr_backward_noalloc checks its sizes before any HIP call: config 2
+    fits its 128 MiB buffer, a problem four times config 2's does not."""
+    lib = _lib.load()
+    need = lib.m4mr_backward_workspace_bytes(16, 1024, 8, 64, 64)
+    assert 0 < need <= _lib.STATIC_SCRATCH_BYTES
+    assert lib.m4mr_backward_workspace_bytes(32, 1024, 16, 64, 64) > _lib.STATIC_SCRATCH_BYTES
+    null = ctypes.c_void_p(0)
+    rc = lib.m4mr_backward_noalloc(*([null] * 6), 32, 1024, 16, 64, 64, *([null] * 16), null)
+    assert rc == _lib.EINVAL
+    message = lib.m4mr_last_error().decode()
+    assert "static" in message and "m4mr_backward" in message
+
