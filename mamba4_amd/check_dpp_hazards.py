@@ -1,14 +1,16 @@
-"""Static check of the hand-written DPP multiply-adds in compiled gfx950 code.
+"""Static check of the hand-written DPP instructions in compiled gfx950 code.
 
-rows16.hpp emits ``v_fmac_f32_dpp`` through inline asm, which the compiler's
-hazard recognizer does not inspect.  GFX9 requires two wait states between
-a VALU instruction that writes a VGPR and a DPP instruction that reads it.
-This script reads the AMD assembly of our own build and fails if any
-``v_fmac_f32_dpp`` reads, as its DPP source, a VGPR written by a VALU
+rows16.hpp emits DPP instructions (``v_fmac_f32_dpp``, ``v_mov_b32_dpp``)
+through inline asm, which the compiler's hazard recognizer does not
+inspect.  GFX9 requires two wait states between a VALU instruction that
+writes a VGPR and a DPP instruction that reads it.  This script reads the
+AMD assembly of our own build and fails if any DPP instruction inside an
+inline-asm block reads, as its DPP source, a VGPR written by a VALU
 instruction fewer than two wait states earlier (every instruction counts
 one wait state, ``s_nop N`` counts N+1).  After a label or branch the
-history is unknown, so a DPP multiply-add within two wait states of one is
-also reported.
+history is unknown, so such a DPP instruction within two wait states of one
+is also reported.  DPP instructions the compiler emits itself are covered by
+its own hazard recognizer and are not checked.
 """
 
 import re
@@ -33,7 +35,12 @@ def check(asm_text):
     history = []  # (wait states since, set of VGPRs written) for recent VALU writes
     unknown = 0  # wait states left during which the history is unknown
     kernel = "?"
+    in_asm = False
     for line_no, raw in enumerate(asm_text.splitlines(), 1):
+        if ";;#ASMSTART" in raw:
+            in_asm = True
+        elif ";;#ASMEND" in raw:
+            in_asm = False
         line = raw.split(";")[0].strip()
         if not line or line.startswith("."):
             if line.startswith(".type") or line.startswith(".globl"):
@@ -43,11 +50,11 @@ def check(asm_text):
             history, unknown = [], 2
             continue
         mnemonic, _, operands = line.partition(" ")
-        if mnemonic == "v_fmac_f32_dpp":
+        if in_asm and mnemonic.endswith("_dpp"):
             ops = [o.strip() for o in operands.split(",")]
             src0 = _regs(ops[1])
             if unknown > 0:
-                problems.append(f"{kernel}:{line_no}: DPP FMA right after a label/branch")
+                problems.append(f"{kernel}:{line_no}: DPP instruction right after a label/branch")
             for age, written in history:
                 if age < 2 and written & src0:
                     problems.append(f"{kernel}:{line_no}: {line} reads v{sorted(written & src0)} "
