@@ -459,10 +459,10 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   }
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
-    hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX>), dim3(seqs), dim3(512), kGradsLdsBytes, st,
-                       d, keys, values, beta, log_decay, solved, ws.z, d_output, d_variance,
-                       start_evidence, start_cross, ws.end_s, ws.end_c, d_keys, d_values,
-                       d_queries, d_beta, d_log_decay, ws.floor_part, mix);
+    hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX>), dim3(persistent_grid(seqs, 1)), dim3(512),
+                       kGradsLdsBytes, st, d, keys, values, beta, log_decay, solved, ws.z,
+                       d_output, d_variance, start_evidence, start_cross, ws.end_s, ws.end_c,
+                       d_keys, d_values, d_queries, d_beta, d_log_decay, ws.floor_part, mix);
   });
   if (rc) return rc;
   return launch("floor_reduce", st, [&] {

@@ -369,6 +369,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // {k, 3 - k} on the waves k and k + 4 that share a SIMD (ws = w8 for
 // w8 < 4, 7 - w8 above).
 //
+// Persistent, one block per compute unit (the seven tiles take 122 KB of
+// LDS): block i handles chunks i, i + gridDim.x, ...  The next chunk's five
+// row tiles and its scalars load into registers while this chunk is
+// computed, one tile at a time between the products of phases 3-5: every
+// block runs the same phases at about the same time, so issuing all of
+// them at once would only move the burst (its issue stalls the waves while
+// the whole chip's requests drain), not hide it.
+//
 // Value-dependent terms run once per 64-column value tile (NV <= 2): gv and
 // H^T v sum over the tiles, d values and H k are per tile; the tiles are
 // restaged in an order that starts from the tile already in LDS.
@@ -395,44 +403,70 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   float* Yt = Vt + TILE;
   float* Zt = Yt + TILE;
   float* Dt = Zt + TILE;  // a dout tile
-  float* M1 = Dt + TILE;  // W * gy, then G_end (then G + G^T)
-  float* M2 = M1 + TILE;  // W * (gv - gz), then an H_end tile
+  float* M1 = Dt + TILE;  // W * gy transposed (M1[s][t]), then G_end
+  float* M2 = M1 + TILE;  // W * (gv - gz) transposed, then an H_end tile
   __shared__ ChunkScalars cs;
   __shared__ float colpart[4][64];
   __shared__ float rowpart[2][64], quadpart[2][64], startpart[2][64];
   __shared__ float rowE[64], colD2[64], quad[64], startdot[64];
   __shared__ float red[GRADS_THREADS];
   __shared__ f4 fpart[8][16];
-  const SeqIndex si = seq_index(d);
-  const int w8 = threadIdx.x >> 6, ws = w8 < 4 ? w8 : 7 - w8, hf = w8 >> 2, l = lane_id();
-  const int r = l & 15, c4 = 4 * r;
-  const int kt = k_terms(si.len), last = d.NV - 1;
-  // Column blocks of this wave's half that hold some s <= t of its strip,
-  // and the first t of its strip (the masked products vanish outside).
-  const int causal_nj = min(2, max(0, ws - 2 * hf + 1)), t_begin = 16 * ws;
-  // d_variance of this thread's tile-fetch rows (threadIdx/16 + 32j).
-  float dvar[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = (threadIdx.x >> 4) + 32 * j;
-    dvar[j] = t < si.len ? d_variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] : 0.f;
-  }
+  const long nseq = (long)d.B * d.H * d.NC;
+  long seq = blockIdx.x;
+  SeqIndex si = seq_at(d, seq);
 
-  {
-    TileRegs2 rt[5];
+  // The row tiles of a chunk (keys, value tile 0, y, z, dout tile 0) in the
+  // tile-fetch layout, and its log decays, betas and d_variance.
+  TileRegs2 rt[5];
+  auto fetch_keys = [&](const SeqIndex& sx) {
     if constexpr (MIX) {
-      rt[0].fetch_rows(si.len, [&](int r) -> const float* {
-        const int t = si.n * d.chunk + r;
-        const float* p = mix_key_row(mix, d, si.b, t, si.h);
-        return p ? p : mix.query + token_head(d, si.b, t, si.h) * 64;
+      rt[0].fetch_rows(sx.len, [&](int r) -> const float* {
+        const int t = sx.n * d.chunk + r;
+        const float* p = mix_key_row(mix, d, sx.b, t, sx.h);
+        return p ? p : mix.query + token_head(d, sx.b, t, sx.h) * 64;
       });
     } else {
-      rt[0].fetch_rows(si.len, rows_of(keys, d, si));
+      rt[0].fetch_rows(sx.len, rows_of(keys, d, sx));
     }
-    rt[1].fetch_rows(si.len, value_rows(values, d, si, 0));
-    rt[2].fetch_rows(si.len, rows_of(solved, d, si));
-    rt[3].fetch_rows(si.len, rows_of(z, d, si));
-    rt[4].fetch_rows(si.len, value_rows(d_output, d, si, 0));
+  };
+  float pg = 0.f, pbt = 0.f, pdv[2];
+  auto fetch_scalars = [&](const SeqIndex& sx) {
+    const int tt = threadIdx.x;
+    pg = 0.f;
+    pbt = 0.f;
+    if (tt < sx.len) {
+      const long th = token_head(d, sx.b, sx.n * d.chunk + tt, sx.h);
+      pg = log_decay[th];
+      pbt = beta[th];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = (tt >> 4) + 32 * j;
+      pdv[j] = t < sx.len ? d_variance[token_head(d, sx.b, sx.n * d.chunk + t, sx.h)] : 0.f;
+    }
+  };
+  fetch_keys(si);
+  rt[1].fetch_rows(si.len, value_rows(values, d, si, 0));
+  rt[2].fetch_rows(si.len, rows_of(solved, d, si));
+  rt[3].fetch_rows(si.len, rows_of(z, d, si));
+  rt[4].fetch_rows(si.len, value_rows(d_output, d, si, 0));
+  fetch_scalars(si);
+
+  for (;;) {
+    // The thread index passes through an empty asm once per chunk, so the
+    // compiler rebuilds the loop-invariant LDS and row addresses in each
+    // chunk instead of keeping about ninety of them live across the loop.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int w8 = tid >> 6, ws = w8 < 4 ? w8 : 7 - w8, hf = w8 >> 2, l = tid & 63;
+    const int r = l & 15, c4 = 4 * r;
+    const int kt = k_terms(si.len), last = d.NV - 1;
+    // Column blocks of this wave's half that hold some s <= t of its strip,
+    // and the first t of its strip (the masked products vanish outside).
+    const int causal_nj = min(2, max(0, ws - 2 * hf + 1)), t_begin = 16 * ws;
+    // d_variance of this thread's tile-fetch rows (tid/16 + 32j).
+    const float dvar[2] = {pdv[0], pdv[1]};
+
     if constexpr (MIX)
       rt[0].store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0);
     else
@@ -441,297 +475,314 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     rt[2].store(Yt);
     rt[3].store(Zt);
     rt[4].store(Dt);
-  }
-  load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
-  // The end-state cotangents of phase 3 load while phases 1 and 2 run (of H,
-  // the last value tile, the one phase 3 starts from).
-  TileRegs2 rg, rh;
-  rg.fetch_matrix(end_s + si.seq * 4096);
-  rh.fetch_matrix(cross_tile(end_c, d, si.seq, last));
-  __syncthreads();
+    if (tid < 64) finish_chunk_scalars(cs, pg, pbt);
+    // The end-state cotangents of phase 3 load while phases 1 and 2 run (of H,
+    // the last value tile, the one phase 3 starts from).
+    TileRegs2 rg, rh;
+    rg.fetch_matrix(end_s + si.seq * 4096);
+    rh.fetch_matrix(cross_tile(end_c, d, si.seq, last));
+    __syncthreads();
 
-  // Phase 1: gy = Y K^T, gz = Z K^T, gv = sum over value tiles of dOut V^T,
-  // and their weighted mixes.  Leaves the last value and dout tiles in LDS.
-  {
-    f4 gy[2], gz[2], gv[2];
-    zero2(gy);
-    zero2(gz);
-    zero2(gv);
-    tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf, 0, causal_nj);
-    tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf, 0, causal_nj);
-    tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
-    for (int v = 1; v < d.NV; ++v) {
-      TileRegs2 rv, rd;
-      rv.fetch_rows(si.len, value_rows(values, d, si, v));
-      rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
-      __syncthreads();
-      rv.store(Vt);
-      rd.store(Dt);
-      __syncthreads();
+    // Phase 1: gy = Y K^T, gz = Z K^T, gv = sum over value tiles of dOut V^T,
+    // and their weighted mixes.  Leaves the last value and dout tiles in LDS.
+    {
+      f4 gy[2], gz[2], gv[2];
+      zero2(gy);
+      zero2(gz);
+      zero2(gv);
+      tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf, 0, causal_nj);
+      tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf, 0, causal_nj);
       tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
-    }
-    float rsum[4] = {0.f, 0.f, 0.f, 0.f};
-    float csum[2] = {0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int t = acc_row(ws, q), s = 16 * (2 * hf + j) + r;
-        float my = 0.f, mz = 0.f, d2 = 0.f;
-        if (s <= t && t < si.len) {
-          const float dec = expf(cs.prefix[t] - cs.prefix[s]);
-          const float mix = gv[j][q] - gz[j][q];
-          d2 = dec * gy[j][q] * mix;
-          my = dec * cs.beta[s] * gy[j][q];
-          mz = dec * cs.beta[s] * mix;
-        }
-        M1[t * LDT + s] = my;
-        M2[t * LDT + s] = mz;
-        rsum[q] += cs.beta[s] * d2;
-        csum[j] += d2;
-      }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float v = row16_sum(rsum[q]);
-      if (r == 0) rowpart[hf][acc_row(ws, q)] = v;
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float v = group4_sum(csum[j]);
-      if (l < 16) colpart[ws][16 * (2 * hf + j) + r] = v;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int s = threadIdx.x;
-    colD2[s] = colpart[0][s] + colpart[1][s] + colpart[2][s] + colpart[3][s];
-    rowE[s] = rowpart[0][s] + rowpart[1][s];
-  }
-
-  // Phase 2: within-chunk key gradient and the value gradient of each tile
-  // (rows s, QUAD columns 4r + 2hf + j).  Tiles from the last down, so the
-  // first dout tile is in LDS afterwards.
-  f4 dk[2], dv[MAX_NV][2];
-  zero2(dk);
-  {
-    f4 tmp[2];
-    zero2(tmp);
-    tile_mma_half<true, false>(dk, M2, Yt, kt, ws, hf, t_begin);   // sum_t W(gv-gz)[t][s] y_t
-    tile_mma_half<true, false>(tmp, M1, Zt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] z_t
-#pragma unroll
-    for (int j = 0; j < 2; ++j) dk[j] -= tmp[j];
-  }
-#pragma unroll
-  for (int v = MAX_NV - 1; v >= 0; --v) {
-    zero2(dv[v]);
-    if (v < d.NV) {
-      if (v < last) {
-        TileRegs2 rd;
+      for (int v = 1; v < d.NV; ++v) {
+        TileRegs2 rv, rd;
+        rv.fetch_rows(si.len, value_rows(values, d, si, v));
         rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
         __syncthreads();
+        rv.store(Vt);
         rd.store(Dt);
         __syncthreads();
+        tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
       }
-      tile_mma_half<true, false>(dv[v], M1, Dt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] dout_t
-    }
-  }
-  __syncthreads();
-
-  // Phase 3: chunk-end terms through the end-state cotangents G, H.  G is
-  // replaced by G + G^T in LDS (each off-diagonal pair by one thread), so
-  // (G + G^T) k_s is a single product.  H and the values go tile by tile from
-  // the last, leaving the first tile of each in LDS.
-  rg.store(M1);
-  rh.store(M2);
-  // The start states of phase 4 load while phase 3 runs.
-  const long bh = si.seq / d.NC;
-  TileRegs2 rs, rc;
-  rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
-  rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
-  __syncthreads();
-  for (int e = threadIdx.x; e < 64 * 64; e += GRADS_THREADS) {
-    const int i = e >> 6, j = e & 63;
-    if (i < j) {
-      const float v = M1[i * LDT + j] + M1[j * LDT + i];
-      M1[i * LDT + j] = v;
-      M1[j * LDT + i] = v;
-    } else if (i == j) {
-      M1[i * LDT + i] *= 2.f;
-    }
-  }
-  __syncthreads();
-  {
-    f4 gk[2], hv[2];
-    zero2(gk);
-    zero2(hv);
-    tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);  // (G + G^T) k_s
-    float qpart[4] = {0.f, 0.f, 0.f, 0.f};
+      // The mixes go to LDS transposed, M[s][t] (a lane's four accumulator
+      // rows t are adjacent there: one 16-byte store per column block), so
+      // phase 2 reads them as row-major A operands.
+      float rsum[4] = {0.f, 0.f, 0.f, 0.f};
+      float csum[2] = {0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float2 kr = *reinterpret_cast<const float2*>(Kt + acc_row(ws, q) * LDT + c4 + 2 * hf);
-      qpart[q] += 0.5f * kr.x * gk[0][q] + 0.5f * kr.y * gk[1][q];
+      for (int j = 0; j < 2; ++j) {
+        const int s = 16 * (2 * hf + j) + r;
+        f4 m1v, m2v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int t = acc_row(ws, q);
+          float my = 0.f, mz = 0.f, d2 = 0.f;
+          if (s <= t && t < si.len) {
+            const float dec = expf(cs.prefix[t] - cs.prefix[s]);
+            const float mix = gv[j][q] - gz[j][q];
+            d2 = dec * gy[j][q] * mix;
+            my = dec * cs.beta[s] * gy[j][q];
+            mz = dec * cs.beta[s] * mix;
+          }
+          m1v[q] = my;
+          m2v[q] = mz;
+          rsum[q] += cs.beta[s] * d2;
+          csum[j] += d2;
+        }
+        *reinterpret_cast<f4*>(M1 + s * LDT + acc_row(ws, 0)) = m1v;
+        *reinterpret_cast<f4*>(M2 + s * LDT + acc_row(ws, 0)) = m2v;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float v = row16_sum(rsum[q]);
+        if (r == 0) rowpart[hf][acc_row(ws, q)] = v;
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float v = group4_sum(csum[j]);
+        if (l < 16) colpart[ws][16 * (2 * hf + j) + r] = v;
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const int s = tid;
+      colD2[s] = colpart[0][s] + colpart[1][s] + colpart[2][s] + colpart[3][s];
+      rowE[s] = rowpart[0][s] + rowpart[1][s];
+    }
+
+    // Phase 2: within-chunk key gradient and the value gradient of each tile
+    // (rows s, QUAD columns 4r + 2hf + j).  Tiles from the last down, so the
+    // first dout tile is in LDS afterwards.
+    f4 dk[2], dv[MAX_NV][2];
+    zero2(dk);
+    {
+      f4 tmp[2];
+      zero2(tmp);
+      tile_mma_half<false, false>(dk, M2, Yt, kt, ws, hf, t_begin);   // sum_t W(gv-gz)[t][s] y_t
+      tile_mma_half<false, false>(tmp, M1, Zt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] z_t
+#pragma unroll
+      for (int j = 0; j < 2; ++j) dk[j] -= tmp[j];
     }
 #pragma unroll
     for (int v = MAX_NV - 1; v >= 0; --v) {
+      zero2(dv[v]);
       if (v < d.NV) {
         if (v < last) {
-          TileRegs2 rv, rhv;
-          rv.fetch_rows(si.len, value_rows(values, d, si, v));
-          rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
+          TileRegs2 rd;
+          rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
           __syncthreads();
-          rv.store(Vt);
-          rhv.store(M2);
+          rd.store(Dt);
           __syncthreads();
         }
-        f4 hk[2];
-        zero2(hk);
-        tile_mma_half<false, true, true>(hk, Kt, M2, 64, ws, hf);  // H k_s
-        tile_mma_half<false, false>(hv, Vt, M2, 64, ws, hf);       // H^T v_s, summed
+        tile_mma_half<false, false>(dv[v], M1, Dt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] dout_t
+      }
+    }
+    __syncthreads();
+
+    // Phase 3: chunk-end terms through the end-state cotangents G, H:
+    // (G + G^T) k_s as two products (G read k-major, then transposed).  H and
+    // the values go tile by tile from the last, leaving the first tile of
+    // each in LDS.
+    rg.store(M1);
+    rh.store(M2);
+    // The start states of phase 4 load while phase 3 runs, then the first of
+    // the next chunk's tiles.
+    const long bh = si.seq / d.NC;
+    TileRegs2 rs, rc;
+    rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
+    rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
+    const long next = seq + gridDim.x;
+    const bool more = next < nseq;  // uniform over the block
+    // The last chunk of a block fetches its own tiles again (unused): every
+    // load stays unconditional.
+    const SeqIndex sx = seq_at(d, more ? next : seq);
+    rt[2].fetch_rows(sx.len, rows_of(solved, d, sx));
+    __syncthreads();
+    {
+      f4 gk[2], hv[2];
+      zero2(gk);
+      zero2(hv);
+      tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // G^T k_s
+      tile_mma_half<false, true, true>(gk, Kt, M1, 64, ws, hf);  // + G k_s
+      rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
+      float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int s = acc_row(ws, q);
-          const float2 vr = *reinterpret_cast<const float2*>(Vt + s * LDT + c4 + 2 * hf);
-          qpart[q] += vr.x * hk[0][q] + vr.y * hk[1][q];
-          if (s < si.len) {
-            const float tl = cs.tail[s];
-            const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
-            *reinterpret_cast<float2*>(d_values + th * d.P + 64 * v + c4 + 2 * hf) =
-                float2{dv[v][0][q] + tl * hk[0][q], dv[v][1][q] + tl * hk[1][q]};
+      for (int q = 0; q < 4; ++q) {
+        const float2 kr = *reinterpret_cast<const float2*>(Kt + acc_row(ws, q) * LDT + c4 + 2 * hf);
+        qpart[q] += 0.5f * kr.x * gk[0][q] + 0.5f * kr.y * gk[1][q];
+      }
+#pragma unroll
+      for (int v = MAX_NV - 1; v >= 0; --v) {
+        if (v < d.NV) {
+          if (v < last) {
+            TileRegs2 rv, rhv;
+            rv.fetch_rows(si.len, value_rows(values, d, si, v));
+            rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
+            __syncthreads();
+            rv.store(Vt);
+            rhv.store(M2);
+            __syncthreads();
+          }
+          f4 hk[2];
+          zero2(hk);
+          tile_mma_half<false, true, true>(hk, Kt, M2, 64, ws, hf);  // H k_s
+          tile_mma_half<false, false>(hv, Vt, M2, 64, ws, hf);       // H^T v_s, summed
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int s = acc_row(ws, q);
+            const float2 vr = *reinterpret_cast<const float2*>(Vt + s * LDT + c4 + 2 * hf);
+            qpart[q] += vr.x * hk[0][q] + vr.y * hk[1][q];
+            if (s < si.len) {
+              const float tl = cs.tail[s];
+              const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
+              *reinterpret_cast<float2*>(d_values + th * d.P + 64 * v + c4 + 2 * hf) =
+                  float2{dv[v][0][q] + tl * hk[0][q], dv[v][1][q] + tl * hk[1][q]};
+            }
           }
         }
       }
-    }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int s = acc_row(ws, q);
-      const float qv = row16_sum(qpart[q]);
-      if (r == 0) quadpart[hf][s] = qv;
-      if (s < si.len) {
-        const float tl = cs.tail[s];
-        const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
-        *reinterpret_cast<float2*>(d_keys + th * 64 + c4 + 2 * hf) =
-            float2{dk[0][q] + tl * (gk[0][q] + hv[0][q]), dk[1][q] + tl * (gk[1][q] + hv[1][q])};
+      for (int q = 0; q < 4; ++q) {
+        const int s = acc_row(ws, q);
+        const float qv = row16_sum(qpart[q]);
+        if (r == 0) quadpart[hf][s] = qv;
+        if (s < si.len) {
+          const float tl = cs.tail[s];
+          const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
+          *reinterpret_cast<float2*>(d_keys + th * 64 + c4 + 2 * hf) =
+              float2{dk[0][q] + tl * (gk[0][q] + hv[0][q]), dk[1][q] + tl * (gk[1][q] + hv[1][q])};
+        }
       }
     }
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) quad[threadIdx.x] = quadpart[0][threadIdx.x] + quadpart[1][threadIdx.x];
+    __syncthreads();
+    if (tid < 64) quad[tid] = quadpart[0][tid] + quadpart[1][tid];
+    fetch_keys(sx);
 
-  // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>
-  // (<G, S0> = <G + G^T, S0> / 2 since S0 is symmetric), the C0 terms summed
-  // over the value tiles from the first (whose H and dout tiles are in LDS).
-  // The chunk's start evidence is the start of its first sub-chunk.
-  rs.store(Kt);
-  rc.store(Vt);
-  __syncthreads();
-  {
-    float part = 0.f;
-    for (int e = threadIdx.x; e < 4096; e += GRADS_THREADS) {
-      const int row = e >> 6, col = e & 63;
-      part += 0.5f * M1[row * LDT + col] * Kt[row * LDT + col];
-    }
-    f4 ys[2], dc[2];
-    zero2(ys);
-    zero2(dc);
-    tile_mma_half<false, false>(ys, Yt, Kt, 64, ws, hf);  // y_t^T S0
-    for (int v = 0; v < d.NV; ++v) {
-      if (v > 0) {
-        TileRegs2 rhv, rcv, rd;
-        rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
-        rcv.fetch_matrix(cross_tile(start_c, d, si.seq, v));
-        rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
-        __syncthreads();
-        rhv.store(M2);
-        rcv.store(Vt);
-        rd.store(Dt);
-        __syncthreads();
+    // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>,
+    // the C0 terms summed over the value tiles from the first (whose H and
+    // dout tiles are in LDS).  <G, S0> and, with one value tile, <H, C0> come
+    // from the fetch registers (both operands in the same layout).  The
+    // chunk's start evidence is the start of its first sub-chunk.
+    rs.store(Kt);
+    rc.store(Vt);
+    __syncthreads();
+    {
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part += rg.v[j][i] * rs.v[j][i];
+      f4 ys[2], dc[2];
+      zero2(ys);
+      zero2(dc);
+      tile_mma_half<false, false>(ys, Yt, Kt, 64, ws, hf);  // y_t^T S0
+      rt[1].fetch_rows(sx.len, value_rows(values, d, sx, 0));
+      for (int v = 0; v < d.NV; ++v) {
+        if (v > 0) {
+          TileRegs2 rhv, rcv, rd;
+          rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
+          rcv.fetch_matrix(cross_tile(start_c, d, si.seq, v));
+          rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+          __syncthreads();
+          rhv.store(M2);
+          rcv.store(Vt);
+          rd.store(Dt);
+          __syncthreads();
+        }
+        if (d.NV == 1) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) part += rh.v[j][i] * rc.v[j][i];
+        } else {
+          for (int e = tid; e < 4096; e += GRADS_THREADS) {
+            const int row = e >> 6, col = e & 63;
+            part += M2[row * LDT + col] * Vt[row * LDT + col];
+          }
+        }
+        tile_mma_half<false, false>(dc, Dt, Vt, 64, ws, hf);  // dout_t^T C0, summed
       }
-      for (int e = threadIdx.x; e < 4096; e += GRADS_THREADS) {
-        const int row = e >> 6, col = e & 63;
-        part += M2[row * LDT + col] * Vt[row * LDT + col];
+      red[tid] = part;
+      rt[4].fetch_rows(sx.len, value_rows(d_output, d, sx, 0));
+      fetch_scalars(sx);
+      float sp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = acc_row(ws, q);
+        const float2 yr = *reinterpret_cast<const float2*>(Yt + t * LDT + c4 + 2 * hf);
+        const float2 zr = *reinterpret_cast<const float2*>(Zt + t * LDT + c4 + 2 * hf);
+        sp[q] += dc[0][q] * yr.x - ys[0][q] * zr.x;
+        sp[q] += dc[1][q] * yr.y - ys[1][q] * zr.y;
       }
-      tile_mma_half<false, false>(dc, Dt, Vt, 64, ws, hf);  // dout_t^T C0, summed
-    }
-    red[threadIdx.x] = part;
-    float sp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(ws, q);
-      const float2 yr = *reinterpret_cast<const float2*>(Yt + t * LDT + c4 + 2 * hf);
-      const float2 zr = *reinterpret_cast<const float2*>(Zt + t * LDT + c4 + 2 * hf);
-      sp[q] += dc[0][q] * yr.x - ys[0][q] * zr.x;
-      sp[q] += dc[1][q] * yr.y - ys[1][q] * zr.y;
+      for (int q = 0; q < 4; ++q) {
+        const float v = row16_sum(sp[q]);
+        if (r == 0) startpart[hf][acc_row(ws, q)] = v;
+      }
     }
+    __syncthreads();
+    if (tid < 64) {
+      const int t = tid;
+      startdot[t] = expf(cs.prefix[t]) * (startpart[0][t] + startpart[1][t]);
+      float v = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float v = row16_sum(sp[q]);
-      if (r == 0) startpart[hf][acc_row(ws, q)] = v;
+      for (int k = 0; k < GRADS_THREADS / 64; ++k) v += red[t + 64 * k];
+      v = group4_sum(row16_sum(v));
+      red[t] = v;  // every lane of wave 0 holds the total
     }
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int t = threadIdx.x;
-    startdot[t] = expf(cs.prefix[t]) * (startpart[0][t] + startpart[1][t]);
-    float v = 0.f;
-#pragma unroll
-    for (int k = 0; k < GRADS_THREADS / 64; ++k) v += red[t + 64 * k];
-    v = group4_sum(row16_sum(v));
-    red[t] = v;  // every lane of wave 0 holds the total
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // Phase 5: beta and log-decay gradients (wave 0), queries and floor.
-  if (threadIdx.x < 64) {
-    const int t = threadIdx.x;
-    const float p_last = cs.prefix[MAXC - 1];
-    float eend = 0.f, dp = 0.f, db = 0.f;
-    if (t < si.len) {
-      eend = cs.tail[t] * quad[t];
-      dp = rowE[t] - cs.beta[t] * colD2[t] + startdot[t] - eend;
-      db = colD2[t] + expf(p_last - cs.prefix[t]) * quad[t];
-    }
-    const float eend_total = group4_sum(row16_sum(eend));
-    if (t == si.len - 1) dp += expf(p_last) * red[0] + eend_total;
-    // d log_decay_r = sum_{t >= r} d prefix_t (reverse inclusive sum).
-    float suffix = dp;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float y = __shfl_down(suffix, o, 64);
-      if (t + o < 64) suffix += y;
-    }
-    if (t < si.len) {
-      const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
-      d_beta[th] = db;
-      d_log_decay[th] = suffix;
-    }
-  }
-  // Queries, d q_t = z_t + dvar_t y_t, in the tile-fetch layout (rows
-  // r0 + 32j, columns c4..c4+3), and the floor partial -sum_t z_t * y_t:
-  // per thread over its two rows, then over the lanes and waves holding the
-  // same columns, in a fixed order.
-  {
-    f4 fsum = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int t = (threadIdx.x >> 4) + 32 * j;
-      const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
-      const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
+    // Phase 5: beta and log-decay gradients (wave 0), queries and floor.
+    if (tid < 64) {
+      const int t = tid;
+      const float p_last = cs.prefix[MAXC - 1];
+      float eend = 0.f, dp = 0.f, db = 0.f;
+      if (t < si.len) {
+        eend = cs.tail[t] * quad[t];
+        dp = rowE[t] - cs.beta[t] * colD2[t] + startdot[t] - eend;
+        db = colD2[t] + expf(p_last - cs.prefix[t]) * quad[t];
+      }
+      const float eend_total = group4_sum(row16_sum(eend));
+      if (t == si.len - 1) dp += expf(p_last) * red[0] + eend_total;
+      // d log_decay_r = sum_{t >= r} d prefix_t (reverse inclusive sum).
+      const float suffix = wave_suffix_sum(dp);
       if (t < si.len) {
         const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
-        *reinterpret_cast<f4*>(d_queries + th * 64 + c4) = zr + dvar[j] * yr;
+        d_beta[th] = db;
+        d_log_decay[th] = suffix;
       }
-      fsum -= zr * yr;  // zero past the chunk's tokens
     }
+    // Queries, d q_t = z_t + dvar_t y_t, in the tile-fetch layout (rows
+    // r0 + 32j, columns c4..c4+3), and the floor partial -sum_t z_t * y_t:
+    // per thread over its two rows, then over the lanes and waves holding the
+    // same columns, in a fixed order.
+    {
+      f4 fsum = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fsum[i] = group4_sum(fsum[i]);
-    if (l < 16) fpart[w8][l] = fsum;
-    __syncthreads();
-    if (threadIdx.x < 16) {
-      f4 total = fpart[0][threadIdx.x];
+      for (int j = 0; j < 2; ++j) {
+        const int t = (tid >> 4) + 32 * j;
+        const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
+        const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
+        if (t < si.len) {
+          const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+          *reinterpret_cast<f4*>(d_queries + th * 64 + c4) = zr + dvar[j] * yr;
+        }
+        fsum -= zr * yr;  // zero past the chunk's tokens
+      }
 #pragma unroll
-      for (int k = 1; k < 8; ++k) total += fpart[k][threadIdx.x];
-      *reinterpret_cast<f4*>(floor_part + si.seq * 64 + 4 * threadIdx.x) = total;
+      for (int i = 0; i < 4; ++i) fsum[i] = group4_sum(fsum[i]);
+      if (l < 16) fpart[w8][l] = fsum;
+      __syncthreads();
+      if (tid < 16) {
+        f4 total = fpart[0][tid];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) total += fpart[k][tid];
+        *reinterpret_cast<f4*>(floor_part + si.seq * 64 + 4 * tid) = total;
+      }
     }
+    if (!more) break;
+    seq = next;
+    si = sx;
+    __syncthreads();  // phase 5 has read the tiles and partial sums
   }
 }
 

@@ -61,31 +61,67 @@ __device__ __forceinline__ int sub_len(const Dims& d, int n, int u) {
   return end > first ? end - first : 0;
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
+// Cross-lane reads on DPP and permlane (no LDS round trip).  dpp_read<CTRL,
+// ROW_MASK>(x) is x at the lane CTRL selects; rows masked off and sources
+// out of range read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_read(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, true));
+}
+
+__device__ __forceinline__ float read_lane(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave: within each 16-lane
+// row by row_shr 1, 2, 4, 8, then row r + 1 takes the end of row r
+// (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3).
 __device__ __forceinline__ float wave_inclusive_sum(float x) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    float y = __shfl_up(x, o, 64);
-    if (l >= o) x += y;
-  }
+  x += dpp_read<0x111>(x);
+  x += dpp_read<0x112>(x);
+  x += dpp_read<0x114>(x);
+  x += dpp_read<0x118>(x);
+  x += dpp_read<0x142, 0xa>(x);
+  x += dpp_read<0x143, 0xc>(x);
   return x;
 }
 
-// Sum over the 16 lanes of a row (lanes differing in bits 0..3).
+// Reverse inclusive sum (lane t: sum over lanes u >= t): within each row by
+// row_shl 1, 2, 4, 8, then the totals of the later rows (read from lanes
+// 16, 32, 48) are added.
+__device__ __forceinline__ float wave_suffix_sum(float x) {
+  x += dpp_read<0x101>(x);
+  x += dpp_read<0x102>(x);
+  x += dpp_read<0x104>(x);
+  x += dpp_read<0x108>(x);
+  const float s1 = read_lane(x, 16), s2 = read_lane(x, 32), s3 = read_lane(x, 48);
+  const int row = lane_id() >> 4;
+  return x + (row == 0 ? s1 + (s2 + s3) : row == 1 ? s2 + s3 : row == 2 ? s3 : 0.f);
+}
+
+// Sum over the 16 lanes of a row (lanes differing in bits 0..3): the pairs,
+// quads, halves and rows meet in the order of xor 1, 2, 4, 8 butterflies,
+// and every lane receives the same total.
 __device__ __forceinline__ float row16_sum(float x) {
-  x += __shfl_xor(x, 1, 64);
-  x += __shfl_xor(x, 2, 64);
-  x += __shfl_xor(x, 4, 64);
-  x += __shfl_xor(x, 8, 64);
+  x += dpp_read<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_read<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_read<0x141>(x);  // row_half_mirror
+  x += dpp_read<0x140>(x);  // row_mirror
   return x;
 }
 
-// Sum over the 4 lane groups of 16 (lanes differing in bits 4..5).
+// Sum over the 4 lane groups of 16 (lanes differing in bits 4..5), in the
+// order of xor 16 then xor 32 butterflies.  permlane16_swap(x, x) yields the
+// rows (x0, x0, x2, x2) and (x1, x1, x3, x3); permlane32_swap(x, x) yields
+// (x0, x1, x0, x1) and (x2, x3, x2, x3).
 __device__ __forceinline__ float group4_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // The mixer's raw keys and queries as the memory read's inputs, transformed
@@ -148,6 +184,17 @@ struct ChunkScalars {
   float beta[MAXC];
 };
 
+// Wave 0 (lane s holds token s's log decay g and beta bt, zero past the
+// chunk): the prefix, betas and tails of the chunk.
+__device__ __forceinline__ void finish_chunk_scalars(ChunkScalars& cs, float g, float bt) {
+  const int s = lane_id();
+  const float p = wave_inclusive_sum(g);
+  const float last = read_lane(p, 63);
+  cs.prefix[s] = p;
+  cs.beta[s] = bt;
+  cs.tail[s] = bt * expf(last - p);
+}
+
 __device__ inline void load_chunk_scalars(ChunkScalars& cs, const Dims& d, const float* beta,
                                           const float* log_decay, int b, int h, int n) {
   if (threadIdx.x < 64) {
@@ -159,11 +206,7 @@ __device__ inline void load_chunk_scalars(ChunkScalars& cs, const Dims& d, const
       g = log_decay[th];
       bt = beta[th];
     }
-    float p = wave_inclusive_sum(g);
-    float last = __shfl(p, 63, 64);
-    cs.prefix[s] = p;
-    cs.beta[s] = bt;
-    cs.tail[s] = bt * expf(last - p);
+    finish_chunk_scalars(cs, g, bt);
   }
 }
 

@@ -393,8 +393,8 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
       // Inclusive log-decay prefix over the chunk; part 0 ends at token
       // `cut` - 1 (the sub-chunk boundary, or the chunk end).
       const int cnt = chunk_len(d, i), cut = parts == 2 ? min(d.sub, cnt) : cnt;
-      const float p = wave_inclusive_sum(R.pg), last = __shfl(p, 63, 64);
-      const float mid = cut > 0 ? __shfl(p, cut - 1, 64) : 0.f;
+      const float p = wave_inclusive_sum(R.pg), last = read_lane(p, 63);
+      const float mid = cut > 0 ? read_lane(p, cut - 1) : 0.f;  // cut is uniform
       if (BWD) {
         sb[u].wt[0][l] = (cross ? 1.f : -0.5f) * expf(p);
       } else {
