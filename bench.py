@@ -43,10 +43,14 @@ lm/kernels/flashmamba.py:1125-1162) forward and backward at the 125M model's
 Mamba-3 mixer shape (B=16, L=1024, H=24 heads of P=64, N=128, A=32 angle
 rates; lm/configs/mamba4-125m.json), fp32, through m3s_forward /
 m3s_backward; the roofline is the dominant kernel's MFMA rate against the
-fp32 peak.
+fp32 peak.  --workload mamba3_bf16 is the same step for a bfloat16 model
+(c, b, x and d_y in bfloat16, m3s_forward_bf16 / m3s_backward_bf16: the
+reference's bfloat16 matrix operands), its roofline against the dense bf16
+MFMA peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload config2|config3|ref125m|config4|mixer|mixer_read|mamba3]
+                       [--workload config2|config3|ref125m|config4|mixer|mixer_read|mamba3
+                                   |mamba3_bf16]
 """
 
 import argparse
@@ -73,6 +77,7 @@ REF125M_METRIC = ("memory-read fwd+bwd tokens/sec at B16 L1024 H12 d64 P128 "
 REF125M_TPU_TOKENS_PER_S = 16 * 1024 / 0.06798
 HBM_PEAK_GBPS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA (no sparsity)
 FACTOR_BYTES = 8320  # packed lower factor per token-head
 CHOLESKY_FLOP = 89440  # D^3/3 + D^2/2 + D/6 at D = 64
 RESOLVE_BYTES = 8832  # factor + rhs + z per token-head in the backward re-solve
@@ -160,7 +165,7 @@ def parse():
     p.add_argument("--chunk", type=int, default=64)
     p.add_argument("--workload", default="config2",
                    choices=["config2", "config3", "ref125m", "config4", "mixer", "mixer_read",
-                            "mamba3"])
+                            "mamba3", "mamba3_bf16"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
@@ -647,6 +652,8 @@ def main_mixer_read(args):
 
 MAMBA3_METRIC = ("Mamba-3 fused scan fwd+bwd tokens/sec at B16 L1024 H24 P64 N128 A32 "
                  "(125M mixer shape); % fp32 MFMA peak")
+MAMBA3_BF16_METRIC = ("Mamba-3 fused scan fwd+bwd tokens/sec, bf16 model, at B16 L1024 H24 P64 "
+                      "N128 A32 (125M mixer shape); % bf16 MFMA peak")
 # Algorithmic flop per (chunk of 64 tokens, head) of each scan kernel at
 # N = 128, P = 64: 2 flop per multiply-add of the products the algorithm
 # needs, causal products counted over the 2080 (t, s <= t) pairs only.
@@ -679,7 +686,7 @@ def mamba3_cpu_baseline(host):
     }
 
 
-def main_mamba3(args):
+def main_mamba3(args, bf16=False):
     import torch
 
     from mamba4_amd import _lib
@@ -692,12 +699,20 @@ def main_mamba3(args):
     host = oracle.inputs(batch=B, length=T, heads=H, dim=N, width=P, angle_count=A, seed=0)
     host["d_y"] = np.random.default_rng(1).normal(size=host["x"].shape)
     dev = {n: torch.tensor(np.asarray(v, np.float32), device="cuda:0") for n, v in host.items()}
+    rows = ("c", "b", "x", "d_y")
+    if bf16:
+        for n in rows:
+            dev[n] = dev[n].to(torch.bfloat16)
+    forward = lib.m3s_forward_bf16 if bf16 else lib.m3s_forward
+    backward = lib.m3s_backward_bf16 if bf16 else lib.m3s_backward
+    peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
     f32 = dict(dtype=torch.float32, device="cuda:0")
-    y = torch.empty(B, T, H * P, **f32)
+    y = torch.empty(B, T, H * P, dtype=dev["x"].dtype, device="cuda:0")
     final = torch.empty(B, H, N, P, **f32)
     starts = torch.empty(B, H, NC, 8192, **f32)
     phases = torch.empty(B, H, NC, 64, **f32)
-    grads = [torch.empty_like(dev[n]) for n in oracle.ARGS]
+    grads = [torch.empty(dev[n].shape, dtype=dev[n].dtype if n == "x" else torch.float32,
+                         device="cuda:0") for n in oracle.ARGS]
     nbytes = lib.m3s_backward_workspace_bytes(B, T, H, N, P, A)
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
     st = torch.cuda.current_stream().cuda_stream
@@ -705,11 +720,10 @@ def main_mamba3(args):
     dims = (B, T, H, N, P, A)
 
     def step():
-        check(lib.m3s_forward(*ins, *dims, y.data_ptr(), final.data_ptr(), starts.data_ptr(),
-                              phases.data_ptr(), st))
-        check(lib.m3s_backward(*ins, *dims, starts.data_ptr(), phases.data_ptr(),
-                               dev["d_y"].data_ptr(), None, *(g.data_ptr() for g in grads),
-                               ws.data_ptr(), nbytes, st))
+        check(forward(*ins, *dims, y.data_ptr(), final.data_ptr(), starts.data_ptr(),
+                      phases.data_ptr(), st))
+        check(backward(*ins, *dims, starts.data_ptr(), phases.data_ptr(), dev["d_y"].data_ptr(),
+                       None, *(g.data_ptr() for g in grads), ws.data_ptr(), nbytes, st))
 
     for _ in range(args.warmup):
         step()
@@ -749,9 +763,9 @@ def main_mamba3(args):
         ms = kernel_ms.get(name)
         if ms:
             rate = flop * units / (ms / 1e3) / 1e12
-            kernels[name] = {"ms": ms, "TFLOPs": rate, "frac": rate / FP32_PEAK_TFLOPS}
+            kernels[name] = {"ms": ms, "TFLOPs": rate, "frac": rate / peak}
     line = {
-        "metric": MAMBA3_METRIC,
+        "metric": MAMBA3_BF16_METRIC if bf16 else MAMBA3_METRIC,
         "value": B * T / seconds,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -761,19 +775,21 @@ def main_mamba3(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16" if bf16 else "f32",
         "data": "synthetic",
-        "config": {"workload": "mamba3 scan fwd+bwd, B=16 L=1024 H=24 P=64 N=128 A=32 fp32",
+        "config": {"workload": "mamba3 scan fwd+bwd, B=16 L=1024 H=24 P=64 N=128 A=32 "
+                               + ("bf16 model (bf16 operands, f32 accumulation)" if bf16
+                                  else "fp32"),
                    "batch": B, "seq_len": T, "heads": H, "state_dim": N, "head_dim": P,
                    "angles": A},
         "roofline": {
             "kernel": dominant,
             "bound": "mfma",
             "achieved": achieved,
-            "peak": FP32_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": achieved / FP32_PEAK_TFLOPS,
-            "traffic": measured_traffic(dominant, MAMBA3_TRAFFIC_SUMMARY),
+            "frac": achieved / peak,
+            "traffic": None if bf16 else measured_traffic(dominant, MAMBA3_TRAFFIC_SUMMARY),
             "traffic_unit": "B per launch (rocprofv3, profiles/mamba3_scan_hbm_traffic.md)",
             "algorithmic_flop": MAMBA3_FLOP[dominant] * units,
         },
@@ -916,8 +932,8 @@ def main():
         return main_mixer_read(args)
     if args.workload == "mixer":
         return main_mixer(args)
-    if args.workload == "mamba3":
-        return main_mamba3(args)
+    if args.workload in ("mamba3", "mamba3_bf16"):
+        return main_mamba3(args, bf16=args.workload == "mamba3_bf16")
     if args.workload == "ref125m":
         from mamba4_amd.inputs import reference_benchmark_inputs
 

@@ -18,6 +18,7 @@
 #define MAMBA3_SCAN_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -53,6 +54,22 @@ int m3s_forward(const float* c, const float* b, const float* x, const float* adt
                 const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
                 int A, float* y, float* final_state, float* starts, float* phases, void* stream);
 
+/*
+ * m3s_forward for a bfloat16 model: c, b, x and y are bfloat16 (raw bits),
+ * and every matrix product takes bfloat16 operands with float32
+ * accumulation at the points where the reference's fused kernel rounds to
+ * the model dtype (lm/kernels/flashmamba.py:575-586, 634-659): the
+ * bias-added rows before their rotation, the rotated queries and keys, the
+ * masked score mix, the carried state and the source-weighted values; y is
+ * rounded once at the end.  The residuals and the final state stay float32
+ * (:971-976).  Alignment: c, b 4 bytes, x 8 bytes.
+ */
+int m3s_forward_bf16(const uint16_t* c, const uint16_t* b, const uint16_t* x, const float* adt,
+                     const float* dt, const float* trap_logits, const float* angles,
+                     const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                     int A, uint16_t* y, float* final_state, float* starts, float* phases,
+                     void* stream);
+
 /* Bytes of the workspace m3s_backward needs for this shape. */
 size_t m3s_backward_workspace_bytes(int B, int T, int H, int N, int P, int A);
 
@@ -75,6 +92,23 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
                  const float* d_final, float* d_c, float* d_b, float* d_x, float* d_adt,
                  float* d_dt, float* d_trap, float* d_angles, float* d_q_bias, float* d_k_bias,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * m3s_backward for a bfloat16 model (the residuals of m3s_forward_bf16):
+ * c, b, x, d_y and d_x are bfloat16; the other gradients float32.  The
+ * products round their operands as the reference's fused backward kernel
+ * does (lm/kernels/flashmamba.py:721-751: the score mixes and their
+ * cotangent, the e^p-scaled cotangent, the carried states), d_y having been
+ * rounded to the model dtype (:1008).  Alignment: c, b 4 bytes, x, d_y 8.
+ */
+int m3s_backward_bf16(const uint16_t* c, const uint16_t* b, const uint16_t* x, const float* adt,
+                      const float* dt, const float* trap_logits, const float* angles,
+                      const float* q_bias, const float* k_bias, int B, int T, int H, int N,
+                      int P, int A, const float* starts, const float* phases,
+                      const uint16_t* d_y, const float* d_final, float* d_c, float* d_b,
+                      uint16_t* d_x, float* d_adt, float* d_dt, float* d_trap, float* d_angles,
+                      float* d_q_bias, float* d_k_bias, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -89,6 +89,8 @@ SIGNATURES = {
     "m3s_forward": (_I, [_P] * 9 + [_I] * 6 + [_P] * 4 + [_P]),
     "m3s_backward_workspace_bytes": (_S, [_I] * 6),
     "m3s_backward": (_I, [_P] * 9 + [_I] * 6 + [_P] * 4 + [_P] * 9 + [_P, _S, _P]),
+    "m3s_forward_bf16": (_I, [_P] * 9 + [_I] * 6 + [_P] * 4 + [_P]),
+    "m3s_backward_bf16": (_I, [_P] * 9 + [_I] * 6 + [_P] * 4 + [_P] * 9 + [_P, _S, _P]),
     "m4mr_profile_enable": (None, [_I]),
     "m4mr_profile_select": (None, [ctypes.c_char_p]),
     "m4mr_profile_reset": (None, []),

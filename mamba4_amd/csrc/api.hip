@@ -163,10 +163,14 @@ int configure() {
              {(const void*)m4::states_kernel<false, m4::bf16_t, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, float, true>, kStatesLdsBytes},
-             {(const void*)m3::walk_kernel<false>, m3::kWalkLds},
-             {(const void*)m3::walk_kernel<true>, m3::kWalkLds},
-             {(const void*)m3::out_kernel, m3::kOutLds},
-             {(const void*)m3::grad_kernel, m3::kGradLds},
+             {(const void*)m3::walk_kernel<false, float>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true, float>, m3::kWalkLds},
+             {(const void*)m3::out_kernel<float>, m3::kOutLds},
+             {(const void*)m3::grad_kernel<float>, m3::kGradLds},
+             {(const void*)m3::walk_kernel<false, m3::bf16_t>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true, m3::bf16_t>, m3::kWalkLds},
+             {(const void*)m3::out_kernel<m3::bf16_t>, m3::kOutLds},
+             {(const void*)m3::grad_kernel<m3::bf16_t>, m3::kGradLds},
              {(const void*)m3::finish_kernel, m3::kFinishLdsMax}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1099,67 +1103,69 @@ bool m3_bad_shape(const char* entry, int B, int T, int H, int N, int P, int A) {
 
 bool misaligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) != 0; }
 
-}  // namespace
+bool misaligned_to(const void* p, uintptr_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) != 0;
+}
 
-extern "C" {
-
-int m3s_forward(const float* c, const float* b, const float* x, const float* adt,
-                const float* dt, const float* trap_logits, const float* angles,
-                const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
-                int A, float* y, float* final_state, float* starts, float* phases, void* stream) {
+// In: float, or m3::bf16_t for the bfloat16 entry points (rows, values and
+// y in bfloat16; c, b need 4-byte and x 8-byte alignment there).
+template <typename In>
+int m3_forward_impl(const char* entry, const In* c, const In* b, const In* x, const float* adt,
+                    const float* dt, const float* trap_logits, const float* angles,
+                    const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                    int A, In* y, float* final_state, float* starts, float* phases,
+                    void* stream) {
   g_error.clear();
-  if (m3_bad_shape("m3s_forward", B, T, H, N, P, A)) return M4MR_EINVAL;
+  const std::string name(entry);
+  if (m3_bad_shape(entry, B, T, H, N, P, A)) return M4MR_EINVAL;
   if (!c || !b || !x || !adt || !dt || !trap_logits || (A > 0 && !angles) || !q_bias ||
       !k_bias || !y || !starts || !phases)
-    return fail(M4MR_EINVAL, "m3s_forward: a required pointer is NULL");
-  if (misaligned8(c) || misaligned8(b) || misaligned8(q_bias) || misaligned8(k_bias) ||
-      misaligned(x) || misaligned(starts))
-    return fail(M4MR_EINVAL, "m3s_forward: c, b, biases need 8-byte and x, starts 16-byte alignment");
+    return fail(M4MR_EINVAL, name + ": a required pointer is NULL");
+  if (misaligned_to(c, 2 * sizeof(In)) || misaligned_to(b, 2 * sizeof(In)) ||
+      misaligned8(q_bias) || misaligned8(k_bias) || misaligned_to(x, 4 * sizeof(In)) ||
+      misaligned(starts))
+    return fail(M4MR_EINVAL, name + ": c, b need 2-element, x 4-element, the biases 8-byte "
+                                    "and starts 16-byte alignment");
   if (int rc = configure()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const m3::Shape s{B, T, H, N, P, A, (T + m3::C - 1) / m3::C};
   int rc = launch("m3_walk", st, [&] {
-    hipLaunchKernelGGL(m3::walk_kernel<false>, dim3(B * H), dim3(512), m3::kWalkLds, st, s, b,
-                       k_bias, x, adt, dt, trap_logits, angles, phases, starts, nullptr,
+    hipLaunchKernelGGL((m3::walk_kernel<false, In>), dim3(B * H), dim3(512), m3::kWalkLds, st, s,
+                       b, k_bias, x, adt, dt, trap_logits, angles, phases, starts, nullptr,
                        final_state);
   });
   if (rc) return rc;
   return launch("m3_out", st, [&] {
-    hipLaunchKernelGGL(m3::out_kernel, dim3(B * s.NC * H), dim3(512), m3::kOutLds, st, s, c, b,
-                       x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, y);
+    hipLaunchKernelGGL(m3::out_kernel<In>, dim3(B * s.NC * H), dim3(512), m3::kOutLds, st, s, c,
+                       b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, y);
   });
 }
 
-size_t m3s_backward_workspace_bytes(int B, int T, int H, int N, int P, int A) {
-  (void)N;
-  (void)P;
-  (void)A;
-  if (B < 1 || T < 1 || H < 1) return 0;
-  return m3_workspace(B, T, H, nullptr, nullptr);
-}
-
-int m3s_backward(const float* c, const float* b, const float* x, const float* adt,
-                 const float* dt, const float* trap_logits, const float* angles,
-                 const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
-                 int A, const float* starts, const float* phases, const float* d_y,
-                 const float* d_final, float* d_c, float* d_b, float* d_x, float* d_adt,
-                 float* d_dt, float* d_trap, float* d_angles, float* d_q_bias, float* d_k_bias,
-                 void* workspace, size_t workspace_bytes, void* stream) {
+template <typename In>
+int m3_backward_impl(const char* entry, const In* c, const In* b, const In* x, const float* adt,
+                     const float* dt, const float* trap_logits, const float* angles,
+                     const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                     int A, const float* starts, const float* phases, const In* d_y,
+                     const float* d_final, float* d_c, float* d_b, In* d_x, float* d_adt,
+                     float* d_dt, float* d_trap, float* d_angles, float* d_q_bias,
+                     float* d_k_bias, void* workspace, size_t workspace_bytes, void* stream) {
   g_error.clear();
-  if (m3_bad_shape("m3s_backward", B, T, H, N, P, A)) return M4MR_EINVAL;
+  const std::string name(entry);
+  if (m3_bad_shape(entry, B, T, H, N, P, A)) return M4MR_EINVAL;
   if (!c || !b || !x || !adt || !dt || !trap_logits || (A > 0 && (!angles || !d_angles)) ||
       !q_bias || !k_bias || !starts || !phases || !d_y || !d_c || !d_b || !d_x || !d_adt ||
       !d_dt || !d_trap || !d_q_bias || !d_k_bias || !workspace)
-    return fail(M4MR_EINVAL, "m3s_backward: a required pointer is NULL");
-  if (misaligned8(c) || misaligned8(b) || misaligned8(q_bias) || misaligned8(k_bias) ||
-      misaligned(x) || misaligned(d_y) || misaligned(starts) ||
+    return fail(M4MR_EINVAL, name + ": a required pointer is NULL");
+  if (misaligned_to(c, 2 * sizeof(In)) || misaligned_to(b, 2 * sizeof(In)) ||
+      misaligned8(q_bias) || misaligned8(k_bias) || misaligned_to(x, 4 * sizeof(In)) ||
+      misaligned_to(d_y, 4 * sizeof(In)) || misaligned(starts) ||
       (reinterpret_cast<uintptr_t>(workspace) & 255))
-    return fail(M4MR_EINVAL,
-                "m3s_backward: c, b, biases need 8-byte, x, d_y, starts 16-byte and the "
-                "workspace 256-byte alignment");
+    return fail(M4MR_EINVAL, name + ": c, b need 2-element, x, d_y 4-element, the biases "
+                                    "8-byte, starts 16-byte and the workspace 256-byte "
+                                    "alignment");
   M3Workspace ws{};
   if (workspace_bytes < m3_workspace(B, T, H, &ws, workspace))
-    return fail(M4MR_EINVAL, "m3s_backward: workspace too small");
+    return fail(M4MR_EINVAL, name + ": workspace too small");
   if (int rc = configure()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const m3::Shape s{B, T, H, N, P, A, (T + m3::C - 1) / m3::C};
@@ -1168,15 +1174,15 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
                       ws.ddt_loc,  ws.D,         ws.qb_part,    ws.kb_part,
                       ws.dc_part,  ws.db_part,   ws.dang_part};
   int rc = launch("m3_walk_bwd", st, [&] {
-    hipLaunchKernelGGL(m3::walk_kernel<true>, dim3(B * H), dim3(512), m3::kWalkLds, st, s, c,
-                       q_bias, d_y, adt, dt, trap_logits, angles, const_cast<float*>(phases),
+    hipLaunchKernelGGL((m3::walk_kernel<true, In>), dim3(B * H), dim3(512), m3::kWalkLds, st, s,
+                       c, q_bias, d_y, adt, dt, trap_logits, angles, const_cast<float*>(phases),
                        ws.dh1, d_final, nullptr);
   });
   if (rc) return rc;
   rc = launch("m3_grad", st, [&] {
-    hipLaunchKernelGGL(m3::grad_kernel, dim3(B * s.NC * groups), dim3(512), m3::kGradLds, st, s,
-                       groups, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases,
-                       starts, ws.dh1, d_y, o);
+    hipLaunchKernelGGL(m3::grad_kernel<In>, dim3(B * s.NC * groups), dim3(512), m3::kGradLds,
+                       st, s, groups, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias,
+                       phases, starts, ws.dh1, d_y, o);
   });
   if (rc) return rc;
   if (A > 0) {
@@ -1195,6 +1201,65 @@ int m3s_backward(const float* c, const float* b, const float* x, const float* ad
   return launch("m3_bias", st, [&] {
     hipLaunchKernelGGL(m3::bias_kernel, dim3(H), dim3(1024), 0, st, s, o, d_q_bias, d_k_bias);
   });
+}
+
+const m3::bf16_t* bf(const uint16_t* p) { return reinterpret_cast<const m3::bf16_t*>(p); }
+
+}  // namespace
+
+extern "C" {
+
+int m3s_forward(const float* c, const float* b, const float* x, const float* adt,
+                const float* dt, const float* trap_logits, const float* angles,
+                const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                int A, float* y, float* final_state, float* starts, float* phases, void* stream) {
+  return m3_forward_impl("m3s_forward", c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias,
+                         B, T, H, N, P, A, y, final_state, starts, phases, stream);
+}
+
+int m3s_forward_bf16(const uint16_t* c, const uint16_t* b, const uint16_t* x, const float* adt,
+                     const float* dt, const float* trap_logits, const float* angles,
+                     const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                     int A, uint16_t* y, float* final_state, float* starts, float* phases,
+                     void* stream) {
+  return m3_forward_impl("m3s_forward_bf16", bf(c), bf(b), bf(x), adt, dt, trap_logits, angles,
+                         q_bias, k_bias, B, T, H, N, P, A, reinterpret_cast<m3::bf16_t*>(y),
+                         final_state, starts, phases, stream);
+}
+
+size_t m3s_backward_workspace_bytes(int B, int T, int H, int N, int P, int A) {
+  (void)N;
+  (void)P;
+  (void)A;
+  if (B < 1 || T < 1 || H < 1) return 0;
+  return m3_workspace(B, T, H, nullptr, nullptr);
+}
+
+int m3s_backward(const float* c, const float* b, const float* x, const float* adt,
+                 const float* dt, const float* trap_logits, const float* angles,
+                 const float* q_bias, const float* k_bias, int B, int T, int H, int N, int P,
+                 int A, const float* starts, const float* phases, const float* d_y,
+                 const float* d_final, float* d_c, float* d_b, float* d_x, float* d_adt,
+                 float* d_dt, float* d_trap, float* d_angles, float* d_q_bias, float* d_k_bias,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  return m3_backward_impl("m3s_backward", c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias,
+                          B, T, H, N, P, A, starts, phases, d_y, d_final, d_c, d_b, d_x, d_adt,
+                          d_dt, d_trap, d_angles, d_q_bias, d_k_bias, workspace,
+                          workspace_bytes, stream);
+}
+
+int m3s_backward_bf16(const uint16_t* c, const uint16_t* b, const uint16_t* x, const float* adt,
+                      const float* dt, const float* trap_logits, const float* angles,
+                      const float* q_bias, const float* k_bias, int B, int T, int H, int N,
+                      int P, int A, const float* starts, const float* phases,
+                      const uint16_t* d_y, const float* d_final, float* d_c, float* d_b,
+                      uint16_t* d_x, float* d_adt, float* d_dt, float* d_trap, float* d_angles,
+                      float* d_q_bias, float* d_k_bias, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return m3_backward_impl("m3s_backward_bf16", bf(c), bf(b), bf(x), adt, dt, trap_logits, angles,
+                          q_bias, k_bias, B, T, H, N, P, A, starts, phases, bf(d_y), d_final,
+                          d_c, d_b, reinterpret_cast<m3::bf16_t*>(d_x), d_adt, d_dt, d_trap,
+                          d_angles, d_q_bias, d_k_bias, workspace, workspace_bytes, stream);
 }
 
 void m4mr_profile_enable(int on) {

@@ -85,10 +85,7 @@ struct TokenGates {
   }
   // Summed log decay of the chunk (every lane receives it).
   __device__ __forceinline__ float total() const {
-    float g = lg;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) g += __shfl_xor(g, off, 64);
-    return g;
+    return group4_sum(row16_sum(lg));
   }
 };
 

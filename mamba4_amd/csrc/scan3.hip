@@ -37,6 +37,68 @@
 namespace m3 {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Inputs in the model dtype: float32, or bfloat16 as raw bits.  With
+// bfloat16 rows and values the kernels also take the reference's bfloat16
+// matrix operands (is_bf16<In>).
+template <typename In>
+struct is_bf16 {
+  static constexpr bool value = false;
+};
+template <>
+struct is_bf16<bf16_t> {
+  static constexpr bool value = true;
+};
+
+__device__ __forceinline__ float lo_bf(unsigned u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float hi_bf(unsigned u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ float2 ld2(const float* p) {
+  return *reinterpret_cast<const float2*>(p);
+}
+__device__ __forceinline__ float2 ld2(const bf16_t* p) {
+  const unsigned u = *reinterpret_cast<const unsigned*>(p);
+  return float2{lo_bf(u), hi_bf(u)};
+}
+__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ f4 ld4(const bf16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return f4{lo_bf(u.x), hi_bf(u.x), lo_bf(u.y), hi_bf(u.y)};
+}
+__device__ __forceinline__ float ld1(const float* p) { return *p; }
+__device__ __forceinline__ float ld1(const bf16_t* p) { return lo_bf(*p); }
+__device__ __forceinline__ void st1(float* p, float v) { *p = v; }
+__device__ __forceinline__ void st1(bf16_t* p, float v) {
+  *p = __builtin_bit_cast(bf16_t, static_cast<__bf16>(v));
+}
+
+// x rounded to bfloat16 (to nearest, ties to even: v_cvt_pk_bf16_f32), as
+// float: the reference's .astype(model dtype) of a float32 value.
+__device__ __forceinline__ float round_bf(float x) {
+  return static_cast<float>(static_cast<__bf16>(x));
+}
+template <bool BF>
+__device__ __forceinline__ float2 round_bf2(float2 v) {
+  if constexpr (BF) return float2{round_bf(v.x), round_bf(v.y)};
+  return v;
+}
+
+__device__ __forceinline__ bf16x2 cvt2(float a, float b) {
+  return __builtin_convertvector(f2{a, b}, bf16x2);
+}
+__device__ __forceinline__ bf16x4 pack4(f4 a) {
+  const bf16x2 p0 = cvt2(a[0], a[1]), p1 = cvt2(a[2], a[3]);
+  return bf16x4{p0[0], p0[1], p1[0], p1[1]};
+}
+__device__ __forceinline__ bf16x8 pack8(f4 a, f4 b) {
+  const bf16x2 p0 = cvt2(a[0], a[1]), p1 = cvt2(a[2], a[3]), p2 = cvt2(b[0], b[1]),
+               p3 = cvt2(b[2], b[3]);
+  return bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
 
 // The thread index through an empty asm: values derived from it cannot be
 // hoisted out of the kernels' chunk and head loops, so index arithmetic is
@@ -82,6 +144,19 @@ __device__ __forceinline__ float row16_sum(float x) {
   x += dpp0<0x122, 0xf>(x);
   x += dpp0<0x121, 0xf>(x);
   return x;
+}
+
+// Sum over the 4 lanes sharing bits 0..3 of the lane index (one per row), in
+// the order of xor 16 then xor 32 butterflies: permlane16_swap(x, x) yields
+// the rows (x0, x0, x2, x2) and (x1, x1, x3, x3), permlane32_swap(x, x)
+// yields (x0, x1, x0, x1) and (x2, x3, x2, x3).
+__device__ __forceinline__ float group4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // sin and cos of x (|x| < 2^16): x = k pi/2 + r with k = rint(2x/pi) and r by
@@ -139,35 +214,69 @@ __device__ __forceinline__ f4 load_k4(const float* p) {
 // (the same assignment for A and B, so the sum is unchanged), which makes a
 // lane's four A (or B) values of the block contiguous when AK (BK) is 1.
 // All of a block's operands are read before its 4 J MFMAs issue.
-template <int J, int AR, int AK, int BK, int BC>
+//
+// BF: both operands rounded to bfloat16 (the reference's model-dtype
+// operands, float32 accumulation), on v_mfma_f32_16x16x32_bf16 over blocks
+// of 32 k (lane group q takes k = 8 q .. 8 q + 7 of each, as eight
+// consecutive operand values) and v_mfma_f32_16x16x16_bf16 for a last block
+// of 16 (k = 4 q .. 4 q + 3).
+template <int J, int AR, int AK, int BK, int BC, bool BF = false>
 __device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const float* B, int c0,
                                     int kb, int ke) {
   const int l = lane_id(), r = l & 15, q = l >> 4;
-  const float* pa = A + (r0 + r) * AR + 4 * q * AK;
-  const float* pb = B + 4 * q * BK + (c0 + r) * BC;
+  if constexpr (BF) {
+    const float* pa = A + (r0 + r) * AR + 8 * q * AK;
+    const float* pb = B + 8 * q * BK + (c0 + r) * BC;
+    int k = kb;
 #pragma unroll 2
-  for (int k = kb; k < ke; k += 16) {
-    const f4 a = load_k4<AK>(pa + k * AK);
-    f4 b[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) b[j] = load_k4<BK>(pb + k * BK + 16 * j * BC);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (; k + 32 <= ke; k += 32) {
+      const bf16x8 a = pack8(load_k4<AK>(pa + k * AK), load_k4<AK>(pa + (k + 4) * AK));
+      bf16x8 b[J];
 #pragma unroll
       for (int j = 0; j < J; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
+        b[j] = pack8(load_k4<BK>(pb + k * BK + 16 * j * BC),
+                     load_k4<BK>(pb + (k + 4) * BK + 16 * j * BC));
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], acc[j], 0, 0, 0);
+    }
+    if (k < ke) {
+      const bf16x4 a = pack4(load_k4<AK>(A + (r0 + r) * AR + (k + 4 * q) * AK));
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const bf16x4 b = pack4(load_k4<BK>(B + (k + 4 * q) * BK + (c0 + 16 * j + r) * BC));
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                           __builtin_bit_cast(s16x4, b),
+                                                           acc[j], 0, 0, 0);
+      }
+    }
+  } else {
+    const float* pa = A + (r0 + r) * AR + 4 * q * AK;
+    const float* pb = B + 4 * q * BK + (c0 + r) * BC;
+#pragma unroll 2
+    for (int k = kb; k < ke; k += 16) {
+      const f4 a = load_k4<AK>(pa + k * AK);
+      f4 b[J];
+#pragma unroll
+      for (int j = 0; j < J; ++j) b[j] = load_k4<BK>(pb + k * BK + 16 * j * BC);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[j][e], acc[j], 0, 0, 0);
+    }
   }
 }
 
 // mma over the first jn (0..2, the same for the whole wave) of two column
 // tiles, each count its own straight-line instantiation.
-template <int AR, int AK, int BK, int BC>
+template <int AR, int AK, int BK, int BC, bool BF = false>
 __device__ __forceinline__ void mma_first2(f4 (&acc)[2], const float* A, int r0, const float* B,
                                            int c0, int kb, int ke, int jn) {
   if (jn >= 2) {
-    mma<2, AR, AK, BK, BC>(acc, A, r0, B, c0, kb, ke);
+    mma<2, AR, AK, BK, BC, BF>(acc, A, r0, B, c0, kb, ke);
   } else if (jn == 1) {
-    mma<1, AR, AK, BK, BC>(*reinterpret_cast<f4(*)[1]>(acc), A, r0, B, c0, kb, ke);
+    mma<1, AR, AK, BK, BC, BF>(*reinterpret_cast<f4(*)[1]>(acc), A, r0, B, c0, kb, ke);
   }
 }
 
@@ -299,9 +408,10 @@ __device__ void phase_table(const Shape& s, const float* ang, const float* dt, i
 // for t < C, n < NT, zero for padding tokens and coordinates.  One pair
 // (2j, 2j+1) per lane, tokens w, w + 4, ... per wave; every global read is
 // issued before the first rotation.  With two sources both are rotated by
-// the same angles.
-template <int NSRC, int NW = 4>
-__device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
+// the same angles.  bfloat16 sources: the bias-added rows are rounded to
+// bfloat16 before the rotation (_rotated, lm/kernels/flashmamba.py:582-585).
+template <int NSRC, int NW = 4, typename In = float>
+__device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
                             const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
                             int b, int c) {
   const int j = lane_id(), n = 2 * j, w = tix() >> 6;
@@ -313,8 +423,7 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
     const bool valid = col && tt < s.T;
 #pragma unroll
     for (int k = 0; k < NSRC; ++k)
-      u[k][m] = valid ? *reinterpret_cast<const float2*>(src[k] + tok_index(s, b, tt) * s.N + n)
-                      : float2{0.f, 0.f};
+      u[k][m] = valid ? ld2(src[k] + tok_index(s, b, tt) * s.N + n) : float2{0.f, 0.f};
   }
   float2 bs[NSRC];
 #pragma unroll
@@ -328,8 +437,8 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
     if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
 #pragma unroll
     for (int k = 0; k < NSRC; ++k) {
-      const float2 v = valid ? float2{u[k][m].x + bs[k].x, u[k][m].y + bs[k].y}
-                             : float2{0.f, 0.f};
+      const float2 v = round_bf2<is_bf16<In>::value>(
+          valid ? float2{u[k][m].x + bs[k].x, u[k][m].y + bs[k].y} : float2{0.f, 0.f});
       *reinterpret_cast<float2*>(dst[k] + t * LQ + n) =
           float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
     }
@@ -339,8 +448,8 @@ __device__ void rotate_rows(const Shape& s, const float* const (&src)[2],
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
 // row_scale[t] (nullptr: 1); zeros past T and P.  Four 16-byte rows pieces
 // per thread, all read before any is stored.
-template <int NTH = 256>
-__device__ void load_values(const Shape& s, const float* src, int b, int c, int h,
+template <int NTH = 256, typename In = float>
+__device__ void load_values(const Shape& s, const In* src, int b, int c, int h,
                             const float* row_scale, float* dst) {
   f4 v[1024 / NTH];
 #pragma unroll
@@ -349,13 +458,13 @@ __device__ void load_values(const Shape& s, const float* src, int b, int c, int 
     const int tt = c * C + t;
     v[i] = f4{0.f, 0.f, 0.f, 0.f};
     if (tt < s.T) {
-      const float* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
+      const In* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
       if (s.P % 4 == 0) {
-        if (p < s.P) v[i] = *reinterpret_cast<const f4*>(row + p);
+        if (p < s.P) v[i] = ld4(row + p);
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          if (p + k < s.P) v[i][k] = row[p + k];
+          if (p + k < s.P) v[i][k] = ld1(row + p + k);
       }
     }
   }
@@ -386,8 +495,8 @@ __device__ void load_state(const float* src, float* dst) {
 // Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
 // takes token t = e % C (consecutive lanes, conflict-free LDS stores) and
 // columns 4 (e / C) .. +3; zeros past T and P.
-template <int NTH = 256>
-__device__ void load_values_t(const Shape& s, const float* src, int b, int c, int h,
+template <int NTH = 256, typename In = float>
+__device__ void load_values_t(const Shape& s, const In* src, int b, int c, int h,
                               float* dst) {
   f4 v[1024 / NTH];
 #pragma unroll
@@ -395,13 +504,13 @@ __device__ void load_values_t(const Shape& s, const float* src, int b, int c, in
     const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C), tt = c * C + t;
     v[i] = f4{0.f, 0.f, 0.f, 0.f};
     if (tt < s.T) {
-      const float* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
+      const In* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
       if (s.P % 4 == 0) {
-        if (p < s.P) v[i] = *reinterpret_cast<const f4*>(row + p);
+        if (p < s.P) v[i] = ld4(row + p);
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          if (p + k < s.P) v[i][k] = row[p + k];
+          if (p + k < s.P) v[i][k] = ld1(row + p + k);
       }
     }
   }
@@ -448,12 +557,13 @@ __device__ __forceinline__ long phase_offset(const Shape& s, int b, int h, int c
 // cotangent of the state at the chunk's end) to `saved`, then
 // S <- e^{p_L} S + Q^T (e^p dy).
 // LDS: rows [C][LQ], vals [C][LV], phase table [C][LA], th0 [AM], scalars.
-template <bool BWD>
-__global__ __launch_bounds__(512) void walk_kernel(Shape s, const float* rows, const float* bias,
-                                                   const float* vals, const float* adt,
+template <bool BWD, typename In>
+__global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, const float* bias,
+                                                   const In* vals, const float* adt,
                                                    const float* dt, const float* trap,
                                                    const float* ang, float* theta0, float* saved,
                                                    const float* init, float* final_state) {
+  constexpr bool BF = is_bf16<In>::value;
   extern __shared__ float sm[];
   float* rt = sm;
   float* vt = rt + C * LQ;
@@ -498,22 +608,20 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const float* rows, c
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const int tt = c * C + w + 8 * m;
-      u[m] = col && tt < s.T
-                 ? *reinterpret_cast<const float2*>(rows + tok_index(s, b, tt) * s.N + 2 * l)
-                 : float2{0.f, 0.f};
+      u[m] = col && tt < s.T ? ld2(rows + tok_index(s, b, tt) * s.N + 2 * l) : float2{0.f, 0.f};
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
       v[i] = f4{0.f, 0.f, 0.f, 0.f};
       if (tt < s.T) {
-        const float* row = vals + (tok_index(s, b, tt) * s.H + h) * s.P;
+        const In* row = vals + (tok_index(s, b, tt) * s.H + h) * s.P;
         if (s.P % 4 == 0) {
-          if (p < s.P) v[i] = *reinterpret_cast<const f4*>(row + p);
+          if (p < s.P) v[i] = ld4(row + p);
         } else {
 #pragma unroll
           for (int k = 0; k < 4; ++k)
-            if (p + k < s.P) v[i][k] = row[p + k];
+            if (p + k < s.P) v[i][k] = ld1(row + p + k);
         }
       }
     }
@@ -539,7 +647,9 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const float* rows, c
       const bool valid = col && tt < s.T;
       float sn = 0.f, cs = 1.f;
       if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
-      const float2 x2 = valid ? float2{u[m].x + bs.x, u[m].y + bs.y} : float2{0.f, 0.f};
+      // The bias-added row in the model dtype, then rotated in float32 (:582-585).
+      const float2 x2 = round_bf2<BF>(valid ? float2{u[m].x + bs.x, u[m].y + bs.y}
+                                            : float2{0.f, 0.f});
       *reinterpret_cast<float2*>(rt + t * LQ + 2 * l) =
           float2{x2.x * cs - x2.y * sn, x2.x * sn + x2.y * cs};
     }
@@ -561,7 +671,7 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const float* rows, c
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[0][j] *= decay;
     // rows^T vals: A(n, t) = rt[t * LQ + n], B(t, p) = vt[t * LV + p].
-    mma<4, 1, LQ, LV, 1>(acc[0], rt, 16 * w, vt, 0, 0, C);
+    mma<4, 1, LQ, LV, 1, BF>(acc[0], rt, 16 * w, vt, 0, 0, C);
   }
   if (!BWD && final_state) {
 #pragma unroll
@@ -589,12 +699,14 @@ __device__ __forceinline__ int xcd_block(int total) {
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
 // LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 transposed
 // [PT][LQ] (first the phase table), V transposed [PT][LV], scalars.
-__global__ __launch_bounds__(512) void out_kernel(Shape s, const float* cq, const float* bk,
-                                                  const float* x, const float* adt,
+template <typename In>
+__global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const In* bk,
+                                                  const In* x, const float* adt,
                                                   const float* dt, const float* trap,
                                                   const float* ang, const float* qb,
                                                   const float* kb, const float* theta0,
-                                                  const float* starts, float* y) {
+                                                  const float* starts, In* y) {
+  constexpr bool BF = is_bf16<In>::value;
   extern __shared__ float sm[];
   float* qt = sm;
   float* kt = qt + C * LQ;
@@ -616,10 +728,10 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const float* cq, cons
   phase_table<8>(s, ang, dt, b, h, c, th0, tab, false);
   __syncthreads();
   {
-    const float* const src[2] = {cq, bk};
+    const In* const src[2] = {cq, bk};
     const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
     float* const dst[2] = {qt, kt};
-    rotate_rows<2, 8>(s, src, bsrc, dst, tab, b, c);
+    rotate_rows<2, 8, In>(s, src, bsrc, dst, tab, b, c);
   }
   __syncthreads();
   // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
@@ -632,8 +744,8 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const float* cq, cons
   f4 sco[2], qh[2];
   zero(sco);
   zero(qh);
-  mma_first2<LQ, 1, 1, LQ>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
-  mma<2, LQ, 1, 1, LQ>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
+  mma_first2<LQ, 1, 1, LQ, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+  mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
   __syncthreads();  // every wave is done with K
   float* gs = kt;
 #pragma unroll
@@ -653,14 +765,14 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const float* cq, cons
   f4 acc[2];
   zero(acc);
   // B(s, p) = Vt[p * LV + s].
-  mma<2, LV, 1, 1, LV>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
+  mma<2, LV, 1, 1, LV, BF>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r, tt = c * C + t;
       if (tt < s.T && p < s.P)
-        y[(tok_index(s, b, tt) * s.H + h) * s.P + p] = acc[j][i] + S.ep[t] * qh[j][i];
+        st1(y + (tok_index(s, b, tt) * s.H + h) * s.P + p, acc[j][i] + S.ep[t] * qh[j][i]);
     }
 }
 
@@ -679,13 +791,16 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const float* cq, cons
 // from the end of the chunk: R_t = sum_{t' >= t} dtheta_t'.
 // LDS: R1 = 2 NT LV floats (Q, K; later H0, dH1; later dQ, dK), R2 = 2 NT LV
 // floats (H0, dH1; later V, dY, S o W, G), phase table [C][LA], scalars.
-__global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const float* cq,
-                                                   const float* bk, const float* x,
+template <typename In>
+__global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In* cq,
+                                                   const In* bk, const In* x,
                                                    const float* adt, const float* dt,
                                                    const float* trap, const float* ang,
                                                    const float* qb, const float* kb,
                                                    const float* theta0, const float* starts,
-                                                   const float* dh1, const float* dy, GradOut o) {
+                                                   const float* dh1, const In* dy, GradOut o) {
+  constexpr bool BF = is_bf16<In>::value;
+  In* const dx = static_cast<In*>(o.dx);
   extern __shared__ float sm[];
   float* R1 = sm;
   float* R2 = R1 + 2 * NT * LV;
@@ -736,10 +851,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
     for (int m = 0; m < 8; ++m) {
       const int tt = c * C + w + 8 * m;
       const bool ok = 2 * l < s.N && tt < s.T;
-      rc[m] = ok ? *reinterpret_cast<const float2*>(cq + tok_index(s, b, tt) * s.N + 2 * l)
-                 : float2{0.f, 0.f};
-      rb[m] = ok ? *reinterpret_cast<const float2*>(bk + tok_index(s, b, tt) * s.N + 2 * l)
-                 : float2{0.f, 0.f};
+      rc[m] = ok ? ld2(cq + tok_index(s, b, tt) * s.N + 2 * l) : float2{0.f, 0.f};
+      rb[m] = ok ? ld2(bk + tok_index(s, b, tt) * s.N + 2 * l) : float2{0.f, 0.f};
     }
   }
 
@@ -779,8 +892,10 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         const bool valid = col && tt < s.T;
         float sn = 0.f, cs = 1.f;
         if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
-        const float2 u = valid ? float2{rc[m].x + bq.x, rc[m].y + bq.y} : float2{0.f, 0.f};
-        const float2 v = valid ? float2{rb[m].x + bkv.x, rb[m].y + bkv.y} : float2{0.f, 0.f};
+        const float2 u = round_bf2<BF>(valid ? float2{rc[m].x + bq.x, rc[m].y + bq.y}
+                                             : float2{0.f, 0.f});
+        const float2 v = round_bf2<BF>(valid ? float2{rb[m].x + bkv.x, rb[m].y + bkv.y}
+                                             : float2{0.f, 0.f});
         *reinterpret_cast<float2*>(qt + t * LQ + n2) =
             float2{u.x * cs - u.y * sn, u.x * sn + u.y * cs};
         *reinterpret_cast<float2*>(kt + t * LQ + n2) =
@@ -796,10 +911,10 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
     zero(sco);
     zero(qh);
     zero(kg);
-    mma_first2<LQ, 1, 1, LQ>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+    mma_first2<LQ, 1, 1, LQ, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
     // B(n, p) = H0t[p * LQ + n].
-    mma<2, LQ, 1, 1, LQ>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
-    mma<2, LQ, 1, 1, LQ>(kg, kt, 16 * wr, g1, 32 * wc, 0, NT);
+    mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
+    mma<2, LQ, 1, 1, LQ, BF>(kg, kt, 16 * wr, g1, 32 * wc, 0, NT);
     {
       float part = 0.f;
 #pragma unroll 8
@@ -822,7 +937,7 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
     f4 dsc[2];
     zero(dsc);
     // dY V^T: A(t, p) = dY[t * LV + p], B(p, s) = V[s * LV + p].
-    mma_first2<LV, 1, 1, LV>(dsc, dyt, 16 * wr, vt, 32 * wc, 0, PT, ns);
+    mma_first2<LV, 1, 1, LV, BF>(dsc, dyt, 16 * wr, vt, 32 * wc, 0, PT, ns);
     {
       float qd[4] = {0.f, 0.f, 0.f, 0.f}, gg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -883,10 +998,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         const int jt = 2 * wc + j;
         if (jt > wr) break;
         float f = colF[j], e = colE[j];
-        f += __shfl_xor(f, 16, 64);
-        f += __shfl_xor(f, 32, 64);
-        e += __shfl_xor(e, 16, 64);
-        e += __shfl_xor(e, 32, 64);
+        f = group4_sum(f);
+        e = group4_sum(e);
         if (q == 0) {
           s_colF[64 * wr + 16 * jt + r] = f;
           s_colE[64 * wr + 16 * jt + r] = e;
@@ -901,31 +1014,45 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
     zero(dk);
     zero(dv);
     // G K: A(t, s) = G[t * LV + s], B(s, n) = K[s * LQ + n].
-    mma<4, LV, 1, LQ, 1>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
+    mma<4, LV, 1, LQ, 1, BF>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
     // G^T Q: A(s, t) = G[t * LV + s], B(t, n) = Q[t * LQ + n].
-    mma<4, 1, LV, LQ, 1>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
+    mma<4, 1, LV, LQ, 1, BF>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
     // (S o W)^T dY.
-    mma<2, 1, LV, LV, 1>(dv, gs, 16 * wr, dyt, 32 * wc, 16 * wr, C);
+    mma<2, 1, LV, LV, 1, BF>(dv, gs, 16 * wr, dyt, 32 * wc, 16 * wr, C);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r, tt = c * C + t;
         if (tt < s.T && p < s.P)
-          o.dx[(tok_index(s, b, tt) * s.H + h) * s.P + p] = dv[j][i] + S.u[t] * kg[j][i];
+          st1(dx + (tok_index(s, b, tt) * s.H + h) * s.P + p, dv[j][i] + S.u[t] * kg[j][i]);
       }
     __syncthreads();  // Q, K, S o W and G are no longer read
+    // dY is scaled by e^p before its product (the reference rounds the scaled
+    // cotangent, :740); V's factor u is applied to the product's rows after
+    // it with bfloat16 operands (the reference scales v dH1^T, :749-750),
+    // before it in float32, where the two agree.
     for (int e = tid; e < C * PT; e += 512) {
       const int t = e / PT, p = e % PT;
       dyt[t * LV + p] *= S.ep[t];
-      vt[t * LV + p] *= S.u[t];
+      if (!BF) vt[t * LV + p] *= S.u[t];
     }
     load_state<512>(starts + state_offset(s, b, h, c), R1);
     load_state<512>(dh1 + state_offset(s, b, h, c), R1 + NT * LV);
     __syncthreads();
     // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0[n * LV + p].
-    mma<4, LV, 1, 1, LV>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
-    mma<4, LV, 1, 1, LV>(dk, vt, 16 * wr, R1 + NT * LV, 64 * wc, 0, PT);
+    mma<4, LV, 1, 1, LV, BF>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
+    if constexpr (BF) {
+      f4 vd[4];
+      zero(vd);
+      mma<4, LV, 1, 1, LV, BF>(vd, vt, 16 * wr, R1 + NT * LV, 64 * wc, 0, PT);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dk[j][i] += S.u[16 * wr + 4 * q + i] * vd[j][i];
+    } else {
+      mma<4, LV, 1, 1, LV>(dk, vt, 16 * wr, R1 + NT * LV, 64 * wc, 0, PT);
+    }
     __syncthreads();
     float* dqt = R1;
     float* dkt = R1 + C * LQ;
@@ -958,11 +1085,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const fl
         if (l < s.A) {
           float sn, cs;
           sin_cos(tab[t * LA + l], &sn, &cs);
-          float2 uq = rc[m], uk = rb[m];
-          uq.x += bq.x;
-          uq.y += bq.y;
-          uk.x += bkv.x;
-          uk.y += bkv.y;
+          const float2 uq = round_bf2<BF>(float2{rc[m].x + bq.x, rc[m].y + bq.y});
+          const float2 uk = round_bf2<BF>(float2{rb[m].x + bkv.x, rb[m].y + bkv.y});
           const float q0 = uq.x * cs - uq.y * sn, q1 = uq.x * sn + uq.y * cs;
           const float k0 = uk.x * cs - uk.y * sn, k1 = uk.x * sn + uk.y * cs;
           tab[t * LA + l] = gq.y * q0 - gq.x * q1 + gk.y * k0 - gk.x * k1;
@@ -1174,11 +1298,26 @@ __global__ __launch_bounds__(1024) void bias_kernel(Shape s, GradOut o, float* d
   }
 }
 
-template __global__ void walk_kernel<false>(Shape, const float*, const float*, const float*,
-                                            const float*, const float*, const float*,
-                                            const float*, float*, float*, const float*, float*);
-template __global__ void walk_kernel<true>(Shape, const float*, const float*, const float*,
-                                           const float*, const float*, const float*,
-                                           const float*, float*, float*, const float*, float*);
+#define M3_SCAN_KERNELS(In)                                                                    \
+  template __global__ void walk_kernel<false, In>(Shape, const In*, const float*, const In*,     \
+                                                  const float*, const float*, const float*,      \
+                                                  const float*, float*, float*, const float*,    \
+                                                  float*);                                       \
+  template __global__ void walk_kernel<true, In>(Shape, const In*, const float*, const In*,      \
+                                                 const float*, const float*, const float*,       \
+                                                 const float*, float*, float*, const float*,     \
+                                                 float*);                                        \
+  template __global__ void out_kernel<In>(Shape, const In*, const In*, const In*, const float*,  \
+                                          const float*, const float*, const float*,              \
+                                          const float*, const float*, const float*,              \
+                                          const float*, In*);                                    \
+  template __global__ void grad_kernel<In>(Shape, int, const In*, const In*, const In*,          \
+                                           const float*, const float*, const float*,             \
+                                           const float*, const float*, const float*,             \
+                                           const float*, const float*, const float*, const In*,  \
+                                           GradOut);
+M3_SCAN_KERNELS(float)
+M3_SCAN_KERNELS(bf16_t)
+#undef M3_SCAN_KERNELS
 
 }  // namespace m3

@@ -5,6 +5,8 @@
 
 namespace m3 {
 
+typedef unsigned short bf16_t;  // bfloat16 bits
+
 constexpr int C = 64;       // tokens per chunk (one per lane of a wave)
 constexpr int NT = 128;     // state rows held (N <= NT; padding is zero)
 constexpr int PT = 64;      // value columns held (P <= PT; padding is zero)
@@ -21,7 +23,7 @@ struct Shape {
 
 // Outputs and per-chunk partials of grad_kernel (workspace except dx, d_adt).
 struct GradOut {
-  float* dx;        // [B,T,H*P]
+  void* dx;         // [B,T,H*P] in the model dtype of x
   float* d_adt;     // [B,T,H]
   float* dgam;      // [B,T,H]  gradient of gamma (diagonal weight and scale)
   float* dscale;    // [B,T,H]  gradient of scale alone
@@ -46,16 +48,20 @@ inline size_t finish_lds(int H, int A) {
   return (size_t)(H * AM + C * (A + 1) + C * (H + 1)) * sizeof(float);
 }
 
-template <bool BWD>
-__global__ void walk_kernel(Shape, const float*, const float*, const float*, const float*,
+// In: the model dtype of the rows, values and their cotangents (float, or
+// bf16_t with the reference's bfloat16 matrix operands).
+template <bool BWD, typename In>
+__global__ void walk_kernel(Shape, const In*, const float*, const In*, const float*,
                             const float*, const float*, const float*, float*, float*,
                             const float*, float*);
-__global__ void out_kernel(Shape, const float*, const float*, const float*, const float*,
+template <typename In>
+__global__ void out_kernel(Shape, const In*, const In*, const In*, const float*, const float*,
                            const float*, const float*, const float*, const float*, const float*,
-                           const float*, const float*, float*);
-__global__ void grad_kernel(Shape, int, const float*, const float*, const float*, const float*,
+                           const float*, In*);
+template <typename In>
+__global__ void grad_kernel(Shape, int, const In*, const In*, const In*, const float*,
                             const float*, const float*, const float*, const float*, const float*,
-                            const float*, const float*, const float*, const float*, GradOut);
+                            const float*, const float*, const float*, const In*, GradOut);
 __global__ void finish_kernel(Shape, int, const float*, const float*, const float*, GradOut,
                               float*, float*, float*, float*, float*);
 __global__ void suffix_kernel(Shape, GradOut);

@@ -9,9 +9,14 @@ final state [B,H,N,P].  Gradients reach all nine inputs (the reference's
 custom VJP, :1000-1110, plus the autodiff of its weight and angle glue).
 
 Runs on the gfx950 HIP library (``m3s_forward`` / ``m3s_backward``,
-include/mamba3_scan.h); there is no other implementation.  Arithmetic is
-float32 (bfloat16 inputs are widened on entry; ``y`` returns in ``x``'s
-dtype, the final state in float32, as in the reference).
+include/mamba3_scan.h); there is no other implementation.  With ``c``, ``b``
+and ``x`` all bfloat16 (a bfloat16 model) it takes ``m3s_forward_bf16`` /
+``m3s_backward_bf16``: the products take bfloat16 operands with float32
+accumulation where the reference's fused kernels round to the model dtype
+(lm/kernels/flashmamba.py:575-786), ``y`` and ``d_x`` come back in bfloat16
+and the other gradients in their inputs' dtypes (:1088-1099).  Otherwise the
+arithmetic is float32 (other inputs are widened on entry; ``y`` returns in
+``x``'s dtype).  The final state is float32 either way, as in the reference.
 """
 
 import torch
@@ -32,9 +37,13 @@ def _f32(t):
 
 
 class _FusedScan(torch.autograd.Function):
+    """c, b, x float32, or all three bfloat16 (the bfloat16 entry points);
+    the other inputs float32."""
+
     @staticmethod
     def forward(ctx, c, b, x, adt, dt, trap, angles, q_bias, k_bias):
         lib = _lib.load()
+        bf16 = x.dtype == torch.bfloat16
         batch, time, state = c.shape
         heads = dt.shape[-1]
         width = x.shape[-1] // heads
@@ -46,8 +55,9 @@ class _FusedScan(torch.autograd.Function):
                              device=x.device)
         phases = torch.empty(batch, heads, chunks, PHASE_FLOATS, dtype=torch.float32,
                              device=x.device)
+        entry = lib.m3s_forward_bf16 if bf16 else lib.m3s_forward
         _lib.check(
-            lib.m3s_forward(
+            entry(
                 _ptr(c), _ptr(b), _ptr(x), _ptr(adt), _ptr(dt), _ptr(trap),
                 _ptr(angles) if count else None, _ptr(q_bias), _ptr(k_bias), batch, time,
                 heads, state, width, count, _ptr(y), _ptr(final), _ptr(starts), _ptr(phases),
@@ -65,13 +75,18 @@ class _FusedScan(torch.autograd.Function):
         heads = dt.shape[-1]
         width = x.shape[-1] // heads
         count = angles.shape[-1]
-        d_y = torch.zeros_like(x) if d_y is None else _f32(d_y)
+        bf16 = x.dtype == torch.bfloat16
+        # The cotangent in the model dtype (the reference's d_y.astype(x.dtype), :1008).
+        d_y = torch.zeros_like(x) if d_y is None else d_y.to(x.dtype).contiguous()
         d_final = None if d_final is None else _f32(d_final)
-        grads = [torch.empty_like(t) for t in (c, b, x, adt, dt, trap, angles, q_bias, k_bias)]
+        grads = [torch.empty(t.shape, dtype=x.dtype if i == 2 else torch.float32,
+                             device=t.device)
+                 for i, t in enumerate((c, b, x, adt, dt, trap, angles, q_bias, k_bias))]
         nbytes = lib.m3s_backward_workspace_bytes(batch, time, heads, state, width, count)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        entry = lib.m3s_backward_bf16 if bf16 else lib.m3s_backward
         _lib.check(
-            lib.m3s_backward(
+            entry(
                 _ptr(c), _ptr(b), _ptr(x), _ptr(adt), _ptr(dt), _ptr(trap),
                 _ptr(angles) if count else None, _ptr(q_bias), _ptr(k_bias), batch, time,
                 heads, state, width, count, _ptr(starts), _ptr(phases), _ptr(d_y),
@@ -80,7 +95,8 @@ class _FusedScan(torch.autograd.Function):
                 _ptr(workspace), nbytes, _stream(),
             )
         )
-        return tuple(grads)
+        return tuple(g.to(t.dtype) for g, t in zip(grads, (c, b, x, adt, dt, trap, angles,
+                                                           q_bias, k_bias)))
 
 
 def mamba3_fused(c, b, x, adt, dt, trap_logits, angles, *, q_bias, k_bias, chunk_size=CHUNK,
@@ -118,8 +134,10 @@ def mamba3_fused(c, b, x, adt, dt, trap_logits, angles, *, q_bias, k_bias, chunk
     if time == 0:
         return x.new_zeros(x.shape), x.new_zeros((batch, heads, state, width),
                                                  dtype=torch.float32)
+    bf16 = c.dtype == b.dtype == x.dtype == torch.bfloat16
+    rows = (lambda t: t.contiguous()) if bf16 else _f32
     y, final = _FusedScan.apply(
-        _f32(c), _f32(b), _f32(x), _f32(adt), _f32(dt), _f32(trap_logits), _f32(angles),
+        rows(c), rows(b), rows(x), _f32(adt), _f32(dt), _f32(trap_logits), _f32(angles),
         _f32(q_bias).reshape(q_bias.shape), _f32(k_bias).reshape(k_bias.shape),
     )
     return y.to(x.dtype), final

@@ -117,3 +117,83 @@ def test_rotation_is_orthogonal_and_back_is_its_transpose():
     np.testing.assert_allclose(np.linalg.norm(r, axis=-1), np.linalg.norm(u, axis=-1))
     np.testing.assert_allclose(np.sum(r * du), np.sum(u * m3.rotate_back(du, theta)))
     np.testing.assert_array_equal(r[:, 6:], u[:, 6:])
+
+
+# The fused-kernel restatement with model-dtype rounding (oracle/mamba3_fused.py).
+
+def test_round_bf16_matches_torch_bfloat16():
+    """Round-to-nearest-even to bfloat16, ties included, equals torch's
+    float32 -> bfloat16 conversion."""
+    torch = pytest.importorskip("torch")
+    from oracle import mamba3_fused as mf
+
+    rng = np.random.default_rng(3)
+    x = np.concatenate([
+        rng.normal(size=20000).astype(np.float32) * 10.0 ** rng.integers(-6, 6, 20000),
+        # exact ties: a bfloat16 value plus half its last place, both parities
+        (np.arange(1, 2001, dtype=np.float32) * 2 ** -7 + 2 ** -16).astype(np.float32),
+        np.array([0.0, -0.0, 1.0, -3.5, 65504.0, 1e-38], np.float32),
+    ])
+    want = torch.tensor(x).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(mf.round_bf16(x), want)
+
+
+@pytest.mark.parametrize("chunk,length", [(16, 37), (64, 130), (8, 8)])
+def test_fused_forward_without_rounding_is_the_chunk_algebra(chunk, length):
+    from oracle import mamba3_fused as mf
+
+    x = m3.inputs(batch=2, length=length, heads=3, dim=16, width=8, angle_count=4, seed=4)
+    y, final = _call(m3.forward, x)
+    _, _, starts = _call(m3.chunked_forward, x, chunk=chunk)
+    y_f, final_f, starts_f, phase0 = _call(mf.fused_forward, x, chunk=chunk, rnd=None,
+                                           dtype=np.float64)
+    np.testing.assert_allclose(y_f, y, rtol=1e-10, atol=1e-11)
+    np.testing.assert_allclose(final_f, final, rtol=1e-10, atol=1e-11)
+    np.testing.assert_allclose(starts_f, starts, rtol=1e-10, atol=1e-11)
+    # Start phases: the running phase at each chunk's first token minus its own step.
+    theta = m3.phases(x["angles"], x["dt"])
+    first = np.arange(0, length, chunk)
+    inc = x["angles"][:, first, None, :] * x["dt"][:, first, :, None]
+    want = np.swapaxes(theta[:, first] - inc, 1, 2)
+    np.testing.assert_allclose(phase0[..., 0:8:2], want, rtol=1e-10, atol=1e-11)
+    np.testing.assert_allclose(phase0[..., 1:8:2], want, rtol=1e-10, atol=1e-11)
+
+
+@pytest.mark.parametrize("chunk,length", [(16, 37), (64, 70)])
+def test_fused_backward_without_rounding_matches_the_recurrence(chunk, length):
+    """All nine gradients of the chunk-form backward (with the chunk-end
+    terms and mamba3_fused's glue) equal the finite-difference-pinned token
+    recurrence's."""
+    from oracle import mamba3_fused as mf
+
+    x = m3.inputs(batch=2, length=length, heads=3, dim=16, width=8, angle_count=4, seed=6)
+    rng = np.random.default_rng(7)
+    y, final = _call(m3.forward, x)
+    dy, dfin = rng.normal(size=y.shape), rng.normal(size=final.shape)
+    want = _call(m3.backward, x, d_y=dy, d_final=dfin)
+    got = _call(mf.fused_backward, x, d_y=dy, d_final=dfin, chunk=chunk, rnd=None,
+                dtype=np.float64)
+    for name in m3.ARGS:
+        np.testing.assert_allclose(got[name], want[name], rtol=1e-9, atol=1e-10, err_msg=name)
+
+
+def test_bfloat16_model_rounding_is_bfloat16_sized():
+    """With bfloat16 operands the results move from the exact ones by a few
+    bfloat16 places (not zero, not float32-sized, not wrong): normwise
+    between 2^-12 and 2^-5, for y and for every gradient."""
+    from oracle import mamba3_fused as mf
+
+    x = m3.inputs(batch=1, length=70, heads=2, dim=16, width=8, angle_count=4, seed=8)
+    for n in ("c", "b", "x"):
+        x[n] = mf.round_bf16(x[n]).astype(np.float64)
+    rng = np.random.default_rng(9)
+    dy = mf.round_bf16(rng.normal(size=(1, 70, 16))).astype(np.float64)
+    y64, _, _, _ = _call(mf.fused_forward, x, rnd=None, dtype=np.float64)
+    y16, _, _, _ = _call(mf.fused_forward, x, rnd=mf.round_bf16, dtype=np.float32)
+    err = np.linalg.norm(y16 - y64) / np.linalg.norm(y64)
+    assert 2.0 ** -12 < err < 2.0 ** -5, err
+    g64 = _call(mf.fused_backward, x, d_y=dy, rnd=None, dtype=np.float64)
+    g16 = _call(mf.fused_backward, x, d_y=dy, rnd=mf.round_bf16, dtype=np.float32)
+    for name in m3.ARGS:
+        err = np.linalg.norm(g16[name] - g64[name]) / np.linalg.norm(g64[name])
+        assert 2.0 ** -14 < err < 2.0 ** -5, (name, err)
