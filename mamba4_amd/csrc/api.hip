@@ -368,14 +368,16 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   if (rc) return rc;
   const int polls = turn_polls();
   rc = launch("fwd_factor", st, [&] {
+    // Sixteen sub-chunk sequences per block: four wave pairs of four.
+    const dim3 grid((subseqs + 15) / 16), block(512);
     if (factors)
-      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, true>), dim3((subseqs + 3) / 4),
-                         dim3(128), 0, st, d, keys, queries, beta, log_decay, floor,
-                         start_evidence, solved, factors, mix, polls);
+      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, true>), grid, block, 0, st, d, keys,
+                         queries, beta, log_decay, floor, start_evidence, solved, factors, mix,
+                         polls);
     else
-      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, false>), dim3((subseqs + 3) / 4),
-                         dim3(128), 0, st, d, keys, queries, beta, log_decay, floor,
-                         start_evidence, solved, factors, mix, polls);
+      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, false>), grid, block, 0, st, d, keys,
+                         queries, beta, log_decay, floor, start_evidence, solved, factors, mix,
+                         polls);
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {
