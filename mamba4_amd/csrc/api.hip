@@ -1138,7 +1138,8 @@ int m3_forward_impl(const char* entry, const In* c, const In* b, const In* x, co
   });
   if (rc) return rc;
   return launch("m3_out", st, [&] {
-    hipLaunchKernelGGL(m3::out_kernel<In>, dim3(B * s.NC * H), dim3(512), m3::kOutLds, st, s, c,
+    hipLaunchKernelGGL(m3::out_kernel<In>, dim3(persistent_grid(B * s.NC * H, 1)), dim3(512),
+                       m3::kOutLds, st, s, c,
                        b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, y);
   });
 }

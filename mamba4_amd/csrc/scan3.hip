@@ -411,12 +411,11 @@ __device__ void phase_table(const Shape& s, const float* ang, const float* dt, i
 // the same angles.  bfloat16 sources: the bias-added rows are rounded to
 // bfloat16 before the rotation (_rotated, lm/kernels/flashmamba.py:582-585).
 template <int NSRC, int NW = 4, typename In = float>
-__device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
-                            const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
-                            int b, int c) {
+__device__ __forceinline__ void fetch_rows(const Shape& s, const In* const (&src)[2],
+                                           const float* const (&bias)[2], int b, int c,
+                                           float2 (&u)[NSRC][64 / NW], float2 (&bs)[NSRC]) {
   const int j = lane_id(), n = 2 * j, w = tix() >> 6;
   const bool col = n < s.N;
-  float2 u[NSRC][64 / NW];
 #pragma unroll
   for (int m = 0; m < 64 / NW; ++m) {
     const int tt = c * C + w + NW * m;
@@ -425,10 +424,17 @@ __device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
     for (int k = 0; k < NSRC; ++k)
       u[k][m] = valid ? ld2(src[k] + tok_index(s, b, tt) * s.N + n) : float2{0.f, 0.f};
   }
-  float2 bs[NSRC];
 #pragma unroll
   for (int k = 0; k < NSRC; ++k)
     bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
+}
+
+template <int NSRC, int NW = 4, bool BF = false>
+__device__ __forceinline__ void rotate_fetched(const Shape& s, const float2 (&u)[NSRC][64 / NW],
+                                               const float2 (&bs)[NSRC], float* const (&dst)[2],
+                                               const float* tab, int c) {
+  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
+  const bool col = n < s.N;
 #pragma unroll
   for (int m = 0; m < 64 / NW; ++m) {
     const int t = w + NW * m, tt = c * C + t;
@@ -437,12 +443,21 @@ __device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
     if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
 #pragma unroll
     for (int k = 0; k < NSRC; ++k) {
-      const float2 v = round_bf2<is_bf16<In>::value>(
+      const float2 v = round_bf2<BF>(
           valid ? float2{u[k][m].x + bs[k].x, u[k][m].y + bs[k].y} : float2{0.f, 0.f});
       *reinterpret_cast<float2*>(dst[k] + t * LQ + n) =
           float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
     }
   }
+}
+
+template <int NSRC, int NW = 4, typename In = float>
+__device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
+                            const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
+                            int b, int c) {
+  float2 u[NSRC][64 / NW], bs[NSRC];
+  fetch_rows<NSRC, NW>(s, src, bias, b, c, u, bs);
+  rotate_fetched<NSRC, NW, is_bf16<In>::value>(s, u, bs, dst, tab, c);
 }
 
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
@@ -494,11 +509,11 @@ __device__ void load_state(const float* src, float* dst) {
 
 // Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
 // takes token t = e % C (consecutive lanes, conflict-free LDS stores) and
-// columns 4 (e / C) .. +3; zeros past T and P.
+// columns 4 (e / C) .. +3; zeros past T and P.  fetch_values_t reads this
+// thread's pieces into registers, store_values_t writes them.
 template <int NTH = 256, typename In = float>
-__device__ void load_values_t(const Shape& s, const In* src, int b, int c, int h,
-                              float* dst) {
-  f4 v[1024 / NTH];
+__device__ __forceinline__ void fetch_values_t(const Shape& s, const In* src, int b, int c,
+                                               int h, f4 (&v)[1024 / NTH]) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C), tt = c * C + t;
@@ -514,6 +529,10 @@ __device__ void load_values_t(const Shape& s, const In* src, int b, int c, int h
       }
     }
   }
+}
+
+template <int NTH = 256>
+__device__ __forceinline__ void store_values_t(const f4 (&v)[1024 / NTH], float* dst) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C);
@@ -522,23 +541,41 @@ __device__ void load_values_t(const Shape& s, const In* src, int b, int c, int h
   }
 }
 
+template <int NTH = 256, typename In = float>
+__device__ void load_values_t(const Shape& s, const In* src, int b, int c, int h,
+                              float* dst) {
+  f4 v[1024 / NTH];
+  fetch_values_t<NTH>(s, src, b, c, h, v);
+  store_values_t<NTH>(v, dst);
+}
+
 // A stored [NT][PT] state tile into LDS transposed, [PT][LQ]: thread e takes
 // row n = e % NT (consecutive lanes, conflict-free LDS stores) and columns
 // 4 (e / NT) .. +3, all read before any is stored.
 template <int NTH = 256>
-__device__ void load_state_t(const float* src, float* dst) {
-  f4 v[2048 / NTH];
+__device__ __forceinline__ void fetch_state_t(const float* src, f4 (&v)[2048 / NTH]) {
 #pragma unroll
   for (int i = 0; i < 2048 / NTH; ++i) {
     const int e = tix() + NTH * i;
     v[i] = *reinterpret_cast<const f4*>(src + (e % NT) * PT + 4 * (e / NT));
   }
+}
+
+template <int NTH = 256>
+__device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], float* dst) {
 #pragma unroll
   for (int i = 0; i < 2048 / NTH; ++i) {
     const int e = tix() + NTH * i, n = e % NT, p = 4 * (e / NT);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[(p + k) * LQ + n] = v[i][k];
   }
+}
+
+template <int NTH = 256>
+__device__ void load_state_t(const float* src, float* dst) {
+  f4 v[2048 / NTH];
+  fetch_state_t<NTH>(src, v);
+  store_state_t<NTH>(v, dst);
 }
 
 __device__ __forceinline__ long state_offset(const Shape& s, int b, int h, int c) {
@@ -694,8 +731,15 @@ __device__ __forceinline__ int xcd_block(int total) {
   return (id % 8) * (total / 8) + id / 8;
 }
 
+// The same remap of a persistent kernel's item index (its grid a multiple
+// of 8, so item it runs on the XCD of block it % 8 as in xcd_block).
+__device__ __forceinline__ int xcd_item(int it, int total) {
+  if (total % 8) return it;
+  return (it % 8) * (total / 8) + it / 8;
+}
+
 // ---------------------------------------------------------------------------
-// Output of one (b, chunk, h): y = (S o W) V + diag(e^p) Q S0 with scores
+// Output of each (b, chunk, h) item: y = (S o W) V + diag(e^p) Q S0 with scores
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
 // LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 transposed
 // [PT][LQ] (first the phase table), V transposed [PT][LV], scalars.
@@ -716,64 +760,104 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
   float* th0 = vt + C * LV;
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
-  const int total = s.B * s.NC * s.H, id = xcd_block(total);
-  const int h = id % s.H, c = (id / s.H) % s.NC, b = id / (s.H * s.NC);
-  // Eight waves: wave w owns row block wr = w & 3 and column half wc = w >> 2.
-  const int tid = tix(), l = lane_id(), r = l & 15, q = l >> 4;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
+  const int total = s.B * s.NC * s.H;
+  const In* const src[2] = {cq, bk};
 
-  if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
-  if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
-  __syncthreads();
-  phase_table<8>(s, ang, dt, b, h, c, th0, tab, false);
-  __syncthreads();
-  {
-    const In* const src[2] = {cq, bk};
+  // Every global input of an item, fetched into registers while the
+  // previous item's products run.
+  struct Fetched {
+    TokenIn tin;
+    float th, rates[8];
+    float2 u[2][8], bs[2];
+    f4 hv[4], vv[2];
+  };
+  auto item_of = [&](int it, int& b, int& c, int& h) {
+    const int id = xcd_item(it, total);
+    h = id % s.H;
+    c = (id / s.H) % s.NC;
+    b = id / (s.H * s.NC);
+  };
+  auto fetch = [&](Fetched& F, int it) {
+    int b, c, h;
+    item_of(it, b, c, h);
+    F.tin = fetch_token(s, adt, dt, trap, b, h, c);
+    const int tid = tix();
+    F.th = tid < s.A ? theta0[phase_offset(s, b, h, c) + tid] : 0.f;
+    fetch_angles<8>(s, ang, b, c, F.rates);
     const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
-    float* const dst[2] = {qt, kt};
-    rotate_rows<2, 8, In>(s, src, bsrc, dst, tab, b, c);
-  }
-  __syncthreads();
-  // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
-  // every product reads both operands contiguously along k.
-  load_state_t<512>(starts + state_offset(s, b, h, c), h0);
-  load_values_t<512>(s, x, b, c, h, vt);
-  __syncthreads();
+    fetch_rows<2, 8>(s, src, bsrc, b, c, F.u, F.bs);
+    fetch_state_t<512>(starts + state_offset(s, b, h, c), F.hv);
+    fetch_values_t<512>(s, x, b, c, h, F.vv);
+  };
 
-  const int ns = min(2, max(0, wr + 1 - 2 * wc));
-  f4 sco[2], qh[2];
-  zero(sco);
-  zero(qh);
-  mma_first2<LQ, 1, 1, LQ, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
-  mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
-  __syncthreads();  // every wave is done with K
-  float* gs = kt;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int jt = 2 * wc + j;
-    if (jt > wr) break;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wr + 4 * q + i, u = 16 * jt + r;
-      float wt = 0.f;
-      if (t > u) wt = expf(fminf(S.p[t] - S.p[u], 0.f)) * S.scale[u];
-      else if (t == u) wt = S.gam[t];
-      gs[t * LV + u] = sco[j][i] * wt;
+  // Persistent: block i handles items i, i + gridDim.x, ... (b, chunk, h),
+  // heads fastest, each XCD a contiguous run of (b, chunk) pairs.
+  Fetched F;
+  int it = blockIdx.x;
+  if (it < total) fetch(F, it);
+  for (; it < total; it += gridDim.x) {
+    int b, c, h;
+    item_of(it, b, c, h);
+    // Eight waves: wave w owns row block wr = w & 3 and column half wc = w >> 2.
+    const int tid = tix(), l = lane_id(), r = l & 15, q = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
+
+    if (w == 0) token_scalars(F.tin, S);
+    if (tid < s.A) th0[tid] = F.th;
+    __syncthreads();
+    phase_table<8>(s, F.rates, F.tin.d, th0, tab, false);
+    __syncthreads();
+    {
+      float* const dst[2] = {qt, kt};
+      rotate_fetched<2, 8, BF>(s, F.u, F.bs, dst, tab, c);
     }
+    __syncthreads();  // the phase table (in h0's space) is read
+    // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
+    // every product reads both operands contiguously along k.
+    store_state_t<512>(F.hv, h0);
+    store_values_t<512>(F.vv, vt);
+    __syncthreads();
+    // The next item's inputs load while this one's products run (no global
+    // load is waited for before the next item's staging).
+    const int next = it + gridDim.x;
+    fetch(F, next < total ? next : it);
+
+    const int ns = min(2, max(0, wr + 1 - 2 * wc));
+    f4 sco[2], qh[2];
+    zero(sco);
+    zero(qh);
+    mma_first2<LQ, 1, 1, LQ, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+    mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
+    __syncthreads();  // every wave is done with K
+    float* gs = kt;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int jt = 2 * wc + j;
+      if (jt > wr) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wr + 4 * q + i, u = 16 * jt + r;
+        float wt = 0.f;
+        if (t > u) wt = expf(fminf(S.p[t] - S.p[u], 0.f)) * S.scale[u];
+        else if (t == u) wt = S.gam[t];
+        gs[t * LV + u] = sco[j][i] * wt;
+      }
+    }
+    __syncthreads();  // a row block's S o W comes from both of its waves
+    f4 acc[2];
+    zero(acc);
+    // B(s, p) = Vt[p * LV + s].
+    mma<2, LV, 1, 1, LV, BF>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r, tt = c * C + t;
+        if (tt < s.T && p < s.P)
+          st1(y + (tok_index(s, b, tt) * s.H + h) * s.P + p, acc[j][i] + S.ep[t] * qh[j][i]);
+      }
+    __syncthreads();  // the tiles and scalars are read before the next item's staging
   }
-  __syncthreads();  // a row block's S o W comes from both of its waves
-  f4 acc[2];
-  zero(acc);
-  // B(s, p) = Vt[p * LV + s].
-  mma<2, LV, 1, 1, LV, BF>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r, tt = c * C + t;
-      if (tt < s.T && p < s.P)
-        st1(y + (tok_index(s, b, tt) * s.H + h) * s.P + p, acc[j][i] + S.ep[t] * qh[j][i]);
-    }
 }
 
 // ---------------------------------------------------------------------------
