@@ -462,11 +462,10 @@ __device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
 
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
 // row_scale[t] (nullptr: 1); zeros past T and P.  Four 16-byte rows pieces
-// per thread, all read before any is stored.
+// per thread, all read before any is stored (fetch_values, store_values).
 template <int NTH = 256, typename In = float>
-__device__ void load_values(const Shape& s, const In* src, int b, int c, int h,
-                            const float* row_scale, float* dst) {
-  f4 v[1024 / NTH];
+__device__ __forceinline__ void fetch_values(const Shape& s, const In* src, int b, int c, int h,
+                                             f4 (&v)[1024 / NTH]) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
@@ -483,6 +482,11 @@ __device__ void load_values(const Shape& s, const In* src, int b, int c, int h,
       }
     }
   }
+}
+
+template <int NTH = 256>
+__device__ __forceinline__ void store_values(const f4 (&v)[1024 / NTH], const float* row_scale,
+                                             float* dst) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
@@ -490,21 +494,12 @@ __device__ void load_values(const Shape& s, const In* src, int b, int c, int h,
   }
 }
 
-// A stored [NT][PT] state tile into LDS [NT][LV]: eight 16-byte pieces per
-// thread, all read before any is stored.
-template <int NTH = 256>
-__device__ void load_state(const float* src, float* dst) {
-  f4 v[2048 / NTH];
-#pragma unroll
-  for (int i = 0; i < 2048 / NTH; ++i) {
-    const int e = tix() + NTH * i;
-    v[i] = *reinterpret_cast<const f4*>(src + (e / (PT / 4)) * PT + 4 * (e % (PT / 4)));
-  }
-#pragma unroll
-  for (int i = 0; i < 2048 / NTH; ++i) {
-    const int e = tix() + NTH * i;
-    *reinterpret_cast<f4*>(dst + (e / (PT / 4)) * LV + 4 * (e % (PT / 4))) = v[i];
-  }
+template <int NTH = 256, typename In = float>
+__device__ void load_values(const Shape& s, const In* src, int b, int c, int h,
+                            const float* row_scale, float* dst) {
+  f4 v[1024 / NTH];
+  fetch_values<NTH>(s, src, b, c, h, v);
+  store_values<NTH>(v, row_scale, dst);
 }
 
 // Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
@@ -568,6 +563,17 @@ __device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], float* 
     const int e = tix() + NTH * i, n = e % NT, p = 4 * (e / NT);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[(p + k) * LQ + n] = v[i][k];
+  }
+}
+
+// The same registers (row n = e % NT, columns 4 (e / NT) .. +3) into the
+// untransposed [NT][LV] layout: one 16-byte store each.
+template <int NTH = 256>
+__device__ __forceinline__ void store_state_rows(const f4 (&v)[2048 / NTH], float* dst) {
+#pragma unroll
+  for (int i = 0; i < 2048 / NTH; ++i) {
+    const int e = tix() + NTH * i, n = e % NT, p = 4 * (e / NT);
+    *reinterpret_cast<f4*>(dst + n * LV + p) = v[i];
   }
 }
 
@@ -926,9 +932,12 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     dbacc[m] = float2{0.f, 0.f};
     dang[m] = 0.f;
   }
-  // The chunk's raw query and key rows are the same for every head: this
-  // thread's 8 (token, pair) slots are read once and kept in registers.
+  // The chunk's raw query and key rows and its angle rates are the same for
+  // every head: this thread's 8 (token, pair) slots and 8 (token = lane,
+  // angle w + 8 m) rates are read once and kept in registers.
   float2 rc[8], rb[8];
+  float rates[8];
+  fetch_angles<8>(s, ang, b, c, rates);
   {
     const int tid = tix(), l = tid & 63, w = tid >> 6;
 #pragma unroll
@@ -940,20 +949,50 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     }
   }
 
+  // A head's own inputs, fetched into registers while the previous head's
+  // last phases run: its per-token scalars, start phase, start state and
+  // end cotangent (in the transposed-staging layout; the same registers
+  // later fill the untransposed copies, so the pair is read once) and
+  // biases.  Its values and d_y load at the head's start, for its fourth
+  // phase.
+  struct HeadIn {
+    TokenIn tin;
+    float th;
+    f4 hs[4], hg[4];
+    float2 bq, bk;
+  };
+  auto fetch_head = [&](HeadIn& F, int h) {
+    F.tin = fetch_token(s, adt, dt, trap, b, h, c);
+    const int tid = tix(), n2 = 2 * (tid & 63);
+    F.th = tid < s.A ? theta0[phase_offset(s, b, h, c) + tid] : 0.f;
+    fetch_state_t<512>(starts + state_offset(s, b, h, c), F.hs);
+    fetch_state_t<512>(dh1 + state_offset(s, b, h, c), F.hg);
+    F.bq = F.bk = float2{0.f, 0.f};
+    if (n2 < s.N) {
+      F.bq = *reinterpret_cast<const float2*>(qb + (long)h * s.N + n2);
+      F.bk = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
+    }
+  };
+  HeadIn F;
+  if (h_begin < h_end) fetch_head(F, h_begin);
+
   for (int h = h_begin; h < h_end; ++h) {
     const int tid = tix(), l = tid & 63, r = l & 15, q = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
     const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
-    if (w == 0) token_scalars(s, adt, dt, trap, b, h, c, S);
-    if (tid < s.A) th0[tid] = theta0[phase_offset(s, b, h, c) + tid];
+    f4 vx[2], vd[2];
+    fetch_values<512>(s, x, b, c, h, vx);
+    fetch_values<512>(s, dy, b, c, h, vd);
+    if (w == 0) token_scalars(F.tin, S);
+    if (tid < s.A) th0[tid] = F.th;
     // Column sums: the row blocks above a column block contribute nothing.
     if (tid < 256) {
       s_colF[tid] = 0.f;
       s_colE[tid] = 0.f;
     }
     __syncthreads();
-    phase_table<8>(s, ang, dt, b, h, c, th0, tab, false);
+    phase_table<8>(s, rates, F.tin.d, th0, tab, false);
     __syncthreads();
     float* qt = R1;
     float* kt = R1 + C * LQ;
@@ -961,15 +1000,11 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     // K dH1 with both operands contiguous along n.
     float* h0 = R2;
     float* g1 = R2 + NT * LV;
-    load_state_t<512>(starts + state_offset(s, b, h, c), h0);
-    load_state_t<512>(dh1 + state_offset(s, b, h, c), g1);
+    store_state_t<512>(F.hs, h0);
+    store_state_t<512>(F.hg, g1);
+    const float2 bq = F.bq, bkv = F.bk;
     {
       const bool col = n2 < s.N;
-      float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
-      if (col) {
-        bq = *reinterpret_cast<const float2*>(qb + (long)h * s.N + n2);
-        bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
-      }
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int t = w + 8 * m, tt = c * C + t;
@@ -1000,12 +1035,12 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
     mma<2, LQ, 1, 1, LQ, BF>(kg, kt, 16 * wr, g1, 32 * wc, 0, NT);
     {
+      // <H0, dH1> from the registers (both tiles in the same layout).
       float part = 0.f;
-#pragma unroll 8
-      for (int e = tid; e < NT * PT; e += 512) {
-        const int n = e % NT, p = e / NT;
-        part += h0[p * LQ + n] * g1[p * LQ + n];
-      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) part += F.hs[i][k] * F.hg[i][k];
       part = wave_sum(part);
       if (l == 0) hsum[w] = part;
     }
@@ -1014,8 +1049,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     float* dyt = R2 + C * LV;
     float* gs = R2 + 2 * C * LV;
     float* gm = R2 + 3 * C * LV;
-    load_values<512>(s, x, b, c, h, nullptr, vt);
-    load_values<512>(s, dy, b, c, h, nullptr, dyt);
+    store_values<512>(vx, nullptr, vt);
+    store_values<512>(vd, nullptr, dyt);
     __syncthreads();
 
     f4 dsc[2];
@@ -1121,9 +1156,12 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
       dyt[t * LV + p] *= S.ep[t];
       if (!BF) vt[t * LV + p] *= S.u[t];
     }
-    load_state<512>(starts + state_offset(s, b, h, c), R1);
-    load_state<512>(dh1 + state_offset(s, b, h, c), R1 + NT * LV);
+    store_state_rows<512>(F.hs, R1);
+    store_state_rows<512>(F.hg, R1 + NT * LV);
     __syncthreads();
+    // Every register of F is staged: the next head's inputs load during this
+    // head's remaining phases (which wait for no global load).
+    if (h + 1 < h_end) fetch_head(F, h + 1);
     // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0[n * LV + p].
     mma<4, LV, 1, 1, LV, BF>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
     if constexpr (BF) {
@@ -1153,11 +1191,6 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     // Through the rotations: one pair per lane, tokens w, w + 8, ...
     {
       const bool col = n2 < s.N;
-      float2 bq = float2{0.f, 0.f}, bkv = float2{0.f, 0.f};
-      if (col) {
-        bq = *reinterpret_cast<const float2*>(qb + (long)h * s.N + n2);
-        bkv = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
-      }
       float2 sq = float2{0.f, 0.f}, sk = float2{0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
@@ -1194,12 +1227,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     {
       const int tt = c * C + l;
       const bool valid = tt < s.T;
-      float ddt = 0.f, av[8];
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const int j = w + 8 * m;
-        av[m] = valid && j < s.A ? ang[tok_index(s, b, tt) * s.A + j] : 0.f;
-      }
+      float ddt = 0.f;
+      const float(&av)[8] = rates;
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int j = w + 8 * m;
