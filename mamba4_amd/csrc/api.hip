@@ -163,14 +163,22 @@ int configure() {
              {(const void*)m4::states_kernel<false, m4::bf16_t, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, float, true>, kStatesLdsBytes},
-             {(const void*)m3::walk_kernel<false, float>, m3::kWalkLds},
-             {(const void*)m3::walk_kernel<true, float>, m3::kWalkLds},
-             {(const void*)m3::out_kernel<float>, m3::kOutLds},
-             {(const void*)m3::grad_kernel<float>, m3::kGradLds},
-             {(const void*)m3::walk_kernel<false, m3::bf16_t>, m3::kWalkLds},
-             {(const void*)m3::walk_kernel<true, m3::bf16_t>, m3::kWalkLds},
-             {(const void*)m3::out_kernel<m3::bf16_t>, m3::kOutLds},
-             {(const void*)m3::grad_kernel<m3::bf16_t>, m3::kGradLds},
+             {(const void*)m3::walk_kernel<false, float, true>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true, float, true>, m3::kWalkLds},
+             {(const void*)m3::out_kernel<float, true>, m3::kOutLds},
+             {(const void*)m3::grad_kernel<float, true>, m3::kGradLds},
+             {(const void*)m3::walk_kernel<false, m3::bf16_t, true>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true, m3::bf16_t, true>, m3::kWalkLds},
+             {(const void*)m3::out_kernel<m3::bf16_t, true>, m3::kOutLds},
+             {(const void*)m3::grad_kernel<m3::bf16_t, true>, m3::kGradLds},
+             {(const void*)m3::walk_kernel<false, float, false>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true, float, false>, m3::kWalkLds},
+             {(const void*)m3::out_kernel<float, false>, m3::kOutLds},
+             {(const void*)m3::grad_kernel<float, false>, m3::kGradLds},
+             {(const void*)m3::walk_kernel<false, m3::bf16_t, false>, m3::kWalkLds},
+             {(const void*)m3::walk_kernel<true, m3::bf16_t, false>, m3::kWalkLds},
+             {(const void*)m3::out_kernel<m3::bf16_t, false>, m3::kOutLds},
+             {(const void*)m3::grad_kernel<m3::bf16_t, false>, m3::kGradLds},
              {(const void*)m3::finish_kernel, m3::kFinishLdsMax}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1131,16 +1139,19 @@ int m3_forward_impl(const char* entry, const In* c, const In* b, const In* x, co
   if (int rc = configure()) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const m3::Shape s{B, T, H, N, P, A, (T + m3::C - 1) / m3::C};
+  // Value rows load as 4-element vectors when P allows (a kernel per case).
+  const bool v4 = P % 4 == 0;
+  const auto walk = v4 ? m3::walk_kernel<false, In, true> : m3::walk_kernel<false, In, false>;
+  const auto out = v4 ? m3::out_kernel<In, true> : m3::out_kernel<In, false>;
   int rc = launch("m3_walk", st, [&] {
-    hipLaunchKernelGGL((m3::walk_kernel<false, In>), dim3(B * H), dim3(512), m3::kWalkLds, st, s,
-                       b, k_bias, x, adt, dt, trap_logits, angles, phases, starts, nullptr,
-                       final_state);
+    hipLaunchKernelGGL(walk, dim3(B * H), dim3(512), m3::kWalkLds, st, s, b, k_bias, x, adt, dt,
+                       trap_logits, angles, phases, starts, nullptr, final_state);
   });
   if (rc) return rc;
   return launch("m3_out", st, [&] {
-    hipLaunchKernelGGL(m3::out_kernel<In>, dim3(persistent_grid(B * s.NC * H, 1)), dim3(512),
-                       m3::kOutLds, st, s, c,
-                       b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, y);
+    hipLaunchKernelGGL(out, dim3(persistent_grid(B * s.NC * H, 1)), dim3(512), m3::kOutLds, st,
+                       s, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts,
+                       y);
   });
 }
 
@@ -1176,16 +1187,19 @@ int m3_backward_impl(const char* entry, const In* c, const In* b, const In* x, c
   const m3::GradOut o{d_x,         d_adt,        ws.dgam,       ws.dscale,
                       ws.ddt_loc,  ws.D,         ws.qb_part,    ws.kb_part,
                       ws.dc_part,  ws.db_part,   ws.dang_part};
+  const bool v4 = P % 4 == 0;
+  const auto walk = v4 ? m3::walk_kernel<true, In, true> : m3::walk_kernel<true, In, false>;
+  const auto grad = v4 ? m3::grad_kernel<In, true> : m3::grad_kernel<In, false>;
   int rc = launch("m3_walk_bwd", st, [&] {
-    hipLaunchKernelGGL((m3::walk_kernel<true, In>), dim3(B * H), dim3(512), m3::kWalkLds, st, s,
-                       c, q_bias, d_y, adt, dt, trap_logits, angles, const_cast<float*>(phases),
-                       ws.dh1, d_final, nullptr);
+    hipLaunchKernelGGL(walk, dim3(B * H), dim3(512), m3::kWalkLds, st, s, c, q_bias, d_y, adt, dt,
+                       trap_logits, angles, const_cast<float*>(phases), ws.dh1, d_final,
+                       nullptr);
   });
   if (rc) return rc;
   rc = launch("m3_grad", st, [&] {
-    hipLaunchKernelGGL(m3::grad_kernel<In>, dim3(B * s.NC * groups), dim3(512), m3::kGradLds,
-                       st, s, groups, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias,
-                       phases, starts, ws.dh1, d_y, o);
+    hipLaunchKernelGGL(grad, dim3(B * s.NC * groups), dim3(512), m3::kGradLds, st, s, groups, c,
+                       b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts, ws.dh1,
+                       d_y, o);
   });
   if (rc) return rc;
   if (A > 0) {

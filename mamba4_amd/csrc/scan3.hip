@@ -57,20 +57,71 @@ struct is_bf16<bf16_t> {
 
 __device__ __forceinline__ float lo_bf(unsigned u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float hi_bf(unsigned u) { return __uint_as_float(u & 0xffff0000u); }
-__device__ __forceinline__ float2 ld2(const float* p) {
-  return *reinterpret_cast<const float2*>(p);
+
+// Inputs are fetched as the raw register image of their dtype (Raw<In>::Pair
+// for two consecutive elements, ::Quad for four) and decoded to float32 by
+// dec() where they are used, so a load is waited for at its use, not at its
+// issue (a bfloat16 load decoded on arrival would stall every load after it).
+typedef unsigned u2 __attribute__((ext_vector_type(2)));
+template <typename In>
+struct Raw {
+  typedef float2 Pair;
+  typedef f4 Quad;
+};
+template <>
+struct Raw<bf16_t> {
+  typedef unsigned Pair;
+  typedef u2 Quad;
+};
+// Inputs load through buffer resources, each spanning one chunk's valid
+// tokens (or one head's row): the hardware's range check returns zeros for
+// an offset at or past the resource's size, so padding tokens and
+// coordinates need no branch around their loads.  Every load of a prefetch
+// then issues unconditionally, and the waits at the uses count exactly the
+// loads issued after the awaited one instead of draining them all.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr unsigned kNoLoad = 0x80000000u;  // an offset past every resource here
+// bytes < 2^31 (every array has fewer than 2^31 elements).
+__device__ __forceinline__ Rsrc rsrc(const void* base, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
 }
-__device__ __forceinline__ float2 ld2(const bf16_t* p) {
-  const unsigned u = *reinterpret_cast<const unsigned*>(p);
-  return float2{lo_bf(u), hi_bf(u)};
+__device__ __forceinline__ float ldb(Rsrc r, unsigned off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
-__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
-__device__ __forceinline__ f4 ld4(const bf16_t* p) {
-  const uint2 u = *reinterpret_cast<const uint2*>(p);
-  return f4{lo_bf(u.x), hi_bf(u.x), lo_bf(u.y), hi_bf(u.y)};
+__device__ __forceinline__ float2 raw2(Rsrc r, unsigned off, const float*) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
-__device__ __forceinline__ float ld1(const float* p) { return *p; }
-__device__ __forceinline__ float ld1(const bf16_t* p) { return lo_bf(*p); }
+__device__ __forceinline__ unsigned raw2(Rsrc r, unsigned off, const bf16_t*) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ f4 raw4(Rsrc r, unsigned off, const float*) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ u2 raw4(Rsrc r, unsigned off, const bf16_t*) {
+  return __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+// The first min(n, 4) of four consecutive elements at any alignment (zeros
+// after), one element per load: rows whose width is not a multiple of 4.
+__device__ __forceinline__ f4 raw4_n(Rsrc r, unsigned off, int n, const float*) {
+  f4 v;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = ldb(r, k < n ? off + 4 * k : kNoLoad);
+  return v;
+}
+__device__ __forceinline__ u2 raw4_n(Rsrc r, unsigned off, int n, const bf16_t*) {
+  unsigned e[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    e[k] = __builtin_amdgcn_raw_buffer_load_b16(r, k < n ? off + 2 * k : kNoLoad, 0, 0);
+  return u2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+}
+__device__ __forceinline__ float2 dec(float2 r) { return r; }
+__device__ __forceinline__ float2 dec(unsigned r) { return float2{lo_bf(r), hi_bf(r)}; }
+__device__ __forceinline__ f4 dec(f4 r) { return r; }
+__device__ __forceinline__ f4 dec(u2 r) {
+  return f4{lo_bf(r.x), hi_bf(r.x), lo_bf(r.y), hi_bf(r.y)};
+}
 __device__ __forceinline__ void st1(float* p, float v) { *p = v; }
 __device__ __forceinline__ void st1(bf16_t* p, float v) {
   *p = __builtin_bit_cast(bf16_t, static_cast<__bf16>(v));
@@ -311,6 +362,12 @@ __device__ __forceinline__ void zero(f4 (&acc)[J]) {
 __device__ __forceinline__ long tok_index(const Shape& s, int b, int t) {
   return (long)b * s.T + t;
 }
+__device__ __forceinline__ long state_offset(const Shape& s, int b, int h, int c) {
+  return (((long)b * s.H + h) * s.NC + c) * (long)(NT * PT);
+}
+__device__ __forceinline__ long phase_offset(const Shape& s, int b, int h, int c) {
+  return (((long)b * s.H + h) * s.NC + c) * (long)AM;
+}
 
 // Per-token scalars of chunk c for head h, one token per lane (lane < 64):
 // p (chunk-local running log decay), e^p, gamma, scale, u = scale e^{p_L - p}
@@ -325,13 +382,35 @@ struct TokenIn {
   float a, d, tr, dn, trn;
 };
 
+// The buffer resource of chunk c's tokens (those below T, and up to `extra`
+// tokens past the chunk) in a [B, T, width] array.
+template <typename E>
+__device__ __forceinline__ Rsrc chunk_rsrc(const Shape& s, const E* base, int b, int c,
+                                           long width, int extra = 0) {
+  return rsrc(base + tok_index(s, b, c * C) * width,
+              (long)min(C + extra, s.T - c * C) * width * (long)sizeof(E));
+}
+
+// Lane l's token c C + l and the next token's dt and trapezoid weight, for
+// the block's first wave (token_scalars' wave; the other waves' offsets are
+// out of range, zeros without a memory access: each of these loads gathers
+// one float per token).  The resources span one token past the chunk, and
+// lane l < 64 < C + 1 is in range exactly when its token is below T (its
+// next token likewise).
 __device__ __forceinline__ TokenIn fetch_token(const Shape& s, const float* adt, const float* dt,
                                                const float* trap, int b, int h, int c) {
-  const int t = c * C + lane_id();
-  const bool valid = t < s.T, next = t + 1 < s.T;
-  const long i = tok_index(s, b, t) * s.H + h;
-  return TokenIn{valid ? adt[i] : 0.f, valid ? dt[i] : 0.f, valid ? trap[i] : 0.f,
-                 next ? dt[i + s.H] : 0.f, next ? trap[i + s.H] : 0.f};
+  const int tid = tix();
+  const unsigned o = tid < 64 ? (tid * s.H + h) * 4 : kNoLoad;
+  const unsigned on = tid < 64 ? o + s.H * 4 : kNoLoad;
+  const Rsrc ra = chunk_rsrc(s, adt, b, c, s.H, 1), rd = chunk_rsrc(s, dt, b, c, s.H, 1),
+             rt = chunk_rsrc(s, trap, b, c, s.H, 1);
+  return TokenIn{ldb(ra, o), ldb(rd, o), ldb(rt, o), ldb(rd, on), ldb(rt, on)};
+}
+
+// The A start phases of an item (zeros past A).
+__device__ __forceinline__ float fetch_phase(const Shape& s, const float* theta0, int b, int h,
+                                             int c) {
+  return ldb(rsrc(theta0 + phase_offset(s, b, h, c), 4L * s.A), tix() * 4);
 }
 
 __device__ void token_scalars(const TokenIn& in, const Scalars& o) {
@@ -348,35 +427,35 @@ __device__ void token_scalars(const TokenIn& in, const Scalars& o) {
   o.dt[l] = d;
 }
 
-__device__ void token_scalars(const Shape& s, const float* adt, const float* dt,
-                              const float* trap, int b, int h, int c, const Scalars& o) {
-  token_scalars(fetch_token(s, adt, dt, trap, b, h, c), o);
-}
-
 // Phase table of chunk c: tab[t * LA + j] = th0[j] + sum_{s <= t} angles_s,j dt_s
-// (j < A), one token per lane, angles split over the four waves.  With
+// (j < A), one token per lane, angles j = w + NW m split over the NW waves
+// of the block, dt from the chunk's scalars in LDS (zero past T).  With
 // `advance`, th0[j] moves to the chunk's end phase reduced modulo 2 pi (th0
 // lives in LDS and each j belongs to one wave, whose lanes read it before
 // lane 63 writes it).
-// This lane's token's angle rates j = w + NW m (zeros past T and A), for a
-// block of NW waves.
+//
+// This lane's token's angle rates j = w + NW m (zeros past T and A), kept in
+// registers by a kernel that reuses them (one float per token and angle:
+// each load gathers 64 tokens).
 template <int NW = 4>
 __device__ __forceinline__ void fetch_angles(const Shape& s, const float* ang, int b, int c,
                                              float (&xs)[64 / NW]) {
-  const int w = tix() >> 6, t = c * C + lane_id();
-  const bool valid = t < s.T;
+  const int w = tix() >> 6;
+  const Rsrc r = chunk_rsrc(s, ang, b, c, s.A);
+  const unsigned o = lane_id() * s.A * 4;
 #pragma unroll
   for (int m = 0; m < 64 / NW; ++m) {
     const int j = w + NW * m;
-    xs[m] = valid && j < s.A ? ang[tok_index(s, b, t) * s.A + j] : 0.f;
+    xs[m] = ldb(r, j < s.A ? o + 4 * j : kNoLoad);
   }
 }
 
-// The phase table from fetched angle rates and this lane's dt.
+// The phase table from register-held angle rates.
 template <int NW = 4>
-__device__ void phase_table(const Shape& s, const float (&rates)[64 / NW], float d, float* th0,
-                            float* tab, bool advance) {
+__device__ void phase_table(const Shape& s, const float (&rates)[64 / NW], const float* dts,
+                            float* th0, float* tab, bool advance) {
   const int l = lane_id(), w = tix() >> 6;
+  const float d = dts[l];
   float xs[64 / NW];
 #pragma unroll
   for (int m = 0; m < 64 / NW; ++m) xs[m] = rates[m] * d;
@@ -394,14 +473,45 @@ __device__ void phase_table(const Shape& s, const float (&rates)[64 / NW], float
   }
 }
 
+// The chunk's angle rates as one block: [tokens][A] is contiguous in memory,
+// so a 512-thread block reads it in eight coalesced loads per thread (A <=
+// 64; zeros past the chunk's tokens), stage_angles writes them into the phase
+// table's [C][LA] layout and phase_table_staged turns them into phases in
+// place.
+__device__ __forceinline__ void fetch_angle_block(const Shape& s, const float* ang, int b, int c,
+                                                  float (&a)[8]) {
+  const Rsrc r = chunk_rsrc(s, ang, b, c, s.A);
+  const int tid = tix();
+#pragma unroll
+  for (int k = 0; k < 8; ++k) a[k] = ldb(r, (tid + 512 * k) * 4);
+}
+
+__device__ __forceinline__ void stage_angles(const Shape& s, const float (&a)[8], float* tab) {
+  const int tid = tix();
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int e = tid + 512 * k;
+    if (e < C * s.A) tab[(e / s.A) * LA + e % s.A] = a[k];
+  }
+}
+
 template <int NW = 4>
-__device__ void phase_table(const Shape& s, const float* ang, const float* dt, int b, int h,
-                            int c, float* th0, float* tab, bool advance) {
-  const int t = c * C + lane_id();
-  const float d = t < s.T ? dt[tok_index(s, b, t) * s.H + h] : 0.f;
-  float rates[64 / NW];
-  fetch_angles<NW>(s, ang, b, c, rates);
-  phase_table<NW>(s, rates, d, th0, tab, advance);
+__device__ void phase_table_staged(const Shape& s, const float* dts, float* th0, float* tab,
+                                   bool advance) {
+  const int l = lane_id(), w = tix() >> 6;
+  const float d = dts[l];
+#pragma unroll
+  for (int m = 0; m < 64 / NW; ++m) {
+    const int j = w + NW * m;
+    if (j >= s.A) break;
+    const float incl = wave_scan(tab[l * LA + j] * d);
+    const float base = th0[j];
+    tab[l * LA + j] = base + incl;
+    if (advance) {
+      __builtin_amdgcn_wave_barrier();
+      if (l == 63) th0[j] = reduce_turns(base + incl);
+    }
+  }
 }
 
 // Rotated rows of chunk c into LDS [C][LQ]: dst[t][n] = rot(src_t + bias, theta_t)[n]
@@ -410,29 +520,32 @@ __device__ void phase_table(const Shape& s, const float* ang, const float* dt, i
 // issued before the first rotation.  With two sources both are rotated by
 // the same angles.  bfloat16 sources: the bias-added rows are rounded to
 // bfloat16 before the rotation (_rotated, lm/kernels/flashmamba.py:582-585).
+// This lane's pair (2 l, 2 l + 1) of a head's N biases (zeros past N).
+__device__ __forceinline__ float2 fetch_bias_pair(const Shape& s, const float* bias) {
+  return raw2(rsrc(bias, 4L * s.N), 8 * lane_id(), bias);
+}
+
 template <int NSRC, int NW = 4, typename In = float>
 __device__ __forceinline__ void fetch_rows(const Shape& s, const In* const (&src)[2],
                                            const float* const (&bias)[2], int b, int c,
-                                           float2 (&u)[NSRC][64 / NW], float2 (&bs)[NSRC]) {
-  const int j = lane_id(), n = 2 * j, w = tix() >> 6;
-  const bool col = n < s.N;
+                                           typename Raw<In>::Pair (&u)[NSRC][64 / NW],
+                                           float2 (&bs)[NSRC]) {
+  const int n = 2 * lane_id(), w = tix() >> 6;
 #pragma unroll
-  for (int m = 0; m < 64 / NW; ++m) {
-    const int tt = c * C + w + NW * m;
-    const bool valid = col && tt < s.T;
+  for (int k = 0; k < NSRC; ++k) {
+    const Rsrc r = chunk_rsrc(s, src[k], b, c, s.N);
 #pragma unroll
-    for (int k = 0; k < NSRC; ++k)
-      u[k][m] = valid ? ld2(src[k] + tok_index(s, b, tt) * s.N + n) : float2{0.f, 0.f};
+    for (int m = 0; m < 64 / NW; ++m)
+      u[k][m] = raw2(r, n < s.N ? ((w + NW * m) * s.N + n) * sizeof(In) : kNoLoad, src[k]);
+    bs[k] = fetch_bias_pair(s, bias[k]);
   }
-#pragma unroll
-  for (int k = 0; k < NSRC; ++k)
-    bs[k] = col ? *reinterpret_cast<const float2*>(bias[k] + n) : float2{0.f, 0.f};
 }
 
-template <int NSRC, int NW = 4, bool BF = false>
-__device__ __forceinline__ void rotate_fetched(const Shape& s, const float2 (&u)[NSRC][64 / NW],
+template <int NSRC, int NW = 4, typename Pair = float2>
+__device__ __forceinline__ void rotate_fetched(const Shape& s, const Pair (&u)[NSRC][64 / NW],
                                                const float2 (&bs)[NSRC], float* const (&dst)[2],
                                                const float* tab, int c) {
+  constexpr bool BF = !__is_same(Pair, float2);
   const int j = lane_id(), n = 2 * j, w = tix() >> 6;
   const bool col = n < s.N;
 #pragma unroll
@@ -443,105 +556,67 @@ __device__ __forceinline__ void rotate_fetched(const Shape& s, const float2 (&u)
     if (valid && j < s.A) sin_cos(tab[t * LA + j], &sn, &cs);
 #pragma unroll
     for (int k = 0; k < NSRC; ++k) {
-      const float2 v = round_bf2<BF>(
-          valid ? float2{u[k][m].x + bs[k].x, u[k][m].y + bs[k].y} : float2{0.f, 0.f});
+      const float2 x = dec(u[k][m]);
+      const float2 v =
+          round_bf2<BF>(valid ? float2{x.x + bs[k].x, x.y + bs[k].y} : float2{0.f, 0.f});
       *reinterpret_cast<float2*>(dst[k] + t * LQ + n) =
           float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
     }
   }
 }
 
-template <int NSRC, int NW = 4, typename In = float>
-__device__ void rotate_rows(const Shape& s, const In* const (&src)[2],
-                            const float* const (&bias)[2], float* const (&dst)[2], const float* tab,
-                            int b, int c) {
-  float2 u[NSRC][64 / NW], bs[NSRC];
-  fetch_rows<NSRC, NW>(s, src, bias, b, c, u, bs);
-  rotate_fetched<NSRC, NW, is_bf16<In>::value>(s, u, bs, dst, tab, c);
-}
-
 // Value rows of head h for chunk c into LDS [C][LV], each row t scaled by
 // row_scale[t] (nullptr: 1); zeros past T and P.  Four 16-byte rows pieces
 // per thread, all read before any is stored (fetch_values, store_values).
-template <int NTH = 256, typename In = float>
+// V4: P is a multiple of 4 (one vector load per piece; otherwise one load
+// per element), chosen per launch so no kernel holds both paths.
+template <int NTH, bool V4, typename In>
 __device__ __forceinline__ void fetch_values(const Shape& s, const In* src, int b, int c, int h,
-                                             f4 (&v)[1024 / NTH]) {
+                                             typename Raw<In>::Quad (&v)[1024 / NTH]) {
+  const Rsrc r = chunk_rsrc(s, src, b, c, (long)s.H * s.P);
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
-    const int tt = c * C + t;
-    v[i] = f4{0.f, 0.f, 0.f, 0.f};
-    if (tt < s.T) {
-      const In* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
-      if (s.P % 4 == 0) {
-        if (p < s.P) v[i] = ld4(row + p);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (p + k < s.P) v[i][k] = ld1(row + p + k);
-      }
-    }
+    const unsigned off = ((t * s.H + h) * s.P + p) * sizeof(In);
+    v[i] = V4 ? raw4(r, p < s.P ? off : kNoLoad, src) : raw4_n(r, off, s.P - p, src);
   }
 }
 
-template <int NTH = 256>
-__device__ __forceinline__ void store_values(const f4 (&v)[1024 / NTH], const float* row_scale,
+template <int NTH, typename Quad>
+__device__ __forceinline__ void store_values(const Quad (&v)[1024 / NTH], const float* row_scale,
                                              float* dst) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
-    *reinterpret_cast<f4*>(dst + t * LV + p) = row_scale ? v[i] * row_scale[t] : v[i];
+    *reinterpret_cast<f4*>(dst + t * LV + p) = row_scale ? dec(v[i]) * row_scale[t] : dec(v[i]);
   }
-}
-
-template <int NTH = 256, typename In = float>
-__device__ void load_values(const Shape& s, const In* src, int b, int c, int h,
-                            const float* row_scale, float* dst) {
-  f4 v[1024 / NTH];
-  fetch_values<NTH>(s, src, b, c, h, v);
-  store_values<NTH>(v, row_scale, dst);
 }
 
 // Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
 // takes token t = e % C (consecutive lanes, conflict-free LDS stores) and
 // columns 4 (e / C) .. +3; zeros past T and P.  fetch_values_t reads this
 // thread's pieces into registers, store_values_t writes them.
-template <int NTH = 256, typename In = float>
+template <int NTH, bool V4, typename In>
 __device__ __forceinline__ void fetch_values_t(const Shape& s, const In* src, int b, int c,
-                                               int h, f4 (&v)[1024 / NTH]) {
-#pragma unroll
-  for (int i = 0; i < 1024 / NTH; ++i) {
-    const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C), tt = c * C + t;
-    v[i] = f4{0.f, 0.f, 0.f, 0.f};
-    if (tt < s.T) {
-      const In* row = src + (tok_index(s, b, tt) * s.H + h) * s.P;
-      if (s.P % 4 == 0) {
-        if (p < s.P) v[i] = ld4(row + p);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (p + k < s.P) v[i][k] = ld1(row + p + k);
-      }
-    }
-  }
-}
-
-template <int NTH = 256>
-__device__ __forceinline__ void store_values_t(const f4 (&v)[1024 / NTH], float* dst) {
+                                               int h, typename Raw<In>::Quad (&v)[1024 / NTH]) {
+  const Rsrc r = chunk_rsrc(s, src, b, c, (long)s.H * s.P);
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) dst[(p + k) * LV + t] = v[i][k];
+    const unsigned off = ((t * s.H + h) * s.P + p) * sizeof(In);
+    v[i] = V4 ? raw4(r, p < s.P ? off : kNoLoad, src) : raw4_n(r, off, s.P - p, src);
   }
 }
 
-template <int NTH = 256, typename In = float>
-__device__ void load_values_t(const Shape& s, const In* src, int b, int c, int h,
-                              float* dst) {
-  f4 v[1024 / NTH];
-  fetch_values_t<NTH>(s, src, b, c, h, v);
-  store_values_t<NTH>(v, dst);
+template <int NTH, typename Quad>
+__device__ __forceinline__ void store_values_t(const Quad (&v)[1024 / NTH], float* dst) {
+#pragma unroll
+  for (int i = 0; i < 1024 / NTH; ++i) {
+    const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C);
+    const f4 x = dec(v[i]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[(p + k) * LV + t] = x[k];
+  }
 }
 
 // A stored [NT][PT] state tile into LDS transposed, [PT][LQ]: thread e takes
@@ -577,19 +652,6 @@ __device__ __forceinline__ void store_state_rows(const f4 (&v)[2048 / NTH], floa
   }
 }
 
-template <int NTH = 256>
-__device__ void load_state_t(const float* src, float* dst) {
-  f4 v[2048 / NTH];
-  fetch_state_t<NTH>(src, v);
-  store_state_t<NTH>(v, dst);
-}
-
-__device__ __forceinline__ long state_offset(const Shape& s, int b, int h, int c) {
-  return (((long)b * s.H + h) * s.NC + c) * (long)(NT * PT);
-}
-__device__ __forceinline__ long phase_offset(const Shape& s, int b, int h, int c) {
-  return (((long)b * s.H + h) * s.NC + c) * (long)AM;
-}
 
 // ---------------------------------------------------------------------------
 // State walks.  Forward (BWD = false): rows = keys b with k_bias, vals = x
@@ -600,7 +662,7 @@ __device__ __forceinline__ long phase_offset(const Shape& s, int b, int h, int c
 // cotangent of the state at the chunk's end) to `saved`, then
 // S <- e^{p_L} S + Q^T (e^p dy).
 // LDS: rows [C][LQ], vals [C][LV], phase table [C][LA], th0 [AM], scalars.
-template <bool BWD, typename In>
+template <bool BWD, typename In, bool V4>
 __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, const float* bias,
                                                    const In* vals, const float* adt,
                                                    const float* dt, const float* trap,
@@ -635,39 +697,23 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, cons
   }
   if (!BWD && tid < AM) th0[tid] = 0.f;
   const bool col = 2 * l < s.N;
-  const float2 bs = col ? *reinterpret_cast<const float2*>(bias + (long)h * s.N + 2 * l)
-                        : float2{0.f, 0.f};
+  const float2 bs = fetch_bias_pair(s, bias + (long)h * s.N);
 
   // Every global input of a chunk is fetched into registers one chunk ahead,
   // while the previous chunk's product runs.
   TokenIn tin;
   float rates[8], th_in = 0.f;
-  float2 u[8];
-  f4 v[2];
+  typename Raw<In>::Pair u[8];
+  typename Raw<In>::Quad v[2];
   auto fetch = [&](int c) {
     tin = fetch_token(s, adt, dt, trap, b, h, c);
-    fetch_angles<8>(s, ang, b, c, rates);
-    if (BWD && tid < s.A) th_in = theta0[phase_offset(s, b, h, c) + tid];
+    fetch_angle_block(s, ang, b, c, rates);
+    if (BWD) th_in = fetch_phase(s, theta0, b, h, c);
+    const Rsrc rr = chunk_rsrc(s, rows, b, c, s.N);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int tt = c * C + w + 8 * m;
-      u[m] = col && tt < s.T ? ld2(rows + tok_index(s, b, tt) * s.N + 2 * l) : float2{0.f, 0.f};
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4)), tt = c * C + t;
-      v[i] = f4{0.f, 0.f, 0.f, 0.f};
-      if (tt < s.T) {
-        const In* row = vals + (tok_index(s, b, tt) * s.H + h) * s.P;
-        if (s.P % 4 == 0) {
-          if (p < s.P) v[i] = ld4(row + p);
-        } else {
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            if (p + k < s.P) v[i][k] = ld1(row + p + k);
-        }
-      }
-    }
+    for (int m = 0; m < 8; ++m)
+      u[m] = raw2(rr, col ? ((w + 8 * m) * s.N + 2 * l) * sizeof(In) : kNoLoad, rows);
+    fetch_values<512, V4>(s, vals, b, c, h, v);
   };
   fetch(BWD ? s.NC - 1 : 0);
 
@@ -675,13 +721,17 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, cons
     const int c = BWD ? s.NC - 1 - step : step;
     __syncthreads();  // the previous chunk's reads of the LDS tiles are done
     if (w == 0) token_scalars(tin, S);
+    stage_angles(s, rates, tab);
     if (BWD) {
       if (tid < s.A) th0[tid] = th_in;
     } else {
-      if (tid < s.A) theta0[phase_offset(s, b, h, c) + tid] = th0[tid];
+      // Lanes at or past A store out of the resource's range (dropped).
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(th0[tid & (AM - 1)]),
+                                            rsrc(theta0 + phase_offset(s, b, h, c), 4L * s.A),
+                                            tid * 4, 0, 0);
     }
     __syncthreads();
-    phase_table<8>(s, rates, tin.d, th0, tab, !BWD);
+    phase_table_staged<8>(s, S.dt, th0, tab, !BWD);
     __syncthreads();
     // Rotated rows (one pair per lane) and scaled values into LDS.
 #pragma unroll
@@ -691,24 +741,22 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, cons
       float sn = 0.f, cs = 1.f;
       if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
       // The bias-added row in the model dtype, then rotated in float32 (:582-585).
-      const float2 x2 = round_bf2<BF>(valid ? float2{u[m].x + bs.x, u[m].y + bs.y}
+      const float2 um = dec(u[m]);
+      const float2 x2 = round_bf2<BF>(valid ? float2{um.x + bs.x, um.y + bs.y}
                                             : float2{0.f, 0.f});
       *reinterpret_cast<float2*>(rt + t * LQ + 2 * l) =
           float2{x2.x * cs - x2.y * sn, x2.x * sn + x2.y * cs};
     }
-    const float* row_scale = BWD ? S.ep : S.u;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
-      *reinterpret_cast<f4*>(vt + t * LV + p) = v[i] * row_scale[t];
-    }
-    // Store this chunk's state (a lane's four rows of one column).
+    store_values<512>(v, BWD ? S.ep : S.u, vt);
+    // The next chunk's inputs (this chunk's again after the last: every
+    // iteration issues the same loads), then this chunk's state (a lane's
+    // four rows of one column).
+    fetch(step + 1 < s.NC ? (BWD ? c - 1 : c + 1) : c);
     float* out = saved + state_offset(s, b, h, c);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[(16 * w + 4 * q + i) * PT + 16 * j + r] = acc[0][j][i];
-    if (step + 1 < s.NC) fetch(BWD ? c - 1 : c + 1);
     __syncthreads();
     const float decay = expf(S.p[63]);
 #pragma unroll
@@ -749,7 +797,7 @@ __device__ __forceinline__ int xcd_item(int it, int total) {
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
 // LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 transposed
 // [PT][LQ] (first the phase table), V transposed [PT][LV], scalars.
-template <typename In>
+template <typename In, bool V4>
 __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const In* bk,
                                                   const In* x, const float* adt,
                                                   const float* dt, const float* trap,
@@ -774,8 +822,10 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
   struct Fetched {
     TokenIn tin;
     float th, rates[8];
-    float2 u[2][8], bs[2];
-    f4 hv[4], vv[2];
+    typename Raw<In>::Pair u[2][8];
+    float2 bs[2];
+    f4 hv[4];
+    typename Raw<In>::Quad vv[2];
   };
   auto item_of = [&](int it, int& b, int& c, int& h) {
     const int id = xcd_item(it, total);
@@ -787,13 +837,12 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
     int b, c, h;
     item_of(it, b, c, h);
     F.tin = fetch_token(s, adt, dt, trap, b, h, c);
-    const int tid = tix();
-    F.th = tid < s.A ? theta0[phase_offset(s, b, h, c) + tid] : 0.f;
-    fetch_angles<8>(s, ang, b, c, F.rates);
+    F.th = fetch_phase(s, theta0, b, h, c);
+    fetch_angle_block(s, ang, b, c, F.rates);
     const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
     fetch_rows<2, 8>(s, src, bsrc, b, c, F.u, F.bs);
     fetch_state_t<512>(starts + state_offset(s, b, h, c), F.hv);
-    fetch_values_t<512>(s, x, b, c, h, F.vv);
+    fetch_values_t<512, V4>(s, x, b, c, h, F.vv);
   };
 
   // Persistent: block i handles items i, i + gridDim.x, ... (b, chunk, h),
@@ -810,12 +859,13 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
 
     if (w == 0) token_scalars(F.tin, S);
     if (tid < s.A) th0[tid] = F.th;
+    stage_angles(s, F.rates, tab);
     __syncthreads();
-    phase_table<8>(s, F.rates, F.tin.d, th0, tab, false);
+    phase_table_staged<8>(s, S.dt, th0, tab, false);
     __syncthreads();
     {
       float* const dst[2] = {qt, kt};
-      rotate_fetched<2, 8, BF>(s, F.u, F.bs, dst, tab, c);
+      rotate_fetched<2, 8>(s, F.u, F.bs, dst, tab, c);
     }
     __syncthreads();  // the phase table (in h0's space) is read
     // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
@@ -881,7 +931,7 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
 // from the end of the chunk: R_t = sum_{t' >= t} dtheta_t'.
 // LDS: R1 = 2 NT LV floats (Q, K; later H0, dH1; later dQ, dK), R2 = 2 NT LV
 // floats (H0, dH1; later V, dY, S o W, G), phase table [C][LA], scalars.
-template <typename In>
+template <typename In, bool V4>
 __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In* cq,
                                                    const In* bk, const In* x,
                                                    const float* adt, const float* dt,
@@ -935,17 +985,17 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
   // The chunk's raw query and key rows and its angle rates are the same for
   // every head: this thread's 8 (token, pair) slots and 8 (token = lane,
   // angle w + 8 m) rates are read once and kept in registers.
-  float2 rc[8], rb[8];
+  typename Raw<In>::Pair rc[8], rb[8];
   float rates[8];
   fetch_angles<8>(s, ang, b, c, rates);
   {
     const int tid = tix(), l = tid & 63, w = tid >> 6;
+    const Rsrc r0 = chunk_rsrc(s, cq, b, c, s.N), r1 = chunk_rsrc(s, bk, b, c, s.N);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      const int tt = c * C + w + 8 * m;
-      const bool ok = 2 * l < s.N && tt < s.T;
-      rc[m] = ok ? ld2(cq + tok_index(s, b, tt) * s.N + 2 * l) : float2{0.f, 0.f};
-      rb[m] = ok ? ld2(bk + tok_index(s, b, tt) * s.N + 2 * l) : float2{0.f, 0.f};
+      const unsigned off = 2 * l < s.N ? ((w + 8 * m) * s.N + 2 * l) * sizeof(In) : kNoLoad;
+      rc[m] = raw2(r0, off, cq);
+      rb[m] = raw2(r1, off, bk);
     }
   }
 
@@ -963,15 +1013,11 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
   };
   auto fetch_head = [&](HeadIn& F, int h) {
     F.tin = fetch_token(s, adt, dt, trap, b, h, c);
-    const int tid = tix(), n2 = 2 * (tid & 63);
-    F.th = tid < s.A ? theta0[phase_offset(s, b, h, c) + tid] : 0.f;
+    F.th = fetch_phase(s, theta0, b, h, c);
     fetch_state_t<512>(starts + state_offset(s, b, h, c), F.hs);
     fetch_state_t<512>(dh1 + state_offset(s, b, h, c), F.hg);
-    F.bq = F.bk = float2{0.f, 0.f};
-    if (n2 < s.N) {
-      F.bq = *reinterpret_cast<const float2*>(qb + (long)h * s.N + n2);
-      F.bk = *reinterpret_cast<const float2*>(kb + (long)h * s.N + n2);
-    }
+    F.bq = fetch_bias_pair(s, qb + (long)h * s.N);
+    F.bk = fetch_bias_pair(s, kb + (long)h * s.N);
   };
   HeadIn F;
   if (h_begin < h_end) fetch_head(F, h_begin);
@@ -981,9 +1027,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
     const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
-    f4 vx[2], vd[2];
-    fetch_values<512>(s, x, b, c, h, vx);
-    fetch_values<512>(s, dy, b, c, h, vd);
+    typename Raw<In>::Quad vx[2], vd[2];
+    fetch_values<512, V4>(s, x, b, c, h, vx);
+    fetch_values<512, V4>(s, dy, b, c, h, vd);
     if (w == 0) token_scalars(F.tin, S);
     if (tid < s.A) th0[tid] = F.th;
     // Column sums: the row blocks above a column block contribute nothing.
@@ -992,7 +1038,7 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
       s_colE[tid] = 0.f;
     }
     __syncthreads();
-    phase_table<8>(s, rates, F.tin.d, th0, tab, false);
+    phase_table<8>(s, rates, S.dt, th0, tab, false);
     __syncthreads();
     float* qt = R1;
     float* kt = R1 + C * LQ;
@@ -1011,9 +1057,10 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
         const bool valid = col && tt < s.T;
         float sn = 0.f, cs = 1.f;
         if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
-        const float2 u = round_bf2<BF>(valid ? float2{rc[m].x + bq.x, rc[m].y + bq.y}
+        const float2 cm = dec(rc[m]), bm = dec(rb[m]);
+        const float2 u = round_bf2<BF>(valid ? float2{cm.x + bq.x, cm.y + bq.y}
                                              : float2{0.f, 0.f});
-        const float2 v = round_bf2<BF>(valid ? float2{rb[m].x + bkv.x, rb[m].y + bkv.y}
+        const float2 v = round_bf2<BF>(valid ? float2{bm.x + bkv.x, bm.y + bkv.y}
                                              : float2{0.f, 0.f});
         *reinterpret_cast<float2*>(qt + t * LQ + n2) =
             float2{u.x * cs - u.y * sn, u.x * sn + u.y * cs};
@@ -1202,8 +1249,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
         if (l < s.A) {
           float sn, cs;
           sin_cos(tab[t * LA + l], &sn, &cs);
-          const float2 uq = round_bf2<BF>(float2{rc[m].x + bq.x, rc[m].y + bq.y});
-          const float2 uk = round_bf2<BF>(float2{rb[m].x + bkv.x, rb[m].y + bkv.y});
+          const float2 cm = dec(rc[m]), bm = dec(rb[m]);
+          const float2 uq = round_bf2<BF>(float2{cm.x + bq.x, cm.y + bq.y});
+          const float2 uk = round_bf2<BF>(float2{bm.x + bkv.x, bm.y + bkv.y});
           const float q0 = uq.x * cs - uq.y * sn, q1 = uq.x * sn + uq.y * cs;
           const float k0 = uk.x * cs - uk.y * sn, k1 = uk.x * sn + uk.y * cs;
           tab[t * LA + l] = gq.y * q0 - gq.x * q1 + gk.y * k0 - gk.x * k1;
@@ -1411,26 +1459,28 @@ __global__ __launch_bounds__(1024) void bias_kernel(Shape s, GradOut o, float* d
   }
 }
 
-#define M3_SCAN_KERNELS(In)                                                                    \
-  template __global__ void walk_kernel<false, In>(Shape, const In*, const float*, const In*,     \
-                                                  const float*, const float*, const float*,      \
-                                                  const float*, float*, float*, const float*,    \
-                                                  float*);                                       \
-  template __global__ void walk_kernel<true, In>(Shape, const In*, const float*, const In*,      \
-                                                 const float*, const float*, const float*,       \
-                                                 const float*, float*, float*, const float*,     \
-                                                 float*);                                        \
-  template __global__ void out_kernel<In>(Shape, const In*, const In*, const In*, const float*,  \
-                                          const float*, const float*, const float*,              \
-                                          const float*, const float*, const float*,              \
-                                          const float*, In*);                                    \
-  template __global__ void grad_kernel<In>(Shape, int, const In*, const In*, const In*,          \
-                                           const float*, const float*, const float*,             \
-                                           const float*, const float*, const float*,             \
-                                           const float*, const float*, const float*, const In*,  \
-                                           GradOut);
-M3_SCAN_KERNELS(float)
-M3_SCAN_KERNELS(bf16_t)
+#define M3_SCAN_KERNELS(In, V4)                                                                \
+  template __global__ void walk_kernel<false, In, V4>(Shape, const In*, const float*, const In*, \
+                                                      const float*, const float*, const float*,  \
+                                                      const float*, float*, float*,              \
+                                                      const float*, float*);                     \
+  template __global__ void walk_kernel<true, In, V4>(Shape, const In*, const float*, const In*,  \
+                                                     const float*, const float*, const float*,   \
+                                                     const float*, float*, float*, const float*, \
+                                                     float*);                                    \
+  template __global__ void out_kernel<In, V4>(Shape, const In*, const In*, const In*,            \
+                                              const float*, const float*, const float*,          \
+                                              const float*, const float*, const float*,          \
+                                              const float*, const float*, In*);                  \
+  template __global__ void grad_kernel<In, V4>(Shape, int, const In*, const In*, const In*,      \
+                                               const float*, const float*, const float*,         \
+                                               const float*, const float*, const float*,         \
+                                               const float*, const float*, const float*,         \
+                                               const In*, GradOut);
+M3_SCAN_KERNELS(float, true)
+M3_SCAN_KERNELS(float, false)
+M3_SCAN_KERNELS(bf16_t, true)
+M3_SCAN_KERNELS(bf16_t, false)
 #undef M3_SCAN_KERNELS
 
 }  // namespace m3

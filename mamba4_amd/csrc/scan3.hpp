@@ -49,16 +49,17 @@ inline size_t finish_lds(int H, int A) {
 }
 
 // In: the model dtype of the rows, values and their cotangents (float, or
-// bf16_t with the reference's bfloat16 matrix operands).
-template <bool BWD, typename In>
+// bf16_t with the reference's bfloat16 matrix operands).  V4: the value width
+// P is a multiple of 4 (vector loads of value rows; otherwise per element).
+template <bool BWD, typename In, bool V4>
 __global__ void walk_kernel(Shape, const In*, const float*, const In*, const float*,
                             const float*, const float*, const float*, float*, float*,
                             const float*, float*);
-template <typename In>
+template <typename In, bool V4>
 __global__ void out_kernel(Shape, const In*, const In*, const In*, const float*, const float*,
                            const float*, const float*, const float*, const float*, const float*,
                            const float*, In*);
-template <typename In>
+template <typename In, bool V4>
 __global__ void grad_kernel(Shape, int, const In*, const In*, const In*, const float*,
                             const float*, const float*, const float*, const float*, const float*,
                             const float*, const float*, const float*, const In*, GradOut);
