@@ -592,17 +592,29 @@ __device__ __forceinline__ void store_values(const Quad (&v)[1024 / NTH], const 
   }
 }
 
-// Value rows of head h for chunk c into LDS transposed, [PT][LV]: thread e
-// takes token t = e % C (consecutive lanes, conflict-free LDS stores) and
-// columns 4 (e / C) .. +3; zeros past T and P.  fetch_values_t reads this
-// thread's pieces into registers, store_values_t writes them.
+// Value rows of head h for chunk c into LDS transposed, [PT][LV]: for
+// i < 1024 / NTH, thread (wave w, lane L) takes the pieces (t, p .. p + 3)
+// of block bi = i NTH / 64 + w, t = 16 (bi / 4) + L / 4, p = 16 (bi % 4) +
+// 4 (L % 4) (zeros past T and P): each load instruction reads 16 tokens'
+// 16-column pieces (not 64 tokens' rows, one cache line per lane), and each
+// transposed LDS store ((p + k) LV + t, LV = 4 mod 64) hits 64 distinct
+// banks.  fetch_values_t reads this thread's pieces into registers,
+// store_values_t writes them.
+template <int NTH>
+__device__ __forceinline__ void value_slot(int i, int& t, int& p) {
+  const int tid = tix(), L = tid & 63, bi = i * (NTH / 64) + (tid >> 6);
+  t = 16 * (bi >> 2) + (L >> 2);
+  p = 16 * (bi & 3) + 4 * (L & 3);
+}
+
 template <int NTH, bool V4, typename In>
 __device__ __forceinline__ void fetch_values_t(const Shape& s, const In* src, int b, int c,
                                                int h, typename Raw<In>::Quad (&v)[1024 / NTH]) {
   const Rsrc r = chunk_rsrc(s, src, b, c, (long)s.H * s.P);
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
-    const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C);
+    int t, p;
+    value_slot<NTH>(i, t, p);
     const unsigned off = ((t * s.H + h) * s.P + p) * sizeof(In);
     v[i] = V4 ? raw4(r, p < s.P ? off : kNoLoad, src) : raw4_n(r, off, s.P - p, src);
   }
@@ -612,42 +624,58 @@ template <int NTH, typename Quad>
 __device__ __forceinline__ void store_values_t(const Quad (&v)[1024 / NTH], float* dst) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
-    const int e = tix() + NTH * i, t = e % C, p = 4 * (e / C);
+    int t, p;
+    value_slot<NTH>(i, t, p);
     const f4 x = dec(v[i]);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[(p + k) * LV + t] = x[k];
   }
 }
 
-// A stored [NT][PT] state tile into LDS transposed, [PT][LQ]: thread e takes
-// row n = e % NT (consecutive lanes, conflict-free LDS stores) and columns
-// 4 (e / NT) .. +3, all read before any is stored.
+// A stored [NT][PT] state tile in registers: for i < 2048 / NTH, thread
+// (wave w, lane L) holds the four elements (n, p .. p + 3) of block
+// bi = i NTH / 64 + w, with n = 16 (bi / 4) + L / 4 and p = 16 (bi % 4) +
+// 4 (L % 4).  Each load instruction reads one 16 x 16 block (16 row pieces
+// of 64 contiguous bytes, not 64 lanes each in its own cache line), and
+// each transposed LDS store instruction ((p + k) LQ + n, LQ = 4 mod 64)
+// hits 64 distinct banks.
+template <int NTH>
+__device__ __forceinline__ void state_slot(int i, int& n, int& p) {
+  const int tid = tix(), L = tid & 63, bi = i * (NTH / 64) + (tid >> 6);
+  n = 16 * (bi >> 2) + (L >> 2);
+  p = 16 * (bi & 3) + 4 * (L & 3);
+}
+
 template <int NTH = 256>
 __device__ __forceinline__ void fetch_state_t(const float* src, f4 (&v)[2048 / NTH]) {
 #pragma unroll
   for (int i = 0; i < 2048 / NTH; ++i) {
-    const int e = tix() + NTH * i;
-    v[i] = *reinterpret_cast<const f4*>(src + (e % NT) * PT + 4 * (e / NT));
+    int n, p;
+    state_slot<NTH>(i, n, p);
+    v[i] = *reinterpret_cast<const f4*>(src + n * PT + p);
   }
 }
 
+// Into LDS transposed, [PT][LQ].
 template <int NTH = 256>
 __device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], float* dst) {
 #pragma unroll
   for (int i = 0; i < 2048 / NTH; ++i) {
-    const int e = tix() + NTH * i, n = e % NT, p = 4 * (e / NT);
+    int n, p;
+    state_slot<NTH>(i, n, p);
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[(p + k) * LQ + n] = v[i][k];
   }
 }
 
-// The same registers (row n = e % NT, columns 4 (e / NT) .. +3) into the
-// untransposed [NT][LV] layout: one 16-byte store each.
+// The same registers into the untransposed [NT][LV] layout: one 16-byte
+// store each.
 template <int NTH = 256>
 __device__ __forceinline__ void store_state_rows(const f4 (&v)[2048 / NTH], float* dst) {
 #pragma unroll
   for (int i = 0; i < 2048 / NTH; ++i) {
-    const int e = tix() + NTH * i, n = e % NT, p = 4 * (e / NT);
+    int n, p;
+    state_slot<NTH>(i, n, p);
     *reinterpret_cast<f4*>(dst + n * LV + p) = v[i];
   }
 }
