@@ -452,23 +452,37 @@ struct TileRegs2 {
 };
 
 // The transpose of a dense row-major 64x64 matrix: tile[c][r] = src[r][c].
-// Thread i fetches row i%64, column quads i/64 + 4j; the scalar LDS stores
-// of a wave then fall in consecutive banks.
+// Fetch j of wave w covers the 16x16 block b = 4 j + w: lane L holds row
+// 16 (b / 4) + L / 4, columns 16 (b % 4) + 4 (L % 4) .. +3.  Each load
+// instruction reads 16 row pieces of 64 contiguous bytes (not one cache
+// line per lane), and the scalar LDS stores of a wave fall in 64 distinct
+// banks (LDT = 4 mod 64).
 struct TileRegsT {
   f4 v[4];
 
+  __device__ __forceinline__ static void slot(int j, int& r, int& c) {
+    const int L = threadIdx.x & 63, b = 4 * j + (threadIdx.x >> 6);
+    r = 16 * (b >> 2) + (L >> 2);
+    c = 16 * (b & 3) + 4 * (L & 3);
+  }
+
   __device__ __forceinline__ void fetch_matrix(const float* src) {
-    const int r = threadIdx.x & 63, q0 = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const f4*>(src + r * 64 + 4 * (q0 + 4 * j));
+    for (int j = 0; j < 4; ++j) {
+      int r, c;
+      slot(j, r, c);
+      v[j] = *reinterpret_cast<const f4*>(src + r * 64 + c);
+    }
   }
 
   __device__ __forceinline__ void store(float* tile) const {
-    const int r = threadIdx.x & 63, q0 = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      int r, c;
+      slot(j, r, c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tile[(4 * (q0 + 4 * j) + i) * LDT + r] = v[j][i];
+      for (int i = 0; i < 4; ++i) tile[(c + i) * LDT + r] = v[j][i];
+    }
   }
 };
 
