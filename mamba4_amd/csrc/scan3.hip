@@ -331,6 +331,72 @@ __device__ __forceinline__ void mma_first2(f4 (&acc)[2], const float* A, int r0,
   }
 }
 
+// acc[jb] += A[r0 .. r0+16, kb .. ke) * B[kb .. ke, c0 + J r + jb] for jb < J
+// (J = 2 or 4), B(k, c) = B[k * BK + c]: lane r's J accumulators are J
+// adjacent columns of one row, so each k's B values for all J tiles arrive
+// in one 8- or 16-byte LDS read, where a B strided along k (BK > 1) costs
+// mma one read per element.  Result element acc[jb][i] is (row
+// r0 + 4 (lane / 16) + i, column c0 + J (lane % 16) + jb).  A, the k
+// assignment and BF as in mma.
+template <int J, int AR, int AK, int BK, bool BF = false>
+__device__ __forceinline__ void mma_quad(f4 (&acc)[J], const float* A, int r0, const float* B,
+                                         int c0, int kb, int ke) {
+  typedef float fJ __attribute__((ext_vector_type(J)));
+  const int l = lane_id(), r = l & 15, q = l >> 4;
+  const float* pb = B + c0 + J * r;
+  auto ldb_row = [&](int k) { return *reinterpret_cast<const fJ*>(pb + k * BK); };
+  if constexpr (BF) {
+    const float* pa = A + (r0 + r) * AR + 8 * q * AK;
+    int k = kb;
+#pragma unroll 1
+    for (; k + 32 <= ke; k += 32) {
+      const bf16x8 a = pack8(load_k4<AK>(pa + k * AK), load_k4<AK>(pa + (k + 4) * AK));
+      // Each pair of k rows is rounded as it arrives: pk[jb][e] holds
+      // k = 8 q + 2 e, +1 of column jb.
+      bf16x2 pk[J][4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const fJ x0 = ldb_row(k + 8 * q + 2 * e), x1 = ldb_row(k + 8 * q + 2 * e + 1);
+#pragma unroll
+        for (int jb = 0; jb < J; ++jb) pk[jb][e] = cvt2(x0[jb], x1[jb]);
+      }
+#pragma unroll
+      for (int jb = 0; jb < J; ++jb) {
+        const bf16x8 b = bf16x8{pk[jb][0][0], pk[jb][0][1], pk[jb][1][0], pk[jb][1][1],
+                                pk[jb][2][0], pk[jb][2][1], pk[jb][3][0], pk[jb][3][1]};
+        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[jb], 0, 0, 0);
+      }
+    }
+    if (k < ke) {
+      const bf16x4 a = pack4(load_k4<AK>(A + (r0 + r) * AR + (k + 4 * q) * AK));
+      fJ bv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = ldb_row(k + 4 * q + e);
+#pragma unroll
+      for (int jb = 0; jb < J; ++jb) {
+        const bf16x4 b = pack4(f4{bv[0][jb], bv[1][jb], bv[2][jb], bv[3][jb]});
+        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                            __builtin_bit_cast(s16x4, b),
+                                                            acc[jb], 0, 0, 0);
+      }
+    }
+  } else {
+    const float* pa = A + (r0 + r) * AR + 4 * q * AK;
+#pragma unroll 2
+    for (int k = kb; k < ke; k += 16) {
+      const f4 a = load_k4<AK>(pa + k * AK);
+      fJ bv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = ldb_row(k + 4 * q + e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jb = 0; jb < J; ++jb)
+          acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], bv[e][jb], acc[jb], 0, 0, 0);
+    }
+  }
+}
+
 // mma over the first jn (1..4, the same for the whole wave) of four column
 // tiles: each count is its own straight-line instantiation, so no MFMA sits
 // under a per-tile branch.
@@ -668,17 +734,6 @@ __device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], float* 
   }
 }
 
-// The same registers into the untransposed [NT][LV] layout: one 16-byte
-// store each.
-template <int NTH = 256>
-__device__ __forceinline__ void store_state_rows(const f4 (&v)[2048 / NTH], float* dst) {
-#pragma unroll
-  for (int i = 0; i < 2048 / NTH; ++i) {
-    int n, p;
-    state_slot<NTH>(i, n, p);
-    *reinterpret_cast<f4*>(dst + n * LV + p) = v[i];
-  }
-}
 
 
 // ---------------------------------------------------------------------------
@@ -881,9 +936,12 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
   for (; it < total; it += gridDim.x) {
     int b, c, h;
     item_of(it, b, c, h);
-    // Eight waves: wave w owns row block wr = w & 3 and column half wc = w >> 2.
+    // Eight waves: wave w owns column half wc = w >> 2 and row block wr =
+    // w & 3, mirrored (3 - (w & 3)) in the second half, so the two waves on
+    // each SIMD (w, w + 4) hold row blocks whose causal work sums to the same.
     const int tid = tix(), l = lane_id(), r = l & 15, q = l >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wc = w >> 2;
+    const int wr = wc ? 3 - (w & 3) : w & 3;
 
     if (w == 0) token_scalars(F.tin, S);
     if (tid < s.A) th0[tid] = F.th;
@@ -957,8 +1015,9 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
 // then the rotation's transpose (dq -> d(c + qb)) and the phase gradient
 // dtheta_t,j = dq_{2j+1} q_{2j} - dq_{2j} q_{2j+1} (+ the same for k), summed
 // from the end of the chunk: R_t = sum_{t' >= t} dtheta_t'.
-// LDS: R1 = 2 NT LV floats (Q, K; later H0, dH1; later dQ, dK), R2 = 2 NT LV
-// floats (H0, dH1; later V, dY, S o W, G), phase table [C][LA], scalars.
+// LDS: R1 = 2 NT LV floats (Q, K; later H0, dH1 transposed; later dQ, dK),
+// R2 = 2 NT LV floats (H0, dH1 transposed; later V, dY, S o W, G), phase
+// table [C][LA], scalars.
 template <typename In, bool V4>
 __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In* cq,
                                                    const In* bk, const In* x,
@@ -997,8 +1056,10 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
   const int g = id % groups, c = (id / groups) % s.NC, b = id / (groups * s.NC);
   const int hpg = (s.H + groups - 1) / groups, h_begin = g * hpg;
   const int h_end = min(s.H, h_begin + hpg);
-  // Eight waves: wave w owns row block wr = w & 3 of every 64-row tile and
-  // column half wc = w >> 2 of its columns.  This group's sums over its
+  // Eight waves: wave w owns column half wc = w >> 2 of every 64-row tile's
+  // columns and its row block wr = w & 3, mirrored (3 - (w & 3)) in the
+  // second half, so the two waves on each SIMD (w, w + 4) hold row blocks
+  // whose causal work sums to the same.  This group's sums over its
   // heads: the rotated-back row gradients of this thread's 8 (token
   // w + 8 m, pair) slots and the angle gradients of its 8 (token = lane,
   // angle w + 8 m) slots stay in registers until the last head.
@@ -1029,9 +1090,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
 
   // A head's own inputs, fetched into registers while the previous head's
   // last phases run: its per-token scalars, start phase, start state and
-  // end cotangent (in the transposed-staging layout; the same registers
-  // later fill the untransposed copies, so the pair is read once) and
-  // biases.  Its values and d_y load at the head's start, for its fourth
+  // end cotangent (staged transposed twice from the same registers, for
+  // the products with Q, K and later with dY, V, so the pair is read once)
+  // and biases.  Its values and d_y load at the head's start, for its fourth
   // phase.
   struct HeadIn {
     TokenIn tin;
@@ -1052,7 +1113,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
 
   for (int h = h_begin; h < h_end; ++h) {
     const int tid = tix(), l = tid & 63, r = l & 15, q = l >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wr = w & 3, wc = w >> 2;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wc = w >> 2;
+    const int wr = wc ? 3 - (w & 3) : w & 3;
     const int n2 = 2 * l;  // this lane's coordinate pair in the rotation passes
     __syncthreads();  // the previous head is done with every LDS array
     typename Raw<In>::Quad vx[2], vd[2];
@@ -1208,9 +1270,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     zero(dk);
     zero(dv);
     // G K: A(t, s) = G[t * LV + s], B(s, n) = K[s * LQ + n].
-    mma<4, LV, 1, LQ, 1, BF>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
+    mma_quad<4, LV, 1, LQ, BF>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
     // G^T Q: A(s, t) = G[t * LV + s], B(t, n) = Q[t * LQ + n].
-    mma<4, 1, LV, LQ, 1, BF>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
+    mma_quad<4, 1, LV, LQ, BF>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
     // (S o W)^T dY.
     mma<2, 1, LV, LV, 1, BF>(dv, gs, 16 * wr, dyt, 32 * wc, 16 * wr, C);
 #pragma unroll
@@ -1231,36 +1293,36 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
       dyt[t * LV + p] *= S.ep[t];
       if (!BF) vt[t * LV + p] *= S.u[t];
     }
-    store_state_rows<512>(F.hs, R1);
-    store_state_rows<512>(F.hg, R1 + NT * LV);
+    store_state_t<512>(F.hs, R1);
+    store_state_t<512>(F.hg, R1 + PT * LQ);
     __syncthreads();
     // Every register of F is staged: the next head's inputs load during this
     // head's remaining phases (which wait for no global load).
     if (h + 1 < h_end) fetch_head(F, h + 1);
-    // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0[n * LV + p].
-    mma<4, LV, 1, 1, LV, BF>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
+    // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0t[p * LQ + n].
+    mma_quad<4, LV, 1, LQ, BF>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
     if constexpr (BF) {
       f4 vd[4];
       zero(vd);
-      mma<4, LV, 1, 1, LV, BF>(vd, vt, 16 * wr, R1 + NT * LV, 64 * wc, 0, PT);
+      mma_quad<4, LV, 1, LQ, BF>(vd, vt, 16 * wr, R1 + PT * LQ, 64 * wc, 0, PT);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) dk[j][i] += S.u[16 * wr + 4 * q + i] * vd[j][i];
     } else {
-      mma<4, LV, 1, 1, LV>(dk, vt, 16 * wr, R1 + NT * LV, 64 * wc, 0, PT);
+      mma_quad<4, LV, 1, LQ>(dk, vt, 16 * wr, R1 + PT * LQ, 64 * wc, 0, PT);
     }
     __syncthreads();
     float* dqt = R1;
     float* dkt = R1 + C * LQ;
+    // mma_quad's layout: a lane's four accumulators are columns
+    // 64 wc + 4 r .. +3 of its rows, one 16-byte store per row.
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * wr + 4 * q + i, n = 64 * wc + 16 * j + r;
-        dqt[t * LQ + n] = dq[j][i];
-        dkt[t * LQ + n] = dk[j][i];
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * wr + 4 * q + i, n = 64 * wc + 4 * r;
+      *reinterpret_cast<f4*>(dqt + t * LQ + n) = f4{dq[0][i], dq[1][i], dq[2][i], dq[3][i]};
+      *reinterpret_cast<f4*>(dkt + t * LQ + n) = f4{dk[0][i], dk[1][i], dk[2][i], dk[3][i]};
+    }
     __syncthreads();
 
     // Through the rotations: one pair per lane, tokens w, w + 8, ...
