@@ -319,18 +319,6 @@ __device__ __forceinline__ void mma(f4 (&acc)[J], const float* A, int r0, const 
   }
 }
 
-// mma over the first jn (0..2, the same for the whole wave) of two column
-// tiles, each count its own straight-line instantiation.
-template <int AR, int AK, int BK, int BC, bool BF = false>
-__device__ __forceinline__ void mma_first2(f4 (&acc)[2], const float* A, int r0, const float* B,
-                                           int c0, int kb, int ke, int jn) {
-  if (jn >= 2) {
-    mma<2, AR, AK, BK, BC, BF>(acc, A, r0, B, c0, kb, ke);
-  } else if (jn == 1) {
-    mma<1, AR, AK, BK, BC, BF>(*reinterpret_cast<f4(*)[1]>(acc), A, r0, B, c0, kb, ke);
-  }
-}
-
 // acc[jb] += A[r0 .. r0+16, kb .. ke) * B[kb .. ke, c0 + J r + jb] for jb < J
 // (J = 2 or 4), B(k, c) = B[k * BK + c]: lane r's J accumulators are J
 // adjacent columns of one row, so each k's B values for all J tiles arrive
@@ -423,6 +411,167 @@ template <int J>
 __device__ __forceinline__ void zero(f4 (&acc)[J]) {
 #pragma unroll
   for (int j = 0; j < J; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+}
+
+// ---------------------------------------------------------------------------
+// bfloat16 LDS tiles.  With bfloat16 operands the products' LDS operands are
+// stored already rounded (to nearest even, as mma<..., BF> rounds a float32
+// tile at its read), so every product is unchanged, with half the LDS bytes
+// and no conversion per read.  Row strides of 68 words (= 4 mod 64) for
+// [.][NT] tiles and 36 words for [.][PT] tiles spread a product's 16-byte
+// operand reads over the banks.
+constexpr int LQB = NT + 8;
+constexpr int LVB = PT + 8;
+
+template <bool BF>
+struct Tile {
+  typedef float T;
+  static constexpr int LQt = LQ, LVt = LV;
+};
+template <>
+struct Tile<true> {
+  typedef bf16_t T;
+  static constexpr int LQt = LQB, LVt = LVB;
+};
+
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16_t to_bf(float x) {
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(x));
+}
+__device__ __forceinline__ unsigned to_bf2(float a, float b) {
+  return __builtin_bit_cast(unsigned, cvt2(a, b));
+}
+
+// A tile's element, two adjacent elements, four adjacent elements.
+__device__ __forceinline__ void put(float* p, float x) { *p = x; }
+__device__ __forceinline__ void put(bf16_t* p, float x) { *p = to_bf(x); }
+__device__ __forceinline__ void put2(float* p, float a, float b) {
+  *reinterpret_cast<float2*>(p) = float2{a, b};
+}
+__device__ __forceinline__ void put2(bf16_t* p, float a, float b) {
+  *reinterpret_cast<unsigned*>(p) = to_bf2(a, b);
+}
+__device__ __forceinline__ void put4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+__device__ __forceinline__ void put4(bf16_t* p, f4 v) {
+  *reinterpret_cast<u2*>(p) = u2{to_bf2(v[0], v[1]), to_bf2(v[2], v[3])};
+}
+__device__ __forceinline__ float get(const float* p) { return *p; }
+__device__ __forceinline__ float get(const bf16_t* p) { return lo_bf(*p); }
+__device__ __forceinline__ f4 get4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ f4 get4(const bf16_t* p) { return dec(*reinterpret_cast<const u2*>(p)); }
+
+// Eight (four) consecutive-in-k bfloat16 operand values, k stride S: one
+// 16-byte (8-byte) read when S is 1.
+template <int S>
+__device__ __forceinline__ bf16x8 load_k8(const bf16_t* p) {
+  if constexpr (S == 1) {
+    return *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(__bf16, p[e * S]);
+    return v;
+  }
+}
+template <int S>
+__device__ __forceinline__ bf16x4 load_k4b(const bf16_t* p) {
+  if constexpr (S == 1) {
+    return *reinterpret_cast<const bf16x4*>(p);
+  } else {
+    bf16x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(__bf16, p[e * S]);
+    return v;
+  }
+}
+
+// mma on bfloat16 tiles (the same k assignment and result layout).
+template <int J, int AR, int AK, int BK, int BC, bool BF>
+__device__ __forceinline__ void mma(f4 (&acc)[J], const bf16_t* A, int r0, const bf16_t* B,
+                                    int c0, int kb, int ke) {
+  static_assert(BF, "bfloat16 tiles hold bfloat16 operands");
+  const int l = lane_id(), r = l & 15, q = l >> 4;
+  const bf16_t* pa = A + (r0 + r) * AR + 8 * q * AK;
+  const bf16_t* pb = B + 8 * q * BK + (c0 + r) * BC;
+  int k = kb;
+#pragma unroll 1
+  for (; k + 32 <= ke; k += 32) {
+    const bf16x8 a = load_k8<AK>(pa + k * AK);
+    bf16x8 b[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) b[j] = load_k8<BK>(pb + k * BK + 16 * j * BC);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], acc[j], 0, 0, 0);
+  }
+  if (k < ke) {
+    const bf16x4 a = load_k4b<AK>(A + (r0 + r) * AR + (k + 4 * q) * AK);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const bf16x4 b = load_k4b<BK>(B + (k + 4 * q) * BK + (c0 + 16 * j + r) * BC);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                         __builtin_bit_cast(s16x4, b),
+                                                         acc[j], 0, 0, 0);
+    }
+  }
+}
+
+// mma_quad on bfloat16 tiles (J = 4): each k's four B values are one 8-byte
+// read (two words, columns jb = 0, 1 and 2, 3), and a tile's operand pairs
+// are assembled with one byte permute per pair of k.
+template <int J, int AR, int AK, int BK, bool BF>
+__device__ __forceinline__ void mma_quad(f4 (&acc)[J], const bf16_t* A, int r0, const bf16_t* B,
+                                         int c0, int kb, int ke) {
+  static_assert(BF && J == 4, "bfloat16 tiles: four columns per lane");
+  const int l = lane_id(), r = l & 15, q = l >> 4;
+  const bf16_t* pb = B + c0 + 4 * r;
+  auto row = [&](int k) { return *reinterpret_cast<const u2*>(pb + k * BK); };
+  // Column jb of rows x0 (low half) and x1 (high half).
+  auto pair = [&](u2 x0, u2 x1, int jb) {
+    return __builtin_amdgcn_perm(x1[jb >> 1], x0[jb >> 1], (jb & 1) ? 0x07060302u : 0x05040100u);
+  };
+  const bf16_t* pa = A + (r0 + r) * AR + 8 * q * AK;
+  int k = kb;
+#pragma unroll 1
+  for (; k + 32 <= ke; k += 32) {
+    const bf16x8 a = load_k8<AK>(pa + k * AK);
+    u2 x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = row(k + 8 * q + e);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const u4 w = u4{pair(x[0], x[1], jb), pair(x[2], x[3], jb), pair(x[4], x[5], jb),
+                      pair(x[6], x[7], jb)};
+      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, w),
+                                                        acc[jb], 0, 0, 0);
+    }
+  }
+  if (k < ke) {
+    const bf16x4 a = load_k4b<AK>(A + (r0 + r) * AR + (k + 4 * q) * AK);
+    u2 x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = row(k + 4 * q + e);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const u2 w = u2{pair(x[0], x[1], jb), pair(x[2], x[3], jb)};
+      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                          __builtin_bit_cast(s16x4, w),
+                                                          acc[jb], 0, 0, 0);
+    }
+  }
+}
+
+// mma over the first jn (0..2, the same for the whole wave) of two column
+// tiles, each count its own straight-line instantiation (float32 or
+// bfloat16 tiles).
+template <int AR, int AK, int BK, int BC, bool BF = false, typename TT>
+__device__ __forceinline__ void mma_first2(f4 (&acc)[2], const TT* A, int r0, const TT* B, int c0,
+                                           int kb, int ke, int jn) {
+  if (jn >= 2) {
+    mma<2, AR, AK, BK, BC, BF>(acc, A, r0, B, c0, kb, ke);
+  } else if (jn == 1) {
+    mma<1, AR, AK, BK, BC, BF>(*reinterpret_cast<f4(*)[1]>(acc), A, r0, B, c0, kb, ke);
+  }
 }
 
 __device__ __forceinline__ long tok_index(const Shape& s, int b, int t) {
@@ -648,13 +797,21 @@ __device__ __forceinline__ void fetch_values(const Shape& s, const In* src, int 
   }
 }
 
-template <int NTH, typename Quad>
+// Into a [C][LD] tile of float32 or bfloat16 (bfloat16 inputs unscaled go
+// in as their bits).
+template <int NTH, int LD = LV, typename Quad, typename TT>
 __device__ __forceinline__ void store_values(const Quad (&v)[1024 / NTH], const float* row_scale,
-                                             float* dst) {
+                                             TT* dst) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     const int e = tix() + NTH * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
-    *reinterpret_cast<f4*>(dst + t * LV + p) = row_scale ? dec(v[i]) * row_scale[t] : dec(v[i]);
+    if constexpr (__is_same(TT, bf16_t) && __is_same(Quad, u2)) {
+      if (!row_scale) {
+        *reinterpret_cast<u2*>(dst + t * LD + p) = v[i];
+        continue;
+      }
+    }
+    put4(dst + t * LD + p, row_scale ? dec(v[i]) * row_scale[t] : dec(v[i]));
   }
 }
 
@@ -686,15 +843,15 @@ __device__ __forceinline__ void fetch_values_t(const Shape& s, const In* src, in
   }
 }
 
-template <int NTH, typename Quad>
-__device__ __forceinline__ void store_values_t(const Quad (&v)[1024 / NTH], float* dst) {
+template <int NTH, int LD = LV, typename Quad, typename TT>
+__device__ __forceinline__ void store_values_t(const Quad (&v)[1024 / NTH], TT* dst) {
 #pragma unroll
   for (int i = 0; i < 1024 / NTH; ++i) {
     int t, p;
     value_slot<NTH>(i, t, p);
     const f4 x = dec(v[i]);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) dst[(p + k) * LV + t] = x[k];
+    for (int k = 0; k < 4; ++k) put(dst + (p + k) * LD + t, x[k]);
   }
 }
 
@@ -722,15 +879,15 @@ __device__ __forceinline__ void fetch_state_t(const float* src, f4 (&v)[2048 / N
   }
 }
 
-// Into LDS transposed, [PT][LQ].
-template <int NTH = 256>
-__device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], float* dst) {
+// Into LDS transposed, [PT][LD] (float32 or bfloat16).
+template <int NTH = 256, int LD = LQ, typename TT>
+__device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], TT* dst) {
 #pragma unroll
   for (int i = 0; i < 2048 / NTH; ++i) {
     int n, p;
     state_slot<NTH>(i, n, p);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) dst[(p + k) * LQ + n] = v[i][k];
+    for (int k = 0; k < 4; ++k) put(dst + (p + k) * LD + n, v[i][k]);
   }
 }
 
@@ -1027,6 +1184,10 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
                                                    const float* theta0, const float* starts,
                                                    const float* dh1, const In* dy, GradOut o) {
   constexpr bool BF = is_bf16<In>::value;
+  // The products' LDS operands: float32, or bfloat16 rounded where they are
+  // written (the dQ / dK epilogue tiles stay float32).
+  typedef typename Tile<BF>::T TT;
+  constexpr int LQt = Tile<BF>::LQt, LVt = Tile<BF>::LVt;
   In* const dx = static_cast<In*>(o.dx);
   extern __shared__ float sm[];
   float* R1 = sm;
@@ -1090,9 +1251,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
 
   // A head's own inputs, fetched into registers while the previous head's
   // last phases run: its per-token scalars, start phase, start state and
-  // end cotangent (staged transposed twice from the same registers, for
-  // the products with Q, K and later with dY, V, so the pair is read once)
-  // and biases.  Its values and d_y load at the head's start, for its fourth
+  // end cotangent (read once: staged transposed for the products with Q
+  // and K, and with float32 tiles staged again from the same registers for
+  // the products with dY and V) and biases.  Its values and d_y load at the head's start, for its fourth
   // phase.
   struct HeadIn {
     TokenIn tin;
@@ -1130,14 +1291,26 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     __syncthreads();
     phase_table<8>(s, rates, S.dt, th0, tab, false);
     __syncthreads();
-    float* qt = R1;
-    float* kt = R1 + C * LQ;
-    // The start state and end cotangent transposed, [PT][LQ], for Q H0 and
-    // K dH1 with both operands contiguous along n.
-    float* h0 = R2;
-    float* g1 = R2 + NT * LV;
-    store_state_t<512>(F.hs, h0);
-    store_state_t<512>(F.hg, g1);
+    TT* const qt = reinterpret_cast<TT*>(R1);
+    TT* const kt = qt + C * LQt;
+    // The start state and end cotangent transposed, [PT][LQt], for Q H0 and
+    // K dH1 with both operands contiguous along n.  bfloat16 tiles: in R1
+    // after Q and K, where they stay for the dY and V products of the
+    // second half; float32: in R2, staged again into R1 for those.
+    TT* const h0 = BF ? kt + C * LQt : reinterpret_cast<TT*>(R2);
+    TT* const g1 = h0 + PT * LQt;
+    store_state_t<512, LQt>(F.hs, h0);
+    store_state_t<512, LQt>(F.hg, g1);
+    {
+      // <H0, dH1> from the registers (both tiles in the same layout).
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) part += F.hs[i][k] * F.hg[i][k];
+      part = wave_sum(part);
+      if (l == 0) hsum[w] = part;
+    }
     const float2 bq = F.bq, bkv = F.bk;
     {
       const bool col = n2 < s.N;
@@ -1152,10 +1325,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
                                              : float2{0.f, 0.f});
         const float2 v = round_bf2<BF>(valid ? float2{bm.x + bkv.x, bm.y + bkv.y}
                                              : float2{0.f, 0.f});
-        *reinterpret_cast<float2*>(qt + t * LQ + n2) =
-            float2{u.x * cs - u.y * sn, u.x * sn + u.y * cs};
-        *reinterpret_cast<float2*>(kt + t * LQ + n2) =
-            float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
+        put2(qt + t * LQt + n2, u.x * cs - u.y * sn, u.x * sn + u.y * cs);
+        put2(kt + t * LQt + n2, v.x * cs - v.y * sn, v.x * sn + v.y * cs);
       }
     }
     __syncthreads();
@@ -1167,33 +1338,39 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     zero(sco);
     zero(qh);
     zero(kg);
-    mma_first2<LQ, 1, 1, LQ, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
-    // B(n, p) = H0t[p * LQ + n].
-    mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
-    mma<2, LQ, 1, 1, LQ, BF>(kg, kt, 16 * wr, g1, 32 * wc, 0, NT);
-    {
-      // <H0, dH1> from the registers (both tiles in the same layout).
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) part += F.hs[i][k] * F.hg[i][k];
-      part = wave_sum(part);
-      if (l == 0) hsum[w] = part;
-    }
+    mma_first2<LQt, 1, 1, LQt, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+    // B(n, p) = H0t[p * LQt + n].
+    mma<2, LQt, 1, 1, LQt, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
+    mma<2, LQt, 1, 1, LQt, BF>(kg, kt, 16 * wr, g1, 32 * wc, 0, NT);
     __syncthreads();
-    float* vt = R2;
-    float* dyt = R2 + C * LV;
-    float* gs = R2 + 2 * C * LV;
-    float* gm = R2 + 3 * C * LV;
-    store_values<512>(vx, nullptr, vt);
-    store_values<512>(vd, nullptr, dyt);
+    // V, dY, S o W and G as [C][LVt] tiles.  With bfloat16 tiles R2 has
+    // room for transposed copies of G and dY, and S o W is kept transposed
+    // only, so every operand of G^T Q and (S o W)^T dY is contiguous along k.
+    TT* const vt = reinterpret_cast<TT*>(R2);
+    TT* const dyt = vt + C * LVt;
+    TT* const gs = vt + 2 * C * LVt;  // float32: [t][s]; bfloat16: [s][t]
+    TT* const gm = vt + 3 * C * LVt;
+    TT* const gmt = vt + 4 * C * LVt;  // bfloat16: G transposed
+    TT* const dyT = vt + 5 * C * LVt;  // bfloat16: dY transposed, [p][t]
+    store_values<512, LVt>(vx, nullptr, vt);
+    store_values<512, LVt>(vd, nullptr, dyt);
+    if constexpr (BF) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+        const u2 x = vd[i];
+        dyT[p * LVt + t] = (bf16_t)x.x;
+        dyT[(p + 1) * LVt + t] = (bf16_t)(x.x >> 16);
+        dyT[(p + 2) * LVt + t] = (bf16_t)x.y;
+        dyT[(p + 3) * LVt + t] = (bf16_t)(x.y >> 16);
+      }
+    }
     __syncthreads();
 
     f4 dsc[2];
     zero(dsc);
-    // dY V^T: A(t, p) = dY[t * LV + p], B(p, s) = V[s * LV + p].
-    mma_first2<LV, 1, 1, LV, BF>(dsc, dyt, 16 * wr, vt, 32 * wc, 0, PT, ns);
+    // dY V^T: A(t, p) = dY[t * LVt + p], B(p, s) = V[s * LVt + p].
+    mma_first2<LVt, 1, 1, LVt, BF>(dsc, dyt, 16 * wr, vt, 32 * wc, 0, PT, ns);
     {
       float qd[4] = {0.f, 0.f, 0.f, 0.f}, gg[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1201,8 +1378,8 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 16 * wr + 4 * q + i, p = 32 * wc + 16 * j + r;
-          qd[i] += qh[j][i] * dyt[t * LV + p];
-          gg[i] += kg[j][i] * vt[t * LV + p];
+          qd[i] += qh[j][i] * get(dyt + t * LVt + p);
+          gg[i] += kg[j][i] * get(vt + t * LVt + p);
         }
       float rowE[4] = {0.f, 0.f, 0.f, 0.f};
       float colF[2] = {0.f, 0.f}, colE[2] = {0.f, 0.f};
@@ -1213,8 +1390,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int t = 16 * wr + 4 * q + i, u = 16 * jt + r;
-            gs[t * LV + u] = 0.f;
-            gm[t * LV + u] = 0.f;
+            put(gs + (BF ? u * LVt + t : t * LVt + u), 0.f);
+            put(gm + t * LVt + u, 0.f);
+            if constexpr (BF) put(gmt + u * LVt + t, 0.f);
           }
           continue;
         }
@@ -1234,8 +1412,9 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
             wt = S.gam[t];
             s_dgd[t] = st * ds;
           }
-          gs[t * LV + u] = st * wt;
-          gm[t * LV + u] = ds * wt;
+          put(gs + (BF ? u * LVt + t : t * LVt + u), st * wt);
+          put(gm + t * LVt + u, ds * wt);
+          if constexpr (BF) put(gmt + u * LVt + t, ds * wt);
         }
       }
 #pragma unroll
@@ -1269,12 +1448,19 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     zero(dq);
     zero(dk);
     zero(dv);
-    // G K: A(t, s) = G[t * LV + s], B(s, n) = K[s * LQ + n].
-    mma_quad<4, LV, 1, LQ, BF>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
-    // G^T Q: A(s, t) = G[t * LV + s], B(t, n) = Q[t * LQ + n].
-    mma_quad<4, 1, LV, LQ, BF>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
-    // (S o W)^T dY.
-    mma<2, 1, LV, LV, 1, BF>(dv, gs, 16 * wr, dyt, 32 * wc, 16 * wr, C);
+    // G K: A(t, s) = G[t * LVt + s], B(s, n) = K[s * LQt + n].
+    mma_quad<4, LVt, 1, LQt, BF>(dq, gm, 16 * wr, kt, 64 * wc, 0, 16 * (wr + 1));
+    if constexpr (BF) {
+      // G^T Q: A(s, t) = Gt[s * LVt + t], B(t, n) = Q[t * LQt + n].
+      mma_quad<4, LVt, 1, LQt, BF>(dk, gmt, 16 * wr, qt, 64 * wc, 16 * wr, C);
+      // (S o W)^T dY: A(s, t) = (S o W)t[s * LVt + t], B(t, p) = dYt[p * LVt + t].
+      mma<2, LVt, 1, 1, LVt, BF>(dv, gs, 16 * wr, dyT, 32 * wc, 16 * wr, C);
+    } else {
+      // G^T Q: A(s, t) = G[t * LV + s], B(t, n) = Q[t * LQ + n].
+      mma_quad<4, 1, LV, LQ, BF>(dk, gm, 16 * wr, qt, 64 * wc, 16 * wr, C);
+      // (S o W)^T dY.
+      mma<2, 1, LV, LV, 1, BF>(dv, gs, 16 * wr, dyt, 32 * wc, 16 * wr, C);
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -1288,29 +1474,33 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     // cotangent, :740); V's factor u is applied to the product's rows after
     // it with bfloat16 operands (the reference scales v dH1^T, :749-750),
     // before it in float32, where the two agree.
-    for (int e = tid; e < C * PT; e += 512) {
-      const int t = e / PT, p = e % PT;
-      dyt[t * LV + p] *= S.ep[t];
-      if (!BF) vt[t * LV + p] *= S.u[t];
+#pragma unroll
+    for (int i = 0; i < C * PT / 2048; ++i) {
+      const int e = tid + 512 * i, t = e / (PT / 4), p = 4 * (e % (PT / 4));
+      put4(dyt + t * LVt + p, get4(dyt + t * LVt + p) * S.ep[t]);
+      if constexpr (!BF) put4(vt + t * LVt + p, get4(vt + t * LVt + p) * S.u[t]);
     }
-    store_state_t<512>(F.hs, R1);
-    store_state_t<512>(F.hg, R1 + PT * LQ);
+    TT* const h0b = BF ? h0 : reinterpret_cast<TT*>(R1);
+    if constexpr (!BF) {
+      store_state_t<512, LQt>(F.hs, h0b);
+      store_state_t<512, LQt>(F.hg, h0b + PT * LQt);
+    }
     __syncthreads();
     // Every register of F is staged: the next head's inputs load during this
     // head's remaining phases (which wait for no global load).
     if (h + 1 < h_end) fetch_head(F, h + 1);
-    // diag(e^p) dY H0^T: A(t, p) = dYe[t * LV + p], B(p, n) = H0t[p * LQ + n].
-    mma_quad<4, LV, 1, LQ, BF>(dq, dyt, 16 * wr, R1, 64 * wc, 0, PT);
+    // diag(e^p) dY H0^T: A(t, p) = dYe[t * LVt + p], B(p, n) = H0t[p * LQt + n].
+    mma_quad<4, LVt, 1, LQt, BF>(dq, dyt, 16 * wr, h0b, 64 * wc, 0, PT);
     if constexpr (BF) {
       f4 vd[4];
       zero(vd);
-      mma_quad<4, LV, 1, LQ, BF>(vd, vt, 16 * wr, R1 + PT * LQ, 64 * wc, 0, PT);
+      mma_quad<4, LVt, 1, LQt, BF>(vd, vt, 16 * wr, h0b + PT * LQt, 64 * wc, 0, PT);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) dk[j][i] += S.u[16 * wr + 4 * q + i] * vd[j][i];
     } else {
-      mma_quad<4, LV, 1, LQ>(dk, vt, 16 * wr, R1 + PT * LQ, 64 * wc, 0, PT);
+      mma_quad<4, LVt, 1, LQt>(dk, vt, 16 * wr, h0b + PT * LQt, 64 * wc, 0, PT);
     }
     __syncthreads();
     float* dqt = R1;
