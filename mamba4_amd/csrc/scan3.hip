@@ -756,9 +756,9 @@ __device__ __forceinline__ void fetch_rows(const Shape& s, const In* const (&src
   }
 }
 
-template <int NSRC, int NW = 4, typename Pair = float2>
+template <int NSRC, int NW = 4, int LD = LQ, typename Pair = float2, typename TT = float>
 __device__ __forceinline__ void rotate_fetched(const Shape& s, const Pair (&u)[NSRC][64 / NW],
-                                               const float2 (&bs)[NSRC], float* const (&dst)[2],
+                                               const float2 (&bs)[NSRC], TT* const (&dst)[2],
                                                const float* tab, int c) {
   constexpr bool BF = !__is_same(Pair, float2);
   const int j = lane_id(), n = 2 * j, w = tix() >> 6;
@@ -774,8 +774,7 @@ __device__ __forceinline__ void rotate_fetched(const Shape& s, const Pair (&u)[N
       const float2 x = dec(u[k][m]);
       const float2 v =
           round_bf2<BF>(valid ? float2{x.x + bs[k].x, x.y + bs[k].y} : float2{0.f, 0.f});
-      *reinterpret_cast<float2*>(dst[k] + t * LQ + n) =
-          float2{v.x * cs - v.y * sn, v.x * sn + v.y * cs};
+      put2(dst[k] + t * LD + n, v.x * cs - v.y * sn, v.x * sn + v.y * cs);
     }
   }
 }
@@ -1045,13 +1044,19 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
                                                   const float* kb, const float* theta0,
                                                   const float* starts, In* y) {
   constexpr bool BF = is_bf16<In>::value;
+  // The products' LDS operands: float32, or bfloat16 rounded where written.
+  typedef typename Tile<BF>::T TT;
+  constexpr int LQt = Tile<BF>::LQt, LVt = Tile<BF>::LVt;
   extern __shared__ float sm[];
-  float* qt = sm;
-  float* kt = qt + C * LQ;
-  float* h0 = kt + C * LQ;
-  float* tab = h0;
-  float* vt = h0 + NT * LV;
-  float* th0 = vt + C * LV;
+  float* const kf = sm + C * LQ;
+  float* const h0f = kf + C * LQ;
+  float* const vf = h0f + NT * LV;
+  TT* const qt = reinterpret_cast<TT*>(sm);
+  TT* const kt = reinterpret_cast<TT*>(kf);
+  TT* const h0 = reinterpret_cast<TT*>(h0f);
+  TT* const vt = reinterpret_cast<TT*>(vf);
+  float* tab = h0f;
+  float* th0 = vf + C * LV;
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
   const int total = s.B * s.NC * s.H;
@@ -1107,14 +1112,14 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
     phase_table_staged<8>(s, S.dt, th0, tab, false);
     __syncthreads();
     {
-      float* const dst[2] = {qt, kt};
-      rotate_fetched<2, 8>(s, F.u, F.bs, dst, tab, c);
+      TT* const dst[2] = {qt, kt};
+      rotate_fetched<2, 8, LQt>(s, F.u, F.bs, dst, tab, c);
     }
     __syncthreads();  // the phase table (in h0's space) is read
     // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
     // every product reads both operands contiguously along k.
-    store_state_t<512>(F.hv, h0);
-    store_values_t<512>(F.vv, vt);
+    store_state_t<512, LQt>(F.hv, h0);
+    store_values_t<512, LVt>(F.vv, vt);
     __syncthreads();
     // The next item's inputs load while this one's products run (no global
     // load is waited for before the next item's staging).
@@ -1125,10 +1130,10 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
     f4 sco[2], qh[2];
     zero(sco);
     zero(qh);
-    mma_first2<LQ, 1, 1, LQ, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
-    mma<2, LQ, 1, 1, LQ, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
+    mma_first2<LQt, 1, 1, LQt, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+    mma<2, LQt, 1, 1, LQt, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
     __syncthreads();  // every wave is done with K
-    float* gs = kt;
+    TT* const gs = kt;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int jt = 2 * wc + j;
@@ -1139,14 +1144,14 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
         float wt = 0.f;
         if (t > u) wt = expf(fminf(S.p[t] - S.p[u], 0.f)) * S.scale[u];
         else if (t == u) wt = S.gam[t];
-        gs[t * LV + u] = sco[j][i] * wt;
+        put(gs + t * LVt + u, sco[j][i] * wt);
       }
     }
     __syncthreads();  // a row block's S o W comes from both of its waves
     f4 acc[2];
     zero(acc);
     // B(s, p) = Vt[p * LV + s].
-    mma<2, LV, 1, 1, LV, BF>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
+    mma<2, LVt, 1, 1, LVt, BF>(acc, gs, 16 * wr, vt, 32 * wc, 0, 16 * (wr + 1));
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
