@@ -1122,15 +1122,18 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
     store_values_t<512, LVt>(F.vv, vt);
     __syncthreads();
     // The next item's inputs load while this one's products run (no global
-    // load is waited for before the next item's staging).
+    // load is waited for before the next item's staging).  The two waves on
+    // a SIMD issue them at different points (before and after the scores),
+    // so one wave's products run while the other waits to issue its loads.
     const int next = it + gridDim.x;
-    fetch(F, next < total ? next : it);
+    if (wc == 0) fetch(F, next < total ? next : it);
 
     const int ns = min(2, max(0, wr + 1 - 2 * wc));
     f4 sco[2], qh[2];
     zero(sco);
     zero(qh);
     mma_first2<LQt, 1, 1, LQt, BF>(sco, qt, 16 * wr, kt, 32 * wc, 0, NT, ns);
+    if (wc == 1) fetch(F, next < total ? next : it);
     mma<2, LQt, 1, 1, LQt, BF>(qh, qt, 16 * wr, h0, 32 * wc, 0, NT);
     __syncthreads();  // every wave is done with K
     TT* const gs = kt;
@@ -1492,10 +1495,13 @@ __global__ __launch_bounds__(512) void grad_kernel(Shape s, int groups, const In
     }
     __syncthreads();
     // Every register of F is staged: the next head's inputs load during this
-    // head's remaining phases (which wait for no global load).
-    if (h + 1 < h_end) fetch_head(F, h + 1);
+    // head's remaining phases (which wait for no global load).  The two waves
+    // on a SIMD issue them before and after their first product, so one
+    // wave's products run while the other waits to issue its loads.
+    if (wc == 0 && h + 1 < h_end) fetch_head(F, h + 1);
     // diag(e^p) dY H0^T: A(t, p) = dYe[t * LVt + p], B(p, n) = H0t[p * LQt + n].
     mma_quad<4, LVt, 1, LQt, BF>(dq, dyt, 16 * wr, h0b, 64 * wc, 0, PT);
+    if (wc == 1 && h + 1 < h_end) fetch_head(F, h + 1);
     if constexpr (BF) {
       f4 vd[4];
       zero(vd);
