@@ -161,7 +161,7 @@ def parse():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=30)
     p.add_argument("--chunk", type=int, default=64)
     p.add_argument("--workload", default="config2",
                    choices=["config2", "config3", "ref125m", "config4", "mixer", "mixer_read",
