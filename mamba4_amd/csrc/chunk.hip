@@ -588,20 +588,27 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     // the next chunk's tiles.
     const long bh = si.seq / d.NC;
     TileRegs2 rs, rc;
-    rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
-    rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
     // The last chunk of a block fetches its own tiles again (unused): every
     // load stays unconditional.
     const SeqIndex sx = seq_at(d, more ? next : seq);
-    rt[2].fetch_rows(sx.len, rows_of(solved, d, sx));
+    // The two waves on a SIMD (ws, hf = 0 and 1) issue these loads before
+    // and after their first product, so one computes while the other waits
+    // to issue.
+    auto fetch_phase4 = [&]() {
+      rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
+      rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
+      rt[2].fetch_rows(sx.len, rows_of(solved, d, sx));
+    };
+    if (hf == 0) fetch_phase4();
     __syncthreads();
     {
       f4 gk[2], hv[2];
       zero2(gk);
       zero2(hv);
       tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // G^T k_s
+      if (hf == 1) fetch_phase4();
       tile_mma_half<false, true, true>(gk, Kt, M1, 64, ws, hf);  // + G k_s
       rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
       float qpart[4] = {0.f, 0.f, 0.f, 0.f};
