@@ -1211,12 +1211,14 @@ int m3_backward_impl(const char* entry, const In* c, const In* b, const In* x, c
     if (rc) return rc;
   }
   rc = launch("m3_finish", st, [&] {
-    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC * 4), dim3(256), m3::finish_lds(H, A), st,
+    hipLaunchKernelGGL(m3::finish_kernel, dim3(B * s.NC * m3::kFinishParts), dim3(256),
+                       m3::finish_lds(H, A), st,
                        s, groups, dt, trap_logits, angles, o, d_c, d_b, d_dt, d_trap, d_angles);
   });
   if (rc) return rc;
   return launch("m3_bias", st, [&] {
-    hipLaunchKernelGGL(m3::bias_kernel, dim3(H), dim3(1024), 0, st, s, o, d_q_bias, d_k_bias);
+    hipLaunchKernelGGL(m3::bias_kernel, dim3(H * (m3::NT / 32)), dim3(1024), 0, st, s, o, d_q_bias,
+                       d_k_bias);
   });
 }
 

@@ -1656,10 +1656,12 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   float* suf = sm;                    // [H][AM] phase gradient from later chunks
   float* angs = suf + s.H * AM;       // [C][A + 1] the chunk's angle rates
   float* dts = angs + C * (s.A + 1);  // [C][H + 1] the chunk's dt
-  // Four blocks per (b, chunk), each taking 16 of its tokens.
-  const int part = blockIdx.x % 4, bc = blockIdx.x / 4;
+  // kFinishParts blocks per (b, chunk), each taking C / kFinishParts of its
+  // tokens.
+  constexpr int TPB = C / kFinishParts;
+  const int part = blockIdx.x % kFinishParts, bc = blockIdx.x / kFinishParts;
   const int b = bc / s.NC, c = bc % s.NC, tid = tix();
-  const int t0 = 16 * part, rows = max(0, min(16, s.T - c * C - t0));
+  const int t0 = TPB * part, rows = max(0, min(TPB, s.T - c * C - t0));
   for (int e = tid; e < rows * s.A; e += 256) {
     const int t = t0 + e / s.A, j = e % s.A;
     angs[t * (s.A + 1) + j] = ang[tok_index(s, b, c * C + t) * s.A + j];
@@ -1727,23 +1729,38 @@ __global__ __launch_bounds__(256) void suffix_kernel(Shape s, GradOut o) {
 // Bias gradients: sums over (b, chunk) of the per-head partials; eight
 // threads per coordinate take every eighth (b, chunk) and combine in LDS.
 __global__ __launch_bounds__(1024) void bias_kernel(Shape s, GradOut o, float* d_qb, float* d_kb) {
-  __shared__ float part[2][8][NT];
-  const int h = blockIdx.x, n = tix() % NT, slice = tix() / NT;
+  // Block (h, 32 of the NT columns): 32 slices of the (b, chunk) partials
+  // per column, each slice's loads issued eight at a time, then the slices
+  // added in a fixed order.
+  __shared__ float part[2][32][33];
+  const int h = blockIdx.x / (NT / 32), n0 = 32 * (blockIdx.x % (NT / 32));
+  const int col = tix() & 31, slice = tix() >> 5, n = n0 + col;
+  const int total = s.B * s.NC;
   float aq = 0.f, ak = 0.f;
-  for (int bc = slice; bc < s.B * s.NC; bc += 8) {
-    const long at = ((long)bc * s.H + h) * NT + n;
-    aq += o.qb_part[at];
-    ak += o.kb_part[at];
+  for (int bc0 = slice; bc0 < total; bc0 += 32 * 8) {
+    float q8[8], k8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int bc = bc0 + 32 * i;
+      const long at = ((long)min(bc, total - 1) * s.H + h) * NT + n;
+      q8[i] = bc < total ? o.qb_part[at] : 0.f;
+      k8[i] = bc < total ? o.kb_part[at] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      aq += q8[i];
+      ak += k8[i];
+    }
   }
-  part[0][slice][n] = aq;
-  part[1][slice][n] = ak;
+  part[0][slice][col] = aq;
+  part[1][slice][col] = ak;
   __syncthreads();
   if (slice == 0 && n < s.N) {
     float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sq += part[0][i][n];
-      sk += part[1][i][n];
+    for (int i = 0; i < 32; ++i) {
+      sq += part[0][i][col];
+      sk += part[1][i][col];
     }
     d_qb[(long)h * s.N + n] = sq;
     d_kb[(long)h * s.N + n] = sk;

@@ -40,7 +40,9 @@ struct GradOut {
 constexpr size_t kWalkLds = (size_t)(C * LQ + C * LV + C * LA + AM + 384) * sizeof(float);
 constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
 constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1352) * sizeof(float);
-// finish_kernel: [H][AM] + [C][A + 1] + [C][H + 1] floats, at most this.
+// finish_kernel: blocks per (b, chunk); [H][AM] + [C][A + 1] + [C][H + 1]
+// floats of LDS, at most this.
+constexpr int kFinishParts = 8;
 constexpr int kMaxHeads = 128;
 constexpr size_t kFinishLdsMax =
     (size_t)(kMaxHeads * AM + C * (AM + 1) + C * (kMaxHeads + 1)) * sizeof(float);
