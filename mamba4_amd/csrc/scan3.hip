@@ -1662,6 +1662,21 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   const int part = blockIdx.x % kFinishParts, bc = blockIdx.x / kFinishParts;
   const int b = bc / s.NC, c = bc % s.NC, tid = tix();
   const int t0 = TPB * part, rows = max(0, min(TPB, s.T - c * C - t0));
+  const long tp = (long)s.NC * C;
+  // The row gradients first: their group sums read no LDS, so their loads
+  // are in flight with the staging loads below.
+#pragma unroll 8
+  for (int e = tid; e < rows * s.N; e += 256) {
+    const int t = t0 + e / s.N, n = e % s.N, tt = c * C + t;
+    float ac = 0.f, ab = 0.f;
+    for (int g = 0; g < groups; ++g) {
+      const long at = (((long)g * s.B + b) * tp + tt) * NT + n;
+      ac += o.dc_part[at];
+      ab += o.db_part[at];
+    }
+    d_c[tok_index(s, b, tt) * s.N + n] = ac;
+    d_b[tok_index(s, b, tt) * s.N + n] = ab;
+  }
   for (int e = tid; e < rows * s.A; e += 256) {
     const int t = t0 + e / s.A, j = e % s.A;
     angs[t * (s.A + 1) + j] = ang[tok_index(s, b, c * C + t) * s.A + j];
@@ -1675,7 +1690,6 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     suf[h * AM + j] = o.D[phase_offset(s, b, h, c) + j];
   }
   __syncthreads();
-  const long tp = (long)s.NC * C;
 #pragma unroll 4
   for (int e = tid; e < rows * s.H; e += 256) {
     const int t = t0 + e / s.H, h = e % s.H, tt = c * C + t;
@@ -1695,18 +1709,6 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dts[t * (s.H + 1) + h];
     d_angles[tok_index(s, b, tt) * s.A + j] = acc;
   }
-#pragma unroll 8
-  for (int e = tid; e < rows * s.N; e += 256) {
-    const int t = t0 + e / s.N, n = e % s.N, tt = c * C + t;
-    float ac = 0.f, ab = 0.f;
-    for (int g = 0; g < groups; ++g) {
-      const long at = (((long)g * s.B + b) * tp + tt) * NT + n;
-      ac += o.dc_part[at];
-      ab += o.db_part[at];
-    }
-    d_c[tok_index(s, b, tt) * s.N + n] = ac;
-    d_b[tok_index(s, b, tt) * s.N + n] = ab;
-  }
 }
 
 // Phase-gradient totals of the chunks after each chunk: o.D[b,h,c,j] becomes
@@ -1719,10 +1721,17 @@ __global__ __launch_bounds__(256) void suffix_kernel(Shape s, GradOut o) {
   const long bh = id / s.A;
   float* d = o.D + bh * s.NC * AM + j;
   float acc = 0.f;
-  for (int c = s.NC - 1; c >= 0; --c) {
-    const float v = d[(long)c * AM];
-    d[(long)c * AM] = acc;
-    acc += v;
+  // Eight chunks' totals are read before any is overwritten, so their loads
+  // are in flight together.
+  for (int c1 = s.NC; c1 > 0; c1 -= 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = c1 - 1 - i >= 0 ? d[(long)(c1 - 1 - i) * AM] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (c1 - 1 - i >= 0) d[(long)(c1 - 1 - i) * AM] = acc;
+      acc += v[i];
+    }
   }
 }
 
