@@ -1653,8 +1653,8 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
                                                      float* d_dt, float* d_trap,
                                                      float* d_angles) {
   extern __shared__ float sm[];
-  float* suf = sm;                    // [H][AM] phase gradient from later chunks
-  float* angs = suf + s.H * AM;       // [C][A + 1] the chunk's angle rates
+  float* suf = sm;                    // [H][LA] phase gradient from later chunks
+  float* angs = suf + s.H * LA;       // [C][A + 1] the chunk's angle rates
   float* dts = angs + C * (s.A + 1);  // [C][H + 1] the chunk's dt
   // kFinishParts blocks per (b, chunk), each taking C / kFinishParts of its
   // tokens.
@@ -1687,7 +1687,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   }
   for (int e = tid; e < s.H * s.A; e += 256) {
     const int h = e / s.A, j = e % s.A;
-    suf[h * AM + j] = o.D[phase_offset(s, b, h, c) + j];
+    suf[h * LA + j] = o.D[phase_offset(s, b, h, c) + j];
   }
   __syncthreads();
 #pragma unroll 4
@@ -1697,7 +1697,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     const float d = dts[t * (s.H + 1) + h], sig = 1.f / (1.f + expf(-trap[i]));
     const float dg = o.dgam[i], dprev = tt > 0 ? o.dscale[i - s.H] : 0.f;
     float carried = 0.f;
-    for (int j = 0; j < s.A; ++j) carried += suf[h * AM + j] * angs[t * (s.A + 1) + j];
+    for (int j = 0; j < s.A; ++j) carried += suf[h * LA + j] * angs[t * (s.A + 1) + j];
     d_dt[i] = dg * sig + dprev * (1.f - sig) + o.ddt_loc[i] + carried;
     d_trap[i] = (dg - dprev) * d * sig * (1.f - sig);
   }
@@ -1706,7 +1706,7 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     const int t = t0 + e / s.A, j = e % s.A, tt = c * C + t;
     float acc = 0.f;
     for (int g = 0; g < groups; ++g) acc += o.dang_part[(((long)g * s.B + b) * tp + tt) * AM + j];
-    for (int h = 0; h < s.H; ++h) acc += suf[h * AM + j] * dts[t * (s.H + 1) + h];
+    for (int h = 0; h < s.H; ++h) acc += suf[h * LA + j] * dts[t * (s.H + 1) + h];
     d_angles[tok_index(s, b, tt) * s.A + j] = acc;
   }
 }

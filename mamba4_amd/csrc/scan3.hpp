@@ -40,14 +40,14 @@ struct GradOut {
 constexpr size_t kWalkLds = (size_t)(C * LQ + C * LV + C * LA + AM + 384) * sizeof(float);
 constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
 constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1352) * sizeof(float);
-// finish_kernel: blocks per (b, chunk); [H][AM] + [C][A + 1] + [C][H + 1]
+// finish_kernel: blocks per (b, chunk); [H][LA] + [C][A + 1] + [C][H + 1]
 // floats of LDS, at most this.
 constexpr int kFinishParts = 8;
 constexpr int kMaxHeads = 128;
 constexpr size_t kFinishLdsMax =
-    (size_t)(kMaxHeads * AM + C * (AM + 1) + C * (kMaxHeads + 1)) * sizeof(float);
+    (size_t)(kMaxHeads * LA + C * (AM + 1) + C * (kMaxHeads + 1)) * sizeof(float);
 inline size_t finish_lds(int H, int A) {
-  return (size_t)(H * AM + C * (A + 1) + C * (H + 1)) * sizeof(float);
+  return (size_t)(H * LA + C * (A + 1) + C * (H + 1)) * sizeof(float);
 }
 
 // In: the model dtype of the rows, values and their cotangents (float, or
