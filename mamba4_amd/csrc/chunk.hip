@@ -607,10 +607,11 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       f4 gk[2], hv[2];
       zero2(gk);
       zero2(hv);
+      if (hf == 0) rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
       tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // G^T k_s
       if (hf == 1) fetch_phase4();
       tile_mma_half<false, true, true>(gk, Kt, M1, 64, ws, hf);  // + G k_s
-      rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
+      if (hf == 1) rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
       float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
