@@ -1144,7 +1144,7 @@ int m3_forward_impl(const char* entry, const In* c, const In* b, const In* x, co
   const auto walk = v4 ? m3::walk_kernel<false, In, true> : m3::walk_kernel<false, In, false>;
   const auto out = v4 ? m3::out_kernel<In, true> : m3::out_kernel<In, false>;
   int rc = launch("m3_walk", st, [&] {
-    hipLaunchKernelGGL(walk, dim3(B * H), dim3(512), m3::kWalkLds, st, s, b, k_bias, x, adt, dt,
+    hipLaunchKernelGGL(walk, dim3(2 * B * H), dim3(256), m3::kWalkLds, st, s, b, k_bias, x, adt, dt,
                        trap_logits, angles, phases, starts, nullptr, final_state);
   });
   if (rc) return rc;
@@ -1191,7 +1191,7 @@ int m3_backward_impl(const char* entry, const In* c, const In* b, const In* x, c
   const auto walk = v4 ? m3::walk_kernel<true, In, true> : m3::walk_kernel<true, In, false>;
   const auto grad = v4 ? m3::grad_kernel<In, true> : m3::grad_kernel<In, false>;
   int rc = launch("m3_walk_bwd", st, [&] {
-    hipLaunchKernelGGL(walk, dim3(B * H), dim3(512), m3::kWalkLds, st, s, c, q_bias, d_y, adt, dt,
+    hipLaunchKernelGGL(walk, dim3(2 * B * H), dim3(256), m3::kWalkLds, st, s, c, q_bias, d_y, adt, dt,
                        trap_logits, angles, const_cast<float*>(phases), ws.dh1, d_final,
                        nullptr);
   });

@@ -900,9 +900,20 @@ __device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], TT* dst
 // e^p; S starts at d_final and the chunks run in reverse; each stores S (the
 // cotangent of the state at the chunk's end) to `saved`, then
 // S <- e^{p_L} S + Q^T (e^p dy).
-// LDS: rows [C][LQ], vals [C][LV], phase table [C][LA], th0 [AM], scalars.
+//
+// Rows of S are independent, so each (b, h) runs as two blocks of four
+// waves, block `half` holding state rows 64 half .. +63 (coordinate pairs,
+// and angles, 32 half .. +31): three of them share a compute unit where
+// two eight-wave blocks fit, and every compute unit carries the same work
+// (with one block per sequence a third of the units held two and set the
+// pace).  Both halves read all of a chunk's values and compute its
+// per-token scalars.
+// LDS: the half's rotated rows [C][LQH], vals [C][LV], its phase table
+// [C][LA] (columns = the half's angles), th0 [AM], scalars.
+constexpr int LQH = 64 + 4;
+
 template <bool BWD, typename In, bool V4>
-__global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, const float* bias,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void walk_kernel(Shape s, const In* rows, const float* bias,
                                                    const In* vals, const float* adt,
                                                    const float* dt, const float* trap,
                                                    const float* ang, float* theta0, float* saved,
@@ -910,49 +921,61 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, cons
   constexpr bool BF = is_bf16<In>::value;
   extern __shared__ float sm[];
   float* rt = sm;
-  float* vt = rt + C * LQ;
+  float* vt = rt + C * LQH;
   float* tab = vt + C * LV;
   float* th0 = tab + C * LA;
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
-  const int bh = blockIdx.x, b = bh / s.H, h = bh % s.H;
+  const int half = blockIdx.x & 1, bh = blockIdx.x >> 1, b = bh / s.H, h = bh % s.H;
+  const int n0 = 64 * half, j0 = 32 * half;   // first state row and angle of the half
+  const int na = max(0, min(32, s.A - j0));  // the half's angles
   const int tid = tix(), w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
 
-  // Eight waves: wave w holds state rows 16 w .. 16 w + 15 as four 16-column
+  // Four waves: wave w holds state rows n0 + 16 w .. +15 as four 16-column
   // tiles.
-  f4 acc[1][4];
+  f4 acc[4];
 #pragma unroll
-  for (int rt2 = 0; rt2 < 1; ++rt2) {
+  for (int j = 0; j < 4; ++j) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int n = 16 * w + 4 * q + i, p = 16 * j + r;
-        float v = 0.f;
-        if (BWD && init && n < s.N && p < s.P) v = init[(((long)b * s.H + h) * s.N + n) * s.P + p];
-        acc[rt2][j][i] = v;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + 16 * w + 4 * q + i, p = 16 * j + r;
+      float v = 0.f;
+      if (BWD && init && n < s.N && p < s.P) v = init[(((long)b * s.H + h) * s.N + n) * s.P + p];
+      acc[j][i] = v;
     }
   }
   if (!BWD && tid < AM) th0[tid] = 0.f;
-  const bool col = 2 * l < s.N;
-  const float2 bs = fetch_bias_pair(s, bias + (long)h * s.N);
+  // This lane's coordinate pair (32 per half, two tokens per wave step).
+  const int pr = l & 31, n = n0 + 2 * pr;
+  const bool col = n < s.N;
+  const float2 bs = raw2(rsrc(bias + (long)h * s.N, 4L * s.N), col ? n * 4 : kNoLoad, bias);
 
   // Every global input of a chunk is fetched into registers one chunk ahead,
   // while the previous chunk's product runs.
   TokenIn tin;
   float rates[8], th_in = 0.f;
   typename Raw<In>::Pair u[8];
-  typename Raw<In>::Quad v[2];
+  typename Raw<In>::Quad v[4];
   auto fetch = [&](int c) {
     tin = fetch_token(s, adt, dt, trap, b, h, c);
-    fetch_angle_block(s, ang, b, c, rates);
-    if (BWD) th_in = fetch_phase(s, theta0, b, h, c);
+    {
+      // The half's angle rates of the chunk's tokens: [t][j0 + j'], j' < na.
+      const Rsrc ra = chunk_rsrc(s, ang, b, c, s.A);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = tid + 256 * k, t = e >> 5, jj = e & 31;
+        rates[k] = ldb(ra, jj < na ? (t * s.A + j0 + jj) * 4 : kNoLoad);
+      }
+    }
+    if (BWD)
+      th_in = ldb(rsrc(theta0 + phase_offset(s, b, h, c) + j0, 4L * na), tid < 64 ? tid * 4 : kNoLoad);
     const Rsrc rr = chunk_rsrc(s, rows, b, c, s.N);
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
-      u[m] = raw2(rr, col ? ((w + 8 * m) * s.N + 2 * l) * sizeof(In) : kNoLoad, rows);
-    fetch_values<512, V4>(s, vals, b, c, h, v);
+    for (int m = 0; m < 8; ++m) {
+      const int t = 2 * (w + 4 * m) + (l >> 5);
+      u[m] = raw2(rr, col ? (t * s.N + n) * sizeof(In) : kNoLoad, rows);
+    }
+    fetch_values<256, V4>(s, vals, b, c, h, v);
   };
   fetch(BWD ? s.NC - 1 : 0);
 
@@ -960,33 +983,53 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, cons
     const int c = BWD ? s.NC - 1 - step : step;
     __syncthreads();  // the previous chunk's reads of the LDS tiles are done
     if (w == 0) token_scalars(tin, S);
-    stage_angles(s, rates, tab);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = tid + 256 * k;
+      tab[(e >> 5) * LA + (e & 31)] = rates[k];
+    }
     if (BWD) {
-      if (tid < s.A) th0[tid] = th_in;
+      if (tid < na) th0[tid] = th_in;
     } else {
-      // Lanes at or past A store out of the resource's range (dropped).
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(th0[tid & (AM - 1)]),
-                                            rsrc(theta0 + phase_offset(s, b, h, c), 4L * s.A),
-                                            tid * 4, 0, 0);
+      // Lanes at or past the half's angles store out of range (dropped).
+      __builtin_amdgcn_raw_buffer_store_b32(
+          __float_as_uint(th0[tid & (AM - 1)]),
+          rsrc(theta0 + phase_offset(s, b, h, c) + j0, 4L * na), tid * 4, 0, 0);
     }
     __syncthreads();
-    phase_table_staged<8>(s, S.dt, th0, tab, !BWD);
+    // The half's phase table: angles j' = w + 4 m, one token per lane.
+    {
+      const float d = S.dt[l];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int jj = w + 4 * m;
+        if (jj >= na) break;
+        const float incl = wave_scan(tab[l * LA + jj] * d);
+        const float base = th0[jj];
+        tab[l * LA + jj] = base + incl;
+        if (!BWD) {
+          __builtin_amdgcn_wave_barrier();
+          if (l == 63) th0[jj] = reduce_turns(base + incl);
+        }
+      }
+    }
     __syncthreads();
-    // Rotated rows (one pair per lane) and scaled values into LDS.
+    // Rotated rows (one pair per lane, two tokens per step) and scaled
+    // values into LDS.
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      const int t = w + 8 * m, tt = c * C + t;
+      const int t = 2 * (w + 4 * m) + (l >> 5), tt = c * C + t;
       const bool valid = col && tt < s.T;
       float sn = 0.f, cs = 1.f;
-      if (valid && l < s.A) sin_cos(tab[t * LA + l], &sn, &cs);
+      if (valid && pr < na) sin_cos(tab[t * LA + pr], &sn, &cs);
       // The bias-added row in the model dtype, then rotated in float32 (:582-585).
       const float2 um = dec(u[m]);
       const float2 x2 = round_bf2<BF>(valid ? float2{um.x + bs.x, um.y + bs.y}
                                             : float2{0.f, 0.f});
-      *reinterpret_cast<float2*>(rt + t * LQ + 2 * l) =
+      *reinterpret_cast<float2*>(rt + t * LQH + 2 * pr) =
           float2{x2.x * cs - x2.y * sn, x2.x * sn + x2.y * cs};
     }
-    store_values<512>(v, BWD ? S.ep : S.u, vt);
+    store_values<256>(v, BWD ? S.ep : S.u, vt);
     // The next chunk's inputs (this chunk's again after the last: every
     // iteration issues the same loads), then this chunk's state (a lane's
     // four rows of one column).
@@ -995,22 +1038,22 @@ __global__ __launch_bounds__(512) void walk_kernel(Shape s, const In* rows, cons
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) out[(16 * w + 4 * q + i) * PT + 16 * j + r] = acc[0][j][i];
+      for (int i = 0; i < 4; ++i) out[(n0 + 16 * w + 4 * q + i) * PT + 16 * j + r] = acc[j][i];
     __syncthreads();
     const float decay = expf(S.p[63]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[0][j] *= decay;
-    // rows^T vals: A(n, t) = rt[t * LQ + n], B(t, p) = vt[t * LV + p].
-    mma<4, 1, LQ, LV, 1, BF>(acc[0], rt, 16 * w, vt, 0, 0, C);
+    for (int j = 0; j < 4; ++j) acc[j] *= decay;
+    // rows^T vals: A(n, t) = rt[t * LQH + n], B(t, p) = vt[t * LV + p].
+    mma<4, 1, LQH, LV, 1, BF>(acc, rt, 16 * w, vt, 0, 0, C);
   }
   if (!BWD && final_state) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int n = 16 * w + 4 * q + i, p = 16 * j + r;
-        if (n < s.N && p < s.P)
-          final_state[(((long)b * s.H + h) * s.N + n) * s.P + p] = acc[0][j][i];
+        const int nn = n0 + 16 * w + 4 * q + i, p = 16 * j + r;
+        if (nn < s.N && p < s.P)
+          final_state[(((long)b * s.H + h) * s.N + nn) * s.P + p] = acc[j][i];
       }
   }
 }

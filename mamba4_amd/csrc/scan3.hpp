@@ -37,7 +37,7 @@ struct GradOut {
 };
 
 // LDS bytes of each kernel.
-constexpr size_t kWalkLds = (size_t)(C * LQ + C * LV + C * LA + AM + 384) * sizeof(float);
+constexpr size_t kWalkLds = (size_t)(C * (64 + 4) + C * LV + C * LA + AM + 384) * sizeof(float);
 constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
 constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1352) * sizeof(float);
 // finish_kernel: blocks per (b, chunk); [H][LA] + [C][A + 1] + [C][H + 1]
