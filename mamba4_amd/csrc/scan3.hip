@@ -913,11 +913,10 @@ __device__ __forceinline__ void store_state_t(const f4 (&v)[2048 / NTH], TT* dst
 constexpr int LQH = 64 + 4;
 
 template <bool BWD, typename In, bool V4>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void walk_kernel(Shape s, const In* rows, const float* bias,
-                                                   const In* vals, const float* adt,
-                                                   const float* dt, const float* trap,
-                                                   const float* ang, float* theta0, float* saved,
-                                                   const float* init, float* final_state) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void walk_kernel(
+    Shape s, const In* rows, const float* bias, const In* vals, const float* adt, const float* dt,
+    const float* trap, const float* ang, float* theta0, float* saved, const float* init,
+    float* final_state) {
   constexpr bool BF = is_bf16<In>::value;
   extern __shared__ float sm[];
   float* rt = sm;
@@ -926,7 +925,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
   float* th0 = tab + C * LA;
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
-  const int half = blockIdx.x & 1, bh = blockIdx.x >> 1, b = bh / s.H, h = bh % s.H;
+  // Both halves of a sequence on one XCD (blocks go round-robin over the
+  // eight), so the second half's value reads hit that XCD's L2.
+  const int G = 2 * s.B * s.H, x = blockIdx.x;
+  int half, bh;
+  if (x < (G & ~15)) {
+    const int slot = x >> 3;
+    half = slot & 1;
+    bh = (slot >> 1) * 8 + (x & 7);
+  } else {
+    half = x & 1;
+    bh = x >> 1;
+  }
+  const int b = bh / s.H, h = bh % s.H;
   const int n0 = 64 * half, j0 = 32 * half;   // first state row and angle of the half
   const int na = max(0, min(32, s.A - j0));  // the half's angles
   const int tid = tix(), w = tid >> 6, l = lane_id(), r = l & 15, q = l >> 4;
@@ -982,6 +993,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
   for (int step = 0; step < s.NC; ++step) {
     const int c = BWD ? s.NC - 1 - step : step;
     __syncthreads();  // the previous chunk's reads of the LDS tiles are done
+    // This chunk's state (a lane's four rows of one column), stored by waves
+    // 1-3 while wave 0 turns the token inputs into the chunk's scalars.
+    float* out = saved + state_offset(s, b, h, c);
+    if (w != 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[(n0 + 16 * w + 4 * q + i) * PT + 16 * j + r] = acc[j][i];
+    }
     if (w == 0) token_scalars(tin, S);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -997,19 +1017,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
           rsrc(theta0 + phase_offset(s, b, h, c) + j0, 4L * na), tid * 4, 0, 0);
     }
     __syncthreads();
-    // The half's phase table: angles j' = w + 4 m, one token per lane.
+    // The half's phase table: angles j' = w + 4 m, one token per lane; the
+    // eight scans of a wave are independent and run interleaved (every read
+    // of th0 comes before lane 63's writes).
     {
       const float d = S.dt[l];
+      float x[8], base[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        x[m] = tab[l * LA + w + 4 * m] * d;
+        base[m] = th0[w + 4 * m];
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) x[m] = base[m] + wave_scan(x[m]);
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int jj = w + 4 * m;
-        if (jj >= na) break;
-        const float incl = wave_scan(tab[l * LA + jj] * d);
-        const float base = th0[jj];
-        tab[l * LA + jj] = base + incl;
-        if (!BWD) {
-          __builtin_amdgcn_wave_barrier();
-          if (l == 63) th0[jj] = reduce_turns(base + incl);
+        if (jj < na) {
+          tab[l * LA + jj] = x[m];
+          if (!BWD && l == 63) th0[jj] = reduce_turns(x[m]);
         }
       }
     }
@@ -1031,14 +1058,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
     }
     store_values<256>(v, BWD ? S.ep : S.u, vt);
     // The next chunk's inputs (this chunk's again after the last: every
-    // iteration issues the same loads), then this chunk's state (a lane's
-    // four rows of one column).
+    // iteration issues the same loads), then wave 0's rows of the state.
     fetch(step + 1 < s.NC ? (BWD ? c - 1 : c + 1) : c);
-    float* out = saved + state_offset(s, b, h, c);
+    if (w == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) out[(n0 + 16 * w + 4 * q + i) * PT + 16 * j + r] = acc[j][i];
+        for (int i = 0; i < 4; ++i) out[(n0 + 16 * w + 4 * q + i) * PT + 16 * j + r] = acc[j][i];
+    }
     __syncthreads();
     const float decay = expf(S.p[63]);
 #pragma unroll
