@@ -10,6 +10,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/mamba3_scan.h"
@@ -169,7 +170,7 @@ int configure() {
              {(const void*)m3::grad_kernel<float, true>, m3::kGradLds},
              {(const void*)m3::walk_kernel<false, m3::bf16_t, true>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true, m3::bf16_t, true>, m3::kWalkLds},
-             {(const void*)m3::out_kernel<m3::bf16_t, true>, m3::kOutLds},
+             {(const void*)m3::out_kernel<m3::bf16_t, true>, m3::kOutLdsBf16},
              {(const void*)m3::grad_kernel<m3::bf16_t, true>, m3::kGradLds},
              {(const void*)m3::walk_kernel<false, float, false>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true, float, false>, m3::kWalkLds},
@@ -177,7 +178,7 @@ int configure() {
              {(const void*)m3::grad_kernel<float, false>, m3::kGradLds},
              {(const void*)m3::walk_kernel<false, m3::bf16_t, false>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true, m3::bf16_t, false>, m3::kWalkLds},
-             {(const void*)m3::out_kernel<m3::bf16_t, false>, m3::kOutLds},
+             {(const void*)m3::out_kernel<m3::bf16_t, false>, m3::kOutLdsBf16},
              {(const void*)m3::grad_kernel<m3::bf16_t, false>, m3::kGradLds},
              {(const void*)m3::finish_kernel, m3::kFinishLdsMax}};
   for (auto& k : big) {
@@ -1148,10 +1149,12 @@ int m3_forward_impl(const char* entry, const In* c, const In* b, const In* x, co
                        trap_logits, angles, phases, starts, nullptr, final_state);
   });
   if (rc) return rc;
+  // bfloat16 tiles: two blocks per compute unit.
+  const bool bf = std::is_same<In, m3::bf16_t>::value;
   return launch("m3_out", st, [&] {
-    hipLaunchKernelGGL(out, dim3(persistent_grid(B * s.NC * H, 1)), dim3(512), m3::kOutLds, st,
-                       s, c, b, x, adt, dt, trap_logits, angles, q_bias, k_bias, phases, starts,
-                       y);
+    hipLaunchKernelGGL(out, dim3(persistent_grid(B * s.NC * H, bf ? 2 : 1)), dim3(512),
+                       bf ? m3::kOutLdsBf16 : m3::kOutLds, st, s, c, b, x, adt, dt, trap_logits,
+                       angles, q_bias, k_bias, phases, starts, y);
   });
 }
 

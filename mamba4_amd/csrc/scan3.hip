@@ -1104,8 +1104,10 @@ __device__ __forceinline__ int xcd_item(int it, int total) {
 // ---------------------------------------------------------------------------
 // Output of each (b, chunk, h) item: y = (S o W) V + diag(e^p) Q S0 with scores
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
-// LDS: Q [C][LQ], K [C][LQ] (later S o W as [C][LV]), H0 transposed
-// [PT][LQ] (first the phase table), V transposed [PT][LV], scalars.
+// LDS: Q [C][LQt], K [C][LQt] (later S o W as [C][LVt]), H0 transposed
+// [PT][LQt] (first the phase table), V transposed [PT][LVt], scalars.  With
+// bfloat16 tiles that is 62 KB, and two blocks share a compute unit (float32:
+// 122 KB, one block).
 template <typename In, bool V4>
 __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const In* bk,
                                                   const In* x, const float* adt,
@@ -1118,15 +1120,13 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
   typedef typename Tile<BF>::T TT;
   constexpr int LQt = Tile<BF>::LQt, LVt = Tile<BF>::LVt;
   extern __shared__ float sm[];
-  float* const kf = sm + C * LQ;
-  float* const h0f = kf + C * LQ;
-  float* const vf = h0f + NT * LV;
   TT* const qt = reinterpret_cast<TT*>(sm);
-  TT* const kt = reinterpret_cast<TT*>(kf);
-  TT* const h0 = reinterpret_cast<TT*>(h0f);
-  TT* const vt = reinterpret_cast<TT*>(vf);
-  float* tab = h0f;
-  float* th0 = vf + C * LV;
+  TT* const kt = qt + C * LQt;
+  TT* const h0 = kt + C * LQt;
+  // H0's region also holds the float32 phase table, [C][LA].
+  TT* const vt = h0 + (BF ? PT * LQt : NT * LV);
+  float* tab = reinterpret_cast<float*>(h0);
+  float* th0 = reinterpret_cast<float*>(vt + PT * LVt);
   float* sc = th0 + AM;
   const Scalars S{sc, sc + 64, sc + 128, sc + 192, sc + 256, sc + 320};
   const int total = s.B * s.NC * s.H;

@@ -39,6 +39,12 @@ struct GradOut {
 // LDS bytes of each kernel.
 constexpr size_t kWalkLds = (size_t)(C * (64 + 4) + C * LV + C * LA + AM + 384) * sizeof(float);
 constexpr size_t kOutLds = (size_t)(2 * C * LQ + NT * LV + C * LV + AM + 384) * sizeof(float);
+// out_kernel with bfloat16 tiles: Q, K, H0 [.][NT + 8] and V [PT][PT + 8] in
+// bfloat16 (the phase table, C * (AM + 1) floats, fits in H0's tile).
+constexpr size_t kOutLdsBf16 =
+    (size_t)(3 * C * (NT + 8) + PT * (PT + 8)) * 2 + (size_t)(AM + 384) * sizeof(float);
+static_assert((size_t)C * (NT + 8) * 2 >= (size_t)C * (AM + 1) * sizeof(float),
+              "the phase table fits in H0's bfloat16 tile");
 constexpr size_t kGradLds = (size_t)(4 * NT * LV + C * LA + AM + 1352) * sizeof(float);
 // finish_kernel: blocks per (b, chunk); [H][LA] + [C][A + 1] + [C][H + 1]
 // floats of LDS, at most this.
