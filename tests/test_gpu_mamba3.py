@@ -96,7 +96,8 @@ def test_reference_test_shapes(gpu_lib, length):
 @pytest.mark.parametrize(
     "batch,length,heads,dim,width,angles",
     [(2, 64, 3, 16, 8, 4), (2, 65, 3, 16, 8, 4), (1, 130, 5, 32, 16, 8), (2, 100, 3, 16, 8, 0),
-     (1, 200, 2, 128, 64, 32), (3, 129, 7, 64, 33, 32), (1, 70, 128, 16, 8, 4)],
+     (1, 200, 2, 128, 64, 32), (3, 129, 7, 64, 33, 32), (1, 70, 128, 16, 8, 4),
+     (2, 90, 6, 128, 64, 64)],
 )
 def test_matches_oracle(gpu_lib, batch, length, heads, dim, width, angles):
     from gpu_helpers import announce
