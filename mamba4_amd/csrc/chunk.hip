@@ -49,6 +49,13 @@ struct TokenRows {
   }
 };
 
+// A chunk's `rows` token rows into a RowTile (consecutive tokens are H rows
+// of `width` apart).
+template <typename T, int NTH>
+__device__ __forceinline__ void fetch_tokens(RowTile<T, NTH>& R, int rows, const TokenRows<T>& tr) {
+  R.fetch_tokens(rows, tr(0), (unsigned)(tr.d.H * tr.width));
+}
+
 template <typename T>
 __device__ __forceinline__ TokenRows<T> rows_of(const T* base, const Dims& d, const SeqIndex& si) {
   return TokenRows<T>{base, d, si.b, si.h, si.n * d.chunk, 64, 0};
@@ -95,7 +102,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
-  TileRegs ry, rk, rv, rq;
+  RowTile<float> ry;
+  RowTile<In> rk, rv, rq;
   TileRegsT rc;
   // MIX key rows: the raw source row of each position (the zero row of
   // position 0 reads its query row and is zeroed at staging).
@@ -107,20 +115,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return p ? p : mix.query + token_head(d, s.b, t, s.h) * 64;
       });
     } else {
-      rk.fetch_rows(s.len, rows_of(keys, d, s));
+      fetch_tokens(rk, s.len, rows_of(keys, d, s));
     }
   };
   auto fetch_queries = [&](const SeqIndex& s) {
     if constexpr (MIX)
       rq.fetch_rows(s.len, rows_of(mix.query, d, s));
     else
-      rq.fetch_rows(s.len, rows_of(queries, d, s));
+      fetch_tokens(rq, s.len, rows_of(queries, d, s));
   };
-  ry.fetch_rows(si.len, rows_of(solved, d, si));
+  // The chunk's log decays and betas, lane s of wave 0 holding token s's
+  // (the other lanes read out of range), fetched with its first tiles.
+  float sg, sb;
+  auto fetch_scalars = [&](const SeqIndex& s) {
+    const unsigned st = (unsigned)d.H * 4, bytes = (unsigned)(s.len - 1) * st + 4;
+    const long th = token_head(d, s.b, s.n * d.chunk, s.h);
+    const unsigned off = threadIdx.x < 64 ? threadIdx.x * st : kNoRow;
+    sg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
+    sb = buf_load1(buf_rsrc(beta + th, bytes), off);
+  };
+  fetch_tokens(ry, si.len, rows_of(solved, d, si));
+  fetch_scalars(si);
   fetch_keys(si);
   rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   fetch_queries(si);
-  rv.fetch_rows(si.len, value_rows(values, d, si, 0));
+  fetch_tokens(rv, si.len, value_rows(values, d, si, 0));
 
   for (;;) {
     ry.store(Y);
@@ -129,25 +148,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     else
       rk.store(K);
     rc.store(C0);
-    load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
+    if (threadIdx.x < 64) finish_chunk_scalars(cs, sg, sb);
     __syncthreads();
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
+    // The last chunk of a block fetches its own inputs again (unused): every
+    // chunk issues the same loads, so each wait counts exactly.
     const SeqIndex sn = seq_at(d, more ? next : seq);
-    if (more) {
-      ry.fetch_rows(sn.len, rows_of(solved, d, sn));
-      fetch_keys(sn);
-      // With more than one value tile, rc carries this chunk's later tiles
-      // and prefetches after the last of them.
-      if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
-    }
+    fetch_tokens(ry, sn.len, rows_of(solved, d, sn));
+    fetch_scalars(sn);
+    fetch_keys(sn);
+    // With more than one value tile, rc carries this chunk's later tiles and
+    // prefetches after the last of them.
+    if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
 
     // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
     // the 16 lanes that hold the rest of each row.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = (threadIdx.x >> 4) + 16 * j;
-      const f4 qt = MIX ? mix_unit(rq.v[j]) : rq.v[j];
+      const f4 qt = MIX ? mix_unit(rq.get(j)) : rq.get(j);
       const f4 prod = qt * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
       const float v = row16_sum(prod[0] + prod[1] + prod[2] + prod[3]);
       if ((threadIdx.x & 15) == 0 && t < si.len)
@@ -155,7 +175,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if constexpr (MIX)
         if ((threadIdx.x & 15) == 0) var_s[t] = v;
     }
-    if (more) fetch_queries(sn);
+    fetch_queries(sn);
 
     f4 acc[4];
     zero4(acc);
@@ -174,7 +194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (v > 0) {
         // Value tile v and cross tile v replace tile v - 1 once every wave
         // has read it.
-        rv.fetch_rows(si.len, value_rows(values, d, si, v));
+        fetch_tokens(rv, si.len, value_rows(values, d, si, v));
         rc.fetch_matrix(cross_tile(start_c, d, si.seq, v));
         __syncthreads();
         rc.store(C0);
@@ -183,8 +203,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       rv.store(K);
       __syncthreads();
-      if (more && v == d.NV - 1) {
-        rv.fetch_rows(sn.len, value_rows(values, d, sn, 0));
+      if (v == d.NV - 1) {
+        fetch_tokens(rv, sn.len, value_rows(values, d, sn, 0));
         if (d.NV > 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
       }
 
@@ -246,25 +266,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
 
-  TileRegs rd, rv, rk, rc;
-  // Queries and d_variance of this lane's accumulator rows (read in the epilogue).
-  f4 qv[4];
+  RowTile<float> rd;
+  RowTile<In> rv, rk;
+  TileRegs rc;
+  // Queries and d_variance of this lane's accumulator rows (read in the
+  // epilogue; zero past the chunk).
+  RowQuad<In> qv[4];
   float dvar[4];
   auto fetch_rows_q = [&](const SeqIndex& s) {
+    const long th = token_head(d, s.b, s.n * d.chunk, s.h);
+    const unsigned st = (unsigned)d.H * 64;
+    const In* qsrc;
+    if constexpr (MIX)
+      qsrc = mix.query;
+    else
+      qsrc = queries;
+    const BufRsrc rq = buf_rsrc(qsrc + th * 64, ((unsigned)(s.len - 1) * st + 64) * sizeof(In));
+    const BufRsrc rv2 = buf_rsrc(d_variance + th, ((unsigned)(s.len - 1) * d.H + 1) * 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int t = acc_row(w, q);
-      qv[q] = f4{0.f, 0.f, 0.f, 0.f};
-      dvar[q] = 0.f;
-      if (t < s.len) {
-        const long th = token_head(d, s.b, s.n * d.chunk + t, s.h);
-        if constexpr (MIX)
-          qv[q] = load4(mix.query + th * 64 + c4);
-        else
-          qv[q] = load4(queries + th * 64 + c4);
-        dvar[q] = d_variance[th];
-      }
+      const unsigned t = acc_row(w, q);
+      qv[q].load(rq, (t * st + c4) * sizeof(In));
+      dvar[q] = buf_load1(rv2, t * d.H * 4);
     }
+  };
+  // The chunk's log decays and betas (lane s of wave 0: token s; the other
+  // lanes read out of range), fetched with its first tiles.
+  float sg, sb;
+  auto fetch_scalars = [&](const SeqIndex& s) {
+    const unsigned st = (unsigned)d.H * 4, bytes = (unsigned)(s.len - 1) * st + 4;
+    const long th = token_head(d, s.b, s.n * d.chunk, s.h);
+    const unsigned off = threadIdx.x < 64 ? threadIdx.x * st : kNoRow;
+    sg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
+    sb = buf_load1(buf_rsrc(beta + th, bytes), off);
   };
   auto fetch_keys = [&](const SeqIndex& s) {
     if constexpr (MIX) {
@@ -274,11 +308,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return p ? p : mix.query + token_head(d, s.b, t, s.h) * 64;
       });
     } else {
-      rk.fetch_rows(s.len, rows_of(keys, d, s));
+      fetch_tokens(rk, s.len, rows_of(keys, d, s));
     }
   };
-  rd.fetch_rows(si.len, value_rows(d_output, d, si, 0));
-  rv.fetch_rows(si.len, value_rows(values, d, si, 0));
+  fetch_tokens(rd, si.len, value_rows(d_output, d, si, 0));
+  fetch_tokens(rv, si.len, value_rows(values, d, si, 0));
+  fetch_scalars(si);
   fetch_keys(si);
   rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   fetch_rows_q(si);
@@ -287,7 +322,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     rd.store(DO);
     rv.store(V);
     rc.store(C0);
-    load_chunk_scalars(cs, d, beta, log_decay, si.b, si.h, si.n);
+    if (threadIdx.x < 64) finish_chunk_scalars(cs, sg, sb);
     __syncthreads();
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
@@ -300,8 +335,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int v = 0; v < d.NV; ++v) {
       if (v > 0) {
         // Tile v replaces tile v - 1 once every wave has read it.
-        rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
-        rv.fetch_rows(si.len, value_rows(values, d, si, v));
+        fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
+        fetch_tokens(rv, si.len, value_rows(values, d, si, v));
         rc.fetch_matrix(cross_tile(start_c, d, si.seq, v));
         __syncthreads();
         rd.store(DO);
@@ -309,10 +344,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         rc.store(C0);
         __syncthreads();
       }
-      if (more && v == d.NV - 1) {
-        rd.fetch_rows(sn.len, value_rows(d_output, d, sn, 0));
-        rv.fetch_rows(sn.len, value_rows(values, d, sn, 0));
+      // The last chunk of a block fetches its own inputs again (unused):
+      // every chunk issues the same loads, so each wait counts exactly.
+      if (v == d.NV - 1) {
+        fetch_tokens(rd, sn.len, value_rows(d_output, d, sn, 0));
+        fetch_tokens(rv, sn.len, value_rows(values, d, sn, 0));
         rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
+        fetch_scalars(sn);
       }
       tile_mma<false, true>(acc, DO, V, 64, w);    // dout_t . v_s
       tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
@@ -332,7 +370,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     else
       rk.store(V);
     __syncthreads();
-    if (more) fetch_keys(sn);
+    fetch_keys(sn);
 
     f4 within[4];
     zero4(within);
@@ -343,7 +381,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (t < si.len) {
         const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
         const float carried = expf(cs.prefix[t]);
-        const f4 qn = MIX ? mix_unit(qv[q]) : qv[q];
+        const f4 qn = MIX ? mix_unit(qv[q].get()) : qv[q].get();
         *reinterpret_cast<f4*>(ybar + th * 64 + c4) =
             quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qn;
       }
@@ -417,39 +455,38 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
 
   // The row tiles of a chunk (keys, value tile 0, y, z, dout tile 0) in the
   // tile-fetch layout, and its log decays, betas and d_variance.
-  TileRegs2 rt[5];
+  RowTile<In, GRADS_THREADS> tk, tv;
+  RowTile<float, GRADS_THREADS> ty, tz, td;
   auto fetch_keys = [&](const SeqIndex& sx) {
     if constexpr (MIX) {
-      rt[0].fetch_rows(sx.len, [&](int r) -> const float* {
+      tk.fetch_rows(sx.len, [&](int r) -> const float* {
         const int t = sx.n * d.chunk + r;
         const float* p = mix_key_row(mix, d, sx.b, t, sx.h);
         return p ? p : mix.query + token_head(d, sx.b, t, sx.h) * 64;
       });
     } else {
-      rt[0].fetch_rows(sx.len, rows_of(keys, d, sx));
+      fetch_tokens(tk, sx.len, rows_of(keys, d, sx));
     }
   };
+  // Token tt's log decay and beta in thread tt < 64, d_variance of this
+  // thread's tile-fetch rows; zero past the chunk (out-of-range offsets).
   float pg = 0.f, pbt = 0.f, pdv[2];
   auto fetch_scalars = [&](const SeqIndex& sx) {
-    const int tt = threadIdx.x;
-    pg = 0.f;
-    pbt = 0.f;
-    if (tt < sx.len) {
-      const long th = token_head(d, sx.b, sx.n * d.chunk + tt, sx.h);
-      pg = log_decay[th];
-      pbt = beta[th];
-    }
+    const unsigned tt = threadIdx.x, st = (unsigned)d.H * 4;
+    const unsigned bytes = (unsigned)(sx.len - 1) * st + 4;
+    const long th = token_head(d, sx.b, sx.n * d.chunk, sx.h);
+    const unsigned off = tt < 64 ? tt * st : kNoRow;
+    pg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
+    pbt = buf_load1(buf_rsrc(beta + th, bytes), off);
+    const BufRsrc rv = buf_rsrc(d_variance + th, bytes);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int t = (tt >> 4) + 32 * j;
-      pdv[j] = t < sx.len ? d_variance[token_head(d, sx.b, sx.n * d.chunk + t, sx.h)] : 0.f;
-    }
+    for (int j = 0; j < 2; ++j) pdv[j] = buf_load1(rv, ((tt >> 4) + 32 * j) * st);
   };
   fetch_keys(si);
-  rt[1].fetch_rows(si.len, value_rows(values, d, si, 0));
-  rt[2].fetch_rows(si.len, rows_of(solved, d, si));
-  rt[3].fetch_rows(si.len, rows_of(z, d, si));
-  rt[4].fetch_rows(si.len, value_rows(d_output, d, si, 0));
+  fetch_tokens(tv, si.len, value_rows(values, d, si, 0));
+  fetch_tokens(ty, si.len, rows_of(solved, d, si));
+  fetch_tokens(tz, si.len, rows_of(z, d, si));
+  fetch_tokens(td, si.len, value_rows(d_output, d, si, 0));
   fetch_scalars(si);
 
   for (;;) {
@@ -468,13 +505,13 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     const float dvar[2] = {pdv[0], pdv[1]};
 
     if constexpr (MIX)
-      rt[0].store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0);
+      tk.store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0);
     else
-      rt[0].store(Kt);
-    rt[1].store(Vt);
-    rt[2].store(Yt);
-    rt[3].store(Zt);
-    rt[4].store(Dt);
+      tk.store(Kt);
+    tv.store(Vt);
+    ty.store(Yt);
+    tz.store(Zt);
+    td.store(Dt);
     if (tid < 64) finish_chunk_scalars(cs, pg, pbt);
     // The end-state cotangents of phase 3 load while phases 1 and 2 run (of H,
     // the last value tile, the one phase 3 starts from).
@@ -494,9 +531,10 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf, 0, causal_nj);
       tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
       for (int v = 1; v < d.NV; ++v) {
-        TileRegs2 rv, rd;
-        rv.fetch_rows(si.len, value_rows(values, d, si, v));
-        rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+        RowTile<In, GRADS_THREADS> rv;
+        RowTile<float, GRADS_THREADS> rd;
+        fetch_tokens(rv, si.len, value_rows(values, d, si, v));
+        fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
         __syncthreads();
         rv.store(Vt);
         rd.store(Dt);
@@ -567,8 +605,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       zero2(dv[v]);
       if (v < d.NV) {
         if (v < last) {
-          TileRegs2 rd;
-          rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+          RowTile<float, GRADS_THREADS> rd;
+          fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
           __syncthreads();
           rd.store(Dt);
           __syncthreads();
@@ -599,7 +637,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     auto fetch_phase4 = [&]() {
       rs.fetch_matrix(start_s + (bh * d.NS + (long)si.n * d.rsub) * 4096);
       rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
-      rt[2].fetch_rows(sx.len, rows_of(solved, d, sx));
+      fetch_tokens(ty, sx.len, rows_of(solved, d, sx));
     };
     if (hf == 0) fetch_phase4();
     __syncthreads();
@@ -607,11 +645,11 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       f4 gk[2], hv[2];
       zero2(gk);
       zero2(hv);
-      if (hf == 0) rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
+      if (hf == 0) fetch_tokens(tz, sx.len, rows_of(z, d, sx));
       tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // G^T k_s
       if (hf == 1) fetch_phase4();
       tile_mma_half<false, true, true>(gk, Kt, M1, 64, ws, hf);  // + G k_s
-      if (hf == 1) rt[3].fetch_rows(sx.len, rows_of(z, d, sx));
+      if (hf == 1) fetch_tokens(tz, sx.len, rows_of(z, d, sx));
       float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -622,8 +660,9 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       for (int v = MAX_NV - 1; v >= 0; --v) {
         if (v < d.NV) {
           if (v < last) {
-            TileRegs2 rv, rhv;
-            rv.fetch_rows(si.len, value_rows(values, d, si, v));
+            RowTile<In, GRADS_THREADS> rv;
+            TileRegs2 rhv;
+            fetch_tokens(rv, si.len, value_rows(values, d, si, v));
             rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
             __syncthreads();
             rv.store(Vt);
@@ -683,13 +722,14 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       zero2(ys);
       zero2(dc);
       tile_mma_half<false, false>(ys, Yt, Kt, 64, ws, hf);  // y_t^T S0
-      rt[1].fetch_rows(sx.len, value_rows(values, d, sx, 0));
+      fetch_tokens(tv, sx.len, value_rows(values, d, sx, 0));
       for (int v = 0; v < d.NV; ++v) {
         if (v > 0) {
-          TileRegs2 rhv, rcv, rd;
+          TileRegs2 rhv, rcv;
+          RowTile<float, GRADS_THREADS> rd;
           rhv.fetch_matrix(cross_tile(end_c, d, si.seq, v));
           rcv.fetch_matrix(cross_tile(start_c, d, si.seq, v));
-          rd.fetch_rows(si.len, value_rows(d_output, d, si, v));
+          fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
           __syncthreads();
           rhv.store(M2);
           rcv.store(Vt);
@@ -710,7 +750,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         tile_mma_half<false, false>(dc, Dt, Vt, 64, ws, hf);  // dout_t^T C0, summed
       }
       red[tid] = part;
-      rt[4].fetch_rows(sx.len, value_rows(d_output, d, sx, 0));
+      fetch_tokens(td, sx.len, value_rows(d_output, d, sx, 0));
       fetch_scalars(sx);
       float sp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

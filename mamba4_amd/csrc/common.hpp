@@ -1,6 +1,8 @@
 // Shared device helpers for the gfx950 memory-read kernels.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 
 namespace m4 {
@@ -25,6 +27,19 @@ __device__ __forceinline__ f4 load4(const bf16_t* p) {
             __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
 }
 __device__ __forceinline__ float load1(const float* p) { return *p; }
+
+// Raw buffer loads: an offset at or past the resource's byte size reads zero
+// without a memory access, so rows past a chunk's end need no branch (and a
+// wait for one load counts exactly the loads issued after it).
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr unsigned kNoRow = 0x80000000u;  // an offset past any resource
+__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ float buf_load1(BufRsrc r, unsigned off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
 __device__ __forceinline__ float load1(const bf16_t* p) {
   return __uint_as_float((unsigned)*p << 16);
 }
@@ -409,6 +424,91 @@ struct TileRegs {
       const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : v[j];
       *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
     }
+  }
+};
+
+// A chunk's 64 token rows held by an NTH-thread block (thread i: column quad
+// i % 16 of rows i / 16 + (NTH / 16) j), in the input's own dtype: float32
+// as f4, bfloat16 as its raw 8 bytes, widened where the rows are stored or
+// read (a widening right after the load would make every load wait for the
+// one before it).  fetch_tokens reads rows [0, rows) at base + r * stride
+// elements through buffer loads (zero past `rows`, no branch); fetch_rows
+// (float32) takes a row-pointer functor instead.
+template <typename In, int NTH = 256>
+struct RowTile {
+  static constexpr bool F32 = std::is_same<In, float>::value;
+  static constexpr int J = 1024 / NTH, RS = NTH / 16;
+  typedef typename std::conditional<F32, f4, uint2>::type Raw;
+  Raw v[J];
+
+  __device__ __forceinline__ void fetch_tokens(int rows, const In* base, unsigned stride) {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+    const BufRsrc rs = buf_rsrc(base, ((unsigned)(rows - 1) * stride + 64) * sizeof(In));
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const unsigned off = ((r0 + RS * j) * stride + q) * sizeof(In);
+      if constexpr (F32)
+        v[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+      else
+        v[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    }
+  }
+  template <typename RowPtr>
+  __device__ __forceinline__ void fetch_rows(int rows, RowPtr row) {
+    static_assert(F32, "row-pointer fetches take float32 rows");
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int r = r0 + RS * j;
+      v[j] = r < rows ? load4(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __device__ __forceinline__ f4 get(int j) const {
+    if constexpr (F32)
+      return v[j];
+    else
+      return f4{__uint_as_float(v[j].x << 16), __uint_as_float(v[j].x & 0xffff0000u),
+                __uint_as_float(v[j].y << 16), __uint_as_float(v[j].y & 0xffff0000u)};
+  }
+  __device__ __forceinline__ void store(float* tile) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < J; ++j) *reinterpret_cast<f4*>(tile + (r0 + RS * j) * LDT + q) = get(j);
+  }
+  // The rows unit-normalised (mix_unit), row 0 as a zero row if zero_row0.
+  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int r = r0 + RS * j;
+      const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : get(j);
+      *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
+    }
+  }
+};
+
+// Four consecutive elements of one row, held raw as RowTile holds them.
+template <typename In>
+struct RowQuad;
+
+template <>
+struct RowQuad<float> {
+  f4 v;
+  __device__ __forceinline__ void load(BufRsrc r, unsigned off) {
+    v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  }
+  __device__ __forceinline__ f4 get() const { return v; }
+};
+
+template <>
+struct RowQuad<bf16_t> {
+  uint2 v;
+  __device__ __forceinline__ void load(BufRsrc r, unsigned off) {
+    v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  }
+  __device__ __forceinline__ f4 get() const {
+    return f4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+              __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
   }
 };
 

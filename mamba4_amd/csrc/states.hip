@@ -352,7 +352,7 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
   // Rows and scalars of one step on their way from HBM to LDS.  Two sets
   // rotate, so a step's loads are issued two steps before it multiplies.
   struct StepRegs {
-    TileRegs2 ra, rb;
+    RowTile<In, STATES_THREADS> ra, rb;
     float pg, pb;
   };
   // MIX (forward): the b rows are the keys from the mixer's raw projections
@@ -367,21 +367,20 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
         return p ? p : mix.query + token_head(d, b, first + r, h) * 64;
       });
     } else {
-      R.rb.fetch_rows(cnt, [&](int r) { return rows_b + token_head(d, b, first + r, h) * 64; });
+      R.rb.fetch_tokens(cnt, rows_b + token_head(d, b, first, h) * 64, (unsigned)d.H * 64);
     }
     if (own_a) {
       const int width = cross ? d.P : 64, offset = cross ? 64 * v : 0;
-      R.ra.fetch_rows(cnt, [&](int r) {
-        return (cross ? rows_ac : rows_a) + token_head(d, b, first + r, h) * width + offset;
-      });
+      R.ra.fetch_tokens(cnt, (cross ? rows_ac : rows_a) + token_head(d, b, first, h) * width + offset,
+                        (unsigned)(d.H * width));
     }
-    R.pg = 0.f;
-    R.pb = 0.f;
-    if (w == 0 && l < cnt) {
-      const long th = token_head(d, b, first + l, h);
-      R.pg = g.log_decay[th];
-      if (!BWD) R.pb = g.beta[th];
-    }
+    // Wave 0's lane l: token l's log decay and beta (zero past the chunk; the
+    // other waves read out of range).
+    const long th = token_head(d, b, first, h);
+    const unsigned bytes = (unsigned)(cnt - 1) * d.H * 4 + 4;
+    const unsigned off = w == 0 ? (unsigned)l * d.H * 4 : kNoRow;
+    R.pg = buf_load1(buf_rsrc(g.log_decay + th, bytes), off);
+    R.pb = BWD ? 0.f : buf_load1(buf_rsrc(g.beta + th, bytes), off);
   };
   auto stage = [&](const StepRegs& R, int u, int i) {
     if constexpr (MIX)
