@@ -109,18 +109,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // position 0 reads its query row and is zeroed at staging).
   auto fetch_keys = [&](const SeqIndex& s) {
     if constexpr (MIX) {
-      rk.fetch_rows(s.len, [&](int r) -> const float* {
-        const int t = s.n * d.chunk + r;
-        const float* p = mix_key_row(mix, d, s.b, t, s.h);
-        return p ? p : mix.query + token_head(d, s.b, t, s.h) * 64;
-      });
+      rk.fetch_mix_keys(s.len, mix, d, s.b, s.h, s.n * d.chunk);
     } else {
       fetch_tokens(rk, s.len, rows_of(keys, d, s));
     }
   };
   auto fetch_queries = [&](const SeqIndex& s) {
     if constexpr (MIX)
-      rq.fetch_rows(s.len, rows_of(mix.query, d, s));
+      fetch_tokens(rq, s.len, rows_of(mix.query, d, s));
     else
       fetch_tokens(rq, s.len, rows_of(queries, d, s));
   };
@@ -302,11 +298,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   auto fetch_keys = [&](const SeqIndex& s) {
     if constexpr (MIX) {
-      rk.fetch_rows(s.len, [&](int r) -> const float* {
-        const int t = s.n * d.chunk + r;
-        const float* p = mix_key_row(mix, d, s.b, t, s.h);
-        return p ? p : mix.query + token_head(d, s.b, t, s.h) * 64;
-      });
+      rk.fetch_mix_keys(s.len, mix, d, s.b, s.h, s.n * d.chunk);
     } else {
       fetch_tokens(rk, s.len, rows_of(keys, d, s));
     }
@@ -459,11 +451,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   RowTile<float, GRADS_THREADS> ty, tz, td;
   auto fetch_keys = [&](const SeqIndex& sx) {
     if constexpr (MIX) {
-      tk.fetch_rows(sx.len, [&](int r) -> const float* {
-        const int t = sx.n * d.chunk + r;
-        const float* p = mix_key_row(mix, d, sx.b, t, sx.h);
-        return p ? p : mix.query + token_head(d, sx.b, t, sx.h) * 64;
-      });
+      tk.fetch_mix_keys(sx.len, mix, d, sx.b, sx.h, sx.n * d.chunk);
     } else {
       fetch_tokens(tk, sx.len, rows_of(keys, d, sx));
     }

@@ -453,6 +453,35 @@ struct RowTile {
         v[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
     }
   }
+  // The mixer's key rows of the chunk at position t0 (with the key shift,
+  // row r holds position t0 + r - 1's raw key and position 0's row is the
+  // decode cache's key, or zero without one): every path issues the same
+  // loads, out-of-range ones reading zero.
+  __device__ __forceinline__ void fetch_mix_keys(int rows, const MixerIn& m, const Dims& d, int b,
+                                                 int h, int t0) {
+    static_assert(F32, "the mixer's rows are float32");
+    const int adj = m.key_shift && t0 == 0 ? 1 : 0;  // row 0 holds no key row
+    const int first = m.key_shift && t0 > 0 ? t0 - 1 : t0;
+    const int n = rows - adj;
+    const unsigned stride = (unsigned)d.H * 64;
+    const BufRsrc rs = buf_rsrc(m.key + token_head(d, b, first, h) * 64,
+                                n > 0 ? ((unsigned)(n - 1) * stride + 64) * 4 : 0);
+    const float* prev = m.previous ? m.previous + ((long)b * d.H + h) * 64 : m.key;
+    const BufRsrc rp = buf_rsrc(prev, adj && m.previous ? 256 : 0);
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int r = r0 + RS * j;
+      const unsigned off = r >= adj ? ((unsigned)(r - adj) * stride + q) * 4 : kNoRow;
+      f4 x = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+      if (j == 0) {
+        const f4 pv = __builtin_bit_cast(
+            f4, __builtin_amdgcn_raw_buffer_load_b128(rp, r == 0 ? q * 4 : kNoRow, 0, 0));
+        if (r == 0 && adj) x = pv;
+      }
+      v[j] = x;
+    }
+  }
   template <typename RowPtr>
   __device__ __forceinline__ void fetch_rows(int rows, RowPtr row) {
     static_assert(F32, "row-pointer fetches take float32 rows");

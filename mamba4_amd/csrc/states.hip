@@ -362,10 +362,7 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
   auto fetch = [&](StepRegs& R, int i) {
     const int first = i * d.chunk, cnt = chunk_len(d, i);
     if constexpr (MIX) {
-      R.rb.fetch_rows(cnt, [&](int r) -> const float* {
-        const float* p = mix_key_row(mix, d, b, first + r, h);
-        return p ? p : mix.query + token_head(d, b, first + r, h) * 64;
-      });
+      R.rb.fetch_mix_keys(cnt, mix, d, b, h, first);
     } else {
       R.rb.fetch_tokens(cnt, rows_b + token_head(d, b, first, h) * 64, (unsigned)d.H * 64);
     }
