@@ -30,7 +30,7 @@ __global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, 
                                 float*, float*);
 template <bool BWD, typename In, bool MIX>
 __global__ void states_kernel(Dims, StateArgs);
-template <typename In, bool MIX, bool STORE>
+template <typename In, bool MIX, bool STORE, int PAIRS>
 __global__ void fwd_factor_kernel(Dims, const In*, const In*, const float*, const float*,
                                   const float*, const float*, float*, float*, MixerIn, int);
 __global__ void factored_solve_kernel(const float*, const float*, float*, long);
@@ -377,16 +377,17 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   if (rc) return rc;
   const int polls = turn_polls();
   rc = launch("fwd_factor", st, [&] {
-    // Sixteen sub-chunk sequences per block: four wave pairs of four.
-    const dim3 grid((subseqs + 15) / 16), block(512);
-    if (factors)
-      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, true>), grid, block, 0, st, d, keys,
-                         queries, beta, log_decay, floor, start_evidence, solved, factors, mix,
-                         polls);
-    else
-      hipLaunchKernelGGL((m4::fwd_factor_kernel<In, MIX, false>), grid, block, 0, st, d, keys,
-                         queries, beta, log_decay, floor, start_evidence, solved, factors, mix,
-                         polls);
+    // Four sub-chunk sequences per wave pair; four pairs per block when those
+    // blocks fill the chip in whole rounds (one resident per CU), else two.
+    const unsigned blocks4 = (subseqs + 15) / 16;
+    const int pairs = blocks4 % (unsigned)g_cus == 0 ? 4 : 2;
+    const dim3 grid((subseqs + 4 * pairs - 1) / (4 * pairs)), block(128 * pairs);
+    const auto kernel = factors ? (pairs == 4 ? m4::fwd_factor_kernel<In, MIX, true, 4>
+                                              : m4::fwd_factor_kernel<In, MIX, true, 2>)
+                                : (pairs == 4 ? m4::fwd_factor_kernel<In, MIX, false, 4>
+                                              : m4::fwd_factor_kernel<In, MIX, false, 2>);
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, d, keys, queries, beta, log_decay, floor,
+                       start_evidence, solved, factors, mix, polls);
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {

@@ -134,10 +134,14 @@ __device__ __forceinline__ void raise_count(lds_int* count, int v) {
 // turn, ... without waiting out the other wave's turn, the two waves offset
 // by one turn.  A pair holds one 40 KB evidence buffer.
 //
-// Four pairs per block (waves 2p, 2p + 1 form pair p), so a CU holds one
-// eight-wave block rather than four two-wave ones: the same waves per SIMD,
-// about 5% faster on the same work (measured; two-wave blocks spent more of
-// each pass waiting for the other wave's turn).
+// PAIRS pairs per block (waves 2p, 2p + 1 form pair p).  Four: a CU holds
+// one eight-wave block rather than four two-wave ones, the same waves per
+// SIMD, about 5% faster on the same work (measured; two-wave blocks spent
+// more of each pass waiting for the other wave's turn).  Two: the launch
+// takes these when the four-pair blocks would not fill the chip in whole
+// rounds; the last round's blocks then spread over every CU at one wave per
+// SIMD (each wave issues faster alone) instead of filling part of the chip
+// at two.  Only the grid changes: every sequence runs the same code.
 //
 // A wave whose wait gives up (wait_turn) may read the evidence before the
 // other wave's update: it poisons the pair's count at once, and every turn of
@@ -151,10 +155,8 @@ __device__ __forceinline__ void raise_count(lds_int* count, int v) {
 // are not stored (`factors` is unused), the reference's store_factors=False
 // mode (lm/kernels/mamba4_fused.py:183-232), for forwards that take no
 // gradient.
-constexpr int FACTOR_THREADS = 512;  // four wave pairs
-
-template <typename In, bool MIX, bool STORE>
-__global__ __launch_bounds__(FACTOR_THREADS) void fwd_factor_kernel(
+template <typename In, bool MIX, bool STORE, int PAIRS>
+__global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ queries,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
     const float* __restrict__ floor, const float* __restrict__ start_s,
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(FACTOR_THREADS) void fwd_factor_kernel(
   const int pair = wave8 >> 1, wave = wave8 & 1;
   const int BH = d.B * d.H;
   const long nseq = (long)BH * d.NS;
-  long seq = ((long)blockIdx.x * 4 + pair) * 4 + mu;
+  long seq = ((long)blockIdx.x * PAIRS + pair) * 4 + mu;
   const bool active = seq < nseq;
   if (!active) seq = nseq - 1;
   // Sequences are ordered sub-chunk-major, so a wave's four rows share the
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(FACTOR_THREADS) void fwd_factor_kernel(
   const int steps = wave_max4(len);
 
   // The running evidence, negated (the factorization's working convention).
-  __shared__ f4 evidence_all[4][40 * 64];  // per pair: [quad][lane]
+  __shared__ f4 evidence_all[PAIRS][40 * 64];  // per pair: [quad][lane]
   f4* const evidence = evidence_all[pair];
   // The turn count lives in the pair's buffer (the four fill the CU's LDS):
   // word 0 of lane 0's quad (0, 3), row 0,
@@ -300,7 +302,10 @@ __global__ __launch_bounds__(FACTOR_THREADS) void fwd_factor_kernel(
 }
 
 #define M4_FWD_FACTOR(IN, MIX, STORE)                                                      \
-  template __global__ void fwd_factor_kernel<IN, MIX, STORE>(                              \
+  template __global__ void fwd_factor_kernel<IN, MIX, STORE, 4>(                           \
+      Dims, const IN*, const IN*, const float*, const float*, const float*, const float*, \
+      float*, float*, MixerIn, int);                                                       \
+  template __global__ void fwd_factor_kernel<IN, MIX, STORE, 2>(                           \
       Dims, const IN*, const IN*, const float*, const float*, const float*, const float*, \
       float*, float*, MixerIn, int);
 M4_FWD_FACTOR(float, false, true)
