@@ -28,7 +28,7 @@ __global__ void bwd_local_kernel(Dims, const float*, const float*, const float*,
                                  const float*, float*, float*);
 __global__ void bwd_scan_kernel(Dims, const float*, const float*, const float*, float*, float*,
                                 float*, float*);
-template <bool BWD, typename In, bool MIX>
+template <bool BWD, typename In, bool MIX, int NBUF>
 __global__ void states_kernel(Dims, StateArgs);
 template <typename In, bool MIX, bool STORE, int PAIRS>
 __global__ void fwd_factor_kernel(Dims, const In*, const In*, const float*, const float*,
@@ -160,10 +160,10 @@ int configure() {
              {(const void*)m4::bwd_grads_kernel<float, false>, kGradsLdsBytes},
              {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false>, kGradsLdsBytes},
              {(const void*)m4::bwd_grads_kernel<float, true>, kGradsLdsBytes},
-             {(const void*)m4::states_kernel<false, float, false>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<false, m4::bf16_t, false>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<true, float, false>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<false, float, true>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<false, float, false, 2>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<false, m4::bf16_t, false, 2>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<true, float, false, 2>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<false, float, true, 2>, kStatesLdsBytes},
              {(const void*)m3::walk_kernel<false, float, true>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true, float, true>, m3::kWalkLds},
              {(const void*)m3::out_kernel<float, true>, m3::kOutLds},
@@ -232,6 +232,12 @@ bool fused_states(int B, int H, const Dims& d) {
     if (std::strcmp(mode, "split") == 0) return false;
   }
   return (long)B * H * (1 + d.NV) >= g_cus;
+}
+
+// The fused walks with one LDS step buffer (three blocks per CU) when their
+// blocks would not all be resident at two per CU.
+bool states_single_buffer(int B, int H, const Dims& d) {
+  return (long)B * H * (1 + d.NV) > 2L * g_cus;
 }
 
 // Poll bound of the factor kernel's turn waits: 2^16, or M4MR_TURN_POLLS
@@ -359,8 +365,10 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
                        init_evidence,   init_cross,  start_evidence, start_cross,
                        final_evidence,  final_cross, mix};
     rc = launch("fwd_states", st, [&] {
-      hipLaunchKernelGGL((m4::states_kernel<false, In, MIX>), dim3(B * H, 1 + d.NV), dim3(512),
-                         kStatesLdsBytes, st, d, args);
+      const bool one = states_single_buffer(B, H, d);
+      const auto walk = one ? m4::states_kernel<false, In, MIX, 1> : m4::states_kernel<false, In, MIX, 2>;
+      hipLaunchKernelGGL(walk, dim3(B * H, 1 + d.NV), dim3(512),
+                         one ? kStatesLdsBytes / 2 : kStatesLdsBytes, st, d, args);
     });
   } else {
     rc = launch("fwd_stats", st, [&] {
@@ -458,8 +466,10 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                              d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
                              d_init_evidence,  d_init_cross};
     rc = launch("bwd_states", st, [&] {
-      hipLaunchKernelGGL((m4::states_kernel<true, float, false>), dim3(B * H, 1 + d.NV), dim3(512),
-                         kStatesLdsBytes, st, d, args);
+      const bool one = states_single_buffer(B, H, d);
+      const auto walk = one ? m4::states_kernel<true, float, false, 1> : m4::states_kernel<true, float, false, 2>;
+      hipLaunchKernelGGL(walk, dim3(B * H, 1 + d.NV), dim3(512),
+                         one ? kStatesLdsBytes / 2 : kStatesLdsBytes, st, d, args);
     });
   } else {
     rc = launch("bwd_local", st, [&] {

@@ -276,8 +276,12 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
 //             cross a = d_output tile, b = y with wt = exp(P_t);  states
 //             descend from the final-state cotangent (the transpose of the
 //             forward carry, as bwd_local_kernel + bwd_scan_kernel).
-// A step's rows load into registers two steps before it multiplies; LDS
-// holds two step buffers, so each step takes one barrier.
+// A step's rows load into registers two steps before it multiplies.  NBUF =
+// 2: LDS holds two step buffers and each step takes one barrier (the next
+// step staged while this one multiplies).  NBUF = 1: one buffer, staged
+// between two barriers, half the LDS, so three blocks fit a CU instead of
+// two; the launch takes it when the walks would not fit the chip at two per
+// CU (the extra resident blocks beat the exposed staging there).
 // Wave w computes rows 16 (w % 4) .. +15 and column quads' halves w / 4 of
 // the 64x64 state tile.
 
@@ -312,7 +316,7 @@ __device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const 
 
 // In: element type of the forward's key and value rows (the backward's rows
 // are float32).
-template <bool BWD, typename In, bool MIX>
+template <bool BWD, typename In, bool MIX, int NBUF>
 __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArgs g) {
   const In* rows_a = static_cast<const In*>(g.rows_a);
   const In* rows_ac = static_cast<const In*>(g.rows_ac);
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
   // the other buffer at the end), `spare` (step k, already staged) receives
   // step k + 2.
   auto step = [&](int k, const StepRegs& next, StepRegs& spare) {
-    const int i = i0 + k * stride, u = k & 1;
+    const int i = i0 + k * stride, u = NBUF == 2 ? k & 1 : 0;
     if (k + 2 < steps) fetch(spare, i + 2 * stride);
     const float* tb = smem + 2 * u * TILE;
     const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
@@ -438,7 +442,12 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
         if (BWD && !cross) weighted_block(acc, tb, ta, sb[u].wt[part], k0, s, hf);
       }
     }
-    if (k + 1 < steps) stage(next, u ^ 1, i + stride);
+    if constexpr (NBUF == 2) {
+      if (k + 1 < steps) stage(next, u ^ 1, i + stride);
+    } else {
+      __syncthreads();  // every wave is done with the buffer
+      if (k + 1 < steps) stage(next, 0, i + stride);
+    }
     __syncthreads();
   };
   for (int k = 0; k < steps; k += 2) {
@@ -451,10 +460,14 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
 }
 
-template __global__ void states_kernel<false, float, false>(Dims, StateArgs);
-template __global__ void states_kernel<false, bf16_t, false>(Dims, StateArgs);
-template __global__ void states_kernel<true, float, false>(Dims, StateArgs);
-template __global__ void states_kernel<false, float, true>(Dims, StateArgs);
+#define M4_STATES(BWD, IN, MIX)                                          \
+  template __global__ void states_kernel<BWD, IN, MIX, 1>(Dims, StateArgs); \
+  template __global__ void states_kernel<BWD, IN, MIX, 2>(Dims, StateArgs);
+M4_STATES(false, float, false)
+M4_STATES(false, bf16_t, false)
+M4_STATES(true, float, false)
+M4_STATES(false, float, true)
+#undef M4_STATES
 template __global__ void fwd_stats_kernel<float>(Dims, const float*, const float*, const float*,
                                                  const float*, float*, float*);
 template __global__ void fwd_stats_kernel<bf16_t>(Dims, const bf16_t*, const bf16_t*,
