@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // (the other lanes read out of range), fetched with its first tiles.
   float sg, sb;
   auto fetch_scalars = [&](const SeqIndex& s) {
-    const unsigned st = (unsigned)d.H * 4, bytes = (unsigned)(s.len - 1) * st + 4;
+    const unsigned st = (unsigned)d.H * 4, bytes = s.len > 0 ? (unsigned)(s.len - 1) * st + 4 : 0;
     const long th = token_head(d, s.b, s.n * d.chunk, s.h);
     const unsigned off = threadIdx.x < 64 ? threadIdx.x * st : kNoRow;
     sg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
@@ -148,15 +148,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
-    // The last chunk of a block fetches its own inputs again (unused): every
-    // chunk issues the same loads, so each wait counts exactly.
-    const SeqIndex sn = seq_at(d, more ? next : seq);
+    // After a block's last chunk the same loads are issued with no rows in
+    // range (zeros, no memory access): every chunk issues the same loads, so
+    // each wait counts exactly.
+    SeqIndex sn = seq_at(d, more ? next : seq);
+    if (!more) sn.len = 0;
     fetch_tokens(ry, sn.len, rows_of(solved, d, sn));
     fetch_scalars(sn);
     fetch_keys(sn);
     // With more than one value tile, rc carries this chunk's later tiles and
     // prefetches after the last of them.
-    if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
+    if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
 
     // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
     // the 16 lanes that hold the rest of each row.
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __syncthreads();
       if (v == d.NV - 1) {
         fetch_tokens(rv, sn.len, value_rows(values, d, sn, 0));
-        if (d.NV > 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
+        if (d.NV > 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
       }
 
       f4 out[4], inh[4];
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // lanes read out of range), fetched with its first tiles.
   float sg, sb;
   auto fetch_scalars = [&](const SeqIndex& s) {
-    const unsigned st = (unsigned)d.H * 4, bytes = (unsigned)(s.len - 1) * st + 4;
+    const unsigned st = (unsigned)d.H * 4, bytes = s.len > 0 ? (unsigned)(s.len - 1) * st + 4 : 0;
     const long th = token_head(d, s.b, s.n * d.chunk, s.h);
     const unsigned off = threadIdx.x < 64 ? threadIdx.x * st : kNoRow;
     sg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
@@ -318,7 +320,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
-    const SeqIndex sn = seq_at(d, more ? next : seq);
+    // After a block's last chunk the same loads are issued with no rows in
+    // range (zeros, no memory access), so each wait counts exactly.
+    SeqIndex sn = seq_at(d, more ? next : seq);
+    if (!more) sn.len = 0;
 
     // Both products sum over the value tiles: dout_t . v_s and C0^T dout_t.
     f4 acc[4], inh[4];
@@ -341,7 +346,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (v == d.NV - 1) {
         fetch_tokens(rd, sn.len, value_rows(d_output, d, sn, 0));
         fetch_tokens(rv, sn.len, value_rows(values, d, sn, 0));
-        rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0));
+        rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
         fetch_scalars(sn);
       }
       tile_mma<false, true>(acc, DO, V, 64, w);    // dout_t . v_s
@@ -461,7 +466,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   float pg = 0.f, pbt = 0.f, pdv[2];
   auto fetch_scalars = [&](const SeqIndex& sx) {
     const unsigned tt = threadIdx.x, st = (unsigned)d.H * 4;
-    const unsigned bytes = (unsigned)(sx.len - 1) * st + 4;
+    const unsigned bytes = sx.len > 0 ? (unsigned)(sx.len - 1) * st + 4 : 0;
     const long th = token_head(d, sx.b, sx.n * d.chunk, sx.h);
     const unsigned off = tt < 64 ? tt * st : kNoRow;
     pg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
@@ -617,7 +622,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
     // The last chunk of a block fetches its own tiles again (unused): every
-    // load stays unconditional.
+    // load stays unconditional.  (Issuing them with no rows in range instead,
+    // as fwd_read and bwd_dy do, ran 2 us slower here.)
     const SeqIndex sx = seq_at(d, more ? next : seq);
     // The two waves on a SIMD (ws, hf = 0 and 1) issue these loads before
     // and after their first product, so one computes while the other waits

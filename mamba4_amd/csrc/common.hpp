@@ -408,6 +408,16 @@ struct TileRegs {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const f4*>(src + (r0 + 16 * j) * 64 + q);
   }
+  // The same through a buffer resource that is empty unless `any`: zeros and
+  // no memory access otherwise, with the same instructions either way.
+  __device__ __forceinline__ void fetch_matrix(const float* src, bool any) {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+    const BufRsrc rs = buf_rsrc(src, any ? 4096 * 4 : 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = __builtin_bit_cast(
+          f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((r0 + 16 * j) * 64 + q) * 4, 0, 0));
+  }
 
   __device__ __forceinline__ void store(float* tile) const {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
@@ -443,7 +453,8 @@ struct RowTile {
 
   __device__ __forceinline__ void fetch_tokens(int rows, const In* base, unsigned stride) {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
-    const BufRsrc rs = buf_rsrc(base, ((unsigned)(rows - 1) * stride + 64) * sizeof(In));
+    const BufRsrc rs =
+        buf_rsrc(base, rows > 0 ? ((unsigned)(rows - 1) * stride + 64) * sizeof(In) : 0);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const unsigned off = ((r0 + RS * j) * stride + q) * sizeof(In);
@@ -467,7 +478,7 @@ struct RowTile {
     const BufRsrc rs = buf_rsrc(m.key + token_head(d, b, first, h) * 64,
                                 n > 0 ? ((unsigned)(n - 1) * stride + 64) * 4 : 0);
     const float* prev = m.previous ? m.previous + ((long)b * d.H + h) * 64 : m.key;
-    const BufRsrc rp = buf_rsrc(prev, adj && m.previous ? 256 : 0);
+    const BufRsrc rp = buf_rsrc(prev, rows > 0 && adj && m.previous ? 256 : 0);
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -601,6 +612,17 @@ struct TileRegsT {
       int r, c;
       slot(j, r, c);
       v[j] = *reinterpret_cast<const f4*>(src + r * 64 + c);
+    }
+  }
+  // Through a buffer resource that is empty unless `any` (as TileRegs).
+  __device__ __forceinline__ void fetch_matrix(const float* src, bool any) {
+    const BufRsrc rs = buf_rsrc(src, any ? 4096 * 4 : 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int r, c;
+      slot(j, r, c);
+      v[j] = __builtin_bit_cast(f4,
+                                __builtin_amdgcn_raw_buffer_load_b128(rs, (r * 64 + c) * 4, 0, 0));
     }
   }
 
