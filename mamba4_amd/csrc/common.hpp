@@ -424,17 +424,6 @@ struct TileRegs {
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<f4*>(tile + (r0 + 16 * j) * LDT + q) = v[j];
   }
-
-  // The rows unit-normalised (mix_unit), row 0 as a zero row if zero_row0.
-  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
-    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = r0 + 16 * j;
-      const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : v[j];
-      *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
-    }
-  }
 };
 
 // A chunk's 64 token rows held by an NTH-thread block (thread i: column quad
@@ -442,8 +431,8 @@ struct TileRegs {
 // as f4, bfloat16 as its raw 8 bytes, widened where the rows are stored or
 // read (a widening right after the load would make every load wait for the
 // one before it).  fetch_tokens reads rows [0, rows) at base + r * stride
-// elements through buffer loads (zero past `rows`, no branch); fetch_rows
-// (float32) takes a row-pointer functor instead.
+// elements through buffer loads (zero past `rows`, no branch);
+// fetch_mix_keys (float32) reads the mixer's shifted key rows.
 template <typename In, int NTH = 256>
 struct RowTile {
   static constexpr bool F32 = std::is_same<In, float>::value;
@@ -491,16 +480,6 @@ struct RowTile {
         if (r == 0 && adj) x = pv;
       }
       v[j] = x;
-    }
-  }
-  template <typename RowPtr>
-  __device__ __forceinline__ void fetch_rows(int rows, RowPtr row) {
-    static_assert(F32, "row-pointer fetches take float32 rows");
-    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int r = r0 + RS * j;
-      v[j] = r < rows ? load4(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
     }
   }
   __device__ __forceinline__ f4 get(int j) const {
@@ -552,20 +531,10 @@ struct RowQuad<bf16_t> {
   }
 };
 
-// TileRegs for a 512-thread block: thread i holds column quad i%16 of rows
-// i/16 + 32j (j = 0, 1).
+// A dense 64x64 matrix in a 512-thread block: thread i holds column quad
+// i%16 of rows i/16 + 32j (j = 0, 1).
 struct TileRegs2 {
   f4 v[2];
-
-  template <typename RowPtr>
-  __device__ __forceinline__ void fetch_rows(int rows, RowPtr row) {
-    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int r = r0 + 32 * j;
-      v[j] = r < rows ? load4(row(r) + q) : f4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
 
   __device__ __forceinline__ void fetch_matrix(const float* src) {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
@@ -577,17 +546,6 @@ struct TileRegs2 {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int j = 0; j < 2; ++j) *reinterpret_cast<f4*>(tile + (r0 + 32 * j) * LDT + q) = v[j];
-  }
-
-  // As TileRegs::store_unit.
-  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
-    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int r = r0 + 32 * j;
-      const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : v[j];
-      *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
-    }
   }
 };
 
