@@ -1734,30 +1734,79 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
   const int t0 = TPB * part, rows = max(0, min(TPB, s.T - c * C - t0));
   const long tp = (long)s.NC * C;
   // The row gradients first: their group sums read no LDS, so their loads
-  // are in flight with the staging loads below.
-#pragma unroll 8
-  for (int e = tid; e < rows * s.N; e += 256) {
-    const int t = t0 + e / s.N, n = e % s.N, tt = c * C + t;
-    float ac = 0.f, ab = 0.f;
-    for (int g = 0; g < groups; ++g) {
-      const long at = (((long)g * s.B + b) * tp + tt) * NT + n;
-      ac += o.dc_part[at];
-      ab += o.db_part[at];
+  // are in flight with the staging loads below.  A thread's K elements load
+  // together for each group (buffer loads, out of range past the rows), so a
+  // group costs one round trip rather than one per element.
+  {
+    constexpr int K = TPB * NT / 256;
+    float ac[K], ab[K];
+    unsigned off[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int e = tid + 256 * k, t = t0 + e / s.N, n = e % s.N;
+      off[k] = e < rows * s.N ? (unsigned)((c * C + t) * NT + n) * 4 : kNoLoad;
+      ac[k] = ab[k] = 0.f;
     }
-    d_c[tok_index(s, b, tt) * s.N + n] = ac;
-    d_b[tok_index(s, b, tt) * s.N + n] = ab;
+    for (int g = 0; g < groups; ++g) {
+      const long slab = ((long)g * s.B + b) * tp * NT;
+      const Rsrc rc = rsrc(o.dc_part + slab, tp * NT * 4), rb = rsrc(o.db_part + slab, tp * NT * 4);
+      float xc[K], xb[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        xc[k] = ldb(rc, off[k]);
+        xb[k] = ldb(rb, off[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        ac[k] += xc[k];
+        ab[k] += xb[k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int e = tid + 256 * k, t = t0 + e / s.N, n = e % s.N, tt = c * C + t;
+      if (e < rows * s.N) {
+        d_c[tok_index(s, b, tt) * s.N + n] = ac[k];
+        d_b[tok_index(s, b, tt) * s.N + n] = ab[k];
+      }
+    }
   }
-  for (int e = tid; e < rows * s.A; e += 256) {
-    const int t = t0 + e / s.A, j = e % s.A;
-    angs[t * (s.A + 1) + j] = ang[tok_index(s, b, c * C + t) * s.A + j];
-  }
-  for (int e = tid; e < rows * s.H; e += 256) {
-    const int t = t0 + e / s.H, h = e % s.H;
-    dts[t * (s.H + 1) + h] = dt[tok_index(s, b, c * C + t) * s.H + h];
-  }
-  for (int e = tid; e < s.H * s.A; e += 256) {
-    const int h = e / s.A, j = e % s.A;
-    suf[h * LA + j] = o.D[phase_offset(s, b, h, c) + j];
+  // The block's angle rates and dt rows (contiguous: rows x A, rows x H
+  // from token t0), and the later chunks' phase gradients of every head:
+  // each set's loads issued together before its LDS stores.
+  {
+    const long tok = tok_index(s, b, c * C + t0);
+    const Rsrc ra = rsrc(ang + tok * s.A, (long)rows * s.A * 4);
+    const Rsrc rd = rsrc(dt + tok * s.H, (long)rows * s.H * 4);
+    constexpr int KA = TPB * AM / 256, KH = TPB * kMaxHeads / 256;
+    float xa[KA], xd[KH];
+#pragma unroll
+    for (int k = 0; k < KA; ++k) xa[k] = ldb(ra, (tid + 256 * k) * 4);
+#pragma unroll
+    for (int k = 0; k < KH; ++k) xd[k] = ldb(rd, (tid + 256 * k) * 4);
+#pragma unroll
+    for (int k = 0; k < KA; ++k) {
+      const int e = tid + 256 * k;
+      if (e < rows * s.A) angs[(t0 + e / s.A) * (s.A + 1) + e % s.A] = xa[k];
+    }
+#pragma unroll
+    for (int k = 0; k < KH; ++k) {
+      const int e = tid + 256 * k;
+      if (e < rows * s.H) dts[(t0 + e / s.H) * (s.H + 1) + e % s.H] = xd[k];
+    }
+    for (int e0 = 0; e0 < s.H * s.A; e0 += 1024) {
+      float xs[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int e = e0 + tid + 256 * k;
+        xs[k] = e < s.H * s.A ? o.D[phase_offset(s, b, e / s.A, c) + e % s.A] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int e = e0 + tid + 256 * k;
+        if (e < s.H * s.A) suf[(e / s.A) * LA + e % s.A] = xs[k];
+      }
+    }
   }
   __syncthreads();
 #pragma unroll 4
@@ -1771,13 +1820,36 @@ __global__ __launch_bounds__(256) void finish_kernel(Shape s, int groups, const 
     d_dt[i] = dg * sig + dprev * (1.f - sig) + o.ddt_loc[i] + carried;
     d_trap[i] = (dg - dprev) * d * sig * (1.f - sig);
   }
-#pragma unroll 4
-  for (int e = tid; e < rows * s.A; e += 256) {
-    const int t = t0 + e / s.A, j = e % s.A, tt = c * C + t;
-    float acc = 0.f;
-    for (int g = 0; g < groups; ++g) acc += o.dang_part[(((long)g * s.B + b) * tp + tt) * AM + j];
-    for (int h = 0; h < s.H; ++h) acc += suf[h * LA + j] * dts[t * (s.H + 1) + h];
-    d_angles[tok_index(s, b, tt) * s.A + j] = acc;
+  {
+    // The angle gradients: the group sums' loads of a thread's elements
+    // issued together per group (out of range past the rows).
+    constexpr int KA = TPB * AM / 256;
+    float acc[KA];
+    unsigned off[KA];
+#pragma unroll
+    for (int k = 0; k < KA; ++k) {
+      const int e = tid + 256 * k, t = t0 + e / max(s.A, 1), j = e % max(s.A, 1);
+      off[k] = e < rows * s.A ? (unsigned)((c * C + t) * AM + j) * 4 : kNoLoad;
+      acc[k] = 0.f;
+    }
+    for (int g = 0; g < groups; ++g) {
+      const Rsrc rg = rsrc(o.dang_part + ((long)g * s.B + b) * tp * AM, tp * AM * 4);
+      float x[KA];
+#pragma unroll
+      for (int k = 0; k < KA; ++k) x[k] = ldb(rg, off[k]);
+#pragma unroll
+      for (int k = 0; k < KA; ++k) acc[k] += x[k];
+    }
+#pragma unroll
+    for (int k = 0; k < KA; ++k) {
+      const int e = tid + 256 * k;
+      if (e < rows * s.A) {
+        const int t = t0 + e / s.A, j = e % s.A, tt = c * C + t;
+        float a = acc[k];
+        for (int h = 0; h < s.H; ++h) a += suf[h * LA + j] * dts[t * (s.H + 1) + h];
+        d_angles[tok_index(s, b, tt) * s.A + j] = a;
+      }
+    }
   }
 }
 
