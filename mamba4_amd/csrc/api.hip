@@ -235,8 +235,13 @@ bool fused_states(int B, int H, const Dims& d) {
 }
 
 // The fused walks with one LDS step buffer (three blocks per CU) when their
-// blocks would not all be resident at two per CU.
+// blocks would not all be resident at two per CU.  M4MR_STATE_BUFFERS = "1"
+// or "2" overrides the choice (the same results either way).
 bool states_single_buffer(int B, int H, const Dims& d) {
+  if (const char* n = std::getenv("M4MR_STATE_BUFFERS")) {
+    if (std::strcmp(n, "1") == 0) return true;
+    if (std::strcmp(n, "2") == 0) return false;
+  }
   return (long)B * H * (1 + d.NV) > 2L * g_cus;
 }
 

@@ -117,8 +117,10 @@ def test_mixer_read_matches_separate_path(gpu_lib, monkeypatch, batch, time, hea
     from gpu_helpers import announce, normwise
     from mamba4_amd import SelectiveState
 
-    # The fused op always takes the fused state walk; so does the separate path here.
+    # The fused op always takes the fused state walk; so does the separate path
+    # here (with one LDS step buffer in the cases with an initial state).
     monkeypatch.setenv("M4MR_STATE_WALK", "fused")
+    monkeypatch.setenv("M4MR_STATE_BUFFERS", "1" if with_initial else "2")
     announce(f"mixer_read vs separate B{batch} T{time} H{heads} P{value_dim} chunk={chunk} "
              f"shift={key_shift} previous={with_previous} initial={with_initial}")
     x = raw_inputs(batch=batch, time=time, heads=heads, dim=64, value_dim=value_dim, seed=23)

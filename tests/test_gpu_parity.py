@@ -342,11 +342,13 @@ def test_wide_value_heads_decode_in_place(gpu_lib):
 
 
 
-@pytest.fixture(params=["split", "fused"])
+@pytest.fixture(params=["split", "fused", "fused1"])
 def state_walk(request, monkeypatch):
-    """Both chunk-boundary state paths (M4MR_STATE_WALK), forced at any size."""
-    monkeypatch.setenv("M4MR_STATE_WALK", request.param)
-    return request.param
+    """Both chunk-boundary state paths (M4MR_STATE_WALK), forced at any size;
+    the fused walk with two LDS step buffers and with one (M4MR_STATE_BUFFERS)."""
+    monkeypatch.setenv("M4MR_STATE_WALK", request.param[:5])
+    monkeypatch.setenv("M4MR_STATE_BUFFERS", "1" if request.param == "fused1" else "2")
+    return request.param[:5]
 
 
 @pytest.mark.parametrize("value_dim,chunk,time", [(5, 4, 21), (64, 64, 90), (128, 48, 100)])
