@@ -130,6 +130,8 @@ constexpr size_t kStatsLdsBytes = 3 * m4::TILE * sizeof(float);
 constexpr size_t kChunkLdsBytes = 4 * m4::TILE * sizeof(float);
 constexpr size_t kGradsLdsBytes = 7 * m4::TILE * sizeof(float);
 constexpr size_t kStatesLdsBytes = 4 * m4::TILE * sizeof(float);
+// The backward walks add one tile (the evidence state's transpose).
+constexpr size_t kStatesBwdExtra = m4::TILE * sizeof(float);
 
 bool configured = false;
 int g_cus = 256;  // compute units of the device (set by configure())
@@ -162,7 +164,8 @@ int configure() {
              {(const void*)m4::bwd_grads_kernel<float, true>, kGradsLdsBytes},
              {(const void*)m4::states_kernel<false, float, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, m4::bf16_t, false, 2>, kStatesLdsBytes},
-             {(const void*)m4::states_kernel<true, float, false, 2>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<true, float, false, 2>,
+              kStatesLdsBytes + kStatesBwdExtra},
              {(const void*)m4::states_kernel<false, float, true, 2>, kStatesLdsBytes},
              {(const void*)m3::walk_kernel<false, float, true>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true, float, true>, m3::kWalkLds},
@@ -474,7 +477,8 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
       const bool one = states_single_buffer(B, H, d);
       const auto walk = one ? m4::states_kernel<true, float, false, 1> : m4::states_kernel<true, float, false, 2>;
       hipLaunchKernelGGL(walk, dim3(B * H, 1 + d.NV), dim3(512),
-                         one ? kStatesLdsBytes / 2 : kStatesLdsBytes, st, d, args);
+                         (one ? kStatesLdsBytes / 2 : kStatesLdsBytes) + kStatesBwdExtra, st, d,
+                         args);
     });
   } else {
     rc = launch("bwd_local", st, [&] {

@@ -352,6 +352,44 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
       acc[1][q] = x.y;
     }
   }
+  // The backward evidence walk adds M + M^T per step (M = Z^T W Y), so its
+  // state is S = D + A + A^T with A the decayed sum of the M alone (one
+  // product per step instead of two) and D the decayed final-state cotangent
+  // (which need not be symmetric): acc holds A, dfin and dscale hold D, and
+  // A^T comes back through an LDS tile when a state is stored.  Both step
+  // buffer counts do this, so a batch's rows give the same bits whichever
+  // variant the batch size selects (its 96 VGPRs leave the one-buffer
+  // backward walk two blocks per CU, not three).
+  const bool sym = BWD && !cross;
+  f4 dfin[2];
+  float dscale = 1.f;
+  dfin[0] = acc[0];
+  dfin[1] = acc[1];
+  if (sym) zero2(acc);
+  float* const tr = smem + 2 * NBUF * TILE;  // the transpose tile (backward only)
+  // Stores the state this lane holds (rows 16 s + 4 (l / 16) + q, columns
+  // 4 (l % 16) + 2 hf + j) at dst (+ 64 q + j).
+  auto put_state = [&](float* dst) {
+    if (sym) {
+      const int r0 = 16 * s + 4 * (l >> 4), c0 = 4 * (l & 15) + 2 * hf;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float2*>(tr + (r0 + q) * LDT + c0) = float2{acc[0][q], acc[1][q]};
+      __syncthreads();
+      f4 t[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) t[j] = *reinterpret_cast<const f4*>(tr + (c0 + j) * LDT + r0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float2*>(dst + 64 * q) =
+            float2{dscale * dfin[0][q] + acc[0][q] + t[0][q],
+                   dscale * dfin[1][q] + acc[1][q] + t[1][q]};
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+    }
+  };
 
   // Rows and scalars of one step on their way from HBM to LDS.  Two sets
   // rotate, so a step's loads are issued two steps before it multiplies.
@@ -427,19 +465,16 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     const float* tb = smem + 2 * u * TILE;
     const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
     for (int part = 0; part < parts; ++part) {
-      float* dst = (cross ? g.steps_c : g.steps_s) + state_index(i, part) * 4096 + elem;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+      put_state((cross ? g.steps_c : g.steps_s) + state_index(i, part) * 4096 + elem);
       const float dk = sb[u].decay[part];
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[j] *= dk;
+      dscale *= dk;
       // 16-token blocks that hold the part's tokens; the weights are zero
       // outside the part.
       const int lo = sb[u].lo[part], hi = lo < sb[u].hi[part] ? sb[u].hi[part] : 0;
       for (int k0 = lo & ~15; k0 < hi; k0 += 16) {
         weighted_block(acc, ta, tb, sb[u].wt[part], k0, s, hf);
-        if (BWD && !cross) weighted_block(acc, tb, ta, sb[u].wt[part], k0, s, hf);
       }
     }
     if constexpr (NBUF == 2) {
@@ -454,10 +489,7 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
     step(k, R1, R0);
     if (k + 1 < steps) step(k + 1, R0, R1);
   }
-  float* dst = (cross ? g.last_c : g.last_s) + edge * 4096 + elem;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+  put_state((cross ? g.last_c : g.last_s) + edge * 4096 + elem);
 }
 
 #define M4_STATES(BWD, IN, MIX)                                          \
