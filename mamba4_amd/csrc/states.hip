@@ -316,8 +316,12 @@ __device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const 
 
 // In: element type of the forward's key and value rows (the backward's rows
 // are float32).
+// The one-buffer backward walk is held to six waves per SIMD (three blocks
+// per CU, as its LDS allows).
 template <bool BWD, typename In, bool MIX, int NBUF>
-__global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArgs g) {
+__global__ __launch_bounds__(STATES_THREADS)
+__attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kernel(Dims d,
+                                                                                  StateArgs g) {
   const In* rows_a = static_cast<const In*>(g.rows_a);
   const In* rows_ac = static_cast<const In*>(g.rows_ac);
   const In* rows_b = static_cast<const In*>(g.rows_b);
@@ -451,17 +455,9 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
   };
 
   const int i0 = BWD ? steps - 1 : 0, stride = BWD ? -1 : 1;
-  StepRegs R0, R1;
-  fetch(R0, i0);
-  if (steps > 1) fetch(R1, i0 + stride);
-  stage(R0, 0, i0);
-  __syncthreads();
-  // Step k multiplies LDS buffer k & 1; `next` holds step k + 1 (staged into
-  // the other buffer at the end), `spare` (step k, already staged) receives
-  // step k + 2.
-  auto step = [&](int k, const StepRegs& next, StepRegs& spare) {
-    const int i = i0 + k * stride, u = NBUF == 2 ? k & 1 : 0;
-    if (k + 2 < steps) fetch(spare, i + 2 * stride);
+  // Step k's products on LDS buffer u.
+  auto multiply = [&](int k, int u) {
+    const int i = i0 + k * stride;
     const float* tb = smem + 2 * u * TILE;
     const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
     for (int part = 0; part < parts; ++part) {
@@ -473,21 +469,52 @@ __global__ __launch_bounds__(STATES_THREADS) void states_kernel(Dims d, StateArg
       // 16-token blocks that hold the part's tokens; the weights are zero
       // outside the part.
       const int lo = sb[u].lo[part], hi = lo < sb[u].hi[part] ? sb[u].hi[part] : 0;
-      for (int k0 = lo & ~15; k0 < hi; k0 += 16) {
-        weighted_block(acc, ta, tb, sb[u].wt[part], k0, s, hf);
-      }
+      for (int k0 = lo & ~15; k0 < hi; k0 += 16) weighted_block(acc, ta, tb, sb[u].wt[part], k0, s, hf);
     }
-    if constexpr (NBUF == 2) {
-      if (k + 1 < steps) stage(next, u ^ 1, i + stride);
-    } else {
-      __syncthreads();  // every wave is done with the buffer
-      if (k + 1 < steps) stage(next, 0, i + stride);
-    }
-    __syncthreads();
   };
-  for (int k = 0; k < steps; k += 2) {
-    step(k, R1, R0);
-    if (k + 1 < steps) step(k + 1, R0, R1);
+  if constexpr (NBUF == 1 && BWD) {
+    // One register set, loaded one step ahead (the backward walk's 16 fewer
+    // VGPRs keep three blocks per CU; the other blocks cover the shorter
+    // lead).
+    StepRegs R;
+    fetch(R, i0);
+    stage(R, 0, i0);
+    __syncthreads();
+    if (steps > 1) fetch(R, i0 + stride);
+    for (int k = 0; k < steps; ++k) {
+      multiply(k, 0);
+      __syncthreads();  // every wave is done with the buffer
+      if (k + 1 < steps) {
+        stage(R, 0, i0 + (k + 1) * stride);
+        if (k + 2 < steps) fetch(R, i0 + (k + 2) * stride);
+      }
+      __syncthreads();
+    }
+  } else {
+    StepRegs R0, R1;
+    fetch(R0, i0);
+    if (steps > 1) fetch(R1, i0 + stride);
+    stage(R0, 0, i0);
+    __syncthreads();
+    // Step k multiplies LDS buffer k & 1 (NBUF = 2); `next` holds step k + 1
+    // (staged at the end), `spare` (step k, already staged) receives step
+    // k + 2.
+    auto step = [&](int k, const StepRegs& next, StepRegs& spare) {
+      const int i = i0 + k * stride, u = NBUF == 2 ? k & 1 : 0;
+      if (k + 2 < steps) fetch(spare, i + 2 * stride);
+      multiply(k, u);
+      if constexpr (NBUF == 2) {
+        if (k + 1 < steps) stage(next, u ^ 1, i + stride);
+      } else {
+        __syncthreads();  // every wave is done with the buffer
+        if (k + 1 < steps) stage(next, 0, i + stride);
+      }
+      __syncthreads();
+    };
+    for (int k = 0; k < steps; k += 2) {
+      step(k, R1, R0);
+      if (k + 1 < steps) step(k + 1, R0, R1);
+    }
   }
   put_state((cross ? g.last_c : g.last_s) + edge * 4096 + elem);
 }
