@@ -88,7 +88,10 @@ const char* m4mr_last_error(void);
  * walk per (b, h) state sequence when B*H*(1 + P/64) reaches the device's
  * compute-unit count, else from chunk-parallel statistics plus a carry; the
  * environment variable M4MR_STATE_WALK=fused|split overrides the choice.
- * The factor kernel's two waves per block hand the running evidence over
+ * The fused walks run with one LDS step buffer (three per compute unit)
+ * when they outnumber two per compute unit, else with two;
+ * M4MR_STATE_BUFFERS=1|2 overrides that (the same results either way).
+ * The factor kernel's two waves per pair hand the running evidence over
  * through a bounded wait (M4MR_TURN_POLLS polls, default 65536, about 2 ms);
  * a wait that gives up never yields a plausible wrong answer: every later
  * solution and factor of that block's sequences is NaN.
