@@ -1172,7 +1172,7 @@ int m3_forward_impl(const char* entry, const In* c, const In* b, const In* x, co
   // bfloat16 tiles: two blocks per compute unit.
   const bool bf = std::is_same<In, m3::bf16_t>::value;
   return launch("m3_out", st, [&] {
-    hipLaunchKernelGGL(out, dim3(persistent_grid(B * s.NC * H, bf ? 2 : 1)), dim3(512),
+    hipLaunchKernelGGL(out, dim3(persistent_grid(B * s.NC * H, bf ? 2 : 1)), dim3(bf ? 512 : 1024),
                        bf ? m3::kOutLdsBf16 : m3::kOutLds, st, s, c, b, x, adt, dt, trap_logits,
                        angles, q_bias, k_bias, phases, starts, y);
   });

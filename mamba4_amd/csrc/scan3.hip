@@ -693,19 +693,22 @@ __device__ void phase_table(const Shape& s, const float (&rates)[64 / NW], const
 // 64; zeros past the chunk's tokens), stage_angles writes them into the phase
 // table's [C][LA] layout and phase_table_staged turns them into phases in
 // place.
+template <int NTH = 512>
 __device__ __forceinline__ void fetch_angle_block(const Shape& s, const float* ang, int b, int c,
-                                                  float (&a)[8]) {
+                                                  float (&a)[4096 / NTH]) {
   const Rsrc r = chunk_rsrc(s, ang, b, c, s.A);
   const int tid = tix();
 #pragma unroll
-  for (int k = 0; k < 8; ++k) a[k] = ldb(r, (tid + 512 * k) * 4);
+  for (int k = 0; k < 4096 / NTH; ++k) a[k] = ldb(r, (tid + NTH * k) * 4);
 }
 
-__device__ __forceinline__ void stage_angles(const Shape& s, const float (&a)[8], float* tab) {
+template <int NTH = 512>
+__device__ __forceinline__ void stage_angles(const Shape& s, const float (&a)[4096 / NTH],
+                                             float* tab) {
   const int tid = tix();
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int e = tid + 512 * k;
+  for (int k = 0; k < 4096 / NTH; ++k) {
+    const int e = tid + NTH * k;
     if (e < C * s.A) tab[(e / s.A) * LA + e % s.A] = a[k];
   }
 }
@@ -1106,16 +1109,19 @@ __device__ __forceinline__ int xcd_item(int it, int total) {
 // S = Q K^T and W_ts = e^{p_t - p_s} scale_s (s < t), gamma_t (s = t).
 // LDS: Q [C][LQt], K [C][LQt] (later S o W as [C][LVt]), H0 transposed
 // [PT][LQt] (first the phase table), V transposed [PT][LVt], scalars.  With
-// bfloat16 tiles that is 62 KB, and two blocks share a compute unit (float32:
-// 122 KB, one block).
+// bfloat16 tiles that is 62 KB, and two blocks of eight waves share a compute
+// unit (float32: 122 KB, one block of sixteen waves).
 template <typename In, bool V4>
-__global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const In* bk,
+__global__ __launch_bounds__(is_bf16<In>::value ? 512 : 1024) void out_kernel(Shape s, const In* cq, const In* bk,
                                                   const In* x, const float* adt,
                                                   const float* dt, const float* trap,
                                                   const float* ang, const float* qb,
                                                   const float* kb, const float* theta0,
                                                   const float* starts, In* y) {
   constexpr bool BF = is_bf16<In>::value;
+  // Waves per block: float32 (one 122 KB block per CU) sixteen, four per
+  // SIMD; bfloat16 (two 62 KB blocks per CU) eight.
+  constexpr int NW = BF ? 8 : 16, NTH = 64 * NW;
   // The products' LDS operands: float32, or bfloat16 rounded where written.
   typedef typename Tile<BF>::T TT;
   constexpr int LQt = Tile<BF>::LQt, LVt = Tile<BF>::LVt;
@@ -1136,11 +1142,11 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
   // previous item's products run.
   struct Fetched {
     TokenIn tin;
-    float th, rates[8];
-    typename Raw<In>::Pair u[2][8];
+    float th, rates[4096 / NTH];
+    typename Raw<In>::Pair u[2][64 / NW];
     float2 bs[2];
-    f4 hv[4];
-    typename Raw<In>::Quad vv[2];
+    f4 hv[2048 / NTH];
+    typename Raw<In>::Quad vv[1024 / NTH];
   };
   auto item_of = [&](int it, int& b, int& c, int& h) {
     const int id = xcd_item(it, total);
@@ -1153,11 +1159,11 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
     item_of(it, b, c, h);
     F.tin = fetch_token(s, adt, dt, trap, b, h, c);
     F.th = fetch_phase(s, theta0, b, h, c);
-    fetch_angle_block(s, ang, b, c, F.rates);
+    fetch_angle_block<NTH>(s, ang, b, c, F.rates);
     const float* const bsrc[2] = {qb + (long)h * s.N, kb + (long)h * s.N};
-    fetch_rows<2, 8>(s, src, bsrc, b, c, F.u, F.bs);
-    fetch_state_t<512>(starts + state_offset(s, b, h, c), F.hv);
-    fetch_values_t<512, V4>(s, x, b, c, h, F.vv);
+    fetch_rows<2, NW>(s, src, bsrc, b, c, F.u, F.bs);
+    fetch_state_t<NTH>(starts + state_offset(s, b, h, c), F.hv);
+    fetch_values_t<NTH, V4>(s, x, b, c, h, F.vv);
   };
 
   // Persistent: block i handles items i, i + gridDim.x, ... (b, chunk, h),
@@ -1168,29 +1174,69 @@ __global__ __launch_bounds__(512) void out_kernel(Shape s, const In* cq, const I
   for (; it < total; it += gridDim.x) {
     int b, c, h;
     item_of(it, b, c, h);
-    // Eight waves: wave w owns column half wc = w >> 2 and row block wr =
-    // w & 3, mirrored (3 - (w & 3)) in the second half, so the two waves on
-    // each SIMD (w, w + 4) hold row blocks whose causal work sums to the same.
     const int tid = tix(), l = lane_id(), r = l & 15, q = l >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wc = w >> 2;
-    const int wr = wc ? 3 - (w & 3) : w & 3;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     if (w == 0) token_scalars(F.tin, S);
     if (tid < s.A) th0[tid] = F.th;
-    stage_angles(s, F.rates, tab);
+    stage_angles<NTH>(s, F.rates, tab);
     __syncthreads();
-    phase_table_staged<8>(s, S.dt, th0, tab, false);
+    phase_table_staged<NW>(s, S.dt, th0, tab, false);
     __syncthreads();
     {
       TT* const dst[2] = {qt, kt};
-      rotate_fetched<2, 8, LQt>(s, F.u, F.bs, dst, tab, c);
+      rotate_fetched<2, NW, LQt>(s, F.u, F.bs, dst, tab, c);
     }
     __syncthreads();  // the phase table (in h0's space) is read
     // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
     // every product reads both operands contiguously along k.
-    store_state_t<512, LQt>(F.hv, h0);
-    store_values_t<512, LVt>(F.vv, vt);
+    store_state_t<NTH, LQt>(F.hv, h0);
+    store_values_t<NTH, LVt>(F.vv, vt);
     __syncthreads();
+    if constexpr (NW == 16) {
+      // Sixteen waves: wave w = m + 4 wr (SIMD m) owns row block wr and
+      // column tile wq = (m - wr) mod 4, so every SIMD holds each row block
+      // once and two or three of the ten causal score tiles (eight waves:
+      // 239 us against 266 us at B16 L1024 H24).  The first eight waves
+      // issue the next item's loads before the scores, the others after.
+      const int wq = ((w & 3) - (w >> 2)) & 3, wr2 = w >> 2;
+      const int next = it + gridDim.x;
+      if (w < 8) fetch(F, next < total ? next : it);
+      f4 sco[1], qh[1];
+      zero(sco);
+      zero(qh);
+      if (wq <= wr2) mma<1, LQt, 1, 1, LQt, BF>(sco, qt, 16 * wr2, kt, 16 * wq, 0, NT);
+      if (w >= 8) fetch(F, next < total ? next : it);
+      mma<1, LQt, 1, 1, LQt, BF>(qh, qt, 16 * wr2, h0, 16 * wq, 0, NT);
+      __syncthreads();  // every wave is done with K
+      TT* const gs = kt;
+      if (wq <= wr2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * wr2 + 4 * q + i, u = 16 * wq + r;
+          float wt = 0.f;
+          if (t > u) wt = expf(fminf(S.p[t] - S.p[u], 0.f)) * S.scale[u];
+          else if (t == u) wt = S.gam[t];
+          put(gs + t * LVt + u, sco[0][i] * wt);
+        }
+      }
+      __syncthreads();  // a row block's S o W comes from four waves
+      f4 acc[1];
+      zero(acc);
+      mma<1, LVt, 1, 1, LVt, BF>(acc, gs, 16 * wr2, vt, 16 * wq, 0, 16 * (wr2 + 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wr2 + 4 * q + i, p = 16 * wq + r, tt = c * C + t;
+        if (tt < s.T && p < s.P)
+          st1(y + (tok_index(s, b, tt) * s.H + h) * s.P + p, acc[0][i] + S.ep[t] * qh[0][i]);
+      }
+      __syncthreads();  // the tiles and scalars are read before the next item's staging
+      continue;
+    }
+    // Eight waves: wave w owns column half wc = w >> 2 and row block wr =
+    // w & 3, mirrored (3 - (w & 3)) in the second half, so the two waves on
+    // each SIMD (w, w + 4) hold row blocks whose causal work sums to the same.
+    const int wc = w >> 2, wr = wc ? 3 - (w & 3) : w & 3;
     // The next item's inputs load while this one's products run (no global
     // load is waited for before the next item's staging).  The two waves on
     // a SIMD issue them at different points (before and after the scores),
