@@ -1180,6 +1180,9 @@ __global__ __launch_bounds__(is_bf16<In>::value ? 512 : 1024) void out_kernel(Sh
     if (w == 0) token_scalars(F.tin, S);
     if (tid < s.A) th0[tid] = F.th;
     stage_angles<NTH>(s, F.rates, tab);
+    // The values transposed, [PT][LV] (their region holds no staging
+    // table), while wave 0 derives the token scalars.
+    store_values_t<NTH, LVt>(F.vv, vt);
     __syncthreads();
     phase_table_staged<NW>(s, S.dt, th0, tab, false);
     __syncthreads();
@@ -1188,10 +1191,9 @@ __global__ __launch_bounds__(is_bf16<In>::value ? 512 : 1024) void out_kernel(Sh
       rotate_fetched<2, NW, LQt>(s, F.u, F.bs, dst, tab, c);
     }
     __syncthreads();  // the phase table (in h0's space) is read
-    // The start state and the values transposed ([PT][LQ], [PT][LV]), so that
-    // every product reads both operands contiguously along k.
+    // The start state transposed, [PT][LQ] (as the values), so that every
+    // product reads both operands contiguously along k.
     store_state_t<NTH, LQt>(F.hv, h0);
-    store_values_t<NTH, LVt>(F.vv, vt);
     __syncthreads();
     if constexpr (NW == 16) {
       // Sixteen waves: wave w = m + 4 wr (SIMD m) owns row block wr and
