@@ -9,8 +9,8 @@ through the C ABI with every buffer preallocated in HBM before the timed
 region.  Prints one JSON line with the throughput, the roofline of the
 dominant kernel (HIP events on the launch stream), the factorization's
 fp32 rate (with and without the factor store), factor-streaming bandwidth
-and a CPU baseline (the NumPy oracle on config 0 and on a sample of the same
-workload, on this host's cores).
+and a CPU baseline (the NumPy oracle on config 0 and on one whole batch row
+of the same workload, on this host's cores).
 
 With --workload ref125m the step is the same fwd+bwd at the one shape the
 reference publishes timings for (B=16, L=1024, H=12, D=64, P=128; inputs
@@ -690,13 +690,13 @@ def main_mamba3(args, bf16=False):
     import torch
 
     from mamba4_amd import _lib
-    from oracle import mamba3 as oracle
+    from mamba4_amd.inputs import MAMBA3_ARGS, mamba3_inputs
 
     lib = _lib.load()
     check = _lib.check
     B, T, H, N, P, A = 16, 1024, 24, 128, 64, 32
     NC = (T + 63) // 64
-    host = oracle.inputs(batch=B, length=T, heads=H, dim=N, width=P, angle_count=A, seed=0)
+    host = mamba3_inputs(batch=B, length=T, heads=H, dim=N, width=P, angle_count=A, seed=0)
     host["d_y"] = np.random.default_rng(1).normal(size=host["x"].shape)
     dev = {n: torch.tensor(np.asarray(v, np.float32), device="cuda:0") for n, v in host.items()}
     rows = ("c", "b", "x", "d_y")
@@ -712,11 +712,11 @@ def main_mamba3(args, bf16=False):
     starts = torch.empty(B, H, NC, 8192, **f32)
     phases = torch.empty(B, H, NC, 64, **f32)
     grads = [torch.empty(dev[n].shape, dtype=dev[n].dtype if n == "x" else torch.float32,
-                         device="cuda:0") for n in oracle.ARGS]
+                         device="cuda:0") for n in MAMBA3_ARGS]
     nbytes = lib.m3s_backward_workspace_bytes(B, T, H, N, P, A)
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
     st = torch.cuda.current_stream().cuda_stream
-    ins = [dev[n].data_ptr() for n in oracle.ARGS]
+    ins = [dev[n].data_ptr() for n in MAMBA3_ARGS]
     dims = (B, T, H, N, P, A)
 
     def step():
@@ -872,13 +872,11 @@ def cpu_baseline(data, workload, config0=True):
     """The CPU baseline of the plan in BASELINE.md: this build's NumPy
     restatement of the reference algorithm (oracle.memread, float32) on this
     host, BLAS on every core, one warm-up then the median of five runs,
-    forward and forward+backward.  Config 0 runs in full; the benchmarked
-    workload on a sample of it (head 0 of batch row 0: the oracle's per-token
-    loop costs about the same for one head as the GPU's batch costs per
-    token-head, while a whole row takes minutes), scaled to the metric's
-    tokens/s by the workload's head count."""
-    heads = data["keys"].shape[2]
-    sample = {n: (a[:1, :, :1] if n != "floor" else a[:1]) for n, a in data.items()}
+    forward and forward+backward.  Config 0 runs in full.  The benchmarked
+    workload runs on one whole batch row (B=1, every head, the full length):
+    the oracle's cost is linear in the batch, so the row's tokens/s is the
+    CPU's tokens/s for the whole batch, measured rather than scaled."""
+    sample = {n: (a[:1] if n != "floor" else a) for n, a in data.items()}
     legs = {}
     if config0:
         from mamba4_amd.inputs import workload_inputs
@@ -886,21 +884,20 @@ def cpu_baseline(data, workload, config0=True):
         for label, leg in oracle_legs(workload_inputs("config0", seed=0, cotangents=True)).items():
             legs["config0_" + label + "_tokens_per_s"] = leg["token_heads_per_s"]
     sampled = oracle_legs(sample)
+    _, T, H, _ = sample["keys"].shape
     for label, leg in sampled.items():
-        legs[workload + "_" + label + "_tokens_per_s"] = leg["token_heads_per_s"] / heads
-    T = data["keys"].shape[1]
+        legs[workload + "_" + label + "_tokens_per_s"] = T / leg["median_s"]
     threads = os.environ.get("OPENBLAS_NUM_THREADS")
     return {
-        "value": sampled["fwd_bwd"]["token_heads_per_s"] / heads,
+        "value": T / sampled["fwd_bwd"]["median_s"],
         "unit": "tokens/s",
         "cores": int(threads or CORES),
         "kind": "port",
         "sample": (
-            f"oracle.memread fwd+bwd in float32 NumPy on head 0 of batch row 0 of the "
-            f"{workload} workload (B=1, L={T}, H=1), median of 5 after 1 warm-up "
-            f"({sampled['fwd_bwd']['median_s']:.3f} s), scaled to tokens/s of the "
-            f"{heads}-head workload; config 0 in full; BLAS threads = {threads}, "
-            f"{CORES} cores in the affinity mask"
+            f"oracle.memread fwd+bwd in float32 NumPy on batch row 0 of the {workload} "
+            f"workload (B=1, L={T}, H={H}: {T} tokens), median of 5 after 1 warm-up "
+            f"({sampled['fwd_bwd']['median_s']:.3f} s per row); config 0 in full; "
+            f"BLAS threads = {threads}, {CORES} cores in the affinity mask"
         ),
         "cpu_model": cpu_model(),
         "legs": legs,

@@ -12,6 +12,9 @@
  * Shapes: B batch, T tokens, H heads (<= M3S_MAX_HEADS), N state width (even,
  * <= M3S_MAX_STATE), P value width per head (<= M3S_MAX_VALUE), A angle rates
  * (A <= N/2); chunks of M3S_CHUNK tokens, NC = ceil(T / M3S_CHUNK).
+ * Limits: B*T*H*P and B*T*N below 2^31 elements, and NC * M3S_CHUNK below
+ * 2^22 tokens (T <= 2^22 - 64; the backward addresses per-batch-row
+ * partials with 32-bit byte offsets).
  * Alignment: c, b and the biases 8 bytes; x, d_y, starts 16 bytes.
  */
 #ifndef MAMBA3_SCAN_H

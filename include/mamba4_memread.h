@@ -265,7 +265,10 @@ int m4mr_backward_bf16(const uint16_t* keys, const uint16_t* values, const uint1
  * backward's intermediates (z, the end-state cotangents, the per-chunk floor
  * partials) live in a static device buffer of M4MR_STATIC_SCRATCH_BYTES
  * (128 MiB) that each GPU the library runs on holds until the process ends;
- * its address on a device is resolved at the first call on that device.
+ * its address on a device is resolved at the first call on that device, so
+ * make that first call outside any graph capture.  Its kernels use no
+ * runtime-provided scratch either: it takes the backward state walk that
+ * spills no registers, whatever the batch size or M4MR_STATE_BUFFERS.
  * Sizes whose m4mr_backward_workspace_bytes exceeds it return M4MR_EINVAL
  * before any launch (128 MiB holds B*T*H = 131072 token-heads at P = 64,
  * BASELINE config 2, with room to spare).  Every call on one GPU shares that

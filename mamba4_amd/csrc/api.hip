@@ -426,7 +426,7 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                   const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
                   float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
                   float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream,
-                  const m4::MixerIn& mix = {}) {
+                  const m4::MixerIn& mix = {}, bool spill_free = false) {
   g_error.clear();
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
@@ -474,7 +474,11 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                              d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
                              d_init_evidence,  d_init_cross};
     rc = launch("bwd_states", st, [&] {
-      const bool one = states_single_buffer(B, H, d);
+      // The one-buffer walk spills two registers to per-lane scratch, device
+      // memory the HIP runtime provides with the dispatch; a caller that
+      // allocates nothing (spill_free) takes the two-buffer walk, which does
+      // not spill and gives the same states.
+      const bool one = !spill_free && states_single_buffer(B, H, d);
       const auto walk = one ? m4::states_kernel<true, float, false, 1> : m4::states_kernel<true, float, false, 2>;
       hipLaunchKernelGGL(walk, dim3(B * H, 1 + d.NV), dim3(512),
                          (one ? kStatesLdsBytes / 2 : kStatesLdsBytes) + kStatesBwdExtra, st, d,
@@ -714,7 +718,8 @@ int m4mr_backward_noalloc(const float* keys, const float* values, const float* q
       "m4mr_backward_noalloc", keys, values, queries, beta, log_decay, floor, B, T, H, value_dim,
       chunk, solved, factors, start_evidence, start_cross, d_output, d_variance,
       d_final_evidence, d_final_cross, d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor,
-      d_init_evidence, d_init_cross, ws, (size_t)M4MR_STATIC_SCRATCH_BYTES, stream);
+      d_init_evidence, d_init_cross, ws, (size_t)M4MR_STATIC_SCRATCH_BYTES, stream, {},
+      /*spill_free=*/true);
 }
 
 int m4mr_factored_solve(const float* factors, const float* rhs, float* z, long N,
@@ -1127,6 +1132,11 @@ bool m3_bad_shape(const char* entry, int B, int T, int H, int N, int P, int A) {
   else if (A < 0 || 2 * A > N) why = "need 0 <= A <= N/2";
   else if ((long)B * T * H * P >= (1L << 31) || (long)B * T * N >= (1L << 31))
     why = "arrays above 2^31 elements";
+  // The backward's finish kernel reads each (head group, batch row) slab of
+  // its row-gradient partials, ceil(T / C) * C tokens of NT floats, through
+  // one buffer resource, whose size and offsets are 32-bit byte counts.
+  else if ((long)(T + m3::C - 1) / m3::C * m3::C * m3::NT * 4 >= (1L << 31))
+    why = "T above 2^22 - 64 tokens";
   if (why.empty()) return false;
   fail(M4MR_EINVAL, std::string(entry) + ": " + why);
   return true;

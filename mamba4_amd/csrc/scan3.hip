@@ -81,7 +81,10 @@ struct Raw<bf16_t> {
 // loads issued after the awaited one instead of draining them all.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 constexpr unsigned kNoLoad = 0x80000000u;  // an offset past every resource here
-// bytes < 2^31 (every array has fewer than 2^31 elements).
+// bytes < 2^31: the host rejects shapes whose largest resource (one
+// (group, batch) slab of the finish kernel's row-gradient partials,
+// ceil(T / C) * C * NT floats) would reach 2^31 bytes; every other resource
+// spans one chunk or one row.
 __device__ __forceinline__ Rsrc rsrc(const void* base, long bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);

@@ -317,7 +317,8 @@ __device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const 
 // In: element type of the forward's key and value rows (the backward's rows
 // are float32).
 // The one-buffer backward walk is held to six waves per SIMD (three blocks
-// per CU, as its LDS allows).
+// per CU, as its LDS allows); at that budget (80 VGPRs) it spills two
+// registers to per-lane scratch, which the two-buffer walks do not.
 template <bool BWD, typename In, bool MIX, int NBUF>
 __global__ __launch_bounds__(STATES_THREADS)
 __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kernel(Dims d,
@@ -362,8 +363,9 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   // (which need not be symmetric): acc holds A, dfin and dscale hold D, and
   // A^T comes back through an LDS tile when a state is stored.  Both step
   // buffer counts do this, so a batch's rows give the same bits whichever
-  // variant the batch size selects (its 96 VGPRs leave the one-buffer
-  // backward walk two blocks per CU, not three).
+  // variant the batch size selects.  The symmetric store needs 98 VGPRs in
+  // the two-buffer walk; the one-buffer walk is held to 80 for three blocks
+  // per CU and spills two of them.
   const bool sym = BWD && !cross;
   f4 dfin[2];
   float dscale = 1.f;

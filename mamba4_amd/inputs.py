@@ -181,3 +181,27 @@ def reference_benchmark_inputs(batch=16, length=1024, heads=12, dim=64, width=12
         phase = np.arange(like.size, dtype=np.float32) * np.float32(factor)
         out[name] = np.cos(phase).astype(np.float32).reshape(like.shape)
     return out
+
+
+# The Mamba-3 scan's nine inputs, in the order of mamba3_fused's arguments
+# (lm/kernels/flashmamba.py:1125-1162) and of m3s_forward.
+MAMBA3_ARGS = ["c", "b", "x", "adt", "dt", "trap", "angles", "q_bias", "k_bias"]
+
+
+def mamba3_inputs(batch=2, length=37, heads=3, dim=16, width=8, angle_count=4, seed=0):
+    """Seeded float64 inputs of the Mamba-3 scan in the reference tests'
+    ranges (lm/tests/test_flashmamba.py:104-118): standard-normal rows, dt a
+    softplus of N(-1, 1), adt = -dt * U(0.5, 2), N(0,1) trap logits and
+    angle rates, biases 0.1 N(0,1)."""
+    rng = np.random.default_rng(seed)
+    c = rng.normal(size=(batch, length, dim))
+    b = rng.normal(size=(batch, length, dim))
+    x = rng.normal(size=(batch, length, heads * width))
+    dt = np.log1p(np.exp(rng.normal(size=(batch, length, heads)) - 1))
+    adt = -dt * rng.uniform(0.5, 2.0, size=dt.shape)
+    trap = rng.normal(size=dt.shape)
+    angles = rng.normal(size=(batch, length, angle_count))
+    q_bias = rng.normal(size=(heads, dim)) * 0.1
+    k_bias = rng.normal(size=(heads, dim)) * 0.1
+    return dict(c=c, b=b, x=x, adt=adt, dt=dt, trap=trap, angles=angles, q_bias=q_bias,
+                k_bias=k_bias)

@@ -244,21 +244,11 @@ def backward(c, b, x, adt, dt, trap, angles, q_bias, k_bias, d_y, d_final=None):
 
 def inputs(batch=2, length=37, heads=3, dim=16, width=8, angle_count=4, seed=0):
     """Seeded inputs in the reference tests' ranges
-    (lm/tests/test_flashmamba.py:104-118): standard-normal rows, dt a
-    softplus of N(-1, 1), adt = -dt * U(0.5, 2), N(0,1) trap logits and
-    angle rates, biases 0.1 N(0,1)."""
-    rng = np.random.default_rng(seed)
-    c = rng.normal(size=(batch, length, dim))
-    b = rng.normal(size=(batch, length, dim))
-    x = rng.normal(size=(batch, length, heads * width))
-    dt = np.log1p(np.exp(rng.normal(size=(batch, length, heads)) - 1))
-    adt = -dt * rng.uniform(0.5, 2.0, size=dt.shape)
-    trap = rng.normal(size=dt.shape)
-    angles = rng.normal(size=(batch, length, angle_count))
-    q_bias = rng.normal(size=(heads, dim)) * 0.1
-    k_bias = rng.normal(size=(heads, dim)) * 0.1
-    return dict(c=c, b=b, x=x, adt=adt, dt=dt, trap=trap, angles=angles, q_bias=q_bias,
-                k_bias=k_bias)
+    (lm/tests/test_flashmamba.py:104-118); the generator lives with the
+    package's other synthetic inputs (mamba4_amd.inputs.mamba3_inputs)."""
+    from mamba4_amd.inputs import mamba3_inputs
+
+    return mamba3_inputs(batch, length, heads, dim, width, angle_count, seed)
 
 
 ARGS = ["c", "b", "x", "adt", "dt", "trap", "angles", "q_bias", "k_bias"]

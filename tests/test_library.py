@@ -134,3 +134,21 @@ def test_noalloc_backward_rejects_sizes_beyond_its_static_buffer():
     message = lib.m4mr_last_error().decode()
     assert "static" in message and "m4mr_backward" in message
 
+
+
+def test_mamba3_shapes_past_the_finish_kernels_32_bit_slabs_are_rejected():
+    """The Mamba-3 backward's finish kernel addresses one (head group, batch)
+    slab of its row-gradient partials, ceil(T/64)*64 tokens of 128 floats,
+    with 32-bit byte offsets; the shape check refuses any T whose slab would
+    reach 2^31 bytes, before any HIP call (every array itself is below 2^31
+    elements at B = H = P = 1)."""
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    for entry in (lib.m3s_forward, lib.m3s_forward_bf16):
+        rc = entry(*([null] * 9), 1, 1 << 22, 1, 128, 1, 0, *([null] * 4), null)
+        assert rc == _lib.EINVAL
+        assert "T above" in lib.m4mr_last_error().decode()
+        # The longest accepted T passes the shape check and fails on the NULLs.
+        rc = entry(*([null] * 9), 1, (1 << 22) - 64, 1, 128, 1, 0, *([null] * 4), null)
+        assert rc == _lib.EINVAL
+        assert "NULL" in lib.m4mr_last_error().decode()
