@@ -118,11 +118,11 @@ constexpr std::integer_sequence<int, (Off + I)...> offset_sequence(std::integer_
 // A[I][16K + c], c = 0..15 (the slot layout above).  "Exchanged": lane
 // (g, j) holds in A[I][16K + 4mu + e] element (16I + j, 16K + 4g + e) of
 // matrix mu.  exchange_block converts one 16x16 block of all four matrices
-// between the two (it is its own inverse).  Exchanged is the operand layout
-// of v_mfma_f32_16x16x4_f32 for a 16x16 block (A(i, k) in lane i + 16k: row
-// i of the block, column 4k + e in MFMA step e) and also its accumulator
-// layout for a product whose rows are block columns (D(i, j) in lane
-// j + 16(i/4), element i%4).
+// between the two (it is its own inverse).  Exchanged is the accumulator
+// layout of v_mfma_f32_16x16x1_4b_f32 for four blocks whose rows are block
+// columns, and rows is that instruction's operand layout (panel_block), so
+// the trailing updates read the panel in rows and accumulate in exchanged;
+// only a trailing block column that becomes the next panel is exchanged.
 
 // One elimination step of column J inside its 16-column panel P = J/16,
 // with the forward substitution of the right-hand side r folded in: the
@@ -194,24 +194,30 @@ __device__ __forceinline__ void exchange_block(float (&row)[64]) {
     exchange_quads(row[C0 + e], row[C0 + 4 + e], row[C0 + 8 + e], row[C0 + 12 + e]);
 }
 
-// Trailing block (I, K) after panel P, both in the exchanged layout:
-// A_IK += L_IP L_KP^T for all four matrices (the working matrix is negated).
-// MFMA step e of matrix mu takes A = block (K, P) and B = block (I, P) in
-// register 16P + 4mu + e, so D(i, j) = sum_c l_{16K+i, c} l_{16I+j, c} lands
-// on element (16I + j, 16K + i): accumulator mu is A[I][16K + 4mu .. +3].
+typedef float f16 __attribute__((ext_vector_type(16)));
+
+// Trailing block (I, K) after panel P: A_IK += L_IP L_KP^T for all four
+// matrices (the working matrix is negated), the block in the exchanged
+// layout, the panel's L blocks in the rows layout.  v_mfma_f32_16x16x1_4b_f32
+// takes its A and B operands as four 16-lane rows, one per block b (lane
+// 16b + i holds A_b[i], lane 16b + j holds B_b[j]), which is the rows layout
+// of column c of a slot, and leaves D_b[i][j] += A_b[i] B_b[j] in lane
+// j + 16(i/4), register 4b + i%4 (both checked on gfx950 with an in-bounds
+// probe).  With A = column 16P + c of slot K and B = the same column of slot
+// I, D_mu[i][j] is element (16I + j, 16K + i) of matrix mu: register
+// A[I][16K + 4mu + e] of lane (g, j) with i = 4g + e, the exchanged layout.
+// Sixteen such rank-one products, one per panel column, make the update, and
+// the panel's blocks need no exchange.
 template <int P, int I, int K>
 __device__ __forceinline__ void panel_block(float (&A)[4][64]) {
+  f16 acc;
 #pragma unroll
-  for (int mu = 0; mu < 4; ++mu) {
-    f4 acc = f4{A[I][16 * K + 4 * mu], A[I][16 * K + 4 * mu + 1], A[I][16 * K + 4 * mu + 2],
-                A[I][16 * K + 4 * mu + 3]};
+  for (int r = 0; r < 16; ++r) acc[r] = A[I][16 * K + r];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[K][16 * P + 4 * mu + e],
-                                                 A[I][16 * P + 4 * mu + e], acc, 0, 0, 0);
+  for (int c = 0; c < 16; ++c)
+    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(A[K][16 * P + c], A[I][16 * P + c], acc, 0, 0, 0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) A[I][16 * K + 4 * mu + e] = acc[e];
-  }
+  for (int r = 0; r < 16; ++r) A[I][16 * K + r] = acc[r];
 }
 
 // Slots I > P of block column C, exchanged in place.
@@ -223,13 +229,10 @@ __device__ __forceinline__ void exchange_below(float (&A)[4][64]) {
 }
 
 // Rank-16 update of the trailing blocks after panel P, then the next panel's
-// block column back to the rows layout.  The panel's L blocks go to the
-// exchanged layout for the MFMA and back to rows for the solves and the
-// store; the blocks of the next panel are updated first.
+// block column back to the rows layout (its blocks are updated first).
 template <int P>
 __device__ __forceinline__ void panel_update(float (&A)[4][64]) {
   if constexpr (P < 3) {
-    exchange_below<P, P>(A);
     if constexpr (P == 0) {
       panel_block<0, 1, 1>(A);
       panel_block<0, 2, 1>(A);
@@ -244,7 +247,6 @@ __device__ __forceinline__ void panel_update(float (&A)[4][64]) {
     } else {
       panel_block<2, 3, 3>(A);
     }
-    exchange_below<P, P>(A);
     exchange_below<P, P + 1>(A);
   }
 }
