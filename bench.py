@@ -83,6 +83,7 @@ CHOLESKY_FLOP = 89440  # D^3/3 + D^2/2 + D/6 at D = 64
 RESOLVE_BYTES = 8832  # factor + rhs + z per token-head in the backward re-solve
 
 NAMES = ["keys", "values", "queries", "beta", "log_decay", "floor"]
+CAUSAL_PAIRS = 2080  # (t, s) pairs with s <= t in a 64-token chunk
 
 # Algorithmic work per token-head of each kernel at D = P = 64, chunk 64:
 # (bound, amount, unit).  HBM kernels count the bytes their algorithm must
@@ -90,9 +91,14 @@ NAMES = ["keys", "values", "queries", "beta", "log_decay", "floor"]
 KERNEL_WORK = {
     "fwd_factor": ("hbm", FACTOR_BYTES, "B"),
     "factored_solve": ("hbm", RESOLVE_BYTES, "B"),
-    "fwd_read": ("mfma", 3 * 8192, "flop"),  # Y K^T, (G) V, Y C0^T
-    "bwd_dy": ("mfma", 3 * 8192, "flop"),  # dO V^T, (G) K, dO C0
-    "bwd_grads": ("mfma", 13 * 8192, "flop"),  # 13 chunk products
+    # Causal products count their s <= t pairs only (64 * 65 / 2 = 2,080 of
+    # 4,096 per 64-token chunk, i.e. 2 * 2,080 flop per token-head at width
+    # 64); full chunk products count 2 * 4,096.
+    "fwd_read": ("mfma", 2 * (2 * CAUSAL_PAIRS + 4096), "flop"),  # Y K^T, (G) V causal; Y C0^T
+    "bwd_dy": ("mfma", 2 * (2 * CAUSAL_PAIRS + 4096), "flop"),  # dO V^T, (G) K causal; dO C0
+    # gy, gz, gv and the three masked contractions over t causal; G^T k, G k,
+    # H k, H^T v, y^T S0, dO^T C0 full
+    "bwd_grads": ("mfma", 2 * (6 * CAUSAL_PAIRS + 6 * 4096), "flop"),
     "fwd_stats": ("mfma", 2 * 8192, "flop"),  # K^T diag K, V^T diag K
     "fwd_scan": ("hbm", 16384 * 3 * 2 // 64, "B"),  # r+w of 2 evidence + 1 cross state / chunk
     "bwd_local": ("mfma", 2 * 8192, "flop"),  # Z^T diag Y, dO^T diag Y

@@ -99,6 +99,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ ChunkScalars cs;
   __shared__ float var_s[MIX ? MAXC : 1];  // MIX: the chunk's variances, for the gate
   const long nseq = (long)d.B * d.H * d.NC;
+  // The wave's 16-row strip (its causal products cost strip + 1 blocks).
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     f4 acc[4];
     zero4(acc);
-    tile_mma<false, true>(acc, Y, K, 64, w);  // scores y_t . k_s
+    tile_mma_causal<false>(acc, Y, K, w);  // scores y_t . k_s, s <= t
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
@@ -209,7 +210,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       f4 out[4], inh[4];
       zero4(out);
       zero4(inh);
-      tile_mma<false, false>(out, G, K, k_terms(si.len), w);  // within-chunk reads
+      // within-chunk reads: G[t][s] is zero past s = t
+      tile_mma_causal_terms<false, false>(out, G, K, si.len, w);
       tile_mma<false, false>(inh, Y, C0, 64, w);              // inherited reads y_t . C0[p]
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -260,6 +262,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* C0 = G + TILE;
   __shared__ ChunkScalars cs;
   const long nseq = (long)d.B * d.H * d.NC;
+  // The wave's 16-row strip (its causal products cost strip + 1 blocks).
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
@@ -349,7 +352,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
         fetch_scalars(sn);
       }
-      tile_mma<false, true>(acc, DO, V, 64, w);    // dout_t . v_s
+      tile_mma_causal<false>(acc, DO, V, w);      // dout_t . v_s, s <= t
       tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
     }
 #pragma unroll
@@ -371,7 +374,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     f4 within[4];
     zero4(within);
-    tile_mma<false, false>(within, G, V, k_terms(si.len), w);  // sum_s G[t][s] k_s
+    // sum_s G[t][s] k_s: G[t][s] is zero past s = t
+    tile_mma_causal_terms<false, false>(within, G, V, si.len, w);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int t = acc_row(w, q);

@@ -240,9 +240,11 @@ __device__ inline void load_chunk_scalars(ChunkScalars& cs, const Dims& d, const
 //                 accumulators are four adjacent columns of one row and a
 //                 k-major B (TB = false) arrives in one 16-byte read per e.
 // TB = false with QUAD = false falls back to scalar B reads.
+// nb < 4 (TB = true, QUAD = false only; uniform over the wave): only the
+// first nb column blocks are computed, the others left as they are.
 template <bool TA, bool TB, bool QUAD>
 __device__ __forceinline__ void mma_block(f4 acc[4], const float* A, const float* B, int k0,
-                                          int w) {
+                                          int w, int nb = 4) {
   const int l = lane_id(), r = l & 15, kk = k0 + 4 * (l >> 4);
   f4 a;
   if (TA) {
@@ -256,14 +258,14 @@ __device__ __forceinline__ void mma_block(f4 acc[4], const float* A, const float
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int col = QUAD ? 4 * r + jb : 16 * jb + r;
-      b[jb] = *reinterpret_cast<const f4*>(B + col * LDT + kk);
+      if (jb < nb) b[jb] = *reinterpret_cast<const f4*>(B + col * LDT + kk);
     }
     // Consecutive MFMAs go to different accumulators (no dependent chain).
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb)
-        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[jb][e], acc[jb], 0, 0, 0);
+        if (jb < nb) acc[jb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[jb][e], acc[jb], 0, 0, 0);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -288,6 +290,52 @@ __device__ __forceinline__ void tile_mma(f4 acc[4], const float* A, const float*
     for (int k0 = 0; k0 < 64; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
   } else {
     for (int k0 = 0; k0 < K; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
+  }
+}
+
+// The causal scores of strip w: A B^T (B k-contiguous) for the column
+// blocks jb <= w only, the blocks a mask s <= t keeps; the others are left
+// as they are (the caller masks them to zero).  One straight-line body per
+// strip (w is uniform over the wave).
+template <bool TA, int NB>
+__device__ __forceinline__ void tile_mma_cols(f4 acc[4], const float* A, const float* B, int w) {
+#pragma unroll
+  for (int k0 = 0; k0 < 64; k0 += 16) mma_block<TA, true, false>(acc, A, B, k0, w, NB);
+}
+template <bool TA>
+__device__ __forceinline__ void tile_mma_causal(f4 acc[4], const float* A, const float* B, int w) {
+  switch (w) {
+    case 0: tile_mma_cols<TA, 1>(acc, A, B, w); break;
+    case 1: tile_mma_cols<TA, 2>(acc, A, B, w); break;
+    case 2: tile_mma_cols<TA, 3>(acc, A, B, w); break;
+    default: tile_mma_cols<TA, 4>(acc, A, B, w); break;
+  }
+}
+
+// A B over the token terms s <= t of strip w (A a causally masked score
+// tile, zero past the chunk's len tokens): 16 (w + 1) terms, fewer for a
+// short chunk; one unrolled body per strip when the chunk is full.
+template <bool TA, bool TB, bool QUAD = !TB>
+__device__ __forceinline__ void tile_mma_causal_terms(f4 acc[4], const float* A, const float* B,
+                                                      int len, int w) {
+  if (len >= 16 * (w + 1)) {
+    switch (w) {
+      case 0: mma_block<TA, TB, QUAD>(acc, A, B, 0, w); break;
+      case 1:
+#pragma unroll
+        for (int k0 = 0; k0 < 32; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
+        break;
+      case 2:
+#pragma unroll
+        for (int k0 = 0; k0 < 48; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
+        break;
+      default:
+#pragma unroll
+        for (int k0 = 0; k0 < 64; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
+        break;
+    }
+  } else {
+    for (int k0 = 0; k0 < len; k0 += 16) mma_block<TA, TB, QUAD>(acc, A, B, k0, w);
   }
 }
 
