@@ -36,7 +36,10 @@ forward and backward; every kernel is HBM-bound and reported against 8 TB/s.
 With --workload mixer_read a step is the mixer's memory path forward at the
 config-2 shape through the fused entry point (m4mr_mixer_forward: prologue,
 memory read and read gating in one pass over the raw projections); the same
-forward through the three separate entry points is timed beside it.
+forward through the three separate entry points is timed beside it.  The
+training step (forward and m4mr_mixer_read_backward, the whole VJP in one
+launch sequence) is timed against the separate entry points' and against
+the fused forward with the three separate backward calls.
 
 With --workload mamba3 a step is the FlashMamba Mamba-3 scan (mamba3_fused,
 lm/kernels/flashmamba.py:1125-1162) forward and backward at the 125M model's
@@ -602,8 +605,27 @@ def main_mixer_read(args):
             p(floor_raw), None, B, T, H, D, 1.0, 1, p(g_mem[0]), p(g_mem[2]), p(g_mem[3]),
             p(g_mem[4]), p(g_mem[5]), None, *(p(g) for g in g_pro), None, p(mix_ws), mix_bytes,
             st))
+        g_mem[1].add_(d_val_skip)  # the value's two paths meet
+
+    # The whole mixer VJP in one launch sequence (m4mr_mixer_read_backward).
+    mr_bytes = lib.m4mr_mixer_read_backward_workspace_bytes(B, T, H, D, 64)
+    mr_ws = torch.empty(mr_bytes, dtype=torch.uint8, device="cuda:0")
+    g_mr = [e(B, T, H, D, **f32), e(B, T, H, D, **f32), e(B, T, H, D, **f32), e(B, T, H, **f32),
+            e(B, T, H, **f32), e(H, **f32), e(H, **f32), e(H, **f32), e(H, D, **f32)]
+    g_mr_tail = [e(H, **f32), e(H, **f32), e(B, H, D, D, **f32), e(B, H, D, D, **f32)]
+
+    def fused_backward():
+        check(lib.m4mr_mixer_read_backward(
+            p(key), p(value), p(query), p(dt_raw), ctypes.byref(params), B, T, H, D, 64, p(read),
+            p(variance), p(beta), p(log_decay), p(floor), p(solved), p(factors), p(start_s),
+            p(start_c), p(d_out), None, None, None, None, *(p(g) for g in g_mr), None,
+            *(p(g) for g in g_mr_tail), p(mr_ws), mr_bytes, st))
 
     def fused_train():
+        fused()
+        fused_backward()
+
+    def partial_train():
         fused()
         backward(True)
 
@@ -628,10 +650,26 @@ def main_mixer_read(args):
     runs = [(timed(fused, args.steps), timed(separate, args.steps)) for _ in range(3)]
     seconds = min(r[0] for r in runs)
     separate_seconds = min(r[1] for r in runs)
-    train = [(timed(fused_train, args.steps), timed(separate_train, args.steps))
-             for _ in range(3)]
+    train = [(timed(fused_train, args.steps), timed(separate_train, args.steps),
+              timed(partial_train, args.steps)) for _ in range(3)]
     train_seconds = min(r[0] for r in train)
     separate_train_seconds = min(r[1] for r in train)
+    partial_train_seconds = min(r[2] for r in train)
+    # Per-kernel milliseconds per fused training step (library timers).
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    profiled = min(args.steps, 10)
+    for _ in range(profiled):
+        fused_train()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    kernel_ms = {}
+    for name in _lib.kernel_names():
+        total, count = _lib.profile_read(name)
+        if count:
+            kernel_ms[name] = total / profiled
+    _lib.profile_reset()
     line = {
         "metric": MIXER_READ_METRIC,
         "value": B * T / seconds,
@@ -652,6 +690,8 @@ def main_mixer_read(args):
         "train_ms_per_step": train_seconds * 1e3,
         "separate_train_ms_per_step": separate_train_seconds * 1e3,
         "train_speedup": separate_train_seconds / train_seconds,
+        "partial_train_ms_per_step": partial_train_seconds * 1e3,
+        "train_kernel_ms": kernel_ms,
     }
     print(json.dumps(line), flush=True)
 

@@ -201,6 +201,54 @@ int m4mr_mixer_backward(const float* key, const float* value, const float* query
                         float* d_init_evidence, float* d_init_cross,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of device workspace m4mr_mixer_read_backward needs for these sizes. */
+size_t m4mr_mixer_read_backward_workspace_bytes(int B, int T, int H, int value_dim, int chunk);
+
+/*
+ * Backward of m4mr_mixer_forward as a whole: the VJP of the read gating
+ * (m4mr_epilogue_backward), of the memory read from the raw keys and
+ * queries (m4mr_mixer_backward) and of the prologue (m4mr_prologue_backward)
+ * in one launch sequence.  The gating's VJP runs inside the first backward
+ * kernel (it forms g d_output and the variance cotangent as it loads each
+ * chunk), the prologue's inside the last (the unit normalisations' VJP to
+ * the raw key and query rows, the gates' to beta_raw and dt_raw, per-chunk
+ * partials of the per-head gradients); the state walk weighs the read's
+ * cotangent by the gate.  Equal to the three calls in a row to float32
+ * rounding (sums in another order).  Replaces, in the mixer's backward, the
+ * VJP of lm/models/mamba4.py:183-273 that the reference's autodiff takes
+ * through the prologue, selective_gaussian_memory and the gating.
+ *
+ * key, query [B,T,H,D] raw projections, value [B,T,H,P], dt_raw [B,T,H]
+ * and params as given to m4mr_mixer_forward; read, variance, beta,
+ * log_decay, floor, solved, factors, start_evidence, start_cross as it
+ * returned them (factors stored).  Cotangents: d_output [B,T,H,P] of the
+ * gated output (required), d_variance [B,T,H] (NULL: zero), the final
+ * states' (NULL: zero) and d_shifted [B,H,D] of `shifted` (NULL: zero).
+ * Gradients: d_key, d_query [B,T,H,D]; d_value [B,T,H,P]; d_beta_raw,
+ * d_dt_raw [B,T,H]; d_beta_bias, d_dt_bias, d_a_log, d_confidence_scale,
+ * d_skip [H]; d_floor_raw [H,D]; d_previous [B,H,D] (may be NULL; zero
+ * without the key shift); d_init_evidence, d_init_cross as m4mr_backward.
+ * workspace: m4mr_mixer_read_backward_workspace_bytes, 256-byte aligned.
+ * Always takes the fused state walk.
+ */
+int m4mr_mixer_read_backward(const float* key, const float* value, const float* query,
+                             const float* dt_raw, const m4mr_mixer_params* params,
+                             int B, int T, int H, int value_dim, int chunk,
+                             const float* read, const float* variance,
+                             const float* beta, const float* log_decay, const float* floor,
+                             const float* solved, const float* factors,
+                             const float* start_evidence, const float* start_cross,
+                             const float* d_output, const float* d_variance,
+                             const float* d_final_evidence, const float* d_final_cross,
+                             const float* d_shifted,
+                             float* d_key, float* d_value, float* d_query,
+                             float* d_beta_raw, float* d_dt_raw,
+                             float* d_beta_bias, float* d_dt_bias, float* d_a_log,
+                             float* d_floor_raw, float* d_previous,
+                             float* d_confidence_scale, float* d_skip,
+                             float* d_init_evidence, float* d_init_cross,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* Number of chunks NC and of evidence start states NS for T tokens. */
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts);
 

@@ -54,6 +54,12 @@ SIGNATURES = {
         [_P] * 5 + [ctypes.POINTER(MixerParams)] + [_P] * 2 + [_I] * 5 + [_P] * 13 + [_P],
     ),
     "m4mr_backward_workspace_bytes": (_S, [_I] * 5),
+    "m4mr_mixer_read_backward_workspace_bytes": (_S, [_I] * 5),
+    "m4mr_mixer_read_backward": (
+        _I,
+        [_P] * 4 + [ctypes.POINTER(MixerParams)] + [_I] * 5 + [_P] * 9 + [_P] * 5 + [_P] * 14
+        + [_P, _S, _P],
+    ),
     "m4mr_mixer_backward": (
         _I,
         [_P] * 7 + [_I] * 6 + [_P] * 4 + [_P] * 4 + [_P] * 8 + [_P, _S, _P],

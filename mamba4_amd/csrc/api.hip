@@ -41,16 +41,16 @@ template <typename In, bool MIX>
 __global__ void fwd_read_kernel(Dims, const In*, const In*, const In*, const float*,
                                 const float*, const float*, const float*, float*, float*, MixerIn,
                                 ReadGate);
-template <typename In, bool MIX>
+template <typename In, bool MIX, bool GATE>
 __global__ void bwd_dy_kernel(Dims, const In*, const In*, const In*, const float*,
                               const float*, const float*, const float*, const float*, float*,
-                              MixerIn);
-template <typename In, bool MIX>
+                              MixerIn, MixerGrad);
+template <typename In, bool MIX, bool GATE>
 __global__ void bwd_grads_kernel(Dims, const In*, const In*, const float*, const float*,
                                  const float*, const float*, const float*, const float*,
                                  const float*, const float*, const float*, const float*, float*,
-                                 float*, float*, float*, float*, float*, MixerIn);
-__global__ void floor_reduce_kernel(Dims, const float*, float*);
+                                 float*, float*, float*, float*, float*, MixerIn, MixerGrad);
+__global__ void floor_reduce_kernel(Dims, const float*, float*, const float*);
 __global__ void prologue_forward_kernel(const float*, const float*, const float*, const float*,
                                         const float*, const float*, const float*, const float*,
                                         const float*, int, int, int, int, float, float, int,
@@ -156,17 +156,21 @@ int configure() {
              {(const void*)m4::fwd_read_kernel<float, false>, kChunkLdsBytes},
              {(const void*)m4::fwd_read_kernel<m4::bf16_t, false>, kChunkLdsBytes},
              {(const void*)m4::fwd_read_kernel<float, true>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<float, false>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<m4::bf16_t, false>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<float, true>, kChunkLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float, false>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float, true>, kGradsLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<float, false, false>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<m4::bf16_t, false, false>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<float, true, false>, kChunkLdsBytes},
+             {(const void*)m4::bwd_dy_kernel<float, true, true>, kChunkLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float, false, false>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false, false>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float, true, false>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float, true, true>, kGradsLdsBytes},
              {(const void*)m4::states_kernel<false, float, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, m4::bf16_t, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false, 2>,
               kStatesLdsBytes + kStatesBwdExtra},
              {(const void*)m4::states_kernel<false, float, true, 2>, kStatesLdsBytes},
+             {(const void*)m4::states_kernel<true, float, true, 2>,
+              kStatesLdsBytes + kStatesBwdExtra},
              {(const void*)m3::walk_kernel<false, float, true>, m3::kWalkLds},
              {(const void*)m3::walk_kernel<true, float, true>, m3::kWalkLds},
              {(const void*)m3::out_kernel<float, true>, m3::kOutLds},
@@ -416,8 +420,13 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
 // The backward launch sequence.  MIX: keys and queries come from the
 // mixer's raw projections (`mix`; the plain key and query pointers are
 // unused), normalised on load by bwd_dy and bwd_grads; the gradients are
-// those of the normalised keys and queries, as in the plain case.
-template <typename In, bool MIX>
+// those of the normalised keys and queries, as in the plain case.  GATE
+// (with MIX): d_output is the cotangent of the mixer's gated output and the
+// gradients are carried on through the read gating and the prologue (`mg`;
+// d_keys, d_queries, d_beta, d_log_decay and d_variance are unused, d_floor
+// is the floor_raw gradient); the per-head parameter partials are left in
+// mg.dy_part and mg.grads_part for the caller's head sums.
+template <typename In, bool MIX, bool GATE = false>
 int backward_impl(const char* entry, const In* keys, const In* values, const In* queries,
                   const float* beta, const float* log_decay, const float* floor, int B, int T,
                   int H, int value_dim, int chunk, const float* solved, const float* factors,
@@ -426,7 +435,9 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                   const float* d_final_cross, float* d_keys, float* d_values, float* d_queries,
                   float* d_beta, float* d_log_decay, float* d_floor, float* d_init_evidence,
                   float* d_init_cross, void* workspace, size_t workspace_bytes, void* stream,
-                  const m4::MixerIn& mix = {}, bool spill_free = false) {
+                  const m4::MixerIn& mix = {}, bool spill_free = false,
+                  const m4::MixerGrad& mg = {}, const float* floor_raw = nullptr) {
+  static_assert(!GATE || MIX, "the gated backward takes the mixer's raw rows");
   g_error.clear();
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
@@ -435,6 +446,23 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
     queries = reinterpret_cast<const In*>(mix.query);
     if (mix.previous && misaligned(mix.previous))
       return fail(M4MR_EINVAL, std::string(entry) + ": arrays must be 16-byte aligned");
+  }
+  if (GATE) {
+    // The gated backward's own outputs and inputs stand in for the plain ones.
+    d_output = mg.d_out;
+    d_variance = mg.d_var;
+    d_keys = mg.d_key;
+    d_queries = mg.d_query;
+    d_beta = mg.d_beta_raw;
+    d_log_decay = mg.d_dt_raw;
+    const void* gate_need[] = {mg.read, mg.variance, mg.scale, mg.skip, mg.dt_raw, mg.dt_bias,
+                               mg.a_log, mg.dy_part, mg.grads_part, floor_raw};
+    for (const void* p : gate_need)
+      if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
+    const void* gate_vec[] = {mg.read, mg.d_shifted, mg.d_previous};
+    for (const void* p : gate_vec)
+      if (p && misaligned(p))
+        return fail(M4MR_EINVAL, std::string(entry) + ": arrays must be 16-byte aligned");
   }
   const void* need[] = {keys,    values,     queries,         beta,         log_decay,
                         floor,   solved,     factors,         start_evidence, start_cross,
@@ -459,9 +487,9 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   const unsigned seqs = (unsigned)B * H * d.NC;
   const long tokens = (long)B * T * H;
   int rc = launch("bwd_dy", st, [&] {
-    hipLaunchKernelGGL((m4::bwd_dy_kernel<In, MIX>), dim3(persistent_grid(seqs, 2)), dim3(256),
-                       kChunkLdsBytes, st, d, keys, values, queries, beta, log_decay, start_cross,
-                       d_output, d_variance, ws.z, mix);
+    hipLaunchKernelGGL((m4::bwd_dy_kernel<In, MIX, GATE>), dim3(persistent_grid(seqs, 2)),
+                       dim3(256), kChunkLdsBytes, st, d, keys, values, queries, beta, log_decay,
+                       start_cross, d_output, d_variance, ws.z, mix, mg);
   });
   if (rc) return rc;
   rc = launch("factored_solve", st, [&] {
@@ -469,17 +497,21 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
                        st, factors, ws.z, ws.z, tokens);
   });
   if (rc) return rc;
-  if (fused_states(B, H, d)) {
-    const m4::StateArgs args{ws.z,             d_output,       solved,   beta,   log_decay,
-                             d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
-                             d_init_evidence,  d_init_cross};
+  // The gated backward always takes the fused walk, whose cross weights
+  // take the read gate.
+  if (GATE || fused_states(B, H, d)) {
+    m4::StateArgs args{ws.z,             d_output,       solved,   beta,   log_decay,
+                       d_final_evidence, d_final_cross,  ws.end_s, ws.end_c,
+                       d_init_evidence,  d_init_cross};
+    args.variance = mg.variance;
+    args.confidence_scale = mg.scale;
     rc = launch("bwd_states", st, [&] {
       // The one-buffer walk spills two registers to per-lane scratch, device
       // memory the HIP runtime provides with the dispatch; a caller that
       // allocates nothing (spill_free) takes the two-buffer walk, which does
       // not spill and gives the same states.
       const bool one = !spill_free && states_single_buffer(B, H, d);
-      const auto walk = one ? m4::states_kernel<true, float, false, 1> : m4::states_kernel<true, float, false, 2>;
+      const auto walk = one ? m4::states_kernel<true, float, GATE, 1> : m4::states_kernel<true, float, GATE, 2>;
       hipLaunchKernelGGL(walk, dim3(B * H, 1 + d.NV), dim3(512),
                          (one ? kStatesLdsBytes / 2 : kStatesLdsBytes) + kStatesBwdExtra, st, d,
                          args);
@@ -498,15 +530,16 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   }
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
-    hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX>), dim3(persistent_grid(seqs, 1)), dim3(512),
-                       kGradsLdsBytes, st, d, keys, values, beta, log_decay, solved, ws.z,
-                       d_output, d_variance, start_evidence, start_cross, ws.end_s, ws.end_c,
-                       d_keys, d_values, d_queries, d_beta, d_log_decay, ws.floor_part, mix);
+    hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX, GATE>), dim3(persistent_grid(seqs, 1)),
+                       dim3(512), kGradsLdsBytes, st, d, keys, values, beta, log_decay, solved,
+                       ws.z, d_output, d_variance, start_evidence, start_cross, ws.end_s,
+                       ws.end_c, d_keys, d_values, d_queries, d_beta, d_log_decay, ws.floor_part,
+                       mix, mg);
   });
   if (rc) return rc;
   return launch("floor_reduce", st, [&] {
     hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H * 16), dim3(256), 0, st, d, ws.floor_part,
-                       d_floor);
+                       d_floor, GATE ? floor_raw : nullptr);
   });
 }
 
@@ -639,6 +672,119 @@ int m4mr_mixer_backward(const float* key, const float* value, const float* query
       chunk, solved, factors, start_evidence, start_cross, d_read, d_variance, d_final_evidence,
       d_final_cross, d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_evidence,
       d_init_cross, workspace, workspace_bytes, stream, mix);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The fused mixer backward's workspace: m4mr_backward's, then the read's
+// variance cotangent [B,T,H] and the per-chunk partials of the gating's
+// (H x 2) and the prologue's (H x 3) per-head parameter gradients.
+struct MixerReadWorkspace {
+  float *d_var, *dy_part, *grads_part;
+  long chunks;  // B NC, the partials per (head, parameter)
+  size_t bytes;
+};
+
+MixerReadWorkspace carve_mixer(void* base, int B, int T, int H, int P, int chunk) {
+  const Dims d = make_dims(B, T, H, P, chunk);
+  MixerReadWorkspace w;
+  size_t off = carve(nullptr, B, T, H, P, chunk).bytes;
+  char* p = static_cast<char*>(base);
+  w.chunks = (long)B * d.NC;
+  w.d_var = reinterpret_cast<float*>(p + off);
+  off = align256(off + (size_t)B * T * H * sizeof(float));
+  w.dy_part = reinterpret_cast<float*>(p + off);
+  off = align256(off + (size_t)H * 2 * w.chunks * sizeof(float));
+  w.grads_part = reinterpret_cast<float*>(p + off);
+  off = align256(off + (size_t)H * 3 * w.chunks * sizeof(float));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t m4mr_mixer_read_backward_workspace_bytes(int B, int T, int H, int value_dim, int chunk) {
+  std::string why;
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return 0;
+  return carve_mixer(nullptr, B, T, H, value_dim, chunk).bytes;
+}
+
+int m4mr_mixer_read_backward(const float* key, const float* value, const float* query,
+                             const float* dt_raw, const m4mr_mixer_params* params, int B, int T,
+                             int H, int value_dim, int chunk, const float* read,
+                             const float* variance, const float* beta, const float* log_decay,
+                             const float* floor, const float* solved, const float* factors,
+                             const float* start_evidence, const float* start_cross,
+                             const float* d_output, const float* d_variance,
+                             const float* d_final_evidence, const float* d_final_cross,
+                             const float* d_shifted, float* d_key, float* d_value,
+                             float* d_query, float* d_beta_raw, float* d_dt_raw,
+                             float* d_beta_bias, float* d_dt_bias, float* d_a_log,
+                             float* d_floor_raw, float* d_previous, float* d_confidence_scale,
+                             float* d_skip, float* d_init_evidence, float* d_init_cross,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  const char* entry = "m4mr_mixer_read_backward";
+  g_error.clear();
+  if (!params) return fail(M4MR_EINVAL, std::string(entry) + ": params is NULL");
+  if (!(params->beta_max > 0.f))
+    return fail(M4MR_EINVAL, std::string(entry) + ": beta_max must be positive");
+  const void* need[] = {key,           query,          params->dt_bias, params->a_log,
+                        params->floor_raw, params->confidence_scale, params->skip,
+                        d_key,         d_query,        d_beta_raw,      d_dt_raw,
+                        d_beta_bias,   d_dt_bias,      d_a_log,         d_floor_raw,
+                        d_confidence_scale, d_skip,    workspace};
+  for (const void* p : need)
+    if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
+  std::string why;
+  if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(M4MR_EINVAL, std::string(entry) + ": workspace must be 256-byte aligned");
+  const MixerReadWorkspace mw = carve_mixer(workspace, B, T, H, value_dim, chunk);
+  if (workspace_bytes < mw.bytes)
+    return fail(M4MR_EINVAL, std::string(entry) + ": workspace too small (need " +
+                                 std::to_string(mw.bytes) + " bytes)");
+  const bool shift = params->key_shift != 0;
+  const m4::MixerIn mix{key, query, shift ? params->previous : nullptr, shift ? 1 : 0};
+  m4::MixerGrad mg{};
+  mg.d_out = d_output;
+  mg.read = read;
+  mg.variance = variance;
+  mg.d_var_in = d_variance;
+  mg.scale = params->confidence_scale;
+  mg.skip = params->skip;
+  mg.d_var = mw.d_var;
+  mg.dy_part = mw.dy_part;
+  mg.dt_raw = dt_raw;
+  mg.dt_bias = params->dt_bias;
+  mg.a_log = params->a_log;
+  mg.beta_max = params->beta_max;
+  mg.d_shifted = shift ? d_shifted : nullptr;
+  mg.d_key = d_key;
+  mg.d_query = d_query;
+  mg.d_beta_raw = d_beta_raw;
+  mg.d_dt_raw = d_dt_raw;
+  mg.d_previous = d_previous;
+  mg.grads_part = mw.grads_part;
+  int rc = backward_impl<float, true, true>(
+      entry, nullptr, value, nullptr, beta, log_decay, floor, B, T, H, value_dim, chunk, solved,
+      factors, start_evidence, start_cross, nullptr, nullptr, d_final_evidence, d_final_cross,
+      nullptr, d_value, nullptr, nullptr, nullptr, d_floor_raw, d_init_evidence, d_init_cross,
+      workspace, workspace_bytes, stream, mix, /*spill_free=*/false, mg, params->floor_raw);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = launch("head_sums", st, [&] {
+    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 2), dim3(1024), 0, st, mw.dy_part,
+                       mw.chunks, H, 2, d_confidence_scale, d_skip, nullptr);
+  });
+  if (rc) return rc;
+  return launch("head_sums", st, [&] {
+    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 3), dim3(1024), 0, st, mw.grads_part,
+                       mw.chunks, H, 3, d_beta_bias, d_dt_bias, d_a_log);
+  });
 }
 
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {

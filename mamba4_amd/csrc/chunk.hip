@@ -247,20 +247,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //
 // MIX: keys and queries from the mixer's raw projections, as in
 // fwd_read_kernel (keys shifted and normalised at staging, queries
-// normalised where used).
-template <typename In, bool MIX>
+// normalised where used).  GATE (with MIX): d_output is the cotangent of
+// the mixer's gated output and d_variance unused; the read's cotangent is
+// g_t d_out_t, applied to the rows of the products (all linear in them),
+// and its variance cotangent d_var_t = (d_out_t . read_t) g (1 - g)
+// (-scale / (1 + var_t)) plus mg.d_var_in, written to mg.d_var; the
+// per-chunk sums of -(d_out . read) g (1 - g) log1p(var) and d_out . value
+// go to mg.dy_part (epilogue_backward_kernel's arithmetic).
+template <typename In, bool MIX, bool GATE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dy_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const In* __restrict__ queries, const float* __restrict__ beta,
     const float* __restrict__ log_decay, const float* __restrict__ start_c,
     const float* __restrict__ d_output, const float* __restrict__ d_variance,
-    float* __restrict__ ybar, MixerIn mix) {
+    float* __restrict__ ybar, MixerIn mix, MixerGrad mg) {
+  static_assert(!GATE || MIX, "the gated backward reads the mixer's raw rows");
   extern __shared__ float smem[];
   float* DO = smem;
   float* V = DO + TILE;  // values, then keys
   float* G = V + TILE;
   float* C0 = G + TILE;
   __shared__ ChunkScalars cs;
+  __shared__ float epart[GATE ? 4 : 1][2];  // GATE: per-wave gate-parameter partials
   const long nseq = (long)d.B * d.H * d.NC;
   // The wave's 16-row strip (its causal products cost strip + 1 blocks).
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
@@ -271,9 +279,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   RowTile<In> rv, rk;
   TileRegs rc;
   // Queries and d_variance of this lane's accumulator rows (read in the
-  // epilogue; zero past the chunk).
+  // epilogue; zero past the chunk).  GATE: the variance cotangent from
+  // mg.d_var_in (zero without it) and the variance itself, in gvar.
   RowQuad<In> qv[4];
-  float dvar[4];
+  float dvar[4], gvar[4];
   auto fetch_rows_q = [&](const SeqIndex& s) {
     const long th = token_head(d, s.b, s.n * d.chunk, s.h);
     const unsigned st = (unsigned)d.H * 64;
@@ -283,12 +292,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     else
       qsrc = queries;
     const BufRsrc rq = buf_rsrc(qsrc + th * 64, ((unsigned)(s.len - 1) * st + 64) * sizeof(In));
-    const BufRsrc rv2 = buf_rsrc(d_variance + th, ((unsigned)(s.len - 1) * d.H + 1) * 4);
+    const unsigned sbytes = ((unsigned)(s.len - 1) * d.H + 1) * 4;
+    const float* dv_src = GATE ? mg.d_var_in : d_variance;
+    const BufRsrc rv2 = buf_rsrc(dv_src ? dv_src + th : d_output, dv_src ? sbytes : 0);
+    const BufRsrc rvar = buf_rsrc(GATE ? mg.variance + th : d_output, GATE ? sbytes : 0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const unsigned t = acc_row(w, q);
       qv[q].load(rq, (t * st + c4) * sizeof(In));
       dvar[q] = buf_load1(rv2, t * d.H * 4);
+      if constexpr (GATE) gvar[q] = buf_load1(rvar, t * d.H * 4);
     }
   };
   // The chunk's log decays and betas (lane s of wave 0: token s; the other
@@ -332,6 +345,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f4 acc[4], inh[4];
     zero4(acc);
     zero4(inh);
+    // GATE: d_out_t . read_t and d_out_t . value_t of this lane's rows.
+    float dotr[4] = {0.f, 0.f, 0.f, 0.f}, dotv[4] = {0.f, 0.f, 0.f, 0.f};
     for (int v = 0; v < d.NV; ++v) {
       if (v > 0) {
         // Tile v replaces tile v - 1 once every wave has read it.
@@ -352,8 +367,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
         fetch_scalars(sn);
       }
+      f4 rq[4];
+      if constexpr (GATE) {
+        // The read rows of value tile v (zero past the chunk), for the
+        // variance cotangent; in flight during the products.
+        const long th = token_head(d, si.b, si.n * d.chunk, si.h);
+        const unsigned st = (unsigned)d.H * d.P;
+        const BufRsrc rr = buf_rsrc(mg.read + th * d.P + 64 * v,
+                                    ((unsigned)(si.len - 1) * st + 64) * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rq[q] = buf_load4(rr, ((unsigned)acc_row(w, q) * st + c4) * 4);
+      }
       tile_mma_causal<false>(acc, DO, V, w);      // dout_t . v_s, s <= t
       tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
+      if constexpr (GATE) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int t = acc_row(w, q);
+          const f4 dq = *reinterpret_cast<const f4*>(DO + t * LDT + c4);
+          const f4 vq = *reinterpret_cast<const f4*>(V + t * LDT + c4);
+          dotr[q] += dq[0] * rq[q][0] + dq[1] * rq[q][1] + dq[2] * rq[q][2] + dq[3] * rq[q][3];
+          dotv[q] += dq[0] * vq[0] + dq[1] * vq[1] + dq[2] * vq[2] + dq[3] * vq[3];
+        }
+      }
+    }
+    // GATE: each row's gate, its variance cotangent and the chunk's
+    // contributions to the gate parameters' gradients.
+    float gate[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (GATE) {
+      const float scale = mg.scale[si.h];
+      float pscale = 0.f, pskip = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = acc_row(w, q);
+        const float dr = row16_sum(dotr[q]), dsk = row16_sum(dotv[q]);
+        const float lv = log1pf(gvar[q]);
+        gate[q] = mix_sigmoid(1.f - scale * lv);
+        const float slope = dr * gate[q] * (1.f - gate[q]);
+        dvar[q] += slope * (-scale / (1.f + gvar[q]));
+        if ((lane_id() & 15) == 0 && t < si.len)
+          mg.d_var[token_head(d, si.b, si.n * d.chunk + t, si.h)] = dvar[q];
+        // Rows past the chunk read zeros: their terms vanish.
+        pscale += -slope * lv;
+        pskip += dsk;
+      }
+      pscale = group4_sum(pscale);
+      pskip = group4_sum(pskip);
+      if (lane_id() == 0) {
+        epart[threadIdx.x >> 6][0] = pscale;
+        epart[threadIdx.x >> 6][1] = pskip;
+      }
     }
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
@@ -361,10 +424,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int q = 0; q < 4; ++q) {
         const int t = acc_row(w, q), s = acc_col<false>(jb);
         float v = 0.f;
-        if (s <= t && t < si.len) v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
+        if (s <= t && t < si.len)
+          v = acc[jb][q] * gate[q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
         G[t * LDT + s] = v;
       }
     __syncthreads();
+    if constexpr (GATE)
+      // The chunk's gate-parameter partials, the four waves' in order.
+      if (threadIdx.x < 2) {
+        const long at = ((long)si.h * 2 + threadIdx.x) * ((long)d.B * d.NC) +
+                        (long)si.b * d.NC + si.n;
+        mg.dy_part[at] = ((epart[0][threadIdx.x] + epart[1][threadIdx.x]) +
+                          epart[2][threadIdx.x]) + epart[3][threadIdx.x];
+      }
     if constexpr (MIX)
       rk.store_unit(V, mix.key_shift && !mix.previous && si.n == 0);
     else
@@ -384,7 +456,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float carried = expf(cs.prefix[t]);
         const f4 qn = MIX ? mix_unit(qv[q].get()) : qv[q].get();
         *reinterpret_cast<f4*>(ybar + th * 64 + c4) =
-            quad_row(within, q) + carried * quad_row(inh, q) + dvar[q] * qn;
+            quad_row(within, q) + (carried * gate[q]) * quad_row(inh, q) + dvar[q] * qn;
       }
     }
     if (!more) break;
@@ -424,8 +496,15 @@ constexpr int MAX_NV = 2;
 
 //
 // MIX: keys from the mixer's raw projections, shifted and normalised at
-// staging (as in fwd_read_kernel).
-template <typename In, bool MIX>
+// staging (as in fwd_read_kernel).  GATE (with MIX): d_output is the
+// cotangent of the mixer's gated output, gated on load (d_variance is then
+// bwd_dy's mg.d_var), the values take the skip term skip d_out, and the
+// gradients go through the prologue's VJP (prologue_backward_kernel's
+// arithmetic): the keys' and queries' unit normalisation to the raw rows
+// (key t's source row is raw key t - 1 with the shift, or the cached key),
+// the gates to beta_raw and dt_raw, and per-chunk partials of the per-head
+// gate-bias and a_log gradients to mg.grads_part.
+template <typename In, bool MIX, bool GATE>
 __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
@@ -435,7 +514,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     const float* __restrict__ end_s, const float* __restrict__ end_c,
     float* __restrict__ d_keys, float* __restrict__ d_values, float* __restrict__ d_queries,
     float* __restrict__ d_beta, float* __restrict__ d_log_decay,
-    float* __restrict__ floor_part, MixerIn mix) {
+    float* __restrict__ floor_part, MixerIn mix, MixerGrad mg) {
+  static_assert(!GATE || MIX, "the gated backward reads the mixer's raw rows");
   extern __shared__ float smem[];
   float* Kt = smem;       // keys, then S0
   float* Vt = Kt + TILE;  // a value tile, then a C0 tile
@@ -467,7 +547,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   };
   // Token tt's log decay and beta in thread tt < 64, d_variance of this
   // thread's tile-fetch rows; zero past the chunk (out-of-range offsets).
-  float pg = 0.f, pbt = 0.f, pdv[2];
+  // GATE: the variance of the same rows (for their read gates).
+  float pg = 0.f, pbt = 0.f, pdv[2], pgv[2];
   auto fetch_scalars = [&](const SeqIndex& sx) {
     const unsigned tt = threadIdx.x, st = (unsigned)d.H * 4;
     const unsigned bytes = sx.len > 0 ? (unsigned)(sx.len - 1) * st + 4 : 0;
@@ -478,6 +559,11 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     const BufRsrc rv = buf_rsrc(d_variance + th, bytes);
 #pragma unroll
     for (int j = 0; j < 2; ++j) pdv[j] = buf_load1(rv, ((tt >> 4) + 32 * j) * st);
+    if constexpr (GATE) {
+      const BufRsrc rg = buf_rsrc(mg.variance + th, bytes);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) pgv[j] = buf_load1(rg, ((tt >> 4) + 32 * j) * st);
+    }
   };
   fetch_keys(si);
   fetch_tokens(tv, si.len, value_rows(values, d, si, 0));
@@ -500,6 +586,17 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     const int causal_nj = min(2, max(0, ws - 2 * hf + 1)), t_begin = 16 * ws;
     // d_variance of this thread's tile-fetch rows (tid/16 + 32j).
     const float dvar[2] = {pdv[0], pdv[1]};
+    // GATE: the read gates of those rows; the dout tiles are gated as staged.
+    float gr[2] = {1.f, 1.f};
+    if constexpr (GATE)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) gr[j] = read_gate(mg.scale[si.h], pgv[j]);
+    auto store_dout = [&](const RowTile<float, GRADS_THREADS>& t) {
+      if constexpr (GATE)
+        t.store_scaled(Dt, gr);
+      else
+        t.store(Dt);
+    };
 
     if constexpr (MIX)
       tk.store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0);
@@ -508,7 +605,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     tv.store(Vt);
     ty.store(Yt);
     tz.store(Zt);
-    td.store(Dt);
+    store_dout(td);
     if (tid < 64) finish_chunk_scalars(cs, pg, pbt);
     // The end-state cotangents of phase 3 load while phases 1 and 2 run (of H,
     // the last value tile, the one phase 3 starts from).
@@ -534,7 +631,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
         __syncthreads();
         rv.store(Vt);
-        rd.store(Dt);
+        store_dout(rd);
         __syncthreads();
         tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
       }
@@ -605,7 +702,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
           RowTile<float, GRADS_THREADS> rd;
           fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
           __syncthreads();
-          rd.store(Dt);
+          store_dout(rd);
           __syncthreads();
         }
         tile_mma_half<false, false>(dv[v], M1, Dt, kt, ws, hf, t_begin);  // sum_t W gy[t][s] dout_t
@@ -613,6 +710,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     }
     __syncthreads();
 
+    float2 dkq[4];  // GATE: this thread's d keys until M1 is free
     // Phase 3: chunk-end terms through the end-state cotangents G, H:
     // (G + G^T) k_s as two products (G read k-major, then transposed).  H and
     // the values go tile by tile from the last, leaving the first tile of
@@ -679,8 +777,16 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
             if (s < si.len) {
               const float tl = cs.tail[s];
               const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
-              *reinterpret_cast<float2*>(d_values + th * d.P + 64 * v + c4 + 2 * hf) =
-                  float2{dv[v][0][q] + tl * hk[0][q], dv[v][1][q] + tl * hk[1][q]};
+              const long at = th * d.P + 64 * v + c4 + 2 * hf;
+              float2 gv2 = float2{dv[v][0][q] + tl * hk[0][q], dv[v][1][q] + tl * hk[1][q]};
+              if constexpr (GATE) {
+                // The skip's term of the value gradient: skip d_out.
+                const float sk = mg.skip[si.h];
+                const float2 dq = *reinterpret_cast<const float2*>(mg.d_out + at);
+                gv2.x += sk * dq.x;
+                gv2.y += sk * dq.y;
+              }
+              *reinterpret_cast<float2*>(d_values + at) = gv2;
             }
           }
         }
@@ -690,15 +796,22 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         const int s = acc_row(ws, q);
         const float qv = row16_sum(qpart[q]);
         if (r == 0) quadpart[hf][s] = qv;
-        if (s < si.len) {
-          const float tl = cs.tail[s];
+        const float tl = cs.tail[s];
+        const float2 dkv =
+            float2{dk[0][q] + tl * (gk[0][q] + hv[0][q]), dk[1][q] + tl * (gk[1][q] + hv[1][q])};
+        if constexpr (GATE) {
+          dkq[q] = dkv;  // staged in M1 once G is read (phase 5 takes it to the raw rows)
+        } else if (s < si.len) {
           const long th = token_head(d, si.b, si.n * d.chunk + s, si.h);
-          *reinterpret_cast<float2*>(d_keys + th * 64 + c4 + 2 * hf) =
-              float2{dk[0][q] + tl * (gk[0][q] + hv[0][q]), dk[1][q] + tl * (gk[1][q] + hv[1][q])};
+          *reinterpret_cast<float2*>(d_keys + th * 64 + c4 + 2 * hf) = dkv;
         }
       }
     }
     __syncthreads();
+    if constexpr (GATE)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float2*>(M1 + acc_row(ws, q) * LDT + c4 + 2 * hf) = dkq[q];
     if (tid < 64) quad[tid] = quadpart[0][tid] + quadpart[1][tid];
     fetch_keys(sx);
 
@@ -731,7 +844,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
           __syncthreads();
           rhv.store(M2);
           rcv.store(Vt);
-          rd.store(Dt);
+          store_dout(rd);
           __syncthreads();
         }
         if (d.NV == 1) {
@@ -791,8 +904,33 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       if (t == si.len - 1) dp += expf(p_last) * red[0] + eend_total;
       // d log_decay_r = sum_{t >= r} d prefix_t (reverse inclusive sum).
       const float suffix = wave_suffix_sum(dp);
-      if (t < si.len) {
-        const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+      const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+      if constexpr (GATE) {
+        // The gates' VJP: beta = beta_max sigmoid(beta_raw + bias), so
+        // d beta_raw = d beta beta (1 - beta / beta_max); log decay =
+        // -exp(a_log) softplus(dt_raw + bias), so d dt_raw = d log_decay
+        // (-exp(a_log) sigmoid(dt_raw + bias)) and d a_log = d log_decay
+        // log_decay.  Past the chunk every term is zero (zero loads).
+        const unsigned st = (unsigned)d.H * 4;
+        const long th0 = token_head(d, si.b, si.n * d.chunk, si.h);
+        const unsigned bytes = (unsigned)(si.len - 1) * st + 4;
+        const float draw = buf_load1(buf_rsrc(mg.dt_raw + th0, bytes), t * st);
+        const float ld = buf_load1(buf_rsrc(log_decay + th0, bytes), t * st);
+        const float bt = cs.beta[t];
+        const float dbr = mg.beta_max != 0.f ? db * bt * (1.f - bt / mg.beta_max) : 0.f;
+        const float ddt = -suffix * expf(mg.a_log[si.h]) * mix_sigmoid(draw + mg.dt_bias[si.h]);
+        if (t < si.len) {
+          mg.d_beta_raw[th] = dbr;
+          mg.d_dt_raw[th] = ddt;
+        }
+        const float sums[3] = {group4_sum(row16_sum(t < si.len ? dbr : 0.f)),
+                               group4_sum(row16_sum(t < si.len ? ddt : 0.f)),
+                               group4_sum(row16_sum(t < si.len ? suffix * ld : 0.f))};
+        if (t < 3) {
+          const long at = ((long)si.h * 3 + t) * ((long)d.B * d.NC) + (long)si.b * d.NC + si.n;
+          mg.grads_part[at] = t == 0 ? sums[0] : t == 1 ? sums[1] : sums[2];
+        }
+      } else if (t < si.len) {
         d_beta[th] = db;
         d_log_decay[th] = suffix;
       }
@@ -808,8 +946,49 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         const int t = (tid >> 4) + 32 * j;
         const f4 zr = *reinterpret_cast<const f4*>(Zt + t * LDT + c4);
         const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
-        if (t < si.len) {
-          const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+        const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
+        if constexpr (GATE) {
+          // Through the unit normalisations to the raw rows: r (g - u (u . g))
+          // with u the normalised row and r its 1 / norm (unit_row_vjp).
+          auto unit_vjp = [&](const f4& x, const f4& g) {
+            const float r2 = __builtin_amdgcn_rsqf(
+                row16_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]) + 1e-6f);
+            const f4 u = r2 * x;
+            const float ug = row16_sum(u[0] * g[0] + u[1] * g[1] + u[2] * g[2] + u[3] * g[3]);
+            return r2 * (g - ug * u);
+          };
+          const int tp = si.n * d.chunk + t;  // position in the sequence
+          const bool in = t < si.len;
+          const f4 xq = in ? *reinterpret_cast<const f4*>(mix.query + th * 64 + c4)
+                           : f4{0.f, 0.f, 0.f, 0.f};
+          const f4 dq = unit_vjp(xq, zr + dvar[j] * yr);
+          if (in) *reinterpret_cast<f4*>(mg.d_query + th * 64 + c4) = dq;
+          // Key t: its source row (raw key t - 1 with the shift, or the
+          // cached key at t = 0, or none) takes the VJP of its unit row.
+          const float* src = in ? mix_key_row(mix, d, si.b, tp, si.h) : nullptr;
+          const f4 xk = src ? *reinterpret_cast<const f4*>(src + c4) : f4{0.f, 0.f, 0.f, 0.f};
+          const f4 dk = unit_vjp(xk, *reinterpret_cast<const f4*>(M1 + t * LDT + c4));
+          float* dst = nullptr;
+          if (in) {
+            if (!mix.key_shift)
+              dst = mg.d_key + th * 64;
+            else if (tp > 0)
+              dst = mg.d_key + token_head(d, si.b, tp - 1, si.h) * 64;
+            else if (mg.d_previous)
+              dst = mg.d_previous + ((long)si.b * d.H + si.h) * 64;
+          }
+          if (dst) *reinterpret_cast<f4*>(dst + c4) = src ? dk : f4{0.f, 0.f, 0.f, 0.f};
+          // The last raw key feeds only the cache entry (its cotangent,
+          // or zero); without the shift the cached key feeds nothing.
+          if (in && mix.key_shift && tp == d.T - 1)
+            *reinterpret_cast<f4*>(mg.d_key + th * 64 + c4) =
+                mg.d_shifted ? *reinterpret_cast<const f4*>(
+                                   mg.d_shifted + ((long)si.b * d.H + si.h) * 64 + c4)
+                             : f4{0.f, 0.f, 0.f, 0.f};
+          if (in && tp == 0 && mg.d_previous && !mix.key_shift)
+            *reinterpret_cast<f4*>(mg.d_previous + ((long)si.b * d.H + si.h) * 64 + c4) =
+                f4{0.f, 0.f, 0.f, 0.f};
+        } else if (t < si.len) {
           *reinterpret_cast<f4*>(d_queries + th * 64 + c4) = zr + dvar[j] * yr;
         }
         fsum -= zr * yr;  // zero past the chunk's tokens
@@ -836,14 +1015,13 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   template __global__ void fwd_read_kernel<In, false>(                                         \
       Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
       const float*, float*, float*, MixerIn, ReadGate);                                        \
-  template __global__ void bwd_dy_kernel<In, false>(Dims, const In*, const In*, const In*,     \
-                                                    const float*, const float*, const float*,  \
-                                                    const float*, const float*, float*,        \
-                                                    MixerIn);                                  \
-  template __global__ void bwd_grads_kernel<In, false>(                                        \
+  template __global__ void bwd_dy_kernel<In, false, false>(                                    \
+      Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
+      const float*, const float*, float*, MixerIn, MixerGrad);                                 \
+  template __global__ void bwd_grads_kernel<In, false, false>(                                 \
       Dims, const In*, const In*, const float*, const float*, const float*, const float*,      \
       const float*, const float*, const float*, const float*, const float*, const float*,      \
-      float*, float*, float*, float*, float*, float*, MixerIn);
+      float*, float*, float*, float*, float*, float*, MixerIn, MixerGrad);
 M4_CHUNK_KERNELS(float)
 M4_CHUNK_KERNELS(bf16_t)
 #undef M4_CHUNK_KERNELS
@@ -851,20 +1029,28 @@ template __global__ void fwd_read_kernel<float, true>(Dims, const float*, const 
                                                       const float*, const float*, const float*,
                                                       const float*, const float*, float*, float*,
                                                       MixerIn, ReadGate);
-template __global__ void bwd_dy_kernel<float, true>(Dims, const float*, const float*, const float*,
-                                                    const float*, const float*, const float*,
-                                                    const float*, const float*, float*, MixerIn);
-template __global__ void bwd_grads_kernel<float, true>(
-    Dims, const float*, const float*, const float*, const float*, const float*, const float*,
-    const float*, const float*, const float*, const float*, const float*, const float*, float*,
-    float*, float*, float*, float*, float*, MixerIn);
+#define M4_MIXER_KERNELS(GATE)                                                                \
+  template __global__ void bwd_dy_kernel<float, true, GATE>(                                   \
+      Dims, const float*, const float*, const float*, const float*, const float*,              \
+      const float*, const float*, const float*, float*, MixerIn, MixerGrad);                   \
+  template __global__ void bwd_grads_kernel<float, true, GATE>(                                \
+      Dims, const float*, const float*, const float*, const float*, const float*,              \
+      const float*, const float*, const float*, const float*, const float*, const float*,      \
+      const float*, float*, float*, float*, float*, float*, float*, MixerIn, MixerGrad);
+M4_MIXER_KERNELS(false)
+M4_MIXER_KERNELS(true)
+#undef M4_MIXER_KERNELS
 
 // d floor[h][4c4 .. 4c4+3] = sum over (b, n) of floor_part[(b*H + h)*NC + n]
 // in a fixed order: block (h, c4) of 256 threads, thread i sums entries
 // e = i, i + 256, ... of the flattened (b, n) index, then a fixed tree adds
 // the 256 partials.  Deterministic run to run.
+// floor_raw (the mixer's fused backward; may be null): the result is carried
+// through floor = floor_min + softplus(floor_raw), d floor_raw = d floor
+// sigmoid(floor_raw).
 __global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* __restrict__ part,
-                                                          float* __restrict__ d_floor) {
+                                                          float* __restrict__ d_floor,
+                                                          const float* __restrict__ floor_raw) {
   const int h = blockIdx.x >> 4, c4 = blockIdx.x & 15;
   const int entries = d.B * d.NC;
   __shared__ f4 partial[256];
@@ -879,7 +1065,15 @@ __global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* 
     if (threadIdx.x < w) partial[threadIdx.x] += partial[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) *reinterpret_cast<f4*>(d_floor + h * 64 + 4 * c4) = partial[0];
+  if (threadIdx.x == 0) {
+    f4 out = partial[0];
+    if (floor_raw) {
+      const f4 fr = *reinterpret_cast<const f4*>(floor_raw + h * 64 + 4 * c4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] *= mix_sigmoid(fr[e]);
+    }
+    *reinterpret_cast<f4*>(d_floor + h * 64 + 4 * c4) = out;
+  }
 }
 
 }  // namespace m4

@@ -40,6 +40,9 @@ __device__ __forceinline__ BufRsrc buf_rsrc(const void* base, unsigned bytes) {
 __device__ __forceinline__ float buf_load1(BufRsrc r, unsigned off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+__device__ __forceinline__ f4 buf_load4(BufRsrc r, unsigned off) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 __device__ __forceinline__ float load1(const bf16_t* p) {
   return __uint_as_float((unsigned)*p << 16);
 }
@@ -189,6 +192,42 @@ struct ReadGate {
   const float* skip;              // [H] (the mixer's D)
   float* read;                    // [B,T,H,P]
 };
+
+// The rest of the mixer's VJP folded into the memory read's backward (GATE
+// kernels; lm/models/mamba4.py:183-237, 266-273 differentiated): the read
+// gating out = g read + skip value with g = sigmoid(1 - scale log1p(var)),
+// and the prologue's unit normalisation and gates.  The memory read's own
+// cotangents are then g d_out and the variance cotangent d_var, which
+// bwd_dy forms and writes for bwd_grads.  Per-chunk partial sums of the
+// per-head parameter gradients go to dy_part ([H][2][B NC]: d scale,
+// d skip) and grads_part ([H][3][B NC]: d beta_bias, d dt_bias, d a_log),
+// entry (h, j, b NC + n), for head_sums_kernel.
+struct MixerGrad {
+  const float* d_out;     // [B,T,H,P] cotangent of the gated output
+  const float* read;      // [B,T,H,P] the forward's ungated read
+  const float* variance;  // [B,T,H]
+  const float* d_var_in;  // [B,T,H] cotangent of the variance output, or null
+  const float* scale;     // [H] confidence scale
+  const float* skip;      // [H]
+  float* d_var;           // [B,T,H] the read's variance cotangent (workspace)
+  float* dy_part;
+  const float* dt_raw;    // [B,T,H]
+  const float* dt_bias;   // [H]
+  const float* a_log;     // [H]
+  float beta_max;
+  const float* d_shifted;  // [B,H,64] cotangent of the cached key, or null
+  float* d_key;            // [B,T,H,64] raw key gradient
+  float* d_query;          // [B,T,H,64] raw query gradient
+  float* d_beta_raw;       // [B,T,H]
+  float* d_dt_raw;         // [B,T,H]
+  float* d_previous;       // [B,H,64], or null
+  float* grads_part;
+};
+
+// The read gate of a token: sigmoid(1 - scale log1p(var)).
+__device__ __forceinline__ float read_gate(float scale, float var) {
+  return mix_sigmoid(1.f - scale * log1pf(var));
+}
 
 // Per-chunk log-decay prefix, tail weights and chunk length, staged in LDS
 // by wave 0: prefix[s] = sum_{r<=s} g_r, tail[s] = beta_s exp(P_last - P_s),
@@ -542,6 +581,13 @@ struct RowTile {
 #pragma unroll
     for (int j = 0; j < J; ++j) *reinterpret_cast<f4*>(tile + (r0 + RS * j) * LDT + q) = get(j);
   }
+  // Row j of this thread scaled by sc[j] (the mixer's read gate of its token).
+  __device__ __forceinline__ void store_scaled(float* tile, const float (&sc)[J]) const {
+    const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      *reinterpret_cast<f4*>(tile + (r0 + RS * j) * LDT + q) = sc[j] * get(j);
+  }
   // The rows unit-normalised (mix_unit), row 0 as a zero row if zero_row0.
   __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
@@ -658,6 +704,11 @@ struct StateArgs {
   float* last_s;         // the state after the last step
   float* last_c;
   MixerIn mix;           // forward with the mixer's projections (MIX): keys and gates
+  // Backward of the mixer's gated output (MIX): the cross a rows are the
+  // gated output's cotangent d_out, so the read's cotangent is g_t d_out_t
+  // with the read gate g_t = read_gate(confidence_scale, variance_t).
+  const float* variance;
+  const float* confidence_scale;
 };
 
 // Shape of the order head's scan: values [B,T,H,W] in chunks of `chunk`

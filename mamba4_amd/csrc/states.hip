@@ -273,7 +273,9 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
 //   forward:  a = key (evidence) or value tile, b = key,
 //             wt = beta_t exp(P_last - P_t);  states ascend from init.
 //   backward: evidence a, b = (z, y) and (y, z) with wt = -exp(P_t) / 2,
-//             cross a = d_output tile, b = y with wt = exp(P_t);  states
+//             cross a = d_output tile, b = y with wt = exp(P_t) (MIX: the
+//             read gate g_t exp(P_t), d_output being the cotangent of the
+//             mixer's gated output g_t read_t + skip value_t);  states
 //             descend from the final-state cotangent (the transpose of the
 //             forward carry, as bwd_local_kernel + bwd_scan_kernel).
 // A step's rows load into registers two steps before it multiplies.  NBUF =
@@ -323,6 +325,9 @@ template <bool BWD, typename In, bool MIX, int NBUF>
 __global__ __launch_bounds__(STATES_THREADS)
 __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kernel(Dims d,
                                                                                   StateArgs g) {
+  // MIX: the forward's keys come from the mixer's raw projections; the
+  // backward's cross weights take the mixer's read gate.
+  constexpr bool MIX_KEYS = MIX && !BWD, GATED = MIX && BWD;
   const In* rows_a = static_cast<const In*>(g.rows_a);
   const In* rows_ac = static_cast<const In*>(g.rows_ac);
   const In* rows_b = static_cast<const In*>(g.rows_b);
@@ -409,7 +414,7 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   const MixerIn& mix = g.mix;
   auto fetch = [&](StepRegs& R, int i) {
     const int first = i * d.chunk, cnt = chunk_len(d, i);
-    if constexpr (MIX) {
+    if constexpr (MIX_KEYS) {
       R.rb.fetch_mix_keys(cnt, mix, d, b, h, first);
     } else {
       R.rb.fetch_tokens(cnt, rows_b + token_head(d, b, first, h) * 64, (unsigned)d.H * 64);
@@ -425,10 +430,12 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
     const unsigned bytes = (unsigned)(cnt - 1) * d.H * 4 + 4;
     const unsigned off = w == 0 ? (unsigned)l * d.H * 4 : kNoRow;
     R.pg = buf_load1(buf_rsrc(g.log_decay + th, bytes), off);
-    R.pb = BWD ? 0.f : buf_load1(buf_rsrc(g.beta + th, bytes), off);
+    // (The backward's gated cross walk takes token l's variance instead.)
+    R.pb = BWD && !(GATED && cross) ? 0.f
+                                    : buf_load1(buf_rsrc((BWD ? g.variance : g.beta) + th, bytes), off);
   };
   auto stage = [&](const StepRegs& R, int u, int i) {
-    if constexpr (MIX)
+    if constexpr (MIX_KEYS)
       R.rb.store_unit(smem + 2 * u * TILE, mix.key_shift && !mix.previous && i == 0);
     else
       R.rb.store(smem + 2 * u * TILE);
@@ -440,7 +447,9 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
       const float p = wave_inclusive_sum(R.pg), last = read_lane(p, 63);
       const float mid = cut > 0 ? read_lane(p, cut - 1) : 0.f;  // cut is uniform
       if (BWD) {
-        sb[u].wt[0][l] = (cross ? 1.f : -0.5f) * expf(p);
+        float c = cross ? 1.f : -0.5f;
+        if (GATED && cross) c = read_gate(g.confidence_scale[h], R.pb);
+        sb[u].wt[0][l] = c * expf(p);
       } else {
         sb[u].wt[0][l] = l < cut ? R.pb * expf(mid - p) : 0.f;
         sb[u].wt[1][l] = l >= cut ? R.pb * expf(last - p) : 0.f;
@@ -528,6 +537,7 @@ M4_STATES(false, float, false)
 M4_STATES(false, bf16_t, false)
 M4_STATES(true, float, false)
 M4_STATES(false, float, true)
+M4_STATES(true, float, true)
 #undef M4_STATES
 template __global__ void fwd_stats_kernel<float>(Dims, const float*, const float*, const float*,
                                                  const float*, float*, float*);

@@ -223,9 +223,9 @@ class MixerRead(NamedTuple):
 
 
 class _MixerRead(torch.autograd.Function):
-    """m4mr_mixer_forward, and its VJP: the epilogue VJP, the memory-read
-    VJP from the forward's residuals with the raw keys and queries
-    normalised on load (m4mr_mixer_backward), and the prologue VJP."""
+    """m4mr_mixer_forward, and its VJP in one launch sequence
+    (m4mr_mixer_read_backward): the gating's VJP folded into the first
+    backward kernel, the prologue's into the last."""
 
     @staticmethod
     def forward(ctx, key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,
@@ -278,25 +278,71 @@ class _MixerRead(torch.autograd.Function):
         (key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
          confidence_scale, skip, read, variance, beta, log_decay, floor, solved, factors,
          start_s, start_c) = ctx.saved_tensors
+        lib = _lib.load()
+        batch, time, heads, dim = key.shape
+        width = value.shape[-1]
         if d_output is None:
             d_output = torch.zeros_like(read)
-        d_read, d_var, d_skip_value, d_scale, d_skip = _epilogue_backward(
-            read, variance, value, confidence_scale, skip, d_output)
-        if d_variance is not None:
-            d_var = d_var + _f32(d_variance)
-        (d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_s,
-         d_init_c) = memread_backward(key, value, query, beta, log_decay, floor, solved,
-                                      factors, start_s, start_c, ctx.chunk, d_read, d_var,
-                                      d_final_s, d_final_c, mixer=(previous, ctx.key_shift))
-        (d_key, d_query, d_beta_raw, d_dt_raw, d_beta_bias, d_dt_bias, d_a_log, d_floor_raw,
-         d_previous) = _prologue_backward(
-            key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
-            ctx.beta_max, ctx.key_shift, d_keys, d_queries, d_beta, d_log_decay, d_floor,
-            d_shifted)
+        grads = [torch.empty_like(t) for t in (key, value, query, beta_raw, dt_raw, beta_bias,
+                                               dt_bias, a_log, floor_raw)]
+        d_previous = None if previous is None else torch.empty_like(previous)
+        d_scale, d_skip = torch.empty_like(confidence_scale), torch.empty_like(skip)
+        f32 = dict(dtype=torch.float32, device=key.device)
+        d_init_s = torch.empty((batch, heads, dim, dim), **f32)
+        d_init_c = torch.empty((batch, heads, width, dim), **f32)
+        nbytes = lib.m4mr_mixer_read_backward_workspace_bytes(batch, time, heads, width,
+                                                              ctx.chunk)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=key.device)
+        params = _lib.MixerParams(
+            _ptr(beta_bias), _ptr(dt_bias), _ptr(a_log), _ptr(floor_raw), _ptr(previous),
+            _ptr(confidence_scale), _ptr(skip), ctx.beta_max, ctx.floor_min, int(ctx.key_shift),
+        )
+        cot = [None if t is None else _f32(t)
+               for t in (d_output, d_variance, d_final_s, d_final_c, d_shifted)]
+        d_key, d_value, d_query, d_beta_raw, d_dt_raw, d_beta_bias, d_dt_bias, d_a_log, \
+            d_floor_raw = grads
+        _lib.check(
+            lib.m4mr_mixer_read_backward(
+                _ptr(key), _ptr(value), _ptr(query), _ptr(dt_raw), ctypes.byref(params), batch,
+                time, heads, width, ctx.chunk, _ptr(read), _ptr(variance), _ptr(beta),
+                _ptr(log_decay), _ptr(floor), _ptr(solved), _ptr(factors), _ptr(start_s),
+                _ptr(start_c), *(_ptr(t) for t in cot), _ptr(d_key), _ptr(d_value),
+                _ptr(d_query), _ptr(d_beta_raw), _ptr(d_dt_raw), _ptr(d_beta_bias),
+                _ptr(d_dt_bias), _ptr(d_a_log), _ptr(d_floor_raw), _ptr(d_previous),
+                _ptr(d_scale), _ptr(d_skip), _ptr(d_init_s), _ptr(d_init_c), _ptr(workspace),
+                nbytes, _stream(),
+            )
+        )
         d_init = (d_init_s, d_init_c) if ctx.has_initial else (None, None)
-        return (d_key, d_values + d_skip_value, d_query, d_beta_raw, d_dt_raw, d_beta_bias,
-                d_dt_bias, d_a_log, d_floor_raw, d_previous, d_scale, d_skip, *d_init,
+        return (d_key, d_value, d_query, d_beta_raw, d_dt_raw, d_beta_bias, d_dt_bias, d_a_log,
+                d_floor_raw, d_previous, d_scale, d_skip, *d_init,
                 None, None, None, None, None)
+
+
+def mixer_read_separate_backward(ctx_tensors, beta_max, key_shift, chunk, d_output, d_variance,
+                                 d_final_s, d_final_c, d_shifted):
+    """The same VJP as three separate steps: m4mr_epilogue_backward,
+    m4mr_mixer_backward, m4mr_prologue_backward (and an add for the value's
+    two paths).  ``ctx_tensors`` are _MixerRead's saved tensors.  Returns
+    the gradients of key, value, query, beta_raw, dt_raw, beta_bias, dt_bias,
+    a_log, floor_raw, previous, confidence_scale, skip, init_s and init_c."""
+    (key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
+     confidence_scale, skip, read, variance, beta, log_decay, floor, solved, factors,
+     start_s, start_c) = ctx_tensors
+    d_read, d_var, d_skip_value, d_scale, d_skip = _epilogue_backward(
+        read, variance, value, confidence_scale, skip, d_output)
+    if d_variance is not None:
+        d_var = d_var + _f32(d_variance)
+    (d_keys, d_values, d_queries, d_beta, d_log_decay, d_floor, d_init_s,
+     d_init_c) = memread_backward(key, value, query, beta, log_decay, floor, solved,
+                                  factors, start_s, start_c, chunk, d_read, d_var,
+                                  d_final_s, d_final_c, mixer=(previous, key_shift))
+    (d_key, d_query, d_beta_raw, d_dt_raw, d_beta_bias, d_dt_bias, d_a_log, d_floor_raw,
+     d_previous) = _prologue_backward(
+        key, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw, previous,
+        beta_max, key_shift, d_keys, d_queries, d_beta, d_log_decay, d_floor, d_shifted)
+    return (d_key, d_values + d_skip_value, d_query, d_beta_raw, d_dt_raw, d_beta_bias,
+            d_dt_bias, d_a_log, d_floor_raw, d_previous, d_scale, d_skip, d_init_s, d_init_c)
 
 
 def mixer_read(key, value, query, beta_raw, dt_raw, beta_bias, dt_bias, a_log, floor_raw,

@@ -8,9 +8,12 @@ north-star tolerances) and against the separate kernels (memory_inputs ->
 selective_gaussian_memory -> gated_read) on the same state walk: the read
 kernel and the state walk normalise each key and query row with the
 prologue kernel's own arithmetic, the factor kernel sums a row's squares in
-another order, so the two paths agree to float32 rounding (1e-5), and
-gradients (which the fused op takes through the separate kernels' VJPs) to
-1e-4.
+another order, so the two paths agree to float32 rounding (1e-5).  The fused op's
+gradients (m4mr_mixer_read_backward: the gating's VJP inside the first
+backward kernel, the prologue's inside the last, the state walk weighted by
+the read gate) agree with the separate kernels' VJPs to 1e-4, with every
+cotangent set (output, variance, final state, shifted key) and with the
+optional ones left out.
 """
 
 import numpy as np
@@ -152,15 +155,44 @@ def test_mixer_read_matches_separate_path(gpu_lib, monkeypatch, batch, time, hea
     d_var = torch.tensor(rng.normal(size=variance.shape), dtype=torch.float32, device="cuda:0")
     d_s = torch.tensor(rng.normal(size=state.evidence.shape), dtype=torch.float32,
                        device="cuda:0")
-    for t, (o, v, s) in ((fused_t, (res.output, res.variance, res.state.evidence)),
-                         (sep_t, (out, variance, state.evidence))):
-        ((o * d_out).sum() + (v * d_var).sum() + (s * d_s).sum()).backward()
+    d_sh = torch.tensor(rng.normal(size=(batch, heads, 64)), dtype=torch.float32,
+                        device="cuda:0")
+    for t, (o, v, s, sh) in ((fused_t, (res.output, res.variance, res.state.evidence,
+                                         res.shifted)),
+                             (sep_t, (out, variance, state.evidence, shifted))):
+        loss = (o * d_out).sum() + (v * d_var).sum() + (s * d_s).sum()
+        if key_shift:
+            loss = loss + (sh * d_sh).sum()
+        loss.backward()
     for n in names:
         a, b = fused_t[n].grad, sep_t[n].grad
         if b is None:
             assert a is None, n
             continue
         assert normwise(_host(a), _host(b)) <= 1e-4, n
+
+
+@pytest.mark.gpu
+def test_mixer_read_backward_with_output_cotangent_only(gpu_lib, monkeypatch):
+    """Only the output enters the loss: the variance, final-state and
+    shifted-key cotangents reach the fused backward as NULL (zero)."""
+    import torch
+
+    from gpu_helpers import announce, normwise
+
+    monkeypatch.setenv("M4MR_STATE_WALK", "fused")
+    announce("mixer_read backward, output cotangent only, B2 T150 H3 P128")
+    x = raw_inputs(batch=2, time=150, heads=3, dim=64, value_dim=128, seed=27)
+    fused_t, sep_t = _gpu(x, MIXER_ARGS + ["previous"], grad=True), _gpu(
+        x, MIXER_ARGS + ["previous"], grad=True)
+    res = _fused(fused_t, previous=fused_t["previous"])
+    out, _, _, _ = _separate(sep_t, previous=sep_t["previous"])
+    d_out = torch.tensor(np.random.default_rng(28).normal(size=out.shape), dtype=torch.float32,
+                         device="cuda:0")
+    (res.output * d_out).sum().backward()
+    (out * d_out).sum().backward()
+    for n in MIXER_ARGS + ["previous"]:
+        assert normwise(_host(fused_t[n].grad), _host(sep_t[n].grad)) <= 1e-4, n
 
 
 @pytest.mark.gpu
@@ -188,8 +220,11 @@ def test_mixer_read_cache_continuation(gpu_lib):
 
 @pytest.mark.gpu
 def test_mixer_read_full_size(gpu_lib, monkeypatch):
-    """The config-2 shape (B16 T1024 H8, D=P=64): the fused forward against
-    the separate kernels, and a batch row against the oracle."""
+    """The config-2 shape (B16 T1024 H8, D=P=64): the fused forward and
+    backward against the separate kernels, and a batch row against the
+    oracle."""
+    import torch
+
     from gpu_helpers import announce, normwise
     from oracle import memread
     from oracle import mixer as oracle
@@ -197,11 +232,18 @@ def test_mixer_read_full_size(gpu_lib, monkeypatch):
     monkeypatch.setenv("M4MR_STATE_WALK", "fused")
     announce("mixer_read full size B16 T1024 H8")
     x = raw_inputs(batch=16, time=1024, heads=8, dim=64, value_dim=64, seed=26)
-    t = _gpu(x, MIXER_ARGS)
+    t, ts = _gpu(x, MIXER_ARGS, grad=True), _gpu(x, MIXER_ARGS, grad=True)
     res = _fused(t)
-    out, variance, _, _ = _separate(t)
+    out, variance, _, _ = _separate(ts)
     assert normwise(_host(res.output), _host(out)) <= 1e-5
     assert normwise(_host(res.variance), _host(variance)) <= 1e-5
+    rng = np.random.default_rng(29)
+    d_out = torch.tensor(rng.normal(size=out.shape), dtype=torch.float32, device="cuda:0")
+    d_var = torch.tensor(rng.normal(size=variance.shape), dtype=torch.float32, device="cuda:0")
+    ((res.output * d_out).sum() + (res.variance * d_var).sum()).backward()
+    ((out * d_out).sum() + (variance * d_var).sum()).backward()
+    for n in MIXER_ARGS:
+        assert normwise(_host(t[n].grad), _host(ts[n].grad)) <= 1e-4, n
     row = {n: (x[n][3:4] if np.ndim(x[n]) >= 3 else x[n]) for n in x}
     keys, queries, beta, log_decay, floor, _ = oracle.prologue(
         *(row[n] for n in PROLOGUE_ARGS), beta_max=BETA_MAX, floor_min=FLOOR_MIN)
