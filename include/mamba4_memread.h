@@ -147,9 +147,10 @@ typedef struct {
  * (to float32 rounding: the row norms are summed in another order), without
  * their separate passes over keys, queries and values: the memory-read
  * kernels shift and unit-normalise each raw key and query row as they load
- * it, a small kernel computes the gates (beta, log_decay [B,T,H] and floor
- * [H,D], written out with the prologue's arithmetic) from the raw gate
- * projections alone, and the read kernel writes
+ * it, the state walk computes the gates (beta, log_decay [B,T,H] and floor
+ * [H,D], with the prologue's arithmetic) from the raw gate projections as
+ * it first needs them and writes them out for the later kernels, and the
+ * read kernel writes
  *   output = read * sigmoid(1 - confidence_scale[h] log1p(variance))
  *            + skip[h] * value
  * (lm/models/mamba4.py:266-273) as well as the ungated `read` (the

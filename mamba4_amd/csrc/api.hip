@@ -51,6 +51,8 @@ __global__ void bwd_grads_kernel(Dims, const In*, const In*, const float*, const
                                  const float*, const float*, const float*, const float*, float*,
                                  float*, float*, float*, float*, float*, MixerIn, MixerGrad);
 __global__ void floor_reduce_kernel(Dims, const float*, float*, const float*);
+__global__ void mixer_finish_kernel(Dims, const float*, float*, const float*, const float*,
+                                    const float*, float*, float*, float*, float*, float*);
 __global__ void prologue_forward_kernel(const float*, const float*, const float*, const float*,
                                         const float*, const float*, const float*, const float*,
                                         const float*, int, int, int, int, float, float, int,
@@ -67,9 +69,6 @@ __global__ void epilogue_backward_kernel(const float*, const float*, const float
                                          const float*, int, int, int, int, const float*, float*,
                                          float*, float*, float*);
 __global__ void head_sums_kernel(const float*, long, int, int, float*, float*, float*);
-__global__ void mixer_gates_kernel(const float*, const float*, const float*, const float*,
-                                   const float*, const float*, const float*, int, int, int, int,
-                                   float, float, float*, float*, float*, float*);
 __global__ void zero_kernel(float*, long);
 __global__ void order_local_kernel(OrderDims, const float*, const float*, float*, float*);
 __global__ void order_carry_kernel(OrderDims, const float*, float*, const float*);
@@ -97,9 +96,10 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "prologue_backward", "epilogue_forward",
                                     "epilogue_backward", "head_sums", "order_local",
                                     "order_carry",    "order_apply", "order_bwd_local",
-                                    "order_bwd_carry", "order_bwd_apply", "mixer_gates",
+                                    "order_bwd_carry", "order_bwd_apply",
                                     "m3_walk",        "m3_out",    "m3_walk_bwd", "m3_grad",
-                                    "m3_finish",      "m3_bias",   "m3_suffix"};
+                                    "m3_finish",      "m3_bias",   "m3_suffix",
+                                    "mixer_finish"};
 
 struct ProfRecord {
   const char* name;
@@ -129,6 +129,7 @@ int fail(int code, const std::string& msg) {
 constexpr size_t kStatsLdsBytes = 3 * m4::TILE * sizeof(float);
 constexpr size_t kChunkLdsBytes = 4 * m4::TILE * sizeof(float);
 constexpr size_t kGradsLdsBytes = 7 * m4::TILE * sizeof(float);
+constexpr size_t kGradsGateLdsBytes = 8 * m4::TILE * sizeof(float);  // + the S0 tile
 constexpr size_t kStatesLdsBytes = 4 * m4::TILE * sizeof(float);
 // The backward walks add one tile (the evidence state's transpose).
 constexpr size_t kStatesBwdExtra = m4::TILE * sizeof(float);
@@ -163,7 +164,7 @@ int configure() {
              {(const void*)m4::bwd_grads_kernel<float, false, false>, kGradsLdsBytes},
              {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false, false>, kGradsLdsBytes},
              {(const void*)m4::bwd_grads_kernel<float, true, false>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float, true, true>, kGradsLdsBytes},
+             {(const void*)m4::bwd_grads_kernel<float, true, true>, kGradsGateLdsBytes},
              {(const void*)m4::states_kernel<false, float, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, m4::bf16_t, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false, 2>,
@@ -342,7 +343,7 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
                  int value_dim, int chunk, float* output, float* variance, float* final_evidence,
                  float* final_cross, float* solved, float* factors, float* start_evidence,
                  float* start_cross, void* stream, const m4::MixerIn& mix = {},
-                 const m4::ReadGate& gate = {}) {
+                 const m4::ReadGate& gate = {}, const m4::MixerGates& gates = {}) {
   g_error.clear();
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why)) return fail(M4MR_EINVAL, std::string(entry) + ": " + why);
@@ -376,6 +377,7 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
     m4::StateArgs args{keys,            values,      keys,           beta,   log_decay,
                        init_evidence,   init_cross,  start_evidence, start_cross,
                        final_evidence,  final_cross, mix};
+    args.gates = gates;
     rc = launch("fwd_states", st, [&] {
       const bool one = states_single_buffer(B, H, d);
       const auto walk = one ? m4::states_kernel<false, In, MIX, 1> : m4::states_kernel<false, In, MIX, 2>;
@@ -455,8 +457,10 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
     d_queries = mg.d_query;
     d_beta = mg.d_beta_raw;
     d_log_decay = mg.d_dt_raw;
-    const void* gate_need[] = {mg.read, mg.variance, mg.scale, mg.skip, mg.dt_raw, mg.dt_bias,
-                               mg.a_log, mg.dy_part, mg.grads_part, floor_raw};
+    const void* gate_need[] = {mg.read,   mg.variance, mg.scale,      mg.skip,
+                               mg.dt_raw, mg.dt_bias,  mg.a_log,      mg.dy_part,
+                               mg.grads_part, floor_raw, mg.d_scale, mg.d_skip,
+                               mg.d_beta_bias, mg.d_dt_bias, mg.d_a_log};
     for (const void* p : gate_need)
       if (!p) return fail(M4MR_EINVAL, std::string(entry) + ": a required pointer is NULL");
     const void* gate_vec[] = {mg.read, mg.d_shifted, mg.d_previous};
@@ -531,15 +535,23 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
     hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX, GATE>), dim3(persistent_grid(seqs, 1)),
-                       dim3(512), kGradsLdsBytes, st, d, keys, values, beta, log_decay, solved,
+                       dim3(512), GATE ? kGradsGateLdsBytes : kGradsLdsBytes, st, d, keys,
+                       values, beta, log_decay, solved,
                        ws.z, d_output, d_variance, start_evidence, start_cross, ws.end_s,
                        ws.end_c, d_keys, d_values, d_queries, d_beta, d_log_decay, ws.floor_part,
                        mix, mg);
   });
   if (rc) return rc;
+  if (GATE)
+    // The floor_raw gradient and the per-head parameter gradients.
+    return launch("mixer_finish", st, [&] {
+      hipLaunchKernelGGL(m4::mixer_finish_kernel, dim3(H * 16 + H * 5), dim3(256), 0, st, d,
+                         ws.floor_part, d_floor, floor_raw, mg.dy_part, mg.grads_part,
+                         mg.d_scale, mg.d_skip, mg.d_beta_bias, mg.d_dt_bias, mg.d_a_log);
+    });
   return launch("floor_reduce", st, [&] {
     hipLaunchKernelGGL(m4::floor_reduce_kernel, dim3(H * 16), dim3(256), 0, st, d, ws.floor_part,
-                       d_floor, GATE ? floor_raw : nullptr);
+                       d_floor, nullptr);
   });
 }
 
@@ -631,26 +643,30 @@ int m4mr_mixer_forward(const float* key, const float* value, const float* query,
   std::string why;
   if (bad_dims(B, T, H, value_dim, chunk, &why))
     return fail(M4MR_EINVAL, "m4mr_mixer_forward: " + why);
-  if (int rc = configure()) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const long tokens = (long)B * T * H;
   if (key && misaligned(key)) return fail(M4MR_EINVAL, "m4mr_mixer_forward: arrays must be 16-byte aligned");
   if (shifted && misaligned(shifted))
     return fail(M4MR_EINVAL, "m4mr_mixer_forward: arrays must be 16-byte aligned");
-  int rc = launch("mixer_gates", st, [&] {
-    hipLaunchKernelGGL(m4::mixer_gates_kernel, dim3((unsigned)((tokens + 255) / 256)), dim3(256),
-                       0, st, beta_raw, dt_raw, params->beta_bias, params->dt_bias,
-                       params->a_log, params->floor_raw, key, B, T, H, 64, params->beta_max,
-                       params->floor_min, beta, log_decay, floor,
-                       params->key_shift ? shifted : nullptr);
-  });
-  if (rc) return rc;
   const m4::MixerIn mix{key, query, params->previous, params->key_shift ? 1 : 0};
   const m4::ReadGate gate{params->confidence_scale, params->skip, read};
+  // The fused state walk computes the gates and writes them out (with the
+  // floor and the shifted key) before the factor and read kernels use them.
+  m4::MixerGates gates{};
+  gates.beta_raw = beta_raw;
+  gates.dt_raw = dt_raw;
+  gates.beta_bias = params->beta_bias;
+  gates.dt_bias = params->dt_bias;
+  gates.a_log = params->a_log;
+  gates.floor_raw = params->floor_raw;
+  gates.beta_max = params->beta_max;
+  gates.floor_min = params->floor_min;
+  gates.beta = beta;
+  gates.log_decay = log_decay;
+  gates.floor = floor;
+  gates.shifted = params->key_shift ? shifted : nullptr;
   return forward_impl<float, true>("m4mr_mixer_forward", nullptr, value, nullptr, beta, log_decay,
                                    floor, init_evidence, init_cross, B, T, H, value_dim, chunk,
                                    output, variance, final_evidence, final_cross, solved, factors,
-                                   start_evidence, start_cross, stream, mix, gate);
+                                   start_evidence, start_cross, stream, mix, gate, gates);
 }
 
 int m4mr_mixer_backward(const float* key, const float* value, const float* query,
@@ -769,22 +785,16 @@ int m4mr_mixer_read_backward(const float* key, const float* value, const float* 
   mg.d_dt_raw = d_dt_raw;
   mg.d_previous = d_previous;
   mg.grads_part = mw.grads_part;
-  int rc = backward_impl<float, true, true>(
+  mg.d_scale = d_confidence_scale;
+  mg.d_skip = d_skip;
+  mg.d_beta_bias = d_beta_bias;
+  mg.d_dt_bias = d_dt_bias;
+  mg.d_a_log = d_a_log;
+  return backward_impl<float, true, true>(
       entry, nullptr, value, nullptr, beta, log_decay, floor, B, T, H, value_dim, chunk, solved,
       factors, start_evidence, start_cross, nullptr, nullptr, d_final_evidence, d_final_cross,
       nullptr, d_value, nullptr, nullptr, nullptr, d_floor_raw, d_init_evidence, d_init_cross,
       workspace, workspace_bytes, stream, mix, /*spill_free=*/false, mg, params->floor_raw);
-  if (rc) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = launch("head_sums", st, [&] {
-    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 2), dim3(1024), 0, st, mw.dy_part,
-                       mw.chunks, H, 2, d_confidence_scale, d_skip, nullptr);
-  });
-  if (rc) return rc;
-  return launch("head_sums", st, [&] {
-    hipLaunchKernelGGL(m4::head_sums_kernel, dim3(H * 3), dim3(1024), 0, st, mw.grads_part,
-                       mw.chunks, H, 3, d_beta_bias, d_dt_bias, d_a_log);
-  });
 }
 
 int m4mr_start_counts(int T, int chunk, int* chunks, int* evidence_starts) {

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* G = K + TILE;
   float* C0 = G + TILE;  // C0 transposed: C0[e][p]
   __shared__ ChunkScalars cs;
-  __shared__ float var_s[MIX ? MAXC : 1];  // MIX: the chunk's variances, for the gate
+  __shared__ float gate_s[MIX ? MAXC : 1];  // MIX: the chunk's read gates
   const long nseq = (long)d.B * d.H * d.NC;
   // The wave's 16-row strip (its causal products cost strip + 1 blocks).
   const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
@@ -123,13 +123,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   // The chunk's log decays and betas, lane s of wave 0 holding token s's
   // (the other lanes read out of range), fetched with its first tiles.
-  float sg, sb;
+  // MIX: the head's gate parameters too.
+  float sg, sb, hscale = 0.f, hskip = 0.f;
   auto fetch_scalars = [&](const SeqIndex& s) {
     const unsigned st = (unsigned)d.H * 4, bytes = s.len > 0 ? (unsigned)(s.len - 1) * st + 4 : 0;
     const long th = token_head(d, s.b, s.n * d.chunk, s.h);
     const unsigned off = threadIdx.x < 64 ? threadIdx.x * st : kNoRow;
     sg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
     sb = buf_load1(buf_rsrc(beta + th, bytes), off);
+    if constexpr (MIX) {
+      hscale = gate.confidence_scale[s.h];
+      hskip = gate.skip[s.h];
+    }
   };
   fetch_tokens(ry, si.len, rows_of(solved, d, si));
   fetch_scalars(si);
@@ -146,6 +151,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       rk.store(K);
     rc.store(C0);
     if (threadIdx.x < 64) finish_chunk_scalars(cs, sg, sb);
+    const float scale = hscale, skip = hskip;  // this chunk's head
     __syncthreads();
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
@@ -163,16 +169,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
     // the 16 lanes that hold the rest of each row.
+    float vrow[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = (threadIdx.x >> 4) + 16 * j;
       const f4 qt = MIX ? mix_unit(rq.get(j)) : rq.get(j);
       const f4 prod = qt * *reinterpret_cast<const f4*>(Y + t * LDT + c4);
       const float v = row16_sum(prod[0] + prod[1] + prod[2] + prod[3]);
+      vrow[j] = v;
       if ((threadIdx.x & 15) == 0 && t < si.len)
         variance[token_head(d, si.b, si.n * d.chunk + t, si.h)] = v;
-      if constexpr (MIX)
-        if ((threadIdx.x & 15) == 0) var_s[t] = v;
+    }
+    if constexpr (MIX) {
+      // The epilogue's gate of each row, evaluated once per row.
+      float g[4];
+      per_row<4>(vrow, g, [&](float v) { return read_gate(scale, v); });
+      if ((threadIdx.x & 15) == 0)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gate_s[(threadIdx.x >> 4) + 16 * j] = g[j];
     }
     fetch_queries(sn);
 
@@ -222,11 +236,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const f4 x = quad_row(out, q) + carried * quad_row(inh, q);
           if constexpr (MIX) {
             // The epilogue's arithmetic: g x + D value (value tile v is in K).
-            const float g = mix_sigmoid(1.f - gate.confidence_scale[si.h] * log1pf(var_s[t]));
-            const float dv = gate.skip[si.h];
+            const float g = gate_s[t];
             const f4 val = *reinterpret_cast<const f4*>(K + t * LDT + c4);
             *reinterpret_cast<f4*>(gate.read + row + c4) = x;
-            *reinterpret_cast<f4*>(output + row + c4) = g * x + dv * val;
+            *reinterpret_cast<f4*>(output + row + c4) = g * x + skip * val;
           } else {
             *reinterpret_cast<f4*>(output + row + c4) = x;
           }
@@ -305,14 +318,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
   // The chunk's log decays and betas (lane s of wave 0: token s; the other
-  // lanes read out of range), fetched with its first tiles.
-  float sg, sb;
+  // lanes read out of range), fetched with its first tiles.  GATE: the
+  // head's confidence scale too.
+  float sg, sb, hscale = 0.f;
   auto fetch_scalars = [&](const SeqIndex& s) {
     const unsigned st = (unsigned)d.H * 4, bytes = s.len > 0 ? (unsigned)(s.len - 1) * st + 4 : 0;
     const long th = token_head(d, s.b, s.n * d.chunk, s.h);
     const unsigned off = threadIdx.x < 64 ? threadIdx.x * st : kNoRow;
     sg = buf_load1(buf_rsrc(log_decay + th, bytes), off);
     sb = buf_load1(buf_rsrc(beta + th, bytes), off);
+    if constexpr (GATE) hscale = mg.scale[s.h];
   };
   auto fetch_keys = [&](const SeqIndex& s) {
     if constexpr (MIX) {
@@ -321,18 +336,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       fetch_tokens(rk, s.len, rows_of(keys, d, s));
     }
   };
+  // GATE: the read rows of value tile v of chunk s (zero past the chunk),
+  // this lane's accumulator rows, for the variance cotangent.  Tile 0's
+  // load with the chunk's first tiles, the others' before their products.
+  f4 rq[4];
+  auto fetch_read = [&](const SeqIndex& s, int v) {
+    if constexpr (GATE) {
+      const long th = token_head(d, s.b, s.n * d.chunk, s.h);
+      const unsigned st = (unsigned)d.H * d.P;
+      const BufRsrc rr = buf_rsrc(mg.read + th * d.P + 64 * v,
+                                  s.len > 0 ? ((unsigned)(s.len - 1) * st + 64) * 4 : 0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) rq[q] = buf_load4(rr, ((unsigned)acc_row(w, q) * st + c4) * 4);
+    }
+  };
   fetch_tokens(rd, si.len, value_rows(d_output, d, si, 0));
   fetch_tokens(rv, si.len, value_rows(values, d, si, 0));
   fetch_scalars(si);
   fetch_keys(si);
   rc.fetch_matrix(cross_tile(start_c, d, si.seq, 0));
   fetch_rows_q(si);
+  fetch_read(si, 0);
 
   for (;;) {
     rd.store(DO);
     rv.store(V);
     rc.store(C0);
     if (threadIdx.x < 64) finish_chunk_scalars(cs, sg, sb);
+    const float scale = hscale;  // this chunk's head (GATE)
     __syncthreads();
     const long next = seq + gridDim.x;
     const bool more = next < nseq;  // uniform over the block
@@ -367,17 +398,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
         fetch_scalars(sn);
       }
-      f4 rq[4];
-      if constexpr (GATE) {
-        // The read rows of value tile v (zero past the chunk), for the
-        // variance cotangent; in flight during the products.
-        const long th = token_head(d, si.b, si.n * d.chunk, si.h);
-        const unsigned st = (unsigned)d.H * d.P;
-        const BufRsrc rr = buf_rsrc(mg.read + th * d.P + 64 * v,
-                                    ((unsigned)(si.len - 1) * st + 64) * 4);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rq[q] = buf_load4(rr, ((unsigned)acc_row(w, q) * st + c4) * 4);
-      }
+      if (v > 0) fetch_read(si, v);  // in flight during the products
       tile_mma_causal<false>(acc, DO, V, w);      // dout_t . v_s, s <= t
       tile_mma<false, false>(inh, DO, C0, 64, w);  // C0^T dout_t
       if constexpr (GATE) {
@@ -391,20 +412,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+    fetch_read(sn, 0);  // the next chunk's first read rows
     // GATE: each row's gate, its variance cotangent and the chunk's
     // contributions to the gate parameters' gradients.
     float gate[4] = {1.f, 1.f, 1.f, 1.f};
     if constexpr (GATE) {
-      const float scale = mg.scale[si.h];
       float pscale = 0.f, pskip = 0.f;
+      // Per row (once per row): log1p(var), the gate and d log1p / d var.
+      float lvs[4], slopes[4];
+      per_row<4>(gvar, lvs, [](float v) { return log1pf(v); });
+      per_row<4>(gvar, slopes, [&](float v) { return -scale / (1.f + v); });
+      per_row<4>(gvar, gate, [&](float v) { return read_gate(scale, v); });
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int t = acc_row(w, q);
         const float dr = row16_sum(dotr[q]), dsk = row16_sum(dotv[q]);
-        const float lv = log1pf(gvar[q]);
-        gate[q] = mix_sigmoid(1.f - scale * lv);
+        const float lv = lvs[q];
         const float slope = dr * gate[q] * (1.f - gate[q]);
-        dvar[q] += slope * (-scale / (1.f + gvar[q]));
+        dvar[q] += slope * slopes[q];
         if ((lane_id() & 15) == 0 && t < si.len)
           mg.d_var[token_head(d, si.b, si.n * d.chunk + t, si.h)] = dvar[q];
         // Rows past the chunk read zeros: their terms vanish.
@@ -517,13 +542,16 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     float* __restrict__ floor_part, MixerIn mix, MixerGrad mg) {
   static_assert(!GATE || MIX, "the gated backward reads the mixer's raw rows");
   extern __shared__ float smem[];
-  float* Kt = smem;       // keys, then S0
+  float* Kt = smem;       // keys, then S0 (but for GATE)
   float* Vt = Kt + TILE;  // a value tile, then a C0 tile
   float* Yt = Vt + TILE;
   float* Zt = Yt + TILE;
   float* Dt = Zt + TILE;  // a dout tile
   float* M1 = Dt + TILE;  // W * gy transposed (M1[s][t]), then G_end
   float* M2 = M1 + TILE;  // W * (gv - gz) transposed, then an H_end tile
+  // GATE: S0 in an eighth tile, so the unit keys stay in Kt for phase 5.
+  float* S0t = GATE ? M2 + TILE : Kt;
+  __shared__ float kinv[GATE ? 64 : 1];  // GATE: each key row's 1 / norm
   __shared__ ChunkScalars cs;
   __shared__ float colpart[4][64];
   __shared__ float rowpart[2][64], quadpart[2][64], startpart[2][64];
@@ -548,7 +576,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   // Token tt's log decay and beta in thread tt < 64, d_variance of this
   // thread's tile-fetch rows; zero past the chunk (out-of-range offsets).
   // GATE: the variance of the same rows (for their read gates).
-  float pg = 0.f, pbt = 0.f, pdv[2], pgv[2];
+  // GATE: the head's gate parameters too.
+  float pg = 0.f, pbt = 0.f, pdv[2], pgv[2], hpar[4] = {0.f, 0.f, 0.f, 0.f};
   auto fetch_scalars = [&](const SeqIndex& sx) {
     const unsigned tt = threadIdx.x, st = (unsigned)d.H * 4;
     const unsigned bytes = sx.len > 0 ? (unsigned)(sx.len - 1) * st + 4 : 0;
@@ -563,6 +592,10 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       const BufRsrc rg = buf_rsrc(mg.variance + th, bytes);
 #pragma unroll
       for (int j = 0; j < 2; ++j) pgv[j] = buf_load1(rg, ((tt >> 4) + 32 * j) * st);
+      hpar[0] = mg.scale[sx.h];
+      hpar[1] = mg.skip[sx.h];
+      hpar[2] = mg.a_log[sx.h];
+      hpar[3] = mg.dt_bias[sx.h];
     }
   };
   fetch_keys(si);
@@ -587,10 +620,10 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     // d_variance of this thread's tile-fetch rows (tid/16 + 32j).
     const float dvar[2] = {pdv[0], pdv[1]};
     // GATE: the read gates of those rows; the dout tiles are gated as staged.
+    // This chunk's head parameters: confidence scale, skip, a_log, dt_bias.
+    const float scale = hpar[0], skip = hpar[1], a_log = hpar[2], dt_bias = hpar[3];
     float gr[2] = {1.f, 1.f};
-    if constexpr (GATE)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) gr[j] = read_gate(mg.scale[si.h], pgv[j]);
+    if constexpr (GATE) per_row<2>(pgv, gr, [&](float v) { return read_gate(scale, v); });
     auto store_dout = [&](const RowTile<float, GRADS_THREADS>& t) {
       if constexpr (GATE)
         t.store_scaled(Dt, gr);
@@ -599,7 +632,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     };
 
     if constexpr (MIX)
-      tk.store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0);
+      tk.store_unit(Kt, mix.key_shift && !mix.previous && si.n == 0, GATE ? kinv : nullptr);
     else
       tk.store(Kt);
     tv.store(Vt);
@@ -765,6 +798,17 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
             rhv.store(M2);
             __syncthreads();
           }
+          // GATE: the skip term's d_out rows, in flight during the products.
+          float2 sk_dout[4];
+          if constexpr (GATE) {
+            const unsigned st = (unsigned)d.H * d.P;
+            const long th0 = token_head(d, si.b, si.n * d.chunk, si.h);
+            const BufRsrc ro = buf_rsrc(mg.d_out + th0 * d.P + 64 * v,
+                                        ((unsigned)(si.len - 1) * st + 64) * 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              sk_dout[q] = buf_load2(ro, ((unsigned)acc_row(ws, q) * st + c4 + 2 * hf) * 4);
+          }
           f4 hk[2];
           zero2(hk);
           tile_mma_half<false, true, true>(hk, Kt, M2, 64, ws, hf);  // H k_s
@@ -781,10 +825,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
               float2 gv2 = float2{dv[v][0][q] + tl * hk[0][q], dv[v][1][q] + tl * hk[1][q]};
               if constexpr (GATE) {
                 // The skip's term of the value gradient: skip d_out.
-                const float sk = mg.skip[si.h];
-                const float2 dq = *reinterpret_cast<const float2*>(mg.d_out + at);
-                gv2.x += sk * dq.x;
-                gv2.y += sk * dq.y;
+                gv2.x += skip * sk_dout[q].x;
+                gv2.y += skip * sk_dout[q].y;
               }
               *reinterpret_cast<float2*>(d_values + at) = gv2;
             }
@@ -814,13 +856,23 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         *reinterpret_cast<float2*>(M1 + acc_row(ws, q) * LDT + c4 + 2 * hf) = dkq[q];
     if (tid < 64) quad[tid] = quadpart[0][tid] + quadpart[1][tid];
     fetch_keys(sx);
+    // GATE: the raw query rows of this thread's tile-fetch rows (zero past
+    // the chunk), for phase 5; in flight during phase 4.
+    f4 xq[2];
+    if constexpr (GATE) {
+      const unsigned st = (unsigned)d.H * 64;
+      const BufRsrc rq = buf_rsrc(mix.query + token_head(d, si.b, si.n * d.chunk, si.h) * 64,
+                                  ((unsigned)(si.len - 1) * st + 64) * 4);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) xq[j] = buf_load4(rq, (((tid >> 4) + 32 * j) * st + c4) * 4);
+    }
 
     // Phase 4: start-state terms <A_bar_t, S0>, <C_bar_t, C0> and <G,S0>+<H,C0>,
     // the C0 terms summed over the value tiles from the first (whose H and
     // dout tiles are in LDS).  <G, S0> and, with one value tile, <H, C0> come
     // from the fetch registers (both operands in the same layout).  The
     // chunk's start evidence is the start of its first sub-chunk.
-    rs.store(Kt);
+    rs.store(S0t);
     rc.store(Vt);
     __syncthreads();
     {
@@ -832,7 +884,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       f4 ys[2], dc[2];
       zero2(ys);
       zero2(dc);
-      tile_mma_half<false, false>(ys, Yt, Kt, 64, ws, hf);  // y_t^T S0
+      tile_mma_half<false, false>(ys, Yt, S0t, 64, ws, hf);  // y_t^T S0
       fetch_tokens(tv, sx.len, value_rows(values, d, sx, 0));
       for (int v = 0; v < d.NV; ++v) {
         if (v > 0) {
@@ -918,7 +970,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         const float ld = buf_load1(buf_rsrc(log_decay + th0, bytes), t * st);
         const float bt = cs.beta[t];
         const float dbr = mg.beta_max != 0.f ? db * bt * (1.f - bt / mg.beta_max) : 0.f;
-        const float ddt = -suffix * expf(mg.a_log[si.h]) * mix_sigmoid(draw + mg.dt_bias[si.h]);
+        const float ddt = -suffix * expf(a_log) * mix_sigmoid(draw + dt_bias);
         if (t < si.len) {
           mg.d_beta_raw[th] = dbr;
           mg.d_dt_raw[th] = ddt;
@@ -948,26 +1000,19 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
         const f4 yr = *reinterpret_cast<const f4*>(Yt + t * LDT + c4);
         const long th = token_head(d, si.b, si.n * d.chunk + t, si.h);
         if constexpr (GATE) {
-          // Through the unit normalisations to the raw rows: r (g - u (u . g))
-          // with u the normalised row and r its 1 / norm (unit_row_vjp).
-          auto unit_vjp = [&](const f4& x, const f4& g) {
-            const float r2 = __builtin_amdgcn_rsqf(
-                row16_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]) + 1e-6f);
-            const f4 u = r2 * x;
-            const float ug = row16_sum(u[0] * g[0] + u[1] * g[1] + u[2] * g[2] + u[3] * g[3]);
-            return r2 * (g - ug * u);
-          };
+          // Through the unit normalisations to the raw rows (mix_unit_vjp):
+          // the queries from their raw rows, the keys from their unit rows
+          // (still in Kt) and 1 / norms.
           const int tp = si.n * d.chunk + t;  // position in the sequence
           const bool in = t < si.len;
-          const f4 xq = in ? *reinterpret_cast<const f4*>(mix.query + th * 64 + c4)
-                           : f4{0.f, 0.f, 0.f, 0.f};
-          const f4 dq = unit_vjp(xq, zr + dvar[j] * yr);
+          const float rq = mix_inv_norm(xq[j]);
+          const f4 dq = mix_unit_vjp(xq[j] * rq, rq, zr + dvar[j] * yr);
           if (in) *reinterpret_cast<f4*>(mg.d_query + th * 64 + c4) = dq;
-          // Key t: its source row (raw key t - 1 with the shift, or the
-          // cached key at t = 0, or none) takes the VJP of its unit row.
-          const float* src = in ? mix_key_row(mix, d, si.b, tp, si.h) : nullptr;
-          const f4 xk = src ? *reinterpret_cast<const f4*>(src + c4) : f4{0.f, 0.f, 0.f, 0.f};
-          const f4 dk = unit_vjp(xk, *reinterpret_cast<const f4*>(M1 + t * LDT + c4));
+          // Key t's source row: raw key t - 1 with the shift (position 0:
+          // the cached key, or none: a zero row, whose cotangent is zero).
+          const f4 dk = mix_unit_vjp(*reinterpret_cast<const f4*>(Kt + t * LDT + c4), kinv[t],
+                                     *reinterpret_cast<const f4*>(M1 + t * LDT + c4));
+          const bool zero_src = mix.key_shift && tp == 0 && !mix.previous;
           float* dst = nullptr;
           if (in) {
             if (!mix.key_shift)
@@ -977,7 +1022,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
             else if (mg.d_previous)
               dst = mg.d_previous + ((long)si.b * d.H + si.h) * 64;
           }
-          if (dst) *reinterpret_cast<f4*>(dst + c4) = src ? dk : f4{0.f, 0.f, 0.f, 0.f};
+          if (dst) *reinterpret_cast<f4*>(dst + c4) = zero_src ? f4{0.f, 0.f, 0.f, 0.f} : dk;
           // The last raw key feeds only the cache entry (its cotangent,
           // or zero); without the shift the cached key feeds nothing.
           if (in && mix.key_shift && tp == d.T - 1)
@@ -1048,12 +1093,11 @@ M4_MIXER_KERNELS(true)
 // floor_raw (the mixer's fused backward; may be null): the result is carried
 // through floor = floor_min + softplus(floor_raw), d floor_raw = d floor
 // sigmoid(floor_raw).
-__global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* __restrict__ part,
-                                                          float* __restrict__ d_floor,
-                                                          const float* __restrict__ floor_raw) {
-  const int h = blockIdx.x >> 4, c4 = blockIdx.x & 15;
+__device__ __forceinline__ void floor_block(const Dims& d, const float* __restrict__ part,
+                                            float* __restrict__ d_floor,
+                                            const float* __restrict__ floor_raw, int h, int c4,
+                                            f4* partial) {
   const int entries = d.B * d.NC;
-  __shared__ f4 partial[256];
   f4 acc = f4{0.f, 0.f, 0.f, 0.f};
   for (int e = threadIdx.x; e < entries; e += 256) {
     const int b = e / d.NC, n = e % d.NC;
@@ -1073,6 +1117,52 @@ __global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* 
       for (int e = 0; e < 4; ++e) out[e] *= mix_sigmoid(fr[e]);
     }
     *reinterpret_cast<f4*>(d_floor + h * 64 + 4 * c4) = out;
+  }
+}
+
+__global__ __launch_bounds__(256) void floor_reduce_kernel(Dims d, const float* __restrict__ part,
+                                                          float* __restrict__ d_floor,
+                                                          const float* __restrict__ floor_raw) {
+  __shared__ f4 partial[256];
+  floor_block(d, part, d_floor, floor_raw, blockIdx.x >> 4, blockIdx.x & 15, partial);
+}
+
+// The fused mixer backward's last launch: blocks 0 .. 16H - 1 reduce the
+// floor_raw gradient (floor_block), the next 5H the per-head parameter
+// gradients from the per-chunk partials (B NC of them per head and
+// parameter): block 16H + 5h + j sums dy_part[(2h + j) B NC ..] for j < 2
+// (d confidence_scale, d skip) or grads_part[(3h + j - 2) B NC ..] (d
+// beta_bias, d dt_bias, d a_log), thread i over entries i, i + 256, ... in
+// order, then a fixed tree.  Deterministic run to run.
+__global__ __launch_bounds__(256) void mixer_finish_kernel(
+    Dims d, const float* __restrict__ floor_part, float* __restrict__ d_floor_raw,
+    const float* __restrict__ floor_raw, const float* __restrict__ dy_part,
+    const float* __restrict__ grads_part, float* __restrict__ d_scale,
+    float* __restrict__ d_skip, float* __restrict__ d_beta_bias, float* __restrict__ d_dt_bias,
+    float* __restrict__ d_a_log) {
+  __shared__ f4 partial[256];
+  const int floor_blocks = d.H * 16;
+  if ((int)blockIdx.x < floor_blocks) {
+    floor_block(d, floor_part, d_floor_raw, floor_raw, blockIdx.x >> 4, blockIdx.x & 15,
+                partial);
+    return;
+  }
+  const int k = blockIdx.x - floor_blocks, h = k / 5, j = k % 5;
+  const long chunks = (long)d.B * d.NC;
+  const float* src = j < 2 ? dy_part + (2L * h + j) * chunks : grads_part + (3L * h + j - 2) * chunks;
+  float acc = 0.f;
+  for (long e = threadIdx.x; e < chunks; e += 256) acc += src[e];
+  float* red = reinterpret_cast<float*>(partial);
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float* out = j == 0 ? d_scale : j == 1 ? d_skip : j == 2 ? d_beta_bias : j == 3 ? d_dt_bias
+                                                                                      : d_a_log;
+    out[h] = red[0];
   }
 }
 

@@ -40,6 +40,9 @@ __device__ __forceinline__ BufRsrc buf_rsrc(const void* base, unsigned bytes) {
 __device__ __forceinline__ float buf_load1(BufRsrc r, unsigned off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+__device__ __forceinline__ float2 buf_load2(BufRsrc r, unsigned off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
 __device__ __forceinline__ f4 buf_load4(BufRsrc r, unsigned off) {
   return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
@@ -157,6 +160,35 @@ struct MixerIn {
 
 __device__ __forceinline__ float mix_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
 
+// log(1 + e^x) without overflow.
+__device__ __forceinline__ float mix_softplus(float x) {
+  return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
+}
+
+// The prologue's gates from the raw gate projections (SelectiveMemoryMixer,
+// lm/models/mamba4.py:196-237), computed where the fused mixer forward's
+// state walk first needs them and written out there for the later kernels
+// and the backward: beta = beta_max sigmoid(beta_raw + beta_bias), log
+// decay = -exp(a_log) softplus(dt_raw + dt_bias), floor = floor_min +
+// softplus(floor_raw), and with the key shift the raw key of position T - 1
+// (`shifted`, may be null).
+struct MixerGates {
+  const float *beta_raw, *dt_raw;                     // [B,T,H]
+  const float *beta_bias, *dt_bias, *a_log;           // [H]
+  const float* floor_raw;                             // [H,64]
+  float beta_max, floor_min;
+  float *beta, *log_decay;                            // [B,T,H]
+  float* floor;                                       // [H,64]
+  float* shifted;                                     // [B,H,64]
+};
+
+__device__ __forceinline__ float mix_beta(const MixerGates& g, float raw, int h) {
+  return g.beta_max * mix_sigmoid(raw + g.beta_bias[h]);
+}
+__device__ __forceinline__ float mix_log_decay(const MixerGates& g, float raw, int h) {
+  return -expf(g.a_log[h]) * mix_softplus(raw + g.dt_bias[h]);
+}
+
 // Raw source row of position t's key (null: the zero row).
 __device__ __forceinline__ const float* mix_key_row(const MixerIn& m, const Dims& d, int b, int t,
                                                     int h) {
@@ -177,10 +209,19 @@ __device__ __forceinline__ float row16_sum_dpp(float x) {
 
 // Unit normalisation of a row held as one 4-float quad per lane of a
 // 16-lane DPP row.
-__device__ __forceinline__ f4 mix_unit(const f4& v) {
+__device__ __forceinline__ float mix_inv_norm(const f4& v) {
   float s = 0.f;
   s += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-  return v * __builtin_amdgcn_rsqf(row16_sum_dpp(s) + 1e-6f);
+  return __builtin_amdgcn_rsqf(row16_sum_dpp(s) + 1e-6f);
+}
+__device__ __forceinline__ f4 mix_unit(const f4& v) { return v * mix_inv_norm(v); }
+
+// VJP of the unit normalisation u = x r, r = rsqrt(sum x^2 + 1e-6), from u
+// and r: dx = r (g - u (u . g)) (prologue_backward_kernel's arithmetic,
+// rearranged).  Rows as in mix_unit.
+__device__ __forceinline__ f4 mix_unit_vjp(const f4& u, float r, const f4& g) {
+  const float ug = row16_sum_dpp(u[0] * g[0] + u[1] * g[1] + u[2] * g[2] + u[3] * g[3]);
+  return r * (g - ug * u);
 }
 
 // The mixer's read gating fused into the read (lm/models/mamba4.py:266-273):
@@ -201,7 +242,8 @@ struct ReadGate {
 // bwd_dy forms and writes for bwd_grads.  Per-chunk partial sums of the
 // per-head parameter gradients go to dy_part ([H][2][B NC]: d scale,
 // d skip) and grads_part ([H][3][B NC]: d beta_bias, d dt_bias, d a_log),
-// entry (h, j, b NC + n), for head_sums_kernel.
+// entry (h, j, b NC + n), which mixer_finish_kernel sums into d_scale ..
+// d_a_log.
 struct MixerGrad {
   const float* d_out;     // [B,T,H,P] cotangent of the gated output
   const float* read;      // [B,T,H,P] the forward's ungated read
@@ -222,11 +264,44 @@ struct MixerGrad {
   float* d_dt_raw;         // [B,T,H]
   float* d_previous;       // [B,H,64], or null
   float* grads_part;
+  float *d_scale, *d_skip, *d_beta_bias, *d_dt_bias, *d_a_log;  // [H] each
 };
 
 // The read gate of a token: sigmoid(1 - scale log1p(var)).
 __device__ __forceinline__ float read_gate(float scale, float var) {
   return mix_sigmoid(1.f - scale * log1pf(var));
+}
+
+// x at lane SRC of this lane's 16-lane DPP row (row_newbcast).
+template <int SRC>
+__device__ __forceinline__ float row_lane(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + SRC, 0xf, 0xf, true));
+}
+
+// One value per row of the N rows a 16-lane row holds (every lane has all N
+// inputs in[0..N-1]): lane k < N evaluates f(in[k]) once, and every lane
+// receives the N results, so a costly per-row function runs once per row
+// instead of once per lane and row.
+template <int N, typename F>
+__device__ __forceinline__ void per_row(const float (&in)[N], float (&out)[N], F f) {
+  const int k = threadIdx.x & 15;
+  // The inputs pass through an empty asm as registers, so the selection
+  // below stays a chain of selects (not a load from a stack copy of in[]).
+  float v[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    v[i] = in[i];
+    asm volatile("" : "+v"(v[i]));
+  }
+  float x = v[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) x = k == i ? v[i] : x;
+  const float y = f(x);
+  if constexpr (N > 0) out[0] = row_lane<0>(y);
+  if constexpr (N > 1) out[1] = row_lane<1>(y);
+  if constexpr (N > 2) out[2] = row_lane<2>(y);
+  if constexpr (N > 3) out[3] = row_lane<3>(y);
 }
 
 // Per-chunk log-decay prefix, tail weights and chunk length, staged in LDS
@@ -589,13 +664,21 @@ struct RowTile {
       *reinterpret_cast<f4*>(tile + (r0 + RS * j) * LDT + q) = sc[j] * get(j);
   }
   // The rows unit-normalised (mix_unit), row 0 as a zero row if zero_row0.
-  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0) const {
+  // inv (may be null): each row's 1 / norm, rsqrt(sum x^2 + 1e-6), as well.
+  __device__ __forceinline__ void store_unit(float* tile, bool zero_row0,
+                                             float* inv = nullptr) const {
     const int r0 = threadIdx.x >> 4, q = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int r = r0 + RS * j;
       const f4 x = zero_row0 && r == 0 ? f4{0.f, 0.f, 0.f, 0.f} : get(j);
-      *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
+      if (inv) {
+        const float rn = mix_inv_norm(x);
+        *reinterpret_cast<f4*>(tile + r * LDT + q) = x * rn;
+        if ((threadIdx.x & 15) == 0) inv[r] = rn;
+      } else {
+        *reinterpret_cast<f4*>(tile + r * LDT + q) = mix_unit(x);
+      }
     }
   }
 };
@@ -704,6 +787,7 @@ struct StateArgs {
   float* last_s;         // the state after the last step
   float* last_c;
   MixerIn mix;           // forward with the mixer's projections (MIX): keys and gates
+  MixerGates gates;      // forward (MIX): the gates from their raw projections
   // Backward of the mixer's gated output (MIX): the cross a rows are the
   // gated output's cotangent d_out, so the read's cotangent is g_t d_out_t
   // with the read gate g_t = read_gate(confidence_scale, variance_t).

@@ -15,8 +15,6 @@
 // epilogue_backward_kernel  its VJP and per-block partials.
 // head_sums_kernel          the per-head parameter gradients: the per-block
 //                           partials summed in block order (deterministic).
-// mixer_gates_kernel        the prologue's beta, log decay and floor alone,
-//                           for the fused mixer read.
 //
 // Every kernel takes 16 lanes per token-head (one 16-lane DPP row), so a
 // 64-float row is one 16-byte access per lane; rows of other widths (a
@@ -27,12 +25,8 @@ namespace m4 {
 
 constexpr int MIX_ROWS = 16;  // token-heads per 256-thread block
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
-
-// log(1 + e^x) without overflow.
-__device__ __forceinline__ float softplusf(float x) {
-  return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
-}
+__device__ __forceinline__ float sigmoidf(float x) { return mix_sigmoid(x); }
+__device__ __forceinline__ float softplusf(float x) { return mix_softplus(x); }
 
 // Sum over the 16 lanes of this thread's row; every lane receives the total.
 __device__ __forceinline__ float row_sum(float x) { return row16_sum(x); }
@@ -164,30 +158,6 @@ __global__ __launch_bounds__(256) void prologue_forward_kernel(
 // its floor, with the same arithmetic; with a non-null `shifted`, the
 // threads of position T-1 copy their raw key row there (the next call's
 // cached key).
-__global__ __launch_bounds__(256) void mixer_gates_kernel(
-    const float* __restrict__ beta_raw, const float* __restrict__ dt_raw,
-    const float* __restrict__ beta_bias, const float* __restrict__ dt_bias,
-    const float* __restrict__ a_log, const float* __restrict__ floor_raw,
-    const float* __restrict__ key, int B, int T, int H, int D, float beta_max, float floor_min,
-    float* __restrict__ beta, float* __restrict__ log_decay, float* __restrict__ floor,
-    float* __restrict__ shifted) {
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < H * D; i += blockDim.x)
-      floor[i] = floor_min + softplusf(floor_raw[i]);
-  const long th = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (th >= (long)B * T * H) return;
-  const int h = (int)(th % H);
-  beta[th] = beta_max * sigmoidf(beta_raw[th] + beta_bias[h]);
-  log_decay[th] = -expf(a_log[h]) * softplusf(dt_raw[th] + dt_bias[h]);
-  const long bt = th / H;
-  if (shifted && bt % T == T - 1) {
-    const long b = bt / T;
-    for (int c = 0; c < D; c += 4)
-      *reinterpret_cast<f4*>(shifted + (b * H + h) * D + c) =
-          *reinterpret_cast<const f4*>(key + th * D + c);
-  }
-}
-
 // Per-block partials of per-head sums: slot j of head h is the sum, in row
 // order, of the values `v` of this block's rows of head h.  Lanes 0 of each
 // row hold their row's values in vals[row][j].

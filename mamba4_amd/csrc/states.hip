@@ -351,6 +351,25 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   };
   const long edge = cross ? (long)bh * d.NV + v : bh;
 
+  // MIX forward: the head's gate parameters, loaded once (the gates are
+  // computed per step on the walk's critical path).
+  // The backward's gated cross walk: the head's confidence scale.
+  float rate = 0.f, dt_bias = 0.f, beta_bias = 0.f, cscale = 0.f;
+  if constexpr (GATED) cscale = g.confidence_scale[h];
+  if constexpr (MIX_KEYS) {
+    rate = expf(g.gates.a_log[h]);
+    dt_bias = g.gates.dt_bias[h];
+    beta_bias = g.gates.beta_bias[h];
+    // The evidence walks of batch row 0 write their head's floor; each
+    // evidence walk its (b, h)'s shifted key.
+    if (!cross && b == 0 && threadIdx.x < 64)
+      g.gates.floor[h * 64 + threadIdx.x] =
+          g.gates.floor_min + mix_softplus(g.gates.floor_raw[h * 64 + threadIdx.x]);
+    if (!cross && g.gates.shifted && threadIdx.x < 16)
+      *reinterpret_cast<f4*>(g.gates.shifted + ((long)b * d.H + h) * 64 + 4 * threadIdx.x) =
+          *reinterpret_cast<const f4*>(g.mix.key + token_head(d, b, d.T - 1, h) * 64 +
+                                       4 * threadIdx.x);
+  }
   f4 acc[2];
   zero2(acc);
   if (const float* first = cross ? g.first_c : g.first_s) {
@@ -425,14 +444,15 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
                         (unsigned)(d.H * width));
     }
     // Wave 0's lane l: token l's log decay and beta (zero past the chunk; the
-    // other waves read out of range).
+    // other waves read out of range).  MIX forward: their raw projections
+    // dt_raw and beta_raw; the backward's gated cross walk: the variance in
+    // place of beta.
     const long th = token_head(d, b, first, h);
     const unsigned bytes = (unsigned)(cnt - 1) * d.H * 4 + 4;
     const unsigned off = w == 0 ? (unsigned)l * d.H * 4 : kNoRow;
-    R.pg = buf_load1(buf_rsrc(g.log_decay + th, bytes), off);
-    // (The backward's gated cross walk takes token l's variance instead.)
-    R.pb = BWD && !(GATED && cross) ? 0.f
-                                    : buf_load1(buf_rsrc((BWD ? g.variance : g.beta) + th, bytes), off);
+    R.pg = buf_load1(buf_rsrc((MIX_KEYS ? g.gates.dt_raw : g.log_decay) + th, bytes), off);
+    const float* pb_src = BWD ? g.variance : MIX_KEYS ? g.gates.beta_raw : g.beta;
+    R.pb = BWD && !(GATED && cross) ? 0.f : buf_load1(buf_rsrc(pb_src + th, bytes), off);
   };
   auto stage = [&](const StepRegs& R, int u, int i) {
     if constexpr (MIX_KEYS)
@@ -441,18 +461,32 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
       R.rb.store(smem + 2 * u * TILE);
     if (own_a) R.ra.store(smem + (2 * u + 1) * TILE);
     if (w == 0) {
+      const int cnt = chunk_len(d, i), cut = parts == 2 ? min(d.sub, cnt) : cnt;
+      float pg = R.pg, pb = R.pb;
+      if constexpr (MIX_KEYS) {
+        // The gates from their raw projections (zero past the chunk); the
+        // evidence walk writes them out for the factor and read kernels.
+        const bool in = l < cnt;
+        // mix_log_decay and mix_beta with the head's parameters preloaded.
+        pg = in ? -rate * mix_softplus(R.pg + dt_bias) : 0.f;
+        pb = in ? g.gates.beta_max * mix_sigmoid(R.pb + beta_bias) : 0.f;
+        if (!cross && in) {
+          const long th = token_head(d, b, i * d.chunk + l, h);
+          g.gates.log_decay[th] = pg;
+          g.gates.beta[th] = pb;
+        }
+      }
       // Inclusive log-decay prefix over the chunk; part 0 ends at token
       // `cut` - 1 (the sub-chunk boundary, or the chunk end).
-      const int cnt = chunk_len(d, i), cut = parts == 2 ? min(d.sub, cnt) : cnt;
-      const float p = wave_inclusive_sum(R.pg), last = read_lane(p, 63);
+      const float p = wave_inclusive_sum(pg), last = read_lane(p, 63);
       const float mid = cut > 0 ? read_lane(p, cut - 1) : 0.f;  // cut is uniform
       if (BWD) {
         float c = cross ? 1.f : -0.5f;
-        if (GATED && cross) c = read_gate(g.confidence_scale[h], R.pb);
+        if (GATED && cross) c = read_gate(cscale, pb);
         sb[u].wt[0][l] = c * expf(p);
       } else {
-        sb[u].wt[0][l] = l < cut ? R.pb * expf(mid - p) : 0.f;
-        sb[u].wt[1][l] = l >= cut ? R.pb * expf(last - p) : 0.f;
+        sb[u].wt[0][l] = l < cut ? pb * expf(mid - p) : 0.f;
+        sb[u].wt[1][l] = l >= cut ? pb * expf(last - p) : 0.f;
       }
       if (l == 0) {
         sb[u].decay[0] = expf(parts == 2 ? mid : last);
