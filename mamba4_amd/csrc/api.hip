@@ -510,10 +510,10 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
     args.variance = mg.variance;
     args.confidence_scale = mg.scale;
     rc = launch("bwd_states", st, [&] {
-      // The one-buffer walk spills two registers to per-lane scratch, device
-      // memory the HIP runtime provides with the dispatch; a caller that
-      // allocates nothing (spill_free) takes the two-buffer walk, which does
-      // not spill and gives the same states.
+      // The one-buffer walk is held to 80 VGPRs, where the compiler may spill
+      // to per-lane scratch (device memory the HIP runtime provides with the
+      // dispatch); a caller that allocates nothing (spill_free) takes the
+      // two-buffer walk, which has room to spare and gives the same states.
       const bool one = !spill_free && states_single_buffer(B, H, d);
       const auto walk = one ? m4::states_kernel<true, float, GATE, 1> : m4::states_kernel<true, float, GATE, 2>;
       hipLaunchKernelGGL(walk, dim3(B * H, 1 + d.NV), dim3(512),

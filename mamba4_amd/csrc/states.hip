@@ -319,8 +319,9 @@ __device__ __forceinline__ void weighted_block(f4 acc[2], const float* A, const 
 // In: element type of the forward's key and value rows (the backward's rows
 // are float32).
 // The one-buffer backward walk is held to six waves per SIMD (three blocks
-// per CU, as its LDS allows); at that budget (80 VGPRs) it spills two
-// registers to per-lane scratch, which the two-buffer walks do not.
+// per CU, as its LDS allows), a budget of 80 VGPRs at which the compiler
+// may spill to per-lane scratch (it fits today); the two-buffer walks have
+// room to spare.
 template <bool BWD, typename In, bool MIX, int NBUF>
 __global__ __launch_bounds__(STATES_THREADS)
 __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kernel(Dims d,
@@ -387,9 +388,9 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   // (which need not be symmetric): acc holds A, dfin and dscale hold D, and
   // A^T comes back through an LDS tile when a state is stored.  Both step
   // buffer counts do this, so a batch's rows give the same bits whichever
-  // variant the batch size selects.  The symmetric store needs 98 VGPRs in
-  // the two-buffer walk; the one-buffer walk is held to 80 for three blocks
-  // per CU and spills two of them.
+  // variant the batch size selects.  The symmetric store needs about 100
+  // VGPRs in the two-buffer walk; the one-buffer walk is held to 80 for three
+  // blocks per CU.
   const bool sym = BWD && !cross;
   f4 dfin[2];
   float dscale = 1.f;
@@ -397,9 +398,9 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   dfin[1] = acc[1];
   if (sym) zero2(acc);
   float* const tr = smem + 2 * NBUF * TILE;  // the transpose tile (backward only)
-  // Stores the state this lane holds (rows 16 s + 4 (l / 16) + q, columns
-  // 4 (l % 16) + 2 hf + j) at dst (+ 64 q + j).
-  auto put_state = [&](float* dst) {
+  // The state this lane holds (rows 16 s + 4 (l / 16) + q, columns
+  // 4 (l % 16) + 2 hf + j), for dst (+ 64 q + j).
+  auto state_now = [&](float2 (&out)[4]) {
     if (sym) {
       const int r0 = 16 * s + 4 * (l >> 4), c0 = 4 * (l & 15) + 2 * hf;
 #pragma unroll
@@ -411,14 +412,34 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
       for (int j = 0; j < 2; ++j) t[j] = *reinterpret_cast<const f4*>(tr + (c0 + j) * LDT + r0);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float2*>(dst + 64 * q) =
-            float2{dscale * dfin[0][q] + acc[0][q] + t[0][q],
-                   dscale * dfin[1][q] + acc[1][q] + t[1][q]};
+        out[q] = float2{dscale * dfin[0][q] + acc[0][q] + t[0][q],
+                        dscale * dfin[1][q] + acc[1][q] + t[1][q]};
     } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float2*>(dst + 64 * q) = float2{acc[0][q], acc[1][q]};
+      for (int q = 0; q < 4; ++q) out[q] = float2{acc[0][q], acc[1][q]};
     }
+  };
+  auto store_state = [&](const float2 (&v)[4], float* dst) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<float2*>(dst + 64 * q) = v[q];
+  };
+  auto put_state = [&](float* dst) {
+    float2 v[4];
+    state_now(v);
+    store_state(v, dst);
+  };
+  // A step's start states (one per part), taken before its products and
+  // stored after its staging: the staging's waits for the loads issued a step
+  // earlier then come before these stores in issue order, so they never
+  // wait for a store (the wait counter retires loads and stores in order).
+  // (parts <= 2: the forward evidence's two sub-chunks, else one; the two
+  // sets are named, not indexed, so they stay in registers.)
+  float2 held0[4], held1[4];
+  int held_i = 0;  // the step the held states start
+  auto store_held = [&]() {
+    float* base = cross ? g.steps_c : g.steps_s;
+    store_state(held0, base + state_index(held_i, 0) * 4096 + elem);
+    if (parts == 2) store_state(held1, base + state_index(held_i, 1) * 4096 + elem);
   };
 
   // Rows and scalars of one step on their way from HBM to LDS.  Two sets
@@ -431,16 +452,24 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   // (shifted; position 0's zero row reads its query row and is zeroed at
   // staging), normalised at staging.
   const MixerIn& mix = g.mix;
+  // Every step issues the same loads: a step past the walk's end (i outside
+  // 0 .. steps - 1) loads with no rows in range (zeros, no memory access), so
+  // the compiler can count the memory operations in flight and each wait
+  // retires only what it needs.
   auto fetch = [&](StepRegs& R, int i) {
-    const int first = i * d.chunk, cnt = chunk_len(d, i);
+    const bool valid = i >= 0 && i < steps;
+    const int ic = valid ? i : 0;
+    const int first = ic * d.chunk, cnt = valid ? chunk_len(d, ic) : 0;
     if constexpr (MIX_KEYS) {
       R.rb.fetch_mix_keys(cnt, mix, d, b, h, first);
     } else {
       R.rb.fetch_tokens(cnt, rows_b + token_head(d, b, first, h) * 64, (unsigned)d.H * 64);
     }
-    if (own_a) {
+    {
+      // (The forward evidence walk has no a rows: no rows in range.)
       const int width = cross ? d.P : 64, offset = cross ? 64 * v : 0;
-      R.ra.fetch_tokens(cnt, (cross ? rows_ac : rows_a) + token_head(d, b, first, h) * width + offset,
+      R.ra.fetch_tokens(own_a ? cnt : 0,
+                        (cross ? rows_ac : rows_a) + token_head(d, b, first, h) * width + offset,
                         (unsigned)(d.H * width));
     }
     // Wave 0's lane l: token l's log decay and beta (zero past the chunk; the
@@ -448,7 +477,7 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
     // dt_raw and beta_raw; the backward's gated cross walk: the variance in
     // place of beta.
     const long th = token_head(d, b, first, h);
-    const unsigned bytes = (unsigned)(cnt - 1) * d.H * 4 + 4;
+    const unsigned bytes = cnt > 0 ? (unsigned)(cnt - 1) * d.H * 4 + 4 : 0;
     const unsigned off = w == 0 ? (unsigned)l * d.H * 4 : kNoRow;
     R.pg = buf_load1(buf_rsrc((MIX_KEYS ? g.gates.dt_raw : g.log_decay) + th, bytes), off);
     const float* pb_src = BWD ? g.variance : MIX_KEYS ? g.gates.beta_raw : g.beta;
@@ -505,8 +534,9 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
     const int i = i0 + k * stride;
     const float* tb = smem + 2 * u * TILE;
     const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
-    for (int part = 0; part < parts; ++part) {
-      put_state((cross ? g.steps_c : g.steps_s) + state_index(i, part) * 4096 + elem);
+    held_i = i;
+    auto one_part = [&](int part, float2 (&held)[4]) {
+      state_now(held);
       const float dk = sb[u].decay[part];
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[j] *= dk;
@@ -515,7 +545,9 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
       // outside the part.
       const int lo = sb[u].lo[part], hi = lo < sb[u].hi[part] ? sb[u].hi[part] : 0;
       for (int k0 = lo & ~15; k0 < hi; k0 += 16) weighted_block(acc, ta, tb, sb[u].wt[part], k0, s, hf);
-    }
+    };
+    one_part(0, held0);
+    if (parts == 2) one_part(1, held1);
   };
   if constexpr (NBUF == 1 && BWD) {
     // One register set, loaded one step ahead (the backward walk's 16 fewer
@@ -525,20 +557,19 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
     fetch(R, i0);
     stage(R, 0, i0);
     __syncthreads();
-    if (steps > 1) fetch(R, i0 + stride);
+    fetch(R, i0 + stride);
     for (int k = 0; k < steps; ++k) {
       multiply(k, 0);
       __syncthreads();  // every wave is done with the buffer
-      if (k + 1 < steps) {
-        stage(R, 0, i0 + (k + 1) * stride);
-        if (k + 2 < steps) fetch(R, i0 + (k + 2) * stride);
-      }
+      if (k + 1 < steps) stage(R, 0, i0 + (k + 1) * stride);
+      store_held();
+      fetch(R, i0 + (k + 2) * stride);
       __syncthreads();
     }
   } else {
     StepRegs R0, R1;
     fetch(R0, i0);
-    if (steps > 1) fetch(R1, i0 + stride);
+    fetch(R1, i0 + stride);
     stage(R0, 0, i0);
     __syncthreads();
     // Step k multiplies LDS buffer k & 1 (NBUF = 2); `next` holds step k + 1
@@ -546,7 +577,7 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
     // k + 2.
     auto step = [&](int k, const StepRegs& next, StepRegs& spare) {
       const int i = i0 + k * stride, u = NBUF == 2 ? k & 1 : 0;
-      if (k + 2 < steps) fetch(spare, i + 2 * stride);
+      fetch(spare, i + 2 * stride);
       multiply(k, u);
       if constexpr (NBUF == 2) {
         if (k + 1 < steps) stage(next, u ^ 1, i + stride);
@@ -554,11 +585,25 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
         __syncthreads();  // every wave is done with the buffer
         if (k + 1 < steps) stage(next, 0, i + stride);
       }
+      store_held();
       __syncthreads();
     };
-    for (int k = 0; k < steps; k += 2) {
-      step(k, R1, R0);
-      if (k + 1 < steps) step(k + 1, R0, R1);
+    // Two steps per iteration (the register sets alternate).  The first
+    // iteration is peeled and an odd last step follows the loop, so the loop
+    // is entered with the loads and stores in flight that each iteration
+    // leaves and its body has no conditional loads: the compiler's count of
+    // what is in flight at each wait stays exact.
+    if (steps >= 2) {
+      step(0, R1, R0);
+      step(1, R0, R1);
+      int k = 2;
+      for (; k + 1 < steps; k += 2) {
+        step(k, R1, R0);
+        step(k + 1, R0, R1);
+      }
+      if (k < steps) step(k, R1, R0);
+    } else {
+      step(0, R1, R0);
     }
   }
   put_state((cross ? g.last_c : g.last_s) + edge * 4096 + elem);

@@ -70,10 +70,11 @@ def test_noalloc_backward_equals_backward_twice_in_a_row(gpu_lib, shapes):
 
 def test_noalloc_backward_takes_the_spill_free_state_walk(gpu_lib, monkeypatch):
     """More backward state walks than two per compute unit (B*H*(1+P/64) =
-    528 > 2 x 256) make m4mr_backward take the one-buffer walk, which spills
-    two registers to runtime-provided scratch; m4mr_backward_noalloc takes the
-    two-buffer walk instead, whatever M4MR_STATE_BUFFERS asks, and must still
-    equal m4mr_backward bit for bit (both walks give the same states)."""
+    528 > 2 x 256) make m4mr_backward take the one-buffer walk, held to 80
+    VGPRs, where the compiler may spill to runtime-provided scratch;
+    m4mr_backward_noalloc takes the two-buffer walk instead, whatever
+    M4MR_STATE_BUFFERS asks, and must still equal m4mr_backward bit for bit
+    (both walks give the same states)."""
     from mamba4_amd import memory
 
     batch, time, heads, width, chunk = 8, 64, 33, 64, 64
