@@ -37,15 +37,15 @@ __global__ void factored_solve_kernel(const float*, const float*, float*, long);
 __global__ void decode_step_kernel(float*, float*, const float*, const float*, const float*,
                                    const float*, const float*, const float*, long, int, int, float*,
                                    float*);
-template <typename In, bool MIX>
+template <typename In, bool MIX, int NV>
 __global__ void fwd_read_kernel(Dims, const In*, const In*, const In*, const float*,
                                 const float*, const float*, const float*, float*, float*, MixerIn,
                                 ReadGate);
-template <typename In, bool MIX, bool GATE>
+template <typename In, bool MIX, bool GATE, int NV>
 __global__ void bwd_dy_kernel(Dims, const In*, const In*, const In*, const float*,
                               const float*, const float*, const float*, const float*, float*,
                               MixerIn, MixerGrad);
-template <typename In, bool MIX, bool GATE>
+template <typename In, bool MIX, bool GATE, int NV>
 __global__ void bwd_grads_kernel(Dims, const In*, const In*, const float*, const float*,
                                  const float*, const float*, const float*, const float*,
                                  const float*, const float*, const float*, const float*, float*,
@@ -154,17 +154,21 @@ int configure() {
   } big[] = {{(const void*)m4::fwd_stats_kernel<float>, kStatsLdsBytes},
              {(const void*)m4::fwd_stats_kernel<m4::bf16_t>, kStatsLdsBytes},
              {(const void*)m4::bwd_local_kernel, kChunkLdsBytes},
-             {(const void*)m4::fwd_read_kernel<float, false>, kChunkLdsBytes},
-             {(const void*)m4::fwd_read_kernel<m4::bf16_t, false>, kChunkLdsBytes},
-             {(const void*)m4::fwd_read_kernel<float, true>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<float, false, false>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<m4::bf16_t, false, false>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<float, true, false>, kChunkLdsBytes},
-             {(const void*)m4::bwd_dy_kernel<float, true, true>, kChunkLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float, false, false>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false, false>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float, true, false>, kGradsLdsBytes},
-             {(const void*)m4::bwd_grads_kernel<float, true, true>, kGradsGateLdsBytes},
+#define M4_CHUNK_ATTRS(NV)                                                                    \
+  {(const void*)m4::fwd_read_kernel<float, false, NV>, kChunkLdsBytes},                       \
+      {(const void*)m4::fwd_read_kernel<m4::bf16_t, false, NV>, kChunkLdsBytes},              \
+      {(const void*)m4::fwd_read_kernel<float, true, NV>, kChunkLdsBytes},                    \
+      {(const void*)m4::bwd_dy_kernel<float, false, false, NV>, kChunkLdsBytes},              \
+      {(const void*)m4::bwd_dy_kernel<m4::bf16_t, false, false, NV>, kChunkLdsBytes},         \
+      {(const void*)m4::bwd_dy_kernel<float, true, false, NV>, kChunkLdsBytes},               \
+      {(const void*)m4::bwd_dy_kernel<float, true, true, NV>, kChunkLdsBytes},                \
+      {(const void*)m4::bwd_grads_kernel<float, false, false, NV>, kGradsLdsBytes},           \
+      {(const void*)m4::bwd_grads_kernel<m4::bf16_t, false, false, NV>, kGradsLdsBytes},      \
+      {(const void*)m4::bwd_grads_kernel<float, true, false, NV>, kGradsLdsBytes},            \
+      {(const void*)m4::bwd_grads_kernel<float, true, true, NV>, kGradsGateLdsBytes}
+             M4_CHUNK_ATTRS(1),
+             M4_CHUNK_ATTRS(2),
+#undef M4_CHUNK_ATTRS
              {(const void*)m4::states_kernel<false, float, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<false, m4::bf16_t, false, 2>, kStatesLdsBytes},
              {(const void*)m4::states_kernel<true, float, false, 2>,
@@ -413,7 +417,8 @@ int forward_impl(const char* entry, const In* keys, const In* values, const In* 
   });
   if (rc) return rc;
   return launch("fwd_read", st, [&] {
-    hipLaunchKernelGGL((m4::fwd_read_kernel<In, MIX>), dim3(persistent_grid(seqs, 2)), dim3(256),
+    const auto read = d.NV == 1 ? m4::fwd_read_kernel<In, MIX, 1> : m4::fwd_read_kernel<In, MIX, 2>;
+    hipLaunchKernelGGL(read, dim3(persistent_grid(seqs, 2)), dim3(256),
                        kChunkLdsBytes, st, d, keys, values, queries, beta, log_decay, solved,
                        start_cross, output, variance, mix, gate);
   });
@@ -491,7 +496,8 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   const unsigned seqs = (unsigned)B * H * d.NC;
   const long tokens = (long)B * T * H;
   int rc = launch("bwd_dy", st, [&] {
-    hipLaunchKernelGGL((m4::bwd_dy_kernel<In, MIX, GATE>), dim3(persistent_grid(seqs, 2)),
+    const auto dy = d.NV == 1 ? m4::bwd_dy_kernel<In, MIX, GATE, 1> : m4::bwd_dy_kernel<In, MIX, GATE, 2>;
+    hipLaunchKernelGGL(dy, dim3(persistent_grid(seqs, 2)),
                        dim3(256), kChunkLdsBytes, st, d, keys, values, queries, beta, log_decay,
                        start_cross, d_output, d_variance, ws.z, mix, mg);
   });
@@ -534,7 +540,9 @@ int backward_impl(const char* entry, const In* keys, const In* values, const In*
   }
   if (rc) return rc;
   rc = launch("bwd_grads", st, [&] {
-    hipLaunchKernelGGL((m4::bwd_grads_kernel<In, MIX, GATE>), dim3(persistent_grid(seqs, 1)),
+    const auto grads = d.NV == 1 ? m4::bwd_grads_kernel<In, MIX, GATE, 1>
+                                 : m4::bwd_grads_kernel<In, MIX, GATE, 2>;
+    hipLaunchKernelGGL(grads, dim3(persistent_grid(seqs, 1)),
                        dim3(512), GATE ? kGradsGateLdsBytes : kGradsLdsBytes, st, d, keys,
                        values, beta, log_decay, solved,
                        ws.z, d_output, d_variance, start_evidence, start_cross, ws.end_s,

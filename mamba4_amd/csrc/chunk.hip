@@ -84,7 +84,7 @@ __device__ __forceinline__ const float* cross_tile(const float* base, const Dims
 // transformed on load: the key rows shifted and normalised at staging, the
 // queries normalised where used), and the output is gated (`gate`), the
 // ungated read kept in gate.read.
-template <typename In, bool MIX>
+template <typename In, bool MIX, int NV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_read_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const In* __restrict__ queries, const float* __restrict__ beta,
@@ -92,6 +92,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float* __restrict__ start_c, float* __restrict__ output,
     float* __restrict__ variance, MixerIn mix, ReadGate gate) {
   extern __shared__ float smem[];
+  // Value tiles per row: compile-time for one (every branch on it folds,
+  // so the compiler can count the loads in flight at each wait), else read.
+  const int nv = NV == 1 ? 1 : d.NV;
   float* Y = smem;
   float* K = Y + TILE;  // keys, then values
   float* G = K + TILE;
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     fetch_keys(sn);
     // With more than one value tile, rc carries this chunk's later tiles and
     // prefetches after the last of them.
-    if (d.NV == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
+    if (nv == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
 
     // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
     // the 16 lanes that hold the rest of each row.
@@ -203,7 +206,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
         G[t * LDT + s] = v;
       }
-    for (int v = 0; v < d.NV; ++v) {
+#pragma unroll 1
+    for (int v = 0; v < nv; ++v) {
       if (v > 0) {
         // Value tile v and cross tile v replace tile v - 1 once every wave
         // has read it.
@@ -216,9 +220,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       rv.store(K);
       __syncthreads();
-      if (v == d.NV - 1) {
+      if (v == nv - 1) {
         fetch_tokens(rv, sn.len, value_rows(values, d, sn, 0));
-        if (d.NV > 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
+        if (nv > 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
       }
 
       f4 out[4], inh[4];
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // (-scale / (1 + var_t)) plus mg.d_var_in, written to mg.d_var; the
 // per-chunk sums of -(d_out . read) g (1 - g) log1p(var) and d_out . value
 // go to mg.dy_part (epilogue_backward_kernel's arithmetic).
-template <typename In, bool MIX, bool GATE>
+template <typename In, bool MIX, bool GATE, int NV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dy_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const In* __restrict__ queries, const float* __restrict__ beta,
@@ -276,6 +280,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float* __restrict__ ybar, MixerIn mix, MixerGrad mg) {
   static_assert(!GATE || MIX, "the gated backward reads the mixer's raw rows");
   extern __shared__ float smem[];
+  // Value tiles per row: compile-time for one (every branch on it folds,
+  // so the compiler can count the loads in flight at each wait), else read.
+  // (GATE: read, which keeps its registers within bounds.)
+  const int nv = NV == 1 && !GATE ? 1 : d.NV;
   float* DO = smem;
   float* V = DO + TILE;  // values, then keys
   float* G = V + TILE;
@@ -378,7 +386,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     zero4(inh);
     // GATE: d_out_t . read_t and d_out_t . value_t of this lane's rows.
     float dotr[4] = {0.f, 0.f, 0.f, 0.f}, dotv[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int v = 0; v < d.NV; ++v) {
+#pragma unroll 1
+    for (int v = 0; v < nv; ++v) {
       if (v > 0) {
         // Tile v replaces tile v - 1 once every wave has read it.
         fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
@@ -392,7 +401,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       // The last chunk of a block fetches its own inputs again (unused):
       // every chunk issues the same loads, so each wait counts exactly.
-      if (v == d.NV - 1) {
+      if (v == nv - 1) {
         fetch_tokens(rd, sn.len, value_rows(d_output, d, sn, 0));
         fetch_tokens(rv, sn.len, value_rows(values, d, sn, 0));
         rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
@@ -529,7 +538,7 @@ constexpr int MAX_NV = 2;
 // (key t's source row is raw key t - 1 with the shift, or the cached key),
 // the gates to beta_raw and dt_raw, and per-chunk partials of the per-head
 // gate-bias and a_log gradients to mg.grads_part.
-template <typename In, bool MIX, bool GATE>
+template <typename In, bool MIX, bool GATE, int NV>
 __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     Dims d, const In* __restrict__ keys, const In* __restrict__ values,
     const float* __restrict__ beta, const float* __restrict__ log_decay,
@@ -542,6 +551,9 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     float* __restrict__ floor_part, MixerIn mix, MixerGrad mg) {
   static_assert(!GATE || MIX, "the gated backward reads the mixer's raw rows");
   extern __shared__ float smem[];
+  // Value tiles per row: compile-time for one (every branch on it folds,
+  // so the compiler can count the loads in flight at each wait), else read.
+  const int nv = NV == 1 ? 1 : d.NV;
   float* Kt = smem;       // keys, then S0 (but for GATE)
   float* Vt = Kt + TILE;  // a value tile, then a C0 tile
   float* Yt = Vt + TILE;
@@ -613,7 +625,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     asm volatile("" : "+v"(tid));
     const int w8 = tid >> 6, ws = w8 < 4 ? w8 : 7 - w8, hf = w8 >> 2, l = tid & 63;
     const int r = l & 15, c4 = 4 * r;
-    const int kt = k_terms(si.len), last = d.NV - 1;
+    const int kt = k_terms(si.len), last = nv - 1;
     // Column blocks of this wave's half that hold some s <= t of its strip,
     // and the first t of its strip (the masked products vanish outside).
     const int causal_nj = min(2, max(0, ws - 2 * hf + 1)), t_begin = 16 * ws;
@@ -657,7 +669,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       tile_mma_half<false, true>(gy, Yt, Kt, 64, ws, hf, 0, causal_nj);
       tile_mma_half<false, true>(gz, Zt, Kt, 64, ws, hf, 0, causal_nj);
       tile_mma_half<false, true>(gv, Dt, Vt, 64, ws, hf, 0, causal_nj);
-      for (int v = 1; v < d.NV; ++v) {
+#pragma unroll 1
+      for (int v = 1; v < nv; ++v) {
         RowTile<In, GRADS_THREADS> rv;
         RowTile<float, GRADS_THREADS> rd;
         fetch_tokens(rv, si.len, value_rows(values, d, si, v));
@@ -730,7 +743,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
 #pragma unroll
     for (int v = MAX_NV - 1; v >= 0; --v) {
       zero2(dv[v]);
-      if (v < d.NV) {
+      if (v < nv) {
         if (v < last) {
           RowTile<float, GRADS_THREADS> rd;
           fetch_tokens(rd, si.len, value_rows(d_output, d, si, v));
@@ -787,7 +800,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       }
 #pragma unroll
       for (int v = MAX_NV - 1; v >= 0; --v) {
-        if (v < d.NV) {
+        if (v < nv) {
           if (v < last) {
             RowTile<In, GRADS_THREADS> rv;
             TileRegs2 rhv;
@@ -886,7 +899,8 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       zero2(dc);
       tile_mma_half<false, false>(ys, Yt, S0t, 64, ws, hf);  // y_t^T S0
       fetch_tokens(tv, sx.len, value_rows(values, d, sx, 0));
-      for (int v = 0; v < d.NV; ++v) {
+#pragma unroll 1
+      for (int v = 0; v < nv; ++v) {
         if (v > 0) {
           TileRegs2 rhv, rcv;
           RowTile<float, GRADS_THREADS> rd;
@@ -899,7 +913,7 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
           store_dout(rd);
           __syncthreads();
         }
-        if (d.NV == 1) {
+        if (nv == 1) {
 #pragma unroll
           for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -1056,35 +1070,34 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
   }
 }
 
-#define M4_CHUNK_KERNELS(In)                                                                  \
-  template __global__ void fwd_read_kernel<In, false>(                                         \
-      Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
-      const float*, float*, float*, MixerIn, ReadGate);                                        \
-  template __global__ void bwd_dy_kernel<In, false, false>(                                    \
+#define M4_CHUNK_KERNELS(In, MIX, GATE, NV)                                                   \
+  template __global__ void bwd_dy_kernel<In, MIX, GATE, NV>(                                   \
       Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
       const float*, const float*, float*, MixerIn, MixerGrad);                                 \
-  template __global__ void bwd_grads_kernel<In, false, false>(                                 \
+  template __global__ void bwd_grads_kernel<In, MIX, GATE, NV>(                                \
       Dims, const In*, const In*, const float*, const float*, const float*, const float*,      \
       const float*, const float*, const float*, const float*, const float*, const float*,      \
       float*, float*, float*, float*, float*, float*, MixerIn, MixerGrad);
-M4_CHUNK_KERNELS(float)
-M4_CHUNK_KERNELS(bf16_t)
+#define M4_READ_KERNEL(In, MIX, NV)                                                           \
+  template __global__ void fwd_read_kernel<In, MIX, NV>(                                       \
+      Dims, const In*, const In*, const In*, const float*, const float*, const float*,         \
+      const float*, float*, float*, MixerIn, ReadGate);
+M4_READ_KERNEL(float, false, 1)
+M4_READ_KERNEL(float, false, 2)
+M4_READ_KERNEL(bf16_t, false, 1)
+M4_READ_KERNEL(bf16_t, false, 2)
+M4_READ_KERNEL(float, true, 1)
+M4_READ_KERNEL(float, true, 2)
+M4_CHUNK_KERNELS(float, false, false, 1)
+M4_CHUNK_KERNELS(float, false, false, 2)
+M4_CHUNK_KERNELS(bf16_t, false, false, 1)
+M4_CHUNK_KERNELS(bf16_t, false, false, 2)
+M4_CHUNK_KERNELS(float, true, false, 1)
+M4_CHUNK_KERNELS(float, true, false, 2)
+M4_CHUNK_KERNELS(float, true, true, 1)
+M4_CHUNK_KERNELS(float, true, true, 2)
+#undef M4_READ_KERNEL
 #undef M4_CHUNK_KERNELS
-template __global__ void fwd_read_kernel<float, true>(Dims, const float*, const float*,
-                                                      const float*, const float*, const float*,
-                                                      const float*, const float*, float*, float*,
-                                                      MixerIn, ReadGate);
-#define M4_MIXER_KERNELS(GATE)                                                                \
-  template __global__ void bwd_dy_kernel<float, true, GATE>(                                   \
-      Dims, const float*, const float*, const float*, const float*, const float*,              \
-      const float*, const float*, const float*, float*, MixerIn, MixerGrad);                   \
-  template __global__ void bwd_grads_kernel<float, true, GATE>(                                \
-      Dims, const float*, const float*, const float*, const float*, const float*,              \
-      const float*, const float*, const float*, const float*, const float*, const float*,      \
-      const float*, float*, float*, float*, float*, float*, float*, MixerIn, MixerGrad);
-M4_MIXER_KERNELS(false)
-M4_MIXER_KERNELS(true)
-#undef M4_MIXER_KERNELS
 
 // d floor[h][4c4 .. 4c4+3] = sum over (b, n) of floor_part[(b*H + h)*NC + n]
 // in a fixed order: block (h, c4) of 256 threads, thread i sums entries
