@@ -103,7 +103,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float gate_s[MIX ? MAXC : 1];  // MIX: the chunk's read gates
   const long nseq = (long)d.B * d.H * d.NC;
   // The wave's 16-row strip (its causal products cost strip + 1 blocks).
-  const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
+  // Blocks in the grid's second half take the strips in reverse order: a
+  // CU's two blocks are normally one from each half, so each SIMD then holds
+  // strips k and 3 - k (k + 1 and 4 - k blocks of causal products) instead
+  // of two heavy or two light waves.
+  const int w = (threadIdx.x >> 6) ^ (blockIdx.x >= gridDim.x / 2 ? 3 : 0);
+  const int c4 = 4 * (lane_id() & 15);
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
   RowTile<float> ry;
@@ -291,8 +296,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ ChunkScalars cs;
   __shared__ float epart[GATE ? 4 : 1][2];  // GATE: per-wave gate-parameter partials
   const long nseq = (long)d.B * d.H * d.NC;
-  // The wave's 16-row strip (its causal products cost strip + 1 blocks).
-  const int w = threadIdx.x >> 6, c4 = 4 * (lane_id() & 15);
+  // The wave's 16-row strip (its causal products cost strip + 1 blocks),
+  // reversed in the grid's second half as in fwd_read_kernel.
+  const int w = (threadIdx.x >> 6) ^ (blockIdx.x >= gridDim.x / 2 ? 3 : 0);
+  const int c4 = 4 * (lane_id() & 15);
   long seq = blockIdx.x;
   SeqIndex si = seq_at(d, seq);
 
