@@ -74,11 +74,56 @@ __device__ __forceinline__ const float* cross_tile(const float* base, const Dims
   return base + (seq * d.NV + v) * 4096;
 }
 
+// G[t][s] = scores(t, s) x_t beta_s exp(P_t - P_s) for s <= t < len, zero
+// elsewhere, for strip W (acc: its scores in the tile_mma layout; x: row
+// factors, the read gates of the gated backward, when ROWS).  Blocks jb < W
+// lie below the diagonal, jb = W straddles it and blocks jb > W are zero:
+// one straight-line body per strip, with no exponentials for the zero
+// blocks and the mask a select rather than a branch per element.
+template <int W, bool ROWS>
+__device__ __forceinline__ void causal_weights_strip(const f4 acc[4], float* G,
+                                                     const ChunkScalars& cs, int len,
+                                                     const float* x) {
+  const int r = lane_id() & 15;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int t = acc_row(W, q);
+    const float pt = cs.prefix[t];
+    const bool in = t < len;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const int s = 16 * jb + r;  // acc_col<false>(jb)
+      float v = 0.f;
+      if (jb <= W) {
+        float a = acc[jb][q];
+        if constexpr (ROWS) a *= x[q];
+        const float e = a * cs.beta[s] * expf(pt - cs.prefix[s]);
+        v = in && (jb < W || s <= t) ? e : 0.f;
+      }
+      G[t * LDT + s] = v;
+    }
+  }
+}
+template <bool ROWS>
+__device__ __forceinline__ void causal_weights(const f4 acc[4], float* G, const ChunkScalars& cs,
+                                               int len, int w, const float* x = nullptr) {
+  switch (w) {
+    case 0: causal_weights_strip<0, ROWS>(acc, G, cs, len, x); break;
+    case 1: causal_weights_strip<1, ROWS>(acc, G, cs, len, x); break;
+    case 2: causal_weights_strip<2, ROWS>(acc, G, cs, len, x); break;
+    default: causal_weights_strip<3, ROWS>(acc, G, cs, len, x); break;
+  }
+}
+
 // Persistent: block i handles chunks i, i + gridDim.x, ...  The next chunk's
-// tiles load into registers while this chunk is computed: Y, K and C0 right
-// after this chunk's are in LDS, its queries once this chunk's variance is
-// done, its values once this chunk's values are in LDS (at most five tiles
-// in flight per thread, keeping two blocks per CU).
+// tiles load into registers while this chunk is computed: Y right after
+// this chunk's tiles are in LDS, its queries once this chunk's variance is
+// done, K and C0 once the scores are in LDS, its values once this chunk's
+// values are in LDS (at most five tiles in flight per thread, keeping two
+// blocks per CU).  Every wave of the CU reaches each of these points at
+// about the same time, so the loads go out in four smaller bursts rather
+// than one: a wave issuing into a full memory pipeline stalls until it
+// drains, and the later bursts drain under the products.
 //
 // MIX: keys and queries come from the mixer's raw projections (`mix`,
 // transformed on load: the key rows shifted and normalised at staging, the
@@ -170,10 +215,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!more) sn.len = 0;
     fetch_tokens(ry, sn.len, rows_of(solved, d, sn));
     fetch_scalars(sn);
-    fetch_keys(sn);
-    // With more than one value tile, rc carries this chunk's later tiles and
-    // prefetches after the last of them.
-    if (nv == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
 
     // variance_t = q_t . y_t: this thread's four tile-fetch rows, summed over
     // the 16 lanes that hold the rest of each row.
@@ -201,16 +242,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f4 acc[4];
     zero4(acc);
     tile_mma_causal<false>(acc, Y, K, w);  // scores y_t . k_s, s <= t
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int t = acc_row(w, q), s = acc_col<false>(jb);
-        float v = 0.f;
-        if (s <= t && t < si.len)
-          v = acc[jb][q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
-        G[t * LDT + s] = v;
-      }
+    causal_weights<false>(acc, G, cs, si.len, w);
+    fetch_keys(sn);
+    // With more than one value tile, rc carries this chunk's later tiles and
+    // prefetches after the last of them.
+    if (nv == 1) rc.fetch_matrix(cross_tile(start_c, d, sn.seq, 0), more);
 #pragma unroll 1
     for (int v = 0; v < nv; ++v) {
       if (v > 0) {
@@ -459,16 +495,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         epart[threadIdx.x >> 6][1] = pskip;
       }
     }
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int t = acc_row(w, q), s = acc_col<false>(jb);
-        float v = 0.f;
-        if (s <= t && t < si.len)
-          v = acc[jb][q] * gate[q] * cs.beta[s] * expf(cs.prefix[t] - cs.prefix[s]);
-        G[t * LDT + s] = v;
-      }
+    causal_weights<GATE>(acc, G, cs, si.len, w, gate);
     __syncthreads();
     if constexpr (GATE)
       // The chunk's gate-parameter partials, the four waves' in order.
