@@ -720,25 +720,28 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       // phase 2 reads them as row-major A operands.
       float rsum[4] = {0.f, 0.f, 0.f, 0.f};
       float csum[2] = {0.f, 0.f};
+      // Column block jb lies below the strip's diagonal (jb < ws), on it
+      // (jb = ws) or above it (jb > ws: all zero, no exponentials); the mask
+      // is a select, not a branch per element.
+      const int wsu = __builtin_amdgcn_readfirstlane(ws), hfu = __builtin_amdgcn_readfirstlane(hf);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int s = 16 * (2 * hf + j) + r;
-        f4 m1v, m2v;
+        const int jb = 2 * hfu + j, s = 16 * jb + r;
+        f4 m1v = {0.f, 0.f, 0.f, 0.f}, m2v = {0.f, 0.f, 0.f, 0.f};
+        if (jb <= wsu) {
+          const float ps = cs.prefix[s], bs = cs.beta[s];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int t = acc_row(ws, q);
-          float my = 0.f, mz = 0.f, d2 = 0.f;
-          if (s <= t && t < si.len) {
-            const float dec = expf(cs.prefix[t] - cs.prefix[s]);
+          for (int q = 0; q < 4; ++q) {
+            const int t = acc_row(ws, q);
+            const bool keep = t < si.len && (jb < wsu || s <= t);
+            const float dec = expf(cs.prefix[t] - ps);
             const float mix = gv[j][q] - gz[j][q];
-            d2 = dec * gy[j][q] * mix;
-            my = dec * cs.beta[s] * gy[j][q];
-            mz = dec * cs.beta[s] * mix;
+            const float d2 = keep ? dec * gy[j][q] * mix : 0.f;
+            m1v[q] = keep ? dec * bs * gy[j][q] : 0.f;
+            m2v[q] = keep ? dec * bs * mix : 0.f;
+            rsum[q] += bs * d2;
+            csum[j] += d2;
           }
-          m1v[q] = my;
-          m2v[q] = mz;
-          rsum[q] += cs.beta[s] * d2;
-          csum[j] += d2;
         }
         *reinterpret_cast<f4*>(M1 + s * LDT + acc_row(ws, 0)) = m1v;
         *reinterpret_cast<f4*>(M2 + s * LDT + acc_row(ws, 0)) = m2v;
@@ -792,9 +795,9 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
 
     float2 dkq[4];  // GATE: this thread's d keys until M1 is free
     // Phase 3: chunk-end terms through the end-state cotangents G, H:
-    // (G + G^T) k_s as two products (G read k-major, then transposed).  H and
-    // the values go tile by tile from the last, leaving the first tile of
-    // each in LDS.
+    // (G + G^T) k_s as one product (the evidence walk stores G + G^T, which
+    // is symmetric).  H and the values go tile by tile from the last, leaving
+    // the first tile of each in LDS.
     rg.store(M1);
     rh.store(M2);
     // The start states of phase 4 load while phase 3 runs, then the first of
@@ -822,10 +825,11 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
       zero2(gk);
       zero2(hv);
       if (hf == 0) fetch_tokens(tz, sx.len, rows_of(z, d, sx));
-      tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);       // G^T k_s
-      if (hf == 1) fetch_phase4();
-      tile_mma_half<false, true, true>(gk, Kt, M1, 64, ws, hf);  // + G k_s
-      if (hf == 1) fetch_tokens(tz, sx.len, rows_of(z, d, sx));
+      tile_mma_half<false, false>(gk, Kt, M1, 64, ws, hf);  // (G + G^T) k_s
+      if (hf == 1) {
+        fetch_phase4();
+        fetch_tokens(tz, sx.len, rows_of(z, d, sx));
+      }
       float qpart[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -923,11 +927,13 @@ __global__ __launch_bounds__(GRADS_THREADS) void bwd_grads_kernel(
     rc.store(Vt);
     __syncthreads();
     {
+      // <G, S0> = <G + G^T, S0> / 2 (S0 symmetric).
       float part = 0.f;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) part += rg.v[j][i] * rs.v[j][i];
+      part *= 0.5f;
       f4 ys[2], dc[2];
       zero2(ys);
       zero2(dc);

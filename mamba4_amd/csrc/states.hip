@@ -18,6 +18,10 @@
 // V = dOut^T diag(e^P) Y; bwd_scan_kernel walks chunks in reverse,
 //   end[n] = running;  running = U_n + exp(sum of log decays in n) running,
 // leaving each chunk's end-state cotangent and the initial-state gradient.
+// The evidence end-state cotangents G are stored as G + G^T: every use the
+// chunk gradients make of G is through its symmetric part ((G + G^T) k,
+// k^T G k, <G, S> with S symmetric), and a symmetric G + G^T takes one
+// product where G itself takes two.
 #include "common.hpp"
 
 namespace m4 {
@@ -199,7 +203,7 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
     const int i = acc_row(w, q);
     f4 v;
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) v[jb] = -0.5f * (acc[jb][q] + M[(c4 + jb) * LDT + i]);
+    for (int jb = 0; jb < 4; ++jb) v[jb] = -(acc[jb][q] + M[(c4 + jb) * LDT + i]);
     *reinterpret_cast<f4*>(us + i * 64 + c4) = v;
   }
   for (int v = 0; v < d.NV; ++v) {
@@ -236,8 +240,24 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
   float* buf = (cross ? end_c : end_s) + (long)bh * d.NC * size;
   const float* fin = cross ? d_final_c : d_final_s;
   __shared__ float decay[256];
-  f4 running = f4{0.f, 0.f, 0.f, 0.f};
-  if (fin) running = *reinterpret_cast<const f4*>(fin + (long)bh * size + elem);
+  // Evidence: the scan carries G + G^T (it starts from D + D^T and adds the
+  // local terms 2U = -(M + M^T), as bwd_local_kernel stores them), so every
+  // stored end-state cotangent is symmetric; the initial-state gradient is
+  // the full one, half the carried sum plus the decayed antisymmetric part
+  // of D.  Cross states carry their cotangent as is.
+  f4 running = f4{0.f, 0.f, 0.f, 0.f}, anti = f4{0.f, 0.f, 0.f, 0.f};
+  float total = 1.f;  // the product of every chunk's decay
+  if (fin) {
+    running = *reinterpret_cast<const f4*>(fin + (long)bh * size + elem);
+    if (!cross) {
+      const int i = elem >> 6, j = elem & 63;
+      f4 tr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tr[e] = fin[(long)bh * size + (j + e) * 64 + i];
+      anti = 0.5f * (running - tr);
+      running += tr;
+    }
+  }
   for (int top = d.NC; top > 0; top -= 256) {
     const int count = min(256, top);
     __syncthreads();
@@ -255,10 +275,12 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(
         if (j < m) {
           *reinterpret_cast<f4*>(buf + (long)(top - count + i0 - j) * size + elem) = running;
           running = local[j] + decay[i0 - j] * running;
+          total *= decay[i0 - j];
         }
     }
   }
   float* dinit = cross ? d_init_c : d_init_s;
+  if (!cross) running = 0.5f * running + total * anti;
   *reinterpret_cast<f4*>(dinit + (long)bh * size + elem) = running;
 }
 
@@ -385,24 +407,35 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   // The backward evidence walk adds M + M^T per step (M = Z^T W Y), so its
   // state is S = D + A + A^T with A the decayed sum of the M alone (one
   // product per step instead of two) and D the decayed final-state cotangent
-  // (which need not be symmetric): acc holds A, dfin and dscale hold D, and
-  // A^T comes back through an LDS tile when a state is stored.  Both step
-  // buffer counts do this, so a batch's rows give the same bits whichever
-  // variant the batch size selects.  The symmetric store needs about 100
-  // VGPRs in the two-buffer walk; the one-buffer walk is held to 80 for three
-  // blocks per CU.
+  // (which need not be symmetric): acc holds A, dscale the decay of D, and
+  // A^T comes back through an LDS tile when a state is stored.  The chunk
+  // end states are stored as S + S^T = dscale (D + D^T) + 2 (A + A^T), which
+  // is all the chunk gradients use of them (exactly symmetric: each element
+  // and its mirror add the same two terms), so dfin holds D + D^T; the
+  // initial-state gradient is the full S, with D read again at the end.
+  // Both step buffer counts do this, so a batch's rows give the same bits
+  // whichever variant the batch size selects.  The symmetric store needs
+  // about 100 VGPRs in the two-buffer walk; the one-buffer walk is held to
+  // 80 for three blocks per CU.
   const bool sym = BWD && !cross;
+  const int r0 = 16 * s + 4 * (l >> 4), c0 = 4 * (l & 15) + 2 * hf;  // elem's row and column
   f4 dfin[2];
   float dscale = 1.f;
   dfin[0] = acc[0];
   dfin[1] = acc[1];
-  if (sym) zero2(acc);
+  const float* const d_final = sym && g.first_s ? g.first_s + edge * 4096 : nullptr;
+  if (sym) {
+    zero2(acc);
+    if (d_final)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) dfin[j] += *reinterpret_cast<const f4*>(d_final + (c0 + j) * 64 + r0);
+  }
   float* const tr = smem + 2 * NBUF * TILE;  // the transpose tile (backward only)
-  // The state this lane holds (rows 16 s + 4 (l / 16) + q, columns
-  // 4 (l % 16) + 2 hf + j), for dst (+ 64 q + j).
-  auto state_now = [&](float2 (&out)[4]) {
+  // The state this lane holds (rows r0 + q, columns c0 + j), for dst
+  // (+ 64 q + j); the backward evidence's chunk end states as S + S^T, its
+  // last (the initial-state gradient, `last`) as S.
+  auto state_now = [&](float2 (&out)[4], bool last) {
     if (sym) {
-      const int r0 = 16 * s + 4 * (l >> 4), c0 = 4 * (l & 15) + 2 * hf;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<float2*>(tr + (r0 + q) * LDT + c0) = float2{acc[0][q], acc[1][q]};
@@ -410,10 +443,26 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
       f4 t[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) t[j] = *reinterpret_cast<const f4*>(tr + (c0 + j) * LDT + r0);
+      if (last) {
+        f4 dd[2];
+        zero2(dd);
+        if (d_final)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        out[q] = float2{dscale * dfin[0][q] + acc[0][q] + t[0][q],
-                        dscale * dfin[1][q] + acc[1][q] + t[1][q]};
+          for (int q = 0; q < 4; ++q) {
+            const float2 x = *reinterpret_cast<const float2*>(d_final + elem + 64 * q);
+            dd[0][q] = x.x;
+            dd[1][q] = x.y;
+          }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          out[q] = float2{dscale * dd[0][q] + acc[0][q] + t[0][q],
+                          dscale * dd[1][q] + acc[1][q] + t[1][q]};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          out[q] = float2{dscale * dfin[0][q] + 2.f * (acc[0][q] + t[0][q]),
+                          dscale * dfin[1][q] + 2.f * (acc[1][q] + t[1][q])};
+      }
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) out[q] = float2{acc[0][q], acc[1][q]};
@@ -425,7 +474,7 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
   };
   auto put_state = [&](float* dst) {
     float2 v[4];
-    state_now(v);
+    state_now(v, true);
     store_state(v, dst);
   };
   // A step's start states (one per part), taken before its products and
@@ -536,7 +585,7 @@ __attribute__((amdgpu_waves_per_eu(NBUF == 1 && BWD ? 6 : 1))) void states_kerne
     const float* ta = own_a ? smem + (2 * u + 1) * TILE : tb;
     held_i = i;
     auto one_part = [&](int part, float2 (&held)[4]) {
-      state_now(held);
+      state_now(held, false);
       const float dk = sb[u].decay[part];
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[j] *= dk;
