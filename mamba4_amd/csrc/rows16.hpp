@@ -119,10 +119,10 @@ constexpr std::integer_sequence<int, (Off + I)...> offset_sequence(std::integer_
 // (g, j) holds in A[I][16K + 4mu + e] element (16I + j, 16K + 4g + e) of
 // matrix mu.  exchange_block converts one 16x16 block of all four matrices
 // between the two (it is its own inverse).  Exchanged is the accumulator
-// layout of v_mfma_f32_16x16x1_4b_f32 for four blocks whose rows are block
-// columns, and rows is that instruction's operand layout (panel_block), so
-// the trailing updates read the panel in rows and accumulate in exchanged;
-// only a trailing block column that becomes the next panel is exchanged.
+// layout of the four-block 16x16 MFMA shapes for four blocks whose rows are
+// block columns, and rows is their operand layout (panel_update), so the
+// trailing updates read the panel in rows and accumulate in exchanged; only
+// a trailing block column that becomes the next panel is exchanged.
 
 // One elimination step of column J inside its 16-column panel P = J/16,
 // with the forward substitution of the right-hand side r folded in: the
@@ -141,6 +141,11 @@ __device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)
   const float rs = __builtin_amdgcn_rsqf(piv);
 #pragma unroll
   for (int m = mj; m < 4; ++m) A[m][J] = -A[m][J] * rs;
+  // The sub-diagonal values are materialised here: the compiler would
+  // otherwise fold the reciprocal pivot into their f16 split (panel_update)
+  // and keep the panel's sixteen pivots live up to it.
+#pragma unroll
+  for (int m = mj + 1; m < 4; ++m) asm volatile("" : "+v"(A[m][J]));
   float nwj = -r[mj] * rs;  // -w_J in lane J%16: r_J is final once column J is reached
   // GFX9 needs two wait states between a VALU write of a VGPR and a DPP read
   // of it, and the compiler's hazard tracking does not see inside inline asm.
@@ -196,30 +201,6 @@ __device__ __forceinline__ void exchange_block(float (&row)[64]) {
 
 typedef float f16 __attribute__((ext_vector_type(16)));
 
-// Trailing block (I, K) after panel P: A_IK += L_IP L_KP^T for all four
-// matrices (the working matrix is negated), the block in the exchanged
-// layout, the panel's L blocks in the rows layout.  v_mfma_f32_16x16x1_4b_f32
-// takes its A and B operands as four 16-lane rows, one per block b (lane
-// 16b + i holds A_b[i], lane 16b + j holds B_b[j]), which is the rows layout
-// of column c of a slot, and leaves D_b[i][j] += A_b[i] B_b[j] in lane
-// j + 16(i/4), register 4b + i%4 (both checked on gfx950 with an in-bounds
-// probe).  With A = column 16P + c of slot K and B = the same column of slot
-// I, D_mu[i][j] is element (16I + j, 16K + i) of matrix mu: register
-// A[I][16K + 4mu + e] of lane (g, j) with i = 4g + e, the exchanged layout.
-// Sixteen such rank-one products, one per panel column, make the update, and
-// the panel's blocks need no exchange.
-template <int P, int I, int K>
-__device__ __forceinline__ void panel_block(float (&A)[4][64]) {
-  f16 acc;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = A[I][16 * K + r];
-#pragma unroll
-  for (int c = 0; c < 16; ++c)
-    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(A[K][16 * P + c], A[I][16 * P + c], acc, 0, 0, 0);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) A[I][16 * K + r] = acc[r];
-}
-
 // Slots I > P of block column C, exchanged in place.
 template <int P, int C>
 __device__ __forceinline__ void exchange_below(float (&A)[4][64]) {
@@ -228,24 +209,90 @@ __device__ __forceinline__ void exchange_below(float (&A)[4][64]) {
   if constexpr (P < 3) exchange_block<16 * C>(A[3]);
 }
 
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// x = hi + lo + O(2^-22 |x|): hi = f16(x) (round to nearest), lo = f16(x -
+// hi) with x - hi formed exactly by v_fma_mix (x * 1 - hi, the f16 source
+// selected by op_sel).  Products of f16 values are exact in the MFMA's fp32
+// sums.  Three instructions per pair of values; the closing s_nop gives the
+// MFMA that reads the pieces the two wait states a VALU write needs before
+// an MFMA operand read (the compiler does not see inside the asm).
+__device__ __forceinline__ void split_f16(const float* x, h4& hi, h4& lo) {
+  unsigned h01, h23, l01, l23;
+  asm volatile(
+      "v_cvt_pk_f16_f32 %0, %4, %5\n\t"
+      "v_cvt_pk_f16_f32 %1, %6, %7\n\t"
+      "v_fma_mixlo_f16 %2, %4, 1.0, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %2, %5, 1.0, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixlo_f16 %3, %6, 1.0, -%1 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %3, %7, 1.0, -%1 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "s_nop 1"
+      : "=&v"(h01), "=&v"(h23), "=&v"(l01), "=&v"(l23)
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+  hi = __builtin_bit_cast(h4, (uint2{h01, h23}));
+  lo = __builtin_bit_cast(h4, (uint2{l01, l23}));
+}
+
+// One MFMA of trailing block (I, K): A_IK += a b^T for all four matrices (the
+// working matrix is negated), a from slot K and b from slot I (rows layout),
+// the block in the exchanged layout.  v_mfma_f32_16x16x4_4b_f16 takes
+// A_b[i][0..3] from lane 16b + i and B_b[j][0..3] from lane 16b + j and leaves
+// D_b[i][j] += sum_k A_b[i][k] B_b[j][k] in lane j + 16(i/4), register
+// 4b + i%4 (checked on gfx950 with an in-bounds probe), so D_mu[i][j] is
+// element (16I + j, 16K + i) of matrix mu: register A[I][16K + 4mu + e] of
+// lane (g, j) with i = 4g + e, the exchanged layout.
+template <int P, int I, int K>
+__device__ __forceinline__ void block_term(float (&A)[4][64], const h4& a, const h4& b) {
+  f16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = A[I][16 * K + r];
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f16(a, b, acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) A[I][16 * K + r] = acc[r];
+}
+
 // Rank-16 update of the trailing blocks after panel P, then the next panel's
-// block column back to the rows layout (its blocks are updated first).
+// block column back to the rows layout.  Four panel columns per MFMA: each
+// fp32 panel value is split into f16 hi + lo and the product L_K L_I^T is
+// formed as hi hi^T + hi lo^T + lo hi^T (the dropped lo lo^T is below 2^-22
+// of it), three instructions per four columns, 12 per block instead of the 16
+// rank-one v_mfma_f32_16x16x1_4b_f32 of an fp32 update.  Both shapes issue in
+// 32 cycles, but the f16 one runs beside the other wave's VALU work while the
+// fp32 one holds the SIMD (measured on gfx950: an FMA wave sharing a SIMD with
+// an MFMA wave ran 1.14x its time alone beside the f16 shape, 2.9x beside the
+// fp32 one).
 template <int P>
 __device__ __forceinline__ void panel_update(float (&A)[4][64]) {
   if constexpr (P < 3) {
-    if constexpr (P == 0) {
-      panel_block<0, 1, 1>(A);
-      panel_block<0, 2, 1>(A);
-      panel_block<0, 3, 1>(A);
-      panel_block<0, 2, 2>(A);
-      panel_block<0, 3, 2>(A);
-      panel_block<0, 3, 3>(A);
-    } else if constexpr (P == 1) {
-      panel_block<1, 2, 2>(A);
-      panel_block<1, 3, 2>(A);
-      panel_block<1, 3, 3>(A);
-    } else {
-      panel_block<2, 3, 3>(A);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // One column group's pieces live at a time (12 registers at P = 0).
+      __builtin_amdgcn_sched_barrier(0);
+      h4 hi[4], lo[4];
+#pragma unroll
+      for (int m = P + 1; m < 4; ++m) split_f16(&A[m][16 * P + 4 * g], hi[m], lo[m]);
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const auto term = [&](auto Ic, auto Kc) {
+          constexpr int I = decltype(Ic)::value, K = decltype(Kc)::value;
+          block_term<P, I, K>(A, t == 2 ? lo[K] : hi[K], t == 1 ? lo[I] : hi[I]);
+        };
+        using std::integral_constant;
+        if constexpr (P == 0) {
+          term(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+          term(integral_constant<int, 2>{}, integral_constant<int, 1>{});
+          term(integral_constant<int, 3>{}, integral_constant<int, 1>{});
+          term(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+          term(integral_constant<int, 3>{}, integral_constant<int, 2>{});
+          term(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+        } else if constexpr (P == 1) {
+          term(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+          term(integral_constant<int, 3>{}, integral_constant<int, 2>{});
+          term(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+        } else {
+          term(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+        }
+      }
     }
     exchange_below<P, P + 1>(A);
   }
