@@ -281,7 +281,7 @@ __global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
     else
       load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
     float nw[4], y[4];
-    factor_exchanged(A, fl, cur.q, nw);
+    factor_exchanged<true>(A, fl, cur.q, nw);
     backward_rows16(A, nw, y);
     float* const sol = valid ? solved + cur.th * 64 : g_discard + ROWS_FACTOR;
 #pragma unroll
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(64) void spd_solve_kernel(const float* __restrict__
     const int i = a + 16 * m;
     r[m] = i < dim ? rhs[n * dim + i] : 0.f;
   }
-  factor_rows16(A, zero, r, nw);
+  factor_rows16<false>(A, zero, r, nw);
   backward_rows16(A, nw, y);
   if (active) {
 #pragma unroll
@@ -529,7 +529,7 @@ decode_step_kernel(float* __restrict__ evidence, float* __restrict__ cross,
     __syncthreads();
   }
   float nw[4], y[4];
-  factor_exchanged(A, fl, qr, nw);
+  factor_exchanged<false>(A, fl, qr, nw);
   backward_rows16(A, nw, y);
 #pragma unroll
   for (int m = 0; m < 4; ++m) qr[m] = query[nidx * 64 + a + 16 * m];

@@ -251,8 +251,46 @@ __device__ __forceinline__ void block_term(float (&A)[4][64], const h4& a, const
   for (int r = 0; r < 16; ++r) A[I][16 * K + r] = acc[r];
 }
 
+// Trailing block (I, K) after panel P in fp32: A_IK += L_IP L_KP^T as sixteen
+// chained rank-one v_mfma_f32_16x16x1_4b_f32, one per panel column, with the
+// operand and accumulator layouts of block_term (lane 16b + i holds A_b[i],
+// D_b[i][j] += A_b[i] B_b[j] in lane j + 16(i/4), register 4b + i%4).
+template <int P, int I, int K>
+__device__ __forceinline__ void block_f32(float (&A)[4][64]) {
+  f16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = A[I][16 * K + r];
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(A[K][16 * P + c], A[I][16 * P + c], acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) A[I][16 * K + r] = acc[r];
+}
+
+// Calls f(I, K) (as integral constants) for every trailing block of panel P.
+template <int P, typename F>
+__device__ __forceinline__ void for_trailing_blocks(F&& f) {
+  using std::integral_constant;
+  if constexpr (P == 0) {
+    f(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+    f(integral_constant<int, 2>{}, integral_constant<int, 1>{});
+    f(integral_constant<int, 3>{}, integral_constant<int, 1>{});
+    f(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+    f(integral_constant<int, 3>{}, integral_constant<int, 2>{});
+    f(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+  } else if constexpr (P == 1) {
+    f(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+    f(integral_constant<int, 3>{}, integral_constant<int, 2>{});
+    f(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+  } else if constexpr (P == 2) {
+    f(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+  }
+}
+
 // Rank-16 update of the trailing blocks after panel P, then the next panel's
-// block column back to the rows layout.  Four panel columns per MFMA: each
+// block column back to the rows layout.
+//
+// F16 (the memory read's factorization): four panel columns per MFMA: each
 // fp32 panel value is split into f16 hi + lo and the product L_K L_I^T is
 // formed as hi hi^T + hi lo^T + lo hi^T (the dropped lo lo^T is below 2^-22
 // of it), three instructions per four columns, 12 per block instead of the 16
@@ -260,49 +298,44 @@ __device__ __forceinline__ void block_term(float (&A)[4][64], const h4& a, const
 // 32 cycles, but the f16 one runs beside the other wave's VALU work while the
 // fp32 one holds the SIMD (measured on gfx950: an FMA wave sharing a SIMD with
 // an MFMA wave ran 1.14x its time alone beside the f16 shape, 2.9x beside the
-// fp32 one).
-template <int P>
+// fp32 one).  The pieces bound the panel values to |l| < 65504 (evidence
+// diagonals below 4.29e9), and below 2^-3 the lo piece is subnormal, so a
+// value carries an absolute error up to 2^-25 rather than 2^-22 of itself.
+//
+// !F16 (generic SPD solves and the decode step): the fp32 rank-one updates,
+// exact to fp32 for every finite matrix.
+template <int P, bool F16>
 __device__ __forceinline__ void panel_update(float (&A)[4][64]) {
   if constexpr (P < 3) {
+    if constexpr (F16) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      // One column group's pieces live at a time (12 registers at P = 0).
-      __builtin_amdgcn_sched_barrier(0);
-      h4 hi[4], lo[4];
+      for (int g = 0; g < 4; ++g) {
+        // One column group's pieces live at a time (12 registers at P = 0).
+        __builtin_amdgcn_sched_barrier(0);
+        h4 hi[4], lo[4];
 #pragma unroll
-      for (int m = P + 1; m < 4; ++m) split_f16(&A[m][16 * P + 4 * g], hi[m], lo[m]);
+        for (int m = P + 1; m < 4; ++m) split_f16(&A[m][16 * P + 4 * g], hi[m], lo[m]);
 #pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        const auto term = [&](auto Ic, auto Kc) {
-          constexpr int I = decltype(Ic)::value, K = decltype(Kc)::value;
-          block_term<P, I, K>(A, t == 2 ? lo[K] : hi[K], t == 1 ? lo[I] : hi[I]);
-        };
-        using std::integral_constant;
-        if constexpr (P == 0) {
-          term(integral_constant<int, 1>{}, integral_constant<int, 1>{});
-          term(integral_constant<int, 2>{}, integral_constant<int, 1>{});
-          term(integral_constant<int, 3>{}, integral_constant<int, 1>{});
-          term(integral_constant<int, 2>{}, integral_constant<int, 2>{});
-          term(integral_constant<int, 3>{}, integral_constant<int, 2>{});
-          term(integral_constant<int, 3>{}, integral_constant<int, 3>{});
-        } else if constexpr (P == 1) {
-          term(integral_constant<int, 2>{}, integral_constant<int, 2>{});
-          term(integral_constant<int, 3>{}, integral_constant<int, 2>{});
-          term(integral_constant<int, 3>{}, integral_constant<int, 3>{});
-        } else {
-          term(integral_constant<int, 3>{}, integral_constant<int, 3>{});
-        }
+        for (int t = 0; t < 3; ++t)
+          for_trailing_blocks<P>([&](auto Ic, auto Kc) {
+            constexpr int I = decltype(Ic)::value, K = decltype(Kc)::value;
+            block_term<P, I, K>(A, t == 2 ? lo[K] : hi[K], t == 1 ? lo[I] : hi[I]);
+          });
       }
+    } else {
+      for_trailing_blocks<P>([&](auto Ic, auto Kc) {
+        block_f32<P, decltype(Ic)::value, decltype(Kc)::value>(A);
+      });
     }
     exchange_below<P, P + 1>(A);
   }
 }
 
-template <int P>
+template <int P, bool F16>
 __device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl)[4],
                                              float (&r)[4], float (&nw)[4], int a) {
   factor_steps(A, fl, r, nw, a, offset_sequence<16 * P>(std::make_integer_sequence<int, 16>{}));
-  panel_update<P>(A);
+  panel_update<P, F16>(A);
 }
 
 // Blocked right-looking Cholesky of E + diag(floor) with the forward
@@ -313,16 +346,18 @@ __device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl
 // panel's rank-16 update on MFMA (panel_update).  On return A holds L below
 // the diagonal, 1/L_ii on it and zeros above (rows layout), r is consumed
 // and nw = -L^-1 r.  All steps are expanded at compile time so every
-// register index is static.
+// register index is static.  F16 selects the trailing-update form
+// (panel_update).
+template <bool F16>
 __device__ __forceinline__ void factor_exchanged(float (&A)[4][64], const float (&fl)[4],
                                                  float (&r)[4], float (&nw)[4]) {
   const int a = threadIdx.x & 15;
 #pragma unroll
   for (int m = 0; m < 4; ++m) nw[m] = 0.f;
-  factor_panel<0>(A, fl, r, nw, a);
-  factor_panel<1>(A, fl, r, nw, a);
-  factor_panel<2>(A, fl, r, nw, a);
-  factor_panel<3>(A, fl, r, nw, a);
+  factor_panel<0, F16>(A, fl, r, nw, a);
+  factor_panel<1, F16>(A, fl, r, nw, a);
+  factor_panel<2, F16>(A, fl, r, nw, a);
+  factor_panel<3, F16>(A, fl, r, nw, a);
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -330,6 +365,7 @@ __device__ __forceinline__ void factor_exchanged(float (&A)[4][64], const float 
 }
 
 // The same from a rows-layout -E: the six trailing blocks are exchanged first.
+template <bool F16>
 __device__ __forceinline__ void factor_rows16(float (&A)[4][64], const float (&fl)[4],
                                               float (&r)[4], float (&nw)[4]) {
   exchange_block<16>(A[1]);
@@ -338,7 +374,7 @@ __device__ __forceinline__ void factor_rows16(float (&A)[4][64], const float (&f
   exchange_block<16>(A[3]);
   exchange_block<32>(A[3]);
   exchange_block<48>(A[3]);
-  factor_exchanged(A, fl, r, nw);
+  factor_exchanged<F16>(A, fl, r, nw);
 }
 
 // y = L^-T w from nw = -w (factor_rows16 / factor_exchanged).
