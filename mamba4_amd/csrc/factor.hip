@@ -185,6 +185,23 @@ __global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
   // columns 12..15 of sequence 0, above the diagonal.  No turn writes that
   // quad; the factorization reads it as scratch and zeroes it.
   lds_int* const turn_count = (lds_int*)(&evidence[slot_quad(0, 3) * 64]);
+  // A row whose head's largest floor lies outside [2^-8, 2^8) factors c E,
+  // c = 2^2s with c max(floor) in [0.5, 2), and brings the factor back to L
+  // (exact power-of-two scalings; factor_exchanged).  The trailing updates
+  // carry the panel values as f16 pieces, whose lo piece turns subnormal
+  // below 2^-3 and whose hi piece overflows above 65504: scaled so, every
+  // row's largest pivot is at least about 0.7 and the pieces' absolute error
+  // stays under fp32's own rounding of c E, whatever the inputs' scale, and
+  // a piece overflows only for evidence above 4.29e9 / c.  Other rows (the
+  // models' floors) factor E as it is.
+  float fl[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) fl[m] = floor[h * 64 + a + 16 * m];
+  const int fexp = __builtin_amdgcn_frexp_expf(max16(fmaxf(fmaxf(fl[0], fl[1]), fmaxf(fl[2], fl[3]))));
+  const int sexp = fexp >= -7 && fexp <= 8 ? 0 : min(max((1 - fexp) >> 1, -60), 60);
+  const float c = __builtin_ldexpf(1.f, 2 * sexp);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) fl[m] *= c;
   {
     // Both waves of the pair stage the start evidence: wave 0 slots 0..2 (24 quads),
     // wave 1 slot 3 (16 quads).
@@ -195,18 +212,15 @@ __global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
 #pragma unroll
         for (int q = 0; q < 4 * m + 4; ++q)
           evidence[slot_quad(m, q) * 64 + lane] =
-              -*reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
+              -c * *reinterpret_cast<const f4*>(s0 + (a + 16 * m) * 64 + 4 * q);
       if (lane == 0) *turn_count = 0;  // after this lane's quad (0, 3): LDS writes stay in order
     } else {
 #pragma unroll
       for (int q = 0; q < 16; ++q)
         evidence[slot_quad(3, q) * 64 + lane] =
-            -*reinterpret_cast<const f4*>(s0 + (a + 48) * 64 + 4 * q);
+            -c * *reinterpret_cast<const f4*>(s0 + (a + 48) * 64 + 4 * q);
     }
   }
-  float fl[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) fl[m] = floor[h * 64 + a + 16 * m];
   // Rows past their sequence read token 0 (in bounds; never stored).
   auto token = [&](int tt) { return tt < len ? t0 + tt : 0; };
   TokenInputs cur;
@@ -235,9 +249,10 @@ __global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
     const bool gave_up = seen < tt || (polls < 0 && tt > 0);
     if (gave_up && lane == 0) raise_count(turn_count, kPoisoned);
     const float lam = gave_up || seen >= kPoisoned ? __builtin_nanf("") : expf(cur.log_lam);
+    const float cbeta = __builtin_ldexpf(cur.beta, 2 * sexp);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const float nbk = -cur.beta * cur.k[m];
+      const float nbk = -cbeta * cur.k[m];
 #pragma unroll
       for (int q = 0; q < 4 * m + 4; ++q) {
         f4 sv = evidence[slot_quad(m, q) * 64 + lane];
@@ -281,7 +296,7 @@ __global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
     else
       load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
     float nw[4], y[4];
-    factor_exchanged<true>(A, fl, cur.q, nw);
+    factor_exchanged<true>(A, fl, cur.q, nw, sexp);
     backward_rows16(A, nw, y);
     float* const sol = valid ? solved + cur.th * 64 : g_discard + ROWS_FACTOR;
 #pragma unroll

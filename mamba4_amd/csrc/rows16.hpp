@@ -75,6 +75,15 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// Maximum over the 16 lanes of the row; every lane receives it.
+__device__ __forceinline__ float max16(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  return x;
+}
+
 // acc += src[lane L of the row] * mul as one v_fmac_f32_dpp (row_newbcast:L).
 // The caller guarantees src was not written by the previous two VALU
 // instructions (see factor_step).
@@ -130,7 +139,8 @@ constexpr std::integer_sequence<int, (Off + I)...> offset_sequence(std::integer_
 // -A_iJ / sqrt(pivot), every later column of the panel takes l_iJ l_KJ by one
 // DPP-fed FMA per slot, and r_i takes -l_iJ w_J with w_J = r_J / l_JJ.  The
 // step records -w_J in nw (lane J%16 of slot J/16) and 1/l_JJ on the
-// diagonal.  Columns right of the panel are updated by panel_update.
+// diagonal.
+// Columns right of the panel are updated by panel_update.
 template <int J>
 __device__ __forceinline__ void factor_step(float (&A)[4][64], const float (&fl)[4],
                                             float (&r)[4], float (&nw)[4], int a) {
@@ -348,9 +358,15 @@ __device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl
 // and nw = -L^-1 r.  All steps are expanded at compile time so every
 // register index is static.  F16 selects the trailing-update form
 // (panel_update).
+//
+// Scaled form (sexp = s != 0): the caller passes -c E, c = 2^2s, and
+// c diag(floor) in fl; the factorization runs on c E, whose factor is 2^s L,
+// and on return A and nw are brought back to L and -L^-1 r (every value
+// times 2^-s, the diagonal's reciprocal pivots times 2^s).  Power-of-two
+// scalings (v_ldexp_f32) are exact.
 template <bool F16>
 __device__ __forceinline__ void factor_exchanged(float (&A)[4][64], const float (&fl)[4],
-                                                 float (&r)[4], float (&nw)[4]) {
+                                                 float (&r)[4], float (&nw)[4], int sexp = 0) {
   const int a = threadIdx.x & 15;
 #pragma unroll
   for (int m = 0; m < 4; ++m) nw[m] = 0.f;
@@ -362,6 +378,21 @@ __device__ __forceinline__ void factor_exchanged(float (&A)[4][64], const float 
   for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int c = 1; c < 16; ++c) A[m][16 * m + c] = c > a ? 0.f : A[m][16 * m + c];
+  // Skipped when no row of the wave is scaled (a wave-uniform branch; folded
+  // away when sexp is the literal 0).
+  if (__builtin_amdgcn_ballot_w64(sexp != 0)) {
+    // Opaque here, so the diagonal's exponents are not hoisted out of the
+    // caller's loop into sixteen live registers.
+    int se = sexp;
+    asm volatile("" : "+v"(se));
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      nw[m] = __builtin_ldexpf(nw[m], se);  // -L^-1 r = 2^s (-(2^s L)^-1 r)
+#pragma unroll
+      for (int k = 0; k < slot_cols(m); ++k)
+        A[m][k] = __builtin_ldexpf(A[m][k], k == 16 * m + a ? se : -se);
+    }
+  }
 }
 
 // The same from a rows-layout -E: the six trailing blocks are exchanged first.

@@ -282,6 +282,33 @@ def test_ragged_lengths_and_empty_sub_chunks(gpu_lib, time, chunk):
         assert normwise(got[key], ref) <= 1e-5, (key, time, chunk)
 
 
+@pytest.mark.parametrize("scale", [1e-3, 1e-2, 1.0, 1e2])
+def test_outputs_and_gradients_hold_at_every_input_scale(gpu_lib, scale):
+    """Keys scaled by s and the floor by s^2 scale every evidence matrix by
+    s^2: the same problem at another magnitude.  The factorization's trailing
+    updates carry panel values as f16 pieces, so a row whose floor lies
+    outside [2^-8, 2^8) is factored at a power-of-two scale (s^2 = 1e-6:
+    panel values near 1e-3 would otherwise sit in f16's subnormal range, and
+    s^2 = 1e4 tests the other side); the tolerances are the configs' own."""
+    from mamba4_amd.inputs import synthetic_inputs
+
+    data = synthetic_inputs(2, 160, 2, seed=31, floor_value=1e-2, cotangents=True)
+    data["keys"] = (data["keys"] * scale).astype(np.float32)
+    data["floor"] = (data["floor"] * scale * scale).astype(np.float32)
+    d_out, d_var = data["d_output"], data["d_variance"]
+    zeros_s = np.zeros((2, 2, 64, 64), np.float32)
+    zeros_c = np.zeros((2, 2, 64, 64), np.float32)
+    announce(f"input scale {scale:g}: B2 T160 H2 D64, floor 1e-2 x {scale * scale:g}")
+    got = run_gpu(data, chunk=64, cotangents=(d_out, d_var, zeros_s, zeros_c))
+    args = [data[n].astype(np.float64) for n in NAMES]
+    (out, var, s_end, c_end), res = oracle.forward(*args, chunk=64)
+    for key, ref in zip(["output", "variance", "evidence", "cross"], (out, var, s_end, c_end)):
+        assert normwise(got[key], ref) <= 1e-4, (key, normwise(got[key], ref))
+    want = oracle.backward(res, d_out.astype(np.float64), d_var.astype(np.float64))
+    for n in NAMES:
+        assert normwise(got["d_" + n], want[n]) <= 1e-3, (n, normwise(got["d_" + n], want[n]))
+
+
 @pytest.mark.parametrize("value_dim,chunk", [(128, 64), (100, 16), (128, 5)])
 def test_wide_value_heads_forward_and_gradients(gpu_lib, value_dim, chunk):
     """P = 128 value heads, the reference's trained memory_head_dim
