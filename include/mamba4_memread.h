@@ -95,6 +95,14 @@ const char* m4mr_last_error(void);
  * through a bounded wait (M4MR_TURN_POLLS polls, default 65536, about 2 ms);
  * a wait that gives up never yields a plausible wrong answer: every later
  * solution and factor of that block's sequences is NaN.
+ * Numerics: the per-token Cholesky runs in fp32 except its trailing block
+ * updates, whose fp32 panel values enter f16 MFMA products as hi + lo
+ * pieces (three products per pair, exact in the fp32 sums, the dropped
+ * lo*lo term below 2^-22 of each product).  A head whose largest floor lies
+ * outside [2^-8, 2^8) is factored at a power-of-two scale that puts that
+ * floor near 1 (exact), so the accuracy does not depend on the inputs'
+ * magnitude; the f16 pieces overflow (NaN results) only for evidence above
+ * 4.29e9 times the head's largest floor (rounded to a power of four).
  */
 int m4mr_forward(const float* keys, const float* values, const float* queries,
                  const float* beta, const float* log_decay, const float* floor,
