@@ -397,6 +397,30 @@ int m4mr_spd_solve_backward(const float* factors, const float* solution,
                             float* d_precision, float* d_rhs, void* stream);
 
 /*
+ * Spectral and finiteness probes of a memory state: replaces
+ * selective_diagnostics (lm/kernels/mamba4.py:358-376), which the mixer
+ * calls on its final state when the "diagnostics" collection is mutable
+ * (lm/models/mamba4.py:290-310).
+ *
+ * inputs   evidence [B,H,D,D], cross [B,H,P,D], floor [H,D] (1 <= D <= 64).
+ * outputs  per_state [B,H,4]: for each (b, h) the smallest and largest
+ *          eigenvalue of the symmetrised precision (E + E^T)/2 + diag(floor)
+ *          (NaN when it has a non-finite entry), 1 if every entry of the
+ *          state is finite else 0, and max |cross| (NaN if a cross entry is
+ *          NaN);
+ *          summary [7]: precision_min_eigenvalue, precision_max_eigenvalue,
+ *          precision_max_condition (max over states of max / max(min,
+ *          1e-30)), state_all_finite (1 / 0), cross_max_abs, floor_min,
+ *          floor_max, in the reference's order.
+ * The eigenvalues come from a cyclic Jacobi iteration in fp32, one wave per
+ * state (absolute error about 1e-7 of the largest eigenvalue); the
+ * reference's eigvalsh (LAPACK on the host, or its TPU lowering) has no
+ * counterpart to call on the device.
+ */
+int m4mr_diagnostics(const float* evidence, const float* cross, const float* floor, int B, int H,
+                     int D, int P, float* per_state, float* summary, void* stream);
+
+/*
  * Mixer prologue: the memory read's inputs from the caller's projections.
  * Replaces the preprocessing inside SelectiveMemoryMixer.__call__
  * (lm/models/mamba4.py:183-237): with key_shift, position t of `keys` is

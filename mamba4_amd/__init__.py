@@ -2,8 +2,8 @@
 
 A drop-in for the reference's lm/kernels memory-read API
 (``selective_gaussian_memory``, ``selective_decode``,
-``selective_initial_state``, ``spd_solve``, ``SelectiveState``,
-``SelectiveResult``),
+``selective_initial_state``, ``spd_solve``, ``selective_diagnostics``,
+``SelectiveState``, ``SelectiveResult``),
 implemented by hand-written HIP kernels behind the C ABI in
 ``include/mamba4_memread.h``, plus the caller's preprocessing and read gating
 (``memory_inputs``, ``gated_read``; lm/models/mamba4.py:183-237, 266-273)
@@ -18,6 +18,7 @@ from mamba4_amd.memory import (  # noqa: F401
     SelectiveState,
     selective_decode,
     selective_decode_,
+    selective_diagnostics,
     selective_gaussian_memory,
     selective_initial_state,
     spd_solve,
@@ -47,6 +48,7 @@ __all__ = [
     "order_memory_chunked",
     "selective_decode",
     "selective_decode_",
+    "selective_diagnostics",
     "selective_gaussian_memory",
     "selective_initial_state",
     "spd_solve",

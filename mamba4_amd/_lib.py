@@ -81,6 +81,7 @@ SIGNATURES = {
     "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _I, _P, _P, _P]),
     "m4mr_spd_solve": (_I, [_P, _P, _L, _I, _P, _P, _P]),
     "m4mr_spd_solve_backward": (_I, [_P, _P, _P, _L, _I, _P, _P, _P]),
+    "m4mr_diagnostics": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
     "m4mr_prologue_forward": (_I, [_P] * 9 + [_I] * 4 + [ctypes.c_float] * 2 + [_I] + [_P] * 7),
     "m4mr_mixer_workspace_bytes": (_S, [_I] * 3),
     "m4mr_prologue_backward": (

@@ -4,6 +4,7 @@
 // fixed sequence of kernels on the caller's stream.  Nothing here allocates
 // device memory or synchronises; the only global state is the optional
 // profiling log (mutex-protected) and a per-thread error message.
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -80,6 +81,8 @@ __global__ void order_bwd_apply_kernel(OrderDims, const float*, const float*, co
 __global__ void spd_solve_kernel(const float*, const float*, long, int, float*, float*);
 __global__ void spd_backward_kernel(const float*, const float*, const float*, long, int, float*,
                                     float*);
+__global__ void diag_eigen_kernel(const float*, const float*, const float*, int, int, int, float*);
+__global__ void diag_summary_kernel(const float*, int, const float*, int, float*);
 }  // namespace m4
 
 namespace {
@@ -99,7 +102,7 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "order_bwd_carry", "order_bwd_apply",
                                     "m3_walk",        "m3_out",    "m3_walk_bwd", "m3_grad",
                                     "m3_finish",      "m3_bias",   "m3_suffix",
-                                    "mixer_finish"};
+                                    "mixer_finish",   "diag_eigen", "diag_summary"};
 
 struct ProfRecord {
   const char* name;
@@ -953,6 +956,26 @@ int m4mr_spd_solve_backward(const float* factors, const float* solution,
   return launch("spd_backward", st, [&] {
     hipLaunchKernelGGL(m4::spd_backward_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
                        factors, solution, d_solution, N, dim, d_precision, d_rhs);
+  });
+}
+
+int m4mr_diagnostics(const float* evidence, const float* cross, const float* floor, int B, int H,
+                     int D, int P, float* per_state, float* summary, void* stream) {
+  g_error.clear();
+  if (B < 1 || H < 1 || D < 1 || D > M4MR_KEY_DIM || P < 1 || (long)B * H > INT_MAX / 4 ||
+      (long)H * D > INT_MAX)
+    return fail(M4MR_EINVAL, "m4mr_diagnostics: need B, H, P >= 1 and 1 <= D <= 64");
+  if (!evidence || !cross || !floor || !per_state || !summary)
+    return fail(M4MR_EINVAL, "m4mr_diagnostics: a required pointer is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = launch("diag_eigen", st, [&] {
+    hipLaunchKernelGGL(m4::diag_eigen_kernel, dim3((unsigned)(B * H)), dim3(64), 0, st, evidence,
+                       cross, floor, H, D, P, per_state);
+  });
+  if (rc) return rc;
+  return launch("diag_summary", st, [&] {
+    hipLaunchKernelGGL(m4::diag_summary_kernel, dim3(1), dim3(256), 0, st, per_state, B * H,
+                       floor, H * D, summary);
   });
 }
 

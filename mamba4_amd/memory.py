@@ -439,3 +439,63 @@ def selective_decode_(state, key, value, query, beta, log_decay, floor, solver=N
             )
         )
     return SelectiveResult(output, variance, state)
+
+
+DIAGNOSTIC_KEYS = (
+    "precision_min_eigenvalue",
+    "precision_max_eigenvalue",
+    "precision_max_condition",
+    "state_all_finite",
+    "cross_max_abs",
+    "floor_min",
+    "floor_max",
+)
+
+
+def selective_diagnostics(state, floor):
+    """Spectral and finiteness probes of the final selective precision
+    (lm/kernels/mamba4.py:358-376): the extreme eigenvalues of the
+    symmetrised evidence + diag(floor) over every state, the largest
+    condition number, whether the state is finite, the largest cross
+    magnitude and the floor's range, as 0-dim tensors under the reference's
+    keys (``state_all_finite`` a bool tensor).
+
+    ``state.evidence`` [..., D, D] (D <= 64) and ``state.cross`` [..., P, D]
+    on the GPU; ``floor`` broadcasts to [..., D].  The eigenvalues come from
+    a Jacobi iteration on the device (m4mr_diagnostics).
+    """
+    lib = _lib.load()
+    evidence, cross = state.evidence, state.cross
+    _require_device(evidence, cross)
+    dim = evidence.shape[-1]
+    if evidence.shape[-2] != dim or cross.shape[-1] != dim:
+        raise ValueError("evidence must be [..., D, D] and cross [..., P, D]")
+    if dim > _lib.KEY_DIM:
+        raise ValueError(f"selective_diagnostics supports widths <= {_lib.KEY_DIM}; got {dim}")
+    lead = tuple(evidence.shape[:-2])
+    if tuple(cross.shape[:-2]) != lead:
+        raise ValueError("evidence and cross must share their leading dimensions")
+    count = 1
+    for n in lead:
+        count *= n
+    device = evidence.device
+    f32 = dict(dtype=torch.float32, device=device)
+    value_dim = cross.shape[-2]
+    evidence = evidence.to(**f32).reshape(count, dim, dim).contiguous()
+    cross = cross.to(**f32).reshape(count, value_dim, dim).contiguous()
+    floor = torch.as_tensor(floor).to(**f32)
+    # Every state carries its own floor row (the kernel's "head" index runs
+    # over the states); the range of the broadcast floor is the floor's own.
+    per_floor = torch.broadcast_to(floor, lead + (dim,)).reshape(count, dim).contiguous()
+    per_state = torch.empty((count, 4), **f32)
+    summary = torch.empty((7,), **f32)
+    with torch.cuda.device(device):
+        _lib.check(
+            lib.m4mr_diagnostics(
+                _ptr(evidence), _ptr(cross), _ptr(per_floor), 1, count, dim, value_dim,
+                _ptr(per_state), _ptr(summary), _stream(),
+            )
+        )
+    out = {k: summary[i] for i, k in enumerate(DIAGNOSTIC_KEYS)}
+    out["state_all_finite"] = summary[3] > 0.5
+    return out

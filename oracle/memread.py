@@ -30,6 +30,8 @@ Functions:
   substitutions with reciprocal pivots (lm/kernels/mamba4_fused.py:45-113).
 * ``spd_solve`` / ``spd_solve_backward`` -- the batched SPD solve and its
   VJP (lm/kernels/mamba4.py:164-215).
+* ``diagnostics`` -- spectral and finiteness probes of a state
+  (lm/kernels/mamba4.py:358-376).
 
 ``PINNED`` names, for every function, the tests that pin it against the
 reference's known answers, invariants, an independent float64 autodiff and
@@ -71,6 +73,10 @@ PINNED = {
     "spd_solve_backward": [
         "tests/test_oracle.py::test_spd_solve_backward_matches_float64_autograd",
         "tests/test_oracle.py::test_planted_spd_backward_mistakes_are_caught",
+    ],
+    "diagnostics": [
+        "tests/test_oracle.py::test_diagnostics_on_known_spectra",
+        "tests/test_oracle.py::test_diagnostics_symmetrise_and_flag_non_finite_states",
     ],
 }
 
@@ -468,3 +474,49 @@ def decode_step(evidence, cross, key, value, query, beta, log_decay, floor, dtyp
     output = np.einsum("...pd,...d->...p", cross, solved)
     variance = np.sum(query * solved, axis=-1)
     return output, variance, evidence, cross
+
+
+DIAGNOSTIC_KEYS = (
+    "precision_min_eigenvalue",
+    "precision_max_eigenvalue",
+    "precision_max_condition",
+    "state_all_finite",
+    "cross_max_abs",
+    "floor_min",
+    "floor_max",
+)
+
+
+def diagnostics(evidence, cross, floor):
+    """Spectral and finiteness probes of a state (float64).
+
+    Restates selective_diagnostics (lm/kernels/mamba4.py:358-376): the
+    eigenvalues of the symmetrised precision (P + P^T)/2, P = evidence +
+    diag(floor), their extremes over every state, the largest ratio of a
+    state's largest to its smallest (floored at 1e-30), whether evidence and
+    cross are finite, the largest cross magnitude and the floor's range.
+    Shapes: evidence [...,D,D], cross [...,P,D], floor broadcastable to
+    [...,D].  A state with a non-finite precision entry has NaN eigenvalues
+    (the device kernel's convention; LAPACK gives NaN or fails there).
+    """
+    evidence = np.asarray(evidence, np.float64)
+    cross = np.asarray(cross, np.float64)
+    floor = np.asarray(floor, np.float64)
+    dim = evidence.shape[-1]
+    precision = evidence + np.broadcast_to(floor, evidence.shape[:-1])[..., :, None] * np.eye(dim)
+    sym = (precision + np.swapaxes(precision, -1, -2)) * 0.5
+    flat = sym.reshape(-1, dim, dim)
+    eig = np.full((flat.shape[0], dim), np.nan)
+    ok = np.isfinite(flat).all(axis=(-1, -2))
+    if ok.any():
+        eig[ok] = np.linalg.eigvalsh(flat[ok])
+    minimum, maximum = eig[:, 0], eig[:, -1]
+    return {
+        "precision_min_eigenvalue": np.min(minimum),
+        "precision_max_eigenvalue": np.max(maximum),
+        "precision_max_condition": np.max(maximum / np.maximum(minimum, 1e-30)),
+        "state_all_finite": bool(np.all(np.isfinite(evidence)) and np.all(np.isfinite(cross))),
+        "cross_max_abs": np.max(np.abs(cross)),
+        "floor_min": np.min(floor),
+        "floor_max": np.max(floor),
+    }

@@ -410,3 +410,72 @@ def test_every_pinning_test_named_by_the_oracle_exists():
             path, test = name.split("::")
             text = open(os.path.join(root, path)).read()
             assert f"def {test}(" in text, name
+
+
+def _known_spectrum_state(rng, batch, heads, dim, value_dim):
+    """States whose precision evidence + diag(floor) has known eigenvalues:
+    Q diag(mu) Q^T minus the floor's diagonal, Q a random orthogonal matrix."""
+    mu = np.exp(rng.uniform(np.log(1e-3), np.log(50.0), size=(batch, heads, dim)))
+    q, _ = np.linalg.qr(rng.normal(size=(batch, heads, dim, dim)))
+    precision = np.einsum("bhij,bhj,bhkj->bhik", q, mu, q)
+    floor = rng.uniform(0.01, 0.5, size=(heads, dim))
+    evidence = precision - floor[None, :, :, None] * np.eye(dim)
+    cross = rng.normal(size=(batch, heads, value_dim, dim))
+    return mu, evidence, cross, floor
+
+
+def test_diagnostics_on_known_spectra():
+    # lm/kernels/mamba4.py:358-376 on states with planted eigenvalues, cross
+    # entries and floors: every statistic has a closed-form answer.
+    rng = np.random.default_rng(40)
+    for dim in (1, 5, 64):
+        mu, evidence, cross, floor = _known_spectrum_state(rng, 2, 3, dim, 4)
+        cross[1, 2, 3, 0] = -9.5  # the largest magnitude, planted
+        got = oracle.diagnostics(evidence, cross, floor)
+        assert set(got) == set(oracle.DIAGNOSTIC_KEYS)
+        np.testing.assert_allclose(got["precision_min_eigenvalue"], mu.min(), rtol=1e-9)
+        np.testing.assert_allclose(got["precision_max_eigenvalue"], mu.max(), rtol=1e-9)
+        cond = (mu.max(axis=-1) / mu.min(axis=-1)).max()
+        np.testing.assert_allclose(got["precision_max_condition"], cond, rtol=1e-8)
+        assert got["state_all_finite"] is True
+        assert got["cross_max_abs"] == max(9.5, np.abs(cross).max())
+        assert got["floor_min"] == floor.min() and got["floor_max"] == floor.max()
+    # A floor shared by every head ([D]) broadcasts like the reference's.
+    mu, evidence, cross, floor = _known_spectrum_state(rng, 1, 2, 3, 2)
+    shared = np.array([0.1, 0.2, 0.3])
+    evidence = evidence + (floor - shared)[None, :, :, None] * np.eye(3)
+    got = oracle.diagnostics(evidence, cross, shared)
+    np.testing.assert_allclose(got["precision_min_eigenvalue"], mu.min(), rtol=1e-9)
+    assert got["floor_min"] == 0.1 and got["floor_max"] == 0.3
+
+
+def test_diagnostics_symmetrise_and_flag_non_finite_states():
+    rng = np.random.default_rng(41)
+    mu, evidence, cross, floor = _known_spectrum_state(rng, 2, 2, 6, 3)
+    skew = rng.normal(size=evidence.shape)
+    skew = skew - np.swapaxes(skew, -1, -2)
+    # An antisymmetric part leaves the symmetrised precision unchanged.
+    got = oracle.diagnostics(evidence + skew, cross, floor)
+    np.testing.assert_allclose(got["precision_min_eigenvalue"], mu.min(), rtol=1e-9)
+    np.testing.assert_allclose(got["precision_max_eigenvalue"], mu.max(), rtol=1e-9)
+    # A NaN cross entry: not finite, and the maximum magnitude is NaN.
+    bad = cross.copy()
+    bad[0, 1, 2, 3] = np.nan
+    got = oracle.diagnostics(evidence, bad, floor)
+    assert got["state_all_finite"] is False and np.isnan(got["cross_max_abs"])
+    assert np.isfinite(got["precision_min_eigenvalue"])
+    # An infinite evidence entry: not finite, NaN eigenvalue extremes.
+    bad = evidence.copy()
+    bad[1, 0, 0, 0] = np.inf
+    got = oracle.diagnostics(bad, cross, floor)
+    assert got["state_all_finite"] is False
+    assert np.isnan(got["precision_min_eigenvalue"]) and np.isnan(got["precision_max_eigenvalue"])
+    assert np.isfinite(got["cross_max_abs"])
+    # A non-positive-definite precision: the condition uses the 1e-30 floor.
+    neg = evidence.copy()
+    shift = mu[0, 0].min() + 1e-3
+    neg[0, 0] -= shift * np.eye(6)
+    got = oracle.diagnostics(neg, cross, floor)
+    np.testing.assert_allclose(got["precision_min_eigenvalue"], -1e-3, rtol=1e-6)
+    want = (mu[0, 0].max() - shift) / 1e-30
+    assert got["precision_max_condition"] == pytest.approx(want, rel=1e-6)
