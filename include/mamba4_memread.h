@@ -47,6 +47,8 @@ extern "C" {
  * convention, lm/kernels/mamba4_fused.py:113).  The layout is private to the
  * residuals, as the reference's packing is (lm/kernels/mamba4_fused.py:36-42). */
 #define M4MR_FACTOR_FLOATS 2176
+/* Widest system m4mr_spd_solve takes (one block per system above 64). */
+#define M4MR_SPD_MAX_DIM 4096
 
 #define M4MR_OK 0
 #define M4MR_EINVAL 1
@@ -374,17 +376,30 @@ int m4mr_decode_step(float* evidence, float* cross,
 
 /*
  * Batched SPD solve: precision_n y_n = rhs_n for N systems of width dim
- * (1 <= dim <= 64).  precision [N,dim,dim] row-major, of which only the
- * lower triangle (column <= row) is read; rhs and solution [N,dim].  When
- * `factors` is non-NULL it receives each system's factor
- * [N, M4MR_FACTOR_FLOATS] (the system padded to 64 with an identity block),
- * the residual m4mr_spd_solve_backward consumes.
+ * (1 <= dim <= M4MR_SPD_MAX_DIM).  precision [N,dim,dim] row-major, of
+ * which only the lower triangle (column <= row) is read; rhs and solution
+ * [N,dim].  When `factors` is non-NULL it receives each system's factor
+ * [N, m4mr_spd_factor_floats(dim)], the residual m4mr_spd_solve_backward
+ * consumes: for dim <= 64 the quad-run layout of M4MR_FACTOR_FLOATS (the
+ * system padded to 64 with an identity block), above 64 the dense
+ * [dim][dim] row-major factor (L below the diagonal, 1/L_ii on it, zero
+ * above).  Above width 128 the factorization runs in `factors`, which is
+ * then required; N < 2^31 above width 64.
  * Replaces spd_solve and its forward rule (lm/kernels/mamba4.py:190-201,
- * _factor_and_solve :164-187); every reference backend ("loop",
- * "blocked", "unrolled", "auto", "fused") solves the same system.
+ * _factor_and_solve :164-187, which take any width); every reference
+ * backend ("loop", "blocked", "unrolled", "auto", "fused") solves the same
+ * system.
  */
 int m4mr_spd_solve(const float* precision, const float* rhs, long N, int dim,
                    float* solution, float* factors, void* stream);
+
+/*
+ * Floats of one system's stored factor for m4mr_spd_solve at width dim:
+ * M4MR_FACTOR_FLOATS up to 64, dim * dim above; 0 outside
+ * 1..M4MR_SPD_MAX_DIM.  No counterpart in the reference, whose residual is
+ * the JAX array itself (lm/kernels/mamba4.py:201).
+ */
+long m4mr_spd_factor_floats(int dim);
 
 /*
  * VJP of m4mr_spd_solve (lm/kernels/mamba4.py:204-215): with

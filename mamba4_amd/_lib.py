@@ -17,6 +17,7 @@ EINVAL = 1
 EHIP = 2
 FACTOR_FLOATS = 2176
 KEY_DIM = 64
+SPD_MAX_DIM = 4096
 VALUE_DIM = 64
 MAX_VALUE_DIM = 128
 MAX_CHUNK = 64
@@ -81,6 +82,7 @@ SIGNATURES = {
     "m4mr_decode_step": (_I, [_P] * 8 + [_L, _I, _I, _P, _P, _P]),
     "m4mr_spd_solve": (_I, [_P, _P, _L, _I, _P, _P, _P]),
     "m4mr_spd_solve_backward": (_I, [_P, _P, _P, _L, _I, _P, _P, _P]),
+    "m4mr_spd_factor_floats": (_L, [_I]),
     "m4mr_diagnostics": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
     "m4mr_prologue_forward": (_I, [_P] * 9 + [_I] * 4 + [ctypes.c_float] * 2 + [_I] + [_P] * 7),
     "m4mr_mixer_workspace_bytes": (_S, [_I] * 3),

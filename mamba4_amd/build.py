@@ -19,7 +19,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIBRARY = os.path.join(HERE, "libmamba4_memread.so")
 SOURCES = ["api.hip", "states.hip", "factor.hip", "chunk.hip", "mixer.hip", "order.hip",
-           "scan3.hip", "diag.hip"]
+           "scan3.hip", "diag.hip", "spd_wide.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -81,6 +81,11 @@ __global__ void order_bwd_apply_kernel(OrderDims, const float*, const float*, co
 __global__ void spd_solve_kernel(const float*, const float*, long, int, float*, float*);
 __global__ void spd_backward_kernel(const float*, const float*, const float*, long, int, float*,
                                     float*);
+template <bool LDS>
+__global__ void spd_wide_kernel(const float*, const float*, int, float*, float*);
+template <bool LDS>
+__global__ void spd_wide_backward_kernel(const float*, const float*, const float*, int, float*,
+                                         float*);
 __global__ void diag_eigen_kernel(const float*, const float*, const float*, int, int, int, float*);
 __global__ void diag_summary_kernel(const float*, int, const float*, int, float*);
 }  // namespace m4
@@ -102,7 +107,8 @@ const char* const kKernelNames[] = {"fwd_stats",      "fwd_scan",  "fwd_states",
                                     "order_bwd_carry", "order_bwd_apply",
                                     "m3_walk",        "m3_out",    "m3_walk_bwd", "m3_grad",
                                     "m3_finish",      "m3_bias",   "m3_suffix",
-                                    "mixer_finish",   "diag_eigen", "diag_summary"};
+                                    "mixer_finish",   "diag_eigen", "diag_summary",
+                                    "spd_wide",       "spd_wide_backward"};
 
 struct ProfRecord {
   const char* name;
@@ -136,6 +142,12 @@ constexpr size_t kGradsGateLdsBytes = 8 * m4::TILE * sizeof(float);  // + the S0
 constexpr size_t kStatesLdsBytes = 4 * m4::TILE * sizeof(float);
 // The backward walks add one tile (the evidence state's transpose).
 constexpr size_t kStatesBwdExtra = m4::TILE * sizeof(float);
+// The widest LDS request of the wide SPD solves (an LDS-resident 128-wide
+// system, or the vectors of a 4096-wide one).
+constexpr size_t kWideLdsMax =
+    sizeof(float) * (m4::wide_lds_floats(m4::kWideLdsDim) > m4::wide_lds_floats(m4::kWideMaxDim)
+                         ? m4::wide_lds_floats(m4::kWideLdsDim)
+                         : m4::wide_lds_floats(m4::kWideMaxDim));
 
 bool configured = false;
 int g_cus = 256;  // compute units of the device (set by configure())
@@ -195,7 +207,11 @@ int configure() {
              {(const void*)m3::walk_kernel<true, m3::bf16_t, false>, m3::kWalkLds},
              {(const void*)m3::out_kernel<m3::bf16_t, false>, m3::kOutLdsBf16},
              {(const void*)m3::grad_kernel<m3::bf16_t, false>, m3::kGradLds},
-             {(const void*)m3::finish_kernel, m3::kFinishLdsMax}};
+             {(const void*)m3::finish_kernel, m3::kFinishLdsMax},
+             {(const void*)m4::spd_wide_kernel<true>, kWideLdsMax},
+             {(const void*)m4::spd_wide_kernel<false>, kWideLdsMax},
+             {(const void*)m4::spd_wide_backward_kernel<true>, kWideLdsMax},
+             {(const void*)m4::spd_wide_backward_kernel<false>, kWideLdsMax}};
   for (auto& k : big) {
     hipError_t e = hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)k.bytes);
@@ -925,16 +941,37 @@ int m4mr_decode_step(float* evidence, float* cross, const float* key, const floa
   });
 }
 
+long m4mr_spd_factor_floats(int dim) {
+  if (dim < 1 || dim > m4::kWideMaxDim) return 0;
+  return dim <= M4MR_KEY_DIM ? (long)M4MR_FACTOR_FLOATS : (long)dim * dim;
+}
+
 int m4mr_spd_solve(const float* precision, const float* rhs, long N, int dim, float* solution,
                    float* factors, void* stream) {
   g_error.clear();
-  if (N <= 0 || N > kMaxSystems || dim < 1 || dim > M4MR_KEY_DIM)
-    return fail(M4MR_EINVAL, "m4mr_spd_solve: need 0 < N < 2^33 and 1 <= dim <= 64");
+  if (N <= 0 || N > kMaxSystems || dim < 1 || dim > m4::kWideMaxDim ||
+      (dim > M4MR_KEY_DIM && N > INT_MAX))
+    return fail(M4MR_EINVAL,
+                "m4mr_spd_solve: need 0 < N < 2^33 (< 2^31 above width 64) and 1 <= dim <= 4096");
   if (!precision || !rhs || !solution)
     return fail(M4MR_EINVAL, "m4mr_spd_solve: a required pointer is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dim > M4MR_KEY_DIM) {
+    const bool lds = dim <= m4::kWideLdsDim;
+    if (!lds && !factors)
+      return fail(M4MR_EINVAL,
+                  "m4mr_spd_solve: above width 128 the factors buffer is required (the "
+                  "factorization runs in it)");
+    if (int rc = configure()) return rc;
+    const size_t bytes = sizeof(float) * m4::wide_lds_floats(dim);
+    return launch("spd_wide", st, [&] {
+      hipLaunchKernelGGL(lds ? m4::spd_wide_kernel<true> : m4::spd_wide_kernel<false>,
+                         dim3((unsigned)N), dim3(m4::kWideThreads), bytes, st, precision, rhs,
+                         dim, solution, factors);
+    });
+  }
   if ((factors && misaligned(factors)) || (dim == M4MR_KEY_DIM && misaligned(precision)))
     return fail(M4MR_EINVAL, "m4mr_spd_solve: factors (and a 64-wide precision) must be 16-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
   return launch("spd_solve", st, [&] {
     hipLaunchKernelGGL(m4::spd_solve_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
                        precision, rhs, N, dim, solution, factors);
@@ -945,14 +982,28 @@ int m4mr_spd_solve_backward(const float* factors, const float* solution,
                             const float* d_solution, long N, int dim, float* d_precision,
                             float* d_rhs, void* stream) {
   g_error.clear();
-  if (N <= 0 || N > kMaxSystems || dim < 1 || dim > M4MR_KEY_DIM)
-    return fail(M4MR_EINVAL, "m4mr_spd_solve_backward: need 0 < N < 2^33 and 1 <= dim <= 64");
+  if (N <= 0 || N > kMaxSystems || dim < 1 || dim > m4::kWideMaxDim ||
+      (dim > M4MR_KEY_DIM && N > INT_MAX))
+    return fail(M4MR_EINVAL,
+                "m4mr_spd_solve_backward: need 0 < N < 2^33 (< 2^31 above width 64) and 1 <= "
+                "dim <= 4096");
   if (!factors || !solution || !d_solution || !d_precision || !d_rhs)
     return fail(M4MR_EINVAL, "m4mr_spd_solve_backward: a required pointer is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dim > M4MR_KEY_DIM) {
+    const bool lds = dim <= m4::kWideLdsDim;
+    if (int rc = configure()) return rc;
+    const size_t bytes = sizeof(float) * m4::wide_lds_floats(dim);
+    return launch("spd_wide_backward", st, [&] {
+      hipLaunchKernelGGL(lds ? m4::spd_wide_backward_kernel<true>
+                             : m4::spd_wide_backward_kernel<false>,
+                         dim3((unsigned)N), dim3(m4::kWideThreads), bytes, st, factors, solution,
+                         d_solution, dim, d_precision, d_rhs);
+    });
+  }
   if (misaligned(factors) || (dim == M4MR_KEY_DIM && misaligned(d_precision)))
     return fail(M4MR_EINVAL,
                 "m4mr_spd_solve_backward: factors (and a 64-wide d_precision) must be 16-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
   return launch("spd_backward", st, [&] {
     hipLaunchKernelGGL(m4::spd_backward_kernel, dim3((unsigned)((N + 3) / 4)), dim3(64), 0, st,
                        factors, solution, d_solution, N, dim, d_precision, d_rhs);

@@ -545,6 +545,17 @@ __device__ __forceinline__ void zero2(f4 acc[2]) {
 // Kernels built on these tiles run 256 threads (4 waves).
 constexpr int BLOCK = 256;
 
+// SPD solves wider than 64 (spd_wide.hip): one 256-thread block per
+// system, factored in LDS up to kWideLdsDim, in the factor buffer above.
+constexpr int kWideThreads = 256;
+constexpr int kWideLdsDim = 128;
+constexpr int kWideMaxDim = 4096;
+// LDS floats a block takes: the column, two vectors and, for LDS systems,
+// the matrix (row stride dim + 1).
+__host__ __device__ constexpr long wide_lds_floats(int dim) {
+  return 3L * dim + (dim <= kWideLdsDim ? (long)dim * (dim + 1) : 0L);
+}
+
 // One 64x64 tile staged through registers: thread i fetches the float4 at
 // column quad i%16 of rows i/16 + 16j (j = 0..3), and stores it later.  A
 // kernel fetches every tile of a phase before storing any, so all of the

@@ -200,7 +200,7 @@ class _SpdSolve(torch.autograd.Function):
         count, dim = rhs.shape
         f32 = dict(dtype=torch.float32, device=rhs.device)
         solution = torch.empty((count, dim), **f32)
-        factors = torch.empty((count, _lib.FACTOR_FLOATS), **f32)
+        factors = torch.empty((count, lib.m4mr_spd_factor_floats(dim)), **f32)
         _lib.check(
             lib.m4mr_spd_solve(
                 _ptr(precision), _ptr(rhs), count, dim, _ptr(solution), _ptr(factors), _stream()
@@ -234,7 +234,8 @@ def spd_solve(precision, rhs, backend=None):
     inverse is formed and nothing is refactored.  Every reference backend
     string selects the same HIP solve (the backend changes only the
     arithmetic schedule, never the solved system, lm/kernels/mamba4.py:193-194).
-    Widths up to 64.
+    Widths up to 64 solve four systems per wave; wider ones (up to 4096) one
+    system per 256-thread block.
     """
     _check_solver(backend)
     precision = torch.as_tensor(precision)
@@ -245,9 +246,9 @@ def spd_solve(precision, rhs, backend=None):
             f"spd_solve needs precision [...,d,d] and rhs [...,d]; got "
             f"{tuple(precision.shape)} and {tuple(rhs.shape)}"
         )
+    if dim > _lib.SPD_MAX_DIM:
+        raise ValueError(f"spd_solve supports widths <= {_lib.SPD_MAX_DIM}; got {dim}")
     _require_device(precision, rhs)
-    if dim > _lib.KEY_DIM:
-        raise ValueError(f"spd_solve supports widths <= {_lib.KEY_DIM}; got {dim}")
     batch = rhs.shape[:-1]
     if rhs.numel() == 0:
         return torch.zeros(rhs.shape, dtype=torch.float32, device=rhs.device)

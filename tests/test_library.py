@@ -101,14 +101,29 @@ def test_spd_solve_arguments_are_checked_before_any_launch():
     buf = ctypes.create_string_buffer(64)
     p = ctypes.c_void_p(ctypes.addressof(buf))
     assert lib.m4mr_spd_solve(p, p, 0, 6, p, null, null) == _lib.EINVAL
-    assert lib.m4mr_spd_solve(p, p, 4, 65, p, null, null) == _lib.EINVAL
+    assert lib.m4mr_spd_solve(p, p, 4, 4097, p, null, null) == _lib.EINVAL
     assert "dim" in lib.m4mr_last_error().decode()
+    # Above width 128 the factorization runs in the factors buffer.
+    assert lib.m4mr_spd_solve(p, p, 4, 129, p, null, null) == _lib.EINVAL
+    assert "factors buffer is required" in lib.m4mr_last_error().decode()
+    assert lib.m4mr_spd_solve(p, p, 1 << 31, 65, p, p, null) == _lib.EINVAL
     assert lib.m4mr_spd_solve(null, p, 4, 6, p, null, null) == _lib.EINVAL
     assert "NULL" in lib.m4mr_last_error().decode()
     assert lib.m4mr_spd_solve(p, p, 1 << 34, 6, p, null, null) == _lib.EINVAL
     assert lib.m4mr_spd_solve_backward(p, p, p, 4, 0, p, p, null) == _lib.EINVAL
+    assert lib.m4mr_spd_solve_backward(p, p, p, 4, 4097, p, p, null) == _lib.EINVAL
     assert lib.m4mr_spd_solve_backward(p, p, null, 4, 6, p, p, null) == _lib.EINVAL
     assert lib.m4mr_factored_solve(p, p, p, 1 << 34, null) == _lib.EINVAL
+
+
+def test_spd_factor_size_per_width():
+    lib = _lib.load()
+    assert lib.m4mr_spd_factor_floats(1) == _lib.FACTOR_FLOATS
+    assert lib.m4mr_spd_factor_floats(64) == _lib.FACTOR_FLOATS
+    assert lib.m4mr_spd_factor_floats(65) == 65 * 65
+    assert lib.m4mr_spd_factor_floats(4096) == 4096 * 4096
+    assert lib.m4mr_spd_factor_floats(0) == 0
+    assert lib.m4mr_spd_factor_floats(4097) == 0
 
 
 def test_spd_solve_python_checks():
@@ -119,6 +134,8 @@ def test_spd_solve_python_checks():
         memory.spd_solve(a, torch.zeros(7, 5))
     with pytest.raises(ValueError, match="Unknown SPD solve backend"):
         memory.spd_solve(a, torch.zeros(7, 6), backend="qr")
+    with pytest.raises(ValueError, match="widths <= 4096"):
+        memory.spd_solve(torch.eye(4097)[None], torch.zeros(1, 4097))
 
 
 def test_noalloc_backward_rejects_sizes_beyond_its_static_buffer():
