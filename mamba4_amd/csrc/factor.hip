@@ -297,7 +297,11 @@ __global__ __launch_bounds__(128 * PAIRS) void fwd_factor_kernel(
       load_token(next, d, keys, queries, beta, log_decay, b, h, token(tt + 2), a);
     float nw[4], y[4];
     factor_exchanged<true>(A, fl, cur.q, nw, sexp);
+    // The substitution's chain of dependent 16-lane sums at priority 2 (see
+    // factor_panel in rows16.hpp); the stores and the next turn at 0.
+    __builtin_amdgcn_s_setprio(2);
     backward_rows16(A, nw, y);
+    __builtin_amdgcn_s_setprio(0);
     float* const sol = valid ? solved + cur.th * 64 : g_discard + ROWS_FACTOR;
 #pragma unroll
     for (int m = 0; m < 4; ++m) sol[a + 16 * m] = y[m];

@@ -341,10 +341,22 @@ __device__ __forceinline__ void panel_update(float (&A)[4][64]) {
   }
 }
 
+// Wave priorities.  The two waves of a SIMD run the same passes offset by a
+// turn, and the factorization is bound by dependent chains (each column's
+// pivot, scale and next-column update; the backward substitution's 16-lane
+// sums) more than by issue.  A panel's elimination therefore runs at
+// priority 1 and its MFMA trailing update at 0: when both waves are ready,
+// the instruction of a chain issues first and the other wave's independent
+// MFMA and split work fills the chain's stalls.  (fwd_factor_kernel raises
+// the backward substitution to 2 the same way.)  Measured at config 2: the
+// factor kernel 0.304 -> 0.293 ms; priorities 3 and 3, a separate level
+// for each column's pivot chain, or one for the turn gained nothing more.
 template <int P, bool F16>
 __device__ __forceinline__ void factor_panel(float (&A)[4][64], const float (&fl)[4],
                                              float (&r)[4], float (&nw)[4], int a) {
+  __builtin_amdgcn_s_setprio(1);
   factor_steps(A, fl, r, nw, a, offset_sequence<16 * P>(std::make_integer_sequence<int, 16>{}));
+  __builtin_amdgcn_s_setprio(0);
   panel_update<P, F16>(A);
 }
 
