@@ -847,6 +847,41 @@ def main_mamba3(args, bf16=False):
     print(json.dumps(line), flush=True)
 
 
+def _best_seconds(fn, reps=10):
+    """Shortest of `reps` timed calls of fn (after two untimed ones)."""
+    import torch
+
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        stop.record()
+        stop.synchronize()
+        best = min(best, start.elapsed_time(stop) / 1e3)
+    return best
+
+
+def stream_probes_gbps(nbytes):
+    """Write-only and read-only rates over an nbytes float32 buffer: torch's
+    fill_ (a vectorized store-only kernel) and row sums over 4096-float rows
+    (torch's fastest read-only reduction here; a whole-buffer sum reads at
+    about 4 TB/s), best of ten.  What a library kernel reaches on this box
+    for the factor store and load, next to the 8 TB/s read+write peak."""
+    import torch
+
+    buf = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    rows = buf[: (nbytes // 4) // 4096 * 4096].view(-1, 4096)
+    out = torch.empty(rows.shape[0], dtype=torch.float32, device="cuda:0")
+    write = nbytes / _best_seconds(lambda: buf.fill_(1.0)) / 1e9
+    read = rows.numel() * 4 / _best_seconds(lambda: torch.sum(rows, dim=1, out=out)) / 1e9
+    del buf, rows, out
+    return write, read
+
+
 def copy_bandwidth_gbps():
     """Read+write bandwidth of a 2 GiB device-to-device copy (torch copy_)."""
     import torch
@@ -1044,6 +1079,7 @@ def main():
     store_gbps = FACTOR_BYTES * token_heads / factor_s / 1e9
     load_gbps = RESOLVE_BYTES * token_heads / resolve_s / 1e9
     copy_gbps = copy_bandwidth_gbps()
+    write_probe, read_probe = stream_probes_gbps(FACTOR_BYTES * token_heads)
 
     vs_baseline = None
     if args.workload == "config3":
@@ -1107,6 +1143,10 @@ def main():
             "load_GBps": load_gbps,
             "load_frac": load_gbps / HBM_PEAK_GBPS,
             "copy_kernel_GBps": copy_gbps,
+            "write_probe_GBps": write_probe,
+            "store_frac_of_write_probe": store_gbps / write_probe,
+            "read_probe_GBps": read_probe,
+            "load_frac_of_read_probe": load_gbps / read_probe,
         },
         "kernel_ms": kernels,
         "kernel_roofline": ({k: roofline(k, v, token_heads, traffic=False)["frac"]
